@@ -1,0 +1,59 @@
+"""The oracle's certificate: every det_* commitment the reference pinned in
+testdata/det_commitment_goldens.json (src/runtime/det_goldens.rs) must be
+reproduced bit-exactly by the CPU restatement."""
+import pytest
+
+import fixtures
+import oracle_lib
+
+
+@pytest.mark.parametrize("name", ["donor_ple", "no_donor_ple"])
+def test_oracle_reproduces_reference_det_goldens(name):
+    cfg, wgt, prompt, steps = fixtures.golden_fixture(name)
+    model = oracle_lib.OracleModel(cfg).load_detwgt(wgt).finalize()
+    got = model.capture(prompt, steps)
+    exp = fixtures.golden_expected(name)
+    assert got["prefill"] == exp["prefill"]
+    assert got["first_step_layers"] == exp["first_step_layers"]
+    for i, (g, e) in enumerate(zip(got["decode_steps"], exp["decode_steps"])):
+        assert g == e, f"decode step {i}"
+    assert len(got["decode_steps"]) == len(exp["decode_steps"])
+    assert got["end_to_end"] == exp["end_to_end"]
+
+
+@pytest.mark.parametrize("name", ["donor_ple", "no_donor_ple"])
+def test_i32_storage_gives_identical_commitments(name):
+    # detwgt v2 invariant: storage width is representation only
+    # (DETWGT_V2_FORMAT.md; schedule_parity.rs:98-139).
+    cfg, _, prompt, _ = fixtures.golden_fixture(name)
+    wide = fixtures.encode_detwgt(fixtures.golden_tensors(), force_i32=True)
+    model = oracle_lib.OracleModel(cfg).load_detwgt(wide).finalize()
+    got = model.capture(prompt, 8)
+    exp = fixtures.golden_expected(name)
+    assert got["prefill"] == exp["prefill"]
+    assert got["decode_steps"] == exp["decode_steps"][:8]
+
+
+@pytest.mark.parametrize("threads", [1, 2, 3, 8])
+def test_thread_count_invariance(threads):
+    # schedule_parity.rs:55-83: committed bytes are identical for every pool size.
+    cfg, wgt, prompt, _ = fixtures.golden_fixture("no_donor_ple")
+    oracle_lib.set_threads(threads)
+    try:
+        got = oracle_lib.OracleModel(cfg).load_detwgt(wgt).finalize().capture(prompt, 4)
+    finally:
+        oracle_lib.set_threads(1)
+    exp = fixtures.golden_expected("no_donor_ple")
+    assert got["prefill"] == exp["prefill"]
+    assert got["decode_steps"] == exp["decode_steps"][:4]
+
+
+def test_loader_fails_closed():
+    cfg, wgt, _, _ = fixtures.golden_fixture("no_donor_ple")
+    bad_version = wgt[:8] + (1).to_bytes(4, "little") + wgt[12:]
+    with pytest.raises(oracle_lib.OracleError):
+        oracle_lib.OracleModel(cfg).load_detwgt(bad_version)
+    with pytest.raises(oracle_lib.OracleError):
+        oracle_lib.OracleModel(cfg).load_detwgt(wgt + b"\0")  # trailing bytes
+    with pytest.raises(oracle_lib.OracleError):
+        oracle_lib.OracleModel(cfg).load_detwgt(wgt[:-2])  # truncated
