@@ -1,0 +1,230 @@
+/*
+ * detgpu — C ABI of the MI355X-native deterministic integer transformer path.
+ *
+ * This is the drop-in boundary for raster-inference's native deterministic
+ * executor: a GPU executor beside src/runtime/executors/native.rs binds these
+ * entry points through FFI and keeps the reference's routine / checkpoint
+ * contract (src/routines/{prefill_range,decode_layer_range,prefill_finalize,
+ * decode_transition_finalize}/native) and the detwgt v2 weight format.
+ *
+ * Conventions
+ *  - Every function returns int status: 0 ok, 1 invalid argument / shape
+ *    mismatch / missing weight (the reference's anyhow::bail!), 2 contract
+ *    violation (the reference's det_num assert! panics), 3 runtime / HIP
+ *    error. No C++ exception crosses this boundary; det_ctx_last_error()
+ *    returns the message of the last failure on that context.
+ *  - Pointers named *_dev are device pointers (allocate with
+ *    det_device_alloc or any HIP allocation on the context's device); all
+ *    other pointers are host pointers.
+ *  - One context owns one HIP stream. Calls on one context are serialized by
+ *    the caller; distinct contexts are independent. Work is enqueued on the
+ *    context stream; functions that return host data synchronize it.
+ *  - Values are canonical det_num bit patterns: Act/Wgt = Q16.16 in int32,
+ *    Acc = Q32.32 in int64 (src/shared/numerics/det_num/types.rs:8-25).
+ */
+#ifndef DETGPU_H
+#define DETGPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct det_ctx det_ctx_t;
+typedef struct det_matrix det_matrix_t;
+typedef struct det_model det_model_t;
+typedef struct det_session det_session_t;
+typedef struct det_event det_event_t;
+
+/* ------------------------------------------------------------------------ */
+/* Context, memory, timing                                                   */
+/* ------------------------------------------------------------------------ */
+int det_ctx_create(int device, det_ctx_t** out);
+void det_ctx_destroy(det_ctx_t* ctx);
+const char* det_ctx_last_error(const det_ctx_t* ctx);
+int det_ctx_synchronize(det_ctx_t* ctx);
+/* Library build string (kernel ISA, version). */
+const char* det_version(void);
+
+int det_device_alloc(det_ctx_t* ctx, size_t bytes, void** out_dev);
+int det_device_free(det_ctx_t* ctx, void* dev);
+int det_memcpy_h2d(det_ctx_t* ctx, void* dst_dev, const void* src, size_t bytes);
+int det_memcpy_d2h(det_ctx_t* ctx, void* dst, const void* src_dev, size_t bytes);
+int det_memcpy_d2d(det_ctx_t* ctx, void* dst_dev, const void* src_dev, size_t bytes);
+
+/* HIP events recorded on the context stream (for timing the hot kernels). */
+int det_event_create(det_ctx_t* ctx, det_event_t** out);
+int det_event_record(det_ctx_t* ctx, det_event_t* ev);
+int det_event_elapsed_ms(det_ctx_t* ctx, det_event_t* start, det_event_t* stop, float* ms);
+void det_event_destroy(det_event_t* ev);
+
+/* ------------------------------------------------------------------------ */
+/* Weights: DetNumMatrix (src/shared/model/transformer.rs:194-198)            */
+/* ------------------------------------------------------------------------ */
+/* Storage after upload (det_matrix_info): */
+#define DET_STORAGE_INT8 8   /* int8 q with per-row integer scale: W = q * s exactly */
+#define DET_STORAGE_I16 16   /* canonical Wgt bits stored as int16 (detwgt v2 i16) */
+#define DET_STORAGE_I32 32   /* canonical Wgt bits stored as int32 (detwgt v2 i32) */
+
+/* Uploads a rows x cols row-major weight matrix.
+ *  elem_width 8 : `values` is int8 q, `row_scale` int32[rows] (W = q*s);
+ *  elem_width 16/32 : `values` are detwgt v2 Wgt bits (row_scale ignored);
+ *                     rows are stored as int8 x scale whenever that
+ *                     factorization is exact for the whole matrix, else wide.
+ * Rejects matrices whose max row mass sum_c |W[r][c]| >= 2^31
+ * (det_num/mod.rs:39-42, gemma/io.rs:327-335). */
+int det_matrix_upload(det_ctx_t* ctx, uint64_t rows, uint64_t cols, int elem_width, const void* values,
+                      const int32_t* row_scale, det_matrix_t** out);
+int det_matrix_info(const det_matrix_t* m, uint64_t* rows, uint64_t* cols, int* storage);
+void det_matrix_free(det_matrix_t* m);
+
+/* ------------------------------------------------------------------------ */
+/* Primitive ops (device pointers, enqueued on the context stream)           */
+/* ------------------------------------------------------------------------ */
+/* det_linear_into / det_linear_into_par (det_kernels.rs:108-178):
+ * out[r] = requantize(sum_c act[c] * W[r][c]) with wrapping i64 MAC. */
+int det_linear(det_ctx_t* ctx, const det_matrix_t* w, const int32_t* act_dev, int32_t* out_dev);
+/* Raw wrapped Q32.32 accumulators (before requantize), for split-K
+ * combination by wrapping i64 addition (det_num/ops.rs:23-30). */
+int det_linear_acc_i64(det_ctx_t* ctx, const det_matrix_t* w, const int32_t* act_dev, int64_t* acc_dev);
+/* det_linear_slab (det_kernels.rs:180-203): m token rows, act [m][cols] -> out [m][rows]. */
+int det_linear_slab(det_ctx_t* ctx, const det_matrix_t* w, uint64_t m, const int32_t* act_dev, int32_t* out_dev);
+
+/* rms_norm_in_place / value_rms_norm_in_place per row (det_num/ops.rs:95-131);
+ * weight_dev NULL selects the value norm. */
+int det_rms_norm(det_ctx_t* ctx, int32_t* x_dev, uint64_t rows, uint64_t cols, const int32_t* weight_dev,
+                 int64_t eps_acc);
+/* rope_rotate_pairs_in_place over rows x heads of head_dim (det_num/ops.rs:151-196);
+ * row r uses position pos0 + r * pos_step. */
+int det_rope(det_ctx_t* ctx, int32_t* x_dev, uint64_t rows, uint64_t heads, uint64_t head_dim, uint64_t rotary_dim,
+             uint64_t freq_base_dim, int64_t base_acc, uint64_t pos0, uint64_t pos_step);
+/* attention_output_into for every (head, query) (det_kernels.rs:340-367, 525-651):
+ * q [n_queries][num_heads*head_dim], k/v [n_rows][num_kv_heads*head_dim],
+ * causal rows [max(0, t+1-window), t+1) (window 0 = unbounded),
+ * out [n_queries][num_heads*head_dim]. */
+int det_attention_causal(det_ctx_t* ctx, const int32_t* q_dev, const int32_t* k_dev, const int32_t* v_dev,
+                         uint64_t n_queries, uint64_t n_rows, uint64_t num_heads, uint64_t num_kv_heads,
+                         uint64_t head_dim, uint64_t window, int32_t* out_dev);
+/* argmax_first (det_num/ops.rs:463-478); result written to *index (host). */
+int det_argmax_first(det_ctx_t* ctx, const int32_t* x_dev, uint64_t n, uint32_t* index);
+/* Elementwise saturating ops (det_kernels.rs:252-282, det_num/ops.rs:33-47, 377-403). */
+#define DET_EW_ADD 0      /* x = add_sat(x, y) */
+#define DET_EW_GELU_MUL 1 /* x = mul_sat(gelu_pytorch_tanh(x), y) */
+#define DET_EW_SCALE 2    /* x = scale_act(x, scalar) */
+#define DET_EW_SOFTCAP 3  /* x = softcap_act(x, scalar) */
+int det_elementwise(det_ctx_t* ctx, int op, int32_t* x_dev, const int32_t* y_dev, uint64_t n, int32_t scalar);
+
+/* ------------------------------------------------------------------------ */
+/* Model: Gemma4TransformerModel in det mode (gemma/io.rs:1043-1123)         */
+/* ------------------------------------------------------------------------ */
+/* Raw config.json text_config (GemmaTextConfigFile, gemma/io.rs:60-96);
+ * has_* flags mark Option<...> fields that were present. */
+typedef struct det_text_config {
+  int32_t enable_moe_block;
+  int32_t hidden_activation_is_gelu_pytorch_tanh;
+  int32_t has_final_logit_softcapping;
+  float final_logit_softcapping;
+  int32_t has_global_head_dim;
+  uint64_t global_head_dim;
+  uint64_t head_dim;
+  uint64_t hidden_size;
+  int32_t has_hidden_size_per_layer_input;
+  uint64_t hidden_size_per_layer_input;
+  uint64_t num_layer_types;
+  const int32_t* layer_types; /* 1 = "sliding_attention", 0 = any other type */
+  int32_t has_num_global_key_value_heads;
+  uint64_t num_global_key_value_heads;
+  uint64_t num_attention_heads;
+  uint64_t num_hidden_layers;
+  uint64_t num_key_value_heads;
+  float rms_norm_eps;
+  int32_t has_full_partial_rotary_factor;
+  float full_partial_rotary_factor;
+  int32_t has_full_rope_theta;
+  float full_rope_theta;
+  int32_t has_sliding_rope_theta;
+  float sliding_rope_theta;
+  int32_t has_rope_theta;
+  float rope_theta;
+  uint64_t sliding_window;
+  int32_t has_tie_word_embeddings;
+  int32_t tie_word_embeddings;
+  uint64_t vocab_size;
+  int32_t has_vocab_size_per_layer_input;
+  uint64_t vocab_size_per_layer_input;
+  int32_t has_attention_k_eq_v;
+  int32_t attention_k_eq_v;
+  int32_t has_num_kv_shared_layers;
+  uint64_t num_kv_shared_layers;
+  int32_t bidirectional_all; /* use_bidirectional_attention == "all" */
+} det_text_config_t;
+
+int det_model_create(det_ctx_t* ctx, const det_text_config_t* cfg, det_model_t** out);
+/* Adds one named tensor (names as in gemma/io.rs, e.g.
+ * "model.language_model.layers.0.self_attn.q_proj.weight"). rank 1 or 2;
+ * elem_width 8 (+row_scale), 16 or 32 as in det_matrix_upload. */
+int det_model_set_tensor(det_model_t* model, const char* name, uint64_t rank, const uint64_t* dims, int elem_width,
+                         const void* values, const int32_t* row_scale);
+/* Parses a whole detwgt v2 artifact with the fail-closed checks of
+ * DetNumTensorReader::load_artifact (gemma/io.rs:224-387). */
+int det_model_load_detwgt(det_model_t* model, const uint8_t* bytes, size_t len);
+/* Resolves layers exactly like load_det_num_gemma4_layer_weights (gemma/io.rs:1896-2045). */
+int det_model_finalize(det_model_t* model);
+void det_model_free(det_model_t* model);
+
+/* ------------------------------------------------------------------------ */
+/* Sessions: the prefill_layer / decode_transition routines on the GPU        */
+/* ------------------------------------------------------------------------ */
+/* A session owns one sequence's KV caches (LayerKvCache per layer) sized for
+ * max_tokens positions, plus device scratch. */
+int det_session_create(det_model_t* model, uint64_t max_tokens, det_session_t** out);
+int det_session_clone(const det_session_t* src, det_session_t** out);
+void det_session_free(det_session_t* s);
+
+/* Commitments are lowercase hex SHA-256 strings (65 bytes incl. NUL) built
+ * exactly like build_det_*_commitment (transformer_kernels.rs:1395-1482);
+ * kv is "" when the reference would return None (a layer without det data). */
+typedef struct det_prefill_result {
+  char embedding[65];    /* input.embedding det_activations_sha256 */
+  char final_hidden[65]; /* prefill final_hidden_states det commitment */
+  char logits[65];       /* det_final_logits_sha256 (vector commitment) */
+  char kv[65];           /* build_det_kv_cache_commitment of all layer caches */
+  uint32_t next_token;   /* argmax_first of the logits (greedy selection) */
+} det_prefill_result_t;
+
+typedef struct det_decode_result {
+  char activation[65]; /* decode activation_state det commitment */
+  char logits[65];
+  char kv[65];
+  uint32_t next_token;
+} det_decode_result_t;
+
+/* Flags for prefill/decode: which commitments to compute on the host. */
+#define DET_COMMIT_NONE 0u
+#define DET_COMMIT_ACTIVATIONS 1u /* embedding / hidden / activation / logits */
+#define DET_COMMIT_KV 2u          /* KV cache commitment */
+#define DET_COMMIT_ALL 3u
+
+/* pipeline::run_prefill_pass_with_mode (runtime/pipeline.rs:55-98): embedding,
+ * PLE inputs, every prefill_layer, prefill_finalize logits. */
+int det_session_prefill(det_session_t* s, const uint32_t* token_ids, uint64_t n, uint32_t flags,
+                        det_prefill_result_t* out);
+/* pipeline::decode_step_with_mode (runtime/pipeline.rs:165-216): embed token,
+ * every decode_transition layer with in-place KV append, finalize logits. */
+int det_session_decode(det_session_t* s, uint32_t token, uint32_t flags, det_decode_result_t* out);
+/* Copies the last logits (vocab int32) to host. */
+int det_session_logits(det_session_t* s, int32_t* out, uint64_t n);
+int det_session_position(const det_session_t* s, uint64_t* position);
+
+/* Runs the det_goldens capture protocol (src/runtime/det_goldens.rs:90-185)
+ * and writes it as compact JSON into out (NUL-terminated). */
+int det_capture(det_model_t* model, const uint32_t* prompt, uint64_t prompt_len, uint64_t decode_steps, char* out,
+                size_t out_cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DETGPU_H */

@@ -1,0 +1,296 @@
+// Canonical Q16.16 / Q32.32 integer arithmetic for the MI355X det path.
+//
+// Every function here is __host__ __device__ and computes exactly the value
+// the reference's det_num contract defines (src/shared/numerics/det_num/ops.rs),
+// but in forms that suit 64-wide wavefronts: floor-based round-half-even
+// shifts, 64-bit divisions by small constants, one 64x64->128 multiply where
+// the reference uses i128, and exact-correction steps instead of 31-step
+// binary searches. No 128-bit division is ever emitted (gfx950 has no
+// library routine for it).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DET_HD __host__ __device__ __forceinline__
+
+namespace det {
+
+constexpr int32_t kOneAct = 1 << 16;
+constexpr int64_t kOneAcc = int64_t(1) << 32;
+
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+DET_HD int32_t sat32(int64_t v) {
+  return v > INT32_MAX ? INT32_MAX : (v < INT32_MIN ? INT32_MIN : int32_t(v));
+}
+DET_HD int32_t add_sat(int32_t a, int32_t b) { return sat32(int64_t(a) + int64_t(b)); }
+DET_HD int32_t sub_sat(int32_t a, int32_t b) { return sat32(int64_t(a) - int64_t(b)); }
+DET_HD int32_t neg_sat32(int32_t a) { return a == INT32_MIN ? INT32_MAX : -a; }
+DET_HD int64_t neg_sat64(int64_t a) { return a == INT64_MIN ? INT64_MAX : -a; }
+DET_HD int64_t add_sat64(int64_t a, int64_t b) {
+  int64_t r;
+  if (__builtin_add_overflow(a, b, &r)) return a < 0 ? INT64_MIN : INT64_MAX;
+  return r;
+}
+// Wrapping i64 MAC (ops.rs:14-16).
+DET_HD int64_t mac(int64_t acc, int32_t a, int32_t w) {
+  return int64_t(uint64_t(acc) + uint64_t(int64_t(a) * int64_t(w)));
+}
+
+// Round x / 2^s to nearest, ties to even, for 1 <= s <= 63 (ops.rs:770-800).
+// Floor quotient + remainder: identical to the reference's truncate-and-step.
+DET_HD int64_t rshift_rte(int64_t x, unsigned s) {
+  if (s == 0) return x;
+  const int64_t q = x >> s;  // arithmetic: floor
+  const uint64_t r = uint64_t(x) & ((uint64_t(1) << s) - 1);
+  const uint64_t half = uint64_t(1) << (s - 1);
+  return (r > half || (r == half && (q & 1))) ? q + 1 : q;
+}
+
+// requantize: Q32.32 -> Q16.16, ties to even, saturating (ops.rs:445-448).
+DET_HD int32_t requant(int64_t acc) { return sat32(rshift_rte(acc, 16)); }
+DET_HD int32_t mul_sat(int32_t a, int32_t b) { return requant(int64_t(a) * int64_t(b)); }
+
+// Round |n| / d to nearest with ties to even on the magnitude, sign restored
+// (the reference's round_ties_even_division for |quotient| < 2^63).
+DET_HD uint64_t udiv_rte(uint64_t n, uint64_t d) {
+  const uint64_t q = n / d, r = n - q * d;
+  const uint64_t rem_twice_hi = r >> 63;  // r < d <= 2^64-1; 2r may overflow
+  const uint64_t twice = r << 1;
+  const bool gt = rem_twice_hi || twice > d;
+  const bool eq = !rem_twice_hi && twice == d;
+  return (gt || (eq && (q & 1))) ? q + 1 : q;
+}
+
+// div_acc_by_u32 (ops.rs:78-85).
+DET_HD int64_t div_acc_u32(int64_t v, uint32_t d) {
+  const bool neg = v < 0;
+  const uint64_t mag = neg ? uint64_t(0) - uint64_t(v) : uint64_t(v);
+  const uint64_t q = udiv_rte(mag, d);
+  return neg ? int64_t(uint64_t(0) - q) : int64_t(q);
+}
+
+// div_act (ops.rs:50-61): round(n * 2^16 / d), saturating to i32. d != 0.
+DET_HD int32_t div_act(int32_t n, int32_t d) {
+  const int64_t num = int64_t(n) * 65536;
+  const bool neg = (num < 0) != (d < 0);
+  const uint64_t un = num < 0 ? uint64_t(-num) : uint64_t(num);
+  const uint64_t ud = d < 0 ? uint64_t(-int64_t(d)) : uint64_t(d);
+  const uint64_t q = udiv_rte(un, ud);
+  return sat32(neg ? -int64_t(q) : int64_t(q));
+}
+
+// acc_mul (ops.rs:682-686): round(lhs * rhs / 2^32), saturating to i64.
+DET_HD int64_t acc_mul(int64_t lhs, int64_t rhs) {
+  const i128 p = i128(lhs) * i128(rhs);
+  const i128 q = p >> 32;  // floor
+  const uint64_t r = uint64_t(p) & 0xffffffffull;
+  const i128 rq = (r > 0x80000000ull || (r == 0x80000000ull && (int64_t(q) & 1))) ? q + 1 : q;
+  if (rq > i128(INT64_MAX)) return INT64_MAX;
+  if (rq < i128(INT64_MIN)) return INT64_MIN;
+  return int64_t(rq);
+}
+
+// inv_sqrt_acc (ops.rs:719-763): the c in [0, 2^31-1] nearest to
+// 2^32/sqrt(x) in the sense |c^2 x - 2^64| minimal, ties to even; x == 0 and
+// tiny x saturate to i32::MAX. Computed from a floating estimate of
+// floor(sqrt(2^64/x)) followed by exact integer correction.
+DET_HD u128 isq_prod(uint64_t c, uint64_t x) { return u128(c * c) * u128(x); }
+DET_HD int32_t inv_sqrt_acc(int64_t x) {
+  if (x <= 0) return INT32_MAX;  // x == 0 (negative x is rejected upstream)
+  const uint64_t ux = uint64_t(x);
+  const u128 target = u128(1) << 64;
+  const uint64_t cmax = uint64_t(INT32_MAX);
+  if (isq_prod(cmax, ux) <= target) return INT32_MAX;
+  // low = max c with c^2 x <= 2^64 (exists below cmax here).
+  uint64_t low = uint64_t(4294967296.0 / __builtin_sqrt(double(ux)));
+  if (low > cmax) low = cmax;
+  while (low > 0 && isq_prod(low, ux) > target) --low;
+  while (low + 1 <= cmax && isq_prod(low + 1, ux) <= target) ++low;
+  const uint64_t up = low + 1 > cmax ? cmax : low + 1;
+  const u128 lp = isq_prod(low, ux), upp = isq_prod(up, ux);
+  const u128 le = target - lp;
+  const u128 ue = upp > target ? upp - target : 0;
+  uint64_t r;
+  if (up == low || le < ue) r = low;
+  else if (ue < le) r = up;
+  else r = (low & 1) == 0 ? low : up;
+  return int32_t(r);
+}
+
+// rms_norm_scale from a saturated sum of squares (ops.rs:406-425). The
+// saturating sum of non-negative terms is min(true sum, i64::MAX) in any order.
+DET_HD int32_t rms_scale_from_sumsq(int64_t sumsq, uint32_t n, int64_t eps) {
+  const int64_t mean = div_acc_u32(sumsq, n);
+  return inv_sqrt_acc(add_sat64(mean, eps));
+}
+DET_HD int64_t sq_term(int32_t v) { return int64_t(v) * int64_t(v); }
+
+// softmax exp term of a max-shifted logit (ops.rs:505-553, 261-263).
+DET_HD int64_t softmax_exp(int32_t logit, int32_t max_logit) {
+  const int64_t delta = int64_t(sub_sat(logit, max_logit)) * 65536;  // act_to_acc, <= 0
+  const int64_t LN2 = 2977044472ll;
+  if (delta <= -(int64_t(16) << 32)) return 0;
+  const int64_t pos = -delta;
+  const int64_t shift = pos / LN2;
+  const int64_t r = pos - shift * LN2;
+  const int64_t r2 = acc_mul(r, r);
+  const int64_t r3 = acc_mul(r2, r);
+  const int64_t r4 = acc_mul(r3, r);
+  const int64_t r5 = acc_mul(r4, r);
+  const int64_t t = add_sat64(
+      add_sat64(kOneAcc, -r),
+      add_sat64(div_acc_u32(r2, 2),
+                add_sat64(-div_acc_u32(r3, 6), add_sat64(div_acc_u32(r4, 24), -div_acc_u32(r5, 120)))));
+  if (t <= 0) return 0;
+  return rshift_rte(t, unsigned(shift));  // shift <= 23 here
+}
+
+// Softmax raw weight: requantize(div_acc(exp, sum)) (ops.rs:266-268) for the
+// softmax domain 0 <= exp <= sum, sum > 0: round(exp * 2^32 / sum), then
+// requantize. The quotient is at most 2^32, so a double estimate corrected
+// with an exact 128-bit remainder gives the exact rounded value.
+DET_HD int32_t softmax_weight(int64_t e, int64_t sum) {
+  const u128 num = u128(uint64_t(e)) << 32;
+  const uint64_t d = uint64_t(sum);
+  uint64_t q = uint64_t(double(e) * 4294967296.0 / double(sum));
+  // exact floor correction: q*d <= num < (q+1)*d
+  while (q > 0 && u128(q) * d > num) --q;
+  while (u128(q + 1) * d <= num) ++q;
+  const u128 rem = num - u128(q) * d;
+  const u128 twice = rem << 1;
+  if (twice > u128(d) || (twice == u128(d) && (q & 1))) ++q;
+  return requant(int64_t(q));
+}
+
+// tanh_act (ops.rs:354-374), softcap_act (ops.rs:377-385),
+// gelu_pytorch_tanh_act (ops.rs:388-403).
+DET_HD int32_t tanh_act(int32_t x) {
+  const int32_t LIN = 27 << 16, QUAD = 9 << 16, SAT = 3 << 16;
+  if (x >= SAT) return kOneAct;
+  if (x <= -SAT) return -kOneAct;
+  const int32_t x2 = mul_sat(x, x);
+  const int32_t num = mul_sat(x, add_sat(LIN, x2));
+  const int32_t den = add_sat(LIN, mul_sat(QUAD, x2));
+  return div_act(num, den);
+}
+DET_HD int32_t softcap_act(int32_t x, int32_t cap) { return mul_sat(cap, tanh_act(div_act(x, cap))); }
+DET_HD int32_t gelu_act(int32_t x) {
+  const int32_t x2 = mul_sat(x, x);
+  const int32_t x3 = mul_sat(x2, x);
+  const int32_t inner = add_sat(x, mul_sat(2930, x3));
+  const int32_t t = tanh_act(mul_sat(52290, inner));
+  return mul_sat(mul_sat(1 << 15, x), add_sat(kOneAct, t));
+}
+
+// sin/cos of a Q32.32 angle (ops.rs:619-680).
+DET_HD int64_t sin_poly(int64_t x) {
+  const int64_t x2 = acc_mul(x, x), x3 = acc_mul(x2, x), x5 = acc_mul(x3, x2), x7 = acc_mul(x5, x2);
+  return add_sat64(add_sat64(x, neg_sat64(div_acc_u32(x3, 6))),
+                   add_sat64(div_acc_u32(x5, 120), neg_sat64(div_acc_u32(x7, 5040))));
+}
+DET_HD int64_t cos_poly(int64_t x) {
+  const int64_t x2 = acc_mul(x, x), x4 = acc_mul(x2, x2), x6 = acc_mul(x4, x2);
+  return add_sat64(add_sat64(kOneAcc, neg_sat64(div_acc_u32(x2, 2))),
+                   add_sat64(div_acc_u32(x4, 24), neg_sat64(div_acc_u32(x6, 720))));
+}
+DET_HD void sin_cos(int64_t angle, int32_t* c, int32_t* s) {
+  const int64_t HALF_PI = 6746518852ll, PI = 13493037705ll, THREE_HALF_PI = 20239556557ll,
+                TWO_PI = 26986075409ll;
+  int64_t red = angle % TWO_PI;
+  if (red < 0) red += TWO_PI;
+  int64_t q;
+  bool sneg, cneg;
+  if (red <= HALF_PI) { q = red; sneg = false; cneg = false; }
+  else if (red <= PI) { q = PI - red; sneg = false; cneg = true; }
+  else if (red <= THREE_HALF_PI) { q = red - PI; sneg = true; cneg = true; }
+  else { q = TWO_PI - red; sneg = true; cneg = false; }
+  int32_t sv = requant(sin_poly(q)), cv = requant(cos_poly(q));
+  *s = sneg ? neg_sat32(sv) : sv;
+  *c = cneg ? neg_sat32(cv) : cv;
+}
+// RoPE angle = position * inv_freq, clamped to i64 (ops.rs:613-617).
+DET_HD int64_t rope_angle(uint64_t position, int64_t inv_freq) {
+  const i128 p = i128(position) * i128(inv_freq);
+  if (p > i128(INT64_MAX)) return INT64_MAX;
+  if (p < i128(INT64_MIN)) return INT64_MIN;
+  return int64_t(p);
+}
+
+// ---------------------------------------------------------------------------
+// Host-only helpers (load-time constants)
+// ---------------------------------------------------------------------------
+// pow_acc_u32 / nth_root_acc / rope_frequency_step (ops.rs:555-611).
+inline int64_t pow_acc(int64_t base, uint32_t e) {
+  int64_t r = kOneAcc;
+  for (uint32_t i = 0; i < e; ++i) r = acc_mul(r, base);
+  return r;
+}
+inline int64_t nth_root(int64_t value, uint32_t degree) {
+  if (degree == 1 || value == kOneAcc) return value;
+  int64_t lo = 0, hi = value > kOneAcc ? value : kOneAcc;
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo + 1) / 2;
+    if (pow_acc(mid, degree) <= value) lo = mid; else hi = mid - 1;
+  }
+  const int64_t up = lo == INT64_MAX ? lo : lo + 1;
+  const i128 le = i128(value) - i128(pow_acc(lo, degree));
+  const i128 ue = i128(pow_acc(up, degree)) - i128(value);
+  const i128 ale = le < 0 ? -le : le, aue = ue < 0 ? -ue : ue;
+  if (aue < ale) return up;
+  if (ale < aue) return lo;
+  return (lo & 1) == 0 ? lo : up;
+}
+// div_acc(one, d) for d > 0: round(2^64 / d).
+inline int64_t recip_acc(int64_t d) {
+  const u128 num = u128(1) << 64;
+  const u128 q = num / u128(uint64_t(d));
+  const u128 r = num - q * u128(uint64_t(d));
+  u128 qq = q;
+  if (r * 2 > u128(uint64_t(d)) || (r * 2 == u128(uint64_t(d)) && (q & 1))) qq = q + 1;
+  if (qq > u128(INT64_MAX)) return INT64_MAX;
+  return int64_t(qq);
+}
+// inv_frequency table: entry i = step^i computed by the sequential rounded
+// product chain of ops.rs:184-195.
+inline void rope_inv_freq_table(int64_t base, uint32_t freq_base_dim, uint32_t half, int64_t* out) {
+  const int64_t step = recip_acc(nth_root(base, freq_base_dim / 2));
+  int64_t f = kOneAcc;
+  for (uint32_t i = 0; i < half; ++i) { out[i] = f; f = acc_mul(f, step); }
+}
+
+// f32 -> Q16.16 / Q32.32 conversions from the IEEE-754 payload
+// (convert.rs:82-153): round half to even, saturate.
+inline int64_t f32_to_fixed(float x, unsigned frac, bool acc) {
+  uint32_t bits;
+  __builtin_memcpy(&bits, &x, 4);
+  const bool neg = bits >> 31;
+  const int eb = int((bits >> 23) & 0xff);
+  const uint32_t fb = bits & 0x7fffff;
+  const u128 maxpos = acc ? u128(INT64_MAX) : u128(INT32_MAX);
+  const u128 maxneg = acc ? (u128(1) << 63) : (u128(1) << 31);
+  if (eb == 0 && fb == 0) return 0;
+  u128 sig = eb == 0 ? u128(fb) : u128((1u << 23) | fb);
+  const int e = (eb == 0 ? -149 : eb - 150) + int(frac);
+  const u128 maxm = neg ? maxneg : maxpos;
+  u128 mag;
+  if (e >= 0) {
+    mag = (e >= 128 || sig > (maxm >> e)) ? maxm : (sig << e);
+  } else {
+    const unsigned s = unsigned(-e);
+    if (s >= 128) mag = 0;
+    else {
+      const u128 q = sig >> s, rem = sig & ((u128(1) << s) - 1), half = u128(1) << (s - 1);
+      mag = (rem > half || (rem == half && (q & 1))) ? q + 1 : q;
+    }
+    if (mag > maxm) mag = maxm;
+  }
+  if (neg) return mag >= maxneg ? -int64_t(maxneg - 1) - 1 : -int64_t(mag);
+  return int64_t(mag);
+}
+inline int32_t f32_to_act(float x) { return int32_t(f32_to_fixed(x, 16, false)); }
+inline int64_t f32_to_acc(float x) { return f32_to_fixed(x, 32, true); }
+
+}  // namespace det

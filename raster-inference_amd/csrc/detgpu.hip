@@ -1,0 +1,1288 @@
+// C ABI (include/detgpu.h) and the GPU executor of the deterministic path.
+//
+// Host side of the MI355X det path: context/stream management, weight upload
+// (int8 x row-scale factorization of detwgt v2 matrices), model resolution
+// mirroring load_det_num_gemma4_layer_weights (gemma/io.rs:1896-2045), and
+// the prefill_layer / decode_transition routines (det_kernels.rs:678-1267,
+// routines/*/native) driven as HIP kernel sequences on one stream.
+#include <hip/hip_runtime.h>
+#include <openssl/sha.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <numeric>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/detgpu.h"
+#include "det_arith.h"
+#include "kernels.h"
+
+using det::DevMatrix;
+
+namespace {
+
+struct Status : std::runtime_error {
+  int code;
+  Status(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+[[noreturn]] void bail(const std::string& m) { throw Status(1, m); }
+[[noreturn]] void contract(const std::string& m) { throw Status(2, m); }
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw Status(3, std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPC(x) hip_check((x), #x)
+
+thread_local std::string g_error;  // errors before a context exists
+
+}  // namespace
+
+struct det_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string last_error;
+  int8_t* limbs = nullptr;  // activation limb scratch for the int8 GEMV
+  size_t limbs_bytes = 0;
+  int64_t* argmax_scratch = nullptr;
+  size_t argmax_parts = 0;
+  uint32_t* argmax_out = nullptr;
+
+  void ensure_limbs(size_t bytes) {
+    if (bytes <= limbs_bytes) return;
+    HIPC(hipStreamSynchronize(stream));
+    if (limbs) HIPC(hipFree(limbs));
+    limbs = nullptr;
+    HIPC(hipMalloc(&limbs, bytes));
+    limbs_bytes = bytes;
+  }
+  uint32_t argmax(const int32_t* x, uint64_t n) {
+    const size_t parts = (n + 1023) / 1024;
+    if (parts > argmax_parts) {
+      HIPC(hipStreamSynchronize(stream));
+      if (argmax_scratch) HIPC(hipFree(argmax_scratch));
+      argmax_scratch = nullptr;
+      HIPC(hipMalloc(&argmax_scratch, parts * sizeof(int64_t)));
+      argmax_parts = parts;
+    }
+    det::launch_argmax(x, n, argmax_scratch, argmax_out, stream);
+    uint32_t r = 0;
+    HIPC(hipMemcpyAsync(&r, argmax_out, 4, hipMemcpyDeviceToHost, stream));
+    HIPC(hipStreamSynchronize(stream));
+    return r;
+  }
+};
+
+struct det_matrix {
+  det_ctx* ctx = nullptr;
+  DevMatrix m;
+};
+
+struct det_event {
+  hipEvent_t ev = nullptr;
+};
+
+namespace {
+
+template <class F>
+int guarded(det_ctx* ctx, F&& f) {
+  try {
+    f();
+    return 0;
+  } catch (const Status& e) {
+    (ctx ? ctx->last_error : g_error) = e.what();
+    return e.code;
+  } catch (const std::exception& e) {
+    (ctx ? ctx->last_error : g_error) = e.what();
+    return 3;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// weight upload
+// ---------------------------------------------------------------------------
+uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+void free_matrix(DevMatrix& m) {
+  if (!m.owns) return;
+  if (m.q) (void)hipFree(m.q);
+  if (m.scale) (void)hipFree(m.scale);
+  if (m.rowsum) (void)hipFree(m.rowsum);
+  if (m.w) (void)hipFree(m.w);
+  m = DevMatrix();
+}
+
+// Uploads int8 q (rows x cols) with per-row scales, padding rows to a multiple
+// of 128 bytes and computing the row sums used by the limb correction.
+DevMatrix upload_int8(det_ctx* ctx, uint64_t rows, uint64_t cols, const int8_t* q, const int32_t* scale) {
+  if (cols > 130000) bail("int8 rows longer than 130000 columns are not supported");
+  DevMatrix m;
+  m.rows = rows;
+  m.cols = cols;
+  m.storage = det::kInt8;
+  m.kpad = round_up(std::max<uint64_t>(cols, 1), 128);
+  std::vector<int8_t> padded(rows * m.kpad, 0);
+  std::vector<int32_t> rowsum(rows, 0);
+  for (uint64_t r = 0; r < rows; ++r) {
+    int32_t s = 0;
+    for (uint64_t c = 0; c < cols; ++c) {
+      padded[r * m.kpad + c] = q[r * cols + c];
+      s += q[r * cols + c];
+    }
+    rowsum[r] = s;
+  }
+  HIPC(hipMalloc(&m.q, std::max<size_t>(padded.size(), 1)));
+  HIPC(hipMalloc(&m.scale, std::max<size_t>(rows, 1) * 4));
+  HIPC(hipMalloc(&m.rowsum, std::max<size_t>(rows, 1) * 4));
+  HIPC(hipMemcpyAsync(m.q, padded.data(), padded.size(), hipMemcpyHostToDevice, ctx->stream));
+  HIPC(hipMemcpyAsync(m.scale, scale, rows * 4, hipMemcpyHostToDevice, ctx->stream));
+  HIPC(hipMemcpyAsync(m.rowsum, rowsum.data(), rows * 4, hipMemcpyHostToDevice, ctx->stream));
+  HIPC(hipStreamSynchronize(ctx->stream));
+  ctx->ensure_limbs(4 * 4 * m.kpad);
+  return m;
+}
+
+// Row mass bound (det_num/mod.rs:39-42).
+void check_row_mass(uint64_t rows, uint64_t cols, const std::vector<int64_t>& mass) {
+  for (uint64_t r = 0; r < rows; ++r)
+    if (mass[r] >= (int64_t(1) << 31)) bail("weight row mass violates the 2^31 overflow bound");
+  (void)cols;
+}
+
+DevMatrix upload_matrix(det_ctx* ctx, uint64_t rows, uint64_t cols, int width, const void* values,
+                        const int32_t* row_scale) {
+  if (width == 8) {
+    if (!row_scale) bail("int8 matrices need a row scale");
+    const int8_t* q = static_cast<const int8_t*>(values);
+    std::vector<int64_t> mass(rows, 0);
+    for (uint64_t r = 0; r < rows; ++r) {
+      int64_t s = 0;
+      for (uint64_t c = 0; c < cols; ++c) s += std::abs(int64_t(q[r * cols + c]));
+      mass[r] = s * std::abs(int64_t(row_scale[r]));
+    }
+    check_row_mass(rows, cols, mass);
+    return upload_int8(ctx, rows, cols, q, row_scale);
+  }
+  if (width != 16 && width != 32) bail("unsupported element width");
+  auto at = [&](uint64_t i) -> int32_t {
+    return width == 16 ? int32_t(static_cast<const int16_t*>(values)[i]) : static_cast<const int32_t*>(values)[i];
+  };
+  // Exact int8 factorization: s_r = gcd_c |W[r][c]|, q = W / s_r, valid when
+  // every |q| <= 127. Products q*s reproduce the Wgt bits exactly.
+  std::vector<int32_t> scale(rows, 1);
+  std::vector<int64_t> mass(rows, 0);
+  bool factor = true;
+  for (uint64_t r = 0; r < rows; ++r) {
+    uint64_t g = 0, mx = 0;
+    int64_t ms = 0;
+    for (uint64_t c = 0; c < cols; ++c) {
+      const uint64_t a = uint64_t(std::abs(int64_t(at(r * cols + c))));
+      g = std::gcd(g, a);
+      mx = std::max(mx, a);
+      ms += int64_t(a);
+    }
+    mass[r] = ms;
+    if (g == 0) g = 1;
+    if (mx / g > 127) factor = false;
+    scale[r] = int32_t(g);
+  }
+  check_row_mass(rows, cols, mass);
+  if (factor) {
+    std::vector<int8_t> q(rows * cols);
+    for (uint64_t r = 0; r < rows; ++r)
+      for (uint64_t c = 0; c < cols; ++c) q[r * cols + c] = int8_t(at(r * cols + c) / scale[r]);
+    return upload_int8(ctx, rows, cols, q.data(), scale.data());
+  }
+  DevMatrix m;
+  m.rows = rows;
+  m.cols = cols;
+  bool fits16 = true;
+  for (uint64_t i = 0; i < rows * cols && fits16; ++i) fits16 = at(i) >= INT16_MIN && at(i) <= INT16_MAX;
+  m.storage = fits16 ? det::kI16 : det::kI32;
+  const size_t esz = fits16 ? 2 : 4;
+  HIPC(hipMalloc(&m.w, std::max<size_t>(rows * cols * esz, 4)));
+  if ((width == 16) == fits16) {
+    HIPC(hipMemcpyAsync(m.w, values, rows * cols * esz, hipMemcpyHostToDevice, ctx->stream));
+  } else {
+    std::vector<int16_t> n16;
+    std::vector<int32_t> n32;
+    if (fits16) { n16.resize(rows * cols); for (uint64_t i = 0; i < rows * cols; ++i) n16[i] = int16_t(at(i)); }
+    else { n32.resize(rows * cols); for (uint64_t i = 0; i < rows * cols; ++i) n32[i] = at(i); }
+    HIPC(hipMemcpyAsync(m.w, fits16 ? (const void*)n16.data() : (const void*)n32.data(), rows * cols * esz,
+                        hipMemcpyHostToDevice, ctx->stream));
+  }
+  HIPC(hipStreamSynchronize(ctx->stream));
+  return m;
+}
+
+int32_t* upload_vec(det_ctx* ctx, const std::vector<int32_t>& v) {
+  int32_t* d = nullptr;
+  HIPC(hipMalloc(&d, std::max<size_t>(v.size(), 1) * 4));
+  HIPC(hipMemcpyAsync(d, v.data(), v.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+  HIPC(hipStreamSynchronize(ctx->stream));
+  return d;
+}
+
+// ---------------------------------------------------------------------------
+// SHA-256 commitments (transformer_kernels.rs:1395-1482)
+// ---------------------------------------------------------------------------
+struct Sha {
+  SHA256_CTX c;
+  Sha() { SHA256_Init(&c); }
+  void put(const void* p, size_t n) { SHA256_Update(&c, p, n); }
+  void u64(uint64_t v) {
+    uint8_t b[8];
+    for (int i = 0; i < 8; ++i) b[i] = uint8_t(v >> (8 * i));
+    put(b, 8);
+  }
+  // int32 values are little-endian on this host: hash the bytes directly.
+  void i32s(const int32_t* v, size_t n) { put(v, n * 4); }
+  void hex(char out[65]) {
+    uint8_t d[32];
+    SHA256_Final(d, &c);
+    static const char* H = "0123456789abcdef";
+    for (int i = 0; i < 32; ++i) { out[2 * i] = H[d[i] >> 4]; out[2 * i + 1] = H[d[i] & 15]; }
+    out[64] = 0;
+  }
+};
+void commit_rows(const int32_t* rows, uint64_t n, uint64_t width, char out[65]) {
+  Sha h;
+  static const char kDom[] = "raster-det-num-act-v1";
+  h.put(kDom, sizeof(kDom) - 1);
+  h.u64(n);
+  for (uint64_t r = 0; r < n; ++r) { h.u64(width); h.i32s(rows + r * width, width); }
+  h.hex(out);
+}
+void commit_vector(const int32_t* v, uint64_t n, char out[65]) {
+  Sha h;
+  static const char kDom[] = "raster-det-num-act-vector-v1";
+  h.put(kDom, sizeof(kDom) - 1);
+  h.u64(n);
+  h.i32s(v, n);
+  h.hex(out);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// model
+// ---------------------------------------------------------------------------
+namespace {
+
+struct HostTensor {
+  std::vector<uint64_t> shape;
+  std::vector<int32_t> vec;  // rank-1 tensors (Wgt bits)
+  DevMatrix mat;             // rank-2 tensors
+  bool is_matrix = false;
+};
+
+struct GLayer {
+  bool sliding = false;
+  uint64_t hidden = 0, num_heads = 0, num_kv_heads = 0, head_dim = 0;
+  std::optional<uint64_t> sliding_window, cache_sliding_window, donor;
+  int64_t eps = 0, rope_base = 0;
+  uint64_t rotary = 0, freq_base_dim = 0;
+  bool k_eq_v = false;
+  const DevMatrix *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr, *gate = nullptr, *up = nullptr,
+                  *down = nullptr, *ple_gate = nullptr, *ple_proj = nullptr;
+  int32_t *q_norm = nullptr, *k_norm = nullptr, *in_ln = nullptr, *post_attn_ln = nullptr, *pre_ff_ln = nullptr,
+          *post_ff_ln = nullptr, *ple_post_norm = nullptr;
+  bool has_ple = false;
+  std::optional<int32_t> layer_scalar;
+  int64_t* inv_freq = nullptr;  // rotary/2 entries
+};
+
+}  // namespace
+
+struct det_model {
+  det_ctx* ctx = nullptr;
+  det_text_config_t cfg{};
+  std::vector<int32_t> layer_types;
+  std::map<std::string, HostTensor> tensors;
+  bool finalized = false;
+  // resolved
+  const DevMatrix* embedding = nullptr;
+  int32_t embed_scale = 0;
+  std::vector<GLayer> layers;
+  bool has_ple = false;
+  uint64_t ple_dim = 0;
+  const DevMatrix* ple_tok = nullptr;  // [ple_vocab x L*ple]
+  std::vector<DevMatrix> ple_proj_views;
+  int32_t* ple_proj_norm = nullptr;
+  int32_t ple_embedding_scale = 0, ple_projection_scalar = 0, ple_input_scale = 0;
+  int32_t* final_norm = nullptr;
+  const DevMatrix* lm_head = nullptr;
+  std::optional<int32_t> softcap;
+  int64_t eps = 0;
+  uint64_t hidden = 0, vocab = 0;
+  std::vector<void*> owned_dev;
+
+  ~det_model() {
+    for (auto& kv : tensors)
+      if (kv.second.is_matrix) free_matrix(kv.second.mat);
+    for (void* p : owned_dev) (void)hipFree(p);
+  }
+  const HostTensor& need(const std::string& n) const {
+    auto it = tensors.find(n);
+    if (it == tensors.end()) bail("missing tensor `" + n + "`");
+    return it->second;
+  }
+  const DevMatrix* need_matrix(const std::string& n) const {
+    const HostTensor& t = need(n);
+    if (!t.is_matrix) bail("tensor `" + n + "` is not a matrix");
+    return &t.mat;
+  }
+  int32_t* need_vector(const std::string& n, uint64_t expect) {
+    const HostTensor& t = need(n);
+    if (t.is_matrix) bail("tensor `" + n + "` is not a vector");
+    if (expect && t.vec.size() != expect)
+      bail("rms norm width mismatch: " + std::to_string(expect) + " vs " + std::to_string(t.vec.size()));
+    int32_t* d = upload_vec(ctx, t.vec);
+    owned_dev.push_back(d);
+    return d;
+  }
+};
+
+namespace {
+
+// gemma/io.rs:165-190
+std::optional<uint64_t> kv_shared_layer_index(const det_model* m, uint64_t l) {
+  const uint64_t ns = m->cfg.has_num_kv_shared_layers ? m->cfg.num_kv_shared_layers : 0;
+  const uint64_t L = m->cfg.num_hidden_layers;
+  const uint64_t first = L > ns ? L - ns : 0;
+  if (ns == 0 || l < first) return std::nullopt;
+  for (uint64_t i = first; i-- > 0;)
+    if (m->layer_types[i] == m->layer_types[l]) return i;
+  bail("Gemma layer " + std::to_string(l) + " is configured to share KV without a prior donor layer");
+}
+
+void finalize(det_model* m) {
+  const det_text_config_t& c = m->cfg;
+  if (c.enable_moe_block) bail("only dense Gemma 4 layers are supported, not MoE checkpoints");
+  if (!c.hidden_activation_is_gelu_pytorch_tanh) bail("only gelu_pytorch_tanh is supported");
+  if (c.num_hidden_layers != m->layer_types.size()) bail("Gemma config layer count mismatch");
+  m->hidden = c.hidden_size;
+  m->eps = det::f32_to_acc(c.rms_norm_eps);
+  for (const char* n : {"model.language_model.embed_tokens.weight", "language_model.embed_tokens.weight",
+                        "embed_tokens.weight"}) {
+    auto it = m->tensors.find(n);
+    if (it != m->tensors.end() && it->second.is_matrix) { m->embedding = &it->second.mat; break; }
+  }
+  if (!m->embedding) bail("missing embedding tensor");
+  if (m->embedding->cols != c.hidden_size) bail("embedding tensor width mismatch");
+  m->embed_scale = det::f32_to_act(std::sqrt(float(m->embedding->cols)));
+
+  std::vector<bool> is_donor(c.num_hidden_layers, false);
+  for (uint64_t l = 0; l < c.num_hidden_layers; ++l)
+    if (auto d = kv_shared_layer_index(m, l)) is_donor[*d] = true;
+  const bool kev = c.has_attention_k_eq_v && c.attention_k_eq_v;
+  const uint64_t win = c.bidirectional_all ? c.sliding_window / 2 + 1 : c.sliding_window;
+  const uint64_t ple = c.has_hidden_size_per_layer_input ? c.hidden_size_per_layer_input : 0;
+  m->layers.assign(c.num_hidden_layers, GLayer());
+  for (uint64_t l = 0; l < c.num_hidden_layers; ++l) {
+    GLayer& L = m->layers[l];
+    const std::string p = "model.language_model.layers." + std::to_string(l);
+    L.sliding = m->layer_types[l] == 1;
+    L.head_dim = L.sliding ? c.head_dim : (c.has_global_head_dim ? c.global_head_dim : c.head_dim);
+    if (L.sliding) L.num_kv_heads = c.num_key_value_heads;
+    else if (kev) L.num_kv_heads = c.has_num_global_key_value_heads ? c.num_global_key_value_heads : c.num_key_value_heads;
+    else L.num_kv_heads = c.num_key_value_heads;
+    const float factor = c.has_full_partial_rotary_factor ? c.full_partial_rotary_factor : 0.25f;
+    L.rotary = L.sliding ? L.head_dim : uint64_t(float(L.head_dim) * factor);
+    L.donor = kv_shared_layer_index(m, l);
+    if (L.sliding) L.sliding_window = win;
+    if (L.sliding && !is_donor[l]) L.cache_sliding_window = win;
+    const float base = L.sliding ? (c.has_sliding_rope_theta ? c.sliding_rope_theta : 10000.0f)
+                                 : (c.has_full_rope_theta ? c.full_rope_theta
+                                                          : (c.has_rope_theta ? c.rope_theta : 1000000.0f));
+    L.rope_base = det::f32_to_acc(base);
+    L.freq_base_dim = L.head_dim;
+    L.hidden = c.hidden_size;
+    L.num_heads = c.num_attention_heads;
+    L.eps = m->eps;
+    L.k_eq_v = !L.sliding && kev;
+    L.q = m->need_matrix(p + ".self_attn.q_proj.weight");
+    L.k = m->need_matrix(p + ".self_attn.k_proj.weight");
+    const std::string vn = p + ".self_attn.v_proj.weight";
+    if (!L.k_eq_v || m->tensors.count(vn)) L.v = m->need_matrix(vn);
+    L.o = m->need_matrix(p + ".self_attn.o_proj.weight");
+    L.q_norm = m->need_vector(p + ".self_attn.q_norm.weight", L.head_dim);
+    L.k_norm = m->need_vector(p + ".self_attn.k_norm.weight", L.head_dim);
+    L.in_ln = m->need_vector(p + ".input_layernorm.weight", L.hidden);
+    L.post_attn_ln = m->need_vector(p + ".post_attention_layernorm.weight", L.hidden);
+    L.pre_ff_ln = m->need_vector(p + ".pre_feedforward_layernorm.weight", L.hidden);
+    L.post_ff_ln = m->need_vector(p + ".post_feedforward_layernorm.weight", L.hidden);
+    L.gate = m->need_matrix(p + ".mlp.gate_proj.weight");
+    L.up = m->need_matrix(p + ".mlp.up_proj.weight");
+    L.down = m->need_matrix(p + ".mlp.down_proj.weight");
+    if (ple > 0) {
+      L.has_ple = true;
+      L.ple_gate = m->need_matrix(p + ".per_layer_input_gate.weight");
+      L.ple_proj = m->need_matrix(p + ".per_layer_projection.weight");
+      L.ple_post_norm = m->need_vector(p + ".post_per_layer_input_norm.weight", L.hidden);
+    }
+    auto sc = m->tensors.find(p + ".layer_scalar");
+    if (sc != m->tensors.end()) {
+      if (sc->second.shape != std::vector<uint64_t>{1}) bail("layer_scalar must have shape [1]");
+      L.layer_scalar = sc->second.vec[0];
+    }
+    // shape checks the kernels rely on
+    if (L.num_kv_heads == 0 || L.num_heads / L.num_kv_heads == 0) bail("invalid Gemma head configuration");
+    if ((L.num_heads - 1) / (L.num_heads / L.num_kv_heads) >= L.num_kv_heads)
+      contract("query head maps past the last KV head");
+    if (L.q->cols != L.hidden || L.k->cols != L.hidden || (L.v && L.v->cols != L.hidden))
+      bail("attention projection input width mismatch");
+    if (L.q->rows != L.num_heads * L.head_dim) bail("q_proj rows do not match heads x head_dim");
+    if (L.k->rows != L.num_kv_heads * L.head_dim || (L.v && L.v->rows != L.k->rows))
+      bail("k/v_proj rows do not match kv heads x head_dim");
+    if (L.o->cols != L.num_heads * L.head_dim || L.o->rows != L.hidden) bail("o_proj shape mismatch");
+    if (L.gate->cols != L.hidden || L.up->cols != L.hidden || L.gate->rows != L.up->rows) bail("gate/up shape mismatch");
+    if (L.down->cols != L.gate->rows || L.down->rows != L.hidden) bail("down_proj shape mismatch");
+    if (L.has_ple && (L.ple_gate->cols != L.hidden || L.ple_proj->cols != L.ple_gate->rows || L.ple_proj->rows != L.hidden ||
+                      L.ple_gate->rows != ple))
+      bail("per-layer input projection shape mismatch");
+    if (L.rotary) {
+      if (L.rotary % 2) contract("rope_rotate_pairs requires an even rotary_dim");
+      if (L.rotary > L.head_dim) contract("rope_rotate_pairs requires rotary_dim to fit within the input width");
+      if (L.freq_base_dim < 2 || L.freq_base_dim % 2) contract("rope_rotate_pairs requires an even freq_base_dim of at least 2");
+      if (L.rope_base <= 0) contract("rope_rotate_pairs requires a positive base");
+      std::vector<int64_t> tab(L.rotary / 2);
+      det::rope_inv_freq_table(L.rope_base, uint32_t(L.freq_base_dim), uint32_t(L.rotary / 2), tab.data());
+      HIPC(hipMalloc(&L.inv_freq, tab.size() * 8));
+      HIPC(hipMemcpy(L.inv_freq, tab.data(), tab.size() * 8, hipMemcpyHostToDevice));
+      m->owned_dev.push_back(L.inv_freq);
+    }
+  }
+  if (ple > 0) {
+    m->has_ple = true;
+    m->ple_dim = ple;
+    const uint64_t pv = c.has_vocab_size_per_layer_input ? c.vocab_size_per_layer_input : c.vocab_size;
+    m->ple_tok = m->need_matrix("model.language_model.embed_tokens_per_layer.weight");
+    const DevMatrix* proj = m->need_matrix("model.language_model.per_layer_model_projection.weight");
+    if (m->ple_tok->rows < pv || m->ple_tok->cols < c.num_hidden_layers * ple) bail("PLE token embedding shape mismatch");
+    if (proj->rows < c.num_hidden_layers * ple || proj->cols != c.hidden_size) bail("PLE model projection shape mismatch");
+    for (uint64_t l = 0; l < c.num_hidden_layers; ++l) m->ple_proj_views.push_back(det::row_view(*proj, l * ple, ple));
+    m->ple_proj_norm = m->need_vector("model.language_model.per_layer_projection_norm.weight", ple);
+    m->ple_embedding_scale = det::f32_to_act(std::sqrt(float(ple)));
+    m->ple_projection_scalar = det::f32_to_act(std::pow(float(c.hidden_size), -0.5f));
+    m->ple_input_scale = det::f32_to_act(std::pow(2.0f, -0.5f));
+  }
+  m->final_norm = m->need_vector("model.language_model.norm.weight", c.hidden_size);
+  const bool tied = c.has_tie_word_embeddings ? c.tie_word_embeddings != 0 : true;
+  m->lm_head = tied ? m->embedding : m->need_matrix("model.language_model.lm_head.weight");
+  if (m->lm_head->cols != c.hidden_size) bail("logits projection input width mismatch");
+  m->vocab = m->lm_head->rows;
+  if (c.has_final_logit_softcapping) {
+    m->softcap = det::f32_to_act(c.final_logit_softcapping);
+    if (*m->softcap <= 0) contract("softcap_act requires a strictly positive softcap");
+  }
+  m->finalized = true;
+}
+
+// detwgt v2 reader (gemma/io.rs:224-387, DETWGT_V2_FORMAT.md).
+void load_detwgt(det_model* m, const uint8_t* b, size_t len) {
+  size_t cur = 0;
+  auto take = [&](size_t n) {
+    if (n > len - cur) bail("artifact ended unexpectedly");
+    const uint8_t* p = b + cur;
+    cur += n;
+    return p;
+  };
+  auto rd32 = [&]() { uint32_t v; std::memcpy(&v, take(4), 4); return v; };
+  auto rd64 = [&]() { uint64_t v; std::memcpy(&v, take(8), 8); return v; };
+  if (std::memcmp(take(8), "DNWGTV0\0", 8) != 0) bail("unsupported deterministic artifact magic");
+  if (rd32() != 2) bail("unsupported deterministic artifact format version; expected 2");
+  if (rd32() != 1) bail("unsupported deterministic artifact det_num spec version; expected 1");
+  const uint64_t count = rd64();
+  struct Rec { std::string name; std::vector<uint64_t> shape; int width; const uint8_t* data; };
+  std::vector<Rec> recs;
+  std::map<std::string, int> seen;
+  for (uint64_t i = 0; i < count; ++i) {
+    const uint32_t nl = rd32();
+    std::string name(reinterpret_cast<const char*>(take(nl)), nl);
+    const uint32_t rank = rd32();
+    std::vector<uint64_t> shape(rank);
+    uint64_t prod = 1;
+    for (auto& d : shape) {
+      d = rd64();
+      if (d && prod > UINT64_MAX / d) bail("tensor shape overflowed");
+      prod *= d;
+    }
+    if (rd64() != prod) bail("tensor `" + name + "` element count mismatch");
+    const uint32_t width = rd32();
+    if (width != 16 && width != 32) bail("tensor `" + name + "` has an invalid element width");
+    if (rd64() != prod * (width / 8)) bail("tensor `" + name + "` payload length mismatch");
+    const uint64_t mass = rd64();
+    if (rank >= 2 && mass >= (uint64_t(1) << 31)) bail("tensor `" + name + "` max row mass violates the overflow bound");
+    const size_t pad = (64 - cur % 64) % 64;
+    const uint8_t* pp = take(pad);
+    for (size_t k = 0; k < pad; ++k)
+      if (pp[k]) bail("tensor `" + name + "` has non-zero payload alignment padding");
+    const uint8_t* data = take(prod * (width / 8));
+    if (seen.count(name)) bail("deterministic artifact contains duplicate tensor `" + name + "`");
+    seen[name] = 1;
+    recs.push_back({name, shape, int(width), data});
+  }
+  if (cur != len) bail("deterministic artifact has trailing bytes after tensor payloads");
+  for (const Rec& r : recs) {
+    if (r.shape.size() > 2 || r.shape.empty()) continue;  // only vectors and matrices are used on this path
+    uint64_t dims[2] = {r.shape[0], r.shape.size() > 1 ? r.shape[1] : 0};
+    const int st = det_model_set_tensor(m, r.name.c_str(), r.shape.size(), dims, r.width, r.data, nullptr);
+    if (st) throw Status(st, m->ctx->last_error);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// per-sequence state
+// ---------------------------------------------------------------------------
+struct GKv {
+  bool has = false;  // LayerKvCache::det is Some
+  int32_t* k = nullptr;
+  int32_t* v = nullptr;
+  uint64_t cap = 0, row_w = 0, heads = 0, hd = 0;
+  bool ring = false;  // sliding-window cache of capacity == window
+  uint64_t start = 0, len = 0;
+};
+
+}  // namespace
+
+struct det_session {
+  det_model* m = nullptr;
+  uint64_t max_tokens = 0, position = 0;
+  std::vector<GKv> kv;
+  // device scratch (sized for max_tokens rows)
+  uint32_t* ids = nullptr;
+  int32_t *x = nullptr, *x2 = nullptr, *normed = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr,
+          *attn = nullptr, *gate = nullptr, *up = nullptr, *ple_all = nullptr, *pe = nullptr, *pp = nullptr,
+          *logits = nullptr, *dec_in = nullptr;
+  std::vector<void*> owned;
+  bool logits_valid = false;
+
+  ~det_session() {
+    for (auto& c : kv) {
+      if (c.k) (void)hipFree(c.k);
+      if (c.v) (void)hipFree(c.v);
+    }
+    for (void* p : owned) (void)hipFree(p);
+  }
+  template <class T>
+  T* alloc(uint64_t n) {
+    void* p = nullptr;
+    HIPC(hipMalloc(&p, std::max<uint64_t>(n, 1) * sizeof(T)));
+    owned.push_back(p);
+    return static_cast<T*>(p);
+  }
+};
+
+namespace {
+
+void session_alloc(det_session* s) {
+  det_model* m = s->m;
+  const uint64_t T = s->max_tokens, H = m->hidden;
+  uint64_t qw = 0, kw = 0, ffw = 0, plew = m->ple_dim;
+  for (const GLayer& L : m->layers) {
+    qw = std::max(qw, L.num_heads * L.head_dim);
+    kw = std::max(kw, L.num_kv_heads * L.head_dim);
+    ffw = std::max(ffw, L.gate->rows);
+  }
+  s->ids = s->alloc<uint32_t>(T);
+  s->x = s->alloc<int32_t>(T * H);
+  s->x2 = s->alloc<int32_t>(T * H);
+  s->normed = s->alloc<int32_t>(T * std::max(H, qw));
+  s->qb = s->alloc<int32_t>(T * qw);
+  s->kb = s->alloc<int32_t>(T * kw);
+  s->vb = s->alloc<int32_t>(T * kw);
+  s->attn = s->alloc<int32_t>(T * std::max(H, qw));
+  s->gate = s->alloc<int32_t>(T * std::max(ffw, H));
+  s->up = s->alloc<int32_t>(T * std::max(ffw, H));
+  s->ple_all = s->alloc<int32_t>(T * m->layers.size() * std::max<uint64_t>(plew, 1));
+  s->pe = s->alloc<int32_t>(T * std::max<uint64_t>(plew, 1));
+  s->pp = s->alloc<int32_t>(T * std::max<uint64_t>(std::max(plew, H), 1));
+  s->logits = s->alloc<int32_t>(m->vocab);
+  s->dec_in = s->alloc<int32_t>(H);
+  s->kv.assign(m->layers.size(), GKv());
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const GLayer& L = m->layers[l];
+    GKv& c = s->kv[l];
+    c.heads = L.num_kv_heads;
+    c.hd = L.head_dim;
+    c.row_w = L.num_kv_heads * L.head_dim;
+    if (L.donor) continue;  // shared layers never hold det data
+    c.ring = L.cache_sliding_window.has_value();
+    c.cap = c.ring ? std::min<uint64_t>(*L.cache_sliding_window, T) : T;
+    if (c.ring && c.cap == 0) c.cap = 1;
+    HIPC(hipMalloc(&c.k, std::max<uint64_t>(c.cap * c.row_w, 1) * 4));
+    HIPC(hipMalloc(&c.v, std::max<uint64_t>(c.cap * c.row_w, 1) * 4));
+  }
+}
+
+// KV commitment (transformer_kernels.rs:1460-1482) over all layers' caches.
+bool commit_kv(det_session* s, const std::vector<const GKv*>& caches, char out[65]) {
+  for (const GKv* c : caches)
+    if (!c->has) { out[0] = 0; return false; }
+  hipStream_t st = s->m->ctx->stream;
+  HIPC(hipStreamSynchronize(st));
+  Sha h;
+  static const char kDom[] = "raster-det-num-kv-cache-v1";
+  h.put(kDom, sizeof(kDom) - 1);
+  h.u64(caches.size());
+  std::vector<int32_t> buf;
+  for (const GKv* c : caches) {
+    h.u64(c->heads);
+    for (int side = 0; side < 2; ++side) {
+      const char kind = side ? 'v' : 'k';
+      h.put(&kind, 1);
+      h.u64(c->heads);
+      buf.resize(std::max<uint64_t>(c->cap * c->row_w, 1));
+      HIPC(hipMemcpy(buf.data(), side ? c->v : c->k, c->cap * c->row_w * 4, hipMemcpyDeviceToHost));
+      const uint64_t w = std::max<uint64_t>(c->hd, 1);
+      for (uint64_t hh = 0; hh < c->heads; ++hh) {
+        h.u64(c->len);
+        for (uint64_t r = 0; r < c->len; ++r) {
+          const uint64_t phys = c->ring ? (c->start + r) % c->cap : r;
+          h.u64(w);
+          h.i32s(buf.data() + phys * c->row_w + hh * c->hd, c->hd);
+        }
+      }
+    }
+  }
+  h.hex(out);
+  return true;
+}
+
+std::vector<const GKv*> all_caches(det_session* s) {
+  std::vector<const GKv*> v;
+  for (auto& c : s->kv) v.push_back(&c);
+  return v;
+}
+
+void linear(det_ctx* ctx, const DevMatrix& W, const int32_t* act, uint64_t m, int32_t* out) {
+  det::launch_linear(W, act, m, W.cols, out, W.rows, nullptr, ctx->limbs, ctx->stream);
+}
+
+void copy_d2d(det_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
+  if (bytes) HIPC(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+}
+
+// Q/K/V projections + head norms + RoPE for M rows at positions pos0.. (det_kernels.rs:499-566, 930-985).
+void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0) {
+  det_ctx* ctx = s->m->ctx;
+  hipStream_t st = ctx->stream;
+  const uint64_t qw = L.num_heads * L.head_dim, kw = L.num_kv_heads * L.head_dim;
+  linear(ctx, *L.q, s->normed, M, s->qb);
+  linear(ctx, *L.k, s->normed, M, s->kb);
+  if (L.v) linear(ctx, *L.v, s->normed, M, s->vb);
+  else if (L.k_eq_v) copy_d2d(ctx, s->vb, s->kb, M * kw * 4);
+  else bail("Gemma layer is missing v_proj without attention_k_eq_v enabled");
+  det::launch_rmsnorm(s->qb, M * L.num_heads, L.head_dim, L.head_dim, L.q_norm, L.eps, st);
+  det::launch_rmsnorm(s->kb, M * L.num_kv_heads, L.head_dim, L.head_dim, L.k_norm, L.eps, st);
+  det::launch_rmsnorm(s->vb, M * L.num_kv_heads, L.head_dim, L.head_dim, nullptr, L.eps, st);
+  if (L.rotary) {
+    det::launch_rope(s->qb, M, qw, L.num_heads, L.head_dim, L.rotary / 2, L.inv_freq, pos0, 1, st);
+    det::launch_rope(s->kb, M, kw, L.num_kv_heads, L.head_dim, L.rotary / 2, L.inv_freq, pos0, 1, st);
+  }
+}
+
+// Everything after attention: O proj, norms, residuals, MLP, PLE, scalar
+// (det_kernels.rs:733-818 / 1054-1128). Input residual in s->x, combined
+// attention heads in s->attn; result in s->x.
+void post_attention(det_session* s, const GLayer& L, uint64_t M, const int32_t* ple_in) {
+  det_ctx* ctx = s->m->ctx;
+  hipStream_t st = ctx->stream;
+  const uint64_t H = L.hidden;
+  linear(ctx, *L.o, s->attn, M, s->x2);
+  det::launch_rmsnorm(s->x2, M, H, H, L.post_attn_ln, L.eps, st);
+  det::launch_add_sat(s->x2, s->x, M * H, st);
+  std::swap(s->x, s->x2);
+  copy_d2d(ctx, s->normed, s->x, M * H * 4);
+  det::launch_rmsnorm(s->normed, M, H, H, L.pre_ff_ln, L.eps, st);
+  linear(ctx, *L.gate, s->normed, M, s->gate);
+  linear(ctx, *L.up, s->normed, M, s->up);
+  det::launch_gelu_mul(s->gate, s->up, M * L.gate->rows, st);
+  linear(ctx, *L.down, s->gate, M, s->x2);
+  det::launch_rmsnorm(s->x2, M, H, H, L.post_ff_ln, L.eps, st);
+  det::launch_add_sat(s->x2, s->x, M * H, st);
+  std::swap(s->x, s->x2);
+  if (L.has_ple && ple_in) {
+    const uint64_t P = L.ple_gate->rows;
+    linear(ctx, *L.ple_gate, s->x, M, s->gate);
+    det::launch_gelu_mul(s->gate, ple_in, M * P, st);
+    linear(ctx, *L.ple_proj, s->gate, M, s->x2);
+    det::launch_rmsnorm(s->x2, M, H, H, L.ple_post_norm, L.eps, st);
+    det::launch_add_sat(s->x2, s->x, M * H, st);
+    std::swap(s->x, s->x2);
+  }
+  if (L.layer_scalar) det::launch_scale(s->x, M * H, *L.layer_scalar, st);
+}
+
+// PLE inputs for M tokens of one layer into out [M x P]
+// (prefill_prepare_aux/native/tiles.rs:111-243, det_kernels.rs:1142-1208).
+void ple_inputs(det_session* s, uint64_t l, const uint32_t* ids_dev, const int32_t* input, uint64_t M, int32_t* out) {
+  det_model* m = s->m;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  const uint64_t P = m->ple_dim;
+  det::launch_gather_rows(*m->ple_tok, ids_dev, M, l * P, P, m->ple_embedding_scale, out, P, st);
+  det::launch_linear(m->ple_proj_views[l], input, M, m->hidden, s->pp, P, nullptr, ctx->limbs, st);
+  det::launch_scale(s->pp, M * P, m->ple_projection_scalar, st);
+  det::launch_rmsnorm(s->pp, M, P, P, m->ple_proj_norm, m->eps, st);
+  det::launch_add_sat(out, s->pp, M * P, st);
+  det::launch_scale(out, M * P, m->ple_input_scale, st);
+}
+
+void check_ids(det_model* m, const uint32_t* ids, uint64_t n) {
+  for (uint64_t i = 0; i < n; ++i) {
+    if (ids[i] >= m->embedding->rows) bail("token id " + std::to_string(ids[i]) + " is out of bounds for embedding tensor");
+    if (m->has_ple) {
+      const uint64_t pv = m->cfg.has_vocab_size_per_layer_input ? m->cfg.vocab_size_per_layer_input : m->cfg.vocab_size;
+      if (ids[i] >= pv) bail("matrix row is out of bounds for PLE slice");
+    }
+  }
+}
+
+void logits_from(det_session* s, const int32_t* hidden_row) {
+  det_model* m = s->m;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  copy_d2d(ctx, s->normed, hidden_row, m->hidden * 4);
+  det::launch_rmsnorm(s->normed, 1, m->hidden, m->hidden, m->final_norm, m->eps, st);
+  linear(ctx, *m->lm_head, s->normed, 1, s->logits);
+  if (m->softcap) det::launch_softcap(s->logits, m->vocab, *m->softcap, st);
+  s->logits_valid = true;
+}
+
+void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, det_prefill_result_t* out) {
+  det_model* m = s->m;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  if (n == 0) bail("transformer layer execution requires at least one activation row");
+  if (n > s->max_tokens) bail("prompt longer than the session capacity");
+  if (s->position != 0) bail("session already holds a prefilled sequence");
+  check_ids(m, ids, n);
+  const uint64_t H = m->hidden;
+  HIPC(hipMemcpyAsync(s->ids, ids, n * 4, hipMemcpyHostToDevice, st));
+  det::launch_gather_rows(*m->embedding, s->ids, n, 0, H, m->embed_scale, s->x, H, st);
+  std::vector<int32_t> host;
+  if (flags & DET_COMMIT_ACTIVATIONS) {
+    host.resize(n * H);
+    HIPC(hipMemcpyAsync(host.data(), s->x, n * H * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    commit_rows(host.data(), n, H, out->embedding);
+  }
+  const uint64_t P = m->ple_dim;
+  if (m->has_ple)
+    for (uint64_t l = 0; l < m->layers.size(); ++l)
+      if (m->layers[l].has_ple) ple_inputs(s, l, s->ids, s->x, n, s->ple_all + l * n * P);
+  for (uint64_t l = 0; l < m->layers.size(); ++l) {
+    const GLayer& L = m->layers[l];
+    // det_layer_prefill (det_kernels.rs:678-821)
+    copy_d2d(ctx, s->normed, s->x, n * H * 4);
+    det::launch_rmsnorm(s->normed, n, H, H, L.in_ln, L.eps, st);
+    qkv_block(s, L, n, 0);
+    const uint64_t kw = L.num_kv_heads * L.head_dim;
+    GKv& c = s->kv[l];
+    det::AttnArgs a{};
+    a.q = s->qb; a.q_ld = L.num_heads * L.head_dim;
+    a.out = s->attn; a.out_ld = L.num_heads * L.head_dim;
+    a.hd = uint32_t(L.head_dim); a.num_heads = uint32_t(L.num_heads);
+    a.groups = uint32_t(L.num_heads / L.num_kv_heads);
+    a.n_queries = uint32_t(n); a.causal = 1;
+    a.window = L.sliding ? *L.sliding_window : 0; a.causal_offset = 0;
+    if (L.donor) {
+      const GKv& d = s->kv[*L.donor];
+      if (!d.has) bail("deterministic attention requires canonical key cache rows");
+      if (d.row_w != kw) bail("layer cache head count mismatch");
+      a.k = d.k; a.v = d.v; a.kv_ld = d.row_w;
+      a.ring_start = d.start; a.ring_cap = d.ring ? d.cap : 0; a.avail = d.len;
+      if (d.len < n) contract("attention_softmax requires a non-empty logits slice");
+    } else {
+      // DetKvCacheData::from_head_slabs: keep the last rows past the window.
+      const uint64_t retained = c.ring ? (n > *L.cache_sliding_window ? n - *L.cache_sliding_window : 0) : 0;
+      const uint64_t kept = n - retained;
+      if (kept > c.cap) bail("KV cache capacity exceeded");
+      copy_d2d(ctx, c.k, s->kb + retained * kw, kept * kw * 4);
+      copy_d2d(ctx, c.v, s->vb + retained * kw, kept * kw * 4);
+      c.start = 0; c.len = kept; c.has = true;
+      a.k = s->kb; a.v = s->vb; a.kv_ld = kw; a.ring_start = 0; a.ring_cap = 0; a.avail = n;
+    }
+    if (a.avail > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
+    det::launch_attention(a, st);
+    post_attention(s, L, n, (m->has_ple && L.has_ple) ? s->ple_all + l * n * P : nullptr);
+  }
+  if (flags & DET_COMMIT_ACTIVATIONS) {
+    host.resize(n * H);
+    HIPC(hipMemcpyAsync(host.data(), s->x, n * H * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    commit_rows(host.data(), n, H, out->final_hidden);
+  }
+  logits_from(s, s->x + (n - 1) * H);
+  s->position = n;
+  if (flags & DET_COMMIT_ACTIVATIONS) {
+    std::vector<int32_t> lg(m->vocab);
+    HIPC(hipMemcpyAsync(lg.data(), s->logits, m->vocab * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    commit_vector(lg.data(), m->vocab, out->logits);
+  }
+  out->kv[0] = 0;
+  if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
+  out->next_token = ctx->argmax(s->logits, m->vocab);
+}
+
+struct LayerHook {
+  virtual void after_layer(det_session* s, uint64_t l) = 0;
+  virtual ~LayerHook() = default;
+};
+
+void decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t* out, LayerHook* hook) {
+  det_model* m = s->m;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  if (s->position == 0) bail("decode requires a prefilled session");
+  if (s->position >= s->max_tokens) bail("session capacity exhausted");
+  check_ids(m, &token, 1);
+  const uint64_t H = m->hidden;
+  HIPC(hipMemcpyAsync(s->ids, &token, 4, hipMemcpyHostToDevice, st));
+  det::launch_gather_rows(*m->embedding, s->ids, 1, 0, H, m->embed_scale, s->dec_in, H, st);
+  copy_d2d(ctx, s->x, s->dec_in, H * 4);
+  const uint64_t pos = s->position;
+  for (uint64_t l = 0; l < m->layers.size(); ++l) {
+    const GLayer& L = m->layers[l];
+    if (m->has_ple && L.has_ple) ple_inputs(s, l, s->ids, s->dec_in, 1, s->pe);
+    // det_layer_decode (det_kernels.rs:866-1133)
+    copy_d2d(ctx, s->normed, s->x, H * 4);
+    det::launch_rmsnorm(s->normed, 1, H, H, L.in_ln, L.eps, st);
+    qkv_block(s, L, 1, pos);
+    const uint64_t kw = L.num_kv_heads * L.head_dim;
+    GKv& own = s->kv[l];
+    if (!L.donor) {
+      // DetKvCacheData::append_rows with sliding-window trim (det_tensor.rs:308-337)
+      uint64_t slot;
+      if (!own.ring) {
+        if (own.len >= own.cap) bail("KV cache capacity exceeded");
+        slot = own.len++;
+      } else if (own.len < own.cap) {
+        slot = (own.start + own.len) % own.cap;
+        ++own.len;
+      } else {
+        slot = own.start;
+        own.start = (own.start + 1) % own.cap;
+      }
+      copy_d2d(ctx, own.k + slot * kw, s->kb, kw * 4);
+      copy_d2d(ctx, own.v + slot * kw, s->vb, kw * 4);
+      own.has = true;
+    }
+    const GKv& ac = L.donor ? s->kv[*L.donor] : own;
+    if (!ac.has) bail("deterministic attention requires canonical key cache rows");
+    if (ac.row_w != kw) bail("layer cache head count mismatch");
+    const uint64_t cur = ac.len;
+    const uint64_t key_start = L.sliding ? (cur > *L.sliding_window ? cur - *L.sliding_window : 0) : 0;
+    const uint64_t count = cur > key_start ? cur - key_start : 0;
+    if (count == 0) contract("attention_softmax requires a non-empty logits slice");
+    det::AttnArgs a{};
+    a.q = s->qb; a.q_ld = L.num_heads * L.head_dim;
+    a.k = ac.k; a.v = ac.v; a.kv_ld = kw;
+    a.ring_start = ac.start; a.ring_cap = ac.ring ? ac.cap : 0;
+    a.out = s->attn; a.out_ld = L.num_heads * L.head_dim;
+    a.hd = uint32_t(L.head_dim); a.num_heads = uint32_t(L.num_heads);
+    a.groups = uint32_t(L.num_heads / L.num_kv_heads);
+    a.n_queries = 1; a.causal = 0; a.fix_start = key_start; a.fix_count = count;
+    if (count > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
+    det::launch_attention(a, st);
+    post_attention(s, L, 1, (m->has_ple && L.has_ple) ? s->pe : nullptr);
+    if (hook) hook->after_layer(s, l);
+  }
+  std::vector<int32_t> host;
+  if (flags & DET_COMMIT_ACTIVATIONS) {
+    host.resize(H);
+    HIPC(hipMemcpyAsync(host.data(), s->x, H * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    commit_rows(host.data(), 1, H, out->activation);
+  }
+  logits_from(s, s->x);
+  s->position += 1;
+  if (flags & DET_COMMIT_ACTIVATIONS) {
+    std::vector<int32_t> lg(m->vocab);
+    HIPC(hipMemcpyAsync(lg.data(), s->logits, m->vocab * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    commit_vector(lg.data(), m->vocab, out->logits);
+  }
+  out->kv[0] = 0;
+  if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
+  out->next_token = ctx->argmax(s->logits, m->vocab);
+}
+
+std::unique_ptr<det_session> clone_session(const det_session* src) {
+  auto s = std::make_unique<det_session>();
+  s->m = src->m;
+  s->max_tokens = src->max_tokens;
+  session_alloc(s.get());
+  s->position = src->position;
+  det_ctx* ctx = src->m->ctx;
+  for (size_t l = 0; l < src->kv.size(); ++l) {
+    const GKv& a = src->kv[l];
+    GKv& b = s->kv[l];
+    b.has = a.has; b.start = a.start; b.len = a.len;
+    if (a.k) {
+      copy_d2d(ctx, b.k, a.k, a.cap * a.row_w * 4);
+      copy_d2d(ctx, b.v, a.v, a.cap * a.row_w * 4);
+    }
+  }
+  copy_d2d(ctx, s->logits, src->logits, src->m->vocab * 4);
+  s->logits_valid = src->logits_valid;
+  HIPC(hipStreamSynchronize(ctx->stream));
+  return s;
+}
+
+// First-step per-layer capture (det_goldens.rs:187-236): layer output and the
+// effective caches (updated layers 0..=l, original layers above).
+struct FirstStepHook : LayerHook {
+  det_session* original = nullptr;
+  std::string json;
+  void after_layer(det_session* s, uint64_t l) override {
+    det_model* m = s->m;
+    std::vector<int32_t> host(m->hidden);
+    HIPC(hipMemcpyAsync(host.data(), s->x, m->hidden * 4, hipMemcpyDeviceToHost, m->ctx->stream));
+    HIPC(hipStreamSynchronize(m->ctx->stream));
+    char out[65], kv[65];
+    commit_rows(host.data(), 1, m->hidden, out);
+    std::vector<const GKv*> eff;
+    for (uint64_t j = 0; j < s->kv.size(); ++j) eff.push_back(j <= l ? &s->kv[j] : &original->kv[j]);
+    const bool has = commit_kv(s, eff, kv);
+    if (!json.empty()) json += ",";
+    json += std::string("{\"layer_output\":\"") + out + "\",\"kv\":" + (has ? "\"" + std::string(kv) + "\"" : "null") + "}";
+  }
+};
+
+std::string capture(det_model* m, const uint32_t* ids, uint64_t n, uint64_t steps) {
+  det_session s0;
+  s0.m = m;
+  s0.max_tokens = n + steps + 1;
+  session_alloc(&s0);
+  det_prefill_result_t pr{};
+  prefill(&s0, ids, n, DET_COMMIT_ALL, &pr);
+  auto kvj = [](const char* kv) { return kv[0] ? "\"" + std::string(kv) + "\"" : std::string("null"); };
+  std::string out = std::string("{\"prefill\":{\"embedding\":\"") + pr.embedding + "\",\"final_hidden\":\"" +
+                    pr.final_hidden + "\",\"logits\":\"" + pr.logits + "\",\"kv\":" + kvj(pr.kv) + "},";
+  {
+    std::unique_ptr<det_session> copy = clone_session(&s0);
+    FirstStepHook hook;
+    hook.original = &s0;
+    det_decode_result_t dr{};
+    decode(copy.get(), pr.next_token, DET_COMMIT_NONE, &dr, &hook);
+    out += "\"first_step_layers\":[" + hook.json + "],";
+  }
+  out += "\"decode_steps\":[";
+  uint32_t tok = pr.next_token;
+  std::string ids_json = "[";
+  for (uint64_t i = 0; i < steps; ++i) {
+    det_decode_result_t dr{};
+    decode(&s0, tok, DET_COMMIT_ALL, &dr, nullptr);
+    if (i) { out += ","; ids_json += ","; }
+    ids_json += std::to_string(tok);
+    out += "{\"token\":" + std::to_string(tok) + ",\"activation\":\"" + dr.activation + "\",\"logits\":\"" + dr.logits +
+           "\",\"kv\":" + kvj(dr.kv) + "}";
+    tok = dr.next_token;
+  }
+  ids_json += "]";
+  Sha h;
+  h.put(ids_json.data(), ids_json.size());
+  char hx[65];
+  h.hex(hx);
+  out += "],\"end_to_end\":{\"generated_token_ids\":" + ids_json + ",\"generated_token_ids_sha256\":\"" + hx + "\"}}";
+  return out;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+const char* det_version(void) { return "detgpu 0.1 gfx950 (int8-limb MFMA GEMV, integer softmax attention)"; }
+
+int det_ctx_create(int device, det_ctx_t** out) {
+  return guarded(nullptr, [&] {
+    if (!out) bail("null output pointer");
+    int n = 0;
+    HIPC(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) bail("invalid HIP device " + std::to_string(device));
+    auto c = std::make_unique<det_ctx>();
+    c->device = device;
+    HIPC(hipSetDevice(device));
+    HIPC(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    HIPC(hipMalloc(&c->argmax_out, 4));
+    *out = c.release();
+  });
+}
+
+void det_ctx_destroy(det_ctx_t* ctx) {
+  if (!ctx) return;
+  (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->limbs) (void)hipFree(ctx->limbs);
+  if (ctx->argmax_scratch) (void)hipFree(ctx->argmax_scratch);
+  if (ctx->argmax_out) (void)hipFree(ctx->argmax_out);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+const char* det_ctx_last_error(const det_ctx_t* ctx) { return ctx ? ctx->last_error.c_str() : g_error.c_str(); }
+
+int det_ctx_synchronize(det_ctx_t* ctx) {
+  return guarded(ctx, [&] { HIPC(hipStreamSynchronize(ctx->stream)); });
+}
+
+int det_device_alloc(det_ctx_t* ctx, size_t bytes, void** out) {
+  return guarded(ctx, [&] { HIPC(hipMalloc(out, std::max<size_t>(bytes, 1))); });
+}
+int det_device_free(det_ctx_t* ctx, void* p) {
+  return guarded(ctx, [&] {
+    HIPC(hipStreamSynchronize(ctx->stream));
+    HIPC(hipFree(p));
+  });
+}
+int det_memcpy_h2d(det_ctx_t* ctx, void* dst, const void* src, size_t bytes) {
+  return guarded(ctx, [&] {
+    HIPC(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    HIPC(hipStreamSynchronize(ctx->stream));
+  });
+}
+int det_memcpy_d2h(det_ctx_t* ctx, void* dst, const void* src, size_t bytes) {
+  return guarded(ctx, [&] {
+    HIPC(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIPC(hipStreamSynchronize(ctx->stream));
+  });
+}
+int det_memcpy_d2d(det_ctx_t* ctx, void* dst, const void* src, size_t bytes) {
+  return guarded(ctx, [&] { copy_d2d(ctx, dst, src, bytes); });
+}
+
+int det_event_create(det_ctx_t* ctx, det_event_t** out) {
+  return guarded(ctx, [&] {
+    auto e = std::make_unique<det_event>();
+    HIPC(hipEventCreate(&e->ev));
+    *out = e.release();
+  });
+}
+int det_event_record(det_ctx_t* ctx, det_event_t* ev) {
+  return guarded(ctx, [&] { HIPC(hipEventRecord(ev->ev, ctx->stream)); });
+}
+int det_event_elapsed_ms(det_ctx_t* ctx, det_event_t* a, det_event_t* b, float* ms) {
+  return guarded(ctx, [&] {
+    HIPC(hipEventSynchronize(b->ev));
+    HIPC(hipEventElapsedTime(ms, a->ev, b->ev));
+  });
+}
+void det_event_destroy(det_event_t* ev) {
+  if (!ev) return;
+  (void)hipEventDestroy(ev->ev);
+  delete ev;
+}
+
+int det_matrix_upload(det_ctx_t* ctx, uint64_t rows, uint64_t cols, int width, const void* values,
+                      const int32_t* row_scale, det_matrix_t** out) {
+  return guarded(ctx, [&] {
+    if (!values && rows * cols) bail("null weight values");
+    auto m = std::make_unique<det_matrix>();
+    m->ctx = ctx;
+    m->m = upload_matrix(ctx, rows, cols, width, values, row_scale);
+    *out = m.release();
+  });
+}
+int det_matrix_info(const det_matrix_t* m, uint64_t* rows, uint64_t* cols, int* storage) {
+  if (!m) return 1;
+  if (rows) *rows = m->m.rows;
+  if (cols) *cols = m->m.cols;
+  if (storage) *storage = m->m.storage;
+  return 0;
+}
+void det_matrix_free(det_matrix_t* m) {
+  if (!m) return;
+  (void)hipStreamSynchronize(m->ctx->stream);
+  free_matrix(m->m);
+  delete m;
+}
+
+int det_linear(det_ctx_t* ctx, const det_matrix_t* w, const int32_t* act, int32_t* out) {
+  return guarded(ctx, [&] { det::launch_linear(w->m, act, 1, w->m.cols, out, w->m.rows, nullptr, ctx->limbs, ctx->stream); });
+}
+int det_linear_acc_i64(det_ctx_t* ctx, const det_matrix_t* w, const int32_t* act, int64_t* acc) {
+  return guarded(ctx, [&] { det::launch_linear(w->m, act, 1, w->m.cols, nullptr, w->m.rows, acc, ctx->limbs, ctx->stream); });
+}
+int det_linear_slab(det_ctx_t* ctx, const det_matrix_t* w, uint64_t m, const int32_t* act, int32_t* out) {
+  return guarded(ctx, [&] { det::launch_linear(w->m, act, m, w->m.cols, out, w->m.rows, nullptr, ctx->limbs, ctx->stream); });
+}
+int det_rms_norm(det_ctx_t* ctx, int32_t* x, uint64_t rows, uint64_t cols, const int32_t* w, int64_t eps) {
+  return guarded(ctx, [&] {
+    if (cols == 0) contract("rms_norm requires a non-empty input slice");
+    if (eps < 0) contract("rms_norm_scale requires a non-negative epsilon");
+    if (cols > UINT32_MAX) bail("row width should fit in u32");
+    det::launch_rmsnorm(x, rows, cols, cols, w, eps, ctx->stream);
+  });
+}
+int det_rope(det_ctx_t* ctx, int32_t* x, uint64_t rows, uint64_t heads, uint64_t hd, uint64_t rotary, uint64_t fbd,
+             int64_t base, uint64_t pos0, uint64_t pos_step) {
+  return guarded(ctx, [&] {
+    if (rotary == 0) return;
+    if (rotary % 2) contract("rope_rotate_pairs requires an even rotary_dim");
+    if (rotary > hd) contract("rope_rotate_pairs requires rotary_dim to fit within the input width");
+    if (fbd < 2 || fbd % 2) contract("rope_rotate_pairs requires an even freq_base_dim of at least 2");
+    if (base <= 0) contract("rope_rotate_pairs requires a positive base");
+    std::vector<int64_t> tab(rotary / 2);
+    det::rope_inv_freq_table(base, uint32_t(fbd), uint32_t(rotary / 2), tab.data());
+    int64_t* d = nullptr;
+    HIPC(hipMalloc(&d, tab.size() * 8));
+    HIPC(hipMemcpyAsync(d, tab.data(), tab.size() * 8, hipMemcpyHostToDevice, ctx->stream));
+    det::launch_rope(x, rows, heads * hd, heads, hd, rotary / 2, d, pos0, pos_step, ctx->stream);
+    HIPC(hipStreamSynchronize(ctx->stream));
+    HIPC(hipFree(d));
+  });
+}
+int det_attention_causal(det_ctx_t* ctx, const int32_t* q, const int32_t* k, const int32_t* v, uint64_t nq,
+                         uint64_t nrows, uint64_t nh, uint64_t nkv, uint64_t hd, uint64_t window, int32_t* out) {
+  return guarded(ctx, [&] {
+    if (nkv == 0 || nh / nkv == 0) bail("invalid Gemma head configuration");
+    if ((nh - 1) / (nh / nkv) >= nkv) contract("query head maps past the last KV head");
+    if (nq == 0 || nh == 0 || hd == 0) bail("empty attention problem");
+    if (nrows < nq) contract("attention_softmax requires a non-empty logits slice");
+    if (nrows > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
+    det::AttnArgs a{};
+    a.q = q; a.q_ld = nh * hd; a.k = k; a.v = v; a.kv_ld = nkv * hd;
+    a.out = out; a.out_ld = nh * hd; a.hd = uint32_t(hd); a.num_heads = uint32_t(nh);
+    a.groups = uint32_t(nh / nkv); a.n_queries = uint32_t(nq); a.causal = 1; a.window = window;
+    a.causal_offset = 0; a.avail = nrows;
+    det::launch_attention(a, ctx->stream);
+  });
+}
+int det_argmax_first(det_ctx_t* ctx, const int32_t* x, uint64_t n, uint32_t* index) {
+  return guarded(ctx, [&] {
+    if (n == 0) contract("argmax_first requires a non-empty slice");
+    *index = ctx->argmax(x, n);
+  });
+}
+int det_elementwise(det_ctx_t* ctx, int op, int32_t* x, const int32_t* y, uint64_t n, int32_t scalar) {
+  return guarded(ctx, [&] {
+    switch (op) {
+      case DET_EW_ADD: det::launch_add_sat(x, y, n, ctx->stream); break;
+      case DET_EW_GELU_MUL: det::launch_gelu_mul(x, y, n, ctx->stream); break;
+      case DET_EW_SCALE: det::launch_scale(x, n, scalar, ctx->stream); break;
+      case DET_EW_SOFTCAP:
+        if (scalar <= 0) contract("softcap_act requires a strictly positive softcap");
+        det::launch_softcap(x, n, scalar, ctx->stream);
+        break;
+      default: bail("unknown elementwise op");
+    }
+  });
+}
+
+int det_model_create(det_ctx_t* ctx, const det_text_config_t* cfg, det_model_t** out) {
+  return guarded(ctx, [&] {
+    auto m = std::make_unique<det_model>();
+    m->ctx = ctx;
+    m->cfg = *cfg;
+    if (cfg->num_layer_types && !cfg->layer_types) bail("layer_types pointer is null");
+    m->layer_types.assign(cfg->layer_types, cfg->layer_types + cfg->num_layer_types);
+    m->cfg.layer_types = nullptr;
+    *out = m.release();
+  });
+}
+
+int det_model_set_tensor(det_model_t* m, const char* name, uint64_t rank, const uint64_t* dims, int width,
+                         const void* values, const int32_t* row_scale) {
+  return guarded(m->ctx, [&] {
+    if (m->finalized) bail("model is already finalized");
+    if (rank < 1 || rank > 2) bail("tensor rank must be 1 or 2");
+    HostTensor t;
+    t.shape.assign(dims, dims + rank);
+    const uint64_t rows = rank == 2 ? dims[0] : 1, cols = rank == 2 ? dims[1] : dims[0];
+    if (rank == 2) {
+      t.is_matrix = true;
+      t.mat = upload_matrix(m->ctx, rows, cols, width, values, row_scale);
+    } else {
+      t.vec.resize(cols);
+      for (uint64_t i = 0; i < cols; ++i) {
+        int64_t v;
+        if (width == 8) v = int64_t(static_cast<const int8_t*>(values)[i]) * (row_scale ? row_scale[0] : 1);
+        else if (width == 16) v = static_cast<const int16_t*>(values)[i];
+        else if (width == 32) v = static_cast<const int32_t*>(values)[i];
+        else bail("unsupported element width");
+        if (v < INT32_MIN || v > INT32_MAX) bail("weight value does not fit Q16.16");
+        t.vec[i] = int32_t(v);
+      }
+    }
+    auto it = m->tensors.find(name);
+    if (it != m->tensors.end() && it->second.is_matrix) free_matrix(it->second.mat);
+    m->tensors[name] = std::move(t);
+  });
+}
+
+int det_model_load_detwgt(det_model_t* m, const uint8_t* bytes, size_t len) {
+  return guarded(m->ctx, [&] {
+    if (m->finalized) bail("model is already finalized");
+    load_detwgt(m, bytes, len);
+  });
+}
+int det_model_finalize(det_model_t* m) { return guarded(m->ctx, [&] { finalize(m); }); }
+void det_model_free(det_model_t* m) {
+  if (!m) return;
+  (void)hipStreamSynchronize(m->ctx->stream);
+  delete m;
+}
+
+int det_session_create(det_model_t* m, uint64_t max_tokens, det_session_t** out) {
+  return guarded(m->ctx, [&] {
+    if (!m->finalized) bail("model is not finalized");
+    if (max_tokens == 0) bail("max_tokens must be positive");
+    auto s = std::make_unique<det_session>();
+    s->m = m;
+    s->max_tokens = max_tokens;
+    session_alloc(s.get());
+    *out = s.release();
+  });
+}
+int det_session_clone(const det_session_t* src, det_session_t** out) {
+  return guarded(src->m->ctx, [&] { *out = clone_session(src).release(); });
+}
+void det_session_free(det_session_t* s) {
+  if (!s) return;
+  (void)hipStreamSynchronize(s->m->ctx->stream);
+  delete s;
+}
+int det_session_prefill(det_session_t* s, const uint32_t* ids, uint64_t n, uint32_t flags, det_prefill_result_t* out) {
+  return guarded(s->m->ctx, [&] {
+    det_prefill_result_t tmp{};
+    prefill(s, ids, n, flags, out ? out : &tmp);
+  });
+}
+int det_session_decode(det_session_t* s, uint32_t token, uint32_t flags, det_decode_result_t* out) {
+  return guarded(s->m->ctx, [&] {
+    det_decode_result_t tmp{};
+    decode(s, token, flags, out ? out : &tmp, nullptr);
+  });
+}
+int det_session_logits(det_session_t* s, int32_t* out, uint64_t n) {
+  return guarded(s->m->ctx, [&] {
+    if (!s->logits_valid) bail("no logits yet");
+    if (n != s->m->vocab) bail("logits length mismatch");
+    HIPC(hipMemcpyAsync(out, s->logits, n * 4, hipMemcpyDeviceToHost, s->m->ctx->stream));
+    HIPC(hipStreamSynchronize(s->m->ctx->stream));
+  });
+}
+int det_session_position(const det_session_t* s, uint64_t* position) {
+  *position = s->position;
+  return 0;
+}
+int det_capture(det_model_t* m, const uint32_t* prompt, uint64_t n, uint64_t steps, char* out, size_t cap) {
+  return guarded(m->ctx, [&] {
+    if (!m->finalized) bail("model is not finalized");
+    std::string s = capture(m, prompt, n, steps);
+    if (s.size() + 1 > cap) bail("capture output buffer too small: need " + std::to_string(s.size() + 1));
+    std::memcpy(out, s.c_str(), s.size() + 1);
+  });
+}
+
+}  // extern "C"

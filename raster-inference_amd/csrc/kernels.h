@@ -1,0 +1,80 @@
+// Launch-side declarations of the det-path HIP kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace det {
+
+// Weight storage of one det matrix on the device.
+enum Storage : int { kInt8 = 8, kI16 = 16, kI32 = 32 };
+
+struct DevMatrix {
+  uint64_t rows = 0, cols = 0;
+  int storage = kInt8;
+  // int8 form: q[rows][kpad] (zero padded), per-row integer scale and row sum.
+  uint64_t kpad = 0;
+  int8_t* q = nullptr;
+  int32_t* scale = nullptr;
+  int32_t* rowsum = nullptr;
+  // wide form: w[rows][cols] as int16 or int32 Wgt bits.
+  void* w = nullptr;
+  bool owns = true;  // false for row-range views
+};
+
+// A view of rows [r0, r0+n) of a matrix (shares storage).
+DevMatrix row_view(const DevMatrix& m, uint64_t r0, uint64_t n);
+
+// Activation limb planes for the int8 path: for each token row, four int8
+// planes of kpad bytes (byte j of a ^ 0x00808080, zero padded).
+void launch_act_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_act, uint64_t kpad,
+                      int8_t* limbs, hipStream_t s);
+
+// out[t][n] = requantize(sum_k act[t][k] * W[n][k]) for t < m; the raw
+// wrapped accumulators go to acc_out instead when it is non-null.
+// `limbs` is scratch of at least m * 4 * kpad bytes (int8 path only).
+void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,
+                   uint64_t ld_out, int64_t* acc_out, int8_t* limbs, hipStream_t s);
+
+void launch_rmsnorm(int32_t* x, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
+                    int64_t eps, hipStream_t s);
+void launch_rope(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t head_dim,
+                 uint64_t half, const int64_t* inv_freq, uint64_t pos0, uint64_t pos_step,
+                 hipStream_t s);
+
+struct AttnArgs {
+  const int32_t* q;  // query rows: q + t*q_ld + h*hd
+  uint64_t q_ld;
+  const int32_t* k;  // key rows: k + phys(r)*kv_ld + kvh*hd
+  const int32_t* v;
+  uint64_t kv_ld;
+  uint64_t ring_start, ring_cap;  // phys(r) = ring_cap ? (ring_start + r) % ring_cap : r
+  int32_t* out;  // out + t*out_ld + h*hd
+  uint64_t out_ld;
+  uint32_t hd, num_heads, groups;
+  uint32_t n_queries;
+  // rows for query t: [start_t, start_t + count_t) where, in causal mode,
+  // end_t = t + 1 + causal_offset, start_t = window ? max(0, end_t - window) : 0,
+  // both clamped to [0, avail); in fixed mode every query uses [fix_start, fix_start+fix_count).
+  int causal;
+  uint64_t window, causal_offset, avail;
+  uint64_t fix_start, fix_count;
+};
+// Windows longer than kMaxAttentionRows are rejected by the callers.
+constexpr uint64_t kMaxAttentionRows = 16000;
+void launch_attention(const AttnArgs& a, hipStream_t s);
+
+// Elementwise ops (saturating Q16.16).
+void launch_add_sat(int32_t* dst, const int32_t* src, uint64_t n, hipStream_t s);
+void launch_gelu_mul(int32_t* gate, const int32_t* up, uint64_t n, hipStream_t s);
+void launch_scale(int32_t* x, uint64_t n, int32_t scalar, hipStream_t s);
+void launch_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s);
+
+// Embedding-style gather: out[t][c] = mul_sat(Wgt(M[ids[t]][col0 + c]), scale).
+void launch_gather_rows(const DevMatrix& M, const uint32_t* ids, uint64_t m, uint64_t col0,
+                        uint64_t ncols, int32_t scale, int32_t* out, uint64_t ld_out, hipStream_t s);
+
+// First index of the maximum; `scratch` holds >= 2*ceil(n/1024) int64 values.
+void launch_argmax(const int32_t* x, uint64_t n, int64_t* scratch, uint32_t* out, hipStream_t s);
+
+}  // namespace det

@@ -1,0 +1,441 @@
+// HIP kernels of the deterministic integer transformer path for MI355X (gfx950).
+//
+// All reductions are integer: wrapping i64 MAC sums (any grouping is exact),
+// saturating sums of non-negative terms (any grouping gives min(sum, MAX)),
+// and (max, first index) selections. Results are therefore bit-identical to
+// the reference's serial order regardless of the launch shape.
+#include <hip/hip_runtime.h>
+
+#include "det_arith.h"
+#include "kernels.h"
+
+namespace det {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// wave / block reductions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t wave_sum_wrap(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = int64_t(uint64_t(v) + uint64_t(__shfl_xor(v, o, 64)));
+  return v;
+}
+__device__ __forceinline__ int64_t wave_sum_sat(int64_t v) {  // non-negative terms
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = add_sat64(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int64_t wave_max(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const int64_t w = __shfl_xor(v, o, 64);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+// Sortable key for "max value, first index": larger value wins, then smaller index.
+__device__ __forceinline__ int64_t argmax_key(int32_t value, uint32_t index) {
+  return (int64_t(value) * 4294967296ll) | int64_t(0xffffffffu - index);
+}
+__device__ __forceinline__ uint32_t key_index(int64_t key) { return 0xffffffffu - uint32_t(uint64_t(key)); }
+
+template <int NW>
+__device__ __forceinline__ int64_t block_reduce(int64_t v, int op, int64_t* red) {
+  // op 0: wrapping sum, 1: saturating sum of non-negatives, 2: max
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = op == 0 ? wave_sum_wrap(v) : (op == 1 ? wave_sum_sat(v) : wave_max(v));
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  int64_t r = red[0];
+  for (int w = 1; w < NW; ++w) {
+    const int64_t x = red[w];
+    r = op == 0 ? int64_t(uint64_t(r) + uint64_t(x)) : (op == 1 ? add_sat64(r, x) : (x > r ? x : r));
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// int8 x Q16.16 GEMV/GEMM via limb-decomposed activations on MFMA
+// ---------------------------------------------------------------------------
+// a = sum_j c_j 256^j + 8421504 with c_j = int8 byte j of (a ^ 0x00808080),
+// so sum_k a_k q_k = sum_j 256^j P_j + 8421504 * S where P_j = sum_k c_{j,k} q_k
+// (int8 x int8 -> i32 on the matrix cores) and S = sum_k q_k.
+__global__ void k_act_limbs(const int32_t* __restrict__ act, uint64_t m, uint64_t k, uint64_t ld,
+                            uint64_t kpad, int8_t* __restrict__ limbs) {
+  const uint64_t idx = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t t = blockIdx.y;
+  if (t >= m || idx >= kpad) return;
+  const uint32_t u = idx < k ? uint32_t(act[t * ld + idx]) ^ 0x00808080u : 0x00808080u;
+  int8_t* base = limbs + t * 4 * kpad + idx;
+  if (idx < k) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) base[j * kpad] = int8_t(uint8_t(u >> (8 * j)));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) base[j * kpad] = 0;
+  }
+}
+
+// One workgroup = 16 output rows x all of K; NW waves split K in 128-byte
+// steps. Lane (g = l/16, i = l%16) loads the 32 bytes [32g, 32g+32) of each
+// 128-byte step for weight row 16*tile + i (B operand) and for activation
+// limb row i = 4*token + limb (A operand). The 16x16 i32 result tile puts all
+// four limb sums of (token g, row i) in the four accumulator registers of
+// lane l, so the combine is lane-local.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ q,
+                                                    const int32_t* __restrict__ scale,
+                                                    const int32_t* __restrict__ rowsum,
+                                                    const int8_t* __restrict__ limbs, uint64_t n_rows,
+                                                    uint64_t kpad, uint32_t m, int32_t* __restrict__ out,
+                                                    uint64_t ld_out, int64_t* __restrict__ acc_out) {
+  __shared__ v4i part[NW][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const uint64_t row = uint64_t(blockIdx.x) * 16 + i;
+  const int at = i >> 2, aj = i & 3;
+  const bool a_on = uint32_t(at) < m;
+  const bool b_on = row < n_rows;
+  const uint64_t nsteps = kpad / 128;
+  const uint64_t per = (nsteps + NW - 1) / NW;
+  const uint64_t s0 = wave * per;
+  const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
+  const v4i* bp = reinterpret_cast<const v4i*>(q + (b_on ? row : 0) * kpad + 32 * g);
+  const v4i* ap = reinterpret_cast<const v4i*>(limbs + (a_on ? (uint64_t(at) * 4 + aj) : 0) * kpad + 32 * g);
+  const v4i zero = {0, 0, 0, 0};
+  v4i acc = zero;
+  uint64_t s = s0;
+  for (; s + 4 <= s1; s += 4) {
+    v4i b[8], a[8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      b[2 * u] = b_on ? __builtin_nontemporal_load(bp + (s + u) * 8) : zero;
+      b[2 * u + 1] = b_on ? __builtin_nontemporal_load(bp + (s + u) * 8 + 1) : zero;
+      a[2 * u] = a_on ? ap[(s + u) * 8] : zero;
+      a[2 * u + 1] = a_on ? ap[(s + u) * 8 + 1] : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+  }
+  for (; s < s1; ++s) {
+    const v4i b0 = b_on ? __builtin_nontemporal_load(bp + s * 8) : zero;
+    const v4i b1 = b_on ? __builtin_nontemporal_load(bp + s * 8 + 1) : zero;
+    const v4i a0 = a_on ? ap[s * 8] : zero;
+    const v4i a1 = a_on ? ap[s * 8 + 1] : zero;
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  // lane (g, i): token g, output row 16*tile + i; limb j in component j.
+  int64_t p[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const v4i v = part[w][lane];
+    p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+  }
+  if (uint32_t(g) >= m || !b_on) return;
+  const int64_t dot = p[0] + p[1] * 256 + p[2] * 65536 + p[3] * 16777216 + int64_t(8421504) * rowsum[row];
+  const int64_t a = int64_t(uint64_t(dot) * uint64_t(int64_t(scale[row])));
+  if (acc_out) acc_out[uint64_t(g) * ld_out + row] = a;
+  else out[uint64_t(g) * ld_out + row] = requant(a);
+}
+
+// Wide (i16 / i32 Wgt) GEMV on the vector ALUs: one wave per output row.
+template <class T>
+__global__ __launch_bounds__(256) void k_gemv_wide(const T* __restrict__ w, uint64_t n_rows, uint64_t k,
+                                                   const int32_t* __restrict__ act, uint64_t ld_act,
+                                                   uint32_t m, int32_t* __restrict__ out, uint64_t ld_out,
+                                                   int64_t* __restrict__ acc_out) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t row = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= n_rows) return;
+  const T* wr = w + row * k;
+  for (uint32_t t = 0; t < m; ++t) {
+    const int32_t* a = act + t * ld_act;
+    int64_t acc = 0;
+    for (uint64_t c = lane; c < k; c += 64) acc = mac(acc, a[c], int32_t(wr[c]));
+    acc = wave_sum_wrap(acc);
+    if (lane == 0) {
+      if (acc_out) acc_out[t * ld_out + row] = acc;
+      else out[t * ld_out + row] = requant(acc);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm (ops.rs:95-131, 406-425): one wave per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_rmsnorm(int32_t* __restrict__ x, uint64_t rows, uint64_t cols,
+                                                 uint64_t ld, const int32_t* __restrict__ w, int64_t eps) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t row = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  int32_t* xr = x + row * ld;
+  int64_t ss = 0;
+  for (uint64_t c = lane; c < cols; c += 64) ss = add_sat64(ss, sq_term(xr[c]));
+  ss = wave_sum_sat(ss);
+  const int32_t scale = rms_scale_from_sumsq(ss, uint32_t(cols), eps);
+  for (uint64_t c = lane; c < cols; c += 64) {
+    const int32_t y = mul_sat(xr[c], scale);
+    xr[c] = w ? mul_sat(y, w[c]) : y;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RoPE (ops.rs:151-196): one thread per (row, head, pair).
+// ---------------------------------------------------------------------------
+__global__ void k_rope(int32_t* __restrict__ x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t hd,
+                       uint64_t half, const int64_t* __restrict__ inv_freq, uint64_t pos0, uint64_t pos_step) {
+  const uint64_t idx = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t total = rows * heads * half;
+  if (idx >= total) return;
+  const uint64_t i = idx % half;
+  const uint64_t h = (idx / half) % heads;
+  const uint64_t r = idx / (half * heads);
+  const uint64_t pos = pos0 + r * pos_step;
+  if (pos == 0) return;  // identity (ops.rs:179-181)
+  int32_t c, s;
+  sin_cos(rope_angle(pos, inv_freq[i]), &c, &s);
+  int32_t* base = x + r * ld + h * hd;
+  const int32_t lhs = base[i], rhs = base[i + half];
+  base[i] = sub_sat(mul_sat(lhs, c), mul_sat(rhs, s));
+  base[i + half] = add_sat(mul_sat(rhs, c), mul_sat(lhs, s));
+}
+
+// ---------------------------------------------------------------------------
+// Attention for one (head, query): score dots -> integer softmax -> weighted
+// sum (det_kernels.rs:340-367, ops.rs:230-258).
+// ---------------------------------------------------------------------------
+constexpr int kAttnThreads = 256;
+constexpr int kAttnWaves = kAttnThreads / 64;
+constexpr uint64_t kMaxAttnRows = 16000;  // LDS: one int32 per window row
+
+__global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
+  extern __shared__ int32_t lds_w[];  // one int32 per window row (scores, then weights)
+  __shared__ int64_t red[kAttnWaves];
+  __shared__ int64_t bcast[2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t h = blockIdx.x, t = blockIdx.y;
+  const uint32_t kvh = h / a.groups;
+  uint64_t start, count;
+  if (a.causal) {
+    uint64_t end = t + 1 + a.causal_offset;
+    start = (a.window && end > a.window) ? end - a.window : 0;
+    if (start > a.avail) start = a.avail;
+    if (end > a.avail) end = a.avail;
+    count = end > start ? end - start : 0;
+  } else {
+    start = a.fix_start;
+    count = a.fix_count;
+  }
+  if (count == 0) return;  // host validation makes every window non-empty
+  const int32_t* qrow = a.q + uint64_t(t) * a.q_ld + uint64_t(h) * a.hd;
+  int32_t* orow = a.out + uint64_t(t) * a.out_ld + uint64_t(h) * a.hd;
+  // 1. scores (wave per row, lanes over head dims)
+  for (uint64_t r = wave; r < count; r += kAttnWaves) {
+    uint64_t phys = start + r;
+    if (a.ring_cap) phys = (a.ring_start + phys) % a.ring_cap;
+    const int32_t* krow = a.k + phys * a.kv_ld + uint64_t(kvh) * a.hd;
+    int64_t acc = 0;
+    for (uint32_t d = lane; d < a.hd; d += 64) acc = mac(acc, qrow[d], krow[d]);
+    acc = wave_sum_wrap(acc);
+    if (lane == 0) lds_w[r] = requant(acc);
+  }
+  __syncthreads();
+  // 2. first argmax
+  int64_t best = INT64_MIN;
+  for (uint64_t r = threadIdx.x; r < count; r += kAttnThreads) {
+    const int64_t key = argmax_key(lds_w[r], uint32_t(r));
+    best = key > best ? key : best;
+  }
+  best = block_reduce<kAttnWaves>(best, 2, red);
+  const uint32_t max_idx = key_index(best);
+  const int32_t max_logit = lds_w[max_idx];
+  // 3. saturating sum of exp terms
+  int64_t sum = 0;
+  for (uint64_t r = threadIdx.x; r < count; r += kAttnThreads) sum = add_sat64(sum, softmax_exp(lds_w[r], max_logit));
+  sum = block_reduce<kAttnWaves>(sum, 1, red);
+  __syncthreads();
+  // 4. weights (in place) and their saturating sum
+  int64_t wsum = 0;
+  for (uint64_t r = threadIdx.x; r < count; r += kAttnThreads) {
+    const int32_t wgt = softmax_weight(softmax_exp(lds_w[r], max_logit), sum);
+    lds_w[r] = wgt;
+    wsum = add_sat64(wsum, int64_t(wgt));
+  }
+  wsum = block_reduce<kAttnWaves>(wsum, 1, red);
+  if (threadIdx.x == 0) {
+    const int32_t summed = sat32(wsum);
+    const int32_t residual = sub_sat(kOneAct, summed);
+    lds_w[max_idx] = add_sat(lds_w[max_idx], residual);
+  }
+  __syncthreads();
+  // 5. weighted sum over value rows
+  for (uint32_t d = threadIdx.x; d < a.hd; d += kAttnThreads) {
+    int64_t acc = 0;
+    for (uint64_t r = 0; r < count; ++r) {
+      uint64_t phys = start + r;
+      if (a.ring_cap) phys = (a.ring_start + phys) % a.ring_cap;
+      acc = mac(acc, a.v[phys * a.kv_ld + uint64_t(kvh) * a.hd + d], lds_w[r]);
+    }
+    orow[d] = requant(acc);
+  }
+  (void)bcast;
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise
+// ---------------------------------------------------------------------------
+__global__ void k_add_sat(int32_t* __restrict__ d, const int32_t* __restrict__ s, uint64_t n) {
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) d[i] = add_sat(d[i], s[i]);
+}
+__global__ void k_gelu_mul(int32_t* __restrict__ g, const int32_t* __restrict__ u, uint64_t n) {
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) g[i] = mul_sat(gelu_act(g[i]), u[i]);
+}
+__global__ void k_scale(int32_t* __restrict__ x, uint64_t n, int32_t s) {
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = mul_sat(x[i], s);
+}
+__global__ void k_softcap(int32_t* __restrict__ x, uint64_t n, int32_t cap) {
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = softcap_act(x[i], cap);
+}
+
+__device__ __forceinline__ int32_t wgt_at(const DevMatrix& M, uint64_t r, uint64_t c) {
+  if (M.storage == kInt8) return int32_t(M.q[r * M.kpad + c]) * M.scale[r];
+  if (M.storage == kI16) return int32_t(static_cast<const int16_t*>(M.w)[r * M.cols + c]);
+  return static_cast<const int32_t*>(M.w)[r * M.cols + c];
+}
+__global__ void k_gather_rows(DevMatrix M, const uint32_t* __restrict__ ids, uint64_t m, uint64_t col0,
+                              uint64_t ncols, int32_t scale, int32_t* __restrict__ out, uint64_t ld_out) {
+  const uint64_t c = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t t = blockIdx.y;
+  if (c >= ncols || t >= m) return;
+  out[t * ld_out + c] = mul_sat(wgt_at(M, ids[t], col0 + c), scale);
+}
+
+__global__ __launch_bounds__(256) void k_argmax_partial(const int32_t* __restrict__ x, uint64_t n,
+                                                        int64_t* __restrict__ part) {
+  __shared__ int64_t red[4];
+  int64_t best = INT64_MIN;
+  const uint64_t base = uint64_t(blockIdx.x) * 1024;
+  for (uint64_t i = base + threadIdx.x; i < base + 1024 && i < n; i += 256) {
+    const int64_t key = argmax_key(x[i], uint32_t(i));
+    best = key > best ? key : best;
+  }
+  best = block_reduce<4>(best, 2, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = best;
+}
+__global__ __launch_bounds__(256) void k_argmax_final(const int64_t* __restrict__ part, uint64_t nparts,
+                                                      uint32_t* __restrict__ out) {
+  __shared__ int64_t red[4];
+  int64_t best = INT64_MIN;
+  for (uint64_t i = threadIdx.x; i < nparts; i += 256) best = part[i] > best ? part[i] : best;
+  best = block_reduce<4>(best, 2, red);
+  if (threadIdx.x == 0) *out = key_index(best);
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+static inline unsigned blocks_for(uint64_t n, unsigned per) { return unsigned((n + per - 1) / per); }
+
+DevMatrix row_view(const DevMatrix& m, uint64_t r0, uint64_t n) {
+  DevMatrix v = m;
+  v.rows = n;
+  v.owns = false;
+  if (m.storage == kInt8) {
+    v.q = m.q + r0 * m.kpad;
+    v.scale = m.scale + r0;
+    v.rowsum = m.rowsum + r0;
+  } else if (m.storage == kI16) {
+    v.w = static_cast<int16_t*>(m.w) + r0 * m.cols;
+  } else {
+    v.w = static_cast<int32_t*>(m.w) + r0 * m.cols;
+  }
+  return v;
+}
+
+void launch_act_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld, uint64_t kpad, int8_t* limbs,
+                      hipStream_t s) {
+  dim3 grid(blocks_for(kpad, 256), unsigned(m));
+  hipLaunchKernelGGL(k_act_limbs, grid, dim3(256), 0, s, act, m, k, ld, kpad, limbs);
+}
+
+void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,
+                   uint64_t ld_out, int64_t* acc_out, int8_t* limbs, hipStream_t s) {
+  if (W.rows == 0 || m == 0) return;
+  if (W.storage == kInt8) {
+    // tokens in groups of 4 (one 16-row MFMA A tile = 4 tokens x 4 limbs)
+    for (uint64_t t0 = 0; t0 < m; t0 += 4) {
+      const uint32_t mm = uint32_t(m - t0 < 4 ? m - t0 : 4);
+      launch_act_limbs(act + t0 * ld_act, mm, W.cols, ld_act, W.kpad, limbs, s);
+      hipLaunchKernelGGL(k_gemv_i8<8>, dim3(blocks_for(W.rows, 16)), dim3(512), 0, s, W.q, W.scale, W.rowsum,
+                         limbs, W.rows, W.kpad, mm, acc_out ? nullptr : out + t0 * ld_out, ld_out,
+                         acc_out ? acc_out + t0 * ld_out : nullptr);
+    }
+  } else if (W.storage == kI16) {
+    hipLaunchKernelGGL(k_gemv_wide<int16_t>, dim3(blocks_for(W.rows, 4)), dim3(256), 0, s,
+                       static_cast<const int16_t*>(W.w), W.rows, W.cols, act, ld_act, uint32_t(m), out, ld_out,
+                       acc_out);
+  } else {
+    hipLaunchKernelGGL(k_gemv_wide<int32_t>, dim3(blocks_for(W.rows, 4)), dim3(256), 0, s,
+                       static_cast<const int32_t*>(W.w), W.rows, W.cols, act, ld_act, uint32_t(m), out, ld_out,
+                       acc_out);
+  }
+}
+
+void launch_rmsnorm(int32_t* x, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w, int64_t eps,
+                    hipStream_t s) {
+  if (rows == 0) return;
+  hipLaunchKernelGGL(k_rmsnorm, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, rows, cols, ld, w, eps);
+}
+
+void launch_rope(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t hd, uint64_t half,
+                 const int64_t* inv_freq, uint64_t pos0, uint64_t pos_step, hipStream_t s) {
+  const uint64_t total = rows * heads * half;
+  if (total == 0) return;
+  hipLaunchKernelGGL(k_rope, dim3(blocks_for(total, 256)), dim3(256), 0, s, x, rows, ld, heads, hd, half, inv_freq,
+                     pos0, pos_step);
+}
+
+void launch_attention(const AttnArgs& a, hipStream_t s) {
+  if (a.n_queries == 0 || a.num_heads == 0) return;
+  uint64_t max_rows = a.causal ? (a.avail) : a.fix_count;
+  if (max_rows == 0) max_rows = 1;
+  if (max_rows > kMaxAttnRows) return;  // callers validate against kMaxAttnRows
+  const size_t lds = size_t(max_rows) * sizeof(int32_t);
+  hipLaunchKernelGGL(k_attention, dim3(a.num_heads, a.n_queries), dim3(kAttnThreads), lds, s, a);
+}
+
+void launch_add_sat(int32_t* d, const int32_t* src, uint64_t n, hipStream_t s) {
+  if (n) hipLaunchKernelGGL(k_add_sat, dim3(blocks_for(n, 256)), dim3(256), 0, s, d, src, n);
+}
+void launch_gelu_mul(int32_t* g, const int32_t* u, uint64_t n, hipStream_t s) {
+  if (n) hipLaunchKernelGGL(k_gelu_mul, dim3(blocks_for(n, 256)), dim3(256), 0, s, g, u, n);
+}
+void launch_scale(int32_t* x, uint64_t n, int32_t sc, hipStream_t s) {
+  if (n) hipLaunchKernelGGL(k_scale, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, n, sc);
+}
+void launch_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s) {
+  if (n) hipLaunchKernelGGL(k_softcap, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, n, cap);
+}
+void launch_gather_rows(const DevMatrix& M, const uint32_t* ids, uint64_t m, uint64_t col0, uint64_t ncols,
+                        int32_t scale, int32_t* out, uint64_t ld_out, hipStream_t s) {
+  if (!m || !ncols) return;
+  hipLaunchKernelGGL(k_gather_rows, dim3(blocks_for(ncols, 256), unsigned(m)), dim3(256), 0, s, M, ids, m, col0,
+                     ncols, scale, out, ld_out);
+}
+void launch_argmax(const int32_t* x, uint64_t n, int64_t* scratch, uint32_t* out, hipStream_t s) {
+  const uint64_t parts = (n + 1023) / 1024;
+  hipLaunchKernelGGL(k_argmax_partial, dim3(unsigned(parts)), dim3(256), 0, s, x, n, scratch);
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, scratch, parts, out);
+}
+
+}  // namespace det
