@@ -6,6 +6,8 @@
 // the reference's serial order regardless of the launch shape.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "det_arith.h"
 #include "kernels.h"
 
@@ -142,6 +144,110 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
   const int64_t a = int64_t(uint64_t(dot) * uint64_t(int64_t(scale[row])));
   if (acc_out) acc_out[uint64_t(g) * ld_out + row] = a;
   else out[uint64_t(g) * ld_out + row] = requant(a);
+}
+
+
+// Single-kernel variant: the workgroup converts the activation rows into limb
+// planes in LDS once, then walks 16-row tiles persistently. KSPLIT waves
+// share one tile (split K, partials combined through LDS); 8/KSPLIT tiles run
+// side by side per workgroup iteration.
+constexpr int kGemvThreads = 512;
+constexpr uint64_t kGemvLdsBudget = 64 * 1024;
+
+__device__ __forceinline__ int64_t limb_combine(const int64_t p[4], int32_t rowsum, int32_t scale) {
+  const int64_t dot = p[0] + p[1] * 256 + p[2] * 65536 + p[3] * 16777216 + int64_t(8421504) * rowsum;
+  return int64_t(uint64_t(dot) * uint64_t(int64_t(scale)));
+}
+
+template <int KSPLIT>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
+    const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
+    const int32_t* __restrict__ act, uint64_t ld_act, uint64_t k, uint64_t n_rows, uint64_t kpad, uint32_t m,
+    int32_t* __restrict__ out, uint64_t ld_out, int64_t* __restrict__ acc_out) {
+  extern __shared__ __attribute__((aligned(16))) int8_t lds_limbs[];
+  __shared__ v4i part[KSPLIT > 1 ? 8 : 1][64];
+  constexpr int TPW = 8 / KSPLIT;
+  const uint64_t pstride = kpad + 32;
+  // prologue: limb planes, 4 activations per thread-iteration
+  for (uint64_t idx = threadIdx.x; idx < uint64_t(m) * (kpad / 4); idx += kGemvThreads) {
+    const uint64_t t = idx / (kpad / 4), c = (idx % (kpad / 4)) * 4;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = c + e < k ? uint32_t(act[t * ld_act + c + e]) ^ 0x00808080u : 0u;
+    // padded columns get limb bytes 0 (their weights are zero as well)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t b = (c + e < k) ? ((w[e] >> (8 * j)) & 0xffu) : 0u;
+        packed |= b << (8 * e);
+      }
+      *reinterpret_cast<uint32_t*>(lds_limbs + (t * 4 + j) * pstride + c) = packed;
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const int slot = wave / KSPLIT, kp = wave % KSPLIT;
+  const int at = i >> 2, aj = i & 3;
+  const bool a_on = uint32_t(at) < m;
+  const int8_t* abase = lds_limbs + (a_on ? (uint64_t(at) * 4 + aj) : 0) * pstride + 32 * g;
+  const uint64_t nsteps = kpad / 128;
+  const uint64_t per = (nsteps + KSPLIT - 1) / KSPLIT;
+  const uint64_t s0 = kp * per;
+  const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
+  const uint64_t ntiles = (n_rows + 15) / 16;
+  const v4i zero = {0, 0, 0, 0};
+  for (uint64_t base = uint64_t(blockIdx.x) * TPW; base < ntiles; base += uint64_t(gridDim.x) * TPW) {
+    const uint64_t tile = base + slot;
+    const uint64_t row = tile * 16 + i;
+    const bool b_on = tile < ntiles && row < n_rows;
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (b_on ? row : 0) * kpad + 32 * g);
+    v4i acc = zero;
+    uint64_t s = s0;
+    for (; s + 4 <= s1; s += 4) {
+      v4i b[8], a[8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        b[2 * u] = b_on ? __builtin_nontemporal_load(bp + (s + u) * 8) : zero;
+        b[2 * u + 1] = b_on ? __builtin_nontemporal_load(bp + (s + u) * 8 + 1) : zero;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a[2 * u] = a_on ? *reinterpret_cast<const v4i*>(abase + (s + u) * 128) : zero;
+        a[2 * u + 1] = a_on ? *reinterpret_cast<const v4i*>(abase + (s + u) * 128 + 16) : zero;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+    }
+    for (; s < s1; ++s) {
+      const v4i b0 = b_on ? __builtin_nontemporal_load(bp + s * 8) : zero;
+      const v4i b1 = b_on ? __builtin_nontemporal_load(bp + s * 8 + 1) : zero;
+      const v4i a0 = a_on ? *reinterpret_cast<const v4i*>(abase + s * 128) : zero;
+      const v4i a1 = a_on ? *reinterpret_cast<const v4i*>(abase + s * 128 + 16) : zero;
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+    }
+    int64_t p[4] = {acc[0], acc[1], acc[2], acc[3]};
+    if (KSPLIT > 1) {
+      part[wave][lane] = acc;
+      __syncthreads();
+      if (kp == 0) {
+#pragma unroll
+        for (int w = 1; w < KSPLIT; ++w) {
+          const v4i v = part[wave + w][lane];
+          p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+        }
+      }
+      __syncthreads();
+    }
+    if (kp == 0 && uint32_t(g) < m && b_on) {
+      const int64_t a = limb_combine(p, rowsum[row], scale[row]);
+      if (acc_out) acc_out[uint64_t(g) * ld_out + row] = a;
+      else out[uint64_t(g) * ld_out + row] = requant(a);
+    }
+  }
 }
 
 // Wide (i16 / i32 Wgt) GEMV on the vector ALUs: one wave per output row.
@@ -375,10 +481,32 @@ void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t 
     // tokens in groups of 4 (one 16-row MFMA A tile = 4 tokens x 4 limbs)
     for (uint64_t t0 = 0; t0 < m; t0 += 4) {
       const uint32_t mm = uint32_t(m - t0 < 4 ? m - t0 : 4);
-      launch_act_limbs(act + t0 * ld_act, mm, W.cols, ld_act, W.kpad, limbs, s);
-      hipLaunchKernelGGL(k_gemv_i8<8>, dim3(blocks_for(W.rows, 16)), dim3(512), 0, s, W.q, W.scale, W.rowsum,
-                         limbs, W.rows, W.kpad, mm, acc_out ? nullptr : out + t0 * ld_out, ld_out,
-                         acc_out ? acc_out + t0 * ld_out : nullptr);
+      int32_t* o = acc_out ? nullptr : out + t0 * ld_out;
+      int64_t* ao = acc_out ? acc_out + t0 * ld_out : nullptr;
+      const uint64_t lds = uint64_t(mm) * 4 * (W.kpad + 32);
+      if (lds <= kGemvLdsBudget) {
+        const uint64_t ntiles = (W.rows + 15) / 16;
+        const uint64_t nsteps = W.kpad / 128;
+        int ks = ntiles <= 256 ? 8 : ntiles <= 512 ? 4 : ntiles <= 1024 ? 2 : 1;
+        while (ks > 1 && uint64_t(ks) > nsteps) ks >>= 1;
+        const uint64_t tpw = 8 / ks;
+        const uint64_t grid = std::min<uint64_t>((ntiles + tpw - 1) / tpw, 2048);
+        const int32_t* a = act + t0 * ld_act;
+#define DET_GEMV_LAUNCH(KS)                                                                                 \
+  hipLaunchKernelGGL(k_gemv_i8_lds<KS>, dim3(unsigned(grid)), dim3(kGemvThreads), size_t(lds), s, W.q, W.scale, \
+                     W.rowsum, a, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao)
+        switch (ks) {
+          case 8: DET_GEMV_LAUNCH(8); break;
+          case 4: DET_GEMV_LAUNCH(4); break;
+          case 2: DET_GEMV_LAUNCH(2); break;
+          default: DET_GEMV_LAUNCH(1); break;
+        }
+#undef DET_GEMV_LAUNCH
+      } else {
+        launch_act_limbs(act + t0 * ld_act, mm, W.cols, ld_act, W.kpad, limbs, s);
+        hipLaunchKernelGGL(k_gemv_i8<8>, dim3(blocks_for(W.rows, 16)), dim3(512), 0, s, W.q, W.scale, W.rowsum,
+                           limbs, W.rows, W.kpad, mm, o, ld_out, ao);
+      }
     }
   } else if (W.storage == kI16) {
     hipLaunchKernelGGL(k_gemv_wide<int16_t>, dim3(blocks_for(W.rows, 4)), dim3(256), 0, s,

@@ -465,3 +465,4 @@ class Session:
             self.ctx.lib.det_session_free(self.handle)
         except Exception:
             pass
+from . import synthetic  # noqa: E402,F401
