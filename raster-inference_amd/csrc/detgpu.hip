@@ -125,25 +125,45 @@ DevMatrix upload_int8(det_ctx* ctx, uint64_t rows, uint64_t cols, const int8_t* 
   m.cols = cols;
   m.storage = det::kInt8;
   m.kpad = round_up(std::max<uint64_t>(cols, 1), 128);
-  std::vector<int8_t> padded(rows * m.kpad, 0);
-  std::vector<int32_t> rowsum(rows, 0);
+  const uint64_t prow = round_up(std::max<uint64_t>(rows, 1), 16);
+  std::vector<int8_t> tiled(prow * m.kpad, 0);
+  std::vector<int32_t> rowsum(prow, 0), sc(prow, 0);
   for (uint64_t r = 0; r < rows; ++r) {
     int32_t s = 0;
-    for (uint64_t c = 0; c < cols; ++c) {
-      padded[r * m.kpad + c] = q[r * cols + c];
-      s += q[r * cols + c];
+    for (uint64_t c0 = 0; c0 < cols; c0 += 32) {
+      const uint64_t n = std::min<uint64_t>(32, cols - c0);
+      std::memcpy(&tiled[det::tiled_offset(m.kpad, r, c0)], q + r * cols + c0, n);
+      for (uint64_t c = c0; c < c0 + n; ++c) s += q[r * cols + c];
     }
     rowsum[r] = s;
+    sc[r] = scale[r];
   }
-  HIPC(hipMalloc(&m.q, std::max<size_t>(padded.size(), 1)));
-  HIPC(hipMalloc(&m.scale, std::max<size_t>(rows, 1) * 4));
-  HIPC(hipMalloc(&m.rowsum, std::max<size_t>(rows, 1) * 4));
-  HIPC(hipMemcpyAsync(m.q, padded.data(), padded.size(), hipMemcpyHostToDevice, ctx->stream));
-  HIPC(hipMemcpyAsync(m.scale, scale, rows * 4, hipMemcpyHostToDevice, ctx->stream));
-  HIPC(hipMemcpyAsync(m.rowsum, rowsum.data(), rows * 4, hipMemcpyHostToDevice, ctx->stream));
+  HIPC(hipMalloc(&m.q, tiled.size()));
+  HIPC(hipMalloc(&m.scale, prow * 4));
+  HIPC(hipMalloc(&m.rowsum, prow * 4));
+  HIPC(hipMemcpyAsync(m.q, tiled.data(), tiled.size(), hipMemcpyHostToDevice, ctx->stream));
+  HIPC(hipMemcpyAsync(m.scale, sc.data(), prow * 4, hipMemcpyHostToDevice, ctx->stream));
+  HIPC(hipMemcpyAsync(m.rowsum, rowsum.data(), prow * 4, hipMemcpyHostToDevice, ctx->stream));
   HIPC(hipStreamSynchronize(ctx->stream));
   ctx->ensure_limbs(4 * 4 * m.kpad);
   return m;
+}
+
+// Copies rows [r0, r0+n) of a device matrix into a new matrix (host round trip;
+// load time only). Used for row slices that are not tile aligned.
+DevMatrix extract_rows(det_ctx* ctx, const DevMatrix& src, uint64_t r0, uint64_t n) {
+  if (r0 + n > src.rows) bail("matrix row slice out of bounds");
+  if (src.storage != det::kInt8) return det::row_view(src, r0, n);
+  if (r0 % 16 == 0) return det::row_view(src, r0, n);
+  const uint64_t prow = round_up(src.rows, 16);
+  std::vector<int8_t> tiled(prow * src.kpad);
+  std::vector<int32_t> sc(prow);
+  HIPC(hipMemcpy(tiled.data(), src.q, tiled.size(), hipMemcpyDeviceToHost));
+  HIPC(hipMemcpy(sc.data(), src.scale, prow * 4, hipMemcpyDeviceToHost));
+  std::vector<int8_t> q(n * src.cols);
+  for (uint64_t r = 0; r < n; ++r)
+    for (uint64_t c = 0; c < src.cols; ++c) q[r * src.cols + c] = tiled[det::tiled_offset(src.kpad, r0 + r, c)];
+  return upload_int8(ctx, n, src.cols, q.data(), sc.data() + r0);
 }
 
 // Row mass bound (det_num/mod.rs:39-42).
@@ -322,6 +342,7 @@ struct det_model {
   std::vector<void*> owned_dev;
 
   ~det_model() {
+    for (auto& v : ple_proj_views) free_matrix(v);
     for (auto& kv : tensors)
       if (kv.second.is_matrix) free_matrix(kv.second.mat);
     for (void* p : owned_dev) (void)hipFree(p);
@@ -465,7 +486,9 @@ void finalize(det_model* m) {
     const DevMatrix* proj = m->need_matrix("model.language_model.per_layer_model_projection.weight");
     if (m->ple_tok->rows < pv || m->ple_tok->cols < c.num_hidden_layers * ple) bail("PLE token embedding shape mismatch");
     if (proj->rows < c.num_hidden_layers * ple || proj->cols != c.hidden_size) bail("PLE model projection shape mismatch");
-    for (uint64_t l = 0; l < c.num_hidden_layers; ++l) m->ple_proj_views.push_back(det::row_view(*proj, l * ple, ple));
+    for (uint64_t l = 0; l < c.num_hidden_layers; ++l) {
+      m->ple_proj_views.push_back(extract_rows(m->ctx, *proj, l * ple, ple));
+    }
     m->ple_proj_norm = m->need_vector("model.language_model.per_layer_projection_norm.weight", ple);
     m->ple_embedding_scale = det::f32_to_act(std::sqrt(float(ple)));
     m->ple_projection_scalar = det::f32_to_act(std::pow(float(c.hidden_size), -0.5f));

@@ -12,7 +12,11 @@ enum Storage : int { kInt8 = 8, kI16 = 16, kI32 = 32 };
 struct DevMatrix {
   uint64_t rows = 0, cols = 0;
   int storage = kInt8;
-  // int8 form: q[rows][kpad] (zero padded), per-row integer scale and row sum.
+  // int8 form, tile-major: 16-row tiles, each stored as kpad/128 steps of
+  // 2048 bytes in the exact order one wavefront loads them (lane l = 16*g + i
+  // holds row 16*tile + i, columns [128*step + 32*g, +32)). Rows are padded
+  // to a multiple of 16 and columns to kpad (a multiple of 128) with zeros.
+  // Per-row integer scale and row sum (sum of q) accompany it.
   uint64_t kpad = 0;
   int8_t* q = nullptr;
   int32_t* scale = nullptr;
@@ -22,8 +26,14 @@ struct DevMatrix {
   bool owns = true;  // false for row-range views
 };
 
-// A view of rows [r0, r0+n) of a matrix (shares storage).
+// A view of rows [r0, r0+n) of a matrix (shares storage). For int8 storage
+// r0 must be a multiple of 16 (tile aligned).
 DevMatrix row_view(const DevMatrix& m, uint64_t r0, uint64_t n);
+// Byte offset of q[r][c] in the tile-major int8 layout.
+__host__ __device__ inline uint64_t tiled_offset(uint64_t kpad, uint64_t r, uint64_t c) {
+  const uint64_t tile = r >> 4, i = r & 15, step = c >> 7, g = (c >> 5) & 3, b = c & 31;
+  return ((tile * (kpad >> 7) + step) * 64 + g * 16 + i) * 32 + b;
+}
 
 // Activation limb planes for the int8 path: for each token row, four int8
 // planes of kpad bytes (byte j of a ^ 0x00808080, zero padded).

@@ -104,7 +104,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
   const uint64_t per = (nsteps + NW - 1) / NW;
   const uint64_t s0 = wave * per;
   const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
-  const v4i* bp = reinterpret_cast<const v4i*>(q + (b_on ? row : 0) * kpad + 32 * g);
+  const v4i* bp = reinterpret_cast<const v4i*>(q + uint64_t(blockIdx.x) * nsteps * 2048 + lane * 32);
   const v4i* ap = reinterpret_cast<const v4i*>(limbs + (a_on ? (uint64_t(at) * 4 + aj) : 0) * kpad + 32 * g);
   const v4i zero = {0, 0, 0, 0};
   v4i acc = zero;
@@ -113,8 +113,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
     v4i b[8], a[8];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      b[2 * u] = b_on ? __builtin_nontemporal_load(bp + (s + u) * 8) : zero;
-      b[2 * u + 1] = b_on ? __builtin_nontemporal_load(bp + (s + u) * 8 + 1) : zero;
+      b[2 * u] = __builtin_nontemporal_load(bp + (s + u) * 128);
+      b[2 * u + 1] = __builtin_nontemporal_load(bp + (s + u) * 128 + 1);
       a[2 * u] = a_on ? ap[(s + u) * 8] : zero;
       a[2 * u + 1] = a_on ? ap[(s + u) * 8 + 1] : zero;
     }
@@ -122,8 +122,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
     for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
   }
   for (; s < s1; ++s) {
-    const v4i b0 = b_on ? __builtin_nontemporal_load(bp + s * 8) : zero;
-    const v4i b1 = b_on ? __builtin_nontemporal_load(bp + s * 8 + 1) : zero;
+    const v4i b0 = __builtin_nontemporal_load(bp + s * 128);
+    const v4i b1 = __builtin_nontemporal_load(bp + s * 128 + 1);
     const v4i a0 = a_on ? ap[s * 8] : zero;
     const v4i a1 = a_on ? ap[s * 8 + 1] : zero;
     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
@@ -202,16 +202,17 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
   for (uint64_t base = uint64_t(blockIdx.x) * TPW; base < ntiles; base += uint64_t(gridDim.x) * TPW) {
     const uint64_t tile = base + slot;
     const uint64_t row = tile * 16 + i;
-    const bool b_on = tile < ntiles && row < n_rows;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + (b_on ? row : 0) * kpad + 32 * g);
+    const bool t_on = tile < ntiles;
+    const bool b_on = t_on && row < n_rows;
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 32);
     v4i acc = zero;
     uint64_t s = s0;
     for (; s + 4 <= s1; s += 4) {
       v4i b[8], a[8];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        b[2 * u] = b_on ? __builtin_nontemporal_load(bp + (s + u) * 8) : zero;
-        b[2 * u + 1] = b_on ? __builtin_nontemporal_load(bp + (s + u) * 8 + 1) : zero;
+        b[2 * u] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128) : zero;
+        b[2 * u + 1] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128 + 1) : zero;
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -222,8 +223,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
       for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
     }
     for (; s < s1; ++s) {
-      const v4i b0 = b_on ? __builtin_nontemporal_load(bp + s * 8) : zero;
-      const v4i b1 = b_on ? __builtin_nontemporal_load(bp + s * 8 + 1) : zero;
+      const v4i b0 = t_on ? __builtin_nontemporal_load(bp + s * 128) : zero;
+      const v4i b1 = t_on ? __builtin_nontemporal_load(bp + s * 128 + 1) : zero;
       const v4i a0 = a_on ? *reinterpret_cast<const v4i*>(abase + s * 128) : zero;
       const v4i a1 = a_on ? *reinterpret_cast<const v4i*>(abase + s * 128 + 16) : zero;
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
@@ -414,7 +415,7 @@ __global__ void k_softcap(int32_t* __restrict__ x, uint64_t n, int32_t cap) {
 }
 
 __device__ __forceinline__ int32_t wgt_at(const DevMatrix& M, uint64_t r, uint64_t c) {
-  if (M.storage == kInt8) return int32_t(M.q[r * M.kpad + c]) * M.scale[r];
+  if (M.storage == kInt8) return int32_t(M.q[tiled_offset(M.kpad, r, c)]) * M.scale[r];
   if (M.storage == kI16) return int32_t(static_cast<const int16_t*>(M.w)[r * M.cols + c]);
   return static_cast<const int32_t*>(M.w)[r * M.cols + c];
 }
@@ -457,7 +458,7 @@ DevMatrix row_view(const DevMatrix& m, uint64_t r0, uint64_t n) {
   v.rows = n;
   v.owns = false;
   if (m.storage == kInt8) {
-    v.q = m.q + r0 * m.kpad;
+    v.q = m.q + (r0 / 16) * (m.kpad / 128) * 2048;  // r0 is tile aligned
     v.scale = m.scale + r0;
     v.rowsum = m.rowsum + r0;
   } else if (m.storage == kI16) {
@@ -490,7 +491,7 @@ void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t 
         int ks = ntiles <= 256 ? 8 : ntiles <= 512 ? 4 : ntiles <= 1024 ? 2 : 1;
         while (ks > 1 && uint64_t(ks) > nsteps) ks >>= 1;
         const uint64_t tpw = 8 / ks;
-        const uint64_t grid = std::min<uint64_t>((ntiles + tpw - 1) / tpw, 2048);
+        const uint64_t grid = std::min<uint64_t>((ntiles + tpw - 1) / tpw, 1024);
         const int32_t* a = act + t0 * ld_act;
 #define DET_GEMV_LAUNCH(KS)                                                                                 \
   hipLaunchKernelGGL(k_gemv_i8_lds<KS>, dim3(unsigned(grid)), dim3(kGemvThreads), size_t(lds), s, W.q, W.scale, \
