@@ -72,6 +72,37 @@ def cpu_baseline(problems, seconds: float, threads: int) -> dict:
     }
 
 
+def measured_traffic():
+    """HBM bytes per lm_head launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary."""
+    p = ROOT / "profiles" / "gemv_lm_head_traffic.md"
+    try:
+        for line in p.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch="):
+                return int(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def profile_pass(ctx, rd, seed: int) -> int:
+    """Counter-collection workload: the lm_head GEMV and a device copy of the
+    same weight byte count, so FETCH_SIZE / WRITE_SIZE of the GEMV can be scaled
+    by what the counters read for a copy of known size."""
+    n, k = SHAPES[-1]
+    q, s, act = rd.synthetic.gemv_problem(n, k, seed=seed + n + k)
+    mat = ctx.upload_matrix(q, s)
+    a, o = ctx.to_device(act), ctx.empty(n)
+    src, dst = ctx.alloc(n * k), ctx.alloc(n * k)
+    for _ in range(5):
+        ctx.det_linear_into(mat, a, o)
+    ctx.synchronize()
+    for _ in range(5):
+        ctx.check(ctx.lib.det_memcpy_d2d(ctx.handle, rd.C.c_void_p(dst.ptr), rd.C.c_void_p(src.ptr), n * k))
+    ctx.synchronize()
+    print(json.dumps({"profile_pass": True, "gemv_alg_bytes": alg_bytes(n, k), "copy_bytes": n * k}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -80,6 +111,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="only 5 lm_head GEMV launches + 5 same-size device copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the det path's sharding "
@@ -89,6 +122,8 @@ def main() -> int:
     import rasterdet as rd
 
     ctx = rd.Context(0)
+    if args.profile_pass:
+        return profile_pass(ctx, rd, args.seed)
     log("[bench] generating and uploading weights")
     problems, mats, copies = [], [], []
     for n, k in SHAPES:
@@ -190,7 +225,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "avg_launch_us": round(lm_avg * 1e3, 2),
             "alg_bytes_per_launch": lm_bytes,
         },

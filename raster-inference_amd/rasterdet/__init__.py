@@ -133,6 +133,7 @@ class DecodeResult(C.Structure):
 
 
 _LIB = None
+C = C  # ctypes, re-exported for callers that pass raw pointers
 
 
 def library_path() -> pathlib.Path:
