@@ -223,6 +223,14 @@ int det_session_position(const det_session_t* s, uint64_t* position);
 int det_capture(det_model_t* model, const uint32_t* prompt, uint64_t prompt_len, uint64_t decode_steps, char* out,
                 size_t out_cap);
 
+/* ------------------------------------------------------------------------ */
+/* Synthetic workloads (no reference counterpart; random-init benchmarks)    */
+/* ------------------------------------------------------------------------ */
+/* Fills q[rows*cols] and s[rows] with counter-hash weights: q in [-127, 127],
+ * s in [1, scale_max]. Host memory; multi-threaded. Same definition as
+ * rasterdet.synthetic.fast_int8_matrix. */
+int det_synthetic_int8(uint64_t seed, uint64_t rows, uint64_t cols, int32_t scale_max, int8_t* q, int32_t* s);
+
 #ifdef __cplusplus
 }
 #endif

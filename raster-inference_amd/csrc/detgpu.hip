@@ -17,6 +17,7 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/detgpu.h"
@@ -107,6 +108,21 @@ int guarded(det_ctx* ctx, F&& f) {
 // ---------------------------------------------------------------------------
 uint64_t round_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
+// Runs fn(r0, r1) over [0, n) on up to 16 host threads (load-time work only).
+template <class F>
+void parallel_rows(uint64_t n, F&& fn) {
+  const unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  const uint64_t per = (n + hw - 1) / hw;
+  if (n < 4096 || hw == 1) { fn(uint64_t(0), n); return; }
+  std::vector<std::thread> th;
+  for (unsigned t = 0; t < hw; ++t) {
+    const uint64_t r0 = t * per, r1 = std::min(n, r0 + per);
+    if (r0 >= r1) break;
+    th.emplace_back([&fn, r0, r1] { fn(r0, r1); });
+  }
+  for (auto& x : th) x.join();
+}
+
 void free_matrix(DevMatrix& m) {
   if (!m.owns) return;
   if (m.q) (void)hipFree(m.q);
@@ -128,16 +144,18 @@ DevMatrix upload_int8(det_ctx* ctx, uint64_t rows, uint64_t cols, const int8_t* 
   const uint64_t prow = round_up(std::max<uint64_t>(rows, 1), 16);
   std::vector<int8_t> tiled(prow * m.kpad, 0);
   std::vector<int32_t> rowsum(prow, 0), sc(prow, 0);
-  for (uint64_t r = 0; r < rows; ++r) {
-    int32_t s = 0;
-    for (uint64_t c0 = 0; c0 < cols; c0 += 32) {
-      const uint64_t n = std::min<uint64_t>(32, cols - c0);
-      std::memcpy(&tiled[det::tiled_offset(m.kpad, r, c0)], q + r * cols + c0, n);
-      for (uint64_t c = c0; c < c0 + n; ++c) s += q[r * cols + c];
+  parallel_rows(rows, [&](uint64_t r0, uint64_t r1) {
+    for (uint64_t r = r0; r < r1; ++r) {
+      int32_t s = 0;
+      for (uint64_t c0 = 0; c0 < cols; c0 += 32) {
+        const uint64_t n = std::min<uint64_t>(32, cols - c0);
+        std::memcpy(&tiled[det::tiled_offset(m.kpad, r, c0)], q + r * cols + c0, n);
+        for (uint64_t c = c0; c < c0 + n; ++c) s += q[r * cols + c];
+      }
+      rowsum[r] = s;
+      sc[r] = scale[r];
     }
-    rowsum[r] = s;
-    sc[r] = scale[r];
-  }
+  });
   HIPC(hipMalloc(&m.q, tiled.size()));
   HIPC(hipMalloc(&m.scale, prow * 4));
   HIPC(hipMalloc(&m.rowsum, prow * 4));
@@ -179,11 +197,13 @@ DevMatrix upload_matrix(det_ctx* ctx, uint64_t rows, uint64_t cols, int width, c
     if (!row_scale) bail("int8 matrices need a row scale");
     const int8_t* q = static_cast<const int8_t*>(values);
     std::vector<int64_t> mass(rows, 0);
-    for (uint64_t r = 0; r < rows; ++r) {
-      int64_t s = 0;
-      for (uint64_t c = 0; c < cols; ++c) s += std::abs(int64_t(q[r * cols + c]));
-      mass[r] = s * std::abs(int64_t(row_scale[r]));
-    }
+    parallel_rows(rows, [&](uint64_t r0, uint64_t r1) {
+      for (uint64_t r = r0; r < r1; ++r) {
+        int64_t s = 0;
+        for (uint64_t c = 0; c < cols; ++c) s += std::abs(int64_t(q[r * cols + c]));
+        mass[r] = s * std::abs(int64_t(row_scale[r]));
+      }
+    });
     check_row_mass(rows, cols, mass);
     return upload_int8(ctx, rows, cols, q, row_scale);
   }
@@ -1299,6 +1319,33 @@ int det_session_position(const det_session_t* s, uint64_t* position) {
   *position = s->position;
   return 0;
 }
+// Counter-hash synthetic int8 weights (splitmix64 finaliser over the byte
+// counter, 8 bytes per hash; q = byte % 255 - 127; s = 1 + u32 % scale_max).
+static inline uint64_t synth_mix(uint64_t x) {
+  x ^= x >> 30; x *= 0xBF58476D1CE4E5B9ull;
+  x ^= x >> 27; x *= 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+int det_synthetic_int8(uint64_t seed, uint64_t rows, uint64_t cols, int32_t scale_max, int8_t* q, int32_t* s) {
+  return guarded(nullptr, [&] {
+    if (scale_max < 1) bail("scale_max must be positive");
+    const uint64_t base = seed * 0x9E3779B97F4A7C15ull;
+    const uint64_t nbytes = rows * cols;
+    parallel_rows((nbytes + 7) / 8, [&](uint64_t w0, uint64_t w1) {
+      for (uint64_t w = w0; w < w1; ++w) {
+        const uint64_t h = synth_mix(base + w);
+        for (int b = 0; b < 8 && w * 8 + b < nbytes; ++b) q[w * 8 + b] = int8_t(int(uint8_t(h >> (8 * b)) % 255) - 127);
+      }
+    });
+    const uint64_t sbase = (seed ^ 0x5CA1Eull) * 0x9E3779B97F4A7C15ull;
+    for (uint64_t r = 0; r < rows; ++r) {
+      const uint64_t h = synth_mix(sbase + r / 2);
+      const uint32_t u = uint32_t(h >> (32 * (r & 1)));
+      s[r] = int32_t(u % uint32_t(scale_max)) + 1;
+    }
+  });
+}
+
 int det_capture(det_model_t* m, const uint32_t* prompt, uint64_t n, uint64_t steps, char* out, size_t cap) {
   return guarded(m->ctx, [&] {
     if (!m->finalized) bail("model is not finalized");

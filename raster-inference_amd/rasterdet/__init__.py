@@ -189,6 +189,7 @@ def lib() -> C.CDLL:
         "det_session_logits": (C.c_int, [P, i32p, u64]),
         "det_session_position": (C.c_int, [P, C.POINTER(u64)]),
         "det_capture": (C.c_int, [P, P, u64, u64, C.c_char_p, C.c_size_t]),
+        "det_synthetic_int8": (C.c_int, [u64, u64, u64, C.c_int32, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -206,6 +207,17 @@ def exported_symbols() -> list[str]:
 
 def _ptr(a: np.ndarray) -> C.c_void_p:
     return C.c_void_p(a.ctypes.data)
+
+
+def synthetic_int8(seed: int, rows: int, cols: int, scale_max: int):
+    """Counter-hash int8 weights + row scales (det_synthetic_int8; same values as
+    synthetic.fast_int8_matrix, generated by multi-threaded native code)."""
+    q = np.empty((rows, cols), dtype=np.int8)
+    s = np.empty(rows, dtype=np.int32)
+    st = lib().det_synthetic_int8(seed & ((1 << 64) - 1), rows, cols, scale_max, _ptr(q), _ptr(s))
+    if st:
+        raise DetError(st, lib().det_ctx_last_error(None).decode())
+    return q, s
 
 
 class Context:

@@ -142,6 +142,46 @@ def gemv_problem(rows: int, cols: int, seed: int, scale_max: int = 256):
     return q, s, act
 
 
+def hash_bytes(seed: int, nbytes: int) -> np.ndarray:
+    """nbytes pseudo-random bytes: splitmix64 finaliser over a counter (vectorised)."""
+    n64 = (nbytes + 7) // 8
+    x = np.arange(n64, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        x += np.uint64((seed * 0x9E3779B97F4A7C15) & MASK64)
+        x ^= x >> np.uint64(30)
+        x *= np.uint64(0xBF58476D1CE4E5B9)
+        x ^= x >> np.uint64(27)
+        x *= np.uint64(0x94D049BB133111EB)
+        x ^= x >> np.uint64(31)
+    return x.view(np.uint8)[:nbytes]
+
+
+def fast_int8_matrix(seed: int, rows: int, cols: int, scale_max: int):
+    """q uniform-ish in [-127, 127] (byte % 255 - 127) and s in [1, scale_max], from counter hashes."""
+    b = hash_bytes(seed, rows * cols)
+    q = (b % np.uint8(255)).astype(np.int16) - 127
+    q = q.astype(np.int8).reshape(rows, cols)
+    sb = hash_bytes(seed ^ 0x5CA1E, rows * 4).view(np.uint32)
+    s = (sb % np.uint32(scale_max)).astype(np.int32) + 1
+    return q, s
+
+
+def synthetic_model_fast(cfg: dict, seed: int, scale_max: int = 16):
+    """Like synthetic_model but with counter-hash weights (fast enough for E4B scale)."""
+    for idx, (name, shape) in enumerate(model_tensor_shapes(cfg)):
+        ts = (seed * 1000003 + idx) & MASK64
+        if len(shape) == 1:
+            b = hash_bytes(ts, shape[0]).astype(np.int32) % 33 - 16
+            yield name, (65536 + b * 1024).astype(np.int32), None
+        else:
+            try:
+                from . import synthetic_int8  # native generator (same values)
+                q, s = synthetic_int8(ts, shape[0], shape[1], scale_max)
+            except RuntimeError:
+                q, s = fast_int8_matrix(ts, shape[0], shape[1], scale_max)
+            yield name, q, s
+
+
 def synthetic_model(cfg: dict, seed: int, scale_max: int = 16):
     """Random int8 x scale weights for any config (used for the E4B shape).
 

@@ -43,3 +43,15 @@ def test_python_wrapper_binds_the_header():
         "enable_moe_block": False, "hidden_activation": "gelu_pytorch_tanh", "head_dim": 2, "hidden_size": 4,
         "layer_types": ["sliding_attention"], "num_attention_heads": 1, "num_hidden_layers": 1,
         "num_key_value_heads": 1, "rms_norm_eps": 1e-6, "sliding_window": 4, "vocab_size": 9}}).hidden_size == 4
+
+
+@pytest.mark.skipif(not LIB.exists(), reason="libdetgpu.so not built")
+def test_native_synthetic_generator_matches_python_definition():
+    import rasterdet
+    from rasterdet import synthetic
+
+    for seed, rows, cols, smax in [(1, 7, 13, 16), (12345, 33, 100, 256), (2**63 + 5, 3, 1, 1)]:
+        q, s = rasterdet.synthetic_int8(seed, rows, cols, smax)
+        q2, s2 = synthetic.fast_int8_matrix(seed, rows, cols, smax)
+        assert (q == q2).all() and (s == s2).all()
+        assert q.min() >= -127 and q.max() <= 127 and s.min() >= 1 and s.max() <= smax
