@@ -206,6 +206,9 @@ typedef struct det_decode_result {
 #define DET_COMMIT_ACTIVATIONS 1u /* embedding / hidden / activation / logits */
 #define DET_COMMIT_KV 2u          /* KV cache commitment */
 #define DET_COMMIT_ALL 3u
+/* Decode flag: run the per-operation kernel sequence instead of the fused,
+ * graph-captured decode step (both are bit-identical; for cross-checks). */
+#define DET_DECODE_PER_OP 0x100u
 
 /* pipeline::run_prefill_pass_with_mode (runtime/pipeline.rs:55-98): embedding,
  * PLE inputs, every prefill_layer, prefill_finalize logits. */

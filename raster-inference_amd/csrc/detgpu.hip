@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "../../include/detgpu.h"
+#include "decode.h"
 #include "det_arith.h"
 #include "kernels.h"
 
@@ -360,8 +361,16 @@ struct det_model {
   int64_t eps = 0;
   uint64_t hidden = 0, vocab = 0;
   std::vector<void*> owned_dev;
+  // fused decode matrices: [q; k; v] rows and interleaved gate/up blocks of 8
+  struct Fused {
+    DevMatrix qkv, gateup;
+    bool has_v = true;
+  };
+  std::vector<Fused> fused;
+  bool fused_ok = false;
 
   ~det_model() {
+    for (auto& f : fused) { free_matrix(f.qkv); free_matrix(f.gateup); }
     for (auto& v : ple_proj_views) free_matrix(v);
     for (auto& kv : tensors)
       if (kv.second.is_matrix) free_matrix(kv.second.mat);
@@ -389,6 +398,53 @@ struct det_model {
 };
 
 namespace {
+
+// Downloads a tile-major int8 matrix back to row-major q + scales.
+void untile(det_ctx* ctx, const DevMatrix& M, std::vector<int8_t>& q, std::vector<int32_t>& sc) {
+  const uint64_t prow = round_up(std::max<uint64_t>(M.rows, 1), 16);
+  std::vector<int8_t> tiled(prow * M.kpad);
+  HIPC(hipMemcpy(tiled.data(), M.q, tiled.size(), hipMemcpyDeviceToHost));
+  sc.resize(M.rows);
+  HIPC(hipMemcpy(sc.data(), M.scale, M.rows * 4, hipMemcpyDeviceToHost));
+  q.resize(M.rows * M.cols);
+  parallel_rows(M.rows, [&](uint64_t r0, uint64_t r1) {
+    for (uint64_t r = r0; r < r1; ++r)
+      for (uint64_t c0 = 0; c0 < M.cols; c0 += 32)
+        std::memcpy(&q[r * M.cols + c0], &tiled[det::tiled_offset(M.kpad, r, c0)], std::min<uint64_t>(32, M.cols - c0));
+  });
+}
+
+// Stacks int8 matrices of equal width row-wise; with interleave8 (two inputs
+// of equal height) rows alternate in blocks of 8: a[0..8), b[0..8), a[8..16), ...
+DevMatrix fuse_rows(det_ctx* ctx, const std::vector<const DevMatrix*>& ms, bool interleave8) {
+  const uint64_t cols = ms[0]->cols;
+  uint64_t rows = 0;
+  std::vector<std::vector<int8_t>> qs(ms.size());
+  std::vector<std::vector<int32_t>> ss(ms.size());
+  for (size_t i = 0; i < ms.size(); ++i) {
+    if (ms[i]->cols != cols || ms[i]->storage != det::kInt8) bail("cannot fuse matrices of different widths");
+    untile(ctx, *ms[i], qs[i], ss[i]);
+    rows += ms[i]->rows;
+  }
+  std::vector<int8_t> q(rows * cols);
+  std::vector<int32_t> sc(rows);
+  uint64_t r = 0;
+  auto put = [&](size_t i, uint64_t src_row) {
+    std::memcpy(&q[r * cols], &qs[i][src_row * cols], cols);
+    sc[r] = ss[i][src_row];
+    ++r;
+  };
+  if (interleave8) {
+    for (uint64_t b = 0; b < ms[0]->rows; b += 8) {
+      for (uint64_t j = 0; j < 8; ++j) put(0, b + j);
+      for (uint64_t j = 0; j < 8; ++j) put(1, b + j);
+    }
+  } else {
+    for (size_t i = 0; i < ms.size(); ++i)
+      for (uint64_t j = 0; j < ms[i]->rows; ++j) put(i, j);
+  }
+  return upload_int8(ctx, rows, cols, q.data(), sc.data());
+}
 
 // gemma/io.rs:165-190
 std::optional<uint64_t> kv_shared_layer_index(const det_model* m, uint64_t l) {
@@ -523,6 +579,31 @@ void finalize(det_model* m) {
     m->softcap = det::f32_to_act(c.final_logit_softcapping);
     if (*m->softcap <= 0) contract("softcap_act requires a strictly positive softcap");
   }
+  // The fused, graph-captured decode step covers int8 models without PLE
+  // whose shapes fit its kernels; everything else runs the per-op sequence.
+  bool ok = !m->has_ple && m->hidden <= det::kDecMaxHidden && m->lm_head->storage == det::kInt8 &&
+            det::gemv_fits_lds(*m->lm_head, 1);
+  for (const GLayer& L : m->layers) {
+    for (const DevMatrix* w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down})
+      if (w && (w->storage != det::kInt8 || !det::gemv_fits_lds(*w, 1))) ok = false;
+    if (L.head_dim % 4 || L.head_dim > det::kDecMaxHeadDim || L.num_heads % L.num_kv_heads ||
+        L.num_heads / L.num_kv_heads > det::kDecMaxGroup || L.gate->rows % 8)
+      ok = false;
+  }
+  if (ok) {
+    m->fused.resize(m->layers.size());
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+      const GLayer& L = m->layers[l];
+      auto& F = m->fused[l];
+      F.has_v = L.v != nullptr;
+      std::vector<const DevMatrix*> parts = {L.q, L.k};
+      if (L.v) parts.push_back(L.v);
+      F.qkv = fuse_rows(m->ctx, parts, false);
+      F.gateup = fuse_rows(m->ctx, {L.gate, L.up}, true);
+      if (!det::gemv_fits_lds(F.qkv, 1) || !det::gemv_fits_lds(F.gateup, 1)) ok = false;
+    }
+  }
+  m->fused_ok = ok;
   m->finalized = true;
 }
 
@@ -604,8 +685,24 @@ struct det_session {
           *logits = nullptr, *dec_in = nullptr;
   std::vector<void*> owned;
   bool logits_valid = false;
+  // fused decode step (HIP graph)
+  det::StepState* st_dev = nullptr;
+  det::StepState* st_host = nullptr;
+  uint32_t* tok_host = nullptr;
+  int32_t *qkv = nullptr, *qbuf = nullptr, *scores = nullptr, *weights = nullptr, *obuf = nullptr, *hbuf = nullptr,
+          *ffbuf = nullptr;
+  int64_t* attn_acc = nullptr;
+  int64_t* am_scratch = nullptr;
+  uint32_t* am_out = nullptr;
+  uint64_t score_stride = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
 
   ~det_session() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (st_host) (void)hipHostFree(st_host);
+    if (tok_host) (void)hipHostFree(tok_host);
     for (auto& c : kv) {
       if (c.k) (void)hipFree(c.k);
       if (c.v) (void)hipFree(c.v);
@@ -648,6 +745,30 @@ void session_alloc(det_session* s) {
   s->logits = s->alloc<int32_t>(m->vocab);
   s->dec_in = s->alloc<int32_t>(H);
   s->kv.assign(m->layers.size(), GKv());
+  if (m->fused_ok) {
+    uint64_t fr = 0, nhd = 0, ff = 0;
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+      fr = std::max(fr, m->fused[l].qkv.rows);
+      nhd = std::max(nhd, m->layers[l].num_heads * m->layers[l].head_dim);
+      ff = std::max(ff, m->layers[l].gate->rows);
+    }
+    uint64_t nh = 0;
+    for (const GLayer& L : m->layers) nh = std::max(nh, L.num_heads);
+    s->score_stride = T;  // no attention window exceeds the session length
+    s->qkv = s->alloc<int32_t>(fr);
+    s->qbuf = s->alloc<int32_t>(nhd);
+    s->scores = s->alloc<int32_t>(nh * T);
+    s->weights = s->alloc<int32_t>(nh * T);
+    s->attn_acc = s->alloc<int64_t>(nhd);
+    s->obuf = s->alloc<int32_t>(H);
+    s->hbuf = s->alloc<int32_t>(ff);
+    s->ffbuf = s->alloc<int32_t>(H);
+    s->am_scratch = s->alloc<int64_t>((m->vocab + 1023) / 1024);
+    s->am_out = s->alloc<uint32_t>(1);
+    s->st_dev = s->alloc<det::StepState>(1);
+    HIPC(hipHostMalloc(reinterpret_cast<void**>(&s->st_host), sizeof(det::StepState), hipHostMallocDefault));
+    HIPC(hipHostMalloc(reinterpret_cast<void**>(&s->tok_host), sizeof(uint32_t), hipHostMallocDefault));
+  }
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
     GKv& c = s->kv[l];
@@ -847,9 +968,15 @@ void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
       const uint64_t retained = c.ring ? (n > *L.cache_sliding_window ? n - *L.cache_sliding_window : 0) : 0;
       const uint64_t kept = n - retained;
       if (kept > c.cap) bail("KV cache capacity exceeded");
-      copy_d2d(ctx, c.k, s->kb + retained * kw, kept * kw * 4);
-      copy_d2d(ctx, c.v, s->vb + retained * kw, kept * kw * 4);
-      c.start = 0; c.len = kept; c.has = true;
+      // canonical slots: token t at t % cap (ring) or t (linear)
+      for (uint64_t t = retained; t < n;) {
+        const uint64_t slot = c.ring ? t % c.cap : t;
+        const uint64_t span = std::min<uint64_t>(n - t, c.cap - slot);
+        copy_d2d(ctx, c.k + slot * kw, s->kb + t * kw, span * kw * 4);
+        copy_d2d(ctx, c.v + slot * kw, s->vb + t * kw, span * kw * 4);
+        t += span;
+      }
+      c.start = c.ring ? retained % c.cap : 0; c.len = kept; c.has = true;
       a.k = s->kb; a.v = s->vb; a.kv_ld = kw; a.ring_start = 0; a.ring_cap = 0; a.avail = n;
     }
     if (a.avail > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
@@ -873,6 +1000,14 @@ void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
   out->kv[0] = 0;
   if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
   out->next_token = ctx->argmax(s->logits, m->vocab);
+}
+
+// Cache bookkeeping after n tokens with canonical slots (token t at t % cap
+// in a ring, t in a linear cache); equals push + trim-front of
+// DetKvCacheData::append_rows (det_tensor.rs:308-337).
+void kv_advance(GKv& c, uint64_t n) {
+  c.len = c.ring ? std::min(n, c.cap) : n;
+  c.start = c.ring ? (n - c.len) % c.cap : 0;
 }
 
 struct LayerHook {
@@ -903,17 +1038,9 @@ void decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
     GKv& own = s->kv[l];
     if (!L.donor) {
       // DetKvCacheData::append_rows with sliding-window trim (det_tensor.rs:308-337)
-      uint64_t slot;
-      if (!own.ring) {
-        if (own.len >= own.cap) bail("KV cache capacity exceeded");
-        slot = own.len++;
-      } else if (own.len < own.cap) {
-        slot = (own.start + own.len) % own.cap;
-        ++own.len;
-      } else {
-        slot = own.start;
-        own.start = (own.start + 1) % own.cap;
-      }
+      if (!own.ring && pos >= own.cap) bail("KV cache capacity exceeded");
+      const uint64_t slot = own.ring ? pos % own.cap : pos;
+      kv_advance(own, pos + 1);
       copy_d2d(ctx, own.k + slot * kw, s->kb, kw * 4);
       copy_d2d(ctx, own.v + slot * kw, s->vb, kw * 4);
       own.has = true;
@@ -956,6 +1083,97 @@ void decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
   out->kv[0] = 0;
   if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
   out->next_token = ctx->argmax(s->logits, m->vocab);
+}
+
+// Enqueues one fused decode step (det_layer_decode for every layer, then
+// det_hidden_to_logits and argmax_first) reading position/token from st_dev.
+void enqueue_fused_step(det_session* s) {
+  det_model* m = s->m;
+  hipStream_t st = m->ctx->stream;
+  const uint64_t H = m->hidden;
+  det::launch_dec_embed(*m->embedding, s->st_dev, m->embed_scale, H, s->x, s->dec_in, m->layers[0].in_ln, m->eps,
+                        s->normed, st);
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const GLayer& L = m->layers[l];
+    const auto& F = m->fused[l];
+    GKv& own = s->kv[l];
+    det::launch_gemv_decode(F.qkv, s->normed, false, 0, s->qkv, st);
+    det::QkvPostArgs qa{};
+    qa.qkv = s->qkv; qa.qbuf = s->qbuf; qa.kc = own.k; qa.vc = own.v;
+    qa.q_norm = L.q_norm; qa.k_norm = L.k_norm; qa.inv_freq = L.inv_freq; qa.st = s->st_dev; qa.eps = L.eps;
+    qa.cap = own.cap; qa.rotary = L.rotary; qa.nh = uint32_t(L.num_heads); qa.nkv = uint32_t(L.num_kv_heads);
+    qa.hd = uint32_t(L.head_dim); qa.ring = own.ring; qa.has_v = F.has_v;
+    det::launch_dec_qkv_post(qa, !L.donor, st);
+    const GKv& ac = L.donor ? s->kv[*L.donor] : own;
+    det::AttnDecArgs aa{};
+    aa.q = s->qbuf; aa.k = ac.k; aa.v = ac.v; aa.st = s->st_dev; aa.cap = ac.cap;
+    aa.window = L.sliding ? *L.sliding_window : 0; aa.max_rows = s->score_stride; aa.ring = ac.ring;
+    aa.hd = uint32_t(L.head_dim); aa.nh = uint32_t(L.num_heads); aa.nkv = uint32_t(L.num_kv_heads);
+    aa.scores = s->scores; aa.weights = s->weights; aa.acc = s->attn_acc;
+    det::launch_dec_attention(aa, st);
+    det::launch_gemv_decode(*L.o, s->attn_acc, true, 0, s->obuf, st);
+    det::launch_dec_mid(s->obuf, s->x, s->normed, L.post_attn_ln, L.pre_ff_ln, H, L.eps, st);
+    det::launch_gemv_decode(F.gateup, s->normed, false, 1, s->hbuf, st);
+    det::launch_gemv_decode(*L.down, s->hbuf, false, 0, s->ffbuf, st);
+    const int32_t* w_next = l + 1 < m->layers.size() ? m->layers[l + 1].in_ln : m->final_norm;
+    det::launch_dec_end(s->ffbuf, s->x, s->normed, L.post_ff_ln, L.layer_scalar.has_value(),
+                        L.layer_scalar.value_or(0), w_next, H, L.eps, st);
+  }
+  det::launch_gemv_decode(*m->lm_head, s->normed, false, 0, s->logits, st);
+  if (m->softcap) det::launch_dec_softcap(s->logits, m->vocab, *m->softcap, st);
+  det::launch_argmax(s->logits, m->vocab, s->am_scratch, s->am_out, st);
+}
+
+void build_decode_graph(det_session* s) {
+  hipStream_t st = s->m->ctx->stream;
+  HIPC(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  try {
+    enqueue_fused_step(s);
+  } catch (...) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(st, &g);
+    if (g) (void)hipGraphDestroy(g);
+    throw;
+  }
+  HIPC(hipStreamEndCapture(st, &s->graph));
+  HIPC(hipGraphInstantiate(&s->exec, s->graph, nullptr, nullptr, 0));
+}
+
+void decode_fused(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t* out) {
+  det_model* m = s->m;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  if (s->position == 0) bail("decode requires a prefilled session");
+  if (s->position >= s->max_tokens) bail("session capacity exhausted");
+  check_ids(m, &token, 1);
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const GKv& c = s->kv[l];
+    if (!m->layers[l].donor && !c.has) bail("deterministic decode cache append requires canonical key rows");
+  }
+  if (!s->exec) build_decode_graph(s);
+  const uint64_t pos = s->position;
+  s->st_host->position = pos;
+  s->st_host->token = token;
+  HIPC(hipMemcpyAsync(s->st_dev, s->st_host, sizeof(det::StepState), hipMemcpyHostToDevice, st));
+  HIPC(hipGraphLaunch(s->exec, st));
+  HIPC(hipMemcpyAsync(s->tok_host, s->am_out, 4, hipMemcpyDeviceToHost, st));
+  HIPC(hipStreamSynchronize(st));
+  for (size_t l = 0; l < m->layers.size(); ++l)
+    if (!m->layers[l].donor) kv_advance(s->kv[l], pos + 1);
+  s->position += 1;
+  s->logits_valid = true;
+  const uint64_t H = m->hidden;
+  if (flags & DET_COMMIT_ACTIVATIONS) {
+    std::vector<int32_t> host(H), lg(m->vocab);
+    HIPC(hipMemcpyAsync(host.data(), s->x, H * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipMemcpyAsync(lg.data(), s->logits, m->vocab * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    commit_rows(host.data(), 1, H, out->activation);
+    commit_vector(lg.data(), m->vocab, out->logits);
+  }
+  out->kv[0] = 0;
+  if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
+  out->next_token = *s->tok_host;
 }
 
 std::unique_ptr<det_session> clone_session(const det_session* src) {
@@ -1023,7 +1241,8 @@ std::string capture(det_model* m, const uint32_t* ids, uint64_t n, uint64_t step
   std::string ids_json = "[";
   for (uint64_t i = 0; i < steps; ++i) {
     det_decode_result_t dr{};
-    decode(&s0, tok, DET_COMMIT_ALL, &dr, nullptr);
+    if (m->fused_ok) decode_fused(&s0, tok, DET_COMMIT_ALL, &dr);
+    else decode(&s0, tok, DET_COMMIT_ALL, &dr, nullptr);
     if (i) { out += ","; ids_json += ","; }
     ids_json += std::to_string(tok);
     out += "{\"token\":" + std::to_string(tok) + ",\"activation\":\"" + dr.activation + "\",\"logits\":\"" + dr.logits +
@@ -1304,7 +1523,8 @@ int det_session_prefill(det_session_t* s, const uint32_t* ids, uint64_t n, uint3
 int det_session_decode(det_session_t* s, uint32_t token, uint32_t flags, det_decode_result_t* out) {
   return guarded(s->m->ctx, [&] {
     det_decode_result_t tmp{};
-    decode(s, token, flags, out ? out : &tmp, nullptr);
+    if (s->m->fused_ok && !(flags & DET_DECODE_PER_OP)) decode_fused(s, token, flags, out ? out : &tmp);
+    else decode(s, token, flags, out ? out : &tmp, nullptr);
   });
 }
 int det_session_logits(det_session_t* s, int32_t* out, uint64_t n) {

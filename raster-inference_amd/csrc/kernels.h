@@ -46,6 +46,13 @@ void launch_act_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_ac
 void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,
                    uint64_t ld_out, int64_t* acc_out, int8_t* limbs, hipStream_t s);
 
+// Batch-1 int8 GEMV for the fused decode step (int8 storage, fits LDS):
+// act_i64 requantizes wrapped accumulators on load; epilogue 1 applies
+// mul_sat(gelu(gate), up) to an interleaved gate/up matrix (out has rows/2).
+bool gemv_fits_lds(const DevMatrix& W, uint64_t m);
+void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int epilogue, int32_t* out,
+                        hipStream_t s);
+
 void launch_rmsnorm(int32_t* x, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
                     int64_t eps, hipStream_t s);
 void launch_rope(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t head_dim,

@@ -159,10 +159,15 @@ __device__ __forceinline__ int64_t limb_combine(const int64_t p[4], int32_t rows
   return int64_t(uint64_t(dot) * uint64_t(int64_t(scale)));
 }
 
-template <int KSPLIT>
+// IN64: the activation rows are wrapped Q32.32 accumulators, requantized on
+// load (the attention weighted sums feeding the O projection).
+// EPI 0: requantize (or raw accumulators to acc_out). EPI 1: rows are
+// interleaved gate/up pairs per tile (rows 0-7 gate f..f+7, rows 8-15 up
+// f..f+7); out[f] = mul_sat(gelu(gate_f), up_f).
+template <int KSPLIT, bool IN64, int EPI>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
-    const int32_t* __restrict__ act, uint64_t ld_act, uint64_t k, uint64_t n_rows, uint64_t kpad, uint32_t m,
+    const void* __restrict__ act_v, uint64_t ld_act, uint64_t k, uint64_t n_rows, uint64_t kpad, uint32_t m,
     int32_t* __restrict__ out, uint64_t ld_out, int64_t* __restrict__ acc_out) {
   extern __shared__ __attribute__((aligned(16))) int8_t lds_limbs[];
   __shared__ v4i part[KSPLIT > 1 ? 8 : 1][64];
@@ -173,7 +178,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     const uint64_t t = idx / (kpad / 4), c = (idx % (kpad / 4)) * 4;
     uint32_t w[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) w[e] = c + e < k ? uint32_t(act[t * ld_act + c + e]) ^ 0x00808080u : 0u;
+    for (int e = 0; e < 4; ++e) {
+      int32_t a = 0;
+      if (c + e < k)
+        a = IN64 ? requant(static_cast<const int64_t*>(act_v)[t * ld_act + c + e])
+                 : static_cast<const int32_t*>(act_v)[t * ld_act + c + e];
+      w[e] = uint32_t(a) ^ 0x00808080u;
+    }
     // padded columns get limb bytes 0 (their weights are zero as well)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -243,10 +254,17 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
       }
       __syncthreads();
     }
-    if (kp == 0 && uint32_t(g) < m && b_on) {
-      const int64_t a = limb_combine(p, rowsum[row], scale[row]);
-      if (acc_out) acc_out[uint64_t(g) * ld_out + row] = a;
-      else out[uint64_t(g) * ld_out + row] = requant(a);
+    if (kp == 0) {
+      const bool ok = uint32_t(g) < m && b_on;
+      const int64_t a = ok ? limb_combine(p, rowsum[row], scale[row]) : 0;
+      if (EPI == 1) {
+        const int32_t r = requant(a);
+        const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
+        if (ok && i < 8) out[uint64_t(g) * ld_out + tile * 8 + i] = mul_sat(gelu_act(r), up);
+      } else if (ok) {
+        if (acc_out) acc_out[uint64_t(g) * ld_out + row] = a;
+        else out[uint64_t(g) * ld_out + row] = requant(a);
+      }
     }
   }
 }
@@ -475,6 +493,37 @@ void launch_act_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld, u
   hipLaunchKernelGGL(k_act_limbs, grid, dim3(256), 0, s, act, m, k, ld, kpad, limbs);
 }
 
+template <bool IN64, int EPI>
+static void launch_lds_gemv(const DevMatrix& W, const void* act, uint64_t ld_act, uint32_t mm, int32_t* o,
+                            uint64_t ld_out, int64_t* ao, hipStream_t s) {
+  const uint64_t lds = uint64_t(mm) * 4 * (W.kpad + 32);
+  const uint64_t ntiles = (W.rows + 15) / 16;
+  const uint64_t nsteps = W.kpad / 128;
+  int ks = ntiles <= 256 ? 8 : ntiles <= 512 ? 4 : ntiles <= 1024 ? 2 : 1;
+  while (ks > 1 && uint64_t(ks) > nsteps) ks >>= 1;
+  const uint64_t tpw = 8 / ks;
+  const uint64_t grid = std::min<uint64_t>((ntiles + tpw - 1) / tpw, 1024);
+#define DET_GEMV_LAUNCH(KS)                                                                                     \
+  hipLaunchKernelGGL((k_gemv_i8_lds<KS, IN64, EPI>), dim3(unsigned(grid)), dim3(kGemvThreads), size_t(lds), s, W.q, \
+                     W.scale, W.rowsum, act, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao)
+  switch (ks) {
+    case 8: DET_GEMV_LAUNCH(8); break;
+    case 4: DET_GEMV_LAUNCH(4); break;
+    case 2: DET_GEMV_LAUNCH(2); break;
+    default: DET_GEMV_LAUNCH(1); break;
+  }
+#undef DET_GEMV_LAUNCH
+}
+
+bool gemv_fits_lds(const DevMatrix& W, uint64_t m) { return m * 4 * (W.kpad + 32) <= kGemvLdsBudget; }
+
+void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int epilogue, int32_t* out,
+                        hipStream_t s) {
+  if (act_i64) launch_lds_gemv<true, 0>(W, act, W.cols, 1, out, W.rows, nullptr, s);
+  else if (epilogue == 1) launch_lds_gemv<false, 1>(W, act, W.cols, 1, out, W.rows / 2, nullptr, s);
+  else launch_lds_gemv<false, 0>(W, act, W.cols, 1, out, W.rows, nullptr, s);
+}
+
 void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,
                    uint64_t ld_out, int64_t* acc_out, int8_t* limbs, hipStream_t s) {
   if (W.rows == 0 || m == 0) return;
@@ -484,25 +533,8 @@ void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t 
       const uint32_t mm = uint32_t(m - t0 < 4 ? m - t0 : 4);
       int32_t* o = acc_out ? nullptr : out + t0 * ld_out;
       int64_t* ao = acc_out ? acc_out + t0 * ld_out : nullptr;
-      const uint64_t lds = uint64_t(mm) * 4 * (W.kpad + 32);
-      if (lds <= kGemvLdsBudget) {
-        const uint64_t ntiles = (W.rows + 15) / 16;
-        const uint64_t nsteps = W.kpad / 128;
-        int ks = ntiles <= 256 ? 8 : ntiles <= 512 ? 4 : ntiles <= 1024 ? 2 : 1;
-        while (ks > 1 && uint64_t(ks) > nsteps) ks >>= 1;
-        const uint64_t tpw = 8 / ks;
-        const uint64_t grid = std::min<uint64_t>((ntiles + tpw - 1) / tpw, 1024);
-        const int32_t* a = act + t0 * ld_act;
-#define DET_GEMV_LAUNCH(KS)                                                                                 \
-  hipLaunchKernelGGL(k_gemv_i8_lds<KS>, dim3(unsigned(grid)), dim3(kGemvThreads), size_t(lds), s, W.q, W.scale, \
-                     W.rowsum, a, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao)
-        switch (ks) {
-          case 8: DET_GEMV_LAUNCH(8); break;
-          case 4: DET_GEMV_LAUNCH(4); break;
-          case 2: DET_GEMV_LAUNCH(2); break;
-          default: DET_GEMV_LAUNCH(1); break;
-        }
-#undef DET_GEMV_LAUNCH
+      if (gemv_fits_lds(W, mm)) {
+        launch_lds_gemv<false, 0>(W, act + t0 * ld_act, ld_act, mm, o, ld_out, ao, s);
       } else {
         launch_act_limbs(act + t0 * ld_act, mm, W.cols, ld_act, W.kpad, limbs, s);
         hipLaunchKernelGGL(k_gemv_i8<8>, dim3(blocks_for(W.rows, 16)), dim3(512), 0, s, W.q, W.scale, W.rowsum,

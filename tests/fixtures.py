@@ -131,3 +131,45 @@ def golden_expected(name: str) -> dict:
 def tiny_gemma_dev():
     d = GOLDEN_DIR / "tiny_gemma_dev"
     return json.loads((d / "config.json").read_text()), (d / "model.detwgt").read_bytes()
+
+
+def custom_model(cfg: dict, seed: int, scale_max: int = 16, layer_scalars: bool = False):
+    """Seeded int8 x scale tensors for a Gemma text config, honouring
+    attention_k_eq_v (full layers without v_proj) and optional layer scalars.
+    Returns a list of (name, values, row_scale)."""
+    import sys
+    sys.path.insert(0, str(GOLDEN_DIR.parents[1] / "raster-inference_amd"))
+    from rasterdet import synthetic
+
+    tc = cfg["text_config"]
+    out = []
+    for idx, (name, shape) in enumerate(synthetic.model_tensor_shapes(cfg)):
+        if tc.get("attention_k_eq_v") and name.endswith("v_proj.weight"):
+            layer = int(name.split(".layers.")[1].split(".")[0])
+            if tc["layer_types"][layer] != "sliding_attention":
+                continue
+        ts = (seed * 1000003 + idx) & MASK64
+        if len(shape) == 1:
+            b = synthetic.hash_bytes(ts, shape[0]).astype(np.int32) % 33 - 16
+            out.append((name, (65536 + b * 1024).astype(np.int32), None))
+        else:
+            q, s = synthetic.fast_int8_matrix(ts, shape[0], shape[1], scale_max)
+            out.append((name, q, s))
+    if layer_scalars:
+        for l in range(tc["num_hidden_layers"]):
+            out.append((f"model.language_model.layers.{l}.layer_scalar", np.array([65536 - 4096 * (l + 1)], dtype=np.int32), None))
+    return out
+
+
+def load_both(cfg, tensors, ctx, threads=8):
+    """Builds the same model in the oracle and on the GPU."""
+    import oracle_lib
+    import rasterdet as rd
+
+    om = oracle_lib.OracleModel(cfg)
+    gm = rd.Model(ctx, cfg)
+    for name, v, s in tensors:
+        om.set_tensor(name, v, 32 if s is None else 8, s)
+        gm.set_tensor(name, v, s)
+    oracle_lib.set_threads(threads)
+    return om.finalize(), gm.finalize()
