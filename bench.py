@@ -98,9 +98,10 @@ def e4b_decode(ctx, rd, args) -> dict:
     tok = pr.next_token
     log(f"[bench] E4B prefill {args.prompt_len} tokens in {prefill_s * 1e3:.1f} ms")
     tokens = []
+    extra = rd.DET_DECODE_EAGER if getattr(args, "eager", False) else 0
     t0 = time.perf_counter()
     for _ in range(steps):
-        r = sess.decode(tok, rd.DET_COMMIT_NONE)
+        r = sess.decode(tok, rd.DET_COMMIT_NONE | extra)
         tok = r.next_token
         tokens.append(tok)
     ctx.synchronize()
@@ -173,6 +174,8 @@ def main() -> int:
     ap.add_argument("--e4b-layers", type=int, default=42)
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--prompt-len", type=int, default=512)
+    ap.add_argument("--decode-profile", action="store_true",
+                    help="only the E4B-shaped model: prefill, then 32 greedy decode steps (for rocprofv3 runs)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only 5 lm_head GEMV launches + 5 same-size device copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -186,6 +189,11 @@ def main() -> int:
     ctx = rd.Context(0)
     if args.profile_pass:
         return profile_pass(ctx, rd, args.seed)
+    if args.decode_profile:
+        args.decode_steps = 32
+        args.eager = True  # profiler kernel tracing of graph replays is not used
+        print(json.dumps(e4b_decode(ctx, rd, args)), flush=True)
+        return 0
     log("[bench] generating and uploading weights")
     problems, mats, copies = [], [], []
     for n, k in SHAPES:

@@ -209,6 +209,9 @@ typedef struct det_decode_result {
 /* Decode flag: run the per-operation kernel sequence instead of the fused,
  * graph-captured decode step (both are bit-identical; for cross-checks). */
 #define DET_DECODE_PER_OP 0x100u
+/* Decode flag: launch the fused step's kernels directly on the stream
+ * instead of replaying the captured graph (same kernels, same results). */
+#define DET_DECODE_EAGER 0x200u
 
 /* pipeline::run_prefill_pass_with_mode (runtime/pipeline.rs:55-98): embedding,
  * PLE inputs, every prefill_layer, prefill_finalize logits. */

@@ -57,6 +57,7 @@ void launch_dec_end(const int32_t* ff, int32_t* x, int32_t* normed, const int32_
                     int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, hipStream_t s);
 void launch_dec_qkv_post(const QkvPostArgs& a, bool own_cache, hipStream_t s);
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s);
+void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, hipStream_t s);
 void launch_dec_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s);
 
 }  // namespace det

@@ -311,6 +311,15 @@ __global__ __launch_bounds__(256) void k_dec_attn_wsum(AttnDecArgs a) {
   }
 }
 
+// Writes the step position and token (passed as kernel arguments) for the
+// graph-captured step that follows on the same stream.
+__global__ void k_dec_set_step(StepState* __restrict__ st, uint64_t position, uint32_t token) {
+  if (threadIdx.x == 0) {
+    st->position = position;
+    st->token = token;
+  }
+}
+
 __global__ void k_dec_softcap(int32_t* __restrict__ x, uint64_t n, int32_t cap) {
   const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) x[i] = softcap_act(x[i], cap);
@@ -341,6 +350,9 @@ void launch_dec_attention(const AttnDecArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(k_dec_attn_scores, dim3(a.nkv, nblk(a.cap, 32)), dim3(256), 0, s, a);
   hipLaunchKernelGGL(k_dec_attn_softmax, dim3(a.nh), dim3(256), 0, s, a);
   hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, 64)), dim3(256), 0, s, a);
+}
+void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, hipStream_t s) {
+  hipLaunchKernelGGL(k_dec_set_step, dim3(1), dim3(64), 0, s, st, position, token);
 }
 void launch_dec_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s) {
   hipLaunchKernelGGL(k_dec_softcap, dim3(nblk(n, 256)), dim3(256), 0, s, x, n, cap);

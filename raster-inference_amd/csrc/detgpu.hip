@@ -687,8 +687,6 @@ struct det_session {
   bool logits_valid = false;
   // fused decode step (HIP graph)
   det::StepState* st_dev = nullptr;
-  det::StepState* st_host = nullptr;
-  uint32_t* tok_host = nullptr;
   int32_t *qkv = nullptr, *qbuf = nullptr, *scores = nullptr, *weights = nullptr, *obuf = nullptr, *hbuf = nullptr,
           *ffbuf = nullptr;
   int64_t* attn_acc = nullptr;
@@ -701,8 +699,6 @@ struct det_session {
   ~det_session() {
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
-    if (st_host) (void)hipHostFree(st_host);
-    if (tok_host) (void)hipHostFree(tok_host);
     for (auto& c : kv) {
       if (c.k) (void)hipFree(c.k);
       if (c.v) (void)hipFree(c.v);
@@ -766,8 +762,6 @@ void session_alloc(det_session* s) {
     s->am_scratch = s->alloc<int64_t>((m->vocab + 1023) / 1024);
     s->am_out = s->alloc<uint32_t>(1);
     s->st_dev = s->alloc<det::StepState>(1);
-    HIPC(hipHostMalloc(reinterpret_cast<void**>(&s->st_host), sizeof(det::StepState), hipHostMallocDefault));
-    HIPC(hipHostMalloc(reinterpret_cast<void**>(&s->tok_host), sizeof(uint32_t), hipHostMallocDefault));
   }
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
@@ -1150,13 +1144,15 @@ void decode_fused(det_session* s, uint32_t token, uint32_t flags, det_decode_res
     const GKv& c = s->kv[l];
     if (!m->layers[l].donor && !c.has) bail("deterministic decode cache append requires canonical key rows");
   }
-  if (!s->exec) build_decode_graph(s);
+  const bool eager = flags & DET_DECODE_EAGER;
+  if (!eager && !s->exec) build_decode_graph(s);
   const uint64_t pos = s->position;
-  s->st_host->position = pos;
-  s->st_host->token = token;
-  HIPC(hipMemcpyAsync(s->st_dev, s->st_host, sizeof(det::StepState), hipMemcpyHostToDevice, st));
-  HIPC(hipGraphLaunch(s->exec, st));
-  HIPC(hipMemcpyAsync(s->tok_host, s->am_out, 4, hipMemcpyDeviceToHost, st));
+  det::launch_dec_set_step(s->st_dev, pos, token, st);
+  HIPC(hipGetLastError());
+  if (eager) enqueue_fused_step(s);
+  else HIPC(hipGraphLaunch(s->exec, st));
+  uint32_t next = 0;
+  HIPC(hipMemcpyAsync(&next, s->am_out, 4, hipMemcpyDeviceToHost, st));
   HIPC(hipStreamSynchronize(st));
   for (size_t l = 0; l < m->layers.size(); ++l)
     if (!m->layers[l].donor) kv_advance(s->kv[l], pos + 1);
@@ -1173,7 +1169,7 @@ void decode_fused(det_session* s, uint32_t token, uint32_t flags, det_decode_res
   }
   out->kv[0] = 0;
   if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
-  out->next_token = *s->tok_host;
+  out->next_token = next;
 }
 
 std::unique_ptr<det_session> clone_session(const det_session* src) {

@@ -22,6 +22,7 @@ DET_STORAGE_INT8, DET_STORAGE_I16, DET_STORAGE_I32 = 8, 16, 32
 DET_EW_ADD, DET_EW_GELU_MUL, DET_EW_SCALE, DET_EW_SOFTCAP = 0, 1, 2, 3
 DET_COMMIT_NONE, DET_COMMIT_ACTIVATIONS, DET_COMMIT_KV, DET_COMMIT_ALL = 0, 1, 2, 3
 DET_DECODE_PER_OP = 0x100
+DET_DECODE_EAGER = 0x200
 
 
 class DetError(RuntimeError):
