@@ -15,19 +15,27 @@ struct StepState {
   uint32_t pad;
 };
 
+// One RoPE inverse-frequency table; its cos/sin pairs for the step position
+// occupy trig[2 * offset, 2 * (offset + pairs)).
+struct RopeTable {
+  const int64_t* inv_freq;
+  uint32_t pairs, offset;
+};
+
 struct QkvPostArgs {
-  const int32_t* qkv;  // fused projection output: [q heads | k heads | v heads (if has_v)]
-  int32_t* qbuf;       // normalised + rotated queries [nh][hd]
+  int64_t* qkv;    // fused projection accumulators [q heads | k heads | v heads (if has_v)], cleared after use
+  int32_t* qbuf;   // normalised + rotated queries [nh][hd]
   int32_t* kc;         // layer KV cache rows [cap][nkv*hd]
   int32_t* vc;
   const int32_t* q_norm;
   const int32_t* k_norm;
-  const int64_t* inv_freq;
+  const int32_t* trig;  // this layer's (cos, sin) pairs at the step position
   const StepState* st;
   int64_t eps;
   uint64_t cap, rotary;
   uint32_t nh, nkv, hd;
   int ring, has_v;
+  int own_cache;  // 0 for layers that read a donor's cache (their projection has query rows only)
 };
 
 struct AttnDecArgs {
@@ -36,28 +44,37 @@ struct AttnDecArgs {
   const int32_t* v;
   const StepState* st;
   uint64_t cap, window;
-  uint64_t max_rows;  // row stride of the scores / weights scratch (>= cap)
+  uint64_t max_rows;  // row stride of the scores scratch (>= cap)
   int ring;
   uint32_t hd, nh, nkv;
-  int32_t* scores;   // scratch [nh][max_rows]
-  int32_t* weights;  // scratch [nh][max_rows]
-  int64_t* acc;      // [nh][hd] wrapped weighted sums (requantized by the O projection)
+  int32_t* scores;  // scratch [nh][max_rows]
+  int64_t* acc;     // [nh][hd] wrapped weighted sums (requantized by the O projection)
 };
 
 // Limits of the fused decode kernels.
 constexpr uint32_t kDecMaxHeadDim = 512;
 constexpr uint32_t kDecMaxGroup = 8;
-constexpr uint64_t kDecMaxHidden = 15360;  // one LDS row of int32 per single-workgroup row kernel
+constexpr uint64_t kDecMaxHidden = 15360;  // 1024 threads x 15 elements per single-workgroup row kernel
+constexpr uint32_t kAttnScoreRows = 16;     // window rows per scores workgroup
+constexpr uint32_t kAttnWsumRows = 32;      // window rows per softmax / weighted-sum workgroup
 
+// The normalised rows are written as int32 (normed) and as limb planes
+// (limbs, plane stride kpad) for the decode GEMV.
 void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, uint64_t H, int32_t* x, int32_t* dec_in,
-                      const int32_t* w_in, int64_t eps, int32_t* normed, hipStream_t s);
-void launch_dec_mid(const int32_t* o, int32_t* x, int32_t* normed, const int32_t* w_post, const int32_t* w_pre,
-                    uint64_t H, int64_t eps, hipStream_t s);
-void launch_dec_end(const int32_t* ff, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
-                    int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, hipStream_t s);
-void launch_dec_qkv_post(const QkvPostArgs& a, bool own_cache, hipStream_t s);
+                      const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s);
+// x = add_sat(x, rmsnorm(requant(src), w_post)) [* scalar]; normed = rmsnorm(x, w_next);
+// src (wrapping Q32.32 accumulators) is cleared after use.
+void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
+                              int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
+                              uint64_t kpad, hipStream_t s);
+void launch_dec_qkv_post(const QkvPostArgs& a, hipStream_t s);
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s);
-void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, hipStream_t s);
+// part 0: scores; part 1: softmax + weighted sum
+void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s);
+// Writes the step position and token and every RoPE table's cos/sin pairs at
+// that position (trig: 2 * total_pairs int32).
+void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, const RopeTable* tables, uint32_t ntables,
+                         uint32_t total_pairs, int32_t* trig, hipStream_t s);
 void launch_dec_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s);
 
 }  // namespace det

@@ -16,8 +16,6 @@
 
 namespace det {
 
-constexpr int kRowThreads = 1024;
-
 __device__ __forceinline__ int64_t wsum_sat(int64_t v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = add_sat64(v, __shfl_xor(v, o, 64));
@@ -36,27 +34,23 @@ __device__ __forceinline__ int64_t wmax(int64_t v) {
   }
   return v;
 }
-// op 1: saturating sum of non-negative terms, op 2: max. All threads get the result.
+// rms scale (ops.rs:406-425) of a row spread over the block, from each
+// thread's saturating partial sum of squares. The saturating sum of
+// non-negative terms is min(total, i64::MAX) in any order. One wave reduces the
+// wave partials and computes the scale once; it reaches the block through LDS.
 template <int NT>
-__device__ __forceinline__ int64_t blk_reduce(int64_t v, int op, int64_t* red) {
-  constexpr int NW = NT / 64;
+__device__ __forceinline__ int32_t blk_rms_scale(int64_t ss, uint64_t n, int64_t eps, int64_t* red, int32_t* bc) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  v = op == 1 ? wsum_sat(v) : wmax(v);
+  ss = wsum_sat(ss);
+  if (lane == 0) red[wave] = ss;
   __syncthreads();
-  if (lane == 0) red[wave] = v;
+  if (wave == 0) {
+    int64_t t = lane < NT / 64 ? red[lane] : 0;
+    t = wsum_sat(t);
+    if (lane == 0) *bc = rms_scale_from_sumsq(t, uint32_t(n), eps);
+  }
   __syncthreads();
-  int64_t r = red[0];
-#pragma unroll
-  for (int w = 1; w < NW; ++w) r = op == 1 ? add_sat64(r, red[w]) : (red[w] > r ? red[w] : r);
-  return r;
-}
-// rms scale of a row held in LDS (ops.rs:406-425)
-template <int NT>
-__device__ __forceinline__ int32_t blk_rms_scale(const int32_t* v, uint64_t n, int64_t eps, int64_t* red) {
-  int64_t ss = 0;
-  for (uint64_t c = threadIdx.x; c < n; c += NT) ss = add_sat64(ss, sq_term(v[c]));
-  ss = blk_reduce<NT>(ss, 1, red);
-  return rms_scale_from_sumsq(ss, uint32_t(n), eps);
+  return *bc;
 }
 
 __device__ __forceinline__ int32_t wgt_bits(const DevMatrix& M, uint64_t r, uint64_t c) {
@@ -65,111 +59,155 @@ __device__ __forceinline__ int32_t wgt_bits(const DevMatrix& M, uint64_t r, uint
   return static_cast<const int32_t*>(M.w)[r * M.cols + c];
 }
 
+// Row kernels: one workgroup of NT threads, element c = tid + NT * e held in
+// registers (e < EPT, so rows up to NT * EPT), every global read issued first.
+// The normalised row is written as int32 and as the four limb planes (plane
+// stride kpad) that the next decode GEMV reads.
+__device__ __forceinline__ void put_row(int32_t* row, int8_t* limbs, uint64_t kpad, uint64_t c, int32_t v) {
+  row[c] = v;
+  const uint32_t u = uint32_t(v) ^ 0x00808080u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) limbs[j * kpad + c] = int8_t(uint8_t(u >> (8 * j)));
+}
+
 // Embed the step token (gemma/io.rs:2446-2518) and normalise it for layer 0.
-__global__ __launch_bounds__(kRowThreads) void k_dec_embed(DevMatrix E, const StepState* __restrict__ st,
-                                                          int32_t scale, uint64_t H, int32_t* __restrict__ x,
-                                                          int32_t* __restrict__ dec_in, const int32_t* __restrict__ w_in,
-                                                          int64_t eps, int32_t* __restrict__ normed) {
-  extern __shared__ int32_t row[];
-  __shared__ int64_t red[kRowThreads / 64];
+template <int NT, int EPT>
+__global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* __restrict__ st, int32_t scale,
+                                                   uint64_t H, int32_t* __restrict__ x, int32_t* __restrict__ dec_in,
+                                                   const int32_t* __restrict__ w_in, int64_t eps,
+                                                   int32_t* __restrict__ normed, int8_t* __restrict__ limbs,
+                                                   uint64_t kpad) {
+  __shared__ int64_t red[NT / 64];
+  __shared__ int32_t bc;
   const uint32_t tok = st->token;
-  for (uint64_t c = threadIdx.x; c < H; c += kRowThreads) {
-    const int32_t v = mul_sat(wgt_bits(E, tok, c), scale);
-    row[c] = v;
-    x[c] = v;
-    dec_in[c] = v;
+  int32_t v[EPT], w[EPT];
+  int64_t ss = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    const bool in = c < H;
+    w[e] = in ? w_in[c] : 0;
+    v[e] = in ? mul_sat(wgt_bits(E, tok, c), scale) : 0;
+    if (in) {
+      x[c] = v[e];
+      dec_in[c] = v[e];
+    }
+    ss = add_sat64(ss, sq_term(v[e]));
   }
-  __syncthreads();
-  const int32_t sc = blk_rms_scale<kRowThreads>(row, H, eps, red);
-  for (uint64_t c = threadIdx.x; c < H; c += kRowThreads) normed[c] = mul_sat(mul_sat(row[c], sc), w_in[c]);
+  const int32_t sc = blk_rms_scale<NT>(ss, H, eps, red, &bc);
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(v[e], sc), w[e]));
+  }
 }
 
-// After the O projection: x = add_sat(rmsnorm(o, w_post), x); normed = rmsnorm(x, w_pre)
-// (det_kernels.rs:1058-1075).
-__global__ __launch_bounds__(kRowThreads) void k_dec_mid(const int32_t* __restrict__ o, int32_t* __restrict__ x,
-                                                        int32_t* __restrict__ normed, const int32_t* __restrict__ w_post,
-                                                        const int32_t* __restrict__ w_pre, uint64_t H, int64_t eps) {
-  extern __shared__ int32_t row[];
-  __shared__ int64_t red[kRowThreads / 64];
-  for (uint64_t c = threadIdx.x; c < H; c += kRowThreads) row[c] = o[c];
-  __syncthreads();
-  const int32_t s1 = blk_rms_scale<kRowThreads>(row, H, eps, red);
-  __syncthreads();
-  for (uint64_t c = threadIdx.x; c < H; c += kRowThreads) {
-    const int32_t v = add_sat(x[c], mul_sat(mul_sat(row[c], s1), w_post[c]));
-    row[c] = v;
-    x[c] = v;
+// Residual add of a normalised sub-block output, then the next input norm:
+// x = add_sat(x, rmsnorm(requant(src), w_post)) (times the layer scalar at the end of a
+// layer); normed = rmsnorm(x, w_next) (det_kernels.rs:1058-1075, 1108-1133).
+// src holds the projection's wrapping accumulators and is cleared after use.
+template <int NT, int EPT>
+__global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ src, int32_t* __restrict__ x,
+                                                           int32_t* __restrict__ normed,
+                                                           const int32_t* __restrict__ w_post, int has_scalar,
+                                                           int32_t scalar, const int32_t* __restrict__ w_next,
+                                                           uint64_t H, int64_t eps, int8_t* __restrict__ limbs,
+                                                           uint64_t kpad) {
+  __shared__ int64_t red[NT / 64];
+  __shared__ int32_t bc;
+  int32_t o[EPT], xv[EPT], wp[EPT], wn[EPT];
+  int64_t ss = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    const bool in = c < H;
+    o[e] = in ? requant(src[c]) : 0;
+    if (in) src[c] = 0;
+    xv[e] = in ? x[c] : 0;
+    wp[e] = in ? w_post[c] : 0;
+    wn[e] = in ? w_next[c] : 0;
   }
-  __syncthreads();
-  const int32_t s2 = blk_rms_scale<kRowThreads>(row, H, eps, red);
-  for (uint64_t c = threadIdx.x; c < H; c += kRowThreads) normed[c] = mul_sat(mul_sat(row[c], s2), w_pre[c]);
-}
-
-// End of layer: x = add_sat(x, rmsnorm(ff, w_post_ff)); optional layer scalar;
-// normed = rmsnorm(x, w_next) for the next layer's input norm (or the final norm).
-__global__ __launch_bounds__(kRowThreads) void k_dec_end(const int32_t* __restrict__ ff, int32_t* __restrict__ x,
-                                                        int32_t* __restrict__ normed, const int32_t* __restrict__ w_post,
-                                                        int has_scalar, int32_t scalar, const int32_t* __restrict__ w_next,
-                                                        uint64_t H, int64_t eps) {
-  extern __shared__ int32_t row[];
-  __shared__ int64_t red[kRowThreads / 64];
-  for (uint64_t c = threadIdx.x; c < H; c += kRowThreads) row[c] = ff[c];
-  __syncthreads();
-  const int32_t s1 = blk_rms_scale<kRowThreads>(row, H, eps, red);
-  __syncthreads();
-  for (uint64_t c = threadIdx.x; c < H; c += kRowThreads) {
-    int32_t v = add_sat(x[c], mul_sat(mul_sat(row[c], s1), w_post[c]));
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) ss = add_sat64(ss, sq_term(o[e]));
+  const int32_t s1 = blk_rms_scale<NT>(ss, H, eps, red, &bc);
+  ss = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    int32_t v = add_sat(xv[e], mul_sat(mul_sat(o[e], s1), wp[e]));
     if (has_scalar) v = mul_sat(v, scalar);
-    row[c] = v;
-    x[c] = v;
+    xv[e] = v;
+    if (c < H) x[c] = v;
+    ss = add_sat64(ss, sq_term(c < H ? v : 0));
   }
-  __syncthreads();
-  const int32_t s2 = blk_rms_scale<kRowThreads>(row, H, eps, red);
-  for (uint64_t c = threadIdx.x; c < H; c += kRowThreads) normed[c] = mul_sat(mul_sat(row[c], s2), w_next[c]);
+  const int32_t s2 = blk_rms_scale<NT>(ss, H, eps, red, &bc);
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(xv[e], s2), wn[e]));
+  }
 }
 
-// Head norms, RoPE and KV append for one step (det_kernels.rs:952-998):
-// block r < nh: query head r; then nkv key heads; then nkv value heads.
+// Head norms, RoPE and KV append for one step (det_kernels.rs:952-998), one
+// wave per head row of the fused projection: block r < nh is query head r;
+// then nkv key heads (for k_eq_v layers each also yields its value head: the
+// same projection row, normalised without a gain); then nkv value heads when
+// the layer has v rows. Layers reading a donor's cache have query rows only.
+// The accumulators are requantized on load and cleared.
 __global__ __launch_bounds__(64) void k_dec_qkv_post(QkvPostArgs a) {
   extern __shared__ int32_t y[];
+  constexpr int kPer = kDecMaxHeadDim / 64;
   const int lane = threadIdx.x;
   const uint32_t r = blockIdx.x;
   const uint64_t pos = a.st->position;
   const uint64_t hd = a.hd, kvw = uint64_t(a.nkv) * hd;
-  const int32_t* src;
+  const uint64_t slot = a.ring ? pos % a.cap : pos;
+  int64_t* src = a.qkv + uint64_t(r) * hd;
   const int32_t* w = nullptr;
   int32_t* dst;
+  int32_t* vdst = nullptr;  // k_eq_v value head
   bool rope = a.rotary > 0;
-  const uint64_t slot = a.ring ? pos % a.cap : pos;
   if (r < a.nh) {
-    src = a.qkv + uint64_t(r) * hd;
     w = a.q_norm;
     dst = a.qbuf + uint64_t(r) * hd;
   } else if (r < a.nh + a.nkv) {
     const uint64_t h = r - a.nh;
-    src = a.qkv + (uint64_t(a.nh) + h) * hd;
     w = a.k_norm;
     dst = a.kc + slot * kvw + h * hd;
+    if (!a.has_v) vdst = a.vc + slot * kvw + h * hd;
   } else {
     const uint64_t h = r - a.nh - a.nkv;
-    src = a.qkv + (uint64_t(a.nh) + (a.has_v ? a.nkv : 0) + h) * hd;
     dst = a.vc + slot * kvw + h * hd;
     rope = false;
   }
+  int32_t xv[kPer];
   int64_t ss = 0;
-  for (uint64_t d = lane; d < hd; d += 64) ss = add_sat64(ss, sq_term(src[d]));
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint64_t d = lane + 64 * k;
+    xv[k] = 0;
+    if (d < hd) {
+      xv[k] = requant(src[d]);
+      src[d] = 0;
+    }
+    ss = add_sat64(ss, sq_term(xv[k]));
+  }
   ss = wsum_sat(ss);
   const int32_t sc = rms_scale_from_sumsq(ss, uint32_t(hd), a.eps);
-  for (uint64_t d = lane; d < hd; d += 64) {
-    const int32_t v = mul_sat(src[d], sc);
-    y[d] = w ? mul_sat(v, w[d]) : v;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint64_t d = lane + 64 * k;
+    if (d < hd) {
+      const int32_t v = mul_sat(xv[k], sc);
+      y[d] = w ? mul_sat(v, w[d]) : v;
+      if (vdst) vdst[d] = v;
+    }
   }
   __syncthreads();
   if (rope && pos != 0) {
     const uint64_t half = a.rotary / 2;
     for (uint64_t i = lane; i < half; i += 64) {
-      int32_t c, s;
-      sin_cos(rope_angle(pos, a.inv_freq[i]), &c, &s);
+      const int32_t c = a.trig[2 * i], s = a.trig[2 * i + 1];
       const int32_t lhs = y[i], rhs = y[i + half];
       y[i] = sub_sat(mul_sat(lhs, c), mul_sat(rhs, s));
       y[i + half] = add_sat(mul_sat(rhs, c), mul_sat(lhs, s));
@@ -180,143 +218,254 @@ __global__ __launch_bounds__(64) void k_dec_qkv_post(QkvPostArgs a) {
 }
 
 // Window of the attention cache at this step (cache_windows + key_start,
-// det_kernels.rs:297-311, 1005-1008), from the canonical slot placement.
+// det_kernels.rs:297-311, 1005-1008), from the canonical slot placement:
+// window row j sits at slot base + j, wrapped once around a ring of cap slots.
 struct Window {
-  uint64_t start, len, ks, cnt;
+  uint64_t base, cnt;
 };
 __device__ __forceinline__ Window attn_window(const AttnDecArgs& a) {
   const uint64_t n = a.st->position + 1;
+  const uint64_t len = a.ring ? (n < a.cap ? n : a.cap) : n;
+  const uint64_t start = (a.ring && n > a.cap) ? n % a.cap : 0;
+  const uint64_t ks = a.window ? (len > a.window ? len - a.window : 0) : 0;
   Window w;
-  w.len = a.ring ? (n < a.cap ? n : a.cap) : n;
-  w.start = a.ring ? (n - w.len) % a.cap : 0;
-  w.ks = a.window ? (w.len > a.window ? w.len - a.window : 0) : 0;
-  w.cnt = w.len - w.ks;
+  w.cnt = len - ks;
+  w.base = start + ks;
+  if (w.base >= a.cap) w.base -= a.cap;
   return w;
 }
 __device__ __forceinline__ uint64_t phys_row(const AttnDecArgs& a, const Window& w, uint64_t j) {
-  const uint64_t l = w.ks + j;
-  return a.ring ? (w.start + l) % a.cap : l;
+  const uint64_t p = w.base + j;
+  return p >= a.cap ? p - a.cap : p;
+}
+// Argmax key of a score at window row j: larger score first, then smaller j
+// (argmax_first order).
+__device__ __forceinline__ int64_t score_key(int32_t score, uint64_t j) {
+  return int64_t(uint64_t(int64_t(score)) << 32 | (0xffffffffull - j));
 }
 
-// Scores for all query heads of one KV head over a chunk of 32 window rows.
+// Scores of every query head of one KV head over kAttnScoreRows window rows
+// (ops.rs:318-333: wrapping dot product, requantized). Sixteen lanes share one
+// key row; the queries sit in LDS. Chunk 0 also zeroes the heads'
+// weighted-sum accumulators.
+template <bool VEC>
 __global__ __launch_bounds__(256) void k_dec_attn_scores(AttnDecArgs a) {
+  __shared__ int32_t ql[kDecMaxGroup * kDecMaxHeadDim];
   const Window win = attn_window(a);
-  const uint32_t kvh = blockIdx.x;
-  const uint64_t r0 = uint64_t(blockIdx.y) * 32;
+  const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
+  const uint64_t r0 = uint64_t(blockIdx.y) * kAttnScoreRows;
+  const uint64_t qoff = uint64_t(kvh) * G * hd;
+  if (blockIdx.y == 0)
+    for (uint32_t i = threadIdx.x; i < G * hd; i += 256) a.acc[qoff + i] = 0;
   if (r0 >= win.cnt) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t G = a.nh / a.nkv, hd = a.hd;
+  for (uint32_t i = threadIdx.x; i < G * hd; i += 256) ql[i] = a.q[qoff + i];
+  const uint32_t grp = threadIdx.x >> 4, li = threadIdx.x & 15;
+  const uint64_t j = r0 + grp;
+  const bool valid = j < win.cnt;
   const uint64_t kvw = uint64_t(a.nkv) * hd;
-  // each lane owns dims [4*lane + 256*j, +4)
-  constexpr int kMaxJ = 2;  // hd <= 512
-  constexpr int kMaxG = 8;
-  int32_t qv[kMaxG][kMaxJ][4];
+  const int32_t* krow = a.k + (valid ? phys_row(a, win, j) : 0) * kvw + uint64_t(kvh) * hd;
+  constexpr int kPer = kDecMaxHeadDim / 16;  // key values per lane
+  int32_t kr[kPer];
+  if (VEC) {
 #pragma unroll
-  for (int g = 0; g < kMaxG; ++g)
+    for (int t = 0; t < kPer / 4; ++t) {
+      const uint32_t d = 4 * li + 64 * t;
+      int4 v = make_int4(0, 0, 0, 0);
+      if (valid && d < hd) v = *reinterpret_cast<const int4*>(krow + d);
+      kr[4 * t] = v.x, kr[4 * t + 1] = v.y, kr[4 * t + 2] = v.z, kr[4 * t + 3] = v.w;
+    }
+  } else {
 #pragma unroll
-    for (int j = 0; j < kMaxJ; ++j)
+    for (int t = 0; t < kPer; ++t) {
+      const uint32_t d = li + 16 * t;
+      kr[t] = (valid && d < hd) ? krow[d] : 0;
+    }
+  }
+  __syncthreads();
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t d = 4 * lane + 256 * j + e;
-        qv[g][j][e] = (uint32_t(g) < G && d < hd) ? a.q[(uint64_t(kvh) * G + g) * hd + d] : 0;
+  for (int g = 0; g < int(kDecMaxGroup); ++g) {
+    if (uint32_t(g) >= G) break;
+    const int32_t* qg = ql + g * hd;
+    int64_t acc = 0;
+    if (VEC) {
+#pragma unroll
+      for (int t = 0; t < kPer / 4; ++t) {
+        const uint32_t d = 4 * li + 64 * t;
+        if (d < hd) {
+          const int4 q = *reinterpret_cast<const int4*>(qg + d);
+          acc = mac(acc, q.x, kr[4 * t]);
+          acc = mac(acc, q.y, kr[4 * t + 1]);
+          acc = mac(acc, q.z, kr[4 * t + 2]);
+          acc = mac(acc, q.w, kr[4 * t + 3]);
+        }
       }
-  for (uint64_t u = 0; u < 8; ++u) {
-    const uint64_t j_row = r0 + wave * 8 + u;
-    if (j_row >= win.cnt) break;
-    const int32_t* krow = a.k + phys_row(a, win, j_row) * kvw + uint64_t(kvh) * hd;
-    int64_t acc[kMaxG];
+    } else {
 #pragma unroll
-    for (int g = 0; g < kMaxG; ++g) acc[g] = 0;
-#pragma unroll
-    for (int j = 0; j < kMaxJ; ++j) {
-      const uint32_t d0 = 4 * lane + 256 * j;
-      if (d0 < hd) {
-        const int4 kv = *reinterpret_cast<const int4*>(krow + d0);
-        const int32_t kk[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-        for (int g = 0; g < kMaxG; ++g)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[g] = mac(acc[g], qv[g][j][e], kk[e]);
+      for (int t = 0; t < kPer; ++t) {
+        const uint32_t d = li + 16 * t;
+        if (d < hd) acc = mac(acc, qg[d], kr[t]);
       }
     }
 #pragma unroll
-    for (int g = 0; g < kMaxG; ++g) {
-      if (uint32_t(g) >= G) break;
-      const int64_t t = wsum_wrap(acc[g]);
-      if (lane == 0) a.scores[(uint64_t(kvh) * G + g) * a.max_rows + j_row] = requant(t);
+    for (int m = 8; m >= 1; m >>= 1) acc = int64_t(uint64_t(acc) + uint64_t(__shfl_xor(acc, m, 64)));
+    if (li == 0 && valid) {
+      const int32_t sc = requant(acc);
+      a.scores[(uint64_t(kvh) * G + g) * a.max_rows + j] = sc;
     }
   }
 }
 
-// Integer softmax per query head (ops.rs:230-258); zeroes the head's output
-// accumulators for the weighted-sum pass.
-__global__ __launch_bounds__(256) void k_dec_attn_softmax(AttnDecArgs a) {
-  __shared__ int64_t red[4];
+// Integer softmax (ops.rs:230-258) and weighted sum (ops.rs:336-351) over
+// kAttnWsumRows window rows for every query head of one KV head, 1024
+// threads. Each workgroup rebuilds the heads' argmax (first maximum) and exp
+// sum over the whole window from the scores, with 16 / G waves per head,
+// weights its own rows, and adds its wrapping partial sums to the accumulators
+// atomically (exact in any order). The workgroup holding a head's argmax row
+// also sums every weight of the window and applies the residual ONE - sum to
+// that row, as the reference does before the weighted sum.
+__global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
+  __shared__ int64_t red[16];
+  __shared__ int64_t hkey[kDecMaxGroup], hsum[kDecMaxGroup];
+  __shared__ int64_t el[kDecMaxGroup][kAttnWsumRows];
+  __shared__ int32_t wl[kDecMaxGroup][kAttnWsumRows];
+  __shared__ int64_t part[3][2 * 256];
   const Window win = attn_window(a);
-  const uint32_t h = blockIdx.x;
-  const int32_t* sc = a.scores + uint64_t(h) * a.max_rows;
-  int32_t* wt = a.weights + uint64_t(h) * a.max_rows;
-  for (uint64_t d = threadIdx.x; d < a.hd; d += 256) a.acc[uint64_t(h) * a.hd + d] = 0;
+  const uint64_t r0 = uint64_t(blockIdx.y) * kAttnWsumRows;
+  if (r0 >= win.cnt) return;
+  const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t nr = win.cnt - r0 < kAttnWsumRows ? win.cnt - r0 : kAttnWsumRows;
+  const uint64_t kvw = uint64_t(a.nkv) * hd;
+  // value rows of this chunk: slice sl takes rows 8 sl .. 8 sl + 7, dims dl and dl + 256
+  const uint32_t sl = threadIdx.x >> 8, dl = threadIdx.x & 255;
+  int32_t vp[2][kAttnWsumRows / 4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+      const uint32_t d = dl + 256 * j;
+      const uint64_t rr = sl * (kAttnWsumRows / 4) + k;
+      vp[j][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
+    }
+  // this wave's head and its rows r = wi * 64 + lane + stride * n
+  const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;
+  const bool active = g < G;
+  const uint64_t stride = 64 * uint64_t(wph);
+  const int32_t* scg = a.scores + (uint64_t(kvh) * G + (active ? g : 0)) * a.max_rows;
+  // argmax
   int64_t best = INT64_MIN;
-  for (uint64_t r = threadIdx.x; r < win.cnt; r += 256) {
-    const int64_t key = (int64_t(sc[r]) * 4294967296ll) | int64_t(0xffffffffu - uint32_t(r));
-    best = key > best ? key : best;
-  }
-  best = blk_reduce<256>(best, 2, red);
-  const uint32_t mi = 0xffffffffu - uint32_t(uint64_t(best));
-  const int32_t mx = sc[mi];
-  int64_t sum = 0;
-  for (uint64_t r = threadIdx.x; r < win.cnt; r += 256) sum = add_sat64(sum, softmax_exp(sc[r], mx));
-  sum = blk_reduce<256>(sum, 1, red);
-  int64_t ws = 0;
-  for (uint64_t r = threadIdx.x; r < win.cnt; r += 256) {
-    const int32_t w = softmax_weight(softmax_exp(sc[r], mx), sum);
-    wt[r] = w;
-    ws = add_sat64(ws, int64_t(w));
-  }
-  ws = blk_reduce<256>(ws, 1, red);
-  __syncthreads();
-  if (threadIdx.x == 0) wt[mi] = add_sat(wt[mi], sub_sat(kOneAct, sat32(ws)));
-}
-
-// Weighted sum over a chunk of 64 window rows for every query head of one KV
-// head; partial wrapping i64 sums are added atomically (exact in any order).
-__global__ __launch_bounds__(256) void k_dec_attn_wsum(AttnDecArgs a) {
-  __shared__ int32_t wl[8][64];
-  const Window win = attn_window(a);
-  const uint32_t kvh = blockIdx.x;
-  const uint64_t r0 = uint64_t(blockIdx.y) * 64;
-  if (r0 >= win.cnt) return;
-  const uint64_t nr = win.cnt - r0 < 64 ? win.cnt - r0 : 64;
-  const uint32_t G = a.nh / a.nkv, hd = a.hd;
-  const uint64_t kvw = uint64_t(a.nkv) * hd;
-  for (uint32_t idx = threadIdx.x; idx < G * 64; idx += 256) {
-    const uint32_t g = idx / 64, r = idx % 64;
-    wl[g][r] = r < nr ? a.weights[(uint64_t(kvh) * G + g) * a.max_rows + r0 + r] : 0;
-  }
-  __syncthreads();
-  for (uint32_t d = threadIdx.x; d < hd; d += 256) {
-    int64_t acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (uint64_t r = 0; r < nr; ++r) {
-      const int32_t v = a.v[phys_row(a, win, r0 + r) * kvw + uint64_t(kvh) * hd + d];
-#pragma unroll
-      for (int g = 0; g < 8; ++g)
-        if (uint32_t(g) < G) acc[g] = mac(acc[g], v, wl[g][r]);
+  if (active)
+    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
+      const int64_t k = score_key(scg[r], r);
+      best = k > best ? k : best;
     }
+  best = wmax(best);
+  if (lane == 0) red[wave] = best;
+  __syncthreads();
+  if (threadIdx.x < G) {
+    int64_t k = red[threadIdx.x * wph];
+    for (uint32_t w = 1; w < wph; ++w) k = red[threadIdx.x * wph + w] > k ? red[threadIdx.x * wph + w] : k;
+    hkey[threadIdx.x] = k;
+  }
+  __syncthreads();
+  const int64_t key = hkey[active ? g : 0];
+  const int32_t mx = int32_t(key >> 32);
+  const uint64_t mi = 0xffffffffull - (uint64_t(key) & 0xffffffffull);
+  // exp sum (non-negative terms with a total below 2^63: the saturating sum is
+  // the plain sum); this chunk's terms go to LDS
+  int64_t s = 0;
+  if (active)
+#pragma unroll 2
+    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
+      const int64_t e = softmax_exp(scg[r], mx);
+      s += e;
+      if (r >= r0 && r < r0 + nr) el[g][r - r0] = e;
+    }
+  s = wsum_wrap(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  if (threadIdx.x < G) {
+    int64_t t = 0;
+    for (uint32_t w = 0; w < wph; ++w) t += red[threadIdx.x * wph + w];
+    hsum[threadIdx.x] = t;
+  }
+  __syncthreads();
+  // raw weights of this chunk
+  if (threadIdx.x < G * kAttnWsumRows) {
+    const uint32_t gg = threadIdx.x / kAttnWsumRows, rr = threadIdx.x % kAttnWsumRows;
+    wl[gg][rr] = rr < nr ? softmax_weight(el[gg][rr], hsum[gg]) : 0;
+  }
+  // residual for heads whose argmax row is in this chunk: their waves sum
+  // every weight of the window
+  const bool owner = active && mi >= r0 && mi < r0 + nr;
+  int64_t ws = 0;
+  if (owner) {
+    const int64_t S = hsum[g];
+#pragma unroll 2
+    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) ws += softmax_weight(softmax_exp(scg[r], mx), S);
+  }
+  ws = wsum_wrap(ws);
+  __syncthreads();  // red[] from the exp sums has been read
+  if (lane == 0) red[wave] = ws;
+  __syncthreads();
+  if (threadIdx.x < G) {
+    const uint64_t m = 0xffffffffull - (uint64_t(hkey[threadIdx.x]) & 0xffffffffull);
+    if (m >= r0 && m < r0 + nr) {
+      int64_t t = 0;
+      for (uint32_t w = 0; w < wph; ++w) t += red[threadIdx.x * wph + w];
+      wl[threadIdx.x][m - r0] = add_sat(wl[threadIdx.x][m - r0], sub_sat(kOneAct, sat32(t)));
+    }
+  }
+  __syncthreads();
+  // weighted sums: 4 row slices per dim, combined in LDS, one atomic per dim
+  for (uint32_t gg = 0; gg < G; ++gg) {
+    int64_t p0 = 0, p1 = 0;
 #pragma unroll
-    for (int g = 0; g < 8; ++g)
-      if (uint32_t(g) < G)
-        atomicAdd(reinterpret_cast<unsigned long long*>(a.acc + (uint64_t(kvh) * G + g) * hd + d),
-                  static_cast<unsigned long long>(acc[g]));
+    for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+      const int32_t w = wl[gg][sl * (kAttnWsumRows / 4) + k];
+      p0 = mac(p0, vp[0][k], w);
+      p1 = mac(p1, vp[1][k], w);
+    }
+    if (sl > 0) {
+      part[sl - 1][dl] = p0;
+      part[sl - 1][256 + dl] = p1;
+    }
+    __syncthreads();
+    if (sl == 0) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        p0 = int64_t(uint64_t(p0) + uint64_t(part[q][dl]));
+        p1 = int64_t(uint64_t(p1) + uint64_t(part[q][256 + dl]));
+      }
+      int64_t* out = a.acc + (uint64_t(kvh) * G + gg) * hd;
+      if (dl < hd) atomicAdd(reinterpret_cast<unsigned long long*>(out + dl), static_cast<unsigned long long>(p0));
+      if (dl + 256 < hd)
+        atomicAdd(reinterpret_cast<unsigned long long*>(out + dl + 256), static_cast<unsigned long long>(p1));
+    }
+    __syncthreads();
   }
 }
 
 // Writes the step position and token (passed as kernel arguments) for the
-// graph-captured step that follows on the same stream.
-__global__ void k_dec_set_step(StepState* __restrict__ st, uint64_t position, uint32_t token) {
-  if (threadIdx.x == 0) {
+// graph-captured step that follows on the same stream, and the cos/sin pairs
+// of every RoPE table at that position (ops.rs:613-680 per pair).
+__global__ __launch_bounds__(256) void k_dec_set_step(StepState* __restrict__ st, uint64_t position, uint32_t token,
+                                                      const RopeTable* __restrict__ tables, uint32_t ntables,
+                                                      uint32_t total_pairs, int32_t* __restrict__ trig) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i == 0) {
     st->position = position;
     st->token = token;
+  }
+  if (i >= total_pairs) return;
+  for (uint32_t t = 0; t < ntables; ++t) {
+    const RopeTable tb = tables[t];
+    if (i >= tb.offset && i < tb.offset + tb.pairs) {
+      int32_t c, s;
+      sin_cos(rope_angle(position, tb.inv_freq[i - tb.offset]), &c, &s);
+      trig[2 * uint64_t(i)] = c;
+      trig[2 * uint64_t(i) + 1] = s;
+    }
   }
 }
 
@@ -328,31 +477,53 @@ __global__ void k_dec_softcap(int32_t* __restrict__ x, uint64_t n, int32_t cap) 
 // ---------------------------------------------------------------------------
 static inline unsigned nblk(uint64_t n, unsigned per) { return unsigned((n + per - 1) / per); }
 
+// Row kernels run 1024 threads with the fewest elements per thread that
+// cover the row (2, 4, 8 or 15; up to kDecMaxHidden).
+#define DET_ROW_DISPATCH(KERNEL, ...)                                                     \
+  do {                                                                                    \
+    if (H <= 2048)                                                                        \
+      hipLaunchKernelGGL((KERNEL<1024, 2>), dim3(1), dim3(1024), 0, s, __VA_ARGS__);      \
+    else if (H <= 4096)                                                                   \
+      hipLaunchKernelGGL((KERNEL<1024, 4>), dim3(1), dim3(1024), 0, s, __VA_ARGS__);      \
+    else if (H <= 8192)                                                                   \
+      hipLaunchKernelGGL((KERNEL<1024, 8>), dim3(1), dim3(1024), 0, s, __VA_ARGS__);      \
+    else                                                                                  \
+      hipLaunchKernelGGL((KERNEL<1024, 15>), dim3(1), dim3(1024), 0, s, __VA_ARGS__);     \
+  } while (0)
 void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, uint64_t H, int32_t* x, int32_t* dec_in,
-                      const int32_t* w_in, int64_t eps, int32_t* normed, hipStream_t s) {
-  hipLaunchKernelGGL(k_dec_embed, dim3(1), dim3(kRowThreads), H * 4, s, E, st, scale, H, x, dec_in, w_in, eps, normed);
+                      const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s) {
+  DET_ROW_DISPATCH(k_dec_embed, E, st, scale, H, x, dec_in, w_in, eps, normed, limbs, kpad);
 }
-void launch_dec_mid(const int32_t* o, int32_t* x, int32_t* normed, const int32_t* w_post, const int32_t* w_pre,
-                    uint64_t H, int64_t eps, hipStream_t s) {
-  hipLaunchKernelGGL(k_dec_mid, dim3(1), dim3(kRowThreads), H * 4, s, o, x, normed, w_post, w_pre, H, eps);
+void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
+                              int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
+                              uint64_t kpad, hipStream_t s) {
+  DET_ROW_DISPATCH(k_dec_residual_norm, src, x, normed, w_post, int(has_scalar), scalar, w_next, H, eps, limbs, kpad);
 }
-void launch_dec_end(const int32_t* ff, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
-                    int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, hipStream_t s) {
-  hipLaunchKernelGGL(k_dec_end, dim3(1), dim3(kRowThreads), H * 4, s, ff, x, normed, w_post, int(has_scalar), scalar,
-                     w_next, H, eps);
-}
-void launch_dec_qkv_post(const QkvPostArgs& a, bool own_cache, hipStream_t s) {
-  const unsigned blocks = a.nh + (own_cache ? 2 * a.nkv : 0);
+#undef DET_ROW_DISPATCH
+void launch_dec_qkv_post(const QkvPostArgs& a, hipStream_t s) {
+  const unsigned blocks = a.nh + (a.own_cache ? (a.has_v ? 2 : 1) * a.nkv : 0);
   hipLaunchKernelGGL(k_dec_qkv_post, dim3(blocks), dim3(64), a.hd * 4, s, a);
 }
-void launch_dec_attention(const AttnDecArgs& a, hipStream_t s) {
+void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
   // grids cover the cache capacity (every window fits in it); idle chunks exit
-  hipLaunchKernelGGL(k_dec_attn_scores, dim3(a.nkv, nblk(a.cap, 32)), dim3(256), 0, s, a);
-  hipLaunchKernelGGL(k_dec_attn_softmax, dim3(a.nh), dim3(256), 0, s, a);
-  hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, 64)), dim3(256), 0, s, a);
+  if (part == 0) {
+    const dim3 grid(a.nkv, nblk(a.cap, kAttnScoreRows));
+    if (a.hd % 64 == 0)
+      hipLaunchKernelGGL(k_dec_attn_scores<true>, grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(k_dec_attn_scores<false>, grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows)), dim3(1024), 0, s, a);
+  }
 }
-void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, hipStream_t s) {
-  hipLaunchKernelGGL(k_dec_set_step, dim3(1), dim3(64), 0, s, st, position, token);
+void launch_dec_attention(const AttnDecArgs& a, hipStream_t s) {
+  launch_dec_attention_part(a, 0, s);
+  launch_dec_attention_part(a, 1, s);
+}
+void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, const RopeTable* tables, uint32_t ntables,
+                         uint32_t total_pairs, int32_t* trig, hipStream_t s) {
+  hipLaunchKernelGGL(k_dec_set_step, dim3(total_pairs ? nblk(total_pairs, 256) : 1), dim3(256), 0, s, st, position,
+                     token, tables, ntables, total_pairs, trig);
 }
 void launch_dec_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s) {
   hipLaunchKernelGGL(k_dec_softcap, dim3(nblk(n, 256)), dim3(256), 0, s, x, n, cap);

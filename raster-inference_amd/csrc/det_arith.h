@@ -95,29 +95,36 @@ DET_HD int64_t acc_mul(int64_t lhs, int64_t rhs) {
 
 // inv_sqrt_acc (ops.rs:719-763): the c in [0, 2^31-1] nearest to
 // 2^32/sqrt(x) in the sense |c^2 x - 2^64| minimal, ties to even; x == 0 and
-// tiny x saturate to i32::MAX. Computed from a floating estimate of
-// floor(sqrt(2^64/x)) followed by exact integer correction.
-DET_HD u128 isq_prod(uint64_t c, uint64_t x) { return u128(c * c) * u128(x); }
+// tiny x saturate to i32::MAX.
+// With Q = floor(2^64 / x) and R = 2^64 - Q x (0 <= R < x):
+//   c^2 x <= 2^64  <=>  c^2 <= Q, so the lower candidate is isqrt(Q);
+//   |lo^2 x - 2^64| - |hi^2 x - 2^64| = D x + 2R with D = 2Q - lo^2 - hi^2,
+// whose sign follows from D alone unless D == -1 (then from 2R vs x).
+// Everything stays in 64-bit integers; no 128-bit products.
+DET_HD uint64_t isqrt_u64(uint64_t q) {  // floor(sqrt(q)) for q < 2^62
+  uint64_t c = uint64_t(__builtin_sqrt(double(q)));
+  while (c * c > q) --c;
+  while ((c + 1) * (c + 1) <= q) ++c;
+  return c;
+}
 DET_HD int32_t inv_sqrt_acc(int64_t x) {
-  if (x <= 0) return INT32_MAX;  // x == 0 (negative x is rejected upstream)
+  // (2^31-1)^2 * x <= 2^64 exactly for x <= 4
+  if (x <= 4) return INT32_MAX;  // includes x == 0 (negative x is rejected upstream)
   const uint64_t ux = uint64_t(x);
-  const u128 target = u128(1) << 64;
-  const uint64_t cmax = uint64_t(INT32_MAX);
-  if (isq_prod(cmax, ux) <= target) return INT32_MAX;
-  // low = max c with c^2 x <= 2^64 (exists below cmax here).
-  uint64_t low = uint64_t(4294967296.0 / __builtin_sqrt(double(ux)));
-  if (low > cmax) low = cmax;
-  while (low > 0 && isq_prod(low, ux) > target) --low;
-  while (low + 1 <= cmax && isq_prod(low + 1, ux) <= target) ++low;
-  const uint64_t up = low + 1 > cmax ? cmax : low + 1;
-  const u128 lp = isq_prod(low, ux), upp = isq_prod(up, ux);
-  const u128 le = target - lp;
-  const u128 ue = upp > target ? upp - target : 0;
-  uint64_t r;
-  if (up == low || le < ue) r = low;
-  else if (ue < le) r = up;
-  else r = (low & 1) == 0 ? low : up;
-  return int32_t(r);
+  uint64_t Q = UINT64_MAX / ux;
+  uint64_t R = UINT64_MAX - Q * ux + 1;  // 2^64 - Q x, in [1, x]
+  if (R == ux) {
+    ++Q;
+    R = 0;
+  }
+  const uint64_t lo = isqrt_u64(Q);  // < 2^31 - 1 since x >= 5
+  const uint64_t hi = lo + 1;
+  const int64_t D = int64_t(2 * Q - lo * lo - hi * hi);
+  const bool lo_nearer = D >= 0 ? false : (D <= -2 ? true : 2 * R < ux);
+  const bool tie = (D == 0 && R == 0) || (D == -1 && 2 * R == ux);
+  if (tie) return int32_t((lo & 1) == 0 ? lo : hi);
+  // D >= 0 with R > 0 or D == 0: the upper candidate is strictly nearer
+  return int32_t(lo_nearer ? lo : hi);
 }
 
 // rms_norm_scale from a saturated sum of squares (ops.rs:406-425). The
@@ -128,35 +135,74 @@ DET_HD int32_t rms_scale_from_sumsq(int64_t sumsq, uint32_t n, int64_t eps) {
 }
 DET_HD int64_t sq_term(int32_t v) { return int64_t(v) * int64_t(v); }
 
-// softmax exp term of a max-shifted logit (ops.rs:505-553, 261-263).
+// Round-half-even quotient of a non-negative v < 2^32 by a constant d.
+template <uint32_t d>
+DET_HD uint32_t div_rte_u32(uint32_t v) {
+  const uint32_t q = v / d, r = v - q * d;
+  return (2 * r > d || (2 * r == d && (q & 1))) ? q + 1 : q;
+}
+// acc_mul of two non-negative values below 2^32: the product fits in 64 bits.
+DET_HD uint32_t acc_mul_u32(uint32_t a, uint32_t b) {
+  const uint64_t p = uint64_t(a) * b;
+  const uint64_t q = p >> 32, r = p & 0xffffffffull;
+  return uint32_t((r > 0x80000000ull || (r == 0x80000000ull && (q & 1))) ? q + 1 : q);
+}
+
+// softmax exp term of a max-shifted logit (ops.rs:505-553, 261-263),
+// requires logit <= max_logit. With d = max_logit - logit the term is zero
+// for d >= 2^20 (delta <= -16 in Q32.32); below that, pos = d * 2^16 < 2^36,
+// the ln2 remainder r is below 2^32 and every power of r stays below 2^32, so
+// the series runs in 32x32->64-bit products with the reference's rounding.
 DET_HD int64_t softmax_exp(int32_t logit, int32_t max_logit) {
-  const int64_t delta = int64_t(sub_sat(logit, max_logit)) * 65536;  // act_to_acc, <= 0
-  const int64_t LN2 = 2977044472ll;
-  if (delta <= -(int64_t(16) << 32)) return 0;
-  const int64_t pos = -delta;
-  const int64_t shift = pos / LN2;
-  const int64_t r = pos - shift * LN2;
-  const int64_t r2 = acc_mul(r, r);
-  const int64_t r3 = acc_mul(r2, r);
-  const int64_t r4 = acc_mul(r3, r);
-  const int64_t r5 = acc_mul(r4, r);
-  const int64_t t = add_sat64(
-      add_sat64(kOneAcc, -r),
-      add_sat64(div_acc_u32(r2, 2),
-                add_sat64(-div_acc_u32(r3, 6), add_sat64(div_acc_u32(r4, 24), -div_acc_u32(r5, 120)))));
+  const int64_t d = int64_t(max_logit) - int64_t(logit);
+  if (d >= (int64_t(1) << 20)) return 0;
+  const uint64_t LN2 = 2977044472ull;
+  const uint64_t pos = uint64_t(d) << 16;
+  uint64_t shift = uint64_t(double(pos) * (1.0 / 2977044472.0));
+  int64_t r = int64_t(pos) - int64_t(shift * LN2);
+  while (r < 0) {
+    --shift;
+    r += int64_t(LN2);
+  }
+  while (r >= int64_t(LN2)) {
+    ++shift;
+    r -= int64_t(LN2);
+  }
+  const uint32_t r1 = uint32_t(r);
+  const uint32_t r2 = acc_mul_u32(r1, r1);
+  const uint32_t r3 = acc_mul_u32(r2, r1);
+  const uint32_t r4 = acc_mul_u32(r3, r1);
+  const uint32_t r5 = acc_mul_u32(r4, r1);
+  const int64_t t = kOneAcc - int64_t(r1) + int64_t(div_rte_u32<2>(r2)) - int64_t(div_rte_u32<6>(r3)) +
+                    int64_t(div_rte_u32<24>(r4)) - int64_t(div_rte_u32<120>(r5));
   if (t <= 0) return 0;
   return rshift_rte(t, unsigned(shift));  // shift <= 23 here
 }
 
 // Softmax raw weight: requantize(div_acc(exp, sum)) (ops.rs:266-268) for the
-// softmax domain 0 <= exp <= sum, sum > 0: round(exp * 2^32 / sum), then
-// requantize. The quotient is at most 2^32, so a double estimate corrected
-// with an exact 128-bit remainder gives the exact rounded value.
+// softmax domain 0 <= exp <= min(sum, 2^32), sum > 0: round(exp * 2^32 / sum)
+// ties to even, then requantize. A double estimate is within one of the floor
+// quotient; the remainder e*2^32 - q*sum is exact in wrapping 64-bit
+// arithmetic while |remainder| < 2^63, i.e. for sum < 2^61 (softmax over
+// fewer than 2^29 rows). Larger sums take 128-bit remainders.
 DET_HD int32_t softmax_weight(int64_t e, int64_t sum) {
-  const u128 num = u128(uint64_t(e)) << 32;
-  const uint64_t d = uint64_t(sum);
+  const uint64_t ue = uint64_t(e), d = uint64_t(sum);
   uint64_t q = uint64_t(double(e) * 4294967296.0 / double(sum));
-  // exact floor correction: q*d <= num < (q+1)*d
+  if (d < (uint64_t(1) << 61)) {
+    int64_t rem = int64_t((ue << 32) - q * d);
+    while (rem < 0) {
+      --q;
+      rem += int64_t(d);
+    }
+    while (rem >= int64_t(d)) {
+      ++q;
+      rem -= int64_t(d);
+    }
+    const uint64_t twice = uint64_t(rem) << 1;
+    if (twice > d || (twice == d && (q & 1))) ++q;
+    return requant(int64_t(q));
+  }
+  const u128 num = u128(ue) << 32;
   while (q > 0 && u128(q) * d > num) --q;
   while (u128(q + 1) * d <= num) ++q;
   const u128 rem = num - u128(q) * d;

@@ -334,7 +334,8 @@ struct GLayer {
           *post_ff_ln = nullptr, *ple_post_norm = nullptr;
   bool has_ple = false;
   std::optional<int32_t> layer_scalar;
-  int64_t* inv_freq = nullptr;  // rotary/2 entries
+  int64_t* inv_freq = nullptr;  // rotary/2 entries (shared by layers with the same table)
+  uint32_t trig_off = 0;        // first cos/sin pair of this layer's table in the step trig buffer
 };
 
 }  // namespace
@@ -367,6 +368,14 @@ struct det_model {
     bool has_v = true;
   };
   std::vector<Fused> fused;
+  // distinct RoPE tables (layers with the same base, base dim and pair count share one)
+  struct RopeKey {
+    int64_t base;
+    uint64_t fbd, pairs;
+  };
+  std::vector<std::pair<RopeKey, det::RopeTable>> rope_tables;
+  det::RopeTable* rope_tables_dev = nullptr;
+  uint32_t trig_pairs = 0;
   bool fused_ok = false;
 
   ~det_model() {
@@ -547,11 +556,22 @@ void finalize(det_model* m) {
       if (L.rotary > L.head_dim) contract("rope_rotate_pairs requires rotary_dim to fit within the input width");
       if (L.freq_base_dim < 2 || L.freq_base_dim % 2) contract("rope_rotate_pairs requires an even freq_base_dim of at least 2");
       if (L.rope_base <= 0) contract("rope_rotate_pairs requires a positive base");
-      std::vector<int64_t> tab(L.rotary / 2);
-      det::rope_inv_freq_table(L.rope_base, uint32_t(L.freq_base_dim), uint32_t(L.rotary / 2), tab.data());
-      HIPC(hipMalloc(&L.inv_freq, tab.size() * 8));
-      HIPC(hipMemcpy(L.inv_freq, tab.data(), tab.size() * 8, hipMemcpyHostToDevice));
-      m->owned_dev.push_back(L.inv_freq);
+      const det_model::RopeKey key{L.rope_base, L.freq_base_dim, L.rotary / 2};
+      for (const auto& [k, t] : m->rope_tables)
+        if (k.base == key.base && k.fbd == key.fbd && k.pairs == key.pairs) {
+          L.inv_freq = const_cast<int64_t*>(t.inv_freq);
+          L.trig_off = t.offset;
+        }
+      if (!L.inv_freq) {
+        std::vector<int64_t> tab(L.rotary / 2);
+        det::rope_inv_freq_table(L.rope_base, uint32_t(L.freq_base_dim), uint32_t(L.rotary / 2), tab.data());
+        HIPC(hipMalloc(&L.inv_freq, tab.size() * 8));
+        HIPC(hipMemcpy(L.inv_freq, tab.data(), tab.size() * 8, hipMemcpyHostToDevice));
+        m->owned_dev.push_back(L.inv_freq);
+        L.trig_off = m->trig_pairs;
+        m->rope_tables.push_back({key, det::RopeTable{L.inv_freq, uint32_t(L.rotary / 2), m->trig_pairs}});
+        m->trig_pairs += uint32_t(L.rotary / 2);
+      }
     }
   }
   if (ple > 0) {
@@ -596,12 +616,25 @@ void finalize(det_model* m) {
       const GLayer& L = m->layers[l];
       auto& F = m->fused[l];
       F.has_v = L.v != nullptr;
-      std::vector<const DevMatrix*> parts = {L.q, L.k};
-      if (L.v) parts.push_back(L.v);
+      // layers reading a donor's cache need the query rows only
+      std::vector<const DevMatrix*> parts = {L.q};
+      if (!L.donor) {
+        parts.push_back(L.k);
+        if (L.v) parts.push_back(L.v);
+      }
       F.qkv = fuse_rows(m->ctx, parts, false);
       F.gateup = fuse_rows(m->ctx, {L.gate, L.up}, true);
       if (!det::gemv_fits_lds(F.qkv, 1) || !det::gemv_fits_lds(F.gateup, 1)) ok = false;
+      // the normalised row's limb planes feed qkv, gate/up and the logits projection
+      if (F.qkv.kpad != m->lm_head->kpad || F.gateup.kpad != m->lm_head->kpad) ok = false;
     }
+  }
+  if (ok && !m->rope_tables.empty()) {
+    std::vector<det::RopeTable> tabs;
+    for (const auto& kt : m->rope_tables) tabs.push_back(kt.second);
+    HIPC(hipMalloc(&m->rope_tables_dev, tabs.size() * sizeof(det::RopeTable)));
+    m->owned_dev.push_back(m->rope_tables_dev);
+    HIPC(hipMemcpy(m->rope_tables_dev, tabs.data(), tabs.size() * sizeof(det::RopeTable), hipMemcpyHostToDevice));
   }
   m->fused_ok = ok;
   m->finalized = true;
@@ -687,9 +720,15 @@ struct det_session {
   bool logits_valid = false;
   // fused decode step (HIP graph)
   det::StepState* st_dev = nullptr;
-  int32_t *qkv = nullptr, *qbuf = nullptr, *scores = nullptr, *weights = nullptr, *obuf = nullptr, *hbuf = nullptr,
-          *ffbuf = nullptr;
+  int32_t *qbuf = nullptr, *scores = nullptr, *hbuf = nullptr;
+  // projection accumulators (wrapping Q32.32); each consumer kernel clears
+  // what it reads, so they are zero whenever a step starts
+  int64_t *qkv_acc = nullptr, *o_acc = nullptr, *ff_acc = nullptr;
+  // limb planes (4 x kpad bytes) of the normalised row and of the MLP hidden row
+  int8_t *limbs_x = nullptr, *limbs_ff = nullptr;
+  uint64_t kpad_x = 0;
   int64_t* attn_acc = nullptr;
+  int32_t* trig = nullptr;  // cos/sin pairs of every RoPE table at the step position
   int64_t* am_scratch = nullptr;
   uint32_t* am_out = nullptr;
   uint64_t score_stride = 0;
@@ -751,17 +790,28 @@ void session_alloc(det_session* s) {
     uint64_t nh = 0;
     for (const GLayer& L : m->layers) nh = std::max(nh, L.num_heads);
     s->score_stride = T;  // no attention window exceeds the session length
-    s->qkv = s->alloc<int32_t>(fr);
+    s->qkv_acc = s->alloc<int64_t>(fr);
+    s->o_acc = s->alloc<int64_t>(H);
+    s->ff_acc = s->alloc<int64_t>(H);
+    uint64_t kff = 0;
+    for (const GLayer& L : m->layers) kff = std::max(kff, L.down->kpad);
+    s->kpad_x = m->fused[0].qkv.kpad;
+    s->limbs_x = s->alloc<int8_t>(4 * s->kpad_x);
+    s->limbs_ff = s->alloc<int8_t>(4 * kff);
+    hipStream_t zst = m->ctx->stream;  // stream-ordered before any step (not inside a graph)
+    HIPC(hipMemsetAsync(s->limbs_x, 0, 4 * s->kpad_x, zst));
+    HIPC(hipMemsetAsync(s->limbs_ff, 0, 4 * kff, zst));
+    HIPC(hipMemsetAsync(s->qkv_acc, 0, fr * 8, zst));
+    HIPC(hipMemsetAsync(s->o_acc, 0, H * 8, zst));
+    HIPC(hipMemsetAsync(s->ff_acc, 0, H * 8, zst));
     s->qbuf = s->alloc<int32_t>(nhd);
     s->scores = s->alloc<int32_t>(nh * T);
-    s->weights = s->alloc<int32_t>(nh * T);
     s->attn_acc = s->alloc<int64_t>(nhd);
-    s->obuf = s->alloc<int32_t>(H);
     s->hbuf = s->alloc<int32_t>(ff);
-    s->ffbuf = s->alloc<int32_t>(H);
     s->am_scratch = s->alloc<int64_t>((m->vocab + 1023) / 1024);
     s->am_out = s->alloc<uint32_t>(1);
     s->st_dev = s->alloc<det::StepState>(1);
+    s->trig = s->alloc<int32_t>(2 * uint64_t(std::max<uint32_t>(m->trig_pairs, 1)));
   }
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
@@ -1086,33 +1136,35 @@ void enqueue_fused_step(det_session* s) {
   hipStream_t st = m->ctx->stream;
   const uint64_t H = m->hidden;
   det::launch_dec_embed(*m->embedding, s->st_dev, m->embed_scale, H, s->x, s->dec_in, m->layers[0].in_ln, m->eps,
-                        s->normed, st);
+                        s->normed, s->limbs_x, s->kpad_x, st);
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
     const auto& F = m->fused[l];
     GKv& own = s->kv[l];
-    det::launch_gemv_decode(F.qkv, s->normed, false, 0, s->qkv, st);
+    det::launch_gemv_dec(F.qkv, s->limbs_x, nullptr, s->qkv_acc, 0, nullptr, 0, st);
     det::QkvPostArgs qa{};
-    qa.qkv = s->qkv; qa.qbuf = s->qbuf; qa.kc = own.k; qa.vc = own.v;
-    qa.q_norm = L.q_norm; qa.k_norm = L.k_norm; qa.inv_freq = L.inv_freq; qa.st = s->st_dev; qa.eps = L.eps;
+    qa.qkv = s->qkv_acc; qa.qbuf = s->qbuf; qa.kc = own.k; qa.vc = own.v;
+    qa.q_norm = L.q_norm; qa.k_norm = L.k_norm; qa.trig = s->trig + 2 * uint64_t(L.trig_off); qa.st = s->st_dev; qa.eps = L.eps;
     qa.cap = own.cap; qa.rotary = L.rotary; qa.nh = uint32_t(L.num_heads); qa.nkv = uint32_t(L.num_kv_heads);
-    qa.hd = uint32_t(L.head_dim); qa.ring = own.ring; qa.has_v = F.has_v;
-    det::launch_dec_qkv_post(qa, !L.donor, st);
+    qa.hd = uint32_t(L.head_dim); qa.ring = own.ring; qa.has_v = F.has_v; qa.own_cache = !L.donor;
+    det::launch_dec_qkv_post(qa, st);
     const GKv& ac = L.donor ? s->kv[*L.donor] : own;
     det::AttnDecArgs aa{};
     aa.q = s->qbuf; aa.k = ac.k; aa.v = ac.v; aa.st = s->st_dev; aa.cap = ac.cap;
     aa.window = L.sliding ? *L.sliding_window : 0; aa.max_rows = s->score_stride; aa.ring = ac.ring;
     aa.hd = uint32_t(L.head_dim); aa.nh = uint32_t(L.num_heads); aa.nkv = uint32_t(L.num_kv_heads);
-    aa.scores = s->scores; aa.weights = s->weights; aa.acc = s->attn_acc;
+    aa.scores = s->scores; aa.acc = s->attn_acc;
     det::launch_dec_attention(aa, st);
-    det::launch_gemv_decode(*L.o, s->attn_acc, true, 0, s->obuf, st);
-    det::launch_dec_mid(s->obuf, s->x, s->normed, L.post_attn_ln, L.pre_ff_ln, H, L.eps, st);
-    det::launch_gemv_decode(F.gateup, s->normed, false, 1, s->hbuf, st);
-    det::launch_gemv_decode(*L.down, s->hbuf, false, 0, s->ffbuf, st);
+    det::launch_gemv_decode_acc(*L.o, s->attn_acc, true, s->o_acc, st);
+    det::launch_dec_residual_norm(s->o_acc, s->x, s->normed, L.post_attn_ln, false, 0, L.pre_ff_ln, H, L.eps,
+                                  s->limbs_x, s->kpad_x, st);
+    det::launch_gemv_dec(F.gateup, s->limbs_x, s->hbuf, nullptr, 1, s->limbs_ff, L.down->kpad, st);
+    det::launch_gemv_dec(*L.down, s->limbs_ff, nullptr, s->ff_acc, 0, nullptr, 0, st);
     const int32_t* w_next = l + 1 < m->layers.size() ? m->layers[l + 1].in_ln : m->final_norm;
-    det::launch_dec_end(s->ffbuf, s->x, s->normed, L.post_ff_ln, L.layer_scalar.has_value(),
-                        L.layer_scalar.value_or(0), w_next, H, L.eps, st);
+    det::launch_dec_residual_norm(s->ff_acc, s->x, s->normed, L.post_ff_ln, L.layer_scalar.has_value(),
+                                  L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st);
   }
+  // the vocabulary projection streams best through the 8-wave LDS kernel
   det::launch_gemv_decode(*m->lm_head, s->normed, false, 0, s->logits, st);
   if (m->softcap) det::launch_dec_softcap(s->logits, m->vocab, *m->softcap, st);
   det::launch_argmax(s->logits, m->vocab, s->am_scratch, s->am_out, st);
@@ -1147,7 +1199,8 @@ void decode_fused(det_session* s, uint32_t token, uint32_t flags, det_decode_res
   const bool eager = flags & DET_DECODE_EAGER;
   if (!eager && !s->exec) build_decode_graph(s);
   const uint64_t pos = s->position;
-  det::launch_dec_set_step(s->st_dev, pos, token, st);
+  det::launch_dec_set_step(s->st_dev, pos, token, m->rope_tables_dev, uint32_t(m->rope_tables.size()), m->trig_pairs,
+                           s->trig, st);
   HIPC(hipGetLastError());
   if (eager) enqueue_fused_step(s);
   else HIPC(hipGraphLaunch(s->exec, st));

@@ -52,6 +52,16 @@ void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t 
 bool gemv_fits_lds(const DevMatrix& W, uint64_t m);
 void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int epilogue, int32_t* out,
                         hipStream_t s);
+// Decode GEMV (one activation row) into wrapping Q32.32 accumulators that must
+// be zero on entry; K is split across workgroups with exact atomic adds.
+void launch_gemv_decode_acc(const DevMatrix& W, const void* act, bool act_i64, int64_t* acc, hipStream_t s);
+// Decode GEMV from an activation given as limb planes (4 planes of W.kpad
+// bytes). acc != null: wrapping Q32.32 sums added atomically (zero on entry);
+// else requantized to out, or with epilogue 1 (interleaved gate/up matrix)
+// out[f] = mul_sat(gelu(gate_f), up_f), also written as limb planes
+// (stride out_kpad) to out_limbs.
+void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int64_t* acc, int epilogue,
+                     int8_t* out_limbs, uint64_t out_kpad, hipStream_t s);
 
 void launch_rmsnorm(int32_t* x, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
                     int64_t eps, hipStream_t s);

@@ -6,6 +6,9 @@
 // the reference's serial order regardless of the launch shape.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <vector>
+
 #include <algorithm>
 
 #include "det_arith.h"
@@ -164,18 +167,29 @@ __device__ __forceinline__ int64_t limb_combine(const int64_t p[4], int32_t rows
 // EPI 0: requantize (or raw accumulators to acc_out). EPI 1: rows are
 // interleaved gate/up pairs per tile (rows 0-7 gate f..f+7, rows 8-15 up
 // f..f+7); out[f] = mul_sat(gelu(gate_f), up_f).
+// kchunks > 1 splits K across workgroups as well (block b takes K chunk
+// b % kchunks): each adds its wrapping share of the Q32.32 accumulator to
+// acc_out atomically (the sum over chunks is the accumulator exactly, since
+// the row scale distributes over wrapping sums); acc_out starts at zero.
 template <int KSPLIT, bool IN64, int EPI>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const void* __restrict__ act_v, uint64_t ld_act, uint64_t k, uint64_t n_rows, uint64_t kpad, uint32_t m,
-    int32_t* __restrict__ out, uint64_t ld_out, int64_t* __restrict__ acc_out) {
+    int32_t* __restrict__ out, uint64_t ld_out, int64_t* __restrict__ acc_out, uint32_t kchunks) {
   extern __shared__ __attribute__((aligned(16))) int8_t lds_limbs[];
   __shared__ v4i part[KSPLIT > 1 ? 8 : 1][64];
   constexpr int TPW = 8 / KSPLIT;
-  const uint64_t pstride = kpad + 32;
-  // prologue: limb planes, 4 activations per thread-iteration
-  for (uint64_t idx = threadIdx.x; idx < uint64_t(m) * (kpad / 4); idx += kGemvThreads) {
-    const uint64_t t = idx / (kpad / 4), c = (idx % (kpad / 4)) * 4;
+  const uint64_t nsteps = kpad / 128;
+  const uint32_t kc = blockIdx.x % kchunks;
+  const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
+  const uint64_t cs0 = kc * cper < nsteps ? kc * cper : nsteps;
+  const uint64_t cs1 = cs0 + cper < nsteps ? cs0 + cper : nsteps;
+  const uint64_t col0 = cs0 * 128, col1 = cs1 * 128;
+  const uint64_t pstride = cper * 128 + 32;
+  const uint64_t quads = (col1 - col0) / 4;
+  // prologue: limb planes of this K chunk, 4 activations per thread-iteration
+  for (uint64_t idx = threadIdx.x; idx < uint64_t(m) * quads; idx += kGemvThreads) {
+    const uint64_t t = idx / quads, c = col0 + (idx % quads) * 4;
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -194,7 +208,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
         const uint32_t b = (c + e < k) ? ((w[e] >> (8 * j)) & 0xffu) : 0u;
         packed |= b << (8 * e);
       }
-      *reinterpret_cast<uint32_t*>(lds_limbs + (t * 4 + j) * pstride + c) = packed;
+      *reinterpret_cast<uint32_t*>(lds_limbs + (t * 4 + j) * pstride + (c - col0)) = packed;
     }
   }
   __syncthreads();
@@ -203,14 +217,15 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
   const int slot = wave / KSPLIT, kp = wave % KSPLIT;
   const int at = i >> 2, aj = i & 3;
   const bool a_on = uint32_t(at) < m;
+  // LDS column (s - cs0) * 128 of this lane's limb plane
   const int8_t* abase = lds_limbs + (a_on ? (uint64_t(at) * 4 + aj) : 0) * pstride + 32 * g;
-  const uint64_t nsteps = kpad / 128;
-  const uint64_t per = (nsteps + KSPLIT - 1) / KSPLIT;
-  const uint64_t s0 = kp * per;
-  const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
+  const uint64_t per = (cs1 - cs0 + KSPLIT - 1) / KSPLIT;
+  const uint64_t s0 = cs0 + kp * per < cs1 ? cs0 + kp * per : cs1;
+  const uint64_t s1 = s0 + per < cs1 ? s0 + per : cs1;
   const uint64_t ntiles = (n_rows + 15) / 16;
+  const uint64_t groups = gridDim.x / kchunks;
   const v4i zero = {0, 0, 0, 0};
-  for (uint64_t base = uint64_t(blockIdx.x) * TPW; base < ntiles; base += uint64_t(gridDim.x) * TPW) {
+  for (uint64_t base = uint64_t(blockIdx.x / kchunks) * TPW; base < ntiles; base += groups * TPW) {
     const uint64_t tile = base + slot;
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles;
@@ -227,8 +242,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        a[2 * u] = a_on ? *reinterpret_cast<const v4i*>(abase + (s + u) * 128) : zero;
-        a[2 * u + 1] = a_on ? *reinterpret_cast<const v4i*>(abase + (s + u) * 128 + 16) : zero;
+        a[2 * u] = a_on ? *reinterpret_cast<const v4i*>(abase + (s - cs0 + u) * 128) : zero;
+        a[2 * u + 1] = a_on ? *reinterpret_cast<const v4i*>(abase + (s - cs0 + u) * 128 + 16) : zero;
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
@@ -236,8 +251,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     for (; s < s1; ++s) {
       const v4i b0 = t_on ? __builtin_nontemporal_load(bp + s * 128) : zero;
       const v4i b1 = t_on ? __builtin_nontemporal_load(bp + s * 128 + 1) : zero;
-      const v4i a0 = a_on ? *reinterpret_cast<const v4i*>(abase + s * 128) : zero;
-      const v4i a1 = a_on ? *reinterpret_cast<const v4i*>(abase + s * 128 + 16) : zero;
+      const v4i a0 = a_on ? *reinterpret_cast<const v4i*>(abase + (s - cs0) * 128) : zero;
+      const v4i a1 = a_on ? *reinterpret_cast<const v4i*>(abase + (s - cs0) * 128 + 16) : zero;
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
     }
@@ -256,6 +271,14 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     }
     if (kp == 0) {
       const bool ok = uint32_t(g) < m && b_on;
+      if (kchunks > 1) {
+        if (ok) {
+          const int64_t a = limb_combine(p, kc == 0 ? rowsum[row] : 0, scale[row]);
+          atomicAdd(reinterpret_cast<unsigned long long*>(acc_out + uint64_t(g) * ld_out + row),
+                    static_cast<unsigned long long>(a));
+        }
+        continue;
+      }
       const int64_t a = ok ? limb_combine(p, rowsum[row], scale[row]) : 0;
       if (EPI == 1) {
         const int32_t r = requant(a);
@@ -265,6 +288,105 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
         if (acc_out) acc_out[uint64_t(g) * ld_out + row] = a;
         else out[uint64_t(g) * ld_out + row] = requant(a);
       }
+    }
+  }
+}
+
+// Decode GEMV (one activation row) reading the activation as four limb planes
+// in global memory (plane j, column c: byte j of a_c ^ 0x00808080; zero past
+// k), so no workgroup prologue: the A operand loads issue with the weight
+// loads and hit L2. 256 threads = 4 waves; KS waves split a tile's K range
+// (4/KS tiles per workgroup and pass); kchunks splits K across workgroups.
+// Outputs: acc_out != null: wrapping Q32.32 partial sums added atomically
+// (acc_out zero on entry); else EPI 0: out = requant; EPI 1: interleaved
+// gate/up tiles, out[f] = mul_sat(gelu(gate_f), up_f), also written as limb
+// planes to out_limbs (plane stride out_kpad) for the next GEMV.
+template <int KS, int EPI>
+__global__ __launch_bounds__(256) void k_gemv_dec(const int8_t* __restrict__ q, const int32_t* __restrict__ scale,
+                                                  const int32_t* __restrict__ rowsum, const int8_t* __restrict__ limbs,
+                                                  uint64_t n_rows, uint64_t kpad, uint32_t kchunks,
+                                                  int32_t* __restrict__ out, int64_t* __restrict__ acc_out,
+                                                  int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
+  __shared__ v4i part[KS > 1 ? 4 : 1][64];
+  constexpr int TPW = 4 / KS;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const int slot = wave / KS, kp = wave % KS;
+  const uint64_t nsteps = kpad / 128;
+  const uint32_t kc = blockIdx.x % kchunks;
+  const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
+  const uint64_t cs0 = kc * cper < nsteps ? kc * cper : nsteps;
+  const uint64_t cs1 = cs0 + cper < nsteps ? cs0 + cper : nsteps;
+  const uint64_t per = (cs1 - cs0 + KS - 1) / KS;
+  const uint64_t s0 = cs0 + kp * per < cs1 ? cs0 + kp * per : cs1;
+  const uint64_t s1 = s0 + per < cs1 ? s0 + per : cs1;
+  // A rows 0-3 are the four limbs of the single activation row; rows 4-15 are zero
+  const bool a_on = i < 4;
+  const v4i* ap = reinterpret_cast<const v4i*>(limbs + (a_on ? uint64_t(i) * kpad : 0) + 32 * g);
+  const uint64_t ntiles = (n_rows + 15) / 16;
+  const uint64_t groups = gridDim.x / kchunks;
+  const v4i zero = {0, 0, 0, 0};
+  for (uint64_t base = uint64_t(blockIdx.x / kchunks) * TPW; base < ntiles; base += groups * TPW) {
+    const uint64_t tile = base + slot;
+    const uint64_t row = tile * 16 + i;
+    const bool t_on = tile < ntiles;
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 32);
+    v4i acc = zero;
+    uint64_t s = s0;
+    for (; s + 4 <= s1; s += 4) {
+      v4i b[8], a[8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        b[2 * u] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128) : zero;
+        b[2 * u + 1] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128 + 1) : zero;
+        a[2 * u] = a_on ? ap[(s + u) * 8] : zero;
+        a[2 * u + 1] = a_on ? ap[(s + u) * 8 + 1] : zero;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+    }
+    for (; s < s1; ++s) {
+      const v4i b0 = t_on ? __builtin_nontemporal_load(bp + s * 128) : zero;
+      const v4i b1 = t_on ? __builtin_nontemporal_load(bp + s * 128 + 1) : zero;
+      const v4i a0 = a_on ? ap[s * 8] : zero;
+      const v4i a1 = a_on ? ap[s * 8 + 1] : zero;
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+    }
+    int64_t p[4] = {acc[0], acc[1], acc[2], acc[3]};
+    if (KS > 1) {
+      part[wave][lane] = acc;
+      __syncthreads();
+      if (kp == 0) {
+#pragma unroll
+        for (int w = 1; w < KS; ++w) {
+          const v4i v = part[wave + w][lane];
+          p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+        }
+      }
+      __syncthreads();
+    }
+    if (kp != 0 || !t_on) continue;
+    // lanes g == 0 hold the limb sums of the activation row (token 0)
+    const bool ok = g == 0 && row < n_rows;
+    if (acc_out) {
+      if (ok) {
+        const int64_t a = limb_combine(p, kc == 0 ? rowsum[row] : 0, scale[row]);
+        atomicAdd(reinterpret_cast<unsigned long long*>(acc_out + row), static_cast<unsigned long long>(a));
+      }
+    } else if (EPI == 1) {
+      const int32_t r = ok ? requant(limb_combine(p, rowsum[row], scale[row])) : 0;
+      const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
+      if (ok && i < 8) {
+        const uint64_t f = tile * 8 + i;
+        const int32_t h = mul_sat(gelu_act(r), up);
+        out[f] = h;
+        const uint32_t u = uint32_t(h) ^ 0x00808080u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out_limbs[j * out_kpad + f] = int8_t(uint8_t(u >> (8 * j)));
+      }
+    } else if (ok) {
+      out[row] = requant(limb_combine(p, rowsum[row], scale[row]));
     }
   }
 }
@@ -493,19 +615,29 @@ void launch_act_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld, u
   hipLaunchKernelGGL(k_act_limbs, grid, dim3(256), 0, s, act, m, k, ld, kpad, limbs);
 }
 
+// In-workgroup K split: the smallest of 1, 2, 4, 8 that gives at least 512
+// workgroups while every wave keeps at least 4 K steps. The grid is capped at
+// 1024 workgroups, which then loop over tile groups.
+static int pick_ksplit(uint64_t ntiles, uint64_t nsteps) {
+  int ks = 1;
+  while (ks < 8 && (ntiles * ks + 7) / 8 < 512 && uint64_t(ks) * 2 * 4 <= nsteps) ks *= 2;
+  return ks;
+}
+
 template <bool IN64, int EPI>
 static void launch_lds_gemv(const DevMatrix& W, const void* act, uint64_t ld_act, uint32_t mm, int32_t* o,
-                            uint64_t ld_out, int64_t* ao, hipStream_t s) {
-  const uint64_t lds = uint64_t(mm) * 4 * (W.kpad + 32);
+                            uint64_t ld_out, int64_t* ao, hipStream_t s, int ks = 0, uint32_t kchunks = 1) {
   const uint64_t ntiles = (W.rows + 15) / 16;
   const uint64_t nsteps = W.kpad / 128;
-  int ks = ntiles <= 256 ? 8 : ntiles <= 512 ? 4 : ntiles <= 1024 ? 2 : 1;
-  while (ks > 1 && uint64_t(ks) > nsteps) ks >>= 1;
+  const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
+  const uint64_t lds = uint64_t(mm) * 4 * (cper * 128 + 32);
+  if (ks == 0) ks = pick_ksplit(ntiles, nsteps);
   const uint64_t tpw = 8 / ks;
-  const uint64_t grid = std::min<uint64_t>((ntiles + tpw - 1) / tpw, 1024);
+  const uint64_t groups = std::min<uint64_t>((ntiles + tpw - 1) / tpw, std::max<uint64_t>(1024 / kchunks, 1));
+  const uint64_t grid = groups * kchunks;
 #define DET_GEMV_LAUNCH(KS)                                                                                     \
   hipLaunchKernelGGL((k_gemv_i8_lds<KS, IN64, EPI>), dim3(unsigned(grid)), dim3(kGemvThreads), size_t(lds), s, W.q, \
-                     W.scale, W.rowsum, act, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao)
+                     W.scale, W.rowsum, act, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao, kchunks)
   switch (ks) {
     case 8: DET_GEMV_LAUNCH(8); break;
     case 4: DET_GEMV_LAUNCH(4); break;
@@ -522,6 +654,71 @@ void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int e
   if (act_i64) launch_lds_gemv<true, 0>(W, act, W.cols, 1, out, W.rows, nullptr, s);
   else if (epilogue == 1) launch_lds_gemv<false, 1>(W, act, W.cols, 1, out, W.rows / 2, nullptr, s);
   else launch_lds_gemv<false, 0>(W, act, W.cols, 1, out, W.rows, nullptr, s);
+}
+
+// Decode GEMV into wrapping Q32.32 accumulators that are zero on entry. Eight
+// waves split K inside each workgroup; K is further split across workgroups
+// (doubling) until the launch has at least 512 workgroups, keeping at least
+// one K step per wave and at most 1024 workgroups.
+void launch_gemv_decode_acc(const DevMatrix& W, const void* act, bool act_i64, int64_t* acc, hipStream_t s) {
+  const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
+  int ks = 8;
+  while (ks > 1 && uint64_t(ks) > nsteps) ks >>= 1;
+  const uint64_t groups = (ntiles * ks + 7) / 8;
+  uint32_t kc = 1;
+  while (groups * kc < 512 && groups * kc * 2 <= 1024 && uint64_t(kc) * 2 * ks <= nsteps) kc *= 2;
+  if (act_i64) launch_lds_gemv<true, 0>(W, act, W.cols, 1, nullptr, W.rows, acc, s, ks, kc);
+  else launch_lds_gemv<false, 0>(W, act, W.cols, 1, nullptr, W.rows, acc, s, ks, kc);
+}
+
+// Workgroups of a kernel that fit on the device at once (occupancy x CUs),
+// queried once per kernel.
+static uint64_t resident_blocks(const void* kernel, int threads) {
+  static std::mutex mu;
+  static std::vector<std::pair<const void*, uint64_t>> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& e : cache)
+    if (e.first == kernel) return e.second;
+  int dev = 0, cus = 0, per = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || cus <= 0 || per <= 0) {
+    cus = 256;
+    per = 1;
+  }
+  const uint64_t n = uint64_t(cus) * uint64_t(per);
+  cache.push_back({kernel, n});
+  return n;
+}
+
+template <int KS, int EPI>
+static void launch_gemv_dec_ks(const DevMatrix& W, const int8_t* limbs, uint32_t kc, uint64_t groups, int32_t* out,
+                               int64_t* acc, int8_t* out_limbs, uint64_t out_kpad, hipStream_t s) {
+  hipLaunchKernelGGL((k_gemv_dec<KS, EPI>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum, limbs,
+                     W.rows, W.kpad, kc, out, acc, out_limbs, out_kpad);
+}
+
+void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int64_t* acc, int epilogue,
+                     int8_t* out_limbs, uint64_t out_kpad, hipStream_t s) {
+  const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
+  const uint64_t cap = resident_blocks(reinterpret_cast<const void*>(&k_gemv_dec<4, 0>), 256);
+  auto groups = [&](int ks) { return (ntiles * ks + 3) / 4; };
+  // in-workgroup K split: smallest that fills the device, keeping >= 4 K steps per wave
+  int ks = 1;
+  while (ks < 4 && groups(ks) < cap && nsteps >= uint64_t(ks) * 2 * 4) ks *= 2;
+  // K chunks across workgroups (atomic outputs only) while the launch stays resident
+  uint32_t kc = 1;
+  if (acc)
+    while (groups(ks) * kc * 2 <= cap && nsteps >= uint64_t(ks) * kc * 2) kc *= 2;
+  const uint64_t g = std::min<uint64_t>(groups(ks), std::max<uint64_t>(cap / kc, 1));
+  if (epilogue == 1) {
+    if (ks == 4) launch_gemv_dec_ks<4, 1>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
+    else if (ks == 2) launch_gemv_dec_ks<2, 1>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
+    else launch_gemv_dec_ks<1, 1>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
+  } else {
+    if (ks == 4) launch_gemv_dec_ks<4, 0>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
+    else if (ks == 2) launch_gemv_dec_ks<2, 0>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
+    else launch_gemv_dec_ks<1, 0>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
+  }
 }
 
 void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,

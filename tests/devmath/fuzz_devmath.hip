@@ -46,6 +46,55 @@ int main(int argc, char** argv) {
   bad = 0; for (long i = 0; i < N; ++i) { int64_t v = pick64(); uint32_t d = uint32_t(rng()) >> (rng() % 32); if (!d) d = 1; int64_t o; orc_div_acc_by_u32(v, d, &o); if (det::div_acc_u32(v, d) != o) bad++; } report("div_acc_u32", N, bad);
   bad = 0; for (long i = 0; i < N; ++i) { int64_t a = pick64(), b = pick64(); if (det::acc_mul(a, b) != orc_acc_mul(a, b)) bad++; } report("acc_mul", N, bad);
   bad = 0; for (long i = 0; i < N; ++i) { int64_t x = pick64(); if (x < 0) x = -(x + 1); int32_t o; orc_inv_sqrt_acc(x, &o); if (det::inv_sqrt_acc(x) != o) { bad++; if (bad < 5) printf("  inv_sqrt x=%lld dev=%d orc=%d\n", (long long)x, det::inv_sqrt_acc(x), o); } } report("inv_sqrt_acc", N, bad);
+  // inv_sqrt_acc near the rounding boundaries: x where c^2 x or (c+1/2)^2 x
+  // sits next to 2^64, for random c, plus every x below 2^16.
+  bad = 0;
+  long nis = 0;
+  for (int64_t x = 0; x < (1 << 16); ++x, ++nis) { int32_t o; orc_inv_sqrt_acc(x, &o); if (det::inv_sqrt_acc(x) != o) bad++; }
+  for (long i = 0; i < N; ++i) {
+    const uint64_t c = 2 + rng() % ((1ull << 31) - 3);
+    const long double target = 18446744073709551616.0L;
+    const long double cc = (rng() & 1) ? (long double)c * c : ((long double)c + 0.5L) * ((long double)c + 0.5L);
+    const int64_t x0 = int64_t(target / cc);
+    for (int64_t dx = -2; dx <= 2; ++dx, ++nis) {
+      const int64_t x = x0 + dx;
+      if (x < 0) continue;
+      int32_t o;
+      orc_inv_sqrt_acc(x, &o);
+      if (det::inv_sqrt_acc(x) != o) { bad++; if (bad < 5) printf("  inv_sqrt_edge x=%lld dev=%d orc=%d\n", (long long)x, det::inv_sqrt_acc(x), o); }
+    }
+  }
+  report("inv_sqrt_acc_edges", nis, bad);
+  // softmax_exp over every max-shift gap that yields a non-zero term (and past it).
+  bad = 0;
+  long nexp = 0;
+  for (int64_t d = 0; d < (1 << 20) + 64; ++d, ++nexp) {
+    const int32_t m = int32_t(rng() % 2000000) - 1000000;
+    const int32_t l = int32_t(int64_t(m) - d);
+    int64_t o;
+    orc_attention_softmax_exp_term(l, m, &o);
+    if (det::softmax_exp(l, m) != o) { bad++; if (bad < 5) printf("  softmax_exp d=%lld dev=%lld orc=%lld\n", (long long)d, (long long)det::softmax_exp(l, m), (long long)o); }
+  }
+  report("softmax_exp_all_gaps", nexp, bad);
+  // softmax_weight at exact half-way quotients and near the 2^61 sum boundary.
+  bad = 0;
+  long nw = 0;
+  for (long i = 0; i < N; ++i, ++nw) {
+    const uint64_t sum = (1ull << 32) + (rng() % (1ull << (20 + rng() % 40)));
+    uint64_t e;
+    switch (i % 4) {
+      case 0: { const uint64_t q = rng() % (1ull << 32); e = uint64_t(((unsigned __int128)q * sum * 2 + sum) / ((unsigned __int128)1 << 33)); break; }
+      case 1: e = sum < (1ull << 32) ? sum : (1ull << 32); break;
+      case 2: e = rng() % ((1ull << 32) + 1); break;
+      default: e = 1 + rng() % 1024; break;
+    }
+    if (e > sum) e = sum;
+    const uint64_t s2 = (i % 7 == 0) ? (1ull << 61) - 1 - rng() % 3 : ((i % 11 == 0) ? (1ull << 61) + rng() % 3 : sum);
+    int64_t q;
+    orc_div_acc(int64_t(e), int64_t(s2), &q);
+    if (det::softmax_weight(int64_t(e), int64_t(s2)) != orc_requantize(q)) bad++;
+  }
+  report("softmax_weight_edges", nw, bad);
   bad = 0;
   for (long i = 0; i < N / 20; ++i) {
     const uint32_t n = 1 + rng() % 300;
