@@ -22,26 +22,19 @@ struct RopeTable {
   uint32_t pairs, offset;
 };
 
-struct QkvPostArgs {
-  int64_t* qkv;    // fused projection accumulators [q heads | k heads | v heads (if has_v)], cleared after use
-  int32_t* qbuf;   // normalised + rotated queries [nh][hd]
-  int32_t* kc;         // layer KV cache rows [cap][nkv*hd]
-  int32_t* vc;
+// One decode step's attention for one layer: head norms, RoPE and KV append
+// of the fused projection rows, then scores, integer softmax and weighted sums.
+struct AttnDecArgs {
+  int64_t* qkv;         // fused projection accumulators [q heads | k heads | v heads (if has_v)]; cleared here
   const int32_t* q_norm;
   const int32_t* k_norm;
   const int32_t* trig;  // this layer's (cos, sin) pairs at the step position
-  const StepState* st;
   int64_t eps;
-  uint64_t cap, rotary;
-  uint32_t nh, nkv, hd;
-  int ring, has_v;
-  int own_cache;  // 0 for layers that read a donor's cache (their projection has query rows only)
-};
-
-struct AttnDecArgs {
-  const int32_t* q;  // [nh][hd]
-  const int32_t* k;  // attention cache (own or donor) [cap][nkv*hd]
-  const int32_t* v;
+  uint64_t rotary;
+  int has_v;            // the projection has v rows (else k_eq_v: values are the un-gained key norms)
+  int own_cache;        // 0: reads a donor's cache and the projection has query rows only
+  int32_t* k;           // attention cache (own or donor) [cap][nkv*hd]
+  int32_t* v;
   const StepState* st;
   uint64_t cap, window;
   uint64_t max_rows;  // row stride of the scores scratch (>= cap)
@@ -49,13 +42,14 @@ struct AttnDecArgs {
   uint32_t hd, nh, nkv;
   int32_t* scores;  // scratch [nh][max_rows]
   int64_t* acc;     // [nh][hd] wrapped weighted sums (requantized by the O projection)
+  int scores_in_lds;  // the weighted-sum kernel keeps G x cap scores in LDS
 };
 
 // Limits of the fused decode kernels.
 constexpr uint32_t kDecMaxHeadDim = 512;
 constexpr uint32_t kDecMaxGroup = 8;
 constexpr uint64_t kDecMaxHidden = 15360;  // 1024 threads x 15 elements per single-workgroup row kernel
-constexpr uint32_t kAttnScoreRows = 16;     // window rows per scores workgroup
+constexpr uint32_t kAttnScoreRows = 32;     // window rows per scores workgroup (512 threads)
 constexpr uint32_t kAttnWsumRows = 32;      // window rows per softmax / weighted-sum workgroup
 
 // The normalised rows are written as int32 (normed) and as limb planes
@@ -67,9 +61,8 @@ void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, ui
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
                               uint64_t kpad, hipStream_t s);
-void launch_dec_qkv_post(const QkvPostArgs& a, hipStream_t s);
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s);
-// part 0: scores; part 1: softmax + weighted sum
+// part 0: head norms, RoPE, KV append and scores; part 1: softmax + weighted sum
 void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s);
 // Writes the step position and token and every RoPE table's cos/sin pairs at
 // that position (trig: 2 * total_pairs int32).

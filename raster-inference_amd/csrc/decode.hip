@@ -13,27 +13,15 @@
 #include "decode.h"
 #include "det_arith.h"
 #include "kernels.h"
+#include "wave.h"
 
 namespace det {
 
-__device__ __forceinline__ int64_t wsum_sat(int64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = add_sat64(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ int64_t wsum_wrap(int64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = int64_t(uint64_t(v) + uint64_t(__shfl_xor(v, o, 64)));
-  return v;
-}
-__device__ __forceinline__ int64_t wmax(int64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const int64_t w = __shfl_xor(v, o, 64);
-    v = w > v ? w : v;
-  }
-  return v;
-}
+// Wavefront reductions (DPP; every lane gets the result).
+__device__ __forceinline__ int64_t wsum_sat(int64_t v) { return wave_sum_sat64(v); }  // non-negative terms
+__device__ __forceinline__ int64_t wsum_wrap(int64_t v) { return wave_sum_wrap64(v); }
+__device__ __forceinline__ int64_t wmax(int64_t v) { return wave_max64(v); }
+
 // rms scale (ops.rs:406-425) of a row spread over the block, from each
 // thread's saturating partial sum of squares. The saturating sum of
 // non-negative terms is min(total, i64::MAX) in any order. One wave reduces the
@@ -148,90 +136,24 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
   }
 }
 
-// Head norms, RoPE and KV append for one step (det_kernels.rs:952-998), one
-// wave per head row of the fused projection: block r < nh is query head r;
-// then nkv key heads (for k_eq_v layers each also yields its value head: the
-// same projection row, normalised without a gain); then nkv value heads when
-// the layer has v rows. Layers reading a donor's cache have query rows only.
-// The accumulators are requantized on load and cleared.
-__global__ __launch_bounds__(64) void k_dec_qkv_post(QkvPostArgs a) {
-  extern __shared__ int32_t y[];
-  constexpr int kPer = kDecMaxHeadDim / 64;
-  const int lane = threadIdx.x;
-  const uint32_t r = blockIdx.x;
-  const uint64_t pos = a.st->position;
-  const uint64_t hd = a.hd, kvw = uint64_t(a.nkv) * hd;
-  const uint64_t slot = a.ring ? pos % a.cap : pos;
-  int64_t* src = a.qkv + uint64_t(r) * hd;
-  const int32_t* w = nullptr;
-  int32_t* dst;
-  int32_t* vdst = nullptr;  // k_eq_v value head
-  bool rope = a.rotary > 0;
-  if (r < a.nh) {
-    w = a.q_norm;
-    dst = a.qbuf + uint64_t(r) * hd;
-  } else if (r < a.nh + a.nkv) {
-    const uint64_t h = r - a.nh;
-    w = a.k_norm;
-    dst = a.kc + slot * kvw + h * hd;
-    if (!a.has_v) vdst = a.vc + slot * kvw + h * hd;
-  } else {
-    const uint64_t h = r - a.nh - a.nkv;
-    dst = a.vc + slot * kvw + h * hd;
-    rope = false;
-  }
-  int32_t xv[kPer];
-  int64_t ss = 0;
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const uint64_t d = lane + 64 * k;
-    xv[k] = 0;
-    if (d < hd) {
-      xv[k] = requant(src[d]);
-      src[d] = 0;
-    }
-    ss = add_sat64(ss, sq_term(xv[k]));
-  }
-  ss = wsum_sat(ss);
-  const int32_t sc = rms_scale_from_sumsq(ss, uint32_t(hd), a.eps);
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const uint64_t d = lane + 64 * k;
-    if (d < hd) {
-      const int32_t v = mul_sat(xv[k], sc);
-      y[d] = w ? mul_sat(v, w[d]) : v;
-      if (vdst) vdst[d] = v;
-    }
-  }
-  __syncthreads();
-  if (rope && pos != 0) {
-    const uint64_t half = a.rotary / 2;
-    for (uint64_t i = lane; i < half; i += 64) {
-      const int32_t c = a.trig[2 * i], s = a.trig[2 * i + 1];
-      const int32_t lhs = y[i], rhs = y[i + half];
-      y[i] = sub_sat(mul_sat(lhs, c), mul_sat(rhs, s));
-      y[i + half] = add_sat(mul_sat(rhs, c), mul_sat(lhs, s));
-    }
-    __syncthreads();
-  }
-  for (uint64_t d = lane; d < hd; d += 64) dst[d] = y[d];
-}
-
 // Window of the attention cache at this step (cache_windows + key_start,
 // det_kernels.rs:297-311, 1005-1008), from the canonical slot placement:
 // window row j sits at slot base + j, wrapped once around a ring of cap slots.
+// The step's own token is the last window row, at slot `slot`.
 struct Window {
-  uint64_t base, cnt;
+  uint64_t base, cnt, pos, slot;
 };
 __device__ __forceinline__ Window attn_window(const AttnDecArgs& a) {
-  const uint64_t n = a.st->position + 1;
+  Window w;
+  w.pos = a.st->position;
+  const uint64_t n = w.pos + 1;
   const uint64_t len = a.ring ? (n < a.cap ? n : a.cap) : n;
   const uint64_t start = (a.ring && n > a.cap) ? n % a.cap : 0;
   const uint64_t ks = a.window ? (len > a.window ? len - a.window : 0) : 0;
-  Window w;
   w.cnt = len - ks;
   w.base = start + ks;
   if (w.base >= a.cap) w.base -= a.cap;
+  w.slot = a.ring ? w.pos % a.cap : w.pos;
   return w;
 }
 __device__ __forceinline__ uint64_t phys_row(const AttnDecArgs& a, const Window& w, uint64_t j) {
@@ -244,47 +166,140 @@ __device__ __forceinline__ int64_t score_key(int32_t score, uint64_t j) {
   return int64_t(uint64_t(int64_t(score)) << 32 | (0xffffffffull - j));
 }
 
+// One head row of the fused projection, normalised by one wavefront
+// (det_kernels.rs:952-998): x = requant(acc) (the accumulators are read
+// here and cleared later), y = rmsnorm(x) * gain; the un-gained norm goes to
+// `plain` when given (k_eq_v values).
+__device__ __forceinline__ void norm_head_row(const int64_t* __restrict__ src, uint32_t hd, int64_t eps,
+                                              const int32_t* __restrict__ gain, int32_t* __restrict__ dst,
+                                              int32_t* __restrict__ plain, uint32_t lane) {
+  constexpr int kPer = kDecMaxHeadDim / 64;
+  int32_t xv[kPer], gv[kPer];
+  int64_t ss = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t d = lane + 64 * k;
+    xv[k] = d < hd ? requant(src[d]) : 0;
+    gv[k] = (gain && d < hd) ? gain[d] : 0;
+    ss = add_sat64(ss, sq_term(xv[k]));
+  }
+  ss = wsum_sat(ss);
+  const int32_t sc = rms_scale_from_sumsq(ss, hd, eps);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const uint32_t d = lane + 64 * k;
+    if (d < hd) {
+      const int32_t v = mul_sat(xv[k], sc);
+      dst[d] = gain ? mul_sat(v, gv[k]) : v;
+      if (plain) plain[d] = v;
+    }
+  }
+}
+
 // Scores of every query head of one KV head over kAttnScoreRows window rows
-// (ops.rs:318-333: wrapping dot product, requantized). Sixteen lanes share one
-// key row; the queries sit in LDS. Chunk 0 also zeroes the heads'
+// (ops.rs:318-333: wrapping dot product, requantized), 512 threads. The
+// workgroup first builds the normalised, rotated queries of its heads in LDS
+// (one wavefront per head row); the workgroup whose rows include the step's
+// own token also normalises and rotates the new key row, appends key and
+// value rows to the cache at the canonical slot and scores that row from LDS.
+// Sixteen lanes share one key row. Chunk 0 also zeroes the heads'
 // weighted-sum accumulators.
 template <bool VEC>
-__global__ __launch_bounds__(256) void k_dec_attn_scores(AttnDecArgs a) {
+__global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   __shared__ int32_t ql[kDecMaxGroup * kDecMaxHeadDim];
+  __shared__ int32_t kn[kDecMaxHeadDim];
   const Window win = attn_window(a);
   const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
   const uint64_t r0 = uint64_t(blockIdx.y) * kAttnScoreRows;
   const uint64_t qoff = uint64_t(kvh) * G * hd;
   if (blockIdx.y == 0)
-    for (uint32_t i = threadIdx.x; i < G * hd; i += 256) a.acc[qoff + i] = 0;
+    for (uint32_t i = threadIdx.x; i < G * hd; i += 512) a.acc[qoff + i] = 0;
   if (r0 >= win.cnt) return;
-  for (uint32_t i = threadIdx.x; i < G * hd; i += 256) ql[i] = a.q[qoff + i];
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t cur = win.cnt - 1;  // window row of the step's own token
+  const bool has_new = a.own_cache && cur >= r0 && cur < r0 + kAttnScoreRows;
+  const uint64_t kvw = uint64_t(a.nkv) * hd;
+  // this lane group's key row, fetched while the head rows are normalised
   const uint32_t grp = threadIdx.x >> 4, li = threadIdx.x & 15;
   const uint64_t j = r0 + grp;
   const bool valid = j < win.cnt;
-  const uint64_t kvw = uint64_t(a.nkv) * hd;
-  const int32_t* krow = a.k + (valid ? phys_row(a, win, j) : 0) * kvw + uint64_t(kvh) * hd;
-  constexpr int kPer = kDecMaxHeadDim / 16;  // key values per lane
+  const bool own_row = has_new && j == cur;
+  const int32_t* krow = a.k + ((valid && !own_row) ? phys_row(a, win, j) : 0) * kvw + uint64_t(kvh) * hd;
+  const bool kload = valid && !own_row;
+  constexpr int kPer = kDecMaxHeadDim / 16;
   int32_t kr[kPer];
   if (VEC) {
 #pragma unroll
     for (int t = 0; t < kPer / 4; ++t) {
       const uint32_t d = 4 * li + 64 * t;
       int4 v = make_int4(0, 0, 0, 0);
-      if (valid && d < hd) v = *reinterpret_cast<const int4*>(krow + d);
+      if (kload && d < hd) v = *reinterpret_cast<const int4*>(krow + d);
       kr[4 * t] = v.x, kr[4 * t + 1] = v.y, kr[4 * t + 2] = v.z, kr[4 * t + 3] = v.w;
     }
   } else {
 #pragma unroll
     for (int t = 0; t < kPer; ++t) {
       const uint32_t d = li + 16 * t;
-      kr[t] = (valid && d < hd) ? krow[d] : 0;
+      kr[t] = (kload && d < hd) ? krow[d] : 0;
+    }
+  }
+  // cos/sin of this thread's first two rotation slots, fetched early (later
+  // slots, for rows x half > 1024, load theirs in the rotation loop)
+  const uint32_t half = uint32_t(a.rotary / 2);
+  int32_t tc[2] = {0, 0}, ts[2] = {0, 0};
+  if (half)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t idx = threadIdx.x + 512 * u;
+      const uint32_t i = idx % half;
+      tc[u] = a.trig[2 * i];
+      ts[u] = a.trig[2 * i + 1];
+    }
+  // head rows: jobs 0..G-1 are the queries, then the new key (and value) rows
+  const uint32_t nkeys = has_new ? (a.has_v ? 2 : 1) : 0;
+  int32_t* kslot = a.k + win.slot * kvw + uint64_t(kvh) * hd;
+  int32_t* vslot = a.v + win.slot * kvw + uint64_t(kvh) * hd;
+  for (uint32_t job = wave; job < G + nkeys; job += 8) {
+    if (job < G) {
+      norm_head_row(a.qkv + (uint64_t(kvh) * G + job) * hd, hd, a.eps, a.q_norm, ql + job * hd, nullptr, lane);
+    } else if (job == G) {
+      norm_head_row(a.qkv + (uint64_t(a.nh) + kvh) * hd, hd, a.eps, a.k_norm, kn, a.has_v ? nullptr : vslot, lane);
+    } else {
+      norm_head_row(a.qkv + (uint64_t(a.nh) + a.nkv + kvh) * hd, hd, a.eps, nullptr, vslot, nullptr, lane);
     }
   }
   __syncthreads();
+  if (half && win.pos != 0) {
+    const uint32_t rows = G + (has_new ? 1 : 0);
+    for (uint32_t idx = threadIdx.x, u = 0; idx < rows * half; idx += 512, ++u) {
+      const uint32_t r = idx / half, i = idx % half;
+      int32_t* y = r < G ? ql + r * hd : kn;
+      const int32_t c = u == 0 ? tc[0] : (u == 1 ? tc[1] : a.trig[2 * i]);
+      const int32_t s = u == 0 ? ts[0] : (u == 1 ? ts[1] : a.trig[2 * i + 1]);
+      const int32_t lhs = y[i], rhs = y[i + half];
+      y[i] = sub_sat(mul_sat(lhs, c), mul_sat(rhs, s));
+      y[i + half] = add_sat(mul_sat(rhs, c), mul_sat(lhs, s));
+    }
+    __syncthreads();
+  }
+  if (has_new)
+    for (uint32_t d = threadIdx.x; d < hd; d += 512) kslot[d] = kn[d];
+  if (own_row) {
+    if (VEC) {
 #pragma unroll
-  for (int g = 0; g < int(kDecMaxGroup); ++g) {
-    if (uint32_t(g) >= G) break;
+      for (int t = 0; t < kPer / 4; ++t) {
+        const uint32_t d = 4 * li + 64 * t;
+        if (d < hd) kr[4 * t] = kn[d], kr[4 * t + 1] = kn[d + 1], kr[4 * t + 2] = kn[d + 2], kr[4 * t + 3] = kn[d + 3];
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) {
+        const uint32_t d = li + 16 * t;
+        if (d < hd) kr[t] = kn[d];
+      }
+    }
+  }
+  for (uint32_t g = 0; g < G; ++g) {
     const int32_t* qg = ql + g * hd;
     int64_t acc = 0;
     if (VEC) {
@@ -306,33 +321,41 @@ __global__ __launch_bounds__(256) void k_dec_attn_scores(AttnDecArgs a) {
         if (d < hd) acc = mac(acc, qg[d], kr[t]);
       }
     }
-#pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) acc = int64_t(uint64_t(acc) + uint64_t(__shfl_xor(acc, m, 64)));
-    if (li == 0 && valid) {
-      const int32_t sc = requant(acc);
-      a.scores[(uint64_t(kvh) * G + g) * a.max_rows + j] = sc;
-    }
+    acc = int64_t(row16_reduce(uint64_t(acc), OpWrapAdd()));  // the 16 lanes of this key row
+    if (li == 0 && valid) a.scores[(uint64_t(kvh) * G + g) * a.max_rows + j] = requant(acc);
   }
 }
 
 // Integer softmax (ops.rs:230-258) and weighted sum (ops.rs:336-351) over
 // kAttnWsumRows window rows for every query head of one KV head, 1024
 // threads. Each workgroup rebuilds the heads' argmax (first maximum) and exp
-// sum over the whole window from the scores, with 16 / G waves per head,
-// weights its own rows, and adds its wrapping partial sums to the accumulators
-// atomically (exact in any order). The workgroup holding a head's argmax row
-// also sums every weight of the window and applies the residual ONE - sum to
-// that row, as the reference does before the weighted sum.
+// sum over the whole window from the scores, with 16 / G waves per head (each
+// thread keeps the scores it reads in LDS for the later passes when they
+// fit), weights its own rows, and adds its wrapping partial sums to the
+// accumulators atomically (exact in any order). The workgroup holding a
+// head's argmax row also sums every weight of the window and applies the
+// residual ONE - sum to that row, as the reference does before the weighted
+// sum. Chunk 0 clears the projection accumulators read by the scores kernel.
 __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
+  extern __shared__ int32_t sl_dyn[];
   __shared__ int64_t red[16];
   __shared__ int64_t hkey[kDecMaxGroup], hsum[kDecMaxGroup];
+  __shared__ uint64_t hrec[kDecMaxGroup];
   __shared__ int64_t el[kDecMaxGroup][kAttnWsumRows];
   __shared__ int32_t wl[kDecMaxGroup][kAttnWsumRows];
-  __shared__ int64_t part[3][2 * 256];
+  __shared__ int64_t part[3][1024];
   const Window win = attn_window(a);
+  const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
+  if (blockIdx.y == 0) {
+    for (uint32_t i = threadIdx.x; i < G * hd; i += 1024) a.qkv[uint64_t(kvh) * G * hd + i] = 0;
+    if (a.own_cache)
+      for (uint32_t i = threadIdx.x; i < hd; i += 1024) {
+        a.qkv[(uint64_t(a.nh) + kvh) * hd + i] = 0;
+        if (a.has_v) a.qkv[(uint64_t(a.nh) + a.nkv + kvh) * hd + i] = 0;
+      }
+  }
   const uint64_t r0 = uint64_t(blockIdx.y) * kAttnWsumRows;
   if (r0 >= win.cnt) return;
-  const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t nr = win.cnt - r0 < kAttnWsumRows ? win.cnt - r0 : kAttnWsumRows;
   const uint64_t kvw = uint64_t(a.nkv) * hd;
@@ -340,25 +363,29 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
   const uint32_t sl = threadIdx.x >> 8, dl = threadIdx.x & 255;
   int32_t vp[2][kAttnWsumRows / 4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
     for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
-      const uint32_t d = dl + 256 * j;
+      const uint32_t d = dl + 256 * jj;
       const uint64_t rr = sl * (kAttnWsumRows / 4) + k;
-      vp[j][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
+      vp[jj][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
     }
   // this wave's head and its rows r = wi * 64 + lane + stride * n
   const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;
   const bool active = g < G;
   const uint64_t stride = 64 * uint64_t(wph);
   const int32_t* scg = a.scores + (uint64_t(kvh) * G + (active ? g : 0)) * a.max_rows;
-  // argmax
+  int32_t* scl = a.scores_in_lds ? sl_dyn + uint64_t(active ? g : 0) * a.cap : nullptr;
+  // argmax (and the LDS copy of this thread's scores)
   int64_t best = INT64_MIN;
   if (active)
     for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
-      const int64_t k = score_key(scg[r], r);
+      const int32_t v = scg[r];
+      if (scl) scl[r] = v;
+      const int64_t k = score_key(v, r);
       best = k > best ? k : best;
     }
+  if (!scl) scl = const_cast<int32_t*>(scg);
   best = wmax(best);
   if (lane == 0) red[wave] = best;
   __syncthreads();
@@ -374,12 +401,16 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
   // exp sum (non-negative terms with a total below 2^63: the saturating sum is
   // the plain sum); this chunk's terms go to LDS
   int64_t s = 0;
+  // With the scores in LDS each exp term replaces its score there for the
+  // residual pass (2^32, the argmax row's term, is stored as 0xffffffff: every
+  // other term is at most 2^32 - 2^16).
+  const bool lds = a.scores_in_lds;
   if (active)
-#pragma unroll 2
     for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
-      const int64_t e = softmax_exp(scg[r], mx);
+      const int64_t e = softmax_exp(scl[r], mx);
       s += e;
       if (r >= r0 && r < r0 + nr) el[g][r - r0] = e;
+      if (lds) scl[r] = int32_t(e == kOneAcc ? 0xffffffffu : uint32_t(e));
     }
   s = wsum_wrap(s);
   if (lane == 0) red[wave] = s;
@@ -388,12 +419,14 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
     int64_t t = 0;
     for (uint32_t w = 0; w < wph; ++w) t += red[threadIdx.x * wph + w];
     hsum[threadIdx.x] = t;
+    hrec[threadIdx.x] = t < (int64_t(1) << 61) ? softmax_recip(t) : 0;  // 0: generic division
   }
   __syncthreads();
   // raw weights of this chunk
   if (threadIdx.x < G * kAttnWsumRows) {
     const uint32_t gg = threadIdx.x / kAttnWsumRows, rr = threadIdx.x % kAttnWsumRows;
-    wl[gg][rr] = rr < nr ? softmax_weight(el[gg][rr], hsum[gg]) : 0;
+    const uint64_t M = hrec[gg];
+    wl[gg][rr] = rr < nr ? (M ? softmax_weight_r(el[gg][rr], hsum[gg], M) : softmax_weight(el[gg][rr], hsum[gg])) : 0;
   }
   // residual for heads whose argmax row is in this chunk: their waves sum
   // every weight of the window
@@ -401,8 +434,17 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
   int64_t ws = 0;
   if (owner) {
     const int64_t S = hsum[g];
-#pragma unroll 2
-    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) ws += softmax_weight(softmax_exp(scg[r], mx), S);
+    const uint64_t M = hrec[g];
+    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
+      int64_t e;
+      if (lds) {
+        const uint32_t u = uint32_t(scl[r]);
+        e = u == 0xffffffffu ? kOneAcc : int64_t(u);
+      } else {
+        e = softmax_exp(scl[r], mx);
+      }
+      ws += M ? softmax_weight_r(e, S, M) : softmax_weight(e, S);
+    }
   }
   ws = wsum_wrap(ws);
   __syncthreads();  // red[] from the exp sums has been read
@@ -417,31 +459,44 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
     }
   }
   __syncthreads();
-  // weighted sums: 4 row slices per dim, combined in LDS, one atomic per dim
-  for (uint32_t gg = 0; gg < G; ++gg) {
-    int64_t p0 = 0, p1 = 0;
+  // weighted sums: 4 row slices per dim, combined in LDS for up to 1024 / dstr
+  // heads per pass, one atomic per (head, dim)
+  const uint32_t dstr = hd > 256 ? 512 : 256;
+  const uint32_t hpp = 1024 / dstr;
+  for (uint32_t h0 = 0; h0 < G; h0 += hpp) {
+    const uint32_t hn = G - h0 < hpp ? G - h0 : hpp;
+    if (sl > 0)
+      for (uint32_t hh = 0; hh < hn; ++hh) {
+        int64_t p0 = 0, p1 = 0;
 #pragma unroll
-    for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
-      const int32_t w = wl[gg][sl * (kAttnWsumRows / 4) + k];
-      p0 = mac(p0, vp[0][k], w);
-      p1 = mac(p1, vp[1][k], w);
-    }
-    if (sl > 0) {
-      part[sl - 1][dl] = p0;
-      part[sl - 1][256 + dl] = p1;
-    }
-    __syncthreads();
-    if (sl == 0) {
-#pragma unroll
-      for (int q = 0; q < 3; ++q) {
-        p0 = int64_t(uint64_t(p0) + uint64_t(part[q][dl]));
-        p1 = int64_t(uint64_t(p1) + uint64_t(part[q][256 + dl]));
+        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+          const int32_t w = wl[h0 + hh][sl * (kAttnWsumRows / 4) + k];
+          p0 = mac(p0, vp[0][k], w);
+          p1 = mac(p1, vp[1][k], w);
+        }
+        part[sl - 1][hh * dstr + dl] = p0;
+        if (dstr == 512) part[sl - 1][hh * dstr + 256 + dl] = p1;
       }
-      int64_t* out = a.acc + (uint64_t(kvh) * G + gg) * hd;
-      if (dl < hd) atomicAdd(reinterpret_cast<unsigned long long*>(out + dl), static_cast<unsigned long long>(p0));
-      if (dl + 256 < hd)
-        atomicAdd(reinterpret_cast<unsigned long long*>(out + dl + 256), static_cast<unsigned long long>(p1));
-    }
+    __syncthreads();
+    if (sl == 0)
+      for (uint32_t hh = 0; hh < hn; ++hh) {
+        int64_t p0 = 0, p1 = 0;
+#pragma unroll
+        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+          const int32_t w = wl[h0 + hh][k];
+          p0 = mac(p0, vp[0][k], w);
+          p1 = mac(p1, vp[1][k], w);
+        }
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+          p0 = int64_t(uint64_t(p0) + uint64_t(part[q][hh * dstr + dl]));
+          if (dstr == 512) p1 = int64_t(uint64_t(p1) + uint64_t(part[q][hh * dstr + 256 + dl]));
+        }
+        int64_t* out = a.acc + (uint64_t(kvh) * G + h0 + hh) * hd;
+        if (dl < hd) atomicAdd(reinterpret_cast<unsigned long long*>(out + dl), static_cast<unsigned long long>(p0));
+        if (dl + 256 < hd)
+          atomicAdd(reinterpret_cast<unsigned long long*>(out + dl + 256), static_cast<unsigned long long>(p1));
+      }
     __syncthreads();
   }
 }
@@ -500,20 +555,17 @@ void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const i
   DET_ROW_DISPATCH(k_dec_residual_norm, src, x, normed, w_post, int(has_scalar), scalar, w_next, H, eps, limbs, kpad);
 }
 #undef DET_ROW_DISPATCH
-void launch_dec_qkv_post(const QkvPostArgs& a, hipStream_t s) {
-  const unsigned blocks = a.nh + (a.own_cache ? (a.has_v ? 2 : 1) * a.nkv : 0);
-  hipLaunchKernelGGL(k_dec_qkv_post, dim3(blocks), dim3(64), a.hd * 4, s, a);
-}
 void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
   // grids cover the cache capacity (every window fits in it); idle chunks exit
   if (part == 0) {
     const dim3 grid(a.nkv, nblk(a.cap, kAttnScoreRows));
     if (a.hd % 64 == 0)
-      hipLaunchKernelGGL(k_dec_attn_scores<true>, grid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL(k_dec_attn_scores<true>, grid, dim3(512), 0, s, a);
     else
-      hipLaunchKernelGGL(k_dec_attn_scores<false>, grid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL(k_dec_attn_scores<false>, grid, dim3(512), 0, s, a);
   } else {
-    hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows)), dim3(1024), 0, s, a);
+    const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.cap * 4 : 0;
+    hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows)), dim3(1024), lds, s, a);
   }
 }
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s) {

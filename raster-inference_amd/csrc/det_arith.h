@@ -46,7 +46,7 @@ DET_HD int64_t rshift_rte(int64_t x, unsigned s) {
   const int64_t q = x >> s;  // arithmetic: floor
   const uint64_t r = uint64_t(x) & ((uint64_t(1) << s) - 1);
   const uint64_t half = uint64_t(1) << (s - 1);
-  return (r > half || (r == half && (q & 1))) ? q + 1 : q;
+  return q + int64_t((r > half) | ((r == half) & uint64_t(q & 1)));
 }
 
 // requantize: Q32.32 -> Q16.16, ties to even, saturating (ops.rs:445-448).
@@ -96,41 +96,56 @@ DET_HD int64_t acc_mul(int64_t lhs, int64_t rhs) {
 // inv_sqrt_acc (ops.rs:719-763): the c in [0, 2^31-1] nearest to
 // 2^32/sqrt(x) in the sense |c^2 x - 2^64| minimal, ties to even; x == 0 and
 // tiny x saturate to i32::MAX.
-// With Q = floor(2^64 / x) and R = 2^64 - Q x (0 <= R < x):
-//   c^2 x <= 2^64  <=>  c^2 <= Q, so the lower candidate is isqrt(Q);
-//   |lo^2 x - 2^64| - |hi^2 x - 2^64| = D x + 2R with D = 2Q - lo^2 - hi^2,
-// whose sign follows from D alone unless D == -1 (then from 2R vs x).
-// Everything stays in 64-bit integers; no 128-bit products.
-DET_HD uint64_t isqrt_u64(uint64_t q) {  // floor(sqrt(q)) for q < 2^62
-  uint64_t c = uint64_t(__builtin_sqrt(double(q)));
-  while (c * c > q) --c;
-  while ((c + 1) * (c + 1) <= q) ++c;
-  return c;
+// For x >= 5 the lower candidate lo = max{c : c^2 x <= 2^64} is below
+// 2^31 - 1. A double estimate of 2^32/sqrt(x) is within 2^-21 of the real
+// value, so lo is found by at most one step either way with the exact test
+// on the 128-bit product c^2 x. Then |lo^2 x - 2^64| vs |hi^2 x - 2^64|
+// (hi = lo + 1) is the sign of 2^65 - (lo^2 + hi^2) x, again one exact
+// 128-bit product.
+DET_HD bool sq_times_le_2_64(uint64_t c, uint64_t x) {  // c^2 x <= 2^64, c < 2^31
+  const u128 p = u128(c * c) * x;
+  return (p >> 64) == 0 || p == (u128(1) << 64);
 }
 DET_HD int32_t inv_sqrt_acc(int64_t x) {
   // (2^31-1)^2 * x <= 2^64 exactly for x <= 4
   if (x <= 4) return INT32_MAX;  // includes x == 0 (negative x is rejected upstream)
   const uint64_t ux = uint64_t(x);
-  uint64_t Q = UINT64_MAX / ux;
-  uint64_t R = UINT64_MAX - Q * ux + 1;  // 2^64 - Q x, in [1, x]
-  if (R == ux) {
-    ++Q;
-    R = 0;
-  }
-  const uint64_t lo = isqrt_u64(Q);  // < 2^31 - 1 since x >= 5
+  uint64_t lo = uint64_t(4294967296.0 / __builtin_sqrt(double(ux)));
+  if (lo > 2147483646ull) lo = 2147483646ull;
+  while (lo > 0 && !sq_times_le_2_64(lo, ux)) --lo;
+  while (sq_times_le_2_64(lo + 1, ux)) ++lo;
   const uint64_t hi = lo + 1;
-  const int64_t D = int64_t(2 * Q - lo * lo - hi * hi);
-  const bool lo_nearer = D >= 0 ? false : (D <= -2 ? true : 2 * R < ux);
-  const bool tie = (D == 0 && R == 0) || (D == -1 && 2 * R == ux);
-  if (tie) return int32_t((lo & 1) == 0 ? lo : hi);
-  // D >= 0 with R > 0 or D == 0: the upper candidate is strictly nearer
-  return int32_t(lo_nearer ? lo : hi);
+  const u128 p = u128(lo * lo + hi * hi) * ux;  // lo^2 + hi^2 < 2^63
+  const u128 two65 = u128(1) << 65;
+  if (p == two65) return int32_t((lo & 1) == 0 ? lo : hi);
+  return int32_t(p > two65 ? lo : hi);
+}
+
+// Round-half-even quotient of a non-negative v < 2^63 by 1 <= d < 2^32
+// (div_acc_by_u32, ops.rs:78-85, on the non-negative domain): a double
+// estimate within two of the floor quotient for quotients below 2^51, then
+// the exact remainder; larger quotients use the integer division.
+DET_HD uint64_t div_rte_nonneg_u32(uint64_t v, uint32_t d) {
+  const double qd = double(v) / double(d);
+  if (qd >= 2251799813685248.0) return udiv_rte(v, d);  // 2^51
+  uint64_t q = uint64_t(qd);
+  int64_t r = int64_t(v - q * d);
+  while (r < 0) {
+    --q;
+    r += d;
+  }
+  while (r >= int64_t(d)) {
+    ++q;
+    r -= d;
+  }
+  const uint64_t twice = uint64_t(r) << 1;
+  return (twice > d || (twice == d && (q & 1))) ? q + 1 : q;
 }
 
 // rms_norm_scale from a saturated sum of squares (ops.rs:406-425). The
 // saturating sum of non-negative terms is min(true sum, i64::MAX) in any order.
 DET_HD int32_t rms_scale_from_sumsq(int64_t sumsq, uint32_t n, int64_t eps) {
-  const int64_t mean = div_acc_u32(sumsq, n);
+  const int64_t mean = int64_t(div_rte_nonneg_u32(uint64_t(sumsq), n));
   return inv_sqrt_acc(add_sat64(mean, eps));
 }
 DET_HD int64_t sq_term(int32_t v) { return int64_t(v) * int64_t(v); }
@@ -138,14 +153,15 @@ DET_HD int64_t sq_term(int32_t v) { return int64_t(v) * int64_t(v); }
 // Round-half-even quotient of a non-negative v < 2^32 by a constant d.
 template <uint32_t d>
 DET_HD uint32_t div_rte_u32(uint32_t v) {
-  const uint32_t q = v / d, r = v - q * d;
-  return (2 * r > d || (2 * r == d && (q & 1))) ? q + 1 : q;
+  const uint32_t q = v / d, r2 = 2 * (v - q * d);
+  return q + uint32_t((r2 > d) | ((r2 == d) & (q & 1)));
 }
-// acc_mul of two non-negative values below 2^32: the product fits in 64 bits.
+// acc_mul of two non-negative values below 2^32: the product fits in 64 bits
+// and the rounded quotient stays below 2^32.
 DET_HD uint32_t acc_mul_u32(uint32_t a, uint32_t b) {
   const uint64_t p = uint64_t(a) * b;
-  const uint64_t q = p >> 32, r = p & 0xffffffffull;
-  return uint32_t((r > 0x80000000ull || (r == 0x80000000ull && (q & 1))) ? q + 1 : q);
+  const uint32_t q = uint32_t(p >> 32), r = uint32_t(p);
+  return q + uint32_t((r > 0x80000000u) | ((r == 0x80000000u) & (q & 1)));
 }
 
 // softmax exp term of a max-shifted logit (ops.rs:505-553, 261-263),
@@ -154,20 +170,17 @@ DET_HD uint32_t acc_mul_u32(uint32_t a, uint32_t b) {
 // the ln2 remainder r is below 2^32 and every power of r stays below 2^32, so
 // the series runs in 32x32->64-bit products with the reference's rounding.
 DET_HD int64_t softmax_exp(int32_t logit, int32_t max_logit) {
-  const int64_t d = int64_t(max_logit) - int64_t(logit);
-  if (d >= (int64_t(1) << 20)) return 0;
-  const uint64_t LN2 = 2977044472ull;
-  const uint64_t pos = uint64_t(d) << 16;
-  uint64_t shift = uint64_t(double(pos) * (1.0 / 2977044472.0));
-  int64_t r = int64_t(pos) - int64_t(shift * LN2);
-  while (r < 0) {
-    --shift;
-    r += int64_t(LN2);
-  }
-  while (r >= int64_t(LN2)) {
-    ++shift;
-    r -= int64_t(LN2);
-  }
+  const int64_t dd = int64_t(max_logit) - int64_t(logit);
+  if (dd >= (int64_t(1) << 20)) return 0;
+  const uint32_t d = uint32_t(dd);
+  const int64_t LN2 = 2977044472ll;
+  // shift = floor(d 2^16 / LN2) <= 23: a float estimate (relative error
+  // below 2^-22, so at most one off) fixed by the remainder's range
+  int32_t shift = int32_t(float(d) * (65536.0f / 2977044472.0f));
+  int64_t r = (int64_t(d) << 16) - int64_t(shift) * LN2;
+  const int32_t lo = r < 0, hi = r >= LN2;
+  shift += hi - lo;
+  r += int64_t(lo - hi) * LN2;
   const uint32_t r1 = uint32_t(r);
   const uint32_t r2 = acc_mul_u32(r1, r1);
   const uint32_t r3 = acc_mul_u32(r2, r1);
@@ -208,6 +221,32 @@ DET_HD int32_t softmax_weight(int64_t e, int64_t sum) {
   const u128 rem = num - u128(q) * d;
   const u128 twice = rem << 1;
   if (twice > u128(d) || (twice == u128(d) && (q & 1))) ++q;
+  return requant(int64_t(q));
+}
+
+// Reciprocal of a softmax exp sum S (2^32 <= S < 2^61) for softmax_weight_r:
+// M = 2^96 / S truncated (relative error below 2^-32), capped at 2^64 - 1.
+DET_HD uint64_t softmax_recip(int64_t sum) {
+  const double m = 79228162514264337593543950336.0 / double(sum);  // 2^96 / S
+  return m >= 18446744073709551615.0 ? UINT64_MAX : uint64_t(m);
+}
+// softmax_weight for 0 <= e <= min(S, 2^32), 2^32 <= S < 2^61 using M =
+// softmax_recip(S): floor(e M / 2^64) is at most two below the floor
+// quotient of e 2^32 / S; the exact remainder fixes it.
+DET_HD int32_t softmax_weight_r(int64_t e, int64_t sum, uint64_t M) {
+  const uint64_t ue = uint64_t(e), d = uint64_t(sum);
+  uint64_t q = uint64_t((u128(ue) * M) >> 64);
+  int64_t rem = int64_t((ue << 32) - q * d);
+  while (rem < 0) {
+    --q;
+    rem += int64_t(d);
+  }
+  while (rem >= int64_t(d)) {
+    ++q;
+    rem -= int64_t(d);
+  }
+  const uint64_t twice = uint64_t(rem) << 1;
+  if (twice > d || (twice == d && (q & 1))) ++q;
   return requant(int64_t(q));
 }
 

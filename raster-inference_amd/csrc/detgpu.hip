@@ -720,7 +720,7 @@ struct det_session {
   bool logits_valid = false;
   // fused decode step (HIP graph)
   det::StepState* st_dev = nullptr;
-  int32_t *qbuf = nullptr, *scores = nullptr, *hbuf = nullptr;
+  int32_t *scores = nullptr, *hbuf = nullptr;
   // projection accumulators (wrapping Q32.32); each consumer kernel clears
   // what it reads, so they are zero whenever a step starts
   int64_t *qkv_acc = nullptr, *o_acc = nullptr, *ff_acc = nullptr;
@@ -804,7 +804,6 @@ void session_alloc(det_session* s) {
     HIPC(hipMemsetAsync(s->qkv_acc, 0, fr * 8, zst));
     HIPC(hipMemsetAsync(s->o_acc, 0, H * 8, zst));
     HIPC(hipMemsetAsync(s->ff_acc, 0, H * 8, zst));
-    s->qbuf = s->alloc<int32_t>(nhd);
     s->scores = s->alloc<int32_t>(nh * T);
     s->attn_acc = s->alloc<int64_t>(nhd);
     s->hbuf = s->alloc<int32_t>(ff);
@@ -1129,6 +1128,37 @@ void decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
   out->next_token = ctx->argmax(s->logits, m->vocab);
 }
 
+// Attention arguments of layer l for the fused decode step.
+det::AttnDecArgs attn_args(det_session* s, size_t l) {
+  det_model* m = s->m;
+  const GLayer& L = m->layers[l];
+  const auto& F = m->fused[l];
+  GKv& ac = L.donor ? s->kv[*L.donor] : s->kv[l];
+  det::AttnDecArgs a{};
+  a.qkv = s->qkv_acc;
+  a.q_norm = L.q_norm;
+  a.k_norm = L.k_norm;
+  a.trig = s->trig + 2 * uint64_t(L.trig_off);
+  a.eps = L.eps;
+  a.rotary = L.rotary;
+  a.has_v = F.has_v;
+  a.own_cache = !L.donor;
+  a.k = ac.k;
+  a.v = ac.v;
+  a.st = s->st_dev;
+  a.cap = ac.cap;
+  a.window = L.sliding ? *L.sliding_window : 0;
+  a.max_rows = s->score_stride;
+  a.ring = ac.ring;
+  a.hd = uint32_t(L.head_dim);
+  a.nh = uint32_t(L.num_heads);
+  a.nkv = uint32_t(L.num_kv_heads);
+  a.scores = s->scores;
+  a.acc = s->attn_acc;
+  a.scores_in_lds = (L.num_heads / L.num_kv_heads) * ac.cap * 4 <= 32768;
+  return a;
+}
+
 // Enqueues one fused decode step (det_layer_decode for every layer, then
 // det_hidden_to_logits and argmax_first) reading position/token from st_dev.
 void enqueue_fused_step(det_session* s) {
@@ -1140,20 +1170,8 @@ void enqueue_fused_step(det_session* s) {
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
     const auto& F = m->fused[l];
-    GKv& own = s->kv[l];
     det::launch_gemv_dec(F.qkv, s->limbs_x, nullptr, s->qkv_acc, 0, nullptr, 0, st);
-    det::QkvPostArgs qa{};
-    qa.qkv = s->qkv_acc; qa.qbuf = s->qbuf; qa.kc = own.k; qa.vc = own.v;
-    qa.q_norm = L.q_norm; qa.k_norm = L.k_norm; qa.trig = s->trig + 2 * uint64_t(L.trig_off); qa.st = s->st_dev; qa.eps = L.eps;
-    qa.cap = own.cap; qa.rotary = L.rotary; qa.nh = uint32_t(L.num_heads); qa.nkv = uint32_t(L.num_kv_heads);
-    qa.hd = uint32_t(L.head_dim); qa.ring = own.ring; qa.has_v = F.has_v; qa.own_cache = !L.donor;
-    det::launch_dec_qkv_post(qa, st);
-    const GKv& ac = L.donor ? s->kv[*L.donor] : own;
-    det::AttnDecArgs aa{};
-    aa.q = s->qbuf; aa.k = ac.k; aa.v = ac.v; aa.st = s->st_dev; aa.cap = ac.cap;
-    aa.window = L.sliding ? *L.sliding_window : 0; aa.max_rows = s->score_stride; aa.ring = ac.ring;
-    aa.hd = uint32_t(L.head_dim); aa.nh = uint32_t(L.num_heads); aa.nkv = uint32_t(L.num_kv_heads);
-    aa.scores = s->scores; aa.acc = s->attn_acc;
+    const det::AttnDecArgs aa = attn_args(s, l);
     det::launch_dec_attention(aa, st);
     det::launch_gemv_decode_acc(*L.o, s->attn_acc, true, s->o_acc, st);
     det::launch_dec_residual_norm(s->o_acc, s->x, s->normed, L.post_attn_ln, false, 0, L.pre_ff_ln, H, L.eps,

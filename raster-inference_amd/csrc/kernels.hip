@@ -13,6 +13,7 @@
 
 #include "det_arith.h"
 #include "kernels.h"
+#include "wave.h"
 
 namespace det {
 
@@ -21,24 +22,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // ---------------------------------------------------------------------------
 // wave / block reductions
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int64_t wave_sum_wrap(int64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = int64_t(uint64_t(v) + uint64_t(__shfl_xor(v, o, 64)));
-  return v;
-}
-__device__ __forceinline__ int64_t wave_sum_sat(int64_t v) {  // non-negative terms
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = add_sat64(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ int64_t wave_max(int64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const int64_t w = __shfl_xor(v, o, 64);
-    v = w > v ? w : v;
-  }
-  return v;
-}
+__device__ __forceinline__ int64_t wave_sum_wrap(int64_t v) { return wave_sum_wrap64(v); }
+__device__ __forceinline__ int64_t wave_sum_sat(int64_t v) { return wave_sum_sat64(v); }  // non-negative terms
+__device__ __forceinline__ int64_t wave_max(int64_t v) { return wave_max64(v); }
 // Sortable key for "max value, first index": larger value wins, then smaller index.
 __device__ __forceinline__ int64_t argmax_key(int32_t value, uint32_t index) {
   return (int64_t(value) * 4294967296ll) | int64_t(0xffffffffu - index);

@@ -74,6 +74,8 @@ int main(int argc, char** argv) {
     int64_t o;
     orc_attention_softmax_exp_term(l, m, &o);
     if (det::softmax_exp(l, m) != o) { bad++; if (bad < 5) printf("  softmax_exp d=%lld dev=%lld orc=%lld\n", (long long)d, (long long)det::softmax_exp(l, m), (long long)o); }
+    // the decode kernel encodes the d == 0 term 2^32 as 0xffffffff in 32 bits: no other term may reach it
+    if (d > 0 && o > int64_t((1ull << 32) - (1ull << 16))) bad++;
   }
   report("softmax_exp_all_gaps", nexp, bad);
   // softmax_weight at exact half-way quotients and near the 2^61 sum boundary.
@@ -95,6 +97,40 @@ int main(int argc, char** argv) {
     if (det::softmax_weight(int64_t(e), int64_t(s2)) != orc_requantize(q)) bad++;
   }
   report("softmax_weight_edges", nw, bad);
+  // reciprocal-based softmax weight (per-head M) on the same kinds of inputs
+  bad = 0;
+  nw = 0;
+  for (long i = 0; i < N; ++i, ++nw) {
+    uint64_t sum = (1ull << 32) + (rng() % (1ull << (rng() % 29)));
+    if (i % 5 == 0) sum = (1ull << 32);
+    if (i % 7 == 0) sum = (1ull << 61) - 1 - rng() % 1000;
+    uint64_t e;
+    switch (i % 4) {
+      case 0: { const uint64_t q = rng() % (1ull << 32); e = uint64_t(((unsigned __int128)q * sum * 2 + sum) / ((unsigned __int128)1 << 33)); break; }
+      case 1: e = 1ull << 32; break;
+      case 2: e = rng() % ((1ull << 32) + 1); break;
+      default: e = 1 + rng() % 1024; break;
+    }
+    if (e > sum) e = sum;
+    int64_t q;
+    orc_div_acc(int64_t(e), int64_t(sum), &q);
+    const int32_t w = det::softmax_weight_r(int64_t(e), int64_t(sum), det::softmax_recip(int64_t(sum)));
+    if (w != orc_requantize(q)) { bad++; if (bad < 5) printf("  weight_r e=%llu s=%llu dev=%d orc=%d\n", (unsigned long long)e, (unsigned long long)sum, w, orc_requantize(q)); }
+  }
+  report("softmax_weight_recip", nw, bad);
+  // round-half-even division of non-negative values (row-norm means)
+  bad = 0;
+  for (long i = 0; i < N; ++i) {
+    int64_t v = pick64();
+    if (v < 0) v = v == INT64_MIN ? INT64_MAX : -v;
+    uint32_t d = uint32_t(rng()) >> (rng() % 32);
+    if (!d) d = 1;
+    if (i % 3 == 0) { const uint64_t q = rng() >> (rng() % 64); d = 1 + uint32_t(rng() % 5000); v = int64_t((q % (uint64_t(INT64_MAX) / d)) * d + d / 2); }
+    int64_t o;
+    orc_div_acc_by_u32(v, d, &o);
+    if (int64_t(det::div_rte_nonneg_u32(uint64_t(v), d)) != o) bad++;
+  }
+  report("div_rte_nonneg", N, bad);
   bad = 0;
   for (long i = 0; i < N / 20; ++i) {
     const uint32_t n = 1 + rng() % 300;
