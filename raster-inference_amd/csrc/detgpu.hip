@@ -54,6 +54,30 @@ struct det_ctx {
   size_t argmax_parts = 0;
   uint32_t* argmax_out = nullptr;
 
+  int8_t* gemm_a = nullptr;  // tiled activation limb rows for the prefill GEMM
+  size_t gemm_a_bytes = 0;
+
+  void ensure_gemm_a(size_t bytes) {
+    if (bytes <= gemm_a_bytes) return;
+    HIPC(hipStreamSynchronize(stream));
+    if (gemm_a) HIPC(hipFree(gemm_a));
+    gemm_a = nullptr;
+    HIPC(hipMalloc(&gemm_a, bytes));
+    gemm_a_bytes = bytes;
+  }
+  // Slab GEMM / GEMV dispatch: int8 weights with at least kGemmMinRows
+  // activation rows take the MFMA GEMM, everything else the GEMV kernels.
+  static constexpr uint64_t kGemmMinRows = 16;
+  void linear(const det::DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
+              int64_t* acc_out) {
+    if (W.storage == det::kInt8 && m >= kGemmMinRows) {
+      ensure_gemm_a(det::gemm_act_bytes(m, W.kpad));
+      det::launch_gemm(W, act, m, ld_act, out, ld_out, acc_out, gemm_a, stream);
+    } else {
+      det::launch_linear(W, act, m, ld_act, out, ld_out, acc_out, limbs, stream);
+    }
+  }
+
   void ensure_limbs(size_t bytes) {
     if (bytes <= limbs_bytes) return;
     HIPC(hipStreamSynchronize(stream));
@@ -868,7 +892,7 @@ std::vector<const GKv*> all_caches(det_session* s) {
 }
 
 void linear(det_ctx* ctx, const DevMatrix& W, const int32_t* act, uint64_t m, int32_t* out) {
-  det::launch_linear(W, act, m, W.cols, out, W.rows, nullptr, ctx->limbs, ctx->stream);
+  ctx->linear(W, act, m, W.cols, out, W.rows, nullptr);
 }
 
 void copy_d2d(det_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
@@ -934,7 +958,7 @@ void ple_inputs(det_session* s, uint64_t l, const uint32_t* ids_dev, const int32
   hipStream_t st = ctx->stream;
   const uint64_t P = m->ple_dim;
   det::launch_gather_rows(*m->ple_tok, ids_dev, M, l * P, P, m->ple_embedding_scale, out, P, st);
-  det::launch_linear(m->ple_proj_views[l], input, M, m->hidden, s->pp, P, nullptr, ctx->limbs, st);
+  ctx->linear(m->ple_proj_views[l], input, M, m->hidden, s->pp, P, nullptr);
   det::launch_scale(s->pp, M * P, m->ple_projection_scalar, st);
   det::launch_rmsnorm(s->pp, M, P, P, m->ple_proj_norm, m->eps, st);
   det::launch_add_sat(out, s->pp, M * P, st);
@@ -1353,6 +1377,7 @@ void det_ctx_destroy(det_ctx_t* ctx) {
   if (!ctx) return;
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->limbs) (void)hipFree(ctx->limbs);
+  if (ctx->gemm_a) (void)hipFree(ctx->gemm_a);
   if (ctx->argmax_scratch) (void)hipFree(ctx->argmax_scratch);
   if (ctx->argmax_out) (void)hipFree(ctx->argmax_out);
   (void)hipStreamDestroy(ctx->stream);
@@ -1443,7 +1468,7 @@ int det_linear_acc_i64(det_ctx_t* ctx, const det_matrix_t* w, const int32_t* act
   return guarded(ctx, [&] { det::launch_linear(w->m, act, 1, w->m.cols, nullptr, w->m.rows, acc, ctx->limbs, ctx->stream); });
 }
 int det_linear_slab(det_ctx_t* ctx, const det_matrix_t* w, uint64_t m, const int32_t* act, int32_t* out) {
-  return guarded(ctx, [&] { det::launch_linear(w->m, act, m, w->m.cols, out, w->m.rows, nullptr, ctx->limbs, ctx->stream); });
+  return guarded(ctx, [&] { ctx->linear(w->m, act, m, w->m.cols, out, w->m.rows, nullptr); });
 }
 int det_rms_norm(det_ctx_t* ctx, int32_t* x, uint64_t rows, uint64_t cols, const int32_t* w, int64_t eps) {
   return guarded(ctx, [&] {

@@ -46,6 +46,14 @@ void launch_act_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_ac
 void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,
                    uint64_t ld_out, int64_t* acc_out, int8_t* limbs, hipStream_t s);
 
+// Int8 GEMM for a slab of m activation rows (prefill): the activations are
+// first expanded into tiled limb rows in a_tiled (gemm_act_bytes(m, W.kpad)
+// bytes), then 128 x 128 MFMA blocks accumulate exactly. Output as for
+// launch_linear (requantized rows, or raw Q32.32 accumulators to acc_out).
+uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad);
+void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
+                 int64_t* acc_out, int8_t* a_tiled, hipStream_t s);
+
 // Batch-1 int8 GEMV for the fused decode step (int8 storage, fits LDS):
 // act_i64 requantizes wrapped accumulators on load; epilogue 1 applies
 // mul_sat(gelu(gate), up) to an interleaved gate/up matrix (out has rows/2).

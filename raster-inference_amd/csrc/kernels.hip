@@ -377,6 +377,129 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t* __restrict__ q, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill GEMM (det_linear_slab, det_kernels.rs:180-203): C[m][n] =
+// requantize(sum_k act[m][k] * W[n][k]) for a slab of M activation rows.
+//
+// The activations enter as limb rows: row 4m + j holds byte j of
+// act[m][k] ^ 0x00808080 (the four int8 limbs c_j with
+// act = sum_j c_j 256^j + 8421504), laid out exactly like the tile-major
+// weights (16-row tiles x 128-column steps of 2 KB; lane 16g + i of a step
+// holds row i, bytes [32g, 32g + 32)). A 16x16x64 MFMA of an A tile (4 tokens
+// x 4 limbs) with a weight tile leaves the four limb sums of (token g, weight
+// row i) in lane 16g + i, which are combined exactly as in the GEMV.
+//
+// Block: 128 limb rows (32 tokens) x 128 weight rows; 4 waves in 2 x 2, each
+// 64 x 64 (4 x 4 MFMA tiles, two MFMAs per 128-column step). Each step's 16
+// tile-steps (8 of A, 8 of weights) are double buffered in LDS, every 2 KB
+// block stored as two 1 KB halves (bytes 0-15 and 16-31 of each lane's 32),
+// so the 128-bit LDS reads of a wave are contiguous.
+// ---------------------------------------------------------------------------
+constexpr int kGemmTiles = 8;   // 16-row tiles per block side
+constexpr uint32_t kGemmLds = 2 * 2 * kGemmTiles * 2 * 64 * 16;  // stages x (A, B) x tiles x halves x lanes x 16 B
+
+// Activation limbs in the tiled layout for a_tiles 16-row tiles (4 tokens
+// each); tokens >= m and columns >= k are zero.
+__global__ void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, uint64_t k, uint64_t ld,
+                                  uint64_t kpad, uint64_t tokens_pad, int8_t* __restrict__ out) {
+  const uint64_t c = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t t = blockIdx.y;
+  if (c >= kpad || t >= tokens_pad) return;
+  const bool live = t < m && c < k;
+  const uint32_t u = live ? uint32_t(act[t * ld + c]) ^ 0x00808080u : 0u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    out[tiled_offset(kpad, 4 * t + j, c)] = live ? int8_t(uint8_t(u >> (8 * j))) : int8_t(0);
+}
+
+__global__ __launch_bounds__(256) void k_gemm_i8(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
+                                                 const int32_t* __restrict__ scale,
+                                                 const int32_t* __restrict__ rowsum, uint64_t n_rows,
+                                                 uint64_t kpad, uint64_t m_tokens, uint64_t a_tiles,
+                                                 uint32_t mblocks, int32_t* __restrict__ out, uint64_t ld_out,
+                                                 int64_t* __restrict__ acc_out) {
+  extern __shared__ v4i lds[];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // XCD-aware order: block b runs on XCD b % 8; each XCD takes a contiguous
+  // range of logical blocks (m fastest), so blocks sharing weight tiles share an L2
+  const uint32_t nblk = gridDim.x;
+  uint32_t logical = blockIdx.x;
+  if (nblk % 8 == 0) logical = (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8;
+  const uint32_t mb = logical % mblocks, nb = logical / mblocks;
+  const uint64_t nsteps = kpad / 128;
+  const uint64_t ntiles = (n_rows + 15) / 16;
+  const uint64_t at0 = uint64_t(mb) * kGemmTiles, bt0 = uint64_t(nb) * kGemmTiles;
+  // copy assignment: chunk c = tid + 256 u (u < 8) of the step's 16 x 128
+  // sixteen-byte chunks: tile-step ts = c / 128 (0-7 A, 8-15 weights), lane c % 128 / 2, half c % 2
+  const v4i zero = {0, 0, 0, 0};
+  v4i stage_regs[8];
+  auto fetch = [&](uint64_t s) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint32_t c = tid + 256 * u;
+      const uint32_t ts = c >> 7, within = c & 127;
+      const uint64_t tile = ts < kGemmTiles ? at0 + ts : bt0 + (ts - kGemmTiles);
+      const bool on = ts < kGemmTiles ? tile < a_tiles : tile < ntiles;
+      const int8_t* base = ts < kGemmTiles ? a : q;
+      stage_regs[u] = on ? *reinterpret_cast<const v4i*>(base + (tile * nsteps + s) * 2048 + within * 16) : zero;
+    }
+  };
+  auto store = [&](int st) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint32_t c = tid + 256 * u;
+      const uint32_t ts = c >> 7, within = c & 127;
+      lds[((st * 16 + ts) * 2 + (within & 1)) * 64 + (within >> 1)] = stage_regs[u];
+    }
+  };
+  const uint32_t wm = wave >> 1, wn = wave & 1;
+  v4i acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = zero;
+  fetch(0);
+  store(0);
+  __syncthreads();
+  for (uint64_t s = 0; s < nsteps; ++s) {
+    const int st = int(s & 1);
+    if (s + 1 < nsteps) fetch(s + 1);
+    v4i a0[4], a1[4], b0[4], b1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ta = wm * 4 + i, tb = kGemmTiles + wn * 4 + i;
+      a0[i] = lds[((st * 16 + ta) * 2 + 0) * 64 + lane];
+      a1[i] = lds[((st * 16 + ta) * 2 + 1) * 64 + lane];
+      b0[i] = lds[((st * 16 + tb) * 2 + 0) * 64 + lane];
+      b1[i] = lds[((st * 16 + tb) * 2 + 1) * 64 + lane];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[i], b0[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[i], b1[j], acc[i][j], 0, 0, 0);
+      }
+    if (s + 1 < nsteps) store(st ^ 1);
+    __syncthreads();
+  }
+  // epilogue: lane 16g + i holds the limb sums of token 4 tile + g, weight row 16 tile + i
+  const uint32_t g = lane >> 4, i = lane & 15;
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti) {
+    const uint64_t token = (at0 + wm * 4 + ti) * 4 + g;
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) {
+      const uint64_t row = (bt0 + wn * 4 + tj) * 16 + i;
+      if (token >= m_tokens || row >= n_rows) continue;
+      const int64_t p[4] = {acc[ti][tj][0], acc[ti][tj][1], acc[ti][tj][2], acc[ti][tj][3]};
+      const int64_t v = limb_combine(p, rowsum[row], scale[row]);
+      if (acc_out) acc_out[token * ld_out + row] = v;
+      else out[token * ld_out + row] = requant(v);
+    }
+  }
+}
+
 // Wide (i16 / i32 Wgt) GEMV on the vector ALUs: one wave per output row.
 template <class T>
 __global__ __launch_bounds__(256) void k_gemv_wide(const T* __restrict__ w, uint64_t n_rows, uint64_t k,
@@ -705,6 +828,19 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
     else if (ks == 2) launch_gemv_dec_ks<2, 0>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
     else launch_gemv_dec_ks<1, 0>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
   }
+}
+
+uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 31) / 32) * 32 * 4 * kpad; }
+
+void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
+                 int64_t* acc_out, int8_t* a_tiled, hipStream_t s) {
+  if (W.rows == 0 || m == 0) return;
+  const uint64_t mblocks = (m + 31) / 32, tokens_pad = mblocks * 32, a_tiles = tokens_pad / 4;
+  hipLaunchKernelGGL(k_act_limbs_tiled, dim3(blocks_for(W.kpad, 256), unsigned(tokens_pad)), dim3(256), 0, s, act, m,
+                     W.cols, ld_act, W.kpad, tokens_pad, a_tiled);
+  const uint64_t nblocks = ((W.rows + 15) / 16 + kGemmTiles - 1) / kGemmTiles;
+  hipLaunchKernelGGL(k_gemm_i8, dim3(unsigned(mblocks * nblocks)), dim3(256), kGemmLds, s, a_tiled, W.q, W.scale,
+                     W.rowsum, W.rows, W.kpad, m, a_tiles, uint32_t(mblocks), out, ld_out, acc_out);
 }
 
 void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,

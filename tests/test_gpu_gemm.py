@@ -1,0 +1,94 @@
+"""GPU parity of the int8 prefill GEMM (det_linear_slab with 16 or more rows).
+
+Small and ragged shapes are compared with the oracle's det_linear_slab
+(det_kernels.rs:180-203); shapes at E4B's projection sizes are compared row
+by row with the GPU GEMV, whose results are themselves pinned to the oracle
+in test_gpu_parity.py (every output element of the slab GEMM has the term set
+of the single-row GEMV).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib
+
+pytestmark = pytest.mark.gpu
+
+rd = pytest.importorskip("rasterdet")
+from rasterdet import synthetic  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = rd.Context(0)
+    yield c
+    c.close()
+
+
+def expand(q, s):
+    w = q.astype(np.int64) * s.astype(np.int64)[:, None]
+    return w.astype(np.int16) if np.abs(w).max(initial=0) < 32768 else w.astype(np.int32)
+
+
+def gpu_slab(ctx, mat, acts):
+    acts = np.ascontiguousarray(acts, dtype=np.int32)
+    m = acts.shape[0]
+    a = ctx.to_device(acts)
+    out = ctx.empty((m, mat.rows))
+    ctx.det_linear_slab(mat, m, a, out)
+    return out.numpy().reshape(m, mat.rows)
+
+
+def gpu_rows(ctx, mat, acts):
+    rows = []
+    for r in acts:
+        a = ctx.to_device(np.ascontiguousarray(r, dtype=np.int32))
+        out = ctx.empty(mat.rows)
+        ctx.det_linear_into(mat, a, out)
+        rows.append(out.numpy().copy())
+    return np.stack(rows)
+
+
+def act_slab(m, k, seed):
+    rng = np.random.default_rng(seed)
+    return synthetic.f32_to_act(rng.standard_normal((m, k)).astype(np.float32))
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 16, 64), (17, 33, 100), (31, 129, 128), (32, 128, 256), (33, 200, 2600),
+                                   (100, 1000, 777), (128, 520, 130), (257, 64, 2048)])
+def test_gemm_matches_oracle(ctx, m, n, k):
+    rng = np.random.default_rng(m * 1000 + n + k)
+    q, s = synthetic.random_int8_matrix(rng, n, k, scale_max=256)
+    acts = act_slab(m, k, seed=m + k)
+    mat = ctx.upload_matrix(q, s)
+    got = gpu_slab(ctx, mat, acts)
+    exp = oracle_lib.det_linear_slab(expand(q, s), acts, threads=oracle_lib.cpu_count())
+    assert np.array_equal(got, exp)
+
+
+def test_gemm_adversarial_values(ctx):
+    # activations at the i32 edges, weights at +-127, scales at the largest
+    # value that keeps every row mass below 2^31 (wrapping accumulators)
+    rng = np.random.default_rng(7)
+    m, n, k = 40, 64, 1024
+    q = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    q[0, :] = 127
+    q[1, :] = -127
+    q[2, ::2] = 127
+    mass = np.abs(q.astype(np.int64)).sum(axis=1)
+    s = ((2**31 - 1) // np.maximum(mass, 1)).astype(np.int32)
+    edges = np.array([-(2**31), 2**31 - 1, 0, 1, -1, 65536, -65536], dtype=np.int32)
+    acts = rng.choice(edges, size=(m, k))
+    acts[0, :] = 2**31 - 1
+    acts[1, :] = -(2**31)
+    mat = ctx.upload_matrix(q, s)
+    got = gpu_slab(ctx, mat, acts)
+    exp = oracle_lib.det_linear_slab(expand(q, s), acts, threads=oracle_lib.cpu_count())
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 3072, 2560), (64, 2560, 10240), (48, 2560, 2048)])
+def test_gemm_e4b_shapes_match_gemv_rows(ctx, m, n, k):
+    q, s = synthetic.fast_int8_matrix(n * 31 + k, n, k, 256)
+    acts = act_slab(m, k, seed=n + k)
+    mat = ctx.upload_matrix(q, s)
+    assert np.array_equal(gpu_slab(ctx, mat, acts), gpu_rows(ctx, mat, acts))
