@@ -131,6 +131,51 @@ def e4b_decode(ctx, rd, args) -> dict:
     }
 
 
+PREFILL_SHAPES = [(2048, 2560), (512, 2560), (512, 2560), (2560, 2048), (10240, 2560), (10240, 2560), (2560, 10240)]
+MFMA_INT8_PEAK_TOPS = 5000.0
+
+
+def prefill_gemm(ctx, rd, args) -> dict:
+    """Prefill GEMM at E4B's per-layer projection shapes (q, k, v, o, gate, up,
+    down: 91 750 400 weights) for M activation rows: algorithmic ops per
+    layer-set = 2 M 91 750 400, timed with HIP events over the seven GEMMs
+    (including each activation limb expansion)."""
+    from rasterdet import synthetic
+
+    mats = []
+    for i, (n, k) in enumerate(PREFILL_SHAPES):
+        q, s = synthetic.fast_int8_matrix(args.seed * 7 + i, n, k, 256)
+        mats.append(ctx.upload_matrix(q, s))
+    weights = sum(n * k for n, k in PREFILL_SHAPES)
+    out = {"shapes": "q 2048x2560, k/v 512x2560, o 2560x2048, gate/up 10240x2560, down 2560x10240",
+           "peak_tops": MFMA_INT8_PEAK_TOPS}
+    rng = np.random.default_rng(args.seed)
+    for m in (128, 512, 2048):
+        acts = {k: ctx.to_device(synthetic.f32_to_act(rng.standard_normal((m, k)).astype(np.float32)))
+                for k in {k for _, k in PREFILL_SHAPES}}
+        outs = [ctx.empty((m, n)) for n, _ in PREFILL_SHAPES]
+
+        def layer_set():
+            for mat, (n, k), o in zip(mats, PREFILL_SHAPES, outs):
+                ctx.det_linear_slab(mat, m, acts[k], o)
+
+        layer_set()
+        ctx.synchronize()
+        reps = 5
+        e0, e1 = ctx.event(), ctx.event()
+        e0.record()
+        for _ in range(reps):
+            layer_set()
+        e1.record()
+        ms = e0.elapsed_ms(e1) / reps
+        tops = 2 * m * weights / (ms / 1e3) / 1e12
+        out[f"M{m}"] = {"ms_per_layer_set": round(ms, 4), "alg_tops": round(tops, 1),
+                        "frac_of_int8_peak": round(tops / MFMA_INT8_PEAK_TOPS, 4),
+                        "hw_frac_with_4_limbs": round(4 * tops / MFMA_INT8_PEAK_TOPS, 4)}
+        log(f"[bench] prefill GEMM M={m}: {ms:.3f} ms per layer-set, {tops:.1f} algorithmic TOPS")
+    return out
+
+
 def measured_traffic():
     """HBM bytes per lm_head launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary."""
     p = ROOT / "profiles" / "gemv_lm_head_traffic.md"
@@ -171,6 +216,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-e4b", action="store_true", help="skip the E4B-shaped decode tok/s measurement")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     ap.add_argument("--e4b-layers", type=int, default=42)
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--prompt-len", type=int, default=512)
@@ -302,6 +348,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode_tok_s": None,
     }
+    if not args.no_gemm:
+        line["prefill_gemm"] = prefill_gemm(ctx, rd, args)
     if not args.no_e4b:
         line.update(e4b_decode(ctx, rd, args))
     print(json.dumps(line), flush=True)

@@ -389,14 +389,15 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t* __restrict__ q, 
 // x 4 limbs) with a weight tile leaves the four limb sums of (token g, weight
 // row i) in lane 16g + i, which are combined exactly as in the GEMV.
 //
-// Block: 128 limb rows (32 tokens) x 128 weight rows; 4 waves in 2 x 2, each
-// 64 x 64 (4 x 4 MFMA tiles, two MFMAs per 128-column step). Each step's 16
-// tile-steps (8 of A, 8 of weights) are double buffered in LDS, every 2 KB
-// block stored as two 1 KB halves (bytes 0-15 and 16-31 of each lane's 32),
-// so the 128-bit LDS reads of a wave are contiguous.
+// Block: TA A tiles (TA x 16 limb rows = 4 TA tokens) x TB weight tiles;
+// WM x WN waves, each (TA / WM) x (TB / WN) MFMA tiles, two MFMAs per
+// 128-column step. Each step's TA + TB tile-steps are double buffered in LDS,
+// every 2 KB block stored as two 1 KB halves (bytes 0-15 and 16-31 of each
+// lane's 32), so the 128-bit LDS reads of a wave are contiguous. Shapes:
+// 8 x 8 tiles on 4 waves (small slabs) and 16 x 16 on 8 waves (4x the MFMA
+// work per staged byte pair, for slabs that fill the device).
 // ---------------------------------------------------------------------------
-constexpr int kGemmTiles = 8;   // 16-row tiles per block side
-constexpr uint32_t kGemmLds = 2 * 2 * kGemmTiles * 2 * 64 * 16;  // stages x (A, B) x tiles x halves x lanes x 16 B
+constexpr uint32_t gemm_lds_bytes(int ta, int tb) { return 2u * uint32_t(ta + tb) * 2u * 64u * 16u; }
 
 // Activation limbs in the tiled layout for a_tiles 16-row tiles (4 tokens
 // each); tokens >= m and columns >= k are zero.
@@ -412,85 +413,100 @@ __global__ void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, u
     out[tiled_offset(kpad, 4 * t + j, c)] = live ? int8_t(uint8_t(u >> (8 * j))) : int8_t(0);
 }
 
-__global__ __launch_bounds__(256) void k_gemm_i8(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
-                                                 const int32_t* __restrict__ scale,
-                                                 const int32_t* __restrict__ rowsum, uint64_t n_rows,
-                                                 uint64_t kpad, uint64_t m_tokens, uint64_t a_tiles,
-                                                 uint32_t mblocks, int32_t* __restrict__ out, uint64_t ld_out,
-                                                 int64_t* __restrict__ acc_out) {
+template <int TA, int TB, int WM, int WN, uint32_t GM>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
+                                                          const int32_t* __restrict__ scale,
+                                                          const int32_t* __restrict__ rowsum, uint64_t n_rows,
+                                                          uint64_t kpad, uint64_t m_tokens, uint64_t a_tiles,
+                                                          uint32_t mblocks, int32_t* __restrict__ out,
+                                                          uint64_t ld_out, int64_t* __restrict__ acc_out) {
+  constexpr int NT = 64 * WM * WN;             // threads
+  constexpr int TS = TA + TB;                  // tile-steps staged per K step
+  constexpr int CPT = TS * 128 / NT;           // 16-byte chunks per thread per K step
+  constexpr int FA = TA / WM, FB = TB / WN;    // MFMA tiles per wave
+  static_assert(TS * 128 % NT == 0, "chunks must divide evenly");
   extern __shared__ v4i lds[];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // XCD-aware order: block b runs on XCD b % 8; each XCD takes a contiguous
-  // range of logical blocks (m fastest), so blocks sharing weight tiles share an L2
+  // Block order: block b runs on XCD b % 8, and each XCD takes a contiguous
+  // range of logical blocks; logical blocks go in groups of GM m-blocks x all
+  // n-blocks with m fastest, so the blocks resident on one XCD at a time form
+  // a compact GM x (resident / GM) patch whose A and weight tiles share its L2.
   const uint32_t nblk = gridDim.x;
   uint32_t logical = blockIdx.x;
   if (nblk % 8 == 0) logical = (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8;
-  const uint32_t mb = logical % mblocks, nb = logical / mblocks;
+  const uint32_t nblocks_n = nblk / mblocks;
+  const uint32_t group = logical / (GM * nblocks_n), first_m = group * GM;
+  const uint32_t gm = mblocks - first_m < GM ? mblocks - first_m : GM;
+  const uint32_t in_group = logical - group * GM * nblocks_n;
+  const uint32_t mb = first_m + in_group % gm, nb = in_group / gm;
   const uint64_t nsteps = kpad / 128;
   const uint64_t ntiles = (n_rows + 15) / 16;
-  const uint64_t at0 = uint64_t(mb) * kGemmTiles, bt0 = uint64_t(nb) * kGemmTiles;
-  // copy assignment: chunk c = tid + 256 u (u < 8) of the step's 16 x 128
-  // sixteen-byte chunks: tile-step ts = c / 128 (0-7 A, 8-15 weights), lane c % 128 / 2, half c % 2
+  const uint64_t at0 = uint64_t(mb) * TA, bt0 = uint64_t(nb) * TB;
+  // chunk c = tid + NT u of a step's TS x 128 sixteen-byte chunks: tile-step
+  // c / 128 (A tiles first), lane c % 128 / 2, half c % 2
   const v4i zero = {0, 0, 0, 0};
-  v4i stage_regs[8];
+  v4i stage_regs[CPT];
   auto fetch = [&](uint64_t s) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const uint32_t c = tid + 256 * u;
+    for (int u = 0; u < CPT; ++u) {
+      const uint32_t c = tid + NT * u;
       const uint32_t ts = c >> 7, within = c & 127;
-      const uint64_t tile = ts < kGemmTiles ? at0 + ts : bt0 + (ts - kGemmTiles);
-      const bool on = ts < kGemmTiles ? tile < a_tiles : tile < ntiles;
-      const int8_t* base = ts < kGemmTiles ? a : q;
+      const bool is_a = ts < uint32_t(TA);
+      const uint64_t tile = is_a ? at0 + ts : bt0 + (ts - TA);
+      const bool on = is_a ? tile < a_tiles : tile < ntiles;
+      const int8_t* base = is_a ? a : q;
       stage_regs[u] = on ? *reinterpret_cast<const v4i*>(base + (tile * nsteps + s) * 2048 + within * 16) : zero;
     }
   };
   auto store = [&](int st) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const uint32_t c = tid + 256 * u;
+    for (int u = 0; u < CPT; ++u) {
+      const uint32_t c = tid + NT * u;
       const uint32_t ts = c >> 7, within = c & 127;
-      lds[((st * 16 + ts) * 2 + (within & 1)) * 64 + (within >> 1)] = stage_regs[u];
+      lds[((st * TS + ts) * 2 + (within & 1)) * 64 + (within >> 1)] = stage_regs[u];
     }
   };
-  const uint32_t wm = wave >> 1, wn = wave & 1;
-  v4i acc[4][4];
+  const uint32_t wm = wave / WN, wn = wave % WN;
+  v4i acc[FA][FB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FA; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = zero;
+    for (int j = 0; j < FB; ++j) acc[i][j] = zero;
   fetch(0);
   store(0);
   __syncthreads();
   for (uint64_t s = 0; s < nsteps; ++s) {
     const int st = int(s & 1);
     if (s + 1 < nsteps) fetch(s + 1);
-    v4i a0[4], a1[4], b0[4], b1[4];
+    v4i b0[FB], b1[FB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ta = wm * 4 + i, tb = kGemmTiles + wn * 4 + i;
-      a0[i] = lds[((st * 16 + ta) * 2 + 0) * 64 + lane];
-      a1[i] = lds[((st * 16 + ta) * 2 + 1) * 64 + lane];
-      b0[i] = lds[((st * 16 + tb) * 2 + 0) * 64 + lane];
-      b1[i] = lds[((st * 16 + tb) * 2 + 1) * 64 + lane];
+    for (int j = 0; j < FB; ++j) {
+      const int tb = TA + int(wn) * FB + j;
+      b0[j] = lds[((st * TS + tb) * 2 + 0) * 64 + lane];
+      b1[j] = lds[((st * TS + tb) * 2 + 1) * 64 + lane];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FA; ++i) {
+      const int ta = int(wm) * FA + i;
+      const v4i a0 = lds[((st * TS + ta) * 2 + 0) * 64 + lane];
+      const v4i a1 = lds[((st * TS + ta) * 2 + 1) * 64 + lane];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[i], b0[j], acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[i], b1[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < FB; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], acc[i][j], 0, 0, 0);
       }
+    }
     if (s + 1 < nsteps) store(st ^ 1);
     __syncthreads();
   }
   // epilogue: lane 16g + i holds the limb sums of token 4 tile + g, weight row 16 tile + i
   const uint32_t g = lane >> 4, i = lane & 15;
 #pragma unroll
-  for (int ti = 0; ti < 4; ++ti) {
-    const uint64_t token = (at0 + wm * 4 + ti) * 4 + g;
+  for (int ti = 0; ti < FA; ++ti) {
+    const uint64_t token = (at0 + wm * FA + ti) * 4 + g;
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
-      const uint64_t row = (bt0 + wn * 4 + tj) * 16 + i;
+    for (int tj = 0; tj < FB; ++tj) {
+      const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
       if (token >= m_tokens || row >= n_rows) continue;
       const int64_t p[4] = {acc[ti][tj][0], acc[ti][tj][1], acc[ti][tj][2], acc[ti][tj][3]};
       const int64_t v = limb_combine(p, rowsum[row], scale[row]);
@@ -830,17 +846,35 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
   }
 }
 
-uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 31) / 32) * 32 * 4 * kpad; }
+uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64 * 4 * kpad; }
+
+template <int TA, int TB, int WM, int WN, uint32_t GM>
+static void launch_gemm_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
+                              const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s) {
+  // the larger shape needs more than 64 KB of dynamic LDS per workgroup
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_i8<TA, TB, WM, WN, GM>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     int(gemm_lds_bytes(TA, TB)));
+  (void)attr;
+  const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
+  const uint64_t nblocks = ((W.rows + 15) / 16 + TB - 1) / TB;
+  hipLaunchKernelGGL((k_gemm_i8<TA, TB, WM, WN, GM>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN),
+                     gemm_lds_bytes(TA, TB), s, a_tiled, W.q, W.scale, W.rowsum, W.rows, W.kpad, m, a_tiles,
+                     uint32_t(mblocks), out, ld_out, acc_out);
+}
 
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
                  int64_t* acc_out, int8_t* a_tiled, hipStream_t s) {
   if (W.rows == 0 || m == 0) return;
-  const uint64_t mblocks = (m + 31) / 32, tokens_pad = mblocks * 32, a_tiles = tokens_pad / 4;
+  // tokens padded to a multiple of 64 (the larger block's 16 A tiles)
+  const uint64_t tokens_pad = (m + 63) / 64 * 64, a_tiles = tokens_pad / 4;
   hipLaunchKernelGGL(k_act_limbs_tiled, dim3(blocks_for(W.kpad, 256), unsigned(tokens_pad)), dim3(256), 0, s, act, m,
                      W.cols, ld_act, W.kpad, tokens_pad, a_tiled);
-  const uint64_t nblocks = ((W.rows + 15) / 16 + kGemmTiles - 1) / kGemmTiles;
-  hipLaunchKernelGGL(k_gemm_i8, dim3(unsigned(mblocks * nblocks)), dim3(256), kGemmLds, s, a_tiled, W.q, W.scale,
-                     W.rowsum, W.rows, W.kpad, m, a_tiles, uint32_t(mblocks), out, ld_out, acc_out);
+  const uint64_t big_blocks = ((m + 63) / 64) * (((W.rows + 15) / 16 + 15) / 16);
+  if (big_blocks >= 256)
+    launch_gemm_shape<16, 16, 2, 4, 4>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
+  else
+    launch_gemm_shape<8, 8, 2, 2, 8>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
 }
 
 void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,

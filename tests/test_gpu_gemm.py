@@ -39,6 +39,7 @@ def gpu_slab(ctx, mat, acts):
 
 
 def gpu_rows(ctx, mat, acts):
+    """Each row through the single-row GEMV (oracle-pinned in test_gpu_parity.py)."""
     rows = []
     for r in acts:
         a = ctx.to_device(np.ascontiguousarray(r, dtype=np.int32))
@@ -86,7 +87,8 @@ def test_gemm_adversarial_values(ctx):
     assert np.array_equal(got, exp)
 
 
-@pytest.mark.parametrize("m,n,k", [(128, 3072, 2560), (64, 2560, 10240), (48, 2560, 2048)])
+@pytest.mark.parametrize("m,n,k", [(128, 3072, 2560), (64, 2560, 10240), (48, 2560, 2048),
+                                   (256, 16384, 512), (300, 13100, 2600)])
 def test_gemm_e4b_shapes_match_gemv_rows(ctx, m, n, k):
     q, s = synthetic.fast_int8_matrix(n * 31 + k, n, k, 256)
     acts = act_slab(m, k, seed=n + k)
