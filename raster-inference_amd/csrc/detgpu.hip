@@ -18,6 +18,7 @@
 #include <stdexcept>
 #include <string>
 #include <thread>
+#include <initializer_list>
 #include <vector>
 
 #include "../../include/detgpu.h"
@@ -76,6 +77,23 @@ struct det_ctx {
     } else {
       det::launch_linear(W, act, m, ld_act, out, ld_out, acc_out, limbs, stream);
     }
+  }
+
+  // Several matrices applied to the same activation rows: with the GEMM, one
+  // limb expansion feeds all of them when their input widths agree.
+  void linear_group(std::initializer_list<std::pair<const det::DevMatrix*, int32_t*>> items, const int32_t* act,
+                    uint64_t m, uint64_t ld_act) {
+    const det::DevMatrix* first = items.begin()->first;
+    bool shared = m >= kGemmMinRows;
+    for (const auto& it : items)
+      shared &= it.first->storage == det::kInt8 && it.first->kpad == first->kpad && it.first->cols == first->cols;
+    if (!shared) {
+      for (const auto& it : items) linear(*it.first, act, m, ld_act, it.second, it.first->rows, nullptr);
+      return;
+    }
+    ensure_gemm_a(det::gemm_act_bytes(m, first->kpad));
+    det::launch_gemm_limbs(act, m, first->cols, ld_act, first->kpad, gemm_a, stream);
+    for (const auto& it : items) det::launch_gemm_tiled(*it.first, m, it.second, it.first->rows, nullptr, gemm_a, stream);
   }
 
   void ensure_limbs(size_t bytes) {
@@ -904,11 +922,14 @@ void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0) {
   det_ctx* ctx = s->m->ctx;
   hipStream_t st = ctx->stream;
   const uint64_t qw = L.num_heads * L.head_dim, kw = L.num_kv_heads * L.head_dim;
-  linear(ctx, *L.q, s->normed, M, s->qb);
-  linear(ctx, *L.k, s->normed, M, s->kb);
-  if (L.v) linear(ctx, *L.v, s->normed, M, s->vb);
-  else if (L.k_eq_v) copy_d2d(ctx, s->vb, s->kb, M * kw * 4);
-  else bail("Gemma layer is missing v_proj without attention_k_eq_v enabled");
+  if (L.v) {
+    ctx->linear_group({{L.q, s->qb}, {L.k, s->kb}, {L.v, s->vb}}, s->normed, M, L.q->cols);
+  } else if (L.k_eq_v) {
+    ctx->linear_group({{L.q, s->qb}, {L.k, s->kb}}, s->normed, M, L.q->cols);
+    copy_d2d(ctx, s->vb, s->kb, M * kw * 4);
+  } else {
+    bail("Gemma layer is missing v_proj without attention_k_eq_v enabled");
+  }
   det::launch_rmsnorm(s->qb, M * L.num_heads, L.head_dim, L.head_dim, L.q_norm, L.eps, st);
   det::launch_rmsnorm(s->kb, M * L.num_kv_heads, L.head_dim, L.head_dim, L.k_norm, L.eps, st);
   det::launch_rmsnorm(s->vb, M * L.num_kv_heads, L.head_dim, L.head_dim, nullptr, L.eps, st);
@@ -926,26 +947,18 @@ void post_attention(det_session* s, const GLayer& L, uint64_t M, const int32_t* 
   hipStream_t st = ctx->stream;
   const uint64_t H = L.hidden;
   linear(ctx, *L.o, s->attn, M, s->x2);
-  det::launch_rmsnorm(s->x2, M, H, H, L.post_attn_ln, L.eps, st);
-  det::launch_add_sat(s->x2, s->x, M * H, st);
-  std::swap(s->x, s->x2);
-  copy_d2d(ctx, s->normed, s->x, M * H * 4);
-  det::launch_rmsnorm(s->normed, M, H, H, L.pre_ff_ln, L.eps, st);
-  linear(ctx, *L.gate, s->normed, M, s->gate);
-  linear(ctx, *L.up, s->normed, M, s->up);
+  det::launch_rmsnorm_add(s->x, s->x2, s->x, M, H, H, L.post_attn_ln, L.eps, st);  // x = add_sat(norm(o), x)
+  det::launch_rmsnorm_to(s->normed, s->x, M, H, H, L.pre_ff_ln, L.eps, st);
+  ctx->linear_group({{L.gate, s->gate}, {L.up, s->up}}, s->normed, M, H);
   det::launch_gelu_mul(s->gate, s->up, M * L.gate->rows, st);
   linear(ctx, *L.down, s->gate, M, s->x2);
-  det::launch_rmsnorm(s->x2, M, H, H, L.post_ff_ln, L.eps, st);
-  det::launch_add_sat(s->x2, s->x, M * H, st);
-  std::swap(s->x, s->x2);
+  det::launch_rmsnorm_add(s->x, s->x2, s->x, M, H, H, L.post_ff_ln, L.eps, st);
   if (L.has_ple && ple_in) {
     const uint64_t P = L.ple_gate->rows;
     linear(ctx, *L.ple_gate, s->x, M, s->gate);
     det::launch_gelu_mul(s->gate, ple_in, M * P, st);
     linear(ctx, *L.ple_proj, s->gate, M, s->x2);
-    det::launch_rmsnorm(s->x2, M, H, H, L.ple_post_norm, L.eps, st);
-    det::launch_add_sat(s->x2, s->x, M * H, st);
-    std::swap(s->x, s->x2);
+    det::launch_rmsnorm_add(s->x, s->x2, s->x, M, H, H, L.ple_post_norm, L.eps, st);
   }
   if (L.layer_scalar) det::launch_scale(s->x, M * H, *L.layer_scalar, st);
 }
@@ -979,8 +992,7 @@ void logits_from(det_session* s, const int32_t* hidden_row) {
   det_model* m = s->m;
   det_ctx* ctx = m->ctx;
   hipStream_t st = ctx->stream;
-  copy_d2d(ctx, s->normed, hidden_row, m->hidden * 4);
-  det::launch_rmsnorm(s->normed, 1, m->hidden, m->hidden, m->final_norm, m->eps, st);
+  det::launch_rmsnorm_to(s->normed, hidden_row, 1, m->hidden, m->hidden, m->final_norm, m->eps, st);
   linear(ctx, *m->lm_head, s->normed, 1, s->logits);
   if (m->softcap) det::launch_softcap(s->logits, m->vocab, *m->softcap, st);
   s->logits_valid = true;
@@ -1011,8 +1023,7 @@ void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
   for (uint64_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
     // det_layer_prefill (det_kernels.rs:678-821)
-    copy_d2d(ctx, s->normed, s->x, n * H * 4);
-    det::launch_rmsnorm(s->normed, n, H, H, L.in_ln, L.eps, st);
+    det::launch_rmsnorm_to(s->normed, s->x, n, H, H, L.in_ln, L.eps, st);
     qkv_block(s, L, n, 0);
     const uint64_t kw = L.num_kv_heads * L.head_dim;
     GKv& c = s->kv[l];
@@ -1098,8 +1109,7 @@ void decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
     const GLayer& L = m->layers[l];
     if (m->has_ple && L.has_ple) ple_inputs(s, l, s->ids, s->dec_in, 1, s->pe);
     // det_layer_decode (det_kernels.rs:866-1133)
-    copy_d2d(ctx, s->normed, s->x, H * 4);
-    det::launch_rmsnorm(s->normed, 1, H, H, L.in_ln, L.eps, st);
+    det::launch_rmsnorm_to(s->normed, s->x, 1, H, H, L.in_ln, L.eps, st);
     qkv_block(s, L, 1, pos);
     const uint64_t kw = L.num_kv_heads * L.head_dim;
     GKv& own = s->kv[l];

@@ -51,6 +51,12 @@ void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t 
 // bytes), then 128 x 128 MFMA blocks accumulate exactly. Output as for
 // launch_linear (requantized rows, or raw Q32.32 accumulators to acc_out).
 uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad);
+// The two halves of launch_gemm, so one limb expansion can feed several
+// matrices with the same input width.
+void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_act, uint64_t kpad, int8_t* a_tiled,
+                       hipStream_t s);
+void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
+                       const int8_t* a_tiled, hipStream_t s);
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
                  int64_t* acc_out, int8_t* a_tiled, hipStream_t s);
 
@@ -73,6 +79,12 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
 
 void launch_rmsnorm(int32_t* x, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
                     int64_t eps, hipStream_t s);
+// dst = add_sat(rmsnorm(src), res) row by row (dst may equal src or res).
+void launch_rmsnorm_add(int32_t* dst, const int32_t* src, const int32_t* res, uint64_t rows, uint64_t cols,
+                        uint64_t ld, const int32_t* w, int64_t eps, hipStream_t s);
+// dst = rmsnorm(src) row by row (dst may equal src).
+void launch_rmsnorm_to(int32_t* dst, const int32_t* src, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
+                       int64_t eps, hipStream_t s);
 void launch_rope(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t head_dim,
                  uint64_t half, const int64_t* inv_freq, uint64_t pos0, uint64_t pos_step,
                  hipStream_t s);

@@ -539,21 +539,66 @@ __global__ __launch_bounds__(256) void k_gemv_wide(const T* __restrict__ w, uint
 }
 
 // ---------------------------------------------------------------------------
-// RMSNorm (ops.rs:95-131, 406-425): one wave per row.
+// RMSNorm (ops.rs:95-131, 406-425): one wave per row; dst = rmsnorm(src)
+// (times the gain w when given), plus res (add_sat) when given.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_rmsnorm(int32_t* __restrict__ x, uint64_t rows, uint64_t cols,
-                                                 uint64_t ld, const int32_t* __restrict__ w, int64_t eps) {
+__global__ __launch_bounds__(256) void k_rmsnorm(const int32_t* src, int32_t* dst, const int32_t* res, uint64_t rows,
+                                                 uint64_t cols, uint64_t ld, const int32_t* __restrict__ w,
+                                                 int64_t eps) {
   const int lane = threadIdx.x & 63;
   const uint64_t row = uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  int32_t* xr = x + row * ld;
+  const int32_t* xr = src + row * ld;
   int64_t ss = 0;
   for (uint64_t c = lane; c < cols; c += 64) ss = add_sat64(ss, sq_term(xr[c]));
   ss = wave_sum_sat(ss);
   const int32_t scale = rms_scale_from_sumsq(ss, uint32_t(cols), eps);
+  // each element is read (src, res) and written (dst) by the same lane, so
+  // dst may alias src or res
   for (uint64_t c = lane; c < cols; c += 64) {
     const int32_t y = mul_sat(xr[c], scale);
-    xr[c] = w ? mul_sat(y, w[c]) : y;
+    const int32_t z = w ? mul_sat(y, w[c]) : y;
+    dst[row * ld + c] = res ? add_sat(z, res[row * ld + c]) : z;
+  }
+}
+
+// Wide rows: one workgroup of NT threads per row, element c = tid + NT * e
+// held in registers (e < EPT); every wave reduces its saturating partial sum
+// of squares, and after one barrier each wave combines the NT / 64 partials
+// and computes the scale itself. src and dst may be the same rows; with res,
+// dst = add_sat(rmsnorm(src), res) (the residual add after a sub-block).
+template <int NT, int EPT>
+__global__ __launch_bounds__(NT) void k_rmsnorm_wide(const int32_t* src, int32_t* dst, uint64_t cols, uint64_t ld,
+                                                     const int32_t* __restrict__ w, int64_t eps,
+                                                     const int32_t* res) {
+  __shared__ int64_t red[NT / 64];
+  const uint64_t row = blockIdx.x;
+  const int32_t* xr = src + row * ld;
+  int32_t v[EPT], g[EPT];
+  int64_t ss = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    v[e] = c < cols ? xr[c] : 0;
+    g[e] = (w && c < cols) ? w[c] : 0;
+    ss = add_sat64(ss, sq_term(v[e]));
+  }
+  ss = wave_sum_sat(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  int64_t tot = 0;
+#pragma unroll
+  for (int k = 0; k < NT / 64; ++k) tot = add_sat64(tot, red[k]);
+  const int32_t scale = rms_scale_from_sumsq(tot, uint32_t(cols), eps);
+  int32_t* yr = dst + row * ld;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    if (c < cols) {
+      const int32_t y = mul_sat(v[e], scale);
+      const int32_t z = w ? mul_sat(y, g[e]) : y;
+      yr[c] = res ? add_sat(z, res[row * ld + c]) : z;
+    }
   }
 }
 
@@ -657,6 +702,180 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
     orow[d] = requant(acc);
   }
   (void)bcast;
+}
+
+// ---------------------------------------------------------------------------
+// Causal / windowed attention for a slab of queries (det_attention_prefill,
+// det_kernels.rs:525-671, and the decode loop :1001-1053): per query head,
+// scores = requantize(wrap-dot(q, k_r)), integer softmax with the residual on
+// the first argmax row (ops.rs:230-273), out = requantize(sum_r w_r v_r).
+// One workgroup (512 threads) per (group of HB query heads sharing a KV
+// head, query): the key and value rows are read once for the HB heads.
+// Scores: sixteen lanes per key row, U rows per lane group in flight;
+// softmax: 8 / HB waves per head; weighted sum: one thread per dimension.
+// ---------------------------------------------------------------------------
+constexpr int kAttnPThreads = 512;
+
+// Score-row stride of a launch: no window of its queries is longer.
+__host__ __device__ inline uint64_t attn_row_stride(const AttnArgs& a) {
+  if (!a.causal) return a.fix_count;
+  return (a.window && a.window < a.avail) ? a.window : a.avail;
+}
+
+template <int KPER, int HB>
+__global__ __launch_bounds__(kAttnPThreads) void k_attention_prefill(AttnArgs a) {
+  extern __shared__ int32_t sc[];  // [HB][max_count] scores, then weights
+  __shared__ int32_t ql[HB * 16 * KPER];
+  __shared__ int64_t red[8];
+  __shared__ int64_t hkey[HB], hsum[HB];
+  __shared__ uint64_t hrec[HB];
+  constexpr int U = 64 / KPER;  // key rows per lane group per pass
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t hg = blockIdx.x, t = blockIdx.y;
+  const uint32_t h0 = hg * HB, kvh = h0 / a.groups;
+  const uint32_t hd = a.hd;
+  uint64_t start, count;
+  if (a.causal) {
+    uint64_t end = t + 1 + a.causal_offset;
+    start = (a.window && end > a.window) ? end - a.window : 0;
+    if (start > a.avail) start = a.avail;
+    if (end > a.avail) end = a.avail;
+    count = end > start ? end - start : 0;
+  } else {
+    start = a.fix_start;
+    count = a.fix_count;
+  }
+  if (count == 0) return;  // host validation makes every window non-empty
+  const uint64_t cstride = attn_row_stride(a);
+  // window row r sits at physical row base + r, wrapped once around a ring
+  const uint64_t base = a.ring_cap ? (a.ring_start + start) % a.ring_cap : start;
+  const uint64_t wrap = a.ring_cap ? a.ring_cap : ~0ull;
+  auto phys = [&](uint64_t r) {
+    const uint64_t p = base + r;
+    return p >= wrap ? p - wrap : p;
+  };
+  for (uint32_t i = threadIdx.x; i < HB * hd; i += kAttnPThreads)
+    ql[i] = a.q[uint64_t(t) * a.q_ld + uint64_t(h0 + i / hd) * hd + i % hd];
+  __syncthreads();
+  // 1. scores
+  const uint32_t grp = threadIdx.x >> 4, li = threadIdx.x & 15;
+  for (uint64_t r0 = 0; r0 < count; r0 += 32 * U) {
+    int32_t kr[U][KPER];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t r = r0 + grp + 32 * u;
+      const bool on = r < count;
+      const int32_t* krow = a.k + (on ? phys(r) : 0) * a.kv_ld + uint64_t(kvh) * hd;
+#pragma unroll
+      for (int tt = 0; tt < KPER / 4; ++tt) {
+        const uint32_t d = 4 * li + 64 * tt;
+        int4 v = make_int4(0, 0, 0, 0);
+        if (on && d < hd) v = *reinterpret_cast<const int4*>(krow + d);
+        kr[u][4 * tt] = v.x, kr[u][4 * tt + 1] = v.y, kr[u][4 * tt + 2] = v.z, kr[u][4 * tt + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < HB; ++g) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int64_t acc = 0;
+#pragma unroll
+        for (int tt = 0; tt < KPER / 4; ++tt) {
+          const uint32_t d = 4 * li + 64 * tt;
+          if (d < hd) {
+            const int4 q = *reinterpret_cast<const int4*>(ql + g * hd + d);
+            acc = mac(acc, q.x, kr[u][4 * tt]);
+            acc = mac(acc, q.y, kr[u][4 * tt + 1]);
+            acc = mac(acc, q.z, kr[u][4 * tt + 2]);
+            acc = mac(acc, q.w, kr[u][4 * tt + 3]);
+          }
+        }
+        acc = int64_t(row16_reduce(uint64_t(acc), OpWrapAdd()));
+        const uint64_t r = r0 + grp + 32 * u;
+        if (li == 0 && r < count) sc[g * cstride + r] = requant(acc);
+      }
+    }
+  }
+  __syncthreads();
+  // 2. softmax per head: waves wi of head g take rows wi*64 + lane + stride*n
+  constexpr uint32_t WPH = 8 / HB;
+  const uint32_t g = wave / WPH, wi = wave % WPH;
+  const uint64_t stride = 64 * uint64_t(WPH);
+  int32_t* sg = sc + g * cstride;
+  int64_t best = INT64_MIN;
+  for (uint64_t r = wi * 64 + lane; r < count; r += stride) {
+    const int64_t k = argmax_key(sg[r], uint32_t(r));
+    best = k > best ? k : best;
+  }
+  best = wave_max64(best);
+  if (lane == 0) red[wave] = best;
+  __syncthreads();
+  if (threadIdx.x < HB) {
+    int64_t k = red[threadIdx.x * WPH];
+    for (uint32_t w = 1; w < WPH; ++w) k = red[threadIdx.x * WPH + w] > k ? red[threadIdx.x * WPH + w] : k;
+    hkey[threadIdx.x] = k;
+  }
+  __syncthreads();
+  const uint32_t mi = key_index(hkey[g]);
+  const int32_t mx = sg[mi];
+  int64_t s = 0;
+  for (uint64_t r = wi * 64 + lane; r < count; r += stride) s += softmax_exp(sg[r], mx);  // below 2^63
+  s = wave_sum_wrap64(s);
+  __syncthreads();
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  if (threadIdx.x < HB) {
+    int64_t tsum = 0;
+    for (uint32_t w = 0; w < WPH; ++w) tsum += red[threadIdx.x * WPH + w];
+    hsum[threadIdx.x] = tsum;
+    hrec[threadIdx.x] = tsum < (int64_t(1) << 61) ? softmax_recip(tsum) : 0;
+  }
+  __syncthreads();
+  const int64_t S = hsum[g];
+  const uint64_t M = hrec[g];
+  int64_t ws = 0;
+  for (uint64_t r = wi * 64 + lane; r < count; r += stride) {
+    const int64_t e = softmax_exp(sg[r], mx);
+    const int32_t w = M ? softmax_weight_r(e, S, M) : softmax_weight(e, S);
+    sg[r] = w;  // each row is read and written by the same thread
+    ws += w;
+  }
+  ws = wave_sum_wrap64(ws);
+  __syncthreads();
+  if (lane == 0) red[wave] = ws;
+  __syncthreads();
+  if (threadIdx.x < HB) {
+    int64_t tsum = 0;
+    for (uint32_t w = 0; w < WPH; ++w) tsum += red[threadIdx.x * WPH + w];
+    const uint32_t m2 = key_index(hkey[threadIdx.x]);
+    int32_t* row = sc + threadIdx.x * cstride;
+    row[m2] = add_sat(row[m2], sub_sat(kOneAct, sat32(tsum)));
+  }
+  __syncthreads();
+  // 3. weighted sums: thread d, rows in batches of 8 loads
+  for (uint32_t d = threadIdx.x; d < hd; d += kAttnPThreads) {
+    int64_t acc[HB];
+#pragma unroll
+    for (int gg = 0; gg < HB; ++gg) acc[gg] = 0;
+    uint64_t r = 0;
+    for (; r + 8 <= count; r += 8) {
+      int32_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = a.v[phys(r + u) * a.kv_ld + uint64_t(kvh) * hd + d];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int gg = 0; gg < HB; ++gg) acc[gg] = mac(acc[gg], v[u], sc[gg * cstride + r + u]);
+    }
+    for (; r < count; ++r) {
+      const int32_t v = a.v[phys(r) * a.kv_ld + uint64_t(kvh) * hd + d];
+#pragma unroll
+      for (int gg = 0; gg < HB; ++gg) acc[gg] = mac(acc[gg], v, sc[gg * cstride + r]);
+    }
+#pragma unroll
+    for (int gg = 0; gg < HB; ++gg)
+      a.out[uint64_t(t) * a.out_ld + uint64_t(h0 + gg) * hd + d] = requant(acc[gg]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -863,18 +1082,30 @@ static void launch_gemm_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint
                      uint32_t(mblocks), out, ld_out, acc_out);
 }
 
-void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
-                 int64_t* acc_out, int8_t* a_tiled, hipStream_t s) {
+void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_act, uint64_t kpad, int8_t* a_tiled,
+                       hipStream_t s) {
+  if (m == 0) return;
+  const uint64_t tokens_pad = (m + 63) / 64 * 64;  // the larger block's 16 A tiles
+  hipLaunchKernelGGL(k_act_limbs_tiled, dim3(blocks_for(kpad, 256), unsigned(tokens_pad)), dim3(256), 0, s, act, m, k,
+                     ld_act, kpad, tokens_pad, a_tiled);
+}
+
+void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
+                       const int8_t* a_tiled, hipStream_t s) {
   if (W.rows == 0 || m == 0) return;
-  // tokens padded to a multiple of 64 (the larger block's 16 A tiles)
-  const uint64_t tokens_pad = (m + 63) / 64 * 64, a_tiles = tokens_pad / 4;
-  hipLaunchKernelGGL(k_act_limbs_tiled, dim3(blocks_for(W.kpad, 256), unsigned(tokens_pad)), dim3(256), 0, s, act, m,
-                     W.cols, ld_act, W.kpad, tokens_pad, a_tiled);
+  const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
   const uint64_t big_blocks = ((m + 63) / 64) * (((W.rows + 15) / 16 + 15) / 16);
   if (big_blocks >= 256)
     launch_gemm_shape<16, 16, 2, 4, 4>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   else
     launch_gemm_shape<8, 8, 2, 2, 8>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
+}
+
+void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
+                 int64_t* acc_out, int8_t* a_tiled, hipStream_t s) {
+  if (W.rows == 0 || m == 0) return;
+  launch_gemm_limbs(act, m, W.cols, ld_act, W.kpad, a_tiled, s);
+  launch_gemm_tiled(W, m, out, ld_out, acc_out, a_tiled, s);
 }
 
 void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,
@@ -905,10 +1136,30 @@ void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t 
   }
 }
 
+void launch_rmsnorm_add(int32_t* dst, const int32_t* src, const int32_t* res, uint64_t rows, uint64_t cols,
+                        uint64_t ld, const int32_t* w, int64_t eps, hipStream_t s) {
+  if (rows == 0) return;
+  const dim3 g(static_cast<unsigned>(rows));
+  if (cols > 512 && cols <= 2048)
+    hipLaunchKernelGGL((k_rmsnorm_wide<256, 8>), g, dim3(256), 0, s, src, dst, cols, ld, w, eps, res);
+  else if (cols > 2048 && cols <= 4096)
+    hipLaunchKernelGGL((k_rmsnorm_wide<256, 16>), g, dim3(256), 0, s, src, dst, cols, ld, w, eps, res);
+  else if (cols > 4096 && cols <= 8192)
+    hipLaunchKernelGGL((k_rmsnorm_wide<512, 16>), g, dim3(512), 0, s, src, dst, cols, ld, w, eps, res);
+  else if (cols > 8192 && cols <= 16384)
+    hipLaunchKernelGGL((k_rmsnorm_wide<1024, 16>), g, dim3(1024), 0, s, src, dst, cols, ld, w, eps, res);
+  else
+    hipLaunchKernelGGL(k_rmsnorm, dim3(blocks_for(rows, 4)), dim3(256), 0, s, src, dst, res, rows, cols, ld, w, eps);
+}
+
+void launch_rmsnorm_to(int32_t* dst, const int32_t* src, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
+                       int64_t eps, hipStream_t s) {
+  launch_rmsnorm_add(dst, src, nullptr, rows, cols, ld, w, eps, s);
+}
+
 void launch_rmsnorm(int32_t* x, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w, int64_t eps,
                     hipStream_t s) {
-  if (rows == 0) return;
-  hipLaunchKernelGGL(k_rmsnorm, dim3(blocks_for(rows, 4)), dim3(256), 0, s, x, rows, cols, ld, w, eps);
+  launch_rmsnorm_to(x, x, rows, cols, ld, w, eps, s);
 }
 
 void launch_rope(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t hd, uint64_t half,
@@ -924,6 +1175,26 @@ void launch_attention(const AttnArgs& a, hipStream_t s) {
   uint64_t max_rows = a.causal ? (a.avail) : a.fix_count;
   if (max_rows == 0) max_rows = 1;
   if (max_rows > kMaxAttnRows) return;  // callers validate against kMaxAttnRows
+  // grouped-head kernel: 128-bit row loads need 4-aligned widths and strides
+  const uint64_t stride = std::max<uint64_t>(attn_row_stride(a), 1);
+  const bool aligned = a.hd % 4 == 0 && a.kv_ld % 4 == 0 && a.hd <= 512;
+  if (aligned) {
+    int hb = 8;
+    while (hb > 1 && (a.groups % hb != 0 || uint64_t(hb) * stride * 4 > 65536)) hb >>= 1;
+    if (uint64_t(hb) * stride * 4 <= 65536) {
+      const dim3 grid(a.num_heads / hb, a.n_queries);
+      const size_t lds = size_t(hb) * stride * 4;
+#define DET_ATTN_P(KPER, HB) \
+  hipLaunchKernelGGL((k_attention_prefill<KPER, HB>), grid, dim3(kAttnPThreads), lds, s, a)
+      if (a.hd <= 256) {
+        if (hb == 8) DET_ATTN_P(16, 8); else if (hb == 4) DET_ATTN_P(16, 4); else if (hb == 2) DET_ATTN_P(16, 2); else DET_ATTN_P(16, 1);
+      } else {
+        if (hb == 8) DET_ATTN_P(32, 8); else if (hb == 4) DET_ATTN_P(32, 4); else if (hb == 2) DET_ATTN_P(32, 2); else DET_ATTN_P(32, 1);
+      }
+#undef DET_ATTN_P
+      return;
+    }
+  }
   const size_t lds = size_t(max_rows) * sizeof(int32_t);
   hipLaunchKernelGGL(k_attention, dim3(a.num_heads, a.n_queries), dim3(kAttnThreads), lds, s, a);
 }

@@ -10,6 +10,7 @@ loudly when the HIP library is missing.
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 import os
 import pathlib
 
@@ -232,6 +233,12 @@ class Context:
         if st:
             raise DetError(st, self.lib.det_ctx_last_error(None).decode())
         self.handle = h
+        # objects holding device resources of this context, released (sessions
+        # first) before the context itself so none outlives it
+        self._children = weakref.WeakSet()
+
+    def _adopt(self, obj) -> None:
+        self._children.add(obj)
 
     def check(self, status: int) -> None:
         if status:
@@ -239,6 +246,9 @@ class Context:
 
     def close(self) -> None:
         if getattr(self, "handle", None):
+            order = {"Session": 0, "Model": 1, "Matrix": 2, "DeviceBuffer": 3, "Event": 4}
+            for child in sorted(list(getattr(self, "_children", ())), key=lambda c: order.get(type(c).__name__, 5)):
+                child._release()
             self.lib.det_ctx_destroy(self.handle)
             self.handle = None
 
@@ -317,6 +327,7 @@ class DeviceBuffer:
     def __init__(self, ctx: Context, ptr: int, nbytes: int):
         self.ctx, self.ptr, self.nbytes = ctx, ptr, nbytes
         self.dtype, self.shape = np.dtype(np.uint8), (nbytes,)
+        ctx._adopt(self)
 
     def numpy(self, dtype=None, shape=None) -> np.ndarray:
         dtype = np.dtype(dtype or self.dtype)
@@ -332,14 +343,18 @@ class DeviceBuffer:
         self.ctx.check(self.ctx.lib.det_memcpy_h2d(self.ctx.handle, C.c_void_p(self.ptr), _ptr(a), a.nbytes))
 
     def free(self) -> None:
-        if self.ptr:
+        if self.ptr and self.ctx.handle:
             self.ctx.check(self.ctx.lib.det_device_free(self.ctx.handle, C.c_void_p(self.ptr)))
-            self.ptr = 0
+        self.ptr = 0
+
+    def _release(self) -> None:
+        if self.ptr and self.ctx.handle:
+            self.ctx.lib.det_device_free(self.ctx.handle, C.c_void_p(self.ptr))
+        self.ptr = 0
 
     def __del__(self):
         try:
-            if self.ptr and self.ctx.handle:
-                self.ctx.lib.det_device_free(self.ctx.handle, C.c_void_p(self.ptr))
+            self._release()
         except Exception:
             pass
 
@@ -350,6 +365,7 @@ class Event:
         h = C.c_void_p()
         ctx.check(ctx.lib.det_event_create(ctx.handle, C.byref(h)))
         self.handle = h
+        ctx._adopt(self)
 
     def record(self) -> "Event":
         self.ctx.check(self.ctx.lib.det_event_record(self.ctx.handle, self.handle))
@@ -360,9 +376,14 @@ class Event:
         self.ctx.check(self.ctx.lib.det_event_elapsed_ms(self.ctx.handle, self.handle, end.handle, C.byref(ms)))
         return ms.value
 
+    def _release(self) -> None:
+        if self.handle and self.ctx.handle:
+            self.ctx.lib.det_event_destroy(self.handle)
+        self.handle = None
+
     def __del__(self):
         try:
-            self.ctx.lib.det_event_destroy(self.handle)
+            self._release()
         except Exception:
             pass
 
@@ -384,6 +405,7 @@ class Matrix:
         ctx.check(ctx.lib.det_matrix_upload(ctx.handle, v.shape[0], v.shape[1], width, _ptr(v), rs, C.byref(h)))
         self.handle = h
         self.rows, self.cols = v.shape
+        ctx._adopt(self)
 
     @property
     def storage(self) -> int:
@@ -391,9 +413,14 @@ class Matrix:
         self.ctx.lib.det_matrix_info(self.handle, None, None, C.byref(s))
         return s.value
 
+    def _release(self) -> None:
+        if self.handle and self.ctx.handle:
+            self.ctx.lib.det_matrix_free(self.handle)
+        self.handle = None
+
     def __del__(self):
         try:
-            self.ctx.lib.det_matrix_free(self.handle)
+            self._release()
         except Exception:
             pass
 
@@ -407,6 +434,7 @@ class Model:
         h = C.c_void_p()
         ctx.check(ctx.lib.det_model_create(ctx.handle, C.byref(self.cfg), C.byref(h)))
         self.handle = h
+        ctx._adopt(self)
 
     def load_detwgt(self, data: bytes) -> "Model":
         buf = np.frombuffer(data, dtype=np.uint8)
@@ -436,9 +464,14 @@ class Model:
         self.ctx.check(self.ctx.lib.det_capture(self.handle, _ptr(ids), ids.size, decode_steps, buf, len(buf)))
         return json.loads(buf.value.decode())
 
+    def _release(self) -> None:
+        if self.handle and self.ctx.handle:
+            self.ctx.lib.det_model_free(self.handle)
+        self.handle = None
+
     def __del__(self):
         try:
-            self.ctx.lib.det_model_free(self.handle)
+            self._release()
         except Exception:
             pass
 
@@ -453,6 +486,7 @@ class Session:
             self.ctx.check(self.ctx.lib.det_session_create(model.handle, max_tokens, C.byref(h)))
             _handle = h
         self.handle = _handle
+        self.ctx._adopt(self)
 
     def prefill(self, token_ids, flags: int = DET_COMMIT_ALL) -> PrefillResult:
         ids = np.asarray(token_ids, dtype=np.uint32)
@@ -475,9 +509,14 @@ class Session:
         self.ctx.check(self.ctx.lib.det_session_clone(self.handle, C.byref(h)))
         return Session(self.model, 0, _handle=h)
 
+    def _release(self) -> None:
+        if self.handle and self.ctx.handle:
+            self.ctx.lib.det_session_free(self.handle)
+        self.handle = None
+
     def __del__(self):
         try:
-            self.ctx.lib.det_session_free(self.handle)
+            self._release()
         except Exception:
             pass
 from . import synthetic  # noqa: E402,F401
