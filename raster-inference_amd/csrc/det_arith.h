@@ -72,13 +72,29 @@ DET_HD int64_t div_acc_u32(int64_t v, uint32_t d) {
   return neg ? int64_t(uint64_t(0) - q) : int64_t(q);
 }
 
-// div_act (ops.rs:50-61): round(n * 2^16 / d), saturating to i32. d != 0.
+// div_act (ops.rs:50-61): round(n * 2^16 / d) ties to even on the magnitude,
+// saturating to i32; d != 0. |n 2^16| < 2^47 and |d| < 2^32 are exact doubles,
+// so the double quotient is within one of the floor quotient; quotients of
+// 2^31 + 2 or more saturate whatever the rounding; below that the exact
+// remainder (products below 2^64) fixes and rounds the estimate.
 DET_HD int32_t div_act(int32_t n, int32_t d) {
   const int64_t num = int64_t(n) * 65536;
   const bool neg = (num < 0) != (d < 0);
   const uint64_t un = num < 0 ? uint64_t(-num) : uint64_t(num);
   const uint64_t ud = d < 0 ? uint64_t(-int64_t(d)) : uint64_t(d);
-  const uint64_t q = udiv_rte(un, ud);
+  const double qd = double(un) / double(ud);
+  if (qd >= 2147483650.0) return neg ? INT32_MIN : INT32_MAX;
+  uint64_t q = uint64_t(qd);
+  int64_t r = int64_t(un - q * ud);
+  if (r < 0) {
+    --q;
+    r += int64_t(ud);
+  } else if (r >= int64_t(ud)) {
+    ++q;
+    r -= int64_t(ud);
+  }
+  const uint64_t twice = uint64_t(r) << 1;
+  q += uint64_t((twice > ud) | ((twice == ud) & (q & 1)));
   return sat32(neg ? -int64_t(q) : int64_t(q));
 }
 

@@ -288,7 +288,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
 // gate/up tiles, out[f] = mul_sat(gelu(gate_f), up_f), also written as limb
 // planes to out_limbs (plane stride out_kpad) for the next GEMV.
 template <int KS, int EPI>
-__global__ __launch_bounds__(256) void k_gemv_dec(const int8_t* __restrict__ q, const int32_t* __restrict__ scale,
+__global__ __launch_bounds__(256, 5) void k_gemv_dec(const int8_t* __restrict__ q, const int32_t* __restrict__ scale,
                                                   const int32_t* __restrict__ rowsum, const int8_t* __restrict__ limbs,
                                                   uint64_t n_rows, uint64_t kpad, uint32_t kchunks,
                                                   int32_t* __restrict__ out, int64_t* __restrict__ acc_out,
@@ -319,17 +319,19 @@ __global__ __launch_bounds__(256) void k_gemv_dec(const int8_t* __restrict__ q, 
     const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 32);
     v4i acc = zero;
     uint64_t s = s0;
-    for (; s + 4 <= s1; s += 4) {
-      v4i b[8], a[8];
+    // three K steps per batch: a wave's 5-step share (K 2560 split four ways)
+    // takes two load round trips either way, with 16 fewer registers than 4
+    for (; s + 3 <= s1; s += 3) {
+      v4i b[6], a[6];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 3; ++u) {
         b[2 * u] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128) : zero;
         b[2 * u + 1] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128 + 1) : zero;
         a[2 * u] = a_on ? ap[(s + u) * 8] : zero;
         a[2 * u + 1] = a_on ? ap[(s + u) * 8 + 1] : zero;
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+      for (int u = 0; u < 6; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
     }
     for (; s < s1; ++s) {
       const v4i b0 = t_on ? __builtin_nontemporal_load(bp + s * 128) : zero;
