@@ -220,6 +220,16 @@ int det_session_prefill(det_session_t* s, const uint32_t* token_ids, uint64_t n,
 /* pipeline::decode_step_with_mode (runtime/pipeline.rs:165-216): embed token,
  * every decode_transition layer with in-place KV append, finalize logits. */
 int det_session_decode(det_session_t* s, uint32_t token, uint32_t flags, det_decode_result_t* out);
+/* One decode_step (runtime/pipeline.rs:165-216, as det_session_decode) for
+ * each of n distinct sessions of one model, in shared launches: every
+ * projection runs once over the n activation rows (M = n) and attention reads
+ * each session's own ragged cache window. tokens[i] feeds sessions[i] and
+ * out[i] (may be NULL) receives its result. Each session's next token, logits,
+ * caches and commitments are bit-identical to det_session_decode of that
+ * session alone. The reference decodes one sequence per call; this entry point
+ * batches those calls and has no other behaviour. */
+int det_session_decode_batch(det_session_t* const* sessions, uint64_t n, const uint32_t* tokens, uint32_t flags,
+                             det_decode_result_t* out);
 /* Copies the last logits (vocab int32) to host. */
 int det_session_logits(det_session_t* s, int32_t* out, uint64_t n);
 int det_session_position(const det_session_t* s, uint64_t* position);

@@ -382,6 +382,11 @@ struct GLayer {
 
 }  // namespace
 
+namespace {
+struct BatchWs;
+void free_batch(BatchWs* b);
+}  // namespace
+
 struct det_model {
   det_ctx* ctx = nullptr;
   det_text_config_t cfg{};
@@ -419,8 +424,10 @@ struct det_model {
   det::RopeTable* rope_tables_dev = nullptr;
   uint32_t trig_pairs = 0;
   bool fused_ok = false;
+  BatchWs* batch = nullptr;  // row scratch of batched decode steps (grown on demand)
 
   ~det_model() {
+    free_batch(batch);
     for (auto& f : fused) { free_matrix(f.qkv); free_matrix(f.gateup); }
     for (auto& v : ple_proj_views) free_matrix(v);
     for (auto& kv : tensors)
@@ -918,7 +925,8 @@ void copy_d2d(det_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
 }
 
 // Q/K/V projections + head norms + RoPE for M rows at positions pos0.. (det_kernels.rs:499-566, 930-985).
-void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0) {
+// positions: one device position per row (batched decode) instead of pos0 + row.
+void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const uint64_t* positions = nullptr) {
   det_ctx* ctx = s->m->ctx;
   hipStream_t st = ctx->stream;
   const uint64_t qw = L.num_heads * L.head_dim, kw = L.num_kv_heads * L.head_dim;
@@ -933,7 +941,10 @@ void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0) {
   det::launch_rmsnorm(s->qb, M * L.num_heads, L.head_dim, L.head_dim, L.q_norm, L.eps, st);
   det::launch_rmsnorm(s->kb, M * L.num_kv_heads, L.head_dim, L.head_dim, L.k_norm, L.eps, st);
   det::launch_rmsnorm(s->vb, M * L.num_kv_heads, L.head_dim, L.head_dim, nullptr, L.eps, st);
-  if (L.rotary) {
+  if (L.rotary && positions) {
+    det::launch_rope_rows(s->qb, M, qw, L.num_heads, L.head_dim, L.rotary / 2, L.inv_freq, positions, st);
+    det::launch_rope_rows(s->kb, M, kw, L.num_kv_heads, L.head_dim, L.rotary / 2, L.inv_freq, positions, st);
+  } else if (L.rotary) {
     det::launch_rope(s->qb, M, qw, L.num_heads, L.head_dim, L.rotary / 2, L.inv_freq, pos0, 1, st);
     det::launch_rope(s->kb, M, kw, L.num_kv_heads, L.head_dim, L.rotary / 2, L.inv_freq, pos0, 1, st);
   }
@@ -1160,6 +1171,196 @@ void decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
   out->kv[0] = 0;
   if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
   out->next_token = ctx->argmax(s->logits, m->vocab);
+}
+
+// ---------------------------------------------------------------------------
+// Batched decode: one decode_step (runtime/pipeline.rs:165-216) for each of n
+// independent sequences of one model, with every projection run once over the
+// n activation rows (the weights stream once for all of them) and attention
+// reading each sequence's own cache window. Per row, every operation is the
+// single-sequence one, so each sequence's outputs, caches and commitments are
+// those of its solo decode.
+// ---------------------------------------------------------------------------
+struct BatchWs {
+  std::unique_ptr<det_session> rows;  // activation scratch sized for cap rows
+  uint64_t cap = 0;
+  int32_t* logits = nullptr;  // [cap][vocab]
+  int32_t* dec_in = nullptr;  // [cap][hidden] token embeddings (PLE input)
+  uint32_t* next = nullptr;   // [cap] greedy tokens
+  uint8_t* desc = nullptr;    // device: positions, per-layer windows and append targets
+  uint8_t* desc_host = nullptr;  // pinned staging of desc
+  size_t desc_bytes = 0;
+  ~BatchWs() {
+    for (void* p : {static_cast<void*>(logits), static_cast<void*>(dec_in), static_cast<void*>(next),
+                    static_cast<void*>(desc)})
+      if (p) (void)hipFree(p);
+    if (desc_host) (void)hipHostFree(desc_host);
+  }
+};
+
+void free_batch(BatchWs* b) { delete b; }
+
+// Byte layout of the per-step descriptor block for n sequences and L layers:
+// positions u64[n] | AttnSeq[L][n] | key rows int32*[L][n] | value rows int32*[L][n].
+struct BatchDesc {
+  size_t pos = 0, seqs = 0, kdst = 0, vdst = 0, bytes = 0;
+  BatchDesc(uint64_t n, uint64_t L) {
+    seqs = pos + 8 * n;
+    kdst = seqs + sizeof(det::AttnSeq) * L * n;
+    vdst = kdst + sizeof(int32_t*) * L * n;
+    bytes = vdst + sizeof(int32_t*) * L * n;
+  }
+};
+
+BatchWs& ensure_batch(det_model* m, uint64_t n) {
+  if (m->batch && m->batch->cap >= n) return *m->batch;
+  HIPC(hipStreamSynchronize(m->ctx->stream));
+  free_batch(m->batch);
+  m->batch = nullptr;
+  auto b = std::make_unique<BatchWs>();
+  b->cap = std::max<uint64_t>(n, 16);
+  b->rows = std::make_unique<det_session>();
+  b->rows->m = m;
+  b->rows->max_tokens = b->cap;
+  session_alloc(b->rows.get());
+  HIPC(hipMalloc(&b->logits, b->cap * m->vocab * 4));
+  HIPC(hipMalloc(&b->dec_in, b->cap * m->hidden * 4));
+  HIPC(hipMalloc(&b->next, b->cap * 4));
+  b->desc_bytes = BatchDesc(b->cap, m->layers.size()).bytes;
+  HIPC(hipMalloc(&b->desc, b->desc_bytes));
+  HIPC(hipHostMalloc(reinterpret_cast<void**>(&b->desc_host), b->desc_bytes, hipHostMallocDefault));
+  m->batch = b.release();
+  return *m->batch;
+}
+
+void check_batch(det_session* const* ss, uint64_t n, const uint32_t* tokens) {
+  if (n == 0) bail("batched decode requires at least one session");
+  det_model* m = ss[0]->m;
+  for (uint64_t i = 0; i < n; ++i) {
+    det_session* s = ss[i];
+    if (!s) bail("null session in batch");
+    if (s->m != m) bail("batched sessions must share one model");
+    for (uint64_t j = 0; j < i; ++j)
+      if (ss[j] == s) bail("a session appears twice in one batch");
+    if (s->position == 0) bail("decode requires a prefilled session");
+    if (s->position >= s->max_tokens) bail("session capacity exhausted");
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+      const GKv& c = s->kv[l];
+      if (m->layers[l].donor) continue;
+      if (!c.has) bail("deterministic decode cache append requires canonical key rows");
+      if (!c.ring && s->position >= c.cap) bail("KV cache capacity exceeded");
+    }
+  }
+  check_ids(m, tokens, n);
+}
+
+void decode_batch(det_session* const* ss, uint64_t n, const uint32_t* tokens, uint32_t flags,
+                  det_decode_result_t* out) {
+  check_batch(ss, n, tokens);
+  det_model* m = ss[0]->m;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  const uint64_t H = m->hidden, V = m->vocab, nl = m->layers.size();
+  BatchWs& b = ensure_batch(m, n);
+  det_session* w = b.rows.get();
+  // host bookkeeping: cache state after this step's append, then the windows
+  const BatchDesc D(n, nl);
+  uint8_t* hb = b.desc_host;
+  auto* pos = reinterpret_cast<uint64_t*>(hb + D.pos);
+  auto* seqs = reinterpret_cast<det::AttnSeq*>(hb + D.seqs);
+  auto* kdst = reinterpret_cast<int32_t**>(hb + D.kdst);
+  auto* vdst = reinterpret_cast<int32_t**>(hb + D.vdst);
+  std::vector<std::vector<GKv>> after(n);
+  std::vector<uint64_t> longest(nl, 1);
+  for (uint64_t i = 0; i < n; ++i) {
+    det_session* s = ss[i];
+    pos[i] = s->position;
+    after[i] = s->kv;
+    for (size_t l = 0; l < nl; ++l) {
+      const GLayer& L = m->layers[l];
+      const uint64_t kw = L.num_kv_heads * L.head_dim;
+      if (!L.donor) {
+        GKv& own = after[i][l];
+        const uint64_t slot = own.ring ? pos[i] % own.cap : pos[i];
+        kv_advance(own, pos[i] + 1);
+        own.has = true;
+        kdst[l * n + i] = own.k + slot * kw;
+        vdst[l * n + i] = own.v + slot * kw;
+      } else {
+        kdst[l * n + i] = vdst[l * n + i] = nullptr;
+      }
+      const GKv& ac = L.donor ? after[i][*L.donor] : after[i][l];
+      if (!ac.has) bail("deterministic attention requires canonical key cache rows");
+      if (ac.row_w != kw) bail("layer cache head count mismatch");
+      const uint64_t cur = ac.len;
+      const uint64_t key_start = L.sliding ? (cur > *L.sliding_window ? cur - *L.sliding_window : 0) : 0;
+      const uint64_t count = cur - key_start;
+      if (count == 0) contract("attention_softmax requires a non-empty logits slice");
+      if (count > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
+      det::AttnSeq& q = seqs[l * n + i];
+      q.k = ac.k;
+      q.v = ac.v;
+      q.base = ac.ring ? (ac.start + key_start) % ac.cap : key_start;
+      q.wrap = ac.ring ? ac.cap : 0;
+      q.count = count;
+      longest[l] = std::max(longest[l], count);
+    }
+  }
+  uint8_t* dd = b.desc;
+  HIPC(hipMemcpyAsync(dd, hb, D.bytes, hipMemcpyHostToDevice, st));
+  HIPC(hipMemcpyAsync(w->ids, tokens, n * 4, hipMemcpyHostToDevice, st));
+  const auto* pos_dev = reinterpret_cast<const uint64_t*>(dd + D.pos);
+  det::launch_gather_rows(*m->embedding, w->ids, n, 0, H, m->embed_scale, b.dec_in, H, st);
+  copy_d2d(ctx, w->x, b.dec_in, n * H * 4);
+  for (size_t l = 0; l < nl; ++l) {
+    const GLayer& L = m->layers[l];
+    const uint64_t kw = L.num_kv_heads * L.head_dim;
+    if (m->has_ple && L.has_ple) ple_inputs(w, l, w->ids, b.dec_in, n, w->pe);
+    det::launch_rmsnorm_to(w->normed, w->x, n, H, H, L.in_ln, L.eps, st);
+    qkv_block(w, L, n, 0, pos_dev);
+    if (!L.donor)
+      det::launch_kv_append(w->kb, w->vb, kw, n, reinterpret_cast<int32_t* const*>(dd + D.kdst) + l * n,
+                            reinterpret_cast<int32_t* const*>(dd + D.vdst) + l * n, st);
+    det::AttnArgs a{};
+    a.q = w->qb; a.q_ld = L.num_heads * L.head_dim;
+    a.kv_ld = kw;
+    a.out = w->attn; a.out_ld = L.num_heads * L.head_dim;
+    a.hd = uint32_t(L.head_dim); a.num_heads = uint32_t(L.num_heads);
+    a.groups = uint32_t(L.num_heads / L.num_kv_heads);
+    a.n_queries = uint32_t(n); a.causal = 0; a.fix_start = 0; a.fix_count = longest[l];
+    a.seqs = reinterpret_cast<const det::AttnSeq*>(dd + D.seqs) + l * n;
+    det::launch_attention(a, st);
+    post_attention(w, L, n, (m->has_ple && L.has_ple) ? w->pe : nullptr);
+  }
+  // det_hidden_to_logits for every row, then argmax_first per row
+  det::launch_rmsnorm_to(w->normed, w->x, n, H, H, m->final_norm, m->eps, st);
+  ctx->linear(*m->lm_head, w->normed, n, H, b.logits, V, nullptr);
+  if (m->softcap) det::launch_softcap(b.logits, n * V, *m->softcap, st);
+  det::launch_argmax_rows(b.logits, n, V, b.next, st);
+  for (uint64_t i = 0; i < n; ++i) copy_d2d(ctx, ss[i]->logits, b.logits + i * V, V * 4);
+  std::vector<uint32_t> next(n);
+  HIPC(hipMemcpyAsync(next.data(), b.next, n * 4, hipMemcpyDeviceToHost, st));
+  HIPC(hipStreamSynchronize(st));
+  for (uint64_t i = 0; i < n; ++i) {
+    ss[i]->kv = after[i];
+    ss[i]->position += 1;
+    ss[i]->logits_valid = true;
+  }
+  if (flags & DET_COMMIT_ACTIVATIONS) {
+    std::vector<int32_t> hx(n * H), lg(n * V);
+    HIPC(hipMemcpyAsync(hx.data(), w->x, n * H * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipMemcpyAsync(lg.data(), b.logits, n * V * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    for (uint64_t i = 0; i < n; ++i) {
+      commit_rows(hx.data() + i * H, 1, H, out[i].activation);
+      commit_vector(lg.data() + i * V, V, out[i].logits);
+    }
+  }
+  for (uint64_t i = 0; i < n; ++i) {
+    out[i].kv[0] = 0;
+    if (flags & DET_COMMIT_KV) commit_kv(ss[i], all_caches(ss[i]), out[i].kv);
+    out[i].next_token = next[i];
+  }
 }
 
 // Attention arguments of layer l for the fused decode step.
@@ -1627,6 +1828,17 @@ int det_session_decode(det_session_t* s, uint32_t token, uint32_t flags, det_dec
     det_decode_result_t tmp{};
     if (s->m->fused_ok && !(flags & DET_DECODE_PER_OP)) decode_fused(s, token, flags, out ? out : &tmp);
     else decode(s, token, flags, out ? out : &tmp, nullptr);
+  });
+}
+int det_session_decode_batch(det_session_t* const* sessions, uint64_t n, const uint32_t* tokens, uint32_t flags,
+                             det_decode_result_t* out) {
+  if (!sessions || n == 0 || !sessions[0]) {
+    g_error = "batched decode requires at least one session";
+    return 1;
+  }
+  return guarded(sessions[0]->m->ctx, [&] {
+    std::vector<det_decode_result_t> tmp(out ? 0 : n);
+    decode_batch(sessions, n, tokens, flags, out ? out : tmp.data());
   });
 }
 int det_session_logits(det_session_t* s, int32_t* out, uint64_t n) {

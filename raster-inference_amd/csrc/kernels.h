@@ -89,6 +89,15 @@ void launch_rope(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_
                  uint64_t half, const int64_t* inv_freq, uint64_t pos0, uint64_t pos_step,
                  hipStream_t s);
 
+// Per-query cache window for batched decode (one query per sequence).
+struct AttnSeq {
+  const int32_t* k;  // the sequence's cache rows
+  const int32_t* v;
+  uint64_t base;     // physical row of window row 0
+  uint64_t wrap;     // ring capacity (window row r at (base + r) mod wrap), 0 for a linear cache
+  uint64_t count;    // window rows
+};
+
 struct AttnArgs {
   const int32_t* q;  // query rows: q + t*q_ld + h*hd
   uint64_t q_ld;
@@ -106,6 +115,9 @@ struct AttnArgs {
   int causal;
   uint64_t window, causal_offset, avail;
   uint64_t fix_start, fix_count;
+  // batched decode: query t uses seqs[t] (k, v, window) instead of the fields
+  // above; fix_count then holds the longest window of the batch
+  const AttnSeq* seqs;
 };
 // Windows longer than kMaxAttentionRows are rejected by the callers.
 constexpr uint64_t kMaxAttentionRows = 16000;
@@ -118,6 +130,14 @@ void launch_scale(int32_t* x, uint64_t n, int32_t scalar, hipStream_t s);
 void launch_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s);
 
 // Embedding-style gather: out[t][c] = mul_sat(Wgt(M[ids[t]][col0 + c]), scale).
+// RoPE with one position per row (positions on the device).
+void launch_rope_rows(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t hd, uint64_t half,
+                      const int64_t* inv_freq, const uint64_t* positions, hipStream_t s);
+// Row i of k and v (width w) to kdst[i] / vdst[i] (device arrays of row pointers).
+void launch_kv_append(const int32_t* k, const int32_t* v, uint64_t w, uint64_t n, int32_t* const* kdst,
+                      int32_t* const* vdst, hipStream_t s);
+// out[r] = first index of the maximum of row r of x [rows][n].
+void launch_argmax_rows(const int32_t* x, uint64_t rows, uint64_t n, uint32_t* out, hipStream_t s);
 void launch_gather_rows(const DevMatrix& M, const uint32_t* ids, uint64_t m, uint64_t col0,
                         uint64_t ncols, int32_t scale, int32_t* out, uint64_t ld_out, hipStream_t s);
 

@@ -608,14 +608,15 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_wide(const int32_t* src, int32_t
 // RoPE (ops.rs:151-196): one thread per (row, head, pair).
 // ---------------------------------------------------------------------------
 __global__ void k_rope(int32_t* __restrict__ x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t hd,
-                       uint64_t half, const int64_t* __restrict__ inv_freq, uint64_t pos0, uint64_t pos_step) {
+                       uint64_t half, const int64_t* __restrict__ inv_freq, uint64_t pos0, uint64_t pos_step,
+                       const uint64_t* __restrict__ positions) {
   const uint64_t idx = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint64_t total = rows * heads * half;
   if (idx >= total) return;
   const uint64_t i = idx % half;
   const uint64_t h = (idx / half) % heads;
   const uint64_t r = idx / (half * heads);
-  const uint64_t pos = pos0 + r * pos_step;
+  const uint64_t pos = positions ? positions[r] : pos0 + r * pos_step;
   if (pos == 0) return;  // identity (ops.rs:179-181)
   int32_t c, s;
   sin_cos(rope_angle(pos, inv_freq[i]), &c, &s);
@@ -633,13 +634,25 @@ constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / 64;
 constexpr uint64_t kMaxAttnRows = 16000;  // LDS: one int32 per window row
 
-__global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
-  extern __shared__ int32_t lds_w[];  // one int32 per window row (scores, then weights)
-  __shared__ int64_t red[kAttnWaves];
-  __shared__ int64_t bcast[2];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t h = blockIdx.x, t = blockIdx.y;
-  const uint32_t kvh = h / a.groups;
+// Key/value window of query t: window row r sits at physical cache row
+// phys(r) = base + r, wrapped once around a ring of `wrap` rows (base < wrap,
+// r < count <= wrap).
+struct AttnWin {
+  const int32_t* k;
+  const int32_t* v;
+  uint64_t base, wrap, count;
+  __device__ uint64_t phys(uint64_t r) const {
+    const uint64_t p = base + r;
+    return p >= wrap ? p - wrap : p;
+  }
+};
+
+__device__ inline AttnWin attn_window_of(const AttnArgs& a, uint32_t t) {
+  if (a.seqs) {
+    // one query per sequence, each over its own cache window
+    const AttnSeq sq = a.seqs[t];
+    return {sq.k, sq.v, sq.base, sq.wrap ? sq.wrap : ~0ull, sq.count};
+  }
   uint64_t start, count;
   if (a.causal) {
     uint64_t end = t + 1 + a.causal_offset;
@@ -651,14 +664,25 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
     start = a.fix_start;
     count = a.fix_count;
   }
+  const uint64_t base = a.ring_cap ? (a.ring_start + start) % a.ring_cap : start;
+  return {a.k, a.v, base, a.ring_cap ? a.ring_cap : ~0ull, count};
+}
+
+__global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
+  extern __shared__ int32_t lds_w[];  // one int32 per window row (scores, then weights)
+  __shared__ int64_t red[kAttnWaves];
+  __shared__ int64_t bcast[2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t h = blockIdx.x, t = blockIdx.y;
+  const uint32_t kvh = h / a.groups;
+  const AttnWin win = attn_window_of(a, t);
+  const uint64_t count = win.count;
   if (count == 0) return;  // host validation makes every window non-empty
   const int32_t* qrow = a.q + uint64_t(t) * a.q_ld + uint64_t(h) * a.hd;
   int32_t* orow = a.out + uint64_t(t) * a.out_ld + uint64_t(h) * a.hd;
   // 1. scores (wave per row, lanes over head dims)
   for (uint64_t r = wave; r < count; r += kAttnWaves) {
-    uint64_t phys = start + r;
-    if (a.ring_cap) phys = (a.ring_start + phys) % a.ring_cap;
-    const int32_t* krow = a.k + phys * a.kv_ld + uint64_t(kvh) * a.hd;
+    const int32_t* krow = win.k + win.phys(r) * a.kv_ld + uint64_t(kvh) * a.hd;
     int64_t acc = 0;
     for (uint32_t d = lane; d < a.hd; d += 64) acc = mac(acc, qrow[d], krow[d]);
     acc = wave_sum_wrap(acc);
@@ -696,11 +720,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   // 5. weighted sum over value rows
   for (uint32_t d = threadIdx.x; d < a.hd; d += kAttnThreads) {
     int64_t acc = 0;
-    for (uint64_t r = 0; r < count; ++r) {
-      uint64_t phys = start + r;
-      if (a.ring_cap) phys = (a.ring_start + phys) % a.ring_cap;
-      acc = mac(acc, a.v[phys * a.kv_ld + uint64_t(kvh) * a.hd + d], lds_w[r]);
-    }
+    for (uint64_t r = 0; r < count; ++r) acc = mac(acc, win.v[win.phys(r) * a.kv_ld + uint64_t(kvh) * a.hd + d], lds_w[r]);
     orow[d] = requant(acc);
   }
   (void)bcast;
@@ -720,7 +740,7 @@ constexpr int kAttnPThreads = 512;
 
 // Score-row stride of a launch: no window of its queries is longer.
 __host__ __device__ inline uint64_t attn_row_stride(const AttnArgs& a) {
-  if (!a.causal) return a.fix_count;
+  if (a.seqs || !a.causal) return a.fix_count;
   return (a.window && a.window < a.avail) ? a.window : a.avail;
 }
 
@@ -736,26 +756,13 @@ __global__ __launch_bounds__(kAttnPThreads) void k_attention_prefill(AttnArgs a)
   const uint32_t hg = blockIdx.x, t = blockIdx.y;
   const uint32_t h0 = hg * HB, kvh = h0 / a.groups;
   const uint32_t hd = a.hd;
-  uint64_t start, count;
-  if (a.causal) {
-    uint64_t end = t + 1 + a.causal_offset;
-    start = (a.window && end > a.window) ? end - a.window : 0;
-    if (start > a.avail) start = a.avail;
-    if (end > a.avail) end = a.avail;
-    count = end > start ? end - start : 0;
-  } else {
-    start = a.fix_start;
-    count = a.fix_count;
-  }
+  const AttnWin win = attn_window_of(a, t);
+  const uint64_t count = win.count;
   if (count == 0) return;  // host validation makes every window non-empty
   const uint64_t cstride = attn_row_stride(a);
-  // window row r sits at physical row base + r, wrapped once around a ring
-  const uint64_t base = a.ring_cap ? (a.ring_start + start) % a.ring_cap : start;
-  const uint64_t wrap = a.ring_cap ? a.ring_cap : ~0ull;
-  auto phys = [&](uint64_t r) {
-    const uint64_t p = base + r;
-    return p >= wrap ? p - wrap : p;
-  };
+  const int32_t* kc = win.k;
+  const int32_t* vc = win.v;
+  auto phys = [&](uint64_t r) { return win.phys(r); };
   for (uint32_t i = threadIdx.x; i < HB * hd; i += kAttnPThreads)
     ql[i] = a.q[uint64_t(t) * a.q_ld + uint64_t(h0 + i / hd) * hd + i % hd];
   __syncthreads();
@@ -767,7 +774,7 @@ __global__ __launch_bounds__(kAttnPThreads) void k_attention_prefill(AttnArgs a)
     for (int u = 0; u < U; ++u) {
       const uint64_t r = r0 + grp + 32 * u;
       const bool on = r < count;
-      const int32_t* krow = a.k + (on ? phys(r) : 0) * a.kv_ld + uint64_t(kvh) * hd;
+      const int32_t* krow = kc + (on ? phys(r) : 0) * a.kv_ld + uint64_t(kvh) * hd;
 #pragma unroll
       for (int tt = 0; tt < KPER / 4; ++tt) {
         const uint32_t d = 4 * li + 64 * tt;
@@ -863,14 +870,14 @@ __global__ __launch_bounds__(kAttnPThreads) void k_attention_prefill(AttnArgs a)
     for (; r + 8 <= count; r += 8) {
       int32_t v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = a.v[phys(r + u) * a.kv_ld + uint64_t(kvh) * hd + d];
+      for (int u = 0; u < 8; ++u) v[u] = vc[phys(r + u) * a.kv_ld + uint64_t(kvh) * hd + d];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll
         for (int gg = 0; gg < HB; ++gg) acc[gg] = mac(acc[gg], v[u], sc[gg * cstride + r + u]);
     }
     for (; r < count; ++r) {
-      const int32_t v = a.v[phys(r) * a.kv_ld + uint64_t(kvh) * hd + d];
+      const int32_t v = vc[phys(r) * a.kv_ld + uint64_t(kvh) * hd + d];
 #pragma unroll
       for (int gg = 0; gg < HB; ++gg) acc[gg] = mac(acc[gg], v, sc[gg * cstride + r]);
     }
@@ -878,6 +885,30 @@ __global__ __launch_bounds__(kAttnPThreads) void k_attention_prefill(AttnArgs a)
     for (int gg = 0; gg < HB; ++gg)
       a.out[uint64_t(t) * a.out_ld + uint64_t(h0 + gg) * hd + d] = requant(acc[gg]);
   }
+}
+
+// Appends one key and one value row per sequence at its canonical slot:
+// dst[i] (key, value) receive rows i of k and v (width w).
+__global__ void k_kv_append(const int32_t* __restrict__ k, const int32_t* __restrict__ v, uint64_t w,
+                            int32_t* const* __restrict__ kdst, int32_t* const* __restrict__ vdst) {
+  const uint64_t i = blockIdx.y, c = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= w) return;
+  kdst[i][c] = k[i * w + c];
+  vdst[i][c] = v[i * w + c];
+}
+
+// First-index argmax of each row of x [rows][n] (one workgroup per row).
+__global__ __launch_bounds__(256) void k_argmax_rows(const int32_t* __restrict__ x, uint64_t n,
+                                                     uint32_t* __restrict__ out) {
+  __shared__ int64_t red[4];
+  const int32_t* xr = x + uint64_t(blockIdx.x) * n;
+  int64_t best = INT64_MIN;
+  for (uint64_t i = threadIdx.x; i < n; i += 256) {
+    const int64_t key = argmax_key(xr[i], uint32_t(i));
+    best = key > best ? key : best;
+  }
+  best = block_reduce<4>(best, 2, red);
+  if (threadIdx.x == 0) out[blockIdx.x] = key_index(best);
 }
 
 // ---------------------------------------------------------------------------
@@ -1169,7 +1200,15 @@ void launch_rope(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_
   const uint64_t total = rows * heads * half;
   if (total == 0) return;
   hipLaunchKernelGGL(k_rope, dim3(blocks_for(total, 256)), dim3(256), 0, s, x, rows, ld, heads, hd, half, inv_freq,
-                     pos0, pos_step);
+                     pos0, pos_step, nullptr);
+}
+
+void launch_rope_rows(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t hd, uint64_t half,
+                      const int64_t* inv_freq, const uint64_t* positions, hipStream_t s) {
+  const uint64_t total = rows * heads * half;
+  if (total == 0) return;
+  hipLaunchKernelGGL(k_rope, dim3(blocks_for(total, 256)), dim3(256), 0, s, x, rows, ld, heads, hd, half, inv_freq,
+                     0, 0, positions);
 }
 
 void launch_attention(const AttnArgs& a, hipStream_t s) {
@@ -1218,6 +1257,13 @@ void launch_gather_rows(const DevMatrix& M, const uint32_t* ids, uint64_t m, uin
   if (!m || !ncols) return;
   hipLaunchKernelGGL(k_gather_rows, dim3(blocks_for(ncols, 256), unsigned(m)), dim3(256), 0, s, M, ids, m, col0,
                      ncols, scale, out, ld_out);
+}
+void launch_kv_append(const int32_t* k, const int32_t* v, uint64_t w, uint64_t n, int32_t* const* kdst,
+                      int32_t* const* vdst, hipStream_t s) {
+  if (n && w) hipLaunchKernelGGL(k_kv_append, dim3(blocks_for(w, 256), unsigned(n)), dim3(256), 0, s, k, v, w, kdst, vdst);
+}
+void launch_argmax_rows(const int32_t* x, uint64_t rows, uint64_t n, uint32_t* out, hipStream_t s) {
+  if (rows) hipLaunchKernelGGL(k_argmax_rows, dim3(unsigned(rows)), dim3(256), 0, s, x, n, out);
 }
 void launch_argmax(const int32_t* x, uint64_t n, int64_t* scratch, uint32_t* out, hipStream_t s) {
   const uint64_t parts = (n + 1023) / 1024;

@@ -189,6 +189,7 @@ def lib() -> C.CDLL:
         "det_session_free": (None, [P]),
         "det_session_prefill": (C.c_int, [P, P, u64, C.c_uint32, C.POINTER(PrefillResult)]),
         "det_session_decode": (C.c_int, [P, C.c_uint32, C.c_uint32, C.POINTER(DecodeResult)]),
+        "det_session_decode_batch": (C.c_int, [P, u64, P, C.c_uint32, P]),
         "det_session_logits": (C.c_int, [P, i32p, u64]),
         "det_session_position": (C.c_int, [P, C.POINTER(u64)]),
         "det_capture": (C.c_int, [P, P, u64, u64, C.c_char_p, C.c_size_t]),
@@ -499,6 +500,11 @@ class Session:
         self.ctx.check(self.ctx.lib.det_session_decode(self.handle, int(token), flags, C.byref(r)))
         return r
 
+    def position(self) -> int:
+        p = C.c_uint64()
+        self.ctx.check(self.ctx.lib.det_session_position(self.handle, C.byref(p)))
+        return p.value
+
     def logits(self, vocab: int) -> np.ndarray:
         out = np.empty(vocab, dtype=np.int32)
         self.ctx.check(self.ctx.lib.det_session_logits(self.handle, out.ctypes.data_as(C.POINTER(C.c_int32)), vocab))
@@ -519,4 +525,21 @@ class Session:
             self._release()
         except Exception:
             pass
+def decode_batch(sessions, tokens, flags: int = DET_COMMIT_ALL) -> list:
+    """One decode step for each session (same model) in shared launches;
+    results[i] is bit-identical to sessions[i].decode(tokens[i], flags)."""
+    sessions = list(sessions)
+    if not sessions:
+        raise ValueError("decode_batch needs at least one session")
+    toks = np.asarray(tokens, dtype=np.uint32)
+    if toks.size != len(sessions):
+        raise ValueError("one token per session")
+    ctx = sessions[0].ctx
+    handles = (C.c_void_p * len(sessions))(*[s.handle for s in sessions])
+    res = (DecodeResult * len(sessions))()
+    ctx.check(ctx.lib.det_session_decode_batch(C.cast(handles, C.c_void_p), len(sessions), _ptr(toks), flags,
+                                               C.cast(res, C.c_void_p)))
+    return list(res)
+
+
 from . import synthetic  # noqa: E402,F401

@@ -1,0 +1,139 @@
+"""GPU parity of batched decode over ragged sequences.
+
+det_session_decode_batch runs one decode step for n independent sessions in
+shared launches (projections over M = n activation rows, attention over each
+session's own cache window). The requirement is that every session's per-step
+results (next token, activation / logits / KV commitments) equal its solo
+decode on an identical session, whose commitments are themselves pinned to
+the oracle in test_gpu_decode_fused.py and test_gpu_parity.py.
+"""
+import numpy as np
+import pytest
+
+import fixtures
+
+pytestmark = pytest.mark.gpu
+rd = pytest.importorskip("rasterdet")
+from rasterdet import synthetic  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = rd.Context(0)
+    yield c
+    c.close()
+
+
+def build(ctx, cfg, tensors):
+    gm = rd.Model(ctx, cfg)
+    for name, v, s in tensors:
+        gm.set_tensor(name, v, s)
+    return gm.finalize()
+
+
+def key(r):
+    return (r.activation, r.logits, r.kv, r.next_token)
+
+
+def ragged_prompts(n, lo, hi, vocab, seed):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lo, hi + 1, size=n)
+    return [rng.integers(0, vocab, size=int(k)).tolist() for k in lens]
+
+
+def run_batch_vs_solo(gm, vocab, prompts, steps, max_tokens, flags=rd.DET_COMMIT_ALL, solo_flags=0, live=None):
+    """Prefills each prompt twice, then decodes one copy per sequence in
+    batches and the other alone; live(step) selects the batch members."""
+    batch = [gm.session(max_tokens) for _ in prompts]
+    solo = [gm.session(max_tokens) for _ in prompts]
+    tok_b = [s.prefill(p).next_token for s, p in zip(batch, prompts)]
+    tok_s = [s.prefill(p).next_token for s, p in zip(solo, prompts)]
+    assert tok_b == tok_s
+    for step in range(steps):
+        members = live(step) if live else list(range(len(prompts)))
+        res = rd.decode_batch([batch[i] for i in members], [tok_b[i] for i in members], flags)
+        for i, r in zip(members, res):
+            e = solo[i].decode(tok_s[i], flags | solo_flags)
+            assert key(r) == key(e), (step, i)
+            tok_b[i], tok_s[i] = r.next_token, e.next_token
+    for b, s in zip(batch, solo):
+        assert b.position() == s.position()
+        assert np.array_equal(b.logits(vocab), s.logits(vocab))
+
+
+def sharing_model(ctx):
+    """KV-sharing donors, k_eq_v full layers, sliding rings, softcap, layer scalars."""
+    cfg = {"text_config": {
+        "enable_moe_block": False, "head_dim": 64, "hidden_activation": "gelu_pytorch_tanh", "hidden_size": 256,
+        "intermediate_size": 512, "layer_types": ["sliding_attention", "full_attention", "sliding_attention",
+                                                  "full_attention"],
+        "num_attention_heads": 4, "num_hidden_layers": 4, "num_key_value_heads": 2, "num_global_key_value_heads": 1,
+        "attention_k_eq_v": True, "num_kv_shared_layers": 2, "final_logit_softcapping": 30.0,
+        "rope_parameters": {"full_attention": {"partial_rotary_factor": 0.5, "rope_theta": 5000.0},
+                            "sliding_attention": {"rope_theta": 10000.0}},
+        "rms_norm_eps": 1e-6, "sliding_window": 5, "tie_word_embeddings": False, "vocab_size": 1000,
+    }}
+    tc = cfg["text_config"]
+    tensors = []
+    for name, v, s in fixtures.custom_model(cfg, seed=3, layer_scalars=True):
+        if (".self_attn.k_proj" in name or ".self_attn.v_proj" in name) and \
+                tc["layer_types"][int(name.split(".layers.")[1].split(".")[0])] == "full_attention":
+            v, s = v[:64], s[:64]
+        tensors.append((name, v, s))
+    return build(ctx, cfg, tensors)
+
+
+def test_tiny_gemma_dev_batch_matches_solo(ctx):
+    cfg, blob = fixtures.tiny_gemma_dev()
+    gm = rd.Model(ctx, cfg).load_detwgt(blob).finalize()
+    vocab = cfg["text_config"]["vocab_size"]
+    prompts = ragged_prompts(6, 1, 12, vocab, seed=1)
+    run_batch_vs_solo(gm, vocab, prompts, steps=5, max_tokens=32)
+
+
+@pytest.mark.parametrize("n", [1, 3, 5, 16, 19])
+def test_sharing_model_batch_matches_solo(ctx, n):
+    # n >= 16 takes the slab GEMM for every projection, fewer rows the GEMV
+    gm = sharing_model(ctx)
+    prompts = ragged_prompts(n, 1, 14, 1000, seed=n)
+    run_batch_vs_solo(gm, 1000, prompts, steps=4, max_tokens=24, solo_flags=rd.DET_DECODE_PER_OP)
+
+
+def test_batch_matches_fused_solo_with_changing_membership(ctx):
+    # sequences join and leave the batch; the solo side uses the fused graph step
+    gm = sharing_model(ctx)
+    prompts = ragged_prompts(7, 2, 16, 1000, seed=9)
+    live = lambda step: [i for i in range(7) if (i + step) % 3 != 0]  # noqa: E731
+    run_batch_vs_solo(gm, 1000, prompts, steps=6, max_tokens=32, live=live)
+
+
+def test_e4b_shaped_layers_batch_of_16_matches_solo(ctx):
+    cfg = synthetic.e4b_config(layers=2, vocab=4096, sliding_window=8)
+    gm = build(ctx, cfg, synthetic.synthetic_model_fast(cfg, seed=7))
+    prompts = ragged_prompts(16, 1, 40, 4096, seed=5)
+    run_batch_vs_solo(gm, 4096, prompts, steps=3, max_tokens=48)
+
+
+def test_batch_rejects_bad_inputs_without_touching_state(ctx):
+    gm = sharing_model(ctx)
+    a, b, full = gm.session(8), gm.session(8), gm.session(4)
+    ta = a.prefill([1, 2, 3]).next_token
+    tb = b.prefill([4, 5]).next_token
+    tf = full.prefill([6, 7, 8, 9]).next_token
+    with pytest.raises(rd.DetError):
+        rd.decode_batch([a, a], [ta, ta])
+    with pytest.raises(rd.DetError):
+        rd.decode_batch([a, full], [ta, tf])  # full is at capacity
+    with pytest.raises(rd.DetError):
+        rd.decode_batch([a, b], [ta, 5000])  # token out of range
+    fresh = gm.session(8)
+    with pytest.raises(rd.DetError):
+        rd.decode_batch([a, fresh], [ta, 1])  # not prefilled
+    assert (a.position(), b.position(), full.position()) == (3, 2, 4)
+    # the failed calls left both sessions as they were
+    ref_a, ref_b = gm.session(8), gm.session(8)
+    ref_a.prefill([1, 2, 3])
+    ref_b.prefill([4, 5])
+    got = rd.decode_batch([a, b], [ta, tb])
+    assert key(got[0]) == key(ref_a.decode(ta))
+    assert key(got[1]) == key(ref_b.decode(tb))
