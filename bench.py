@@ -72,10 +72,9 @@ def cpu_baseline(problems, seconds: float, threads: int) -> dict:
     }
 
 
-def e4b_decode(ctx, rd, args) -> dict:
-    """E4B-shaped greedy decode (42 layers, hidden 2560, 8/2 heads x 256, FF 10240,
-    vocab 262144, alternating sliding/full): prefill a seeded uniform-random prompt,
-    then time greedy decode steps with the argmax token fed back each step."""
+def e4b_model(ctx, rd, args):
+    """E4B-shaped model (42 layers, hidden 2560, 8/2 heads x 256, FF 10240,
+    vocab 262144, alternating sliding/full) with counter-hash int8 weights."""
     from rasterdet import synthetic
 
     cfg = synthetic.e4b_config(layers=args.e4b_layers)
@@ -86,6 +85,12 @@ def e4b_decode(ctx, rd, args) -> dict:
     model.finalize()
     load_s = time.perf_counter() - t0
     log(f"[bench] E4B model resident in {load_s:.1f}s")
+    return model, load_s
+
+
+def e4b_decode(ctx, rd, args, model, load_s) -> dict:
+    """E4B-shaped greedy decode: prefill a seeded uniform-random prompt, then
+    time greedy decode steps with the argmax token fed back each step."""
     rng = np.random.default_rng(args.seed)
     prompt = rng.integers(0, 262144, size=args.prompt_len).tolist()
     steps = args.decode_steps
@@ -128,6 +133,54 @@ def e4b_decode(ctx, rd, args) -> dict:
                 "load_s": round(load_s, 1), "repeat_run_tokens_identical": bool(same),
                 "weights": "counter-hash int8 q, row scales in [1,16]",
                 "commitments": "decode_tok_s: none; with_commitments: activation+logits SHA-256 per step"},
+    }
+
+
+def ragged_batch(ctx, rd, args, model) -> dict:
+    """E4B-shaped decode of several independent sequences with ragged prompt
+    lengths (seeded uniform in [32, 2048]): each prompt is prefilled on its
+    own, then every greedy step runs all sequences through one batched decode
+    call (projections over M = sequences, attention over each ragged cache).
+    Aggregate tok/s = sequences x steps / wall time of the decode steps."""
+    n, steps = args.ragged_seqs, args.ragged_steps
+    rng = np.random.default_rng(args.seed + 5)
+    lens = rng.integers(32, 2049, size=n)
+    prompts = [rng.integers(0, 262144, size=int(k)).tolist() for k in lens]
+    sess = [model.session(int(k) + steps + 1) for k in lens]
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    toks = [s.prefill(p, rd.DET_COMMIT_NONE).next_token for s, p in zip(sess, prompts)]
+    ctx.synchronize()
+    prefill_s = time.perf_counter() - t0
+    # solo copies of the shortest and longest sequence, to check the batch against
+    check = [int(np.argmin(lens)), int(np.argmax(lens))]
+    solo = {i: sess[i].clone() for i in check}
+    first = toks[:]
+    out = [[] for _ in range(n)]
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        res = rd.decode_batch(sess, toks, rd.DET_COMMIT_NONE)
+        toks = [r.next_token for r in res]
+        for i, t in enumerate(toks):
+            out[i].append(t)
+    ctx.synchronize()
+    dec_s = time.perf_counter() - t0
+    n_check = min(steps, 16)
+    same = True
+    for i, s in solo.items():
+        t = first[i]
+        for j in range(n_check):
+            t = s.decode(t, rd.DET_COMMIT_NONE).next_token
+            same &= t == out[i][j]
+    log(f"[bench] ragged x{n}: prefill {int(lens.sum())} tokens in {prefill_s * 1e3:.0f} ms, "
+        f"{steps} batched steps in {dec_s * 1e3:.0f} ms ({n * steps / dec_s:.1f} tok/s aggregate)")
+    return {
+        "aggregate_tok_s": round(n * steps / dec_s, 1),
+        "ms_per_batched_step": round(dec_s / steps * 1e3, 3),
+        "sequences": n, "steps": steps, "prompt_lens": [int(k) for k in lens],
+        "prefill_s": round(prefill_s, 3),
+        "solo_tokens_identical": bool(same),
+        "solo_check": f"shortest and longest sequence decoded alone for {n_check} steps",
     }
 
 
@@ -217,6 +270,10 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-e4b", action="store_true", help="skip the E4B-shaped decode tok/s measurement")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the ragged multi-sequence decode measurement")
+    ap.add_argument("--ragged-only", action="store_true", help="only the ragged multi-sequence decode measurement")
+    ap.add_argument("--ragged-seqs", type=int, default=16)
+    ap.add_argument("--ragged-steps", type=int, default=128)
     ap.add_argument("--e4b-layers", type=int, default=42)
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--prompt-len", type=int, default=512)
@@ -238,7 +295,11 @@ def main() -> int:
     if args.decode_profile:
         args.decode_steps = 32
         args.eager = True  # profiler kernel tracing of graph replays is not used
-        print(json.dumps(e4b_decode(ctx, rd, args)), flush=True)
+        print(json.dumps(e4b_decode(ctx, rd, args, *e4b_model(ctx, rd, args))), flush=True)
+        return 0
+    if args.ragged_only:
+        model, _ = e4b_model(ctx, rd, args)
+        print(json.dumps(ragged_batch(ctx, rd, args, model)), flush=True)
         return 0
     log("[bench] generating and uploading weights")
     problems, mats, copies = [], [], []
@@ -350,8 +411,12 @@ def main() -> int:
     }
     if not args.no_gemm:
         line["prefill_gemm"] = prefill_gemm(ctx, rd, args)
-    if not args.no_e4b:
-        line.update(e4b_decode(ctx, rd, args))
+    if not (args.no_e4b and args.no_ragged):
+        model, load_s = e4b_model(ctx, rd, args)
+        if not args.no_e4b:
+            line.update(e4b_decode(ctx, rd, args, model, load_s))
+        if not args.no_ragged:
+            line["ragged_batch"] = ragged_batch(ctx, rd, args, model)
     print(json.dumps(line), flush=True)
     return 0 if parity else 1
 

@@ -22,6 +22,13 @@ struct RopeTable {
   uint32_t pairs, offset;
 };
 
+// One sequence's cache of one layer in a batched step.
+struct DecSeqCache {
+  int32_t* k;
+  int32_t* v;
+  uint64_t cap;
+};
+
 // One decode step's attention for one layer: head norms, RoPE and KV append
 // of the fused projection rows, then scores, integer softmax and weighted sums.
 struct AttnDecArgs {
@@ -42,7 +49,14 @@ struct AttnDecArgs {
   uint32_t hd, nh, nkv;
   int32_t* scores;  // scratch [nh][max_rows]
   int64_t* acc;     // [nh][hd] wrapped weighted sums (requantized by the O projection)
-  int scores_in_lds;  // the weighted-sum kernel keeps G x cap scores in LDS
+  int scores_in_lds;  // the weighted-sum kernel keeps G x lds_stride scores in LDS
+  uint64_t lds_stride;  // LDS row stride of the kept scores (>= every window)
+  // Batched steps (grid z = sequence): caches[seq] replaces k, v and cap (cap
+  // above then only sizes the grid), and st, trig, qkv, scores and acc advance
+  // by one StepState and by the strides below per sequence.
+  const DecSeqCache* caches;
+  uint64_t trig_stride, qkv_stride, scores_stride, acc_stride;
+  uint32_t nseq;
 };
 
 // Limits of the fused decode kernels.
@@ -54,13 +68,16 @@ constexpr uint32_t kAttnWsumRows = 32;      // window rows per softmax / weighte
 
 // The normalised rows are written as int32 (normed) and as limb planes
 // (limbs, plane stride kpad) for the decode GEMV.
+// With nseq > 1, sequence i uses st[i] and rows i of x, dec_in and normed
+// (stride H) and limb planes 4i..4i+3 (stride kpad).
 void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, uint64_t H, int32_t* x, int32_t* dec_in,
-                      const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s);
+                      const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s,
+                      uint32_t nseq = 1);
 // x = add_sat(x, rmsnorm(requant(src), w_post)) [* scalar]; normed = rmsnorm(x, w_next);
 // src (wrapping Q32.32 accumulators) is cleared after use.
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
-                              uint64_t kpad, hipStream_t s);
+                              uint64_t kpad, hipStream_t s, uint32_t nseq = 1);
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s);
 // part 0: head norms, RoPE, KV append and scores; part 1: softmax + weighted sum
 void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s);
@@ -69,5 +86,16 @@ void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s);
 void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, const RopeTable* tables, uint32_t ntables,
                          uint32_t total_pairs, int32_t* trig, hipStream_t s);
 void launch_dec_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s);
+// Batched steps: the cos/sin pairs of every RoPE table at each sequence's
+// position st[i].position, into trig + i * 2 * total_pairs.
+void launch_dec_set_trig(const StepState* st, uint32_t nseq, const RopeTable* tables, uint32_t ntables,
+                         uint32_t total_pairs, int32_t* trig, hipStream_t s);
+// Requantizes the wrapped weighted sums acc[t][0..k) (row stride ld) of nseq
+// sequences into limb planes (token t: planes 4t..4t+3, stride kpad; zero
+// past k) for the O projection GEMV, and clears acc.
+void launch_dec_acc_limbs(int64_t* acc, uint64_t k, uint64_t ld, uint32_t nseq, int8_t* limbs, uint64_t kpad,
+                          hipStream_t s);
+// dst[i][0..w) = src[i * w ..] for i < n (device array of row pointers).
+void launch_copy_rows(const int32_t* src, uint64_t w, uint64_t n, int32_t* const* dst, hipStream_t s);
 
 }  // namespace det

@@ -67,7 +67,12 @@ __global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* 
                                                    uint64_t kpad) {
   __shared__ int64_t red[NT / 64];
   __shared__ int32_t bc;
-  const uint32_t tok = st->token;
+  const uint32_t seq = blockIdx.y;
+  x += uint64_t(seq) * H;
+  dec_in += uint64_t(seq) * H;
+  normed += uint64_t(seq) * H;
+  limbs += uint64_t(seq) * 4 * kpad;
+  const uint32_t tok = st[seq].token;
   int32_t v[EPT], w[EPT];
   int64_t ss = 0;
 #pragma unroll
@@ -103,6 +108,11 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
                                                            uint64_t kpad) {
   __shared__ int64_t red[NT / 64];
   __shared__ int32_t bc;
+  const uint32_t seq = blockIdx.y;
+  src += uint64_t(seq) * H;
+  x += uint64_t(seq) * H;
+  normed += uint64_t(seq) * H;
+  limbs += uint64_t(seq) * 4 * kpad;
   int32_t o[EPT], xv[EPT], wp[EPT], wn[EPT];
   int64_t ss = 0;
 #pragma unroll
@@ -196,6 +206,23 @@ __device__ __forceinline__ void norm_head_row(const int64_t* __restrict__ src, u
   }
 }
 
+// This workgroup's sequence view of a (possibly batched) launch: grid z picks
+// the sequence, its cache and its slices of the per-step buffers.
+__device__ __forceinline__ void seq_view(AttnDecArgs& a) {
+  const uint32_t seq = blockIdx.z;
+  a.st += seq;
+  a.trig += seq * a.trig_stride;
+  a.qkv += seq * a.qkv_stride;
+  a.scores += seq * a.scores_stride;
+  a.acc += seq * a.acc_stride;
+  if (a.caches) {
+    const DecSeqCache c = a.caches[seq];
+    a.k = c.k;
+    a.v = c.v;
+    a.cap = c.cap;
+  }
+}
+
 // Scores of every query head of one KV head over kAttnScoreRows window rows
 // (ops.rs:318-333: wrapping dot product, requantized), 512 threads. The
 // workgroup first builds the normalised, rotated queries of its heads in LDS
@@ -208,6 +235,7 @@ template <bool VEC>
 __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   __shared__ int32_t ql[kDecMaxGroup * kDecMaxHeadDim];
   __shared__ int32_t kn[kDecMaxHeadDim];
+  seq_view(a);
   const Window win = attn_window(a);
   const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
   const uint64_t r0 = uint64_t(blockIdx.y) * kAttnScoreRows;
@@ -344,6 +372,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
   __shared__ int64_t el[kDecMaxGroup][kAttnWsumRows];
   __shared__ int32_t wl[kDecMaxGroup][kAttnWsumRows];
   __shared__ int64_t part[3][1024];
+  seq_view(a);
   const Window win = attn_window(a);
   const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
   if (blockIdx.y == 0) {
@@ -375,7 +404,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
   const bool active = g < G;
   const uint64_t stride = 64 * uint64_t(wph);
   const int32_t* scg = a.scores + (uint64_t(kvh) * G + (active ? g : 0)) * a.max_rows;
-  int32_t* scl = a.scores_in_lds ? sl_dyn + uint64_t(active ? g : 0) * a.cap : nullptr;
+  int32_t* scl = a.scores_in_lds ? sl_dyn + uint64_t(active ? g : 0) * a.lds_stride : nullptr;
   // argmax (and the LDS copy of this thread's scores)
   int64_t best = INT64_MIN;
   if (active)
@@ -524,6 +553,61 @@ __global__ __launch_bounds__(256) void k_dec_set_step(StepState* __restrict__ st
   }
 }
 
+// Batched form: positions from st[seq] (grid y = sequence).
+__global__ __launch_bounds__(256) void k_dec_set_trig(const StepState* __restrict__ st,
+                                                      const RopeTable* __restrict__ tables, uint32_t ntables,
+                                                      uint32_t total_pairs, int32_t* __restrict__ trig) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= total_pairs) return;
+  const uint64_t position = st[blockIdx.y].position;
+  trig += uint64_t(blockIdx.y) * 2 * total_pairs;
+  for (uint32_t t = 0; t < ntables; ++t) {
+    const RopeTable tb = tables[t];
+    if (i >= tb.offset && i < tb.offset + tb.pairs) {
+      int32_t c, s;
+      sin_cos(rope_angle(position, tb.inv_freq[i - tb.offset]), &c, &s);
+      trig[2 * uint64_t(i)] = c;
+      trig[2 * uint64_t(i) + 1] = s;
+    }
+  }
+}
+
+// Weighted-sum accumulators of one sequence (grid y) to the O projection's
+// limb planes, 4 columns per thread; the accumulators are cleared for the
+// next step.
+__global__ __launch_bounds__(256) void k_dec_acc_limbs(int64_t* __restrict__ acc, uint64_t k, uint64_t ld,
+                                                       int8_t* __restrict__ limbs, uint64_t kpad) {
+  const uint64_t c0 = (uint64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (c0 >= kpad) return;
+  const uint64_t t = blockIdx.y;
+  int64_t* row = acc + t * ld;
+  uint32_t packed[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint64_t c = c0 + e;
+    if (c < k) {
+      const uint32_t u = uint32_t(requant(row[c])) ^ 0x00808080u;
+      row[c] = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) packed[j] |= ((u >> (8 * j)) & 0xffu) << (8 * e);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(limbs + (t * 4 + j) * kpad + c0) = packed[j];
+}
+
+__global__ void k_copy_rows(const int32_t* __restrict__ src, uint64_t w, int32_t* const* __restrict__ dst) {
+  const uint64_t c = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (c >= w) return;
+  const int32_t* s = src + uint64_t(blockIdx.y) * w;
+  int32_t* d = dst[blockIdx.y];
+  if (c + 4 <= w && (w & 3) == 0) {
+    *reinterpret_cast<int4*>(d + c) = *reinterpret_cast<const int4*>(s + c);
+  } else {
+    for (uint64_t e = c; e < w && e < c + 4; ++e) d[e] = s[e];
+  }
+}
+
 __global__ void k_dec_softcap(int32_t* __restrict__ x, uint64_t n, int32_t cap) {
   const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) x[i] = softcap_act(x[i], cap);
@@ -537,35 +621,37 @@ static inline unsigned nblk(uint64_t n, unsigned per) { return unsigned((n + per
 #define DET_ROW_DISPATCH(KERNEL, ...)                                                     \
   do {                                                                                    \
     if (H <= 2048)                                                                        \
-      hipLaunchKernelGGL((KERNEL<1024, 2>), dim3(1), dim3(1024), 0, s, __VA_ARGS__);      \
+      hipLaunchKernelGGL((KERNEL<1024, 2>), dim3(1, nseq), dim3(1024), 0, s, __VA_ARGS__); \
     else if (H <= 4096)                                                                   \
-      hipLaunchKernelGGL((KERNEL<1024, 4>), dim3(1), dim3(1024), 0, s, __VA_ARGS__);      \
+      hipLaunchKernelGGL((KERNEL<1024, 4>), dim3(1, nseq), dim3(1024), 0, s, __VA_ARGS__); \
     else if (H <= 8192)                                                                   \
-      hipLaunchKernelGGL((KERNEL<1024, 8>), dim3(1), dim3(1024), 0, s, __VA_ARGS__);      \
+      hipLaunchKernelGGL((KERNEL<1024, 8>), dim3(1, nseq), dim3(1024), 0, s, __VA_ARGS__); \
     else                                                                                  \
-      hipLaunchKernelGGL((KERNEL<1024, 15>), dim3(1), dim3(1024), 0, s, __VA_ARGS__);     \
+      hipLaunchKernelGGL((KERNEL<1024, 15>), dim3(1, nseq), dim3(1024), 0, s, __VA_ARGS__);\
   } while (0)
 void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, uint64_t H, int32_t* x, int32_t* dec_in,
-                      const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s) {
+                      const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s,
+                      uint32_t nseq) {
   DET_ROW_DISPATCH(k_dec_embed, E, st, scale, H, x, dec_in, w_in, eps, normed, limbs, kpad);
 }
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
-                              uint64_t kpad, hipStream_t s) {
+                              uint64_t kpad, hipStream_t s, uint32_t nseq) {
   DET_ROW_DISPATCH(k_dec_residual_norm, src, x, normed, w_post, int(has_scalar), scalar, w_next, H, eps, limbs, kpad);
 }
 #undef DET_ROW_DISPATCH
 void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
   // grids cover the cache capacity (every window fits in it); idle chunks exit
+  const uint32_t ns = a.nseq ? a.nseq : 1;
   if (part == 0) {
-    const dim3 grid(a.nkv, nblk(a.cap, kAttnScoreRows));
+    const dim3 grid(a.nkv, nblk(a.cap, kAttnScoreRows), ns);
     if (a.hd % 64 == 0)
       hipLaunchKernelGGL(k_dec_attn_scores<true>, grid, dim3(512), 0, s, a);
     else
       hipLaunchKernelGGL(k_dec_attn_scores<false>, grid, dim3(512), 0, s, a);
   } else {
-    const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.cap * 4 : 0;
-    hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows)), dim3(1024), lds, s, a);
+    const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.lds_stride * 4 : 0;
+    hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows), ns), dim3(1024), lds, s, a);
   }
 }
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s) {
@@ -579,6 +665,19 @@ void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, const
 }
 void launch_dec_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s) {
   hipLaunchKernelGGL(k_dec_softcap, dim3(nblk(n, 256)), dim3(256), 0, s, x, n, cap);
+}
+void launch_dec_set_trig(const StepState* st, uint32_t nseq, const RopeTable* tables, uint32_t ntables,
+                         uint32_t total_pairs, int32_t* trig, hipStream_t s) {
+  if (total_pairs && nseq)
+    hipLaunchKernelGGL(k_dec_set_trig, dim3(nblk(total_pairs, 256), nseq), dim3(256), 0, s, st, tables, ntables,
+                       total_pairs, trig);
+}
+void launch_dec_acc_limbs(int64_t* acc, uint64_t k, uint64_t ld, uint32_t nseq, int8_t* limbs, uint64_t kpad,
+                          hipStream_t s) {
+  if (nseq && kpad) hipLaunchKernelGGL(k_dec_acc_limbs, dim3(nblk(kpad / 4, 256), nseq), dim3(256), 0, s, acc, k, ld, limbs, kpad);
+}
+void launch_copy_rows(const int32_t* src, uint64_t w, uint64_t n, int32_t* const* dst, hipStream_t s) {
+  if (n && w) hipLaunchKernelGGL(k_copy_rows, dim3(nblk((w + 3) / 4, 256), unsigned(n)), dim3(256), 0, s, src, w, dst);
 }
 
 }  // namespace det

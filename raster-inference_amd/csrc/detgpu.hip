@@ -1190,10 +1190,37 @@ struct BatchWs {
   uint8_t* desc = nullptr;    // device: positions, per-layer windows and append targets
   uint8_t* desc_host = nullptr;  // pinned staging of desc
   size_t desc_bytes = 0;
+  // fused batched step: per-sequence rows of the fused decode buffers
+  bool fused = false;
+  uint64_t grid_cap = 0;  // cache rows the captured attention grids cover
+  uint64_t qkv_stride = 0, attn_stride = 0, ff_stride = 0, score_heads = 0;
+  int32_t *x = nullptr, *normed = nullptr, *trig = nullptr, *hbuf = nullptr, *scores = nullptr;
+  int64_t *qkv_acc = nullptr, *attn_acc = nullptr, *o_acc = nullptr, *ff_acc = nullptr;
+  int8_t *limbs_x = nullptr, *limbs_o = nullptr, *limbs_ff = nullptr;
+  std::vector<void*> owned;
+  uint32_t graph_n = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  void drop_graph() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    exec = nullptr;
+    graph = nullptr;
+    graph_n = 0;
+  }
+  template <class T>
+  T* alloc(uint64_t n) {
+    void* p = nullptr;
+    HIPC(hipMalloc(&p, std::max<uint64_t>(n, 1) * sizeof(T)));
+    owned.push_back(p);
+    return static_cast<T*>(p);
+  }
   ~BatchWs() {
+    drop_graph();
     for (void* p : {static_cast<void*>(logits), static_cast<void*>(dec_in), static_cast<void*>(next),
-                    static_cast<void*>(desc)})
+                    static_cast<void*>(desc), static_cast<void*>(scores)})
       if (p) (void)hipFree(p);
+    for (void* p : owned) (void)hipFree(p);
     if (desc_host) (void)hipHostFree(desc_host);
   }
 };
@@ -1212,6 +1239,17 @@ struct BatchDesc {
   }
 };
 
+// Per-step descriptor block of the fused batched step for n sequences and L
+// layers: StepState[n] | DecSeqCache[L][n] | logits row pointers int32*[n].
+struct FusedDesc {
+  size_t st = 0, caches = 0, logit_dst = 0, bytes = 0;
+  FusedDesc(uint64_t n, uint64_t L) {
+    caches = st + sizeof(det::StepState) * n;
+    logit_dst = caches + sizeof(det::DecSeqCache) * L * n;
+    bytes = logit_dst + sizeof(int32_t*) * n;
+  }
+};
+
 BatchWs& ensure_batch(det_model* m, uint64_t n) {
   if (m->batch && m->batch->cap >= n) return *m->batch;
   HIPC(hipStreamSynchronize(m->ctx->stream));
@@ -1226,7 +1264,7 @@ BatchWs& ensure_batch(det_model* m, uint64_t n) {
   HIPC(hipMalloc(&b->logits, b->cap * m->vocab * 4));
   HIPC(hipMalloc(&b->dec_in, b->cap * m->hidden * 4));
   HIPC(hipMalloc(&b->next, b->cap * 4));
-  b->desc_bytes = BatchDesc(b->cap, m->layers.size()).bytes;
+  b->desc_bytes = std::max(BatchDesc(b->cap, m->layers.size()).bytes, FusedDesc(b->cap, m->layers.size()).bytes);
   HIPC(hipMalloc(&b->desc, b->desc_bytes));
   HIPC(hipHostMalloc(reinterpret_cast<void**>(&b->desc_host), b->desc_bytes, hipHostMallocDefault));
   m->batch = b.release();
@@ -1363,6 +1401,209 @@ void decode_batch(det_session* const* ss, uint64_t n, const uint32_t* tokens, ui
   }
 }
 
+// Buffers of the fused batched step for b.cap sequences; the attention
+// grids and score rows cover caches of up to `need` rows (grown on demand,
+// which drops the captured graph).
+void ensure_fused_batch(det_model* m, BatchWs& b, uint64_t need) {
+  const uint64_t T = b.cap, H = m->hidden;
+  if (!b.fused) {
+    uint64_t fr = 0, nhd = 0, ff = 0, kpo = 0, kff = 0, nh = 0;
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+      const GLayer& L = m->layers[l];
+      fr = std::max(fr, m->fused[l].qkv.rows);
+      nhd = std::max(nhd, L.num_heads * L.head_dim);
+      ff = std::max(ff, L.gate->rows);
+      kpo = std::max(kpo, L.o->kpad);
+      kff = std::max(kff, L.down->kpad);
+      nh = std::max(nh, L.num_heads);
+    }
+    b.qkv_stride = fr;
+    b.attn_stride = nhd;
+    b.ff_stride = ff;
+    b.score_heads = nh;
+    b.x = b.alloc<int32_t>(T * H);
+    b.normed = b.alloc<int32_t>(T * H);
+    b.trig = b.alloc<int32_t>(T * 2 * uint64_t(std::max<uint32_t>(m->trig_pairs, 1)));
+    b.hbuf = b.alloc<int32_t>(T * ff);
+    b.qkv_acc = b.alloc<int64_t>(T * fr);
+    b.attn_acc = b.alloc<int64_t>(T * nhd);
+    b.o_acc = b.alloc<int64_t>(T * H);
+    b.ff_acc = b.alloc<int64_t>(T * H);
+    b.limbs_x = b.alloc<int8_t>(T * 4 * m->fused[0].qkv.kpad);
+    b.limbs_o = b.alloc<int8_t>(T * 4 * kpo);
+    b.limbs_ff = b.alloc<int8_t>(T * 4 * kff);
+    // every accumulator is cleared by the kernel that consumes it, so they
+    // only need to start at zero (stream-ordered, outside any graph)
+    hipStream_t zst = m->ctx->stream;
+    HIPC(hipMemsetAsync(b.qkv_acc, 0, T * fr * 8, zst));
+    HIPC(hipMemsetAsync(b.attn_acc, 0, T * nhd * 8, zst));
+    HIPC(hipMemsetAsync(b.o_acc, 0, T * H * 8, zst));
+    HIPC(hipMemsetAsync(b.ff_acc, 0, T * H * 8, zst));
+    HIPC(hipMemsetAsync(b.limbs_o, 0, T * 4 * kpo, zst));
+    HIPC(hipMemsetAsync(b.limbs_ff, 0, T * 4 * kff, zst));
+    HIPC(hipMemsetAsync(b.limbs_x, 0, T * 4 * m->fused[0].qkv.kpad, zst));
+    b.fused = true;
+  }
+  if (need > b.grid_cap) {
+    const uint64_t rows = (need + 255) / 256 * 256;
+    HIPC(hipStreamSynchronize(m->ctx->stream));
+    b.drop_graph();
+    if (b.scores) HIPC(hipFree(b.scores));
+    b.scores = nullptr;
+    HIPC(hipMalloc(&b.scores, T * b.score_heads * rows * 4));
+    b.grid_cap = rows;
+  }
+}
+
+// Attention arguments of layer l for a batched step of n sequences.
+det::AttnDecArgs batch_attn_args(det_model* m, BatchWs& b, size_t l, uint32_t n) {
+  const GLayer& L = m->layers[l];
+  const auto& F = m->fused[l];
+  const FusedDesc D(n, m->layers.size());
+  det::AttnDecArgs a{};
+  a.qkv = b.qkv_acc;
+  a.q_norm = L.q_norm;
+  a.k_norm = L.k_norm;
+  a.trig = b.trig + 2 * uint64_t(L.trig_off);
+  a.eps = L.eps;
+  a.rotary = L.rotary;
+  a.has_v = F.has_v;
+  a.own_cache = !L.donor;
+  a.st = reinterpret_cast<const det::StepState*>(b.desc + D.st);
+  const size_t src = L.donor ? *L.donor : l;
+  const bool ring = m->layers[src].cache_sliding_window.has_value();
+  // ring caches hold at most the cache window; linear ones the session length
+  a.cap = ring ? std::min<uint64_t>(std::max<uint64_t>(*m->layers[src].cache_sliding_window, 1), b.grid_cap) : b.grid_cap;
+  a.window = L.sliding ? *L.sliding_window : 0;
+  a.max_rows = b.grid_cap;
+  a.ring = ring;
+  a.hd = uint32_t(L.head_dim);
+  a.nh = uint32_t(L.num_heads);
+  a.nkv = uint32_t(L.num_kv_heads);
+  a.scores = b.scores;
+  a.acc = b.attn_acc;
+  a.lds_stride = a.cap;
+  a.scores_in_lds = (L.num_heads / L.num_kv_heads) * a.cap * 4 <= 32768;
+  a.caches = reinterpret_cast<const det::DecSeqCache*>(b.desc + D.caches) + l * n;
+  a.trig_stride = 2 * uint64_t(std::max<uint32_t>(m->trig_pairs, 1));
+  a.qkv_stride = b.qkv_stride;
+  a.scores_stride = b.score_heads * b.grid_cap;
+  a.acc_stride = b.attn_stride;
+  a.nseq = n;
+  return a;
+}
+
+// One fused decode step for n sequences: the single-sequence fused step with
+// every kernel over the n rows (GEMVs with up to 16 tokens per weight pass).
+void enqueue_fused_batch(det_model* m, BatchWs& b, uint32_t n) {
+  hipStream_t st = m->ctx->stream;
+  const uint64_t H = m->hidden, V = m->vocab;
+  const FusedDesc D(n, m->layers.size());
+  const auto* st_dev = reinterpret_cast<const det::StepState*>(b.desc + D.st);
+  const uint64_t kpad_x = m->fused[0].qkv.kpad;
+  det::launch_dec_set_trig(st_dev, n, m->rope_tables_dev, uint32_t(m->rope_tables.size()), m->trig_pairs, b.trig, st);
+  det::launch_dec_embed(*m->embedding, st_dev, m->embed_scale, H, b.x, b.dec_in, m->layers[0].in_ln, m->eps, b.normed,
+                        b.limbs_x, kpad_x, st, n);
+  for (size_t l = 0; l < m->layers.size(); ++l) {
+    const GLayer& L = m->layers[l];
+    const auto& F = m->fused[l];
+    det::launch_gemv_dec_batch(F.qkv, b.limbs_x, n, nullptr, 0, b.qkv_acc, b.qkv_stride, 0, nullptr, 0, st);
+    det::launch_dec_attention(batch_attn_args(m, b, l, n), st);
+    det::launch_dec_acc_limbs(b.attn_acc, L.num_heads * L.head_dim, b.attn_stride, n, b.limbs_o, L.o->kpad, st);
+    det::launch_gemv_dec_batch(*L.o, b.limbs_o, n, nullptr, 0, b.o_acc, H, 0, nullptr, 0, st);
+    det::launch_dec_residual_norm(b.o_acc, b.x, b.normed, L.post_attn_ln, false, 0, L.pre_ff_ln, H, L.eps, b.limbs_x,
+                                  kpad_x, st, n);
+    det::launch_gemv_dec_batch(F.gateup, b.limbs_x, n, b.hbuf, b.ff_stride, nullptr, 0, 1, b.limbs_ff, L.down->kpad, st);
+    det::launch_gemv_dec_batch(*L.down, b.limbs_ff, n, nullptr, 0, b.ff_acc, H, 0, nullptr, 0, st);
+    const int32_t* w_next = l + 1 < m->layers.size() ? m->layers[l + 1].in_ln : m->final_norm;
+    det::launch_dec_residual_norm(b.ff_acc, b.x, b.normed, L.post_ff_ln, L.layer_scalar.has_value(),
+                                  L.layer_scalar.value_or(0), w_next, H, L.eps, b.limbs_x, kpad_x, st, n);
+  }
+  det::launch_gemv_dec_batch(*m->lm_head, b.limbs_x, n, b.logits, V, nullptr, 0, 0, nullptr, 0, st);
+  if (m->softcap) det::launch_dec_softcap(b.logits, n * V, *m->softcap, st);
+  det::launch_copy_rows(b.logits, V, n, reinterpret_cast<int32_t* const*>(b.desc + D.logit_dst), st);
+  det::launch_argmax_rows(b.logits, n, V, b.next, st);
+}
+
+void decode_batch_fused(det_session* const* ss, uint64_t n, const uint32_t* tokens, uint32_t flags,
+                        det_decode_result_t* out) {
+  check_batch(ss, n, tokens);
+  det_model* m = ss[0]->m;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  const uint64_t H = m->hidden, V = m->vocab, nl = m->layers.size();
+  BatchWs& b = ensure_batch(m, n);
+  uint64_t need = 1;
+  for (uint64_t i = 0; i < n; ++i) need = std::max(need, ss[i]->max_tokens);
+  ensure_fused_batch(m, b, need);
+  const FusedDesc D(n, nl);
+  uint8_t* hb = b.desc_host;
+  auto* sts = reinterpret_cast<det::StepState*>(hb + D.st);
+  auto* caches = reinterpret_cast<det::DecSeqCache*>(hb + D.caches);
+  auto* dst = reinterpret_cast<int32_t**>(hb + D.logit_dst);
+  for (uint64_t i = 0; i < n; ++i) {
+    det_session* s = ss[i];
+    sts[i].position = s->position;
+    sts[i].token = tokens[i];
+    sts[i].pad = 0;
+    dst[i] = s->logits;
+    for (size_t l = 0; l < nl; ++l) {
+      const GLayer& L = m->layers[l];
+      const GKv& c = L.donor ? s->kv[*L.donor] : s->kv[l];
+      if (L.donor && !c.has) bail("deterministic attention requires canonical key cache rows");
+      if (c.row_w != L.num_kv_heads * L.head_dim) bail("layer cache head count mismatch");
+      caches[l * n + i] = det::DecSeqCache{c.k, c.v, c.cap};
+    }
+  }
+  HIPC(hipMemcpyAsync(b.desc, hb, D.bytes, hipMemcpyHostToDevice, st));
+  const bool eager = flags & DET_DECODE_EAGER;
+  if (eager) {
+    enqueue_fused_batch(m, b, uint32_t(n));
+  } else {
+    if (!b.exec || b.graph_n != n) {
+      b.drop_graph();
+      HIPC(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+      try {
+        enqueue_fused_batch(m, b, uint32_t(n));
+      } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(st, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      HIPC(hipStreamEndCapture(st, &b.graph));
+      HIPC(hipGraphInstantiate(&b.exec, b.graph, nullptr, nullptr, 0));
+      b.graph_n = uint32_t(n);
+    }
+    HIPC(hipGraphLaunch(b.exec, st));
+  }
+  std::vector<uint32_t> next(n);
+  HIPC(hipMemcpyAsync(next.data(), b.next, n * 4, hipMemcpyDeviceToHost, st));
+  HIPC(hipStreamSynchronize(st));
+  for (uint64_t i = 0; i < n; ++i) {
+    det_session* s = ss[i];
+    for (size_t l = 0; l < nl; ++l)
+      if (!m->layers[l].donor) kv_advance(s->kv[l], s->position + 1);
+    s->position += 1;
+    s->logits_valid = true;
+  }
+  if (flags & DET_COMMIT_ACTIVATIONS) {
+    std::vector<int32_t> hx(n * H), lg(n * V);
+    HIPC(hipMemcpyAsync(hx.data(), b.x, n * H * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipMemcpyAsync(lg.data(), b.logits, n * V * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    for (uint64_t i = 0; i < n; ++i) {
+      commit_rows(hx.data() + i * H, 1, H, out[i].activation);
+      commit_vector(lg.data() + i * V, V, out[i].logits);
+    }
+  }
+  for (uint64_t i = 0; i < n; ++i) {
+    out[i].kv[0] = 0;
+    if (flags & DET_COMMIT_KV) commit_kv(ss[i], all_caches(ss[i]), out[i].kv);
+    out[i].next_token = next[i];
+  }
+}
+
 // Attention arguments of layer l for the fused decode step.
 det::AttnDecArgs attn_args(det_session* s, size_t l) {
   det_model* m = s->m;
@@ -1391,6 +1632,7 @@ det::AttnDecArgs attn_args(det_session* s, size_t l) {
   a.scores = s->scores;
   a.acc = s->attn_acc;
   a.scores_in_lds = (L.num_heads / L.num_kv_heads) * ac.cap * 4 <= 32768;
+  a.lds_stride = ac.cap;
   return a;
 }
 
@@ -1838,7 +2080,10 @@ int det_session_decode_batch(det_session_t* const* sessions, uint64_t n, const u
   }
   return guarded(sessions[0]->m->ctx, [&] {
     std::vector<det_decode_result_t> tmp(out ? 0 : n);
-    decode_batch(sessions, n, tokens, flags, out ? out : tmp.data());
+    if (sessions[0]->m->fused_ok && !(flags & DET_DECODE_PER_OP))
+      decode_batch_fused(sessions, n, tokens, flags, out ? out : tmp.data());
+    else
+      decode_batch(sessions, n, tokens, flags, out ? out : tmp.data());
   });
 }
 int det_session_logits(det_session_t* s, int32_t* out, uint64_t n) {

@@ -76,6 +76,12 @@ void launch_gemv_decode_acc(const DevMatrix& W, const void* act, bool act_i64, i
 // (stride out_kpad) to out_limbs.
 void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int64_t* acc, int epilogue,
                      int8_t* out_limbs, uint64_t out_kpad, hipStream_t s);
+// The same for ntok activation rows (token t: limb planes 4t..4t+3), every
+// weight tile serving up to 16 tokens; token t's outputs go to
+// out + t * out_ld, acc + t * acc_ld and planes 4t..4t+3 of out_limbs.
+void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
+                           int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
+                           hipStream_t s);
 
 void launch_rmsnorm(int32_t* x, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
                     int64_t eps, hipStream_t s);

@@ -278,23 +278,31 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
   }
 }
 
-// Decode GEMV (one activation row) reading the activation as four limb planes
-// in global memory (plane j, column c: byte j of a_c ^ 0x00808080; zero past
-// k), so no workgroup prologue: the A operand loads issue with the weight
-// loads and hit L2. 256 threads = 4 waves; KS waves split a tile's K range
-// (4/KS tiles per workgroup and pass); kchunks splits K across workgroups.
-// Outputs: acc_out != null: wrapping Q32.32 partial sums added atomically
-// (acc_out zero on entry); else EPI 0: out = requant; EPI 1: interleaved
-// gate/up tiles, out[f] = mul_sat(gelu(gate_f), up_f), also written as limb
-// planes to out_limbs (plane stride out_kpad) for the next GEMV.
-template <int KS, int EPI>
-__global__ __launch_bounds__(256, 5) void k_gemv_dec(const int8_t* __restrict__ q, const int32_t* __restrict__ scale,
-                                                  const int32_t* __restrict__ rowsum, const int8_t* __restrict__ limbs,
-                                                  uint64_t n_rows, uint64_t kpad, uint32_t kchunks,
-                                                  int32_t* __restrict__ out, int64_t* __restrict__ acc_out,
-                                                  int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
-  __shared__ v4i part[KS > 1 ? 4 : 1][64];
+// Decode GEMV reading the activations as limb planes in global memory (token
+// t, limb j: plane 4t + j, stride kpad; byte c is byte j of a_c ^ 0x00808080,
+// zero past k), so no workgroup prologue: the A operand loads issue with the
+// weight loads and hit L2. NG groups of 4 tokens (one 16-row MFMA A tile
+// each: row i = limb i % 4 of token 4 tg + i / 4) share every weight tile, so
+// up to 4 NG sequences decode for one pass over the weights; tokens >= ntok
+// are zero rows. 256 threads = 4 waves; KS waves split a tile's K range (4/KS
+// tiles per workgroup and pass); kchunks splits K across workgroups.
+// Outputs (token t): acc_out != null: wrapping Q32.32 partial sums added
+// atomically to acc_out[t * acc_ld + row] (zero on entry); else EPI 0:
+// out[t * out_ld + row] = requant; EPI 1: interleaved gate/up tiles,
+// out[t * out_ld + f] = mul_sat(gelu(gate_f), up_f), also written as limb
+// planes 4t..4t+3 of out_limbs (plane stride out_kpad) for the next GEMV.
+template <int KS, int EPI, int NG>
+__global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_dec(
+    const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
+    const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
+    int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
+    int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
+  __shared__ v4i part[KS > 1 ? 4 : 1][NG][64];
   constexpr int TPW = 4 / KS;
+  // K steps per load batch: three for one token group (a wave's 5-step share
+  // of K 2560 split four ways takes two load round trips either way), two when
+  // the A tiles of several groups share the registers
+  constexpr int D = NG == 1 ? 3 : 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
   const int slot = wave / KS, kp = wave % KS;
@@ -306,9 +314,13 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec(const int8_t* __restrict__ 
   const uint64_t per = (cs1 - cs0 + KS - 1) / KS;
   const uint64_t s0 = cs0 + kp * per < cs1 ? cs0 + kp * per : cs1;
   const uint64_t s1 = s0 + per < cs1 ? s0 + per : cs1;
-  // A rows 0-3 are the four limbs of the single activation row; rows 4-15 are zero
-  const bool a_on = i < 4;
-  const v4i* ap = reinterpret_cast<const v4i*>(limbs + (a_on ? uint64_t(i) * kpad : 0) + 32 * g);
+  const v4i* ap[NG];
+  bool a_on[NG];
+#pragma unroll
+  for (int tg = 0; tg < NG; ++tg) {
+    a_on[tg] = uint32_t(4 * tg + (i >> 2)) < ntok;
+    ap[tg] = reinterpret_cast<const v4i*>(limbs + (a_on[tg] ? uint64_t(16 * tg + i) * kpad : 0) + 32 * g);
+  }
   const uint64_t ntiles = (n_rows + 15) / 16;
   const uint64_t groups = gridDim.x / kchunks;
   const v4i zero = {0, 0, 0, 0};
@@ -317,64 +329,87 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec(const int8_t* __restrict__ 
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles;
     const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 32);
-    v4i acc = zero;
-    uint64_t s = s0;
-    // three K steps per batch: a wave's 5-step share (K 2560 split four ways)
-    // takes two load round trips either way, with 16 fewer registers than 4
-    for (; s + 3 <= s1; s += 3) {
-      v4i b[6], a[6];
+    v4i acc[NG];
 #pragma unroll
-      for (int u = 0; u < 3; ++u) {
+    for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
+    uint64_t s = s0;
+    for (; s + D <= s1; s += D) {
+      v4i b[2 * D], a[NG][2 * D];
+#pragma unroll
+      for (int u = 0; u < D; ++u) {
         b[2 * u] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128) : zero;
         b[2 * u + 1] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128 + 1) : zero;
-        a[2 * u] = a_on ? ap[(s + u) * 8] : zero;
-        a[2 * u + 1] = a_on ? ap[(s + u) * 8 + 1] : zero;
+#pragma unroll
+        for (int tg = 0; tg < NG; ++tg) {
+          a[tg][2 * u] = a_on[tg] ? ap[tg][(s + u) * 8] : zero;
+          a[tg][2 * u + 1] = a_on[tg] ? ap[tg][(s + u) * 8 + 1] : zero;
+        }
       }
 #pragma unroll
-      for (int u = 0; u < 6; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+      for (int u = 0; u < 2 * D; ++u)
+#pragma unroll
+        for (int tg = 0; tg < NG; ++tg) acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[tg][u], b[u], acc[tg], 0, 0, 0);
     }
     for (; s < s1; ++s) {
       const v4i b0 = t_on ? __builtin_nontemporal_load(bp + s * 128) : zero;
       const v4i b1 = t_on ? __builtin_nontemporal_load(bp + s * 128 + 1) : zero;
-      const v4i a0 = a_on ? ap[s * 8] : zero;
-      const v4i a1 = a_on ? ap[s * 8 + 1] : zero;
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+#pragma unroll
+      for (int tg = 0; tg < NG; ++tg) {
+        const v4i a0 = a_on[tg] ? ap[tg][s * 8] : zero;
+        const v4i a1 = a_on[tg] ? ap[tg][s * 8 + 1] : zero;
+        acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc[tg], 0, 0, 0);
+        acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc[tg], 0, 0, 0);
+      }
     }
-    int64_t p[4] = {acc[0], acc[1], acc[2], acc[3]};
+    int64_t p[NG][4];
+#pragma unroll
+    for (int tg = 0; tg < NG; ++tg)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) p[tg][e] = acc[tg][e];
     if (KS > 1) {
-      part[wave][lane] = acc;
+#pragma unroll
+      for (int tg = 0; tg < NG; ++tg) part[wave][tg][lane] = acc[tg];
       __syncthreads();
       if (kp == 0) {
 #pragma unroll
-        for (int w = 1; w < KS; ++w) {
-          const v4i v = part[wave + w][lane];
-          p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
-        }
+        for (int w = 1; w < KS; ++w)
+#pragma unroll
+          for (int tg = 0; tg < NG; ++tg) {
+            const v4i v = part[wave + w][tg][lane];
+            p[tg][0] += v[0]; p[tg][1] += v[1]; p[tg][2] += v[2]; p[tg][3] += v[3];
+          }
       }
       __syncthreads();
     }
     if (kp != 0 || !t_on) continue;
-    // lanes g == 0 hold the limb sums of the activation row (token 0)
-    const bool ok = g == 0 && row < n_rows;
-    if (acc_out) {
-      if (ok) {
-        const int64_t a = limb_combine(p, kc == 0 ? rowsum[row] : 0, scale[row]);
-        atomicAdd(reinterpret_cast<unsigned long long*>(acc_out + row), static_cast<unsigned long long>(a));
-      }
-    } else if (EPI == 1) {
-      const int32_t r = ok ? requant(limb_combine(p, rowsum[row], scale[row])) : 0;
-      const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
-      if (ok && i < 8) {
-        const uint64_t f = tile * 8 + i;
-        const int32_t h = mul_sat(gelu_act(r), up);
-        out[f] = h;
-        const uint32_t u = uint32_t(h) ^ 0x00808080u;
+    const bool r_on = row < n_rows;
+    const int32_t rs = r_on ? rowsum[row] : 0, sc = r_on ? scale[row] : 0;
+    // lane 16 g + i of group tg holds the limb sums of token 4 tg + g, row i
 #pragma unroll
-        for (int j = 0; j < 4; ++j) out_limbs[j * out_kpad + f] = int8_t(uint8_t(u >> (8 * j)));
+    for (int tg = 0; tg < NG; ++tg) {
+      const uint32_t tok = 4 * tg + g;
+      const bool ok = tok < ntok && r_on;
+      if (acc_out) {
+        if (ok) {
+          const int64_t a = limb_combine(p[tg], kc == 0 ? rs : 0, sc);
+          atomicAdd(reinterpret_cast<unsigned long long*>(acc_out + tok * acc_ld + row),
+                    static_cast<unsigned long long>(a));
+        }
+      } else if (EPI == 1) {
+        const int32_t r = ok ? requant(limb_combine(p[tg], rs, sc)) : 0;
+        const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
+        if (ok && i < 8) {
+          const uint64_t f = tile * 8 + i;
+          const int32_t h = mul_sat(gelu_act(r), up);
+          out[tok * out_ld + f] = h;
+          const uint32_t u = uint32_t(h) ^ 0x00808080u;
+          int8_t* ol = out_limbs + uint64_t(tok) * 4 * out_kpad + f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ol[j * out_kpad] = int8_t(uint8_t(u >> (8 * j)));
+        }
+      } else if (ok) {
+        out[tok * out_ld + row] = requant(limb_combine(p[tg], rs, sc));
       }
-    } else if (ok) {
-      out[row] = requant(limb_combine(p, rowsum[row], scale[row]));
     }
   }
 }
@@ -1067,17 +1102,20 @@ static uint64_t resident_blocks(const void* kernel, int threads) {
   return n;
 }
 
-template <int KS, int EPI>
-static void launch_gemv_dec_ks(const DevMatrix& W, const int8_t* limbs, uint32_t kc, uint64_t groups, int32_t* out,
-                               int64_t* acc, int8_t* out_limbs, uint64_t out_kpad, hipStream_t s) {
-  hipLaunchKernelGGL((k_gemv_dec<KS, EPI>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum, limbs,
-                     W.rows, W.kpad, kc, out, acc, out_limbs, out_kpad);
+template <int KS, int EPI, int NG>
+static void launch_gemv_dec_ks(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, uint32_t kc, uint64_t groups,
+                               int32_t* out, uint64_t out_ld, int64_t* acc, uint64_t acc_ld, int8_t* out_limbs,
+                               uint64_t out_kpad, hipStream_t s) {
+  hipLaunchKernelGGL((k_gemv_dec<KS, EPI, NG>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,
+                     limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad);
 }
 
-void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int64_t* acc, int epilogue,
-                     int8_t* out_limbs, uint64_t out_kpad, hipStream_t s) {
+template <int NG>
+static void launch_gemv_dec_ng(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
+                               int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
+                               hipStream_t s) {
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
-  const uint64_t cap = resident_blocks(reinterpret_cast<const void*>(&k_gemv_dec<4, 0>), 256);
+  const uint64_t cap = resident_blocks(reinterpret_cast<const void*>(&k_gemv_dec<4, 0, NG>), 256);
   auto groups = [&](int ks) { return (ntiles * ks + 3) / 4; };
   // in-workgroup K split: smallest that fills the device, keeping >= 4 K steps per wave
   int ks = 1;
@@ -1087,15 +1125,36 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
   if (acc)
     while (groups(ks) * kc * 2 <= cap && nsteps >= uint64_t(ks) * kc * 2) kc *= 2;
   const uint64_t g = std::min<uint64_t>(groups(ks), std::max<uint64_t>(cap / kc, 1));
+#define DET_GEMV_DEC(KS, EPI) \
+  launch_gemv_dec_ks<KS, EPI, NG>(W, limbs, ntok, kc, g, out, out_ld, acc, acc_ld, out_limbs, out_kpad, s)
   if (epilogue == 1) {
-    if (ks == 4) launch_gemv_dec_ks<4, 1>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
-    else if (ks == 2) launch_gemv_dec_ks<2, 1>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
-    else launch_gemv_dec_ks<1, 1>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
+    if (ks == 4) DET_GEMV_DEC(4, 1); else if (ks == 2) DET_GEMV_DEC(2, 1); else DET_GEMV_DEC(1, 1);
   } else {
-    if (ks == 4) launch_gemv_dec_ks<4, 0>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
-    else if (ks == 2) launch_gemv_dec_ks<2, 0>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
-    else launch_gemv_dec_ks<1, 0>(W, limbs, kc, g, out, acc, out_limbs, out_kpad, s);
+    if (ks == 4) DET_GEMV_DEC(4, 0); else if (ks == 2) DET_GEMV_DEC(2, 0); else DET_GEMV_DEC(1, 0);
   }
+#undef DET_GEMV_DEC
+}
+
+void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
+                           int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
+                           hipStream_t s) {
+  if (W.rows == 0 || ntok == 0) return;
+  // up to 16 tokens per pass over the weights
+  for (uint32_t t0 = 0; t0 < ntok; t0 += 16) {
+    const uint32_t nt = ntok - t0 < 16 ? ntok - t0 : 16;
+    const int8_t* l = limbs + uint64_t(t0) * 4 * W.kpad;
+    int32_t* o = out ? out + uint64_t(t0) * out_ld : nullptr;
+    int64_t* a = acc ? acc + uint64_t(t0) * acc_ld : nullptr;
+    int8_t* ol = out_limbs ? out_limbs + uint64_t(t0) * 4 * out_kpad : nullptr;
+    if (nt <= 4) launch_gemv_dec_ng<1>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
+    else if (nt <= 8) launch_gemv_dec_ng<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
+    else launch_gemv_dec_ng<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
+  }
+}
+
+void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int64_t* acc, int epilogue,
+                     int8_t* out_limbs, uint64_t out_kpad, hipStream_t s) {
+  launch_gemv_dec_ng<1>(W, limbs, 1, out, 0, acc, 0, epilogue, out_limbs, out_kpad, s);
 }
 
 uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64 * 4 * kpad; }

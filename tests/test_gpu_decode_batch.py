@@ -91,12 +91,38 @@ def test_tiny_gemma_dev_batch_matches_solo(ctx):
     run_batch_vs_solo(gm, vocab, prompts, steps=5, max_tokens=32)
 
 
-@pytest.mark.parametrize("n", [1, 3, 5, 16, 19])
-def test_sharing_model_batch_matches_solo(ctx, n):
-    # n >= 16 takes the slab GEMM for every projection, fewer rows the GEMV
+MODES = {"graph": 0, "eager": rd.DET_DECODE_EAGER, "per_op": rd.DET_DECODE_PER_OP}
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+@pytest.mark.parametrize("n", [1, 3, 5, 8, 16, 19])
+def test_sharing_model_batch_matches_solo(ctx, n, mode):
+    # fused step: GEMVs with 1, 2 or 4 token groups (19 = one pass of 16 + one
+    # of 3); per-op step: n >= 16 takes the slab GEMM, fewer rows the GEMV
     gm = sharing_model(ctx)
     prompts = ragged_prompts(n, 1, 14, 1000, seed=n)
-    run_batch_vs_solo(gm, 1000, prompts, steps=4, max_tokens=24, solo_flags=rd.DET_DECODE_PER_OP)
+    run_batch_vs_solo(gm, 1000, prompts, steps=4, max_tokens=24, flags=rd.DET_COMMIT_ALL | MODES[mode],
+                      solo_flags=rd.DET_DECODE_PER_OP)
+
+
+def test_batch_with_longer_session_joining_later(ctx):
+    # a session with a larger cache joins: the batched attention grids grow and
+    # the captured step is rebuilt; windows wrap the rings of sliding layers
+    gm = sharing_model(ctx)
+    caps = [24, 24, 300, 24]
+    prompts = ragged_prompts(4, 3, 20, 1000, seed=21)
+    prompts[2] = ragged_prompts(1, 260, 260, 1000, seed=22)[0]
+    batch = [gm.session(c) for c in caps]
+    solo = [gm.session(c) for c in caps]
+    tb = [s.prefill(p).next_token for s, p in zip(batch, prompts)]
+    ts = [s.prefill(p).next_token for s, p in zip(solo, prompts)]
+    for step in range(5):
+        members = [0, 1, 3] if step < 2 else [0, 1, 2, 3]
+        res = rd.decode_batch([batch[i] for i in members], [tb[i] for i in members])
+        for i, r in zip(members, res):
+            e = solo[i].decode(ts[i])
+            assert key(r) == key(e), (step, i)
+            tb[i], ts[i] = r.next_token, e.next_token
 
 
 def test_batch_matches_fused_solo_with_changing_membership(ctx):
@@ -107,11 +133,12 @@ def test_batch_matches_fused_solo_with_changing_membership(ctx):
     run_batch_vs_solo(gm, 1000, prompts, steps=6, max_tokens=32, live=live)
 
 
-def test_e4b_shaped_layers_batch_of_16_matches_solo(ctx):
+@pytest.mark.parametrize("mode", ["graph", "per_op"])
+def test_e4b_shaped_layers_batch_of_16_matches_solo(ctx, mode):
     cfg = synthetic.e4b_config(layers=2, vocab=4096, sliding_window=8)
     gm = build(ctx, cfg, synthetic.synthetic_model_fast(cfg, seed=7))
     prompts = ragged_prompts(16, 1, 40, 4096, seed=5)
-    run_batch_vs_solo(gm, 4096, prompts, steps=3, max_tokens=48)
+    run_batch_vs_solo(gm, 4096, prompts, steps=3, max_tokens=48, flags=rd.DET_COMMIT_ALL | MODES[mode])
 
 
 def test_batch_rejects_bad_inputs_without_touching_state(ctx):
