@@ -158,8 +158,9 @@ def ragged_batch(ctx, rd, args, model) -> dict:
     first = toks[:]
     out = [[] for _ in range(n)]
     t0 = time.perf_counter()
+    extra = rd.DET_DECODE_EAGER if getattr(args, "eager", False) else 0
     for _ in range(steps):
-        res = rd.decode_batch(sess, toks, rd.DET_COMMIT_NONE)
+        res = rd.decode_batch(sess, toks, rd.DET_COMMIT_NONE | extra)
         toks = [r.next_token for r in res]
         for i, t in enumerate(toks):
             out[i].append(t)
@@ -170,7 +171,7 @@ def ragged_batch(ctx, rd, args, model) -> dict:
     for i, s in solo.items():
         t = first[i]
         for j in range(n_check):
-            t = s.decode(t, rd.DET_COMMIT_NONE).next_token
+            t = s.decode(t, rd.DET_COMMIT_NONE | extra).next_token
             same &= t == out[i][j]
     log(f"[bench] ragged x{n}: prefill {int(lens.sum())} tokens in {prefill_s * 1e3:.0f} ms, "
         f"{steps} batched steps in {dec_s * 1e3:.0f} ms ({n * steps / dec_s:.1f} tok/s aggregate)")
@@ -272,6 +273,8 @@ def main() -> int:
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     ap.add_argument("--no-ragged", action="store_true", help="skip the ragged multi-sequence decode measurement")
     ap.add_argument("--ragged-only", action="store_true", help="only the ragged multi-sequence decode measurement")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch decode kernels directly instead of replaying graphs (for kernel tracing)")
     ap.add_argument("--ragged-seqs", type=int, default=16)
     ap.add_argument("--ragged-steps", type=int, default=128)
     ap.add_argument("--e4b-layers", type=int, default=42)

@@ -29,6 +29,18 @@ struct DecSeqCache {
   uint64_t cap;
 };
 
+// Integer softmax statistics of one query head over its window
+// (ops.rs:230-258): the first argmax, the exp sum with its reciprocal, and the
+// residual ONE - sum(weights) that the argmax row's weight receives.
+struct AttnStat {
+  int32_t mx;     // maximum score
+  uint32_t mi;    // window row of its first occurrence
+  int64_t sum;    // sum of exp terms
+  uint64_t rec;   // 2^96 / sum, 0 when the generic division is needed
+  int32_t resid;  // added (saturating) to the weight of row mi
+  int32_t pad;
+};
+
 // One decode step's attention for one layer: head norms, RoPE and KV append
 // of the fused projection rows, then scores, integer softmax and weighted sums.
 struct AttnDecArgs {
@@ -49,13 +61,16 @@ struct AttnDecArgs {
   uint32_t hd, nh, nkv;
   int32_t* scores;  // scratch [nh][max_rows]
   int64_t* acc;     // [nh][hd] wrapped weighted sums (requantized by the O projection)
-  int scores_in_lds;  // the weighted-sum kernel keeps G x lds_stride scores in LDS
-  uint64_t lds_stride;  // LDS row stride of the kept scores (>= every window)
+  int scores_in_lds;  // the statistics kernel keeps G x lds_stride exp terms in LDS
+  uint64_t lds_stride;  // LDS row stride of the kept terms (>= every window)
+  int64_t* keys;        // [nh][key_chunks] argmax key of each kAttnScoreRows chunk of scores
+  uint64_t key_chunks;  // >= max_rows / kAttnScoreRows
+  AttnStat* stats;      // [nh]
   // Batched steps (grid z = sequence): caches[seq] replaces k, v and cap (cap
   // above then only sizes the grid), and st, trig, qkv, scores and acc advance
   // by one StepState and by the strides below per sequence.
   const DecSeqCache* caches;
-  uint64_t trig_stride, qkv_stride, scores_stride, acc_stride;
+  uint64_t trig_stride, qkv_stride, scores_stride, acc_stride, keys_stride, stats_stride;
   uint32_t nseq;
 };
 
@@ -79,7 +94,11 @@ void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const i
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
                               uint64_t kpad, hipStream_t s, uint32_t nseq = 1);
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s);
-// part 0: head norms, RoPE, KV append and scores; part 1: softmax + weighted sum
+// Whether launch_dec_attention runs the statistics as a separate pass.
+bool dec_attention_split(const AttnDecArgs& a);
+// part 0: head norms, RoPE, KV append and scores; part 1: softmax statistics;
+// part 2: weights and weighted sums; part 3: parts 1 and 2 in one kernel whose
+// workgroups each rebuild the statistics (for grids that fit the device once)
 void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s);
 // Writes the step position and token and every RoPE table's cos/sin pairs at
 // that position (trig: 2 * total_pairs int32).

@@ -215,6 +215,8 @@ __device__ __forceinline__ void seq_view(AttnDecArgs& a) {
   a.qkv += seq * a.qkv_stride;
   a.scores += seq * a.scores_stride;
   a.acc += seq * a.acc_stride;
+  a.keys += seq * a.keys_stride;
+  a.stats += seq * a.stats_stride;
   if (a.caches) {
     const DecSeqCache c = a.caches[seq];
     a.k = c.k;
@@ -235,6 +237,7 @@ template <bool VEC>
 __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   __shared__ int32_t ql[kDecMaxGroup * kDecMaxHeadDim];
   __shared__ int32_t kn[kDecMaxHeadDim];
+  __shared__ int64_t ck[kDecMaxGroup][kAttnScoreRows];
   seq_view(a);
   const Window win = attn_window(a);
   const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
@@ -350,11 +353,206 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
       }
     }
     acc = int64_t(row16_reduce(uint64_t(acc), OpWrapAdd()));  // the 16 lanes of this key row
-    if (li == 0 && valid) a.scores[(uint64_t(kvh) * G + g) * a.max_rows + j] = requant(acc);
+    if (li == 0) {
+      const int32_t sc = requant(acc);
+      if (valid) a.scores[(uint64_t(kvh) * G + g) * a.max_rows + j] = sc;
+      ck[g][grp] = valid ? score_key(sc, j) : INT64_MIN;
+    }
+  }
+  __syncthreads();
+  // this chunk's argmax key per head (the maximum of the chunk maxima is the
+  // window's first argmax)
+  if (threadIdx.x < G) {
+    int64_t best = ck[threadIdx.x][0];
+    for (uint32_t r = 1; r < kAttnScoreRows; ++r) best = ck[threadIdx.x][r] > best ? ck[threadIdx.x][r] : best;
+    a.keys[(uint64_t(kvh) * G + threadIdx.x) * a.key_chunks + blockIdx.y] = best;
   }
 }
 
-// Integer softmax (ops.rs:230-258) and weighted sum (ops.rs:336-351) over
+// Integer softmax statistics (ops.rs:230-258) of every query head of one KV
+// head over its whole window, 1024 threads, 16 / G waves per head: the first
+// argmax (from the scores kernel's chunk maxima), the exp sum (non-negative
+// terms with a total below 2^63, so the saturating sum is the plain sum) with
+// its reciprocal, and the sum of every weight of the window, whose
+// complement to ONE the reference adds to the argmax row's weight. With room
+// in LDS each exp term is kept there for the weight pass (2^32, the argmax
+// row's term, stored as 0xffffffff: every other term is at most 2^32 - 2^16).
+__global__ __launch_bounds__(1024) void k_dec_attn_stats(AttnDecArgs a) {
+  extern __shared__ int32_t sl_dyn[];
+  __shared__ int64_t red[16];
+  __shared__ int64_t hkey[kDecMaxGroup], hsum[kDecMaxGroup];
+  __shared__ uint64_t hrec[kDecMaxGroup];
+  seq_view(a);
+  const Window win = attn_window(a);
+  const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv;
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;
+  const bool active = g < G;
+  const uint64_t stride = 64 * uint64_t(wph);
+  const uint64_t head = uint64_t(kvh) * G + (active ? g : 0);
+  const uint64_t nch = (win.cnt + kAttnScoreRows - 1) / kAttnScoreRows;
+  int64_t best = INT64_MIN;
+  if (active)
+    for (uint64_t c = wi * 64 + lane; c < nch; c += stride) {
+      const int64_t k = a.keys[head * a.key_chunks + c];
+      best = k > best ? k : best;
+    }
+  best = wmax(best);
+  if (lane == 0) red[wave] = best;
+  __syncthreads();
+  if (threadIdx.x < G) {
+    int64_t k = red[threadIdx.x * wph];
+    for (uint32_t w = 1; w < wph; ++w) k = red[threadIdx.x * wph + w] > k ? red[threadIdx.x * wph + w] : k;
+    hkey[threadIdx.x] = k;
+  }
+  __syncthreads();
+  const int32_t mx = int32_t(hkey[active ? g : 0] >> 32);
+  const int32_t* scg = a.scores + head * a.max_rows;
+  int32_t* scl = a.scores_in_lds ? sl_dyn + uint64_t(active ? g : 0) * a.lds_stride : nullptr;
+  int64_t s = 0;
+  if (active)
+    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
+      const int64_t e = softmax_exp(scg[r], mx);
+      s += e;
+      if (scl) scl[r] = int32_t(e == kOneAcc ? 0xffffffffu : uint32_t(e));
+    }
+  s = wsum_wrap(s);
+  __syncthreads();  // red[] from the argmax has been read
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  if (threadIdx.x < G) {
+    int64_t t = 0;
+    for (uint32_t w = 0; w < wph; ++w) t += red[threadIdx.x * wph + w];
+    hsum[threadIdx.x] = t;
+    hrec[threadIdx.x] = t < (int64_t(1) << 61) ? softmax_recip(t) : 0;  // 0: generic division
+  }
+  __syncthreads();
+  int64_t ws = 0;
+  if (active) {
+    const int64_t S = hsum[g];
+    const uint64_t M = hrec[g];
+    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
+      int64_t e;
+      if (scl) {
+        const uint32_t u = uint32_t(scl[r]);
+        e = u == 0xffffffffu ? kOneAcc : int64_t(u);
+      } else {
+        e = softmax_exp(scg[r], mx);
+      }
+      ws += M ? softmax_weight_r(e, S, M) : softmax_weight(e, S);
+    }
+  }
+  ws = wsum_wrap(ws);
+  __syncthreads();  // red[] from the exp sums has been read
+  if (lane == 0) red[wave] = ws;
+  __syncthreads();
+  if (threadIdx.x < G) {
+    int64_t t = 0;
+    for (uint32_t w = 0; w < wph; ++w) t += red[threadIdx.x * wph + w];
+    const int64_t key = hkey[threadIdx.x];
+    AttnStat st;
+    st.mx = int32_t(key >> 32);
+    st.mi = uint32_t(0xffffffffull - (uint64_t(key) & 0xffffffffull));
+    st.sum = hsum[threadIdx.x];
+    st.rec = hrec[threadIdx.x];
+    st.resid = sub_sat(kOneAct, sat32(t));
+    st.pad = 0;
+    a.stats[uint64_t(kvh) * G + threadIdx.x] = st;
+  }
+}
+
+// Weights (ops.rs:245-258, from the head statistics) and weighted sums
+// (ops.rs:336-351) over kAttnWsumRows window rows for every query head of one
+// KV head, 1024 threads; each workgroup adds its wrapping partial sums to the
+// accumulators atomically (exact in any order). Chunk 0 clears the projection
+// accumulators read by the scores kernel.
+__global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
+  __shared__ int32_t wl[kDecMaxGroup][kAttnWsumRows];
+  __shared__ int64_t part[3][1024];
+  seq_view(a);
+  const Window win = attn_window(a);
+  const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
+  if (blockIdx.y == 0) {
+    for (uint32_t i = threadIdx.x; i < G * hd; i += 1024) a.qkv[uint64_t(kvh) * G * hd + i] = 0;
+    if (a.own_cache)
+      for (uint32_t i = threadIdx.x; i < hd; i += 1024) {
+        a.qkv[(uint64_t(a.nh) + kvh) * hd + i] = 0;
+        if (a.has_v) a.qkv[(uint64_t(a.nh) + a.nkv + kvh) * hd + i] = 0;
+      }
+  }
+  const uint64_t r0 = uint64_t(blockIdx.y) * kAttnWsumRows;
+  if (r0 >= win.cnt) return;
+  const uint64_t nr = win.cnt - r0 < kAttnWsumRows ? win.cnt - r0 : kAttnWsumRows;
+  const uint64_t kvw = uint64_t(a.nkv) * hd;
+  // value rows of this chunk: slice sl takes rows 8 sl .. 8 sl + 7, dims dl and dl + 256
+  const uint32_t sl = threadIdx.x >> 8, dl = threadIdx.x & 255;
+  int32_t vp[2][kAttnWsumRows / 4];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+      const uint32_t d = dl + 256 * jj;
+      const uint64_t rr = sl * (kAttnWsumRows / 4) + k;
+      vp[jj][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
+    }
+  if (threadIdx.x < G * kAttnWsumRows) {
+    const uint32_t gg = threadIdx.x / kAttnWsumRows, rr = threadIdx.x % kAttnWsumRows;
+    const uint64_t head = uint64_t(kvh) * G + gg;
+    int32_t w = 0;
+    if (rr < nr) {
+      const AttnStat st = a.stats[head];
+      const uint64_t r = r0 + rr;
+      const int64_t e = softmax_exp(a.scores[head * a.max_rows + r], st.mx);
+      w = st.rec ? softmax_weight_r(e, st.sum, st.rec) : softmax_weight(e, st.sum);
+      if (r == st.mi) w = add_sat(w, st.resid);
+    }
+    wl[gg][rr] = w;
+  }
+  __syncthreads();
+  // weighted sums: 4 row slices per dim, combined in LDS for up to 1024 / dstr
+  // heads per pass, one atomic per (head, dim)
+  const uint32_t dstr = hd > 256 ? 512 : 256;
+  const uint32_t hpp = 1024 / dstr;
+  for (uint32_t h0 = 0; h0 < G; h0 += hpp) {
+    const uint32_t hn = G - h0 < hpp ? G - h0 : hpp;
+    if (sl > 0)
+      for (uint32_t hh = 0; hh < hn; ++hh) {
+        int64_t p0 = 0, p1 = 0;
+#pragma unroll
+        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+          const int32_t w = wl[h0 + hh][sl * (kAttnWsumRows / 4) + k];
+          p0 = mac(p0, vp[0][k], w);
+          p1 = mac(p1, vp[1][k], w);
+        }
+        part[sl - 1][hh * dstr + dl] = p0;
+        if (dstr == 512) part[sl - 1][hh * dstr + 256 + dl] = p1;
+      }
+    __syncthreads();
+    if (sl == 0)
+      for (uint32_t hh = 0; hh < hn; ++hh) {
+        int64_t p0 = 0, p1 = 0;
+#pragma unroll
+        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+          const int32_t w = wl[h0 + hh][k];
+          p0 = mac(p0, vp[0][k], w);
+          p1 = mac(p1, vp[1][k], w);
+        }
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+          p0 = int64_t(uint64_t(p0) + uint64_t(part[q][hh * dstr + dl]));
+          if (dstr == 512) p1 = int64_t(uint64_t(p1) + uint64_t(part[q][hh * dstr + 256 + dl]));
+        }
+        int64_t* out = a.acc + (uint64_t(kvh) * G + h0 + hh) * hd;
+        if (dl < hd) atomicAdd(reinterpret_cast<unsigned long long*>(out + dl), static_cast<unsigned long long>(p0));
+        if (dl + 256 < hd)
+          atomicAdd(reinterpret_cast<unsigned long long*>(out + dl + 256), static_cast<unsigned long long>(p1));
+      }
+    __syncthreads();
+  }
+}
+
+// Single-kernel form for small grids (one sequence, short windows): integer
+// softmax (ops.rs:230-258) and weighted sum (ops.rs:336-351) over
 // kAttnWsumRows window rows for every query head of one KV head, 1024
 // threads. Each workgroup rebuilds the heads' argmax (first maximum) and exp
 // sum over the whole window from the scores, with 16 / G waves per head (each
@@ -364,7 +562,7 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
 // head's argmax row also sums every weight of the window and applies the
 // residual ONE - sum to that row, as the reference does before the weighted
 // sum. Chunk 0 clears the projection accumulators read by the scores kernel.
-__global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
+__global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   extern __shared__ int32_t sl_dyn[];
   __shared__ int64_t red[16];
   __shared__ int64_t hkey[kDecMaxGroup], hsum[kDecMaxGroup];
@@ -649,14 +847,31 @@ void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
       hipLaunchKernelGGL(k_dec_attn_scores<true>, grid, dim3(512), 0, s, a);
     else
       hipLaunchKernelGGL(k_dec_attn_scores<false>, grid, dim3(512), 0, s, a);
+  } else if (part == 1) {
+    const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.lds_stride * 4 : 0;
+    hipLaunchKernelGGL(k_dec_attn_stats, dim3(a.nkv, 1, ns), dim3(1024), lds, s, a);
+  } else if (part == 2) {
+    hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows), ns), dim3(1024), 0, s, a);
   } else {
     const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.lds_stride * 4 : 0;
-    hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows), ns), dim3(1024), lds, s, a);
+    hipLaunchKernelGGL(k_dec_attn_softmax_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows), ns), dim3(1024), lds, s, a);
   }
+}
+// The weighted-sum workgroups of the single-kernel form each rebuild the
+// window statistics; that redundancy is free while the grid fits the device
+// in one pass, beyond it a separate statistics pass is cheaper.
+bool dec_attention_split(const AttnDecArgs& a) {
+  const uint64_t wgs = uint64_t(a.nkv) * nblk(a.cap, kAttnWsumRows) * (a.nseq ? a.nseq : 1);
+  return wgs > 256;
 }
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s) {
   launch_dec_attention_part(a, 0, s);
-  launch_dec_attention_part(a, 1, s);
+  if (dec_attention_split(a)) {
+    launch_dec_attention_part(a, 1, s);
+    launch_dec_attention_part(a, 2, s);
+  } else {
+    launch_dec_attention_part(a, 3, s);
+  }
 }
 void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, const RopeTable* tables, uint32_t ntables,
                          uint32_t total_pairs, int32_t* trig, hipStream_t s) {

@@ -777,6 +777,8 @@ struct det_session {
   int8_t *limbs_x = nullptr, *limbs_ff = nullptr;
   uint64_t kpad_x = 0;
   int64_t* attn_acc = nullptr;
+  int64_t* attn_keys = nullptr;      // per-chunk argmax keys of the scores
+  det::AttnStat* attn_stats = nullptr;  // per-head softmax statistics
   int32_t* trig = nullptr;  // cos/sin pairs of every RoPE table at the step position
   int64_t* am_scratch = nullptr;
   uint32_t* am_out = nullptr;
@@ -854,6 +856,8 @@ void session_alloc(det_session* s) {
     HIPC(hipMemsetAsync(s->o_acc, 0, H * 8, zst));
     HIPC(hipMemsetAsync(s->ff_acc, 0, H * 8, zst));
     s->scores = s->alloc<int32_t>(nh * T);
+    s->attn_keys = s->alloc<int64_t>(nh * ((T + det::kAttnScoreRows - 1) / det::kAttnScoreRows));
+    s->attn_stats = s->alloc<det::AttnStat>(nh);
     s->attn_acc = s->alloc<int64_t>(nhd);
     s->hbuf = s->alloc<int32_t>(ff);
     s->am_scratch = s->alloc<int64_t>((m->vocab + 1023) / 1024);
@@ -1187,6 +1191,7 @@ struct BatchWs {
   int32_t* logits = nullptr;  // [cap][vocab]
   int32_t* dec_in = nullptr;  // [cap][hidden] token embeddings (PLE input)
   uint32_t* next = nullptr;   // [cap] greedy tokens
+  int64_t* am_keys = nullptr;  // argmax partial keys of cap logits rows
   uint8_t* desc = nullptr;    // device: positions, per-layer windows and append targets
   uint8_t* desc_host = nullptr;  // pinned staging of desc
   size_t desc_bytes = 0;
@@ -1195,6 +1200,8 @@ struct BatchWs {
   uint64_t grid_cap = 0;  // cache rows the captured attention grids cover
   uint64_t qkv_stride = 0, attn_stride = 0, ff_stride = 0, score_heads = 0;
   int32_t *x = nullptr, *normed = nullptr, *trig = nullptr, *hbuf = nullptr, *scores = nullptr;
+  int64_t* attn_keys = nullptr;  // [cap][score_heads][grid_cap / kAttnScoreRows]
+  det::AttnStat* attn_stats = nullptr;  // [cap][score_heads]
   int64_t *qkv_acc = nullptr, *attn_acc = nullptr, *o_acc = nullptr, *ff_acc = nullptr;
   int8_t *limbs_x = nullptr, *limbs_o = nullptr, *limbs_ff = nullptr;
   std::vector<void*> owned;
@@ -1218,7 +1225,8 @@ struct BatchWs {
   ~BatchWs() {
     drop_graph();
     for (void* p : {static_cast<void*>(logits), static_cast<void*>(dec_in), static_cast<void*>(next),
-                    static_cast<void*>(desc), static_cast<void*>(scores)})
+                    static_cast<void*>(desc), static_cast<void*>(scores), static_cast<void*>(am_keys),
+                    static_cast<void*>(attn_keys)})
       if (p) (void)hipFree(p);
     for (void* p : owned) (void)hipFree(p);
     if (desc_host) (void)hipHostFree(desc_host);
@@ -1264,6 +1272,7 @@ BatchWs& ensure_batch(det_model* m, uint64_t n) {
   HIPC(hipMalloc(&b->logits, b->cap * m->vocab * 4));
   HIPC(hipMalloc(&b->dec_in, b->cap * m->hidden * 4));
   HIPC(hipMalloc(&b->next, b->cap * 4));
+  HIPC(hipMalloc(&b->am_keys, det::argmax_rows_scratch(b->cap, m->vocab) * 8));
   b->desc_bytes = std::max(BatchDesc(b->cap, m->layers.size()).bytes, FusedDesc(b->cap, m->layers.size()).bytes);
   HIPC(hipMalloc(&b->desc, b->desc_bytes));
   HIPC(hipHostMalloc(reinterpret_cast<void**>(&b->desc_host), b->desc_bytes, hipHostMallocDefault));
@@ -1374,7 +1383,7 @@ void decode_batch(det_session* const* ss, uint64_t n, const uint32_t* tokens, ui
   det::launch_rmsnorm_to(w->normed, w->x, n, H, H, m->final_norm, m->eps, st);
   ctx->linear(*m->lm_head, w->normed, n, H, b.logits, V, nullptr);
   if (m->softcap) det::launch_softcap(b.logits, n * V, *m->softcap, st);
-  det::launch_argmax_rows(b.logits, n, V, b.next, st);
+  det::launch_argmax_rows(b.logits, n, V, b.am_keys, b.next, st);
   for (uint64_t i = 0; i < n; ++i) copy_d2d(ctx, ss[i]->logits, b.logits + i * V, V * 4);
   std::vector<uint32_t> next(n);
   HIPC(hipMemcpyAsync(next.data(), b.next, n * 4, hipMemcpyDeviceToHost, st));
@@ -1432,6 +1441,7 @@ void ensure_fused_batch(det_model* m, BatchWs& b, uint64_t need) {
     b.limbs_x = b.alloc<int8_t>(T * 4 * m->fused[0].qkv.kpad);
     b.limbs_o = b.alloc<int8_t>(T * 4 * kpo);
     b.limbs_ff = b.alloc<int8_t>(T * 4 * kff);
+    b.attn_stats = b.alloc<det::AttnStat>(T * nh);
     // every accumulator is cleared by the kernel that consumes it, so they
     // only need to start at zero (stream-ordered, outside any graph)
     hipStream_t zst = m->ctx->stream;
@@ -1449,8 +1459,11 @@ void ensure_fused_batch(det_model* m, BatchWs& b, uint64_t need) {
     HIPC(hipStreamSynchronize(m->ctx->stream));
     b.drop_graph();
     if (b.scores) HIPC(hipFree(b.scores));
+    if (b.attn_keys) HIPC(hipFree(b.attn_keys));
     b.scores = nullptr;
+    b.attn_keys = nullptr;
     HIPC(hipMalloc(&b.scores, T * b.score_heads * rows * 4));
+    HIPC(hipMalloc(&b.attn_keys, T * b.score_heads * (rows / det::kAttnScoreRows) * 8));
     b.grid_cap = rows;
   }
 }
@@ -1489,6 +1502,11 @@ det::AttnDecArgs batch_attn_args(det_model* m, BatchWs& b, size_t l, uint32_t n)
   a.qkv_stride = b.qkv_stride;
   a.scores_stride = b.score_heads * b.grid_cap;
   a.acc_stride = b.attn_stride;
+  a.keys = b.attn_keys;
+  a.key_chunks = b.grid_cap / det::kAttnScoreRows;
+  a.keys_stride = b.score_heads * a.key_chunks;
+  a.stats = b.attn_stats;
+  a.stats_stride = b.score_heads;
   a.nseq = n;
   return a;
 }
@@ -1522,7 +1540,7 @@ void enqueue_fused_batch(det_model* m, BatchWs& b, uint32_t n) {
   det::launch_gemv_dec_batch(*m->lm_head, b.limbs_x, n, b.logits, V, nullptr, 0, 0, nullptr, 0, st);
   if (m->softcap) det::launch_dec_softcap(b.logits, n * V, *m->softcap, st);
   det::launch_copy_rows(b.logits, V, n, reinterpret_cast<int32_t* const*>(b.desc + D.logit_dst), st);
-  det::launch_argmax_rows(b.logits, n, V, b.next, st);
+  det::launch_argmax_rows(b.logits, n, V, b.am_keys, b.next, st);
 }
 
 void decode_batch_fused(det_session* const* ss, uint64_t n, const uint32_t* tokens, uint32_t flags,
@@ -1633,6 +1651,9 @@ det::AttnDecArgs attn_args(det_session* s, size_t l) {
   a.acc = s->attn_acc;
   a.scores_in_lds = (L.num_heads / L.num_kv_heads) * ac.cap * 4 <= 32768;
   a.lds_stride = ac.cap;
+  a.keys = s->attn_keys;
+  a.key_chunks = (s->score_stride + det::kAttnScoreRows - 1) / det::kAttnScoreRows;
+  a.stats = s->attn_stats;
   return a;
 }
 

@@ -142,8 +142,10 @@ void launch_rope_rows(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, ui
 // Row i of k and v (width w) to kdst[i] / vdst[i] (device arrays of row pointers).
 void launch_kv_append(const int32_t* k, const int32_t* v, uint64_t w, uint64_t n, int32_t* const* kdst,
                       int32_t* const* vdst, hipStream_t s);
-// out[r] = first index of the maximum of row r of x [rows][n].
-void launch_argmax_rows(const int32_t* x, uint64_t rows, uint64_t n, uint32_t* out, hipStream_t s);
+// out[r] = first index of the maximum of row r of x [rows][n]; scratch holds
+// argmax_rows_scratch(rows, n) int64 keys.
+uint64_t argmax_rows_scratch(uint64_t rows, uint64_t n);
+void launch_argmax_rows(const int32_t* x, uint64_t rows, uint64_t n, int64_t* scratch, uint32_t* out, hipStream_t s);
 void launch_gather_rows(const DevMatrix& M, const uint32_t* ids, uint64_t m, uint64_t col0,
                         uint64_t ncols, int32_t scale, int32_t* out, uint64_t ld_out, hipStream_t s);
 

@@ -932,15 +932,31 @@ __global__ void k_kv_append(const int32_t* __restrict__ k, const int32_t* __rest
   vdst[i][c] = v[i * w + c];
 }
 
-// First-index argmax of each row of x [rows][n] (one workgroup per row).
-__global__ __launch_bounds__(256) void k_argmax_rows(const int32_t* __restrict__ x, uint64_t n,
-                                                     uint32_t* __restrict__ out) {
+// First-index argmax of each row of x [rows][n] in two passes: workgroup
+// (p, r) reduces columns [p * kArgmaxSpan, (p + 1) * kArgmaxSpan) of row r to
+// one argmax key; one workgroup per row then reduces the row's keys.
+constexpr uint64_t kArgmaxSpan = 4096;
+__global__ __launch_bounds__(256) void k_argmax_rows_part(const int32_t* __restrict__ x, uint64_t n,
+                                                          int64_t* __restrict__ keys, uint32_t parts) {
   __shared__ int64_t red[4];
-  const int32_t* xr = x + uint64_t(blockIdx.x) * n;
+  const int32_t* xr = x + uint64_t(blockIdx.y) * n;
+  const uint64_t c0 = uint64_t(blockIdx.x) * kArgmaxSpan;
+  const uint64_t c1 = c0 + kArgmaxSpan < n ? c0 + kArgmaxSpan : n;
   int64_t best = INT64_MIN;
-  for (uint64_t i = threadIdx.x; i < n; i += 256) {
+  for (uint64_t i = c0 + threadIdx.x; i < c1; i += 256) {
     const int64_t key = argmax_key(xr[i], uint32_t(i));
     best = key > best ? key : best;
+  }
+  best = block_reduce<4>(best, 2, red);
+  if (threadIdx.x == 0) keys[uint64_t(blockIdx.y) * parts + blockIdx.x] = best;
+}
+__global__ __launch_bounds__(256) void k_argmax_rows_final(const int64_t* __restrict__ keys, uint32_t parts,
+                                                           uint32_t* __restrict__ out) {
+  __shared__ int64_t red[4];
+  int64_t best = INT64_MIN;
+  for (uint32_t p = threadIdx.x; p < parts; p += 256) {
+    const int64_t k = keys[uint64_t(blockIdx.x) * parts + p];
+    best = k > best ? k : best;
   }
   best = block_reduce<4>(best, 2, red);
   if (threadIdx.x == 0) out[blockIdx.x] = key_index(best);
@@ -1321,8 +1337,12 @@ void launch_kv_append(const int32_t* k, const int32_t* v, uint64_t w, uint64_t n
                       int32_t* const* vdst, hipStream_t s) {
   if (n && w) hipLaunchKernelGGL(k_kv_append, dim3(blocks_for(w, 256), unsigned(n)), dim3(256), 0, s, k, v, w, kdst, vdst);
 }
-void launch_argmax_rows(const int32_t* x, uint64_t rows, uint64_t n, uint32_t* out, hipStream_t s) {
-  if (rows) hipLaunchKernelGGL(k_argmax_rows, dim3(unsigned(rows)), dim3(256), 0, s, x, n, out);
+uint64_t argmax_rows_scratch(uint64_t rows, uint64_t n) { return rows * ((n + kArgmaxSpan - 1) / kArgmaxSpan); }
+void launch_argmax_rows(const int32_t* x, uint64_t rows, uint64_t n, int64_t* scratch, uint32_t* out, hipStream_t s) {
+  if (rows == 0 || n == 0) return;
+  const uint32_t parts = uint32_t((n + kArgmaxSpan - 1) / kArgmaxSpan);
+  hipLaunchKernelGGL(k_argmax_rows_part, dim3(parts, unsigned(rows)), dim3(256), 0, s, x, n, scratch, parts);
+  hipLaunchKernelGGL(k_argmax_rows_final, dim3(unsigned(rows)), dim3(256), 0, s, scratch, parts, out);
 }
 void launch_argmax(const int32_t* x, uint64_t n, int64_t* scratch, uint32_t* out, hipStream_t s) {
   const uint64_t parts = (n + 1023) / 1024;

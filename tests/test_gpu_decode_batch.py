@@ -164,3 +164,12 @@ def test_batch_rejects_bad_inputs_without_touching_state(ctx):
     got = rd.decode_batch([a, b], [ta, tb])
     assert key(got[0]) == key(ref_a.decode(ta))
     assert key(got[1]) == key(ref_b.decode(tb))
+
+
+def test_batch_of_16_long_windows_split_softmax(ctx):
+    # full-attention windows up to ~650 rows over 16 sequences: more than 256
+    # weighted-sum workgroups, so the batched step runs the separate
+    # statistics pass; sliding layers keep the single-kernel form
+    gm = sharing_model(ctx)
+    prompts = ragged_prompts(16, 300, 640, 1000, seed=33)
+    run_batch_vs_solo(gm, 1000, prompts, steps=3, max_tokens=700, solo_flags=rd.DET_DECODE_PER_OP)

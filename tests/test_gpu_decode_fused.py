@@ -84,3 +84,28 @@ def test_fused_decode_with_kv_sharing_k_eq_v_softcap_and_scalars(ctx):
     exp = om.capture(prompt, 12)
     got = gm.capture(prompt, 12)
     assert got == exp
+
+
+def test_fused_decode_long_context_split_softmax_matches_per_op(ctx):
+    # a full-attention window of ~9000 rows: the fused step computes the
+    # softmax statistics in their own pass (more than 256 weighted-sum
+    # workgroups); the per-op schedule uses the prefill attention kernel
+    cfg = e4b_two_layer_config(window=5, vocab=1024)
+    tc = cfg["text_config"]
+    tc.update({"hidden_size": 256, "intermediate_size": 512, "head_dim": 64, "num_attention_heads": 4,
+               "num_key_value_heads": 1})
+    gm = rd.Model(ctx, cfg)
+    for name, v, s in fixtures.custom_model(cfg, seed=17):
+        gm.set_tensor(name, v, s)
+    gm.finalize()
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, 1024, size=9000).tolist()
+    a, b = gm.session(9024), gm.session(9024)
+    ta = a.prefill(prompt, rd.DET_COMMIT_NONE).next_token
+    tb = b.prefill(prompt, rd.DET_COMMIT_NONE).next_token
+    assert ta == tb
+    for step in range(6):
+        ra = a.decode(ta, rd.DET_COMMIT_ALL | (rd.DET_DECODE_EAGER if step % 2 else 0))
+        rb = b.decode(tb, rd.DET_COMMIT_ALL | rd.DET_DECODE_PER_OP)
+        assert (ra.activation, ra.logits, ra.kv, ra.next_token) == (rb.activation, rb.logits, rb.kv, rb.next_token), step
+        ta, tb = ra.next_token, rb.next_token
