@@ -414,6 +414,116 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
   }
 }
 
+// Decode GEMV for 5-16 tokens (NG = 2 or 4 groups of 4): the A tiles of a K
+// step are as large as the weight tile or larger, so the four waves of a
+// workgroup take four consecutive weight tiles over the same K steps and
+// share each step's A tiles through LDS (two buffers; the next step's weight
+// and A loads are issued before the current step's MFMAs, one barrier per
+// step). Outputs as in k_gemv_dec; kchunks splits K across workgroups
+// (atomic outputs only).
+template <int EPI, int NG>
+__global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
+    const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
+    const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
+    int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
+    int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
+  __shared__ v4i al[2][NG][2][64];  // [buffer][token group][half][lane]
+  constexpr int CH = (NG * 2 * 64 + 255) / 256;  // A chunks per thread and step
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const uint64_t nsteps = kpad / 128;
+  const uint32_t kc = blockIdx.x % kchunks;
+  const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
+  const uint64_t cs0 = kc * cper < nsteps ? kc * cper : nsteps;
+  const uint64_t cs1 = cs0 + cper < nsteps ? cs0 + cper : nsteps;
+  const uint64_t ntiles = (n_rows + 15) / 16;
+  const uint64_t groups = gridDim.x / kchunks;
+  const v4i zero = {0, 0, 0, 0};
+  // this thread's share of a step's A tiles: chunk e = tid + 256 c is lane
+  // e % 64, half (e / 64) % 2, token group e / 128 of the LDS buffer
+  const v4i* asrc[CH];
+  bool aon[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const uint32_t e = threadIdx.x + 256 * c;
+    const uint32_t ln = e & 63, h = (e >> 6) & 1, tg = e >> 7;
+    aon[c] = e < uint32_t(NG * 128) && 4 * tg + ((ln & 15) >> 2) < ntok;
+    asrc[c] = reinterpret_cast<const v4i*>(limbs + (aon[c] ? uint64_t(16 * tg + (ln & 15)) * kpad : 0) +
+                                           32 * (ln >> 4) + 16 * h);
+  }
+  for (uint64_t base = uint64_t(blockIdx.x / kchunks) * 4; base < ntiles; base += groups * 4) {
+    const uint64_t tile = base + wave;
+    const bool t_on = tile < ntiles;
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 32);
+    v4i acc[NG];
+#pragma unroll
+    for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
+    v4i b0 = zero, b1 = zero, ar[CH];
+    if (cs0 < cs1) {
+      b0 = t_on ? __builtin_nontemporal_load(bp + cs0 * 128) : zero;
+      b1 = t_on ? __builtin_nontemporal_load(bp + cs0 * 128 + 1) : zero;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) ar[c] = aon[c] ? asrc[c][cs0 * 8] : zero;
+    }
+    for (uint64_t s = cs0; s < cs1; ++s) {
+      const int buf = int((s - cs0) & 1);
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const uint32_t e = threadIdx.x + 256 * c;
+        if (e < uint32_t(NG * 128)) (&al[buf][0][0][0])[e] = ar[c];
+      }
+      __syncthreads();
+      v4i n0 = zero, n1 = zero;
+      if (s + 1 < cs1) {
+        n0 = t_on ? __builtin_nontemporal_load(bp + (s + 1) * 128) : zero;
+        n1 = t_on ? __builtin_nontemporal_load(bp + (s + 1) * 128 + 1) : zero;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) ar[c] = aon[c] ? asrc[c][(s + 1) * 8] : zero;
+      }
+#pragma unroll
+      for (int tg = 0; tg < NG; ++tg) {
+        acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[buf][tg][0][lane], b0, acc[tg], 0, 0, 0);
+        acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[buf][tg][1][lane], b1, acc[tg], 0, 0, 0);
+      }
+      b0 = n0;
+      b1 = n1;
+    }
+    __syncthreads();  // both buffers are read before the next tile group refills them
+    if (!t_on) continue;
+    const uint64_t row = tile * 16 + i;
+    const bool r_on = row < n_rows;
+    const int32_t rs = r_on ? rowsum[row] : 0, sc = r_on ? scale[row] : 0;
+    // lane 16 g + i of group tg holds the limb sums of token 4 tg + g, row i
+#pragma unroll
+    for (int tg = 0; tg < NG; ++tg) {
+      const int64_t p[4] = {acc[tg][0], acc[tg][1], acc[tg][2], acc[tg][3]};
+      const uint32_t tok = 4 * tg + g;
+      const bool ok = tok < ntok && r_on;
+      if (acc_out) {
+        if (ok) {
+          const int64_t a = limb_combine(p, kc == 0 ? rs : 0, sc);
+          atomicAdd(reinterpret_cast<unsigned long long*>(acc_out + tok * acc_ld + row),
+                    static_cast<unsigned long long>(a));
+        }
+      } else if (EPI == 1) {
+        const int32_t r = ok ? requant(limb_combine(p, rs, sc)) : 0;
+        const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
+        if (ok && i < 8) {
+          const uint64_t f = tile * 8 + i;
+          const int32_t h = mul_sat(gelu_act(r), up);
+          out[tok * out_ld + f] = h;
+          const uint32_t u = uint32_t(h) ^ 0x00808080u;
+          int8_t* ol = out_limbs + uint64_t(tok) * 4 * out_kpad + f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ol[j * out_kpad] = int8_t(uint8_t(u >> (8 * j)));
+        }
+      } else if (ok) {
+        out[tok * out_ld + row] = requant(limb_combine(p, rs, sc));
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Prefill GEMM (det_linear_slab, det_kernels.rs:180-203): C[m][n] =
 // requantize(sum_k act[m][k] * W[n][k]) for a slab of M activation rows.
@@ -1151,6 +1261,29 @@ static void launch_gemv_dec_ng(const DevMatrix& W, const int8_t* limbs, uint32_t
 #undef DET_GEMV_DEC
 }
 
+template <int NG>
+static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
+                               int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
+                               hipStream_t s) {
+  const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
+  const void* fn = epilogue == 1 ? reinterpret_cast<const void*>(&k_gemv_dec_wg<1, NG>)
+                                 : reinterpret_cast<const void*>(&k_gemv_dec_wg<0, NG>);
+  const uint64_t cap = resident_blocks(fn, 256);
+  const uint64_t groups = (ntiles + 3) / 4;
+  // K chunks across workgroups (atomic outputs only) while the launch stays
+  // resident, keeping at least two K steps per chunk
+  uint32_t kc = 1;
+  if (acc)
+    while (groups * kc * 2 <= cap && nsteps >= uint64_t(kc) * 2 * 2) kc *= 2;
+  const uint64_t g = std::min<uint64_t>(groups, std::max<uint64_t>(cap / kc, 1));
+  if (epilogue == 1)
+    hipLaunchKernelGGL((k_gemv_dec_wg<1, NG>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum, limbs,
+                       W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad);
+  else
+    hipLaunchKernelGGL((k_gemv_dec_wg<0, NG>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum, limbs,
+                       W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad);
+}
+
 void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                            int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
                            hipStream_t s) {
@@ -1163,8 +1296,8 @@ void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t nto
     int64_t* a = acc ? acc + uint64_t(t0) * acc_ld : nullptr;
     int8_t* ol = out_limbs ? out_limbs + uint64_t(t0) * 4 * out_kpad : nullptr;
     if (nt <= 4) launch_gemv_dec_ng<1>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
-    else if (nt <= 8) launch_gemv_dec_ng<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
-    else launch_gemv_dec_ng<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
+    else if (nt <= 8) launch_gemv_dec_wg<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
+    else launch_gemv_dec_wg<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
   }
 }
 
