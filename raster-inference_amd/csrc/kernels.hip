@@ -439,16 +439,20 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
   const uint64_t ntiles = (n_rows + 15) / 16;
   const uint64_t groups = gridDim.x / kchunks;
   const v4i zero = {0, 0, 0, 0};
+  static_assert(NG * 128 % 256 == 0, "every thread copies whole A chunks");
   // this thread's share of a step's A tiles: chunk e = tid + 256 c is lane
-  // e % 64, half (e / 64) % 2, token group e / 128 of the LDS buffer
+  // e % 64, half (e / 64) % 2, token group e / 128 of the LDS buffer. Every
+  // load below is unconditional (tokens >= ntok read limb row 0 and tiles
+  // past the matrix read tile 0, whose products land only in outputs that are
+  // never written), so the loads issue back to back without exec-masked
+  // branches between them.
   const v4i* asrc[CH];
-  bool aon[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const uint32_t e = threadIdx.x + 256 * c;
     const uint32_t ln = e & 63, h = (e >> 6) & 1, tg = e >> 7;
-    aon[c] = e < uint32_t(NG * 128) && 4 * tg + ((ln & 15) >> 2) < ntok;
-    asrc[c] = reinterpret_cast<const v4i*>(limbs + (aon[c] ? uint64_t(16 * tg + (ln & 15)) * kpad : 0) +
+    const bool on = 4 * tg + ((ln & 15) >> 2) < ntok;
+    asrc[c] = reinterpret_cast<const v4i*>(limbs + (on ? uint64_t(16 * tg + (ln & 15)) * kpad : 0) +
                                            32 * (ln >> 4) + 16 * h);
   }
   for (uint64_t base = uint64_t(blockIdx.x / kchunks) * 4; base < ntiles; base += groups * 4) {
@@ -458,28 +462,34 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
     v4i acc[NG];
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
+    // workgroups walk their K range from different starting steps, so at
+    // any moment they read different A lines (a common order makes every
+    // workgroup request the same few L2 lines at once); the sums are exact in
+    // any order
+    const uint64_t len = cs1 - cs0;
+    const uint64_t first = len ? cs0 + (blockIdx.x / kchunks) % len : cs0;
     v4i b0 = zero, b1 = zero, ar[CH];
-    if (cs0 < cs1) {
-      b0 = t_on ? __builtin_nontemporal_load(bp + cs0 * 128) : zero;
-      b1 = t_on ? __builtin_nontemporal_load(bp + cs0 * 128 + 1) : zero;
+    if (len) {
+      b0 = __builtin_nontemporal_load(bp + first * 128);
+      b1 = __builtin_nontemporal_load(bp + first * 128 + 1);
 #pragma unroll
-      for (int c = 0; c < CH; ++c) ar[c] = aon[c] ? asrc[c][cs0 * 8] : zero;
+      for (int c = 0; c < CH; ++c) ar[c] = asrc[c][first * 8];
     }
-    for (uint64_t s = cs0; s < cs1; ++s) {
-      const int buf = int((s - cs0) & 1);
+    uint64_t s = first;
+    for (uint64_t j = 0; j < len; ++j) {
+      const int buf = int(j & 1);
 #pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const uint32_t e = threadIdx.x + 256 * c;
-        if (e < uint32_t(NG * 128)) (&al[buf][0][0][0])[e] = ar[c];
-      }
+      for (int c = 0; c < CH; ++c) (&al[buf][0][0][0])[threadIdx.x + 256 * c] = ar[c];
       __syncthreads();
       v4i n0 = zero, n1 = zero;
-      if (s + 1 < cs1) {
-        n0 = t_on ? __builtin_nontemporal_load(bp + (s + 1) * 128) : zero;
-        n1 = t_on ? __builtin_nontemporal_load(bp + (s + 1) * 128 + 1) : zero;
+      const uint64_t sn = s + 1 == cs1 ? cs0 : s + 1;
+      if (j + 1 < len) {
+        n0 = __builtin_nontemporal_load(bp + sn * 128);
+        n1 = __builtin_nontemporal_load(bp + sn * 128 + 1);
 #pragma unroll
-        for (int c = 0; c < CH; ++c) ar[c] = aon[c] ? asrc[c][(s + 1) * 8] : zero;
+        for (int c = 0; c < CH; ++c) ar[c] = asrc[c][sn * 8];
       }
+      s = sn;
 #pragma unroll
       for (int tg = 0; tg < NG; ++tg) {
         acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[buf][tg][0][lane], b0, acc[tg], 0, 0, 0);
@@ -1261,6 +1271,17 @@ static void launch_gemv_dec_ng(const DevMatrix& W, const int8_t* limbs, uint32_t
 #undef DET_GEMV_DEC
 }
 
+static uint64_t device_cus() {
+  static const uint64_t n = [] {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    return uint64_t(cus);
+  }();
+  return n;
+}
+
 template <int NG>
 static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                                int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
@@ -1270,11 +1291,13 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
                                  : reinterpret_cast<const void*>(&k_gemv_dec_wg<0, NG>);
   const uint64_t cap = resident_blocks(fn, 256);
   const uint64_t groups = (ntiles + 3) / 4;
-  // K chunks across workgroups (atomic outputs only) while the launch stays
-  // resident, keeping at least two K steps per chunk
+  // K chunks across workgroups (atomic outputs only) up to about 2.5
+  // workgroups per CU (measured best at E4B shapes), keeping at least two K
+  // steps per chunk
   uint32_t kc = 1;
+  const uint64_t target = device_cus() * 5 / 2;
   if (acc)
-    while (groups * kc * 2 <= cap && nsteps >= uint64_t(kc) * 2 * 2) kc *= 2;
+    while (groups * kc * 2 <= target && nsteps >= uint64_t(kc) * 2 * 2) kc *= 2;
   const uint64_t g = std::min<uint64_t>(groups, std::max<uint64_t>(cap / kc, 1));
   if (epilogue == 1)
     hipLaunchKernelGGL((k_gemv_dec_wg<1, NG>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum, limbs,
