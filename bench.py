@@ -153,7 +153,7 @@ def ragged_batch(ctx, rd, args, model) -> dict:
     ctx.synchronize()
     prefill_s = time.perf_counter() - t0
     # solo copies of the shortest and longest sequence, to check the batch against
-    check = [int(np.argmin(lens)), int(np.argmax(lens))]
+    check = [] if getattr(args, "no_solo_check", False) else [int(np.argmin(lens)), int(np.argmax(lens))]
     solo = {i: sess[i].clone() for i in check}
     first = toks[:]
     out = [[] for _ in range(n)]
@@ -180,8 +180,8 @@ def ragged_batch(ctx, rd, args, model) -> dict:
         "ms_per_batched_step": round(dec_s / steps * 1e3, 3),
         "sequences": n, "steps": steps, "prompt_lens": [int(k) for k in lens],
         "prefill_s": round(prefill_s, 3),
-        "solo_tokens_identical": bool(same),
-        "solo_check": f"shortest and longest sequence decoded alone for {n_check} steps",
+        "solo_tokens_identical": bool(same) if solo else None,
+        "solo_check": f"shortest and longest sequence decoded alone for {n_check} steps" if solo else "skipped",
     }
 
 
@@ -275,6 +275,8 @@ def main() -> int:
     ap.add_argument("--ragged-only", action="store_true", help="only the ragged multi-sequence decode measurement")
     ap.add_argument("--eager", action="store_true",
                     help="launch decode kernels directly instead of replaying graphs (for kernel tracing)")
+    ap.add_argument("--no-solo-check", action="store_true",
+                    help="skip the solo re-decode of two ragged sequences (profiling runs)")
     ap.add_argument("--ragged-seqs", type=int, default=16)
     ap.add_argument("--ragged-steps", type=int, default=128)
     ap.add_argument("--e4b-layers", type=int, default=42)

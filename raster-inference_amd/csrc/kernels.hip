@@ -462,34 +462,25 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
     v4i acc[NG];
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
-    // workgroups walk their K range from different starting steps, so at
-    // any moment they read different A lines (a common order makes every
-    // workgroup request the same few L2 lines at once); the sums are exact in
-    // any order
-    const uint64_t len = cs1 - cs0;
-    const uint64_t first = len ? cs0 + (blockIdx.x / kchunks) % len : cs0;
     v4i b0 = zero, b1 = zero, ar[CH];
-    if (len) {
-      b0 = __builtin_nontemporal_load(bp + first * 128);
-      b1 = __builtin_nontemporal_load(bp + first * 128 + 1);
+    if (cs0 < cs1) {
+      b0 = __builtin_nontemporal_load(bp + cs0 * 128);
+      b1 = __builtin_nontemporal_load(bp + cs0 * 128 + 1);
 #pragma unroll
-      for (int c = 0; c < CH; ++c) ar[c] = asrc[c][first * 8];
+      for (int c = 0; c < CH; ++c) ar[c] = asrc[c][cs0 * 8];
     }
-    uint64_t s = first;
-    for (uint64_t j = 0; j < len; ++j) {
-      const int buf = int(j & 1);
+    for (uint64_t s = cs0; s < cs1; ++s) {
+      const int buf = int((s - cs0) & 1);
 #pragma unroll
       for (int c = 0; c < CH; ++c) (&al[buf][0][0][0])[threadIdx.x + 256 * c] = ar[c];
       __syncthreads();
       v4i n0 = zero, n1 = zero;
-      const uint64_t sn = s + 1 == cs1 ? cs0 : s + 1;
-      if (j + 1 < len) {
-        n0 = __builtin_nontemporal_load(bp + sn * 128);
-        n1 = __builtin_nontemporal_load(bp + sn * 128 + 1);
+      if (s + 1 < cs1) {
+        n0 = __builtin_nontemporal_load(bp + (s + 1) * 128);
+        n1 = __builtin_nontemporal_load(bp + (s + 1) * 128 + 1);
 #pragma unroll
-        for (int c = 0; c < CH; ++c) ar[c] = asrc[c][sn * 8];
+        for (int c = 0; c < CH; ++c) ar[c] = asrc[c][(s + 1) * 8];
       }
-      s = sn;
 #pragma unroll
       for (int tg = 0; tg < NG; ++tg) {
         acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[buf][tg][0][lane], b0, acc[tg], 0, 0, 0);
