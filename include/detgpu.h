@@ -240,6 +240,53 @@ int det_capture(det_model_t* model, const uint32_t* prompt, uint64_t prompt_len,
                 size_t out_cap);
 
 /* ------------------------------------------------------------------------ */
+/* Checkpoint trace (runtime/trace.rs, runtime/sequence.rs)                  */
+/* ------------------------------------------------------------------------ */
+/* SamplingConfig (src/shared/api/input.rs:45-50); has_* = Some(..). */
+typedef struct det_sampling {
+  int32_t has_max_new_tokens;
+  uint64_t max_new_tokens;
+  int32_t has_temperature;
+  float temperature;
+  int32_t has_top_k;
+  uint64_t top_k;
+  int32_t has_top_p;
+  float top_p;
+} det_sampling_t;
+
+/* Text of generated token ids (the tokenizer's decode with special tokens
+ * skipped, output_finalize/native/tiles.rs:5-13). Writes up to cap bytes of
+ * UTF-8 plus a NUL into out and returns the text length; a length >= cap asks
+ * for a call with a larger buffer; a negative value is a failure. */
+typedef int64_t (*det_detokenize_fn)(const uint32_t* ids, uint64_t n, char* out, size_t cap, void* user);
+
+typedef struct det_trace_request {
+  const char* prompt_text;          /* prompt.prepare's decoded prompt text (UTF-8) */
+  const uint32_t* prompt_token_ids; /* the rendered prompt's token ids (prompt_prepare::tokenize_prompt) */
+  uint64_t prompt_token_count;
+  det_sampling_t sampling;          /* max_new_tokens (None = 0); temperature must be 1, no top_k / top_p */
+  int32_t prompt_checkpoint;        /* emit prompt.prepare (det runs with an authenticated tokenizer source) */
+  const char* terminal_checkpoint;  /* NULL, "checkpoint" or "checkpoint:occurrence" */
+  uint64_t prefill_token_range_width; /* 0 = unbounded (InferenceControls default) */
+  uint64_t decode_layer_range_width;  /* 0 = unbounded */
+  det_detokenize_fn detokenize;     /* needed once a token is generated */
+  void* detokenize_user;
+} det_trace_request_t;
+
+/* Runs the native deterministic sequence with checkpoint commitment
+ * (runtime/sequence.rs; runtime/executors/native.rs:60-450): prompt.prepare,
+ * input.embedding, prefill.prepare_aux, prefill.range / prefill.range_finalize
+ * per layer, prefill.finalize, then per generated token decode.select_token,
+ * decode.layer_range(s) and decode.transition_finalize, and output.finalize.
+ * Writes the checkpoint trace artifact (serde_json pretty array of
+ * {checkpoint: sha256(payload)}, runtime/trace.rs:262-330, 555-566) plus a
+ * NUL into out; *out_len is its length. *paused = 1 when the terminal
+ * checkpoint was reached. On an error the artifact of the checkpoints so far is
+ * still written (abort_inference_trace) and the status is nonzero. */
+int det_trace_run(det_model_t* model, const det_trace_request_t* request, char* out, size_t out_cap, size_t* out_len,
+                  int32_t* paused);
+
+/* ------------------------------------------------------------------------ */
 /* Synthetic workloads (no reference counterpart; random-init benchmarks)    */
 /* ------------------------------------------------------------------------ */
 /* Fills q[rows*cols] and s[rows] with counter-hash weights: q in [-127, 127],

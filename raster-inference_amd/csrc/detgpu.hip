@@ -9,7 +9,10 @@
 #include <openssl/sha.h>
 
 #include <algorithm>
+#include <cfloat>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -1013,7 +1016,18 @@ void logits_from(det_session* s, const int32_t* hidden_row) {
   s->logits_valid = true;
 }
 
-void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, det_prefill_result_t* out) {
+// Observer of the prefill pass (checkpoint traces). Each callback returns
+// true to stop the pass there (a terminal checkpoint was reached).
+struct PrefillHook {
+  virtual bool after_embedding(det_session* s, uint64_t n) = 0;
+  virtual bool after_layer(det_session* s, uint64_t l, uint64_t n) = 0;
+  virtual ~PrefillHook() = default;
+};
+
+// Returns false when the hook stopped the pass early (the session is then
+// left mid-prefill and must not be used further).
+bool prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, det_prefill_result_t* out,
+             PrefillHook* hook = nullptr) {
   det_model* m = s->m;
   det_ctx* ctx = m->ctx;
   hipStream_t st = ctx->stream;
@@ -1031,6 +1045,7 @@ void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
     HIPC(hipStreamSynchronize(st));
     commit_rows(host.data(), n, H, out->embedding);
   }
+  if (hook && hook->after_embedding(s, n)) return false;
   const uint64_t P = m->ple_dim;
   if (m->has_ple)
     for (uint64_t l = 0; l < m->layers.size(); ++l)
@@ -1075,6 +1090,7 @@ void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
     if (a.avail > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
     det::launch_attention(a, st);
     post_attention(s, L, n, (m->has_ple && L.has_ple) ? s->ple_all + l * n * P : nullptr);
+    if (hook && hook->after_layer(s, l, n)) return false;
   }
   if (flags & DET_COMMIT_ACTIVATIONS) {
     host.resize(n * H);
@@ -1093,6 +1109,7 @@ void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
   out->kv[0] = 0;
   if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
   out->next_token = ctx->argmax(s->logits, m->vocab);
+  return true;
 }
 
 // Cache bookkeeping after n tokens with canonical slots (token t at t % cap
@@ -1103,12 +1120,16 @@ void kv_advance(GKv& c, uint64_t n) {
   c.start = c.ring ? (n - c.len) % c.cap : 0;
 }
 
+// Observer of a per-op decode step; after_layer returns true to stop the
+// step there (a terminal checkpoint was reached).
 struct LayerHook {
-  virtual void after_layer(det_session* s, uint64_t l) = 0;
+  virtual bool after_layer(det_session* s, uint64_t l) = 0;
   virtual ~LayerHook() = default;
 };
 
-void decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t* out, LayerHook* hook) {
+// Returns false when the hook stopped the step early (the session is then
+// left mid-step and must not be used further).
+bool decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t* out, LayerHook* hook) {
   det_model* m = s->m;
   det_ctx* ctx = m->ctx;
   hipStream_t st = ctx->stream;
@@ -1155,7 +1176,7 @@ void decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
     if (count > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
     det::launch_attention(a, st);
     post_attention(s, L, 1, (m->has_ple && L.has_ple) ? s->pe : nullptr);
-    if (hook) hook->after_layer(s, l);
+    if (hook && hook->after_layer(s, l)) return false;
   }
   std::vector<int32_t> host;
   if (flags & DET_COMMIT_ACTIVATIONS) {
@@ -1175,6 +1196,7 @@ void decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
   out->kv[0] = 0;
   if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
   out->next_token = ctx->argmax(s->logits, m->vocab);
+  return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -1768,7 +1790,7 @@ std::unique_ptr<det_session> clone_session(const det_session* src) {
 struct FirstStepHook : LayerHook {
   det_session* original = nullptr;
   std::string json;
-  void after_layer(det_session* s, uint64_t l) override {
+  bool after_layer(det_session* s, uint64_t l) override {
     det_model* m = s->m;
     std::vector<int32_t> host(m->hidden);
     HIPC(hipMemcpyAsync(host.data(), s->x, m->hidden * 4, hipMemcpyDeviceToHost, m->ctx->stream));
@@ -1780,6 +1802,7 @@ struct FirstStepHook : LayerHook {
     const bool has = commit_kv(s, eff, kv);
     if (!json.empty()) json += ",";
     json += std::string("{\"layer_output\":\"") + out + "\",\"kv\":" + (has ? "\"" + std::string(kv) + "\"" : "null") + "}";
+    return false;
   }
 };
 
@@ -1821,6 +1844,406 @@ std::string capture(det_model* m, const uint32_t* ids, uint64_t n, uint64_t step
   h.hex(hx);
   out += "],\"end_to_end\":{\"generated_token_ids\":" + ids_json + ",\"generated_token_ids_sha256\":\"" + hx + "\"}}";
   return out;
+}
+
+// ---------------------------------------------------------------------------
+// Checkpoint trace: the native deterministic sequence (runtime/sequence.rs,
+// runtime/executors/native.rs:60-450) with checkpoint commitment. Every
+// committed checkpoint adds {name: sha256(compact JSON payload)}
+// (runtime/trace.rs:262-330, 425-430); the artifact is the pretty-printed
+// array (trace.rs:555-566). Payloads are serde_json maps, whose keys are
+// ordered bytewise, so they are written here from std::map.
+// ---------------------------------------------------------------------------
+// serde_json string escaping: quote, backslash and control characters; all
+// other bytes, non-ASCII UTF-8 included, are copied.
+std::string json_str(const std::string& v) {
+  std::string o = "\"";
+  for (unsigned char ch : v) {
+    switch (ch) {
+      case '"': o += "\\\""; break;
+      case '\\': o += "\\\\"; break;
+      case '\b': o += "\\b"; break;
+      case '\f': o += "\\f"; break;
+      case '\n': o += "\\n"; break;
+      case '\r': o += "\\r"; break;
+      case '\t': o += "\\t"; break;
+      default:
+        if (ch < 0x20) {
+          char b[8];
+          snprintf(b, sizeof b, "\\u%04x", unsigned(ch));
+          o += b;
+        } else {
+          o += char(ch);
+        }
+    }
+  }
+  return o + "\"";
+}
+
+// A finite f32 as serde_json writes it: the shortest digit string that reads
+// back as the same f32, in plain notation when the decimal point falls within
+// [-5, 13] places (with ".0" for whole numbers), else d.ddde<exp>.
+std::string json_f32(float v) {
+  if (!std::isfinite(v)) return "null";
+  if (v == 0.0f) return std::signbit(v) ? "-0.0" : "0.0";
+  char buf[64];
+  int p = 1;
+  for (; p <= 9; ++p) {
+    snprintf(buf, sizeof buf, "%.*e", p - 1, double(v));
+    if (strtof(buf, nullptr) == v) break;
+  }
+  std::string t(buf);
+  std::string sign;
+  if (t[0] == '-') {
+    sign = "-";
+    t = t.substr(1);
+  }
+  const size_t epos = t.find('e');
+  const int e = std::atoi(t.c_str() + epos + 1);
+  std::string d;
+  for (size_t i = 0; i < epos; ++i)
+    if (t[i] != '.') d += t[i];
+  while (d.size() > 1 && d.back() == '0') d.pop_back();
+  const int len = int(d.size()), kk = e + 1;  // decimal point after kk digits
+  std::string o;
+  if (kk >= len && kk <= 13) {
+    o = d + std::string(size_t(kk - len), '0') + ".0";
+  } else if (kk > 0 && kk <= 13) {
+    o = d.substr(0, size_t(kk)) + "." + d.substr(size_t(kk));
+  } else if (kk > -6 && kk <= 0) {
+    o = "0." + std::string(size_t(-kk), '0') + d;
+  } else {
+    o = d.substr(0, 1) + (len > 1 ? "." + d.substr(1) : std::string()) + "e" + std::to_string(kk - 1);
+  }
+  return sign + o;
+}
+
+std::string json_u32s(const std::vector<uint32_t>& v) {
+  std::string o = "[";
+  for (size_t i = 0; i < v.size(); ++i) o += (i ? "," : "") + std::to_string(v[i]);
+  return o + "]";
+}
+
+std::string json_hex_or_null(const char* hex, bool has) { return has ? json_str(hex) : "null"; }
+
+std::string json_obj(const std::map<std::string, std::string>& o) {
+  std::string s = "{";
+  bool first = true;
+  for (const auto& kv : o) {
+    if (!first) s += ",";
+    first = false;
+    s += json_str(kv.first) + ":" + kv.second;
+  }
+  return s + "}";
+}
+
+std::string sha_hex(const std::string& bytes) {
+  Sha h;
+  h.put(bytes.data(), bytes.size());
+  char out[65];
+  h.hex(out);
+  return out;
+}
+
+struct TraceCollector {
+  std::vector<std::pair<std::string, std::string>> entries;  // checkpoint, sha256 of its payload
+  bool has_terminal = false, reached = false;
+  std::string terminal_id;
+  uint64_t occurrence = 1, seen = 0;
+
+  // TerminalCheckpointSpec::parse (trace.rs): "id" or "id:occurrence".
+  void set_terminal(const char* spec) {
+    if (!spec || !*spec) return;
+    std::string s(spec);
+    const size_t colon = s.rfind(':');
+    if (colon != std::string::npos) {
+      const std::string n = s.substr(colon + 1);
+      if (n.empty() || n.find_first_not_of("0123456789") != std::string::npos)
+        bail("terminal checkpoint occurrence must be a positive integer");
+      occurrence = std::stoull(n);
+      if (occurrence == 0) bail("terminal checkpoint occurrence must be a positive integer");
+      s = s.substr(0, colon);
+    }
+    if (s.empty()) bail("terminal checkpoint id must not be empty");
+    terminal_id = s;
+    has_terminal = true;
+  }
+  // mark_terminal_checkpoint (trace.rs:465-480)
+  bool mark(const std::string& name) {
+    if (!has_terminal) return false;
+    if (reached || name != terminal_id) return reached;
+    if (++seen == occurrence) reached = true;
+    return reached;
+  }
+  // trace_checkpoint_lazy (trace.rs:266-288); layer_token checkpoints are
+  // never committed (trace.rs:451-454), so their payload is not built.
+  template <class F>
+  bool checkpoint(const std::string& name, F&& payload) {
+    const bool commit = name.rfind("prefill.layer_token.", 0) != 0 && name.rfind("decode.layer_token.", 0) != 0;
+    const bool r = mark(name);
+    if (commit) entries.push_back({name, sha_hex(payload())});
+    return r;
+  }
+  // serde_json::to_vec_pretty of the array of single-entry maps
+  std::string artifact() const {
+    if (entries.empty()) return "[]";
+    std::string o = "[\n";
+    for (size_t i = 0; i < entries.size(); ++i) {
+      o += "  {\n    " + json_str(entries[i].first) + ": " + json_str(entries[i].second) + "\n  }";
+      o += i + 1 < entries.size() ? ",\n" : "\n";
+    }
+    return o + "]";
+  }
+};
+
+const char* const kDetMode = "\"deterministic\"";
+
+// prefill.prepare_aux / input.embedding / prefill.range / range_finalize /
+// layer_token marks from the prefill pass
+// (runtime/executors/native.rs:60-263, routines/input_embedding/mod.rs:88-130,
+// routines/prefill_prepare_aux/mod.rs:175-210, routines/prefill_range/mod.rs:36-88,
+// routines/prefill_range_finalize/mod.rs:17-73,
+// routines/prefill_range/native/deterministic_tiles.rs:140-190).
+struct TracePrefill : PrefillHook {
+  TraceCollector& tc;
+  std::string ids_json, ids_sha;
+  uint64_t width;  // prefill token range width (0 = unbounded)
+  std::vector<std::string> completed;
+  std::vector<int32_t> host;
+  TracePrefill(TraceCollector& t, std::string ij, std::string is, uint64_t w)
+      : tc(t), ids_json(std::move(ij)), ids_sha(std::move(is)), width(w) {}
+  bool after_embedding(det_session* s, uint64_t n) override {
+    const uint64_t H = s->m->hidden;
+    host.resize(n * H);
+    HIPC(hipMemcpyAsync(host.data(), s->x, n * H * 4, hipMemcpyDeviceToHost, s->m->ctx->stream));
+    HIPC(hipStreamSynchronize(s->m->ctx->stream));
+    char emb[65];
+    commit_rows(host.data(), n, H, emb);
+    if (tc.checkpoint("input.embedding", [&] {
+          return json_obj({{"det_embedded_prompt_activations_sha256", json_str(emb)},
+                           {"prompt_token_ids", ids_json},
+                           {"prompt_token_ids_sha256", json_str(ids_sha)},
+                           {"raster", "null"}});
+        }))
+      return true;
+    return tc.checkpoint("prefill.prepare_aux", [&] {
+      return json_obj({{"det_embedded_prompt_activations_sha256", json_str(emb)},
+                       {"prompt_token_ids", ids_json},
+                       {"prompt_token_ids_sha256", json_str(ids_sha)}});
+    });
+  }
+  bool after_layer(det_session* s, uint64_t l, uint64_t n) override {
+    const uint64_t H = s->m->hidden;
+    host.resize(n * H);
+    HIPC(hipMemcpyAsync(host.data(), s->x, n * H * 4, hipMemcpyDeviceToHost, s->m->ctx->stream));
+    HIPC(hipStreamSynchronize(s->m->ctx->stream));
+    char all[65];
+    commit_rows(host.data(), n, H, all);
+    completed.push_back(all);
+    // range_bounds (prefill_range/mod.rs:25-34)
+    const uint64_t w = std::min<uint64_t>(std::max<uint64_t>(width ? width : UINT64_MAX, 1), std::max<uint64_t>(n, 1));
+    for (uint64_t a = 0; a < n; a += w) {
+      const uint64_t b = std::min(n, a + w);
+      if (tc.checkpoint("prefill.range", [&] {
+            char rc[65];
+            commit_rows(host.data() + a * H, b - a, H, rc);
+            return json_obj({{"det_range_activations_sha256", json_str(rc)},
+                             {"execution_mode", kDetMode},
+                             {"layer_idx", std::to_string(l)},
+                             {"range_end", std::to_string(b)},
+                             {"range_start", std::to_string(a)},
+                             {"token_count", std::to_string(n)}});
+          }))
+        return true;
+    }
+    if (tc.checkpoint("prefill.range_finalize", [&] {
+          std::vector<const GKv*> caches;
+          for (uint64_t j = 0; j <= l; ++j) caches.push_back(&s->kv[j]);
+          char kv[65];
+          const bool has = commit_kv(s, caches, kv);
+          std::string list = "[";
+          for (size_t i = 0; i < completed.size(); ++i) list += (i ? "," : "") + json_str(completed[i]);
+          list += "]";
+          return json_obj({{"completed_layer_output_det_sha256s", list},
+                           {"det_current_activations_sha256", json_str(all)},
+                           {"det_layer_caches_sha256", json_hex_or_null(kv, has)},
+                           {"execution_mode", kDetMode},
+                           {"next_layer_idx", std::to_string(l + 1)}});
+        }))
+      return true;
+    for (uint64_t t = 0; t < n; ++t)
+      if (tc.mark("prefill.layer_token.layer_" + std::to_string(l) + ".token_" + std::to_string(t))) return true;
+    return false;
+  }
+};
+
+// decode.layer_range checkpoints of one decode step
+// (routines/decode_layer_range/mod.rs:553-664, native/tiles.rs:35-70):
+// after each layer range, the current activation, the effective caches
+// (updated layers, then the untouched ones) and the layer outputs so far.
+struct TraceDecode : LayerHook {
+  TraceCollector& tc;
+  uint32_t token;
+  uint64_t position, layers, width, range_start = 0;
+  std::vector<std::string> completed;
+  std::vector<int32_t> host;
+  TraceDecode(TraceCollector& t, uint32_t tok, uint64_t pos, uint64_t nl, uint64_t w)
+      : tc(t), token(tok), position(pos), layers(nl), width(std::min<uint64_t>(std::max<uint64_t>(w ? w : UINT64_MAX, 1), std::max<uint64_t>(nl, 1))) {}
+  bool after_layer(det_session* s, uint64_t l) override {
+    const uint64_t H = s->m->hidden;
+    host.resize(H);
+    HIPC(hipMemcpyAsync(host.data(), s->x, H * 4, hipMemcpyDeviceToHost, s->m->ctx->stream));
+    HIPC(hipStreamSynchronize(s->m->ctx->stream));
+    char act[65];
+    commit_rows(host.data(), 1, H, act);
+    completed.push_back(act);
+    const uint64_t range_end = std::min(layers, range_start + width);
+    if (l + 1 != range_end) return false;
+    const uint64_t start = range_start;
+    range_start = range_end;
+    return tc.checkpoint("decode.layer_range", [&] {
+      char kv[65];
+      const bool has = commit_kv(s, all_caches(s), kv);
+      std::string list = "[";
+      for (size_t i = 0; i < completed.size(); ++i) list += (i ? "," : "") + json_str(completed[i]);
+      list += "]";
+      return json_obj({{"completed_layer_output_det_sha256s", list},
+                       {"decode_position", std::to_string(position)},
+                       {"decode_token_count", std::to_string(position)},
+                       {"det_current_activation_sha256", json_str(act)},
+                       {"det_layer_caches_sha256", json_hex_or_null(kv, has)},
+                       {"execution_mode", kDetMode},
+                       {"layer_count", std::to_string(layers)},
+                       {"layer_end", std::to_string(range_end)},
+                       {"layer_start", std::to_string(start)},
+                       {"next_token", std::to_string(token)}});
+    });
+  }
+};
+
+// SamplingConfig (shared/api/input.rs:45-50) as serialized into prompt.prepare.
+std::string sampling_json(const det_sampling_t& sp) {
+  return std::string("{\"max_new_tokens\":") + (sp.has_max_new_tokens ? std::to_string(sp.max_new_tokens) : "null") +
+         ",\"temperature\":" + (sp.has_temperature ? json_f32(sp.temperature) : "null") +
+         ",\"top_k\":" + (sp.has_top_k ? std::to_string(sp.top_k) : "null") +
+         ",\"top_p\":" + (sp.has_top_p ? json_f32(sp.top_p) : "null") + "}";
+}
+
+// Runs the traced sequence; returns true when it paused at the terminal
+// checkpoint. On an error the collector keeps the checkpoints so far, as
+// abort_inference_trace does.
+bool trace_run(det_model* m, const det_trace_request_t* rq, TraceCollector& tc) {
+  if (!rq) bail("trace request is required");
+  tc.set_terminal(rq->terminal_checkpoint);
+  if (!rq->prompt_text || !*rq->prompt_text) bail("input embedding requires a non-empty prompt");
+  if (!rq->prompt_token_ids || rq->prompt_token_count == 0)
+    bail("transformer layer execution requires at least one activation row");
+  const std::vector<uint32_t> ids(rq->prompt_token_ids, rq->prompt_token_ids + rq->prompt_token_count);
+  const uint64_t n = ids.size();
+  const std::string ids_json = json_u32s(ids), ids_sha = sha_hex(ids_json);
+  // prompt.prepare (executors/native.rs:68-90): emitted when an authenticated
+  // tokenizer source accompanies a deterministic run
+  if (rq->prompt_checkpoint &&
+      tc.checkpoint("prompt.prepare", [&] {
+        return json_obj({{"prompt_text", json_str(rq->prompt_text)},
+                         {"prompt_token_ids", ids_json},
+                         {"prompt_token_ids_sha256", json_str(ids_sha)},
+                         {"sampling", sampling_json(rq->sampling)}});
+      }))
+    return true;
+  const uint64_t max_new = rq->sampling.has_max_new_tokens ? rq->sampling.max_new_tokens : 0;
+  det_session sess;
+  sess.m = m;
+  sess.max_tokens = n + max_new + 1;
+  session_alloc(&sess);
+  TracePrefill ph(tc, ids_json, ids_sha, rq->prefill_token_range_width);
+  det_prefill_result_t pr{};
+  if (!prefill(&sess, ids.data(), n, DET_COMMIT_ALL, &pr, &ph)) return true;
+  // prefill.finalize (prefill_finalize/native/tiles.rs:68-94)
+  if (tc.checkpoint("prefill.finalize", [&] {
+        return json_obj({{"decode_position", std::to_string(n)},
+                         {"decode_token_count", std::to_string(n)},
+                         {"det_final_hidden_states_sha256", json_str(pr.final_hidden)},
+                         {"det_layer_caches_sha256", json_hex_or_null(pr.kv, pr.kv[0] != 0)},
+                         {"det_prefill_logits_sha256", json_str(pr.logits)}});
+      }))
+    return true;
+  // validate_sampling_config (runtime/pipeline.rs:22-40)
+  if (rq->sampling.has_temperature && std::fabs(rq->sampling.temperature - 1.0f) > FLT_EPSILON)
+    bail("output decode only supports deterministic greedy decode; expected temperature 1, got " +
+         json_f32(rq->sampling.temperature));
+  if (rq->sampling.has_top_k) bail("output decode does not support top_k yet, got " + std::to_string(rq->sampling.top_k));
+  if (rq->sampling.has_top_p) bail("output decode does not support top_p yet, got " + json_f32(rq->sampling.top_p));
+  // the output decode loop (executors/native.rs:265-450)
+  std::vector<uint32_t> full = ids, gen;
+  std::string logits = pr.logits;
+  uint32_t next = pr.next_token;
+  const uint64_t nl = m->layers.size();
+  for (;;) {
+    if (gen.size() >= max_new) {
+      // output.finalize (output_finalize/mod.rs:18-52)
+      std::string text;
+      if (!gen.empty()) {
+        if (!rq->detokenize) bail("output.finalize requires a detokenize callback");
+        std::vector<char> buf(4096);
+        for (;;) {
+          const int64_t len = rq->detokenize(gen.data(), gen.size(), buf.data(), buf.size(), rq->detokenize_user);
+          if (len < 0) bail("detokenize callback failed");
+          if (uint64_t(len) < buf.size()) {
+            text.assign(buf.data(), size_t(len));
+            break;
+          }
+          buf.resize(size_t(len) + 1);
+        }
+      }
+      const std::string full_json = json_u32s(full), gen_json = json_u32s(gen);
+      tc.checkpoint("output.finalize", [&] {
+        return json_obj({{"full_token_ids", full_json},
+                         {"full_token_ids_sha256", json_str(sha_hex(full_json))},
+                         {"generated_text", json_str(text)},
+                         {"generated_token_count", std::to_string(gen.size())},
+                         {"generated_token_ids", gen_json},
+                         {"generated_token_ids_sha256", json_str(sha_hex(gen_json))},
+                         {"stop_reason", "\"max_new_tokens\""}});
+      });
+      return tc.reached;
+    }
+    // decode.select_token (decode_select_token/mod.rs:19-47, 362-390)
+    const uint32_t t = next;
+    full.push_back(t);
+    gen.push_back(t);
+    const uint64_t pos = sess.position;
+    const std::string full_json = json_u32s(full), gen_json = json_u32s(gen);
+    if (tc.checkpoint("decode.select_token", [&] {
+          return json_obj({{"decode_position", std::to_string(pos)},
+                           {"decode_token_count", std::to_string(pos)},
+                           {"det_current_logits_sha256", json_str(logits)},
+                           {"full_token_ids", full_json},
+                           {"full_token_ids_sha256", json_str(sha_hex(full_json))},
+                           {"generated_token_ids", gen_json},
+                           {"generated_token_ids_sha256", json_str(sha_hex(gen_json))},
+                           {"max_new_tokens", std::to_string(max_new)},
+                           {"selected_next_token", std::to_string(t)}});
+        }))
+      return true;
+    // decode.layer_range(s), then decode.transition_finalize
+    // (decode_transition_finalize/mod.rs:67-99)
+    TraceDecode dh(tc, t, pos, nl, rq->decode_layer_range_width);
+    det_decode_result_t dr{};
+    if (!decode(&sess, t, DET_COMMIT_ALL, &dr, &dh)) return true;
+    logits = dr.logits;
+    next = dr.next_token;
+    if (tc.checkpoint("decode.transition_finalize", [&] {
+          return json_obj({{"decode_position", std::to_string(pos + 1)},
+                           {"decode_token_count", std::to_string(pos + 1)},
+                           {"det_current_logits_sha256", json_str(logits)},
+                           {"full_token_ids", full_json},
+                           {"full_token_ids_sha256", json_str(sha_hex(full_json))},
+                           {"generated_token_ids", gen_json},
+                           {"generated_token_ids_sha256", json_str(sha_hex(gen_json))}});
+        }))
+      return true;
+  }
 }
 
 }  // namespace
@@ -2153,6 +2576,31 @@ int det_capture(det_model_t* m, const uint32_t* prompt, uint64_t n, uint64_t ste
     if (s.size() + 1 > cap) bail("capture output buffer too small: need " + std::to_string(s.size() + 1));
     std::memcpy(out, s.c_str(), s.size() + 1);
   });
+}
+
+int det_trace_run(det_model_t* m, const det_trace_request_t* request, char* out, size_t out_cap, size_t* out_len,
+                  int32_t* paused) {
+  if (!m) {
+    g_error = "model is required";
+    return 1;
+  }
+  TraceCollector tc;
+  bool p = false;
+  int st = guarded(m->ctx, [&] {
+    if (!m->finalized) bail("model is not finalized");
+    p = trace_run(m, request, tc);
+  });
+  const std::string art = tc.artifact();
+  if (out_len) *out_len = art.size();
+  if (paused) *paused = p ? 1 : 0;
+  if (out && out_cap > art.size()) {
+    std::memcpy(out, art.data(), art.size());
+    out[art.size()] = 0;
+  } else if (st == 0) {
+    m->ctx->last_error = "trace artifact buffer too small: need " + std::to_string(art.size() + 1) + " bytes";
+    st = 1;
+  }
+  return st;
 }
 
 }  // extern "C"

@@ -135,6 +135,34 @@ class DecodeResult(C.Structure):
                 ("next_token", C.c_uint32)]
 
 
+class Sampling(C.Structure):
+    """det_sampling_t: SamplingConfig (shared/api/input.rs:45-50)."""
+
+    _fields_ = [("has_max_new_tokens", C.c_int32), ("max_new_tokens", C.c_uint64),
+                ("has_temperature", C.c_int32), ("temperature", C.c_float),
+                ("has_top_k", C.c_int32), ("top_k", C.c_uint64),
+                ("has_top_p", C.c_int32), ("top_p", C.c_float)]
+
+
+DETOKENIZE_FN = C.CFUNCTYPE(C.c_int64, C.POINTER(C.c_uint32), C.c_uint64, C.c_void_p, C.c_size_t, C.c_void_p)
+
+
+class TraceRequest(C.Structure):
+    _fields_ = [("prompt_text", C.c_char_p), ("prompt_token_ids", C.POINTER(C.c_uint32)),
+                ("prompt_token_count", C.c_uint64), ("sampling", Sampling), ("prompt_checkpoint", C.c_int32),
+                ("terminal_checkpoint", C.c_char_p), ("prefill_token_range_width", C.c_uint64),
+                ("decode_layer_range_width", C.c_uint64), ("detokenize", DETOKENIZE_FN),
+                ("detokenize_user", C.c_void_p)]
+
+
+class TraceError(DetError):
+    """A failed traced run; .artifact holds the trace of the checkpoints before the failure."""
+
+    def __init__(self, status: int, message: str, artifact: bytes):
+        super().__init__(status, message)
+        self.artifact = artifact
+
+
 _LIB = None
 C = C  # ctypes, re-exported for callers that pass raw pointers
 
@@ -193,6 +221,8 @@ def lib() -> C.CDLL:
         "det_session_logits": (C.c_int, [P, i32p, u64]),
         "det_session_position": (C.c_int, [P, C.POINTER(u64)]),
         "det_capture": (C.c_int, [P, P, u64, u64, C.c_char_p, C.c_size_t]),
+        "det_trace_run": (C.c_int, [P, C.POINTER(TraceRequest), C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t),
+                                    C.POINTER(C.c_int32)]),
         "det_synthetic_int8": (C.c_int, [u64, u64, u64, C.c_int32, P, P]),
     }
     for name, (res, args) in sig.items():
@@ -464,6 +494,50 @@ class Model:
         buf = C.create_string_buffer((1 << 20) + decode_steps * 512)
         self.ctx.check(self.ctx.lib.det_capture(self.handle, _ptr(ids), ids.size, decode_steps, buf, len(buf)))
         return json.loads(buf.value.decode())
+
+    def trace(self, prompt_text: str, prompt_token_ids, max_new_tokens=None, temperature=1.0, top_k=None,
+              top_p=None, detokenize=None, prompt_checkpoint: bool = True, terminal_checkpoint=None,
+              prefill_token_range_width: int = 0, decode_layer_range_width: int = 0):
+        """Runs the native deterministic sequence with checkpoint commitment and
+        returns (trace artifact bytes, paused). detokenize(ids) -> str decodes
+        generated ids (special tokens skipped). None means an Option left unset."""
+        ids = np.ascontiguousarray(prompt_token_ids, dtype=np.uint32)
+        sp = Sampling(max_new_tokens is not None, max_new_tokens or 0, temperature is not None,
+                      temperature if temperature is not None else 0.0, top_k is not None, top_k or 0,
+                      top_p is not None, top_p if top_p is not None else 0.0)
+        errors = []
+
+        def detok(ptr_ids, n, out, cap, _user):
+            try:
+                text = detokenize([ptr_ids[i] for i in range(n)]).encode()
+                if len(text) < cap:
+                    C.memmove(out, text + b"\0", len(text) + 1)
+                return len(text)
+            except Exception as e:  # noqa: BLE001 - reported through the status
+                errors.append(e)
+                return -1
+
+        cb = DETOKENIZE_FN(detok) if detokenize is not None else DETOKENIZE_FN()
+        req = TraceRequest(prompt_text.encode(), ids.ctypes.data_as(C.POINTER(C.c_uint32)), ids.size, sp,
+                           int(prompt_checkpoint), terminal_checkpoint.encode() if terminal_checkpoint else None,
+                           prefill_token_range_width, decode_layer_range_width, cb, None)
+        cap = 1 << 16
+        while True:
+            buf = C.create_string_buffer(cap)
+            n = C.c_size_t()
+            paused = C.c_int32()
+            st = self.ctx.lib.det_trace_run(self.handle, C.byref(req), buf, cap, C.byref(n), C.byref(paused))
+            if st == 1 and n.value + 1 > cap and b"buffer too small" in (self.ctx.lib.det_ctx_last_error(self.ctx.handle) or b""):
+                cap = n.value + 1
+                continue
+            break
+        artifact = buf.raw[:n.value]
+        if st != 0:
+            msg = (self.ctx.lib.det_ctx_last_error(self.ctx.handle) or b"").decode()
+            if errors:
+                msg += f" ({errors[0]!r})"
+            raise TraceError(st, msg, artifact)
+        return artifact, bool(paused.value)
 
     def _release(self) -> None:
         if self.handle and self.ctx.handle:
