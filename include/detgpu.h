@@ -168,7 +168,12 @@ int det_model_create(det_ctx_t* ctx, const det_text_config_t* cfg, det_model_t**
 int det_model_set_tensor(det_model_t* model, const char* name, uint64_t rank, const uint64_t* dims, int elem_width,
                          const void* values, const int32_t* row_scale);
 /* Parses a whole detwgt v2 artifact with the fail-closed checks of
- * DetNumTensorReader::load_artifact (gemma/io.rs:224-387). */
+ * DetNumTensorReader::load_artifact (gemma/io.rs:224-387). Also accepts the
+ * int8 variant detwgt-q8 (magic "DNWGTQ8\0", version 1; no reference
+ * counterpart): the same records, where a rank >= 2 tensor may be stored at
+ * element_width 8 as int8 q followed by a u64 scale count (= rows), a
+ * 64-byte aligned int8 payload and a 64-byte aligned i32 scale per row
+ * (W = q * s, which must fit i32). Written by rasterdet.detwgt. */
 int det_model_load_detwgt(det_model_t* model, const uint8_t* bytes, size_t len);
 /* Resolves layers exactly like load_det_num_gemma4_layer_weights (gemma/io.rs:1896-2045). */
 int det_model_finalize(det_model_t* model);

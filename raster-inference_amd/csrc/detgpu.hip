@@ -692,7 +692,8 @@ void finalize(det_model* m) {
   m->finalized = true;
 }
 
-// detwgt v2 reader (gemma/io.rs:224-387, DETWGT_V2_FORMAT.md).
+// detwgt v2 reader (gemma/io.rs:224-387, DETWGT_V2_FORMAT.md), also reading
+// the int8 variant detwgt-q8 written by rasterdet.detwgt.
 void load_detwgt(det_model* m, const uint8_t* b, size_t len) {
   size_t cur = 0;
   auto take = [&](size_t n) {
@@ -703,11 +704,19 @@ void load_detwgt(det_model* m, const uint8_t* b, size_t len) {
   };
   auto rd32 = [&]() { uint32_t v; std::memcpy(&v, take(4), 4); return v; };
   auto rd64 = [&]() { uint64_t v; std::memcpy(&v, take(8), 8); return v; };
-  if (std::memcmp(take(8), "DNWGTV0\0", 8) != 0) bail("unsupported deterministic artifact magic");
-  if (rd32() != 2) bail("unsupported deterministic artifact format version; expected 2");
+  // detwgt v2, or detwgt-q8 (same records; rank >= 2 tensors may be int8 q
+  // plus one i32 scale per row, W = q * s)
+  const uint8_t* magic = take(8);
+  const bool q8 = std::memcmp(magic, "DNWGTQ8\0", 8) == 0;
+  if (!q8 && std::memcmp(magic, "DNWGTV0\0", 8) != 0) bail("unsupported deterministic artifact magic");
+  if (rd32() != (q8 ? 1u : 2u))
+    bail(q8 ? "unsupported detwgt-q8 format version; expected 1"
+            : "unsupported deterministic artifact format version; expected 2");
   if (rd32() != 1) bail("unsupported deterministic artifact det_num spec version; expected 1");
   const uint64_t count = rd64();
-  struct Rec { std::string name; std::vector<uint64_t> shape; int width; const uint8_t* data; };
+  struct Rec { std::string name; std::vector<uint64_t> shape; int width; const uint8_t* data; const int32_t* scale; };
+  std::vector<std::vector<int32_t>> scales;
+  scales.reserve(count);
   std::vector<Rec> recs;
   std::map<std::string, int> seen;
   for (uint64_t i = 0; i < count; ++i) {
@@ -723,24 +732,45 @@ void load_detwgt(det_model* m, const uint8_t* b, size_t len) {
     }
     if (rd64() != prod) bail("tensor `" + name + "` element count mismatch");
     const uint32_t width = rd32();
-    if (width != 16 && width != 32) bail("tensor `" + name + "` has an invalid element width");
+    if (width != 16 && width != 32 && !(q8 && width == 8 && rank >= 2))
+      bail("tensor `" + name + "` has an invalid element width");
     if (rd64() != prod * (width / 8)) bail("tensor `" + name + "` payload length mismatch");
     const uint64_t mass = rd64();
     if (rank >= 2 && mass >= (uint64_t(1) << 31)) bail("tensor `" + name + "` max row mass violates the overflow bound");
-    const size_t pad = (64 - cur % 64) % 64;
-    const uint8_t* pp = take(pad);
-    for (size_t k = 0; k < pad; ++k)
-      if (pp[k]) bail("tensor `" + name + "` has non-zero payload alignment padding");
+    const uint64_t rows = (width == 8 && shape.back()) ? prod / shape.back() : 0;
+    if (width == 8 && rd64() != rows) bail("tensor `" + name + "` scale count mismatch");
+    auto pad = [&]() {
+      const size_t n = (64 - cur % 64) % 64;
+      const uint8_t* pp = take(n);
+      for (size_t k = 0; k < n; ++k)
+        if (pp[k]) bail("tensor `" + name + "` has non-zero payload alignment padding");
+    };
+    pad();
     const uint8_t* data = take(prod * (width / 8));
+    const int32_t* scale = nullptr;
+    if (width == 8) {
+      pad();
+      scales.emplace_back(rows);
+      if (rows) std::memcpy(scales.back().data(), take(rows * 4), rows * 4);
+      scale = scales.back().data();
+      // W = q * s must be a canonical (i32) Wgt value
+      const uint64_t cols = shape.back();
+      for (uint64_t r = 0; r < rows; ++r) {
+        int64_t mx = 0;
+        for (uint64_t c = 0; c < cols; ++c) mx = std::max<int64_t>(mx, std::abs(int64_t(int8_t(data[r * cols + c]))));
+        if (mx * std::abs(int64_t(scale[r])) > INT32_MAX)
+          bail("tensor `" + name + "` has q * scale values outside i32");
+      }
+    }
     if (seen.count(name)) bail("deterministic artifact contains duplicate tensor `" + name + "`");
     seen[name] = 1;
-    recs.push_back({name, shape, int(width), data});
+    recs.push_back({name, shape, int(width), data, scale});
   }
   if (cur != len) bail("deterministic artifact has trailing bytes after tensor payloads");
   for (const Rec& r : recs) {
     if (r.shape.size() > 2 || r.shape.empty()) continue;  // only vectors and matrices are used on this path
     uint64_t dims[2] = {r.shape[0], r.shape.size() > 1 ? r.shape[1] : 0};
-    const int st = det_model_set_tensor(m, r.name.c_str(), r.shape.size(), dims, r.width, r.data, nullptr);
+    const int st = det_model_set_tensor(m, r.name.c_str(), r.shape.size(), dims, r.width, r.data, r.scale);
     if (st) throw Status(st, m->ctx->last_error);
   }
 }
