@@ -292,6 +292,35 @@ int det_trace_run(det_model_t* model, const det_trace_request_t* request, char* 
                   int32_t* paused);
 
 /* ------------------------------------------------------------------------ */
+/* Challenger audit (runtime/roles/challenger.rs, shared/api/audit.rs)       */
+/* ------------------------------------------------------------------------ */
+/* Audit outcomes are written as compact JSON plus a NUL into out (*out_len =
+ * its length; *diverged = 1 on a divergence):
+ *   {"diverged":false}                                  AuditOutcome::NoDivergence
+ *   {"diverged":true,"divergence":{...},"detour":S}     AuditOutcome::Diverged
+ * The divergence object is CheckpointDivergence (audit.rs:85-110) in its
+ * serde form: entry_index, checkpoint_id, occurrence, then whichever of
+ * claimed_checkpoint_id, claimed_commitment, replayed_commitment are set. S is
+ * the --raster-at spec of the divergent routine occurrence
+ * (challenger.rs:185-210) or null for a structural divergence or a routine
+ * without a raster detour; running that detour is the raster executor's job.
+ * A claimed trace that is not a JSON array of single-key
+ * {"checkpoint": "commitment"} objects is an error (ClaimedTrace,
+ * audit.rs:34-82). */
+
+/* locate_first_divergence (challenger.rs:136-183) between two serialized
+ * trace artifacts. Host only: no device work. */
+int det_trace_locate_divergence(const char* claimed, size_t claimed_len, const char* replayed, size_t replayed_len,
+                                char* out, size_t out_cap, size_t* out_len, int32_t* diverged);
+
+/* challenger::audit (challenger.rs:55-113): parses the claimed trace, replays
+ * the request on the GPU under the claimer policy (claimer.rs:34-61: commitment
+ * on, prompt_checkpoint set, no terminal checkpoint, unbounded ranges; other
+ * control settings are refused) and locates the first divergence. */
+int det_audit_trace(det_model_t* model, const det_trace_request_t* request, const char* claimed, size_t claimed_len,
+                    char* out, size_t out_cap, size_t* out_len, int32_t* diverged);
+
+/* ------------------------------------------------------------------------ */
 /* Synthetic workloads (no reference counterpart; random-init benchmarks)    */
 /* ------------------------------------------------------------------------ */
 /* Fills q[rows*cols] and s[rows] with counter-hash weights: q in [-127, 127],

@@ -27,6 +27,7 @@
 #include "../../include/detgpu.h"
 #include "decode.h"
 #include "det_arith.h"
+#include "audit.h"
 #include "kernels.h"
 
 using det::DevMatrix;
@@ -1884,31 +1885,7 @@ std::string capture(det_model* m, const uint32_t* ids, uint64_t n, uint64_t step
 // array (trace.rs:555-566). Payloads are serde_json maps, whose keys are
 // ordered bytewise, so they are written here from std::map.
 // ---------------------------------------------------------------------------
-// serde_json string escaping: quote, backslash and control characters; all
-// other bytes, non-ASCII UTF-8 included, are copied.
-std::string json_str(const std::string& v) {
-  std::string o = "\"";
-  for (unsigned char ch : v) {
-    switch (ch) {
-      case '"': o += "\\\""; break;
-      case '\\': o += "\\\\"; break;
-      case '\b': o += "\\b"; break;
-      case '\f': o += "\\f"; break;
-      case '\n': o += "\\n"; break;
-      case '\r': o += "\\r"; break;
-      case '\t': o += "\\t"; break;
-      default:
-        if (ch < 0x20) {
-          char b[8];
-          snprintf(b, sizeof b, "\\u%04x", unsigned(ch));
-          o += b;
-        } else {
-          o += char(ch);
-        }
-    }
-  }
-  return o + "\"";
-}
+std::string json_str(const std::string& v) { return det_audit::json_quote(v); }
 
 // A finite f32 as serde_json writes it: the shortest digit string that reads
 // back as the same f32, in plain notation when the decimal point falls within
@@ -2281,6 +2258,25 @@ bool trace_run(det_model* m, const det_trace_request_t* rq, TraceCollector& tc) 
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
+namespace {
+// Writes s plus a NUL into out when it fits; *out_len = its length.
+void put_text(const std::string& s, char* out, size_t out_cap, size_t* out_len, const char* what) {
+  if (out_len) *out_len = s.size();
+  if (!out || out_cap <= s.size())
+    bail(std::string(what) + " buffer too small: need " + std::to_string(s.size() + 1) + " bytes");
+  std::memcpy(out, s.data(), s.size());
+  out[s.size()] = 0;
+}
+template <class F>
+auto audit_input(F&& f) -> decltype(f()) {
+  try {
+    return f();
+  } catch (const det_audit::Error& e) {
+    bail(e.what());
+  }
+}
+}  // namespace
+
 extern "C" {
 
 const char* det_version(void) { return "detgpu 0.1 gfx950 (int8-limb MFMA GEMV, integer softmax attention)"; }
@@ -2631,6 +2627,47 @@ int det_trace_run(det_model_t* m, const det_trace_request_t* request, char* out,
     st = 1;
   }
   return st;
+}
+
+int det_trace_locate_divergence(const char* claimed, size_t claimed_len, const char* replayed, size_t replayed_len,
+                                char* out, size_t out_cap, size_t* out_len, int32_t* diverged) {
+  return guarded(nullptr, [&] {
+    if ((!claimed && claimed_len) || (!replayed && replayed_len)) bail("trace bytes are required");
+    const auto c = audit_input([&] { return det_audit::parse_trace(claimed, claimed_len); });
+    const auto r = audit_input([&] { return det_audit::parse_trace(replayed, replayed_len); });
+    bool d = false;
+    const std::string o = det_audit::outcome_json(c, r, &d);
+    if (diverged) *diverged = d ? 1 : 0;
+    put_text(o, out, out_cap, out_len, "audit outcome");
+  });
+}
+
+int det_audit_trace(det_model_t* m, const det_trace_request_t* request, const char* claimed, size_t claimed_len,
+                    char* out, size_t out_cap, size_t* out_len, int32_t* diverged) {
+  if (!m) {
+    g_error = "model is required";
+    return 1;
+  }
+  return guarded(m->ctx, [&] {
+    if (!m->finalized) bail("model is not finalized");
+    if (!request) bail("trace request is required");
+    if (!claimed && claimed_len) bail("claimed trace bytes are required");
+    // challenger::audit (runtime/roles/challenger.rs:55-113): the claimed
+    // trace is parsed first, then the request is replayed under the claimer
+    // policy (checkpoint commitment, prompt.prepare, no terminal checkpoint,
+    // unbounded ranges) and must run to completion.
+    if (!request->prompt_checkpoint || (request->terminal_checkpoint && *request->terminal_checkpoint) ||
+        request->prefill_token_range_width || request->decode_layer_range_width)
+      bail("challenger audit replays under the claimer policy: prompt_checkpoint must be set and "
+           "terminal_checkpoint and the range widths unset");
+    const auto c = audit_input([&] { return det_audit::parse_trace(claimed, claimed_len); });
+    TraceCollector tc;
+    if (trace_run(m, request, tc)) bail("challenger replay paused unexpectedly");
+    bool d = false;
+    const std::string o = det_audit::outcome_json(c, det_audit::entries_of(tc.entries), &d);
+    if (diverged) *diverged = d ? 1 : 0;
+    put_text(o, out, out_cap, out_len, "audit outcome");
+  });
 }
 
 }  // extern "C"

@@ -10,9 +10,11 @@ loudly when the HIP library is missing.
 from __future__ import annotations
 
 import ctypes as C
+import dataclasses
 import weakref
 import os
 import pathlib
+from typing import Optional
 
 import numpy as np
 
@@ -163,6 +165,63 @@ class TraceError(DetError):
         self.artifact = artifact
 
 
+@dataclasses.dataclass(frozen=True)
+class CheckpointDivergence:
+    """The first divergence between a claimed trace and a replay
+    (shared/api/audit.rs:85-110); None fields are the reference's None."""
+
+    entry_index: int
+    checkpoint_id: str
+    occurrence: int
+    claimed_checkpoint_id: Optional[str] = None
+    claimed_commitment: Optional[str] = None
+    replayed_commitment: Optional[str] = None
+
+
+@dataclasses.dataclass(frozen=True)
+class AuditOutcome:
+    """challenger::audit's outcome (audit.rs:124-138): divergence None is
+    NoDivergence. detour is the --raster-at spec of the divergent routine
+    occurrence (None for structural divergences and routines without a raster
+    detour); the raster detour run itself belongs to the raster executor."""
+
+    divergence: Optional[CheckpointDivergence] = None
+    detour: Optional[str] = None
+
+    @property
+    def diverged(self) -> bool:
+        return self.divergence is not None
+
+    @classmethod
+    def from_json(cls, text: bytes) -> "AuditOutcome":
+        import json
+
+        o = json.loads(text)
+        if not o["diverged"]:
+            return cls()
+        return cls(CheckpointDivergence(**o["divergence"]), o["detour"])
+
+
+def _outcome_cap(*traces: bytes) -> int:
+    # every string in the outcome comes from one of the traces or is a
+    # replayed 64-hex commitment; escaping takes at most 6 bytes per byte
+    return 1024 + 6 * sum(len(t) for t in traces)
+
+
+def locate_divergence(claimed: bytes, replayed: bytes) -> AuditOutcome:
+    """locate_first_divergence (runtime/roles/challenger.rs:136-183) between two
+    serialized trace artifacts, with the detour spec of the divergence."""
+    L = lib()
+    cap = _outcome_cap(claimed, replayed)
+    buf = C.create_string_buffer(cap)
+    n, d = C.c_size_t(), C.c_int32()
+    st = L.det_trace_locate_divergence(claimed, len(claimed), replayed, len(replayed), buf, cap, C.byref(n),
+                                       C.byref(d))
+    if st != 0:
+        raise DetError(st, (L.det_ctx_last_error(None) or b"").decode())
+    return AuditOutcome.from_json(buf.raw[:n.value])
+
+
 _LIB = None
 C = C  # ctypes, re-exported for callers that pass raw pointers
 
@@ -223,6 +282,10 @@ def lib() -> C.CDLL:
         "det_capture": (C.c_int, [P, P, u64, u64, C.c_char_p, C.c_size_t]),
         "det_trace_run": (C.c_int, [P, C.POINTER(TraceRequest), C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t),
                                     C.POINTER(C.c_int32)]),
+        "det_trace_locate_divergence": (C.c_int, [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t, C.c_char_p,
+                                                  C.c_size_t, C.POINTER(C.c_size_t), C.POINTER(C.c_int32)]),
+        "det_audit_trace": (C.c_int, [P, C.POINTER(TraceRequest), C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t,
+                                      C.POINTER(C.c_size_t), C.POINTER(C.c_int32)]),
         "det_synthetic_int8": (C.c_int, [u64, u64, u64, C.c_int32, P, P]),
     }
     for name, (res, args) in sig.items():
@@ -495,12 +558,10 @@ class Model:
         self.ctx.check(self.ctx.lib.det_capture(self.handle, _ptr(ids), ids.size, decode_steps, buf, len(buf)))
         return json.loads(buf.value.decode())
 
-    def trace(self, prompt_text: str, prompt_token_ids, max_new_tokens=None, temperature=1.0, top_k=None,
-              top_p=None, detokenize=None, prompt_checkpoint: bool = True, terminal_checkpoint=None,
-              prefill_token_range_width: int = 0, decode_layer_range_width: int = 0):
-        """Runs the native deterministic sequence with checkpoint commitment and
-        returns (trace artifact bytes, paused). detokenize(ids) -> str decodes
-        generated ids (special tokens skipped). None means an Option left unset."""
+    def _trace_request(self, prompt_text, prompt_token_ids, max_new_tokens, temperature, top_k, top_p, detokenize,
+                       prompt_checkpoint, terminal_checkpoint, prefill_token_range_width, decode_layer_range_width):
+        """det_trace_request_t plus what must outlive the call (ids, callback)
+        and the list that collects the detokenizer's exceptions."""
         ids = np.ascontiguousarray(prompt_token_ids, dtype=np.uint32)
         sp = Sampling(max_new_tokens is not None, max_new_tokens or 0, temperature is not None,
                       temperature if temperature is not None else 0.0, top_k is not None, top_k or 0,
@@ -521,6 +582,21 @@ class Model:
         req = TraceRequest(prompt_text.encode(), ids.ctypes.data_as(C.POINTER(C.c_uint32)), ids.size, sp,
                            int(prompt_checkpoint), terminal_checkpoint.encode() if terminal_checkpoint else None,
                            prefill_token_range_width, decode_layer_range_width, cb, None)
+        return req, (ids, cb), errors
+
+    def _error_message(self, errors) -> str:
+        msg = (self.ctx.lib.det_ctx_last_error(self.ctx.handle) or b"").decode()
+        return msg + (f" ({errors[0]!r})" if errors else "")
+
+    def trace(self, prompt_text: str, prompt_token_ids, max_new_tokens=None, temperature=1.0, top_k=None,
+              top_p=None, detokenize=None, prompt_checkpoint: bool = True, terminal_checkpoint=None,
+              prefill_token_range_width: int = 0, decode_layer_range_width: int = 0):
+        """Runs the native deterministic sequence with checkpoint commitment and
+        returns (trace artifact bytes, paused). detokenize(ids) -> str decodes
+        generated ids (special tokens skipped). None means an Option left unset."""
+        req, _keep, errors = self._trace_request(prompt_text, prompt_token_ids, max_new_tokens, temperature, top_k,
+                                                 top_p, detokenize, prompt_checkpoint, terminal_checkpoint,
+                                                 prefill_token_range_width, decode_layer_range_width)
         cap = 1 << 16
         while True:
             buf = C.create_string_buffer(cap)
@@ -533,11 +609,34 @@ class Model:
             break
         artifact = buf.raw[:n.value]
         if st != 0:
-            msg = (self.ctx.lib.det_ctx_last_error(self.ctx.handle) or b"").decode()
-            if errors:
-                msg += f" ({errors[0]!r})"
-            raise TraceError(st, msg, artifact)
+            raise TraceError(st, self._error_message(errors), artifact)
         return artifact, bool(paused.value)
+
+    def claim(self, prompt_text: str, prompt_token_ids, max_new_tokens=None, temperature=1.0, top_k=None,
+              top_p=None, detokenize=None) -> bytes:
+        """claimer::run (runtime/roles/claimer.rs:34-61): the full committed
+        trace artifact of the request, prompt.prepare included."""
+        artifact, paused = self.trace(prompt_text, prompt_token_ids, max_new_tokens, temperature, top_k, top_p,
+                                      detokenize)
+        if paused:
+            raise DetError(1, "claimer run paused unexpectedly")
+        return artifact
+
+    def audit(self, prompt_text: str, prompt_token_ids, claimed_trace: bytes, max_new_tokens=None,
+              temperature=1.0, top_k=None, top_p=None, detokenize=None) -> AuditOutcome:
+        """challenger::audit (runtime/roles/challenger.rs:55-113): replays the
+        request on the GPU under the claimer policy and locates the first
+        divergence of claimed_trace from the replay."""
+        req, _keep, errors = self._trace_request(prompt_text, prompt_token_ids, max_new_tokens, temperature, top_k,
+                                                 top_p, detokenize, True, None, 0, 0)
+        cap = _outcome_cap(claimed_trace)
+        buf = C.create_string_buffer(cap)
+        n, d = C.c_size_t(), C.c_int32()
+        st = self.ctx.lib.det_audit_trace(self.handle, C.byref(req), claimed_trace, len(claimed_trace), buf, cap,
+                                          C.byref(n), C.byref(d))
+        if st != 0:
+            raise DetError(st, self._error_message(errors))
+        return AuditOutcome.from_json(buf.raw[:n.value])
 
     def _release(self) -> None:
         if self.handle and self.ctx.handle:
