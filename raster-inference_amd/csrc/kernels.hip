@@ -536,45 +536,85 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
 // holds row i, bytes [32g, 32g + 32)). A 16x16x64 MFMA of an A tile (4 tokens
 // x 4 limbs) with a weight tile leaves the four limb sums of (token g, weight
 // row i) in lane 16g + i, which are combined exactly as in the GEMV.
-//
-// Block: TA A tiles (TA x 16 limb rows = 4 TA tokens) x TB weight tiles;
-// WM x WN waves, each (TA / WM) x (TB / WN) MFMA tiles, two MFMAs per
-// 128-column step. Each step's TA + TB tile-steps are double buffered in LDS,
-// every 2 KB block stored as two 1 KB halves (bytes 0-15 and 16-31 of each
-// lane's 32), so the 128-bit LDS reads of a wave are contiguous. Shapes:
-// 8 x 8 tiles on 4 waves (small slabs) and 16 x 16 on 8 waves (4x the MFMA
-// work per staged byte pair, for slabs that fill the device).
 // ---------------------------------------------------------------------------
-constexpr uint32_t gemm_lds_bytes(int ta, int tb) { return 2u * uint32_t(ta + tb) * 2u * 64u * 16u; }
 
 // Activation limbs in the tiled layout for a_tiles 16-row tiles (4 tokens
-// each); tokens >= m and columns >= k are zero.
+// each); tokens >= m and columns >= k are zero. One thread per token and 32
+// columns: its four limb rows are four consecutive 32-byte lane slots of the
+// tile-step (lanes 16 g + 4 (t % 4) + j), so it writes 128 contiguous bytes,
+// and the four tokens of a tile go to consecutive threads (512 contiguous
+// bytes). vec: act rows are 16-byte aligned (base and ld), so a thread's 32
+// columns load as eight 128-bit reads.
 __global__ void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, uint64_t k, uint64_t ld,
-                                  uint64_t kpad, uint64_t tokens_pad, int8_t* __restrict__ out) {
-  const uint64_t c = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  const uint64_t t = blockIdx.y;
-  if (c >= kpad || t >= tokens_pad) return;
-  const bool live = t < m && c < k;
-  const uint32_t u = live ? uint32_t(act[t * ld + c]) ^ 0x00808080u : 0u;
+                                  uint64_t kpad, uint64_t tokens_pad, int vec, int8_t* __restrict__ out) {
+  const uint64_t id = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t nsteps = kpad / 128;
+  const uint64_t tq = id & 3, g = (id >> 2) & 3, rest = id >> 4;
+  const uint64_t step = rest % nsteps, tile = rest / nsteps;
+  const uint64_t t = 4 * tile + tq;
+  if (t >= tokens_pad) return;
+  const uint64_t c0 = 128 * step + 32 * g;
+  uint32_t u[32];
+  if (vec && t < m && c0 + 32 <= k) {
+    const int4* src = reinterpret_cast<const int4*>(act + t * ld + c0);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int4 v = src[q];
+      u[4 * q] = uint32_t(v.x) ^ 0x00808080u;
+      u[4 * q + 1] = uint32_t(v.y) ^ 0x00808080u;
+      u[4 * q + 2] = uint32_t(v.z) ^ 0x00808080u;
+      u[4 * q + 3] = uint32_t(v.w) ^ 0x00808080u;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const bool live = t < m && c0 + e < k;
+      u[e] = live ? uint32_t(act[t * ld + c0 + e]) ^ 0x00808080u : 0u;
+    }
+  }
+  // lane slot 16 g + 4 tq + j of tile-step (tile, step)
+  int4* dst = reinterpret_cast<int4*>(out + ((tile * nsteps + step) * 64 + 16 * g + 4 * tq) * 32);
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    out[tiled_offset(kpad, 4 * t + j, c)] = live ? int8_t(uint8_t(u >> (8 * j))) : int8_t(0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        w[q] = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) w[q] |= ((u[16 * h + 4 * q + b] >> (8 * j)) & 0xffu) << (8 * b);
+      }
+      dst[2 * j + h] = make_int4(int(w[0]), int(w[1]), int(w[2]), int(w[3]));
+    }
 }
 
-template <int TA, int TB, int WM, int WN, uint32_t GM>
-__global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
-                                                          const int32_t* __restrict__ scale,
-                                                          const int32_t* __restrict__ rowsum, uint64_t n_rows,
-                                                          uint64_t kpad, uint64_t m_tokens, uint64_t a_tiles,
-                                                          uint32_t mblocks, int32_t* __restrict__ out,
-                                                          uint64_t ld_out, int64_t* __restrict__ acc_out) {
-  constexpr int NT = 64 * WM * WN;             // threads
-  constexpr int TS = TA + TB;                  // tile-steps staged per K step
-  constexpr int CPT = TS * 128 / NT;           // 16-byte chunks per thread per K step
+// Block: TA A tiles (4 TA tokens) x TB weight tiles on WM x WN waves, each
+// wave (TA / WM) x (TB / WN) MFMA tiles. Every 128-column K step, the block's
+// TA + TB tile-steps (2 KB each) are copied straight from global memory into
+// one of NBUF LDS buffers with global_load_lds_dwordx4 (no register staging):
+// the copies of the next NBUF - 1 steps are in flight while step s's MFMAs
+// run, and one barrier per step hands a buffer over. Copy h of a tile-step
+// takes bytes [16 h, 16 h + 16) of every lane's 32 (a 32-byte source stride),
+// so each 1 KB LDS half holds one MFMA operand of all 64 lanes contiguously
+// and the 128-bit operand reads do not conflict on LDS banks. The MFMAs of a
+// step run as two passes over the wave's tile pairs (first 64 columns, then
+// the second 64), so consecutive MFMAs never share an accumulator.
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
+                                                           const int32_t* __restrict__ scale,
+                                                           const int32_t* __restrict__ rowsum, uint64_t n_rows,
+                                                           uint64_t kpad, uint64_t m_tokens, uint64_t a_tiles,
+                                                           uint32_t mblocks, int32_t* __restrict__ out,
+                                                           uint64_t ld_out, int64_t* __restrict__ acc_out) {
+  constexpr int NW = WM * WN;                  // waves
+  constexpr int TS = TA + TB;                  // tile-steps per K step
+  constexpr int LPW = 2 * TS / NW;             // 1 KB wave copies per wave per K step
   constexpr int FA = TA / WM, FB = TB / WN;    // MFMA tiles per wave
-  static_assert(TS * 128 % NT == 0, "chunks must divide evenly");
-  extern __shared__ v4i lds[];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  static_assert(2 * TS % NW == 0, "copies must divide evenly");
+  extern __shared__ __attribute__((aligned(16))) int8_t lds_gemm[];
+  // the wave index as a scalar, so that copy addresses and LDS targets stay in SGPRs
+  const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // Block order: block b runs on XCD b % 8, and each XCD takes a contiguous
   // range of logical blocks; logical blocks go in groups of GM m-blocks x all
   // n-blocks with m fastest, so the blocks resident on one XCD at a time form
@@ -590,62 +630,79 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_i8(const int8_t* __restri
   const uint64_t nsteps = kpad / 128;
   const uint64_t ntiles = (n_rows + 15) / 16;
   const uint64_t at0 = uint64_t(mb) * TA, bt0 = uint64_t(nb) * TB;
-  // chunk c = tid + NT u of a step's TS x 128 sixteen-byte chunks: tile-step
-  // c / 128 (A tiles first), lane c % 128 / 2, half c % 2
-  const v4i zero = {0, 0, 0, 0};
-  v4i stage_regs[CPT];
-  auto fetch = [&](uint64_t s) {
+  // this wave's copies: chunk c = wave * LPW + u is tile-step c / 2 (A tiles
+  // first), half c % 2; tiles past the matrix re-read its last tile (their
+  // results are never stored)
+  const int8_t* src[LPW];
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) {
-      const uint32_t c = tid + NT * u;
-      const uint32_t ts = c >> 7, within = c & 127;
-      const bool is_a = ts < uint32_t(TA);
-      const uint64_t tile = is_a ? at0 + ts : bt0 + (ts - TA);
-      const bool on = is_a ? tile < a_tiles : tile < ntiles;
-      const int8_t* base = is_a ? a : q;
-      stage_regs[u] = on ? *reinterpret_cast<const v4i*>(base + (tile * nsteps + s) * 2048 + within * 16) : zero;
-    }
-  };
-  auto store = [&](int st) {
+  for (int u = 0; u < LPW; ++u) {
+    const uint32_t c = wave * LPW + u, ts = c >> 1, h = c & 1;
+    const bool is_a = ts < uint32_t(TA);
+    uint64_t tile = is_a ? at0 + ts : bt0 + (ts - TA);
+    if (is_a ? tile >= a_tiles : tile >= ntiles) tile = (is_a ? a_tiles : ntiles) - 1;
+    src[u] = (is_a ? a : q) + tile * nsteps * 2048 + lane * 32 + h * 16;
+  }
+  auto copy_step = [&](uint64_t s, int buf) {
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) {
-      const uint32_t c = tid + NT * u;
-      const uint32_t ts = c >> 7, within = c & 127;
-      lds[((st * TS + ts) * 2 + (within & 1)) * 64 + (within >> 1)] = stage_regs[u];
+    for (int u = 0; u < LPW; ++u) {
+      const uint32_t c = wave * LPW + u;
+      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[u] + s * 2048),
+                                       (void __attribute__((address_space(3)))*)(lds_gemm + (buf * TS * 2 + c) * 1024),
+                                       16, 0, 0);
     }
   };
   const uint32_t wm = wave / WN, wn = wave % WN;
+  const v4i zero = {0, 0, 0, 0};
   v4i acc[FA][FB];
 #pragma unroll
   for (int i = 0; i < FA; ++i)
 #pragma unroll
     for (int j = 0; j < FB; ++j) acc[i][j] = zero;
-  fetch(0);
-  store(0);
-  __syncthreads();
+  // NBUF - 1 steps in flight ahead of the one being multiplied
+#pragma unroll
+  for (int p = 0; p < NBUF - 1; ++p)
+    if (uint64_t(p) < nsteps) copy_step(p, p);
+  // vmcnt immediate: wait until at most (NBUF - 2) steps of copies are outstanding
+  constexpr int kWait = (NBUF - 2) * LPW;
+  static_assert(kWait < 64, "vmcnt range");
+  constexpr int kWaitImm = (kWait & 15) | (7 << 4) | (15 << 8) | ((kWait >> 4) << 14);
+  // Each wave waits for its own copies of a step (vmcnt, in issue order),
+  // then the barrier makes every wave's copies of that step visible. A bare
+  // s_barrier (not __syncthreads, whose fence would wait for every copy in
+  // flight) between compiler memory barriers keeps the later steps' copies
+  // outstanding across it.
+  auto step_barrier = [&](bool more) {
+    asm volatile("" ::: "memory");
+    if (more) __builtin_amdgcn_s_waitcnt(kWaitImm);
+    else __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  step_barrier(nsteps >= uint64_t(NBUF - 1));
   for (uint64_t s = 0; s < nsteps; ++s) {
-    const int st = int(s & 1);
-    if (s + 1 < nsteps) fetch(s + 1);
-    v4i b0[FB], b1[FB];
+    const int buf = int(s % NBUF);
+    const int8_t* base = lds_gemm + buf * TS * 2048 + lane * 16;
+    // the first half's operands, the copies, the second half's operands
+    // (read while the first half's MFMAs run), then the MFMAs
+    v4i ao[2][FA], bo[2][FB];
+    auto read_half = [&](int h) {
 #pragma unroll
-    for (int j = 0; j < FB; ++j) {
-      const int tb = TA + int(wn) * FB + j;
-      b0[j] = lds[((st * TS + tb) * 2 + 0) * 64 + lane];
-      b1[j] = lds[((st * TS + tb) * 2 + 1) * 64 + lane];
-    }
+      for (int j = 0; j < FB; ++j) bo[h][j] = *reinterpret_cast<const v4i*>(base + (TA + wn * FB + j) * 2048 + 1024 * h);
 #pragma unroll
-    for (int i = 0; i < FA; ++i) {
-      const int ta = int(wm) * FA + i;
-      const v4i a0 = lds[((st * TS + ta) * 2 + 0) * 64 + lane];
-      const v4i a1 = lds[((st * TS + ta) * 2 + 1) * 64 + lane];
+      for (int i = 0; i < FA; ++i) ao[h][i] = *reinterpret_cast<const v4i*>(base + (wm * FA + i) * 2048 + 1024 * h);
+    };
+    read_half(0);
+    if (s + NBUF - 1 < nsteps) copy_step(s + NBUF - 1, int((s + NBUF - 1) % NBUF));
+    read_half(1);
 #pragma unroll
-      for (int j = 0; j < FB; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[j], acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[j], acc[i][j], 0, 0, 0);
-      }
-    }
-    if (s + 1 < nsteps) store(st ^ 1);
-    __syncthreads();
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < FA; ++i)
+#pragma unroll
+        for (int j = 0; j < FB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ao[h][i], bo[h][j], acc[i][j], 0, 0, 0);
+    // step s + 1's copies are complete when no more than the later steps' are outstanding
+    step_barrier(s + NBUF - 1 < nsteps);
   }
   // epilogue: lane 16g + i holds the limb sums of token 4 tile + g, weight row 16 tile + i
   const uint32_t g = lane >> 4, i = lane & 15;
@@ -1322,38 +1379,45 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
 
 uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64 * 4 * kpad; }
 
-template <int TA, int TB, int WM, int WN, uint32_t GM>
-static void launch_gemm_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                              const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s) {
-  // the larger shape needs more than 64 KB of dynamic LDS per workgroup
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_i8<TA, TB, WM, WN, GM>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     int(gemm_lds_bytes(TA, TB)));
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF>
+static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
+                                  const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s) {
+  constexpr uint32_t lds = uint32_t(NBUF) * (TA + TB) * 2048u;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      int(lds));
   (void)attr;
   const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
   const uint64_t nblocks = ((W.rows + 15) / 16 + TB - 1) / TB;
-  hipLaunchKernelGGL((k_gemm_i8<TA, TB, WM, WN, GM>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN),
-                     gemm_lds_bytes(TA, TB), s, a_tiled, W.q, W.scale, W.rowsum, W.rows, W.kpad, m, a_tiles,
-                     uint32_t(mblocks), out, ld_out, acc_out);
+  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN), lds, s,
+                     a_tiled, W.q, W.scale, W.rowsum, W.rows, W.kpad, m, a_tiles, uint32_t(mblocks), out, ld_out,
+                     acc_out);
 }
 
 void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_act, uint64_t kpad, int8_t* a_tiled,
                        hipStream_t s) {
   if (m == 0) return;
   const uint64_t tokens_pad = (m + 63) / 64 * 64;  // the larger block's 16 A tiles
-  hipLaunchKernelGGL(k_act_limbs_tiled, dim3(blocks_for(kpad, 256), unsigned(tokens_pad)), dim3(256), 0, s, act, m, k,
-                     ld_act, kpad, tokens_pad, a_tiled);
+  const int vec = (reinterpret_cast<uintptr_t>(act) % 16 == 0 && ld_act % 4 == 0) ? 1 : 0;
+  const uint64_t threads = tokens_pad * (kpad / 128) * 4;
+  hipLaunchKernelGGL(k_act_limbs_tiled, dim3(blocks_for(threads, 256)), dim3(256), 0, s, act, m, k, ld_act, kpad,
+                     tokens_pad, vec, a_tiled);
 }
 
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
                        const int8_t* a_tiled, hipStream_t s) {
   if (W.rows == 0 || m == 0) return;
   const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
-  const uint64_t big_blocks = ((m + 63) / 64) * (((W.rows + 15) / 16 + 15) / 16);
-  if (big_blocks >= 256)
-    launch_gemm_shape<16, 16, 2, 4, 4>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
+  // 64 tokens x 256 rows on 8 waves (one block per CU) when its blocks fill
+  // whole rounds of the device; otherwise 32 tokens x 128 rows on 4 waves
+  // (two blocks per CU), whose finer grid leaves a smaller last round
+  const uint64_t cus = device_cus();
+  const uint64_t big = ((m + 63) / 64) * (((W.rows + 15) / 16 + 15) / 16);
+  const uint64_t rounds = (big + cus - 1) / cus;
+  if (big >= cus && big * 10 >= rounds * cus * 9)
+    launch_gemm_lds_shape<16, 16, 2, 4, 4, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   else
-    launch_gemm_shape<8, 8, 2, 2, 8>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
+    launch_gemm_lds_shape<8, 8, 2, 2, 8, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
 }
 
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
