@@ -242,6 +242,26 @@ def measured_traffic():
     return None
 
 
+def gemm_profile(ctx, rd, seed: int) -> int:
+    """Counter-collection workload for the prefill GEMM: the gate projection
+    (10240 x 2560) at M = 2048 through det_linear_slab, 10 launches."""
+    from rasterdet import synthetic
+
+    n, k = PREFILL_SHAPES[4]
+    q, s = synthetic.fast_int8_matrix(seed * 7 + 4, n, k, 256)
+    mat = ctx.upload_matrix(q, s)
+    m = 2048
+    rng = np.random.default_rng(seed)
+    act = ctx.to_device(synthetic.f32_to_act(rng.standard_normal((m, k)).astype(np.float32)))
+    o = ctx.empty((m, n))
+    for _ in range(10):
+        ctx.det_linear_slab(mat, m, act, o)
+    ctx.synchronize()
+    print(json.dumps({"gemm_profile": True, "m": m, "n": n, "k": k, "launches": 10,
+                      "alg_ops_per_launch": 2 * m * n * k}), flush=True)
+    return 0
+
+
 def profile_pass(ctx, rd, seed: int) -> int:
     """Counter-collection workload: the lm_head GEMV and a device copy of the
     same weight byte count, so FETCH_SIZE / WRITE_SIZE of the GEMV can be scaled
@@ -284,6 +304,8 @@ def main() -> int:
     ap.add_argument("--prompt-len", type=int, default=512)
     ap.add_argument("--decode-profile", action="store_true",
                     help="only the E4B-shaped model: prefill, then 32 greedy decode steps (for rocprofv3 runs)")
+    ap.add_argument("--gemm-profile", action="store_true",
+                    help="only 10 prefill GEMMs (gate 10240x2560, M 2048) for rocprofv3 runs")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only 5 lm_head GEMV launches + 5 same-size device copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -297,6 +319,8 @@ def main() -> int:
     ctx = rd.Context(0)
     if args.profile_pass:
         return profile_pass(ctx, rd, args.seed)
+    if args.gemm_profile:
+        return gemm_profile(ctx, rd, args.seed)
     if args.decode_profile:
         args.decode_steps = 32
         args.eager = True  # profiler kernel tracing of graph replays is not used
