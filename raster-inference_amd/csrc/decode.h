@@ -72,6 +72,9 @@ struct AttnDecArgs {
   const DecSeqCache* caches;
   uint64_t trig_stride, qkv_stride, scores_stride, acc_stride, keys_stride, stats_stride;
   uint32_t nseq;
+  // kAttnScoreRows chunks per scores / weighted-sum workgroup (1, 2 or 4; 0
+  // picks by cache size). Any choice gives the same results.
+  uint32_t rows_mul;
 };
 
 // Limits of the fused decode kernels.

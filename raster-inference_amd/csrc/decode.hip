@@ -225,53 +225,59 @@ __device__ __forceinline__ void seq_view(AttnDecArgs& a) {
   }
 }
 
-// Scores of every query head of one KV head over kAttnScoreRows window rows
-// (ops.rs:318-333: wrapping dot product, requantized), 512 threads. The
+// Scores of every query head of one KV head over P chunks of kAttnScoreRows
+// window rows (ops.rs:318-333: wrapping dot product, requantized), 512
+// threads. The
 // workgroup first builds the normalised, rotated queries of its heads in LDS
 // (one wavefront per head row); the workgroup whose rows include the step's
 // own token also normalises and rotates the new key row, appends key and
 // value rows to the cache at the canonical slot and scores that row from LDS.
-// Sixteen lanes share one key row. Chunk 0 also zeroes the heads'
-// weighted-sum accumulators.
-template <bool VEC>
+// Sixteen lanes share one key row per chunk; the key rows of all P chunks are
+// fetched at the start. Workgroup 0 also zeroes the heads' weighted-sum
+// accumulators. The argmax key of every chunk goes to keys.
+template <bool VEC, int P, uint32_t MAXHD>
 __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   __shared__ int32_t ql[kDecMaxGroup * kDecMaxHeadDim];
   __shared__ int32_t kn[kDecMaxHeadDim];
-  __shared__ int64_t ck[kDecMaxGroup][kAttnScoreRows];
+  __shared__ int64_t ck[P][kDecMaxGroup][kAttnScoreRows];
   seq_view(a);
   const Window win = attn_window(a);
   const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
-  const uint64_t r0 = uint64_t(blockIdx.y) * kAttnScoreRows;
+  const uint64_t r0 = uint64_t(blockIdx.y) * P * kAttnScoreRows;
   const uint64_t qoff = uint64_t(kvh) * G * hd;
   if (blockIdx.y == 0)
     for (uint32_t i = threadIdx.x; i < G * hd; i += 512) a.acc[qoff + i] = 0;
   if (r0 >= win.cnt) return;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t cur = win.cnt - 1;  // window row of the step's own token
-  const bool has_new = a.own_cache && cur >= r0 && cur < r0 + kAttnScoreRows;
+  const bool has_new = a.own_cache && cur >= r0 && cur < r0 + P * kAttnScoreRows;
   const uint64_t kvw = uint64_t(a.nkv) * hd;
-  // this lane group's key row, fetched while the head rows are normalised
+  // this lane group's key row of every chunk, fetched while the head rows are normalised
   const uint32_t grp = threadIdx.x >> 4, li = threadIdx.x & 15;
-  const uint64_t j = r0 + grp;
-  const bool valid = j < win.cnt;
-  const bool own_row = has_new && j == cur;
-  const int32_t* krow = a.k + ((valid && !own_row) ? phys_row(a, win, j) : 0) * kvw + uint64_t(kvh) * hd;
-  const bool kload = valid && !own_row;
-  constexpr int kPer = kDecMaxHeadDim / 16;
-  int32_t kr[kPer];
-  if (VEC) {
+  constexpr int kPer = MAXHD / 16;  // key elements per lane (head_dim <= MAXHD)
+  int32_t kr[P][kPer];
+  bool valid[P], own_row[P];
 #pragma unroll
-    for (int t = 0; t < kPer / 4; ++t) {
-      const uint32_t d = 4 * li + 64 * t;
-      int4 v = make_int4(0, 0, 0, 0);
-      if (kload && d < hd) v = *reinterpret_cast<const int4*>(krow + d);
-      kr[4 * t] = v.x, kr[4 * t + 1] = v.y, kr[4 * t + 2] = v.z, kr[4 * t + 3] = v.w;
-    }
-  } else {
+  for (int p = 0; p < P; ++p) {
+    const uint64_t j = r0 + p * kAttnScoreRows + grp;
+    valid[p] = j < win.cnt;
+    own_row[p] = has_new && j == cur;
+    const bool kload = valid[p] && !own_row[p];
+    const int32_t* krow = a.k + (kload ? phys_row(a, win, j) : 0) * kvw + uint64_t(kvh) * hd;
+    if (VEC) {
 #pragma unroll
-    for (int t = 0; t < kPer; ++t) {
-      const uint32_t d = li + 16 * t;
-      kr[t] = (kload && d < hd) ? krow[d] : 0;
+      for (int t = 0; t < kPer / 4; ++t) {
+        const uint32_t d = 4 * li + 64 * t;
+        int4 v = make_int4(0, 0, 0, 0);
+        if (kload && d < hd) v = *reinterpret_cast<const int4*>(krow + d);
+        kr[p][4 * t] = v.x, kr[p][4 * t + 1] = v.y, kr[p][4 * t + 2] = v.z, kr[p][4 * t + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) {
+        const uint32_t d = li + 16 * t;
+        kr[p][t] = (kload && d < hd) ? krow[d] : 0;
+      }
     }
   }
   // cos/sin of this thread's first two rotation slots, fetched early (later
@@ -315,57 +321,68 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   }
   if (has_new)
     for (uint32_t d = threadIdx.x; d < hd; d += 512) kslot[d] = kn[d];
-  if (own_row) {
-    if (VEC) {
 #pragma unroll
-      for (int t = 0; t < kPer / 4; ++t) {
-        const uint32_t d = 4 * li + 64 * t;
-        if (d < hd) kr[4 * t] = kn[d], kr[4 * t + 1] = kn[d + 1], kr[4 * t + 2] = kn[d + 2], kr[4 * t + 3] = kn[d + 3];
-      }
-    } else {
+  for (int p = 0; p < P; ++p)
+    if (own_row[p]) {
+      if (VEC) {
 #pragma unroll
-      for (int t = 0; t < kPer; ++t) {
-        const uint32_t d = li + 16 * t;
-        if (d < hd) kr[t] = kn[d];
-      }
-    }
-  }
-  for (uint32_t g = 0; g < G; ++g) {
-    const int32_t* qg = ql + g * hd;
-    int64_t acc = 0;
-    if (VEC) {
+        for (int t = 0; t < kPer / 4; ++t) {
+          const uint32_t d = 4 * li + 64 * t;
+          if (d < hd)
+            kr[p][4 * t] = kn[d], kr[p][4 * t + 1] = kn[d + 1], kr[p][4 * t + 2] = kn[d + 2], kr[p][4 * t + 3] = kn[d + 3];
+        }
+      } else {
 #pragma unroll
-      for (int t = 0; t < kPer / 4; ++t) {
-        const uint32_t d = 4 * li + 64 * t;
-        if (d < hd) {
-          const int4 q = *reinterpret_cast<const int4*>(qg + d);
-          acc = mac(acc, q.x, kr[4 * t]);
-          acc = mac(acc, q.y, kr[4 * t + 1]);
-          acc = mac(acc, q.z, kr[4 * t + 2]);
-          acc = mac(acc, q.w, kr[4 * t + 3]);
+        for (int t = 0; t < kPer; ++t) {
+          const uint32_t d = li + 16 * t;
+          if (d < hd) kr[p][t] = kn[d];
         }
       }
-    } else {
-#pragma unroll
-      for (int t = 0; t < kPer; ++t) {
-        const uint32_t d = li + 16 * t;
-        if (d < hd) acc = mac(acc, qg[d], kr[t]);
-      }
     }
-    acc = int64_t(row16_reduce(uint64_t(acc), OpWrapAdd()));  // the 16 lanes of this key row
-    if (li == 0) {
-      const int32_t sc = requant(acc);
-      if (valid) a.scores[(uint64_t(kvh) * G + g) * a.max_rows + j] = sc;
-      ck[g][grp] = valid ? score_key(sc, j) : INT64_MIN;
+  for (uint32_t g = 0; g < G; ++g) {
+    const int32_t* qg = ql + g * hd;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      int64_t acc = 0;
+      if (VEC) {
+#pragma unroll
+        for (int t = 0; t < kPer / 4; ++t) {
+          const uint32_t d = 4 * li + 64 * t;
+          if (d < hd) {
+            const int4 q = *reinterpret_cast<const int4*>(qg + d);
+            acc = mac(acc, q.x, kr[p][4 * t]);
+            acc = mac(acc, q.y, kr[p][4 * t + 1]);
+            acc = mac(acc, q.z, kr[p][4 * t + 2]);
+            acc = mac(acc, q.w, kr[p][4 * t + 3]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) {
+          const uint32_t d = li + 16 * t;
+          if (d < hd) acc = mac(acc, qg[d], kr[p][t]);
+        }
+      }
+      acc = int64_t(row16_reduce(uint64_t(acc), OpWrapAdd()));  // the 16 lanes of this key row
+      if (li == 0) {
+        const uint64_t j = r0 + p * kAttnScoreRows + grp;
+        const int32_t sc = requant(acc);
+        if (valid[p]) a.scores[(uint64_t(kvh) * G + g) * a.max_rows + j] = sc;
+        ck[p][g][grp] = valid[p] ? score_key(sc, j) : INT64_MIN;
+      }
     }
   }
   __syncthreads();
-  // this chunk's argmax key per head (the maximum of the chunk maxima is the
-  // window's first argmax)
-  if (threadIdx.x < G) {
-    int64_t best = ck[threadIdx.x][0];
-    for (uint32_t r = 1; r < kAttnScoreRows; ++r) best = ck[threadIdx.x][r] > best ? ck[threadIdx.x][r] : best;
-    a.keys[(uint64_t(kvh) * G + threadIdx.x) * a.key_chunks + blockIdx.y] = best;
+  // every chunk's argmax key per head (the maximum of the chunk maxima is the
+  // window's first argmax); chunks past the window are never read
+  if (threadIdx.x < P * G) {
+    const uint32_t p = threadIdx.x / G, g = threadIdx.x % G;
+    const uint64_t c = uint64_t(blockIdx.y) * P + p;
+    if (c * kAttnScoreRows < win.cnt) {
+      int64_t best = ck[p][g][0];
+      for (uint32_t r = 1; r < kAttnScoreRows; ++r) best = ck[p][g][r] > best ? ck[p][g][r] : best;
+      a.keys[(uint64_t(kvh) * G + g) * a.key_chunks + c] = best;
+    }
   }
 }
 
@@ -462,12 +479,14 @@ __global__ __launch_bounds__(1024) void k_dec_attn_stats(AttnDecArgs a) {
 }
 
 // Weights (ops.rs:245-258, from the head statistics) and weighted sums
-// (ops.rs:336-351) over kAttnWsumRows window rows for every query head of one
-// KV head, 1024 threads; each workgroup adds its wrapping partial sums to the
-// accumulators atomically (exact in any order). Chunk 0 clears the projection
-// accumulators read by the scores kernel.
+// (ops.rs:336-351) over P chunks of kAttnWsumRows window rows for every query
+// head of one KV head, 1024 threads; each workgroup adds its wrapping partial
+// sums to the accumulators atomically (exact in any order). Workgroup 0
+// clears the projection accumulators read by the scores kernel.
+template <int P, uint32_t MAXHD>
 __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
-  __shared__ int32_t wl[kDecMaxGroup][kAttnWsumRows];
+  constexpr uint32_t R = P * kAttnWsumRows;  // window rows of this workgroup
+  __shared__ int32_t wl[kDecMaxGroup][R];
   __shared__ int64_t part[3][1024];
   seq_view(a);
   const Window win = attn_window(a);
@@ -480,23 +499,26 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
         if (a.has_v) a.qkv[(uint64_t(a.nh) + a.nkv + kvh) * hd + i] = 0;
       }
   }
-  const uint64_t r0 = uint64_t(blockIdx.y) * kAttnWsumRows;
+  const uint64_t r0 = uint64_t(blockIdx.y) * R;
   if (r0 >= win.cnt) return;
-  const uint64_t nr = win.cnt - r0 < kAttnWsumRows ? win.cnt - r0 : kAttnWsumRows;
+  const uint64_t nr = win.cnt - r0 < R ? win.cnt - r0 : R;
   const uint64_t kvw = uint64_t(a.nkv) * hd;
-  // value rows of this chunk: slice sl takes rows 8 sl .. 8 sl + 7, dims dl and dl + 256
+  // value rows: slice sl takes rows 8 sl .. 8 sl + 7 of every chunk, dims dl and dl + 256
   const uint32_t sl = threadIdx.x >> 8, dl = threadIdx.x & 255;
-  int32_t vp[2][kAttnWsumRows / 4];
+  constexpr int JJ = MAXHD > 256 ? 2 : 1;  // dims dl (and dl + 256)
+  int32_t vp[P][JJ][kAttnWsumRows / 4];
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj)
+  for (int p = 0; p < P; ++p)
 #pragma unroll
-    for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
-      const uint32_t d = dl + 256 * jj;
-      const uint64_t rr = sl * (kAttnWsumRows / 4) + k;
-      vp[jj][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
-    }
-  if (threadIdx.x < G * kAttnWsumRows) {
-    const uint32_t gg = threadIdx.x / kAttnWsumRows, rr = threadIdx.x % kAttnWsumRows;
+    for (int jj = 0; jj < JJ; ++jj)
+#pragma unroll
+      for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+        const uint32_t d = dl + 256 * jj;
+        const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
+        vp[p][jj][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
+      }
+  for (uint32_t idx = threadIdx.x; idx < G * R; idx += 1024) {
+    const uint32_t gg = idx / R, rr = idx % R;
     const uint64_t head = uint64_t(kvh) * G + gg;
     int32_t w = 0;
     if (rr < nr) {
@@ -519,11 +541,13 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
       for (uint32_t hh = 0; hh < hn; ++hh) {
         int64_t p0 = 0, p1 = 0;
 #pragma unroll
-        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
-          const int32_t w = wl[h0 + hh][sl * (kAttnWsumRows / 4) + k];
-          p0 = mac(p0, vp[0][k], w);
-          p1 = mac(p1, vp[1][k], w);
-        }
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+          for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+            const int32_t w = wl[h0 + hh][p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k];
+            p0 = mac(p0, vp[p][0][k], w);
+            if (JJ > 1) p1 = mac(p1, vp[p][JJ - 1][k], w);
+          }
         part[sl - 1][hh * dstr + dl] = p0;
         if (dstr == 512) part[sl - 1][hh * dstr + 256 + dl] = p1;
       }
@@ -532,11 +556,13 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
       for (uint32_t hh = 0; hh < hn; ++hh) {
         int64_t p0 = 0, p1 = 0;
 #pragma unroll
-        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
-          const int32_t w = wl[h0 + hh][k];
-          p0 = mac(p0, vp[0][k], w);
-          p1 = mac(p1, vp[1][k], w);
-        }
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+          for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+            const int32_t w = wl[h0 + hh][p * kAttnWsumRows + k];
+            p0 = mac(p0, vp[p][0][k], w);
+            if (JJ > 1) p1 = mac(p1, vp[p][JJ - 1][k], w);
+          }
 #pragma unroll
         for (int q = 0; q < 3; ++q) {
           p0 = int64_t(uint64_t(p0) + uint64_t(part[q][hh * dstr + dl]));
@@ -553,22 +579,24 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
 
 // Single-kernel form for small grids (one sequence, short windows): integer
 // softmax (ops.rs:230-258) and weighted sum (ops.rs:336-351) over
-// kAttnWsumRows window rows for every query head of one KV head, 1024
-// threads. Each workgroup rebuilds the heads' argmax (first maximum) and exp
+// P chunks of kAttnWsumRows window rows for every query head of one KV head,
+// 1024 threads. Each workgroup rebuilds the heads' argmax (first maximum) and exp
 // sum over the whole window from the scores, with 16 / G waves per head (each
 // thread keeps the scores it reads in LDS for the later passes when they
 // fit), weights its own rows, and adds its wrapping partial sums to the
 // accumulators atomically (exact in any order). The workgroup holding a
 // head's argmax row also sums every weight of the window and applies the
 // residual ONE - sum to that row, as the reference does before the weighted
-// sum. Chunk 0 clears the projection accumulators read by the scores kernel.
+// sum. Workgroup 0 clears the projection accumulators read by the scores kernel.
+template <int P, uint32_t MAXHD>
 __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
+  constexpr uint32_t R = P * kAttnWsumRows;  // window rows of this workgroup
   extern __shared__ int32_t sl_dyn[];
   __shared__ int64_t red[16];
   __shared__ int64_t hkey[kDecMaxGroup], hsum[kDecMaxGroup];
   __shared__ uint64_t hrec[kDecMaxGroup];
-  __shared__ int64_t el[kDecMaxGroup][kAttnWsumRows];
-  __shared__ int32_t wl[kDecMaxGroup][kAttnWsumRows];
+  __shared__ int64_t el[kDecMaxGroup][R];
+  __shared__ int32_t wl[kDecMaxGroup][R];
   __shared__ int64_t part[3][1024];
   seq_view(a);
   const Window win = attn_window(a);
@@ -581,22 +609,25 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
         if (a.has_v) a.qkv[(uint64_t(a.nh) + a.nkv + kvh) * hd + i] = 0;
       }
   }
-  const uint64_t r0 = uint64_t(blockIdx.y) * kAttnWsumRows;
+  const uint64_t r0 = uint64_t(blockIdx.y) * R;
   if (r0 >= win.cnt) return;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t nr = win.cnt - r0 < kAttnWsumRows ? win.cnt - r0 : kAttnWsumRows;
+  const uint64_t nr = win.cnt - r0 < R ? win.cnt - r0 : R;
   const uint64_t kvw = uint64_t(a.nkv) * hd;
-  // value rows of this chunk: slice sl takes rows 8 sl .. 8 sl + 7, dims dl and dl + 256
+  // value rows: slice sl takes rows 8 sl .. 8 sl + 7 of every chunk, dims dl and dl + 256
   const uint32_t sl = threadIdx.x >> 8, dl = threadIdx.x & 255;
-  int32_t vp[2][kAttnWsumRows / 4];
+  constexpr int JJ = MAXHD > 256 ? 2 : 1;  // dims dl (and dl + 256)
+  int32_t vp[P][JJ][kAttnWsumRows / 4];
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj)
+  for (int p = 0; p < P; ++p)
 #pragma unroll
-    for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
-      const uint32_t d = dl + 256 * jj;
-      const uint64_t rr = sl * (kAttnWsumRows / 4) + k;
-      vp[jj][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
-    }
+    for (int jj = 0; jj < JJ; ++jj)
+#pragma unroll
+      for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+        const uint32_t d = dl + 256 * jj;
+        const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
+        vp[p][jj][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
+      }
   // this wave's head and its rows r = wi * 64 + lane + stride * n
   const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;
   const bool active = g < G;
@@ -649,9 +680,9 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
     hrec[threadIdx.x] = t < (int64_t(1) << 61) ? softmax_recip(t) : 0;  // 0: generic division
   }
   __syncthreads();
-  // raw weights of this chunk
-  if (threadIdx.x < G * kAttnWsumRows) {
-    const uint32_t gg = threadIdx.x / kAttnWsumRows, rr = threadIdx.x % kAttnWsumRows;
+  // raw weights of this workgroup's rows
+  for (uint32_t idx = threadIdx.x; idx < G * R; idx += 1024) {
+    const uint32_t gg = idx / R, rr = idx % R;
     const uint64_t M = hrec[gg];
     wl[gg][rr] = rr < nr ? (M ? softmax_weight_r(el[gg][rr], hsum[gg], M) : softmax_weight(el[gg][rr], hsum[gg])) : 0;
   }
@@ -696,11 +727,13 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
       for (uint32_t hh = 0; hh < hn; ++hh) {
         int64_t p0 = 0, p1 = 0;
 #pragma unroll
-        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
-          const int32_t w = wl[h0 + hh][sl * (kAttnWsumRows / 4) + k];
-          p0 = mac(p0, vp[0][k], w);
-          p1 = mac(p1, vp[1][k], w);
-        }
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+          for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+            const int32_t w = wl[h0 + hh][p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k];
+            p0 = mac(p0, vp[p][0][k], w);
+            if (JJ > 1) p1 = mac(p1, vp[p][JJ - 1][k], w);
+          }
         part[sl - 1][hh * dstr + dl] = p0;
         if (dstr == 512) part[sl - 1][hh * dstr + 256 + dl] = p1;
       }
@@ -709,11 +742,13 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
       for (uint32_t hh = 0; hh < hn; ++hh) {
         int64_t p0 = 0, p1 = 0;
 #pragma unroll
-        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
-          const int32_t w = wl[h0 + hh][k];
-          p0 = mac(p0, vp[0][k], w);
-          p1 = mac(p1, vp[1][k], w);
-        }
+        for (int p = 0; p < P; ++p)
+#pragma unroll
+          for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+            const int32_t w = wl[h0 + hh][p * kAttnWsumRows + k];
+            p0 = mac(p0, vp[p][0][k], w);
+            if (JJ > 1) p1 = mac(p1, vp[p][JJ - 1][k], w);
+          }
 #pragma unroll
         for (int q = 0; q < 3; ++q) {
           p0 = int64_t(uint64_t(p0) + uint64_t(part[q][hh * dstr + dl]));
@@ -838,30 +873,69 @@ void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const i
   DET_ROW_DISPATCH(k_dec_residual_norm, src, x, normed, w_post, int(has_scalar), scalar, w_next, H, eps, limbs, kpad);
 }
 #undef DET_ROW_DISPATCH
+// Window chunks per attention workgroup: a.rows_mul when set (1, 2 or 4),
+// else the largest that still leaves a workgroup for every CU (a single
+// sequence is latency-bound and keeps one chunk per workgroup; batched steps
+// share each workgroup's head norms, RoPE and atomic adds over more rows); at
+// most 2 for head dims above 256 (register room).
+static uint32_t attn_rows_mul(const AttnDecArgs& a) {
+  const uint32_t cap = a.hd > 256 ? 2 : 4;
+  uint32_t p;
+  if (a.rows_mul == 1 || a.rows_mul == 2 || a.rows_mul == 4) {
+    p = a.rows_mul;
+  } else {
+    const uint64_t wgs = uint64_t(a.nkv) * nblk(a.cap, kAttnScoreRows) * (a.nseq ? a.nseq : 1);
+    p = wgs >= 4 * 256 ? 4 : (wgs >= 2 * 256 ? 2 : 1);
+  }
+  return p < cap ? p : cap;
+}
+#define DET_ATTN_P(P, HD, KERNEL, ...)                                                       \
+  do {                                                                                       \
+    if ((HD) <= 256) {                                                                       \
+      if ((P) == 4) hipLaunchKernelGGL((KERNEL<4, 256>), __VA_ARGS__);                       \
+      else if ((P) == 2) hipLaunchKernelGGL((KERNEL<2, 256>), __VA_ARGS__);                  \
+      else hipLaunchKernelGGL((KERNEL<1, 256>), __VA_ARGS__);                                \
+    } else {                                                                                 \
+      if ((P) == 2) hipLaunchKernelGGL((KERNEL<2, kDecMaxHeadDim>), __VA_ARGS__);            \
+      else hipLaunchKernelGGL((KERNEL<1, kDecMaxHeadDim>), __VA_ARGS__);                     \
+    }                                                                                        \
+  } while (0)
+template <bool VEC>
+static void launch_scores(const AttnDecArgs& a, uint32_t P, dim3 grid, hipStream_t s) {
+  if (a.hd <= 256) {
+    if (P == 4) hipLaunchKernelGGL((k_dec_attn_scores<VEC, 4, 256>), grid, dim3(512), 0, s, a);
+    else if (P == 2) hipLaunchKernelGGL((k_dec_attn_scores<VEC, 2, 256>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((k_dec_attn_scores<VEC, 1, 256>), grid, dim3(512), 0, s, a);
+  } else {
+    if (P == 2) hipLaunchKernelGGL((k_dec_attn_scores<VEC, 2, kDecMaxHeadDim>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((k_dec_attn_scores<VEC, 1, kDecMaxHeadDim>), grid, dim3(512), 0, s, a);
+  }
+}
 void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
   // grids cover the cache capacity (every window fits in it); idle chunks exit
   const uint32_t ns = a.nseq ? a.nseq : 1;
+  const uint32_t P = attn_rows_mul(a);
   if (part == 0) {
-    const dim3 grid(a.nkv, nblk(a.cap, kAttnScoreRows), ns);
-    if (a.hd % 64 == 0)
-      hipLaunchKernelGGL(k_dec_attn_scores<true>, grid, dim3(512), 0, s, a);
-    else
-      hipLaunchKernelGGL(k_dec_attn_scores<false>, grid, dim3(512), 0, s, a);
+    const dim3 grid(a.nkv, nblk(a.cap, P * kAttnScoreRows), ns);
+    if (a.hd % 64 == 0) launch_scores<true>(a, P, grid, s);
+    else launch_scores<false>(a, P, grid, s);
   } else if (part == 1) {
     const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.lds_stride * 4 : 0;
     hipLaunchKernelGGL(k_dec_attn_stats, dim3(a.nkv, 1, ns), dim3(1024), lds, s, a);
   } else if (part == 2) {
-    hipLaunchKernelGGL(k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows), ns), dim3(1024), 0, s, a);
+    DET_ATTN_P(P, a.hd, k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, P * kAttnWsumRows), ns), dim3(1024), 0, s, a);
   } else {
     const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.lds_stride * 4 : 0;
-    hipLaunchKernelGGL(k_dec_attn_softmax_wsum, dim3(a.nkv, nblk(a.cap, kAttnWsumRows), ns), dim3(1024), lds, s, a);
+    DET_ATTN_P(P, a.hd, k_dec_attn_softmax_wsum, dim3(a.nkv, nblk(a.cap, P * kAttnWsumRows), ns), dim3(1024), lds, s,
+               a);
   }
 }
+#undef DET_ATTN_P
 // The weighted-sum workgroups of the single-kernel form each rebuild the
 // window statistics; that redundancy is free while the grid fits the device
 // in one pass, beyond it a separate statistics pass is cheaper.
 bool dec_attention_split(const AttnDecArgs& a) {
-  const uint64_t wgs = uint64_t(a.nkv) * nblk(a.cap, kAttnWsumRows) * (a.nseq ? a.nseq : 1);
+  const uint64_t wgs = uint64_t(a.nkv) * nblk(a.cap, attn_rows_mul(a) * kAttnWsumRows) * (a.nseq ? a.nseq : 1);
   return wgs > 256;
 }
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s) {
