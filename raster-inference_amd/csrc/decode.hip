@@ -180,17 +180,29 @@ __device__ __forceinline__ int64_t score_key(int32_t score, uint64_t j) {
 // (det_kernels.rs:952-998): x = requant(acc) (the accumulators are read
 // here and cleared later), y = rmsnorm(x) * gain; the un-gained norm goes to
 // `plain` when given (k_eq_v values).
-__device__ __forceinline__ void norm_head_row(const int64_t* __restrict__ src, uint32_t hd, int64_t eps,
-                                              const int32_t* __restrict__ gain, int32_t* __restrict__ dst,
-                                              int32_t* __restrict__ plain, uint32_t lane) {
+// A head row's accumulators and gains as one lane reads them (element
+// lane + 64 k), so that they can be fetched before other loads are issued.
+struct HeadRowIn {
+  int64_t acc[kDecMaxHeadDim / 64];
+  int32_t gain[kDecMaxHeadDim / 64];
+};
+__device__ __forceinline__ void load_head_row(const int64_t* __restrict__ src, uint32_t hd,
+                                              const int32_t* __restrict__ gain, uint32_t lane, HeadRowIn& in) {
+#pragma unroll
+  for (int k = 0; k < int(kDecMaxHeadDim / 64); ++k) {
+    const uint32_t d = lane + 64 * k;
+    in.acc[k] = d < hd ? src[d] : 0;
+    in.gain[k] = (gain && d < hd) ? gain[d] : 0;
+  }
+}
+__device__ __forceinline__ void norm_head_row(const HeadRowIn& in, uint32_t hd, int64_t eps, bool has_gain,
+                                              int32_t* __restrict__ dst, int32_t* __restrict__ plain, uint32_t lane) {
   constexpr int kPer = kDecMaxHeadDim / 64;
-  int32_t xv[kPer], gv[kPer];
+  int32_t xv[kPer];
   int64_t ss = 0;
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
-    const uint32_t d = lane + 64 * k;
-    xv[k] = d < hd ? requant(src[d]) : 0;
-    gv[k] = (gain && d < hd) ? gain[d] : 0;
+    xv[k] = requant(in.acc[k]);  // zero past hd
     ss = add_sat64(ss, sq_term(xv[k]));
   }
   ss = wsum_sat(ss);
@@ -200,10 +212,17 @@ __device__ __forceinline__ void norm_head_row(const int64_t* __restrict__ src, u
     const uint32_t d = lane + 64 * k;
     if (d < hd) {
       const int32_t v = mul_sat(xv[k], sc);
-      dst[d] = gain ? mul_sat(v, gv[k]) : v;
+      dst[d] = has_gain ? mul_sat(v, in.gain[k]) : v;
       if (plain) plain[d] = v;
     }
   }
+}
+__device__ __forceinline__ void norm_head_row(const int64_t* __restrict__ src, uint32_t hd, int64_t eps,
+                                              const int32_t* __restrict__ gain, int32_t* __restrict__ dst,
+                                              int32_t* __restrict__ plain, uint32_t lane) {
+  HeadRowIn in;
+  load_head_row(src, hd, gain, lane, in);
+  norm_head_row(in, hd, eps, gain != nullptr, dst, plain, lane);
 }
 
 // This workgroup's sequence view of a (possibly batched) launch: grid z picks
@@ -241,8 +260,22 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   __shared__ int32_t kn[kDecMaxHeadDim];
   __shared__ int64_t ck[P][kDecMaxGroup][kAttnScoreRows];
   seq_view(a);
-  const Window win = attn_window(a);
   const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
+  // head-norm jobs: 0..G-1 the queries, G the new key, G + 1 the new value.
+  // This wave's first job's accumulators are read before anything else (the
+  // key-row loads below would otherwise be waited for first); the key and
+  // value rows are read even where this workgroup turns out not to hold the
+  // step's own row, and then go unused.
+  const uint32_t wv = threadIdx.x >> 6;
+  const uint32_t njobs_max = G + (a.own_cache ? (a.has_v ? 2u : 1u) : 0u);
+  HeadRowIn pre;
+  auto job_src = [&](uint32_t job) {
+    return job < G ? a.qkv + (uint64_t(kvh) * G + job) * hd
+                   : a.qkv + (uint64_t(a.nh) + (job == G ? 0 : a.nkv) + kvh) * hd;
+  };
+  auto job_gain = [&](uint32_t job) { return job < G ? a.q_norm : (job == G ? a.k_norm : nullptr); };
+  if (wv < njobs_max) load_head_row(job_src(wv), hd, job_gain(wv), threadIdx.x & 63, pre);
+  const Window win = attn_window(a);
   const uint64_t r0 = uint64_t(blockIdx.y) * P * kAttnScoreRows;
   const uint64_t qoff = uint64_t(kvh) * G * hd;
   if (blockIdx.y == 0)
@@ -297,12 +330,16 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   int32_t* kslot = a.k + win.slot * kvw + uint64_t(kvh) * hd;
   int32_t* vslot = a.v + win.slot * kvw + uint64_t(kvh) * hd;
   for (uint32_t job = wave; job < G + nkeys; job += 8) {
+    HeadRowIn in;
+    if (job == wave) in = pre;
+    else load_head_row(job_src(job), hd, job_gain(job), lane, in);
+    const bool gained = job_gain(job) != nullptr;
     if (job < G) {
-      norm_head_row(a.qkv + (uint64_t(kvh) * G + job) * hd, hd, a.eps, a.q_norm, ql + job * hd, nullptr, lane);
+      norm_head_row(in, hd, a.eps, gained, ql + job * hd, nullptr, lane);
     } else if (job == G) {
-      norm_head_row(a.qkv + (uint64_t(a.nh) + kvh) * hd, hd, a.eps, a.k_norm, kn, a.has_v ? nullptr : vslot, lane);
+      norm_head_row(in, hd, a.eps, gained, kn, a.has_v ? nullptr : vslot, lane);
     } else {
-      norm_head_row(a.qkv + (uint64_t(a.nh) + a.nkv + kvh) * hd, hd, a.eps, nullptr, vslot, nullptr, lane);
+      norm_head_row(in, hd, a.eps, gained, vslot, nullptr, lane);
     }
   }
   __syncthreads();
