@@ -275,6 +275,19 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   };
   auto job_gain = [&](uint32_t job) { return job < G ? a.q_norm : (job == G ? a.k_norm : nullptr); };
   if (wv < njobs_max) load_head_row(job_src(wv), hd, job_gain(wv), threadIdx.x & 63, pre);
+  // cos/sin of this thread's first two rotation slots, also read ahead of the
+  // key rows (later slots, for rows x half > 1024, load theirs in the rotation
+  // loop)
+  const uint32_t half = uint32_t(a.rotary / 2);
+  int32_t tc[2] = {0, 0}, ts[2] = {0, 0};
+  if (half)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t idx = threadIdx.x + 512 * u;
+      const uint32_t i = idx % half;
+      tc[u] = a.trig[2 * i];
+      ts[u] = a.trig[2 * i + 1];
+    }
   const Window win = attn_window(a);
   const uint64_t r0 = uint64_t(blockIdx.y) * P * kAttnScoreRows;
   const uint64_t qoff = uint64_t(kvh) * G * hd;
@@ -313,18 +326,6 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
       }
     }
   }
-  // cos/sin of this thread's first two rotation slots, fetched early (later
-  // slots, for rows x half > 1024, load theirs in the rotation loop)
-  const uint32_t half = uint32_t(a.rotary / 2);
-  int32_t tc[2] = {0, 0}, ts[2] = {0, 0};
-  if (half)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const uint32_t idx = threadIdx.x + 512 * u;
-      const uint32_t i = idx % half;
-      tc[u] = a.trig[2 * i];
-      ts[u] = a.trig[2 * i + 1];
-    }
   // head rows: jobs 0..G-1 are the queries, then the new key (and value) rows
   const uint32_t nkeys = has_new ? (a.has_v ? 2 : 1) : 0;
   int32_t* kslot = a.k + win.slot * kvw + uint64_t(kvh) * hd;
