@@ -113,28 +113,51 @@ DET_HD int64_t acc_mul(int64_t lhs, int64_t rhs) {
 // 2^32/sqrt(x) in the sense |c^2 x - 2^64| minimal, ties to even; x == 0 and
 // tiny x saturate to i32::MAX.
 // For x >= 5 the lower candidate lo = max{c : c^2 x <= 2^64} is below
-// 2^31 - 1. A double estimate of 2^32/sqrt(x) is within 2^-21 of the real
-// value, so lo is found by at most one step either way with the exact test
-// on the 128-bit product c^2 x. Then |lo^2 x - 2^64| vs |hi^2 x - 2^64|
-// (hi = lo + 1) is the sign of 2^65 - (lo^2 + hi^2) x, again one exact
-// 128-bit product.
+// 2^31 - 1. An estimate of 2^32/sqrt(x) is moved to lo one step at a time
+// with the exact test on the 128-bit product c^2 x, so lo is exact whatever
+// the estimate's error (the double estimate is within one of it). Then
+// |lo^2 x - 2^64| vs |hi^2 x - 2^64| (hi = lo + 1) is the sign of
+// 2^65 - (lo^2 + hi^2) x, again one exact 128-bit product. On the GPU the
+// 128-bit products are a 64-bit multiply and multiply-high, and the estimate
+// is the hardware reciprocal square root refined by one Newton step.
+DET_HD void mul_64x64(uint64_t a, uint64_t b, uint64_t* hi, uint64_t* lo) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  *hi = __umul64hi(a, b);
+  *lo = a * b;
+#else
+  const u128 p = u128(a) * b;
+  *hi = uint64_t(p >> 64);
+  *lo = uint64_t(p);
+#endif
+}
 DET_HD bool sq_times_le_2_64(uint64_t c, uint64_t x) {  // c^2 x <= 2^64, c < 2^31
-  const u128 p = u128(c * c) * x;
-  return (p >> 64) == 0 || p == (u128(1) << 64);
+  uint64_t hi, lo;
+  mul_64x64(c * c, x, &hi, &lo);
+  return hi == 0 || (hi == 1 && lo == 0);
+}
+DET_HD uint64_t inv_sqrt_estimate(uint64_t ux) {  // about 2^32 / sqrt(ux)
+#if defined(__HIP_DEVICE_COMPILE__)
+  const double xd = double(ux);
+  double r = __builtin_amdgcn_rsq(xd);
+  r = r * (1.5 - 0.5 * xd * r * r);
+  return uint64_t(4294967296.0 * r);
+#else
+  return uint64_t(4294967296.0 / __builtin_sqrt(double(ux)));
+#endif
 }
 DET_HD int32_t inv_sqrt_acc(int64_t x) {
   // (2^31-1)^2 * x <= 2^64 exactly for x <= 4
   if (x <= 4) return INT32_MAX;  // includes x == 0 (negative x is rejected upstream)
   const uint64_t ux = uint64_t(x);
-  uint64_t lo = uint64_t(4294967296.0 / __builtin_sqrt(double(ux)));
+  uint64_t lo = inv_sqrt_estimate(ux);
   if (lo > 2147483646ull) lo = 2147483646ull;
   while (lo > 0 && !sq_times_le_2_64(lo, ux)) --lo;
   while (sq_times_le_2_64(lo + 1, ux)) ++lo;
   const uint64_t hi = lo + 1;
-  const u128 p = u128(lo * lo + hi * hi) * ux;  // lo^2 + hi^2 < 2^63
-  const u128 two65 = u128(1) << 65;
-  if (p == two65) return int32_t((lo & 1) == 0 ? lo : hi);
-  return int32_t(p > two65 ? lo : hi);
+  uint64_t ph, pl;  // (lo^2 + hi^2) x against 2^65 = (2, 0); lo^2 + hi^2 < 2^63
+  mul_64x64(lo * lo + hi * hi, ux, &ph, &pl);
+  if (ph == 2 && pl == 0) return int32_t((lo & 1) == 0 ? lo : hi);
+  return int32_t(ph >= 2 ? lo : hi);
 }
 
 // Round-half-even quotient of a non-negative v < 2^63 by 1 <= d < 2^32

@@ -1,0 +1,28 @@
+"""The product's integer arithmetic (det_arith.h) as the GPU executes it,
+against the oracle: the device build of inv_sqrt_acc takes its own path (a
+hardware reciprocal-square-root estimate refined by one Newton step, then the
+exact integer correction) and its own 64x64->128-bit products, which the host
+build of the same header never compiles. The driver (tests/devmath/
+gpu_devmath.hip) is built in-tree before the run."""
+import pathlib
+import subprocess
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+BIN = pathlib.Path(__file__).resolve().parent / "devmath" / "build" / "gpu_devmath"
+
+
+def test_device_inv_sqrt_and_rms_scale_match_oracle():
+    if not BIN.exists():
+        pytest.fail(f"{BIN} is not built (make -C tests/devmath)")
+    res = subprocess.run([str(BIN), "2000000"], capture_output=True, text=True, timeout=100)
+    rows = {}
+    for line in res.stdout.splitlines():
+        if line and not line.startswith(" "):
+            name, n, bad = line.split()
+            rows[name] = (int(n), int(bad))
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert set(rows) == {"gpu_inv_sqrt_acc", "gpu_rms_scale"}, res.stdout
+    assert all(bad == 0 and n > 0 for n, bad in rows.values()), res.stdout
