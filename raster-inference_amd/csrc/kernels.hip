@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include <algorithm>
@@ -276,6 +277,118 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
       }
     }
   }
+}
+
+// Batch-1 GEMV for matrices of a few thousand tiles or fewer: one workgroup
+// per 16-row tile, NW waves splitting K into shares of at most D steps per
+// load batch, so that up to NW * D * 128 columns take a single weight round
+// trip. Each wave reads the raw activations of its batch, then issues its
+// weight loads, and converts the activations into limb planes in a private
+// LDS slice while the weights are in flight (no workgroup barrier before the
+// MFMAs). The NW partial tiles combine through LDS; acc_out != null receives
+// the Q32.32 accumulators (plain stores), else out the requantized rows.
+// IN64: the activation row is a wrapped Q32.32 accumulator row, requantized
+// on load.
+constexpr int kTileD = 5;
+template <int NW, bool IN64>
+__global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict__ q, const int32_t* __restrict__ scale,
+                                                       const int32_t* __restrict__ rowsum, const void* __restrict__ act_v,
+                                                       uint64_t k, uint64_t n_rows, uint64_t kpad,
+                                                       int32_t* __restrict__ out, int64_t* __restrict__ acc_out) {
+  constexpr int D = kTileD;
+  constexpr int kPass = (D * 32 + 63) / 64;             // activation quads per lane and batch
+  constexpr uint32_t kPlane = kPass * 256 + 32;          // limb plane stride of a wave slice
+  static_assert(4 * kPlane >= 64 * sizeof(v4i), "a wave slice holds the wave's partial tile");
+  __shared__ __attribute__((aligned(16))) uint8_t al[NW][4 * kPlane];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const uint64_t tile = blockIdx.x;
+  const uint64_t nsteps = kpad / 128;
+  const uint64_t per = (nsteps + NW - 1) / NW;
+  const uint64_t s0 = uint64_t(wave) * per < nsteps ? uint64_t(wave) * per : nsteps;
+  const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
+  const v4i* bp = reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 32);
+  const bool a_on = i < 4;  // A row i = limb i of the one token
+  const uint8_t* aread = al[wave] + (i & 3) * kPlane + 32 * g;
+  const v4i zero = {0, 0, 0, 0};
+  v4i acc = zero;
+  for (uint64_t sb = s0; sb < s1; sb += D) {
+    const uint64_t c0 = sb * 128, cend = (sb + D < s1 ? sb + D : s1) * 128;
+    // raw activations (lane takes columns c0 + 4 (lane + 64 r) .. + 3), read
+    // at clamped addresses and masked afterwards so that no load is predicated
+    using AT = typename std::conditional<IN64, int64_t, int32_t>::type;
+    const AT* act = static_cast<const AT*>(act_v);
+    AT av[kPass][4];
+#pragma unroll
+    for (int r = 0; r < kPass; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t c = c0 + 4 * (uint64_t(lane) + 64 * r) + e;
+        av[r][e] = act[c < k ? c : k - 1];
+      }
+    // weights of the batch; steps past the share re-read its last step and
+    // meet zero A operands
+    v4i b[2 * D];
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const uint64_t st = sb + u < s1 ? sb + u : s1 - 1;
+      b[2 * u] = __builtin_nontemporal_load(bp + st * 128);
+      b[2 * u + 1] = __builtin_nontemporal_load(bp + st * 128 + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the conversion waits
+    // limb planes of the batch: byte j of a ^ 0x00808080, 0 past k (where the
+    // weights are 0 too) and past the share
+#pragma unroll
+    for (int r = 0; r < kPass; ++r) {
+      const uint32_t qd = uint32_t(lane) + 64 * r;
+      const uint64_t c = c0 + 4 * uint64_t(qd);
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int32_t a = IN64 ? requant(int64_t(av[r][e])) : int32_t(av[r][e]);
+        w[e] = (c + e < k && c + e < cend) ? (uint32_t(a) ^ 0x00808080u) : 0u;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) packed |= ((w[e] >> (8 * j)) & 0xffu) << (8 * e);
+        *reinterpret_cast<uint32_t*>(al[wave] + j * kPlane + 4 * qd) = packed;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    v4i a[2 * D];
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      a[2 * u] = *reinterpret_cast<const v4i*>(aread + u * 128);
+      a[2 * u + 1] = *reinterpret_cast<const v4i*>(aread + u * 128 + 16);
+    }
+    if (!a_on)
+#pragma unroll
+      for (int u = 0; u < 2 * D; ++u) a[u] = zero;
+#pragma unroll
+    for (int u = 0; u < 2 * D; ++u) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u], b[u], acc, 0, 0, 0);
+    // this batch's A reads precede the next batch's plane writes
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
+  // each wave's partial tile goes to its own slice (which only it has used)
+  reinterpret_cast<v4i*>(al[wave])[lane] = acc;
+  __syncthreads();
+  if (wave != 0 || g != 0) return;
+  // lane i: output row 16 tile + i, limb j in component j
+  int64_t p[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const v4i v = reinterpret_cast<const v4i*>(al[w])[lane];
+    p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+  }
+  const uint64_t row = tile * 16 + i;
+  if (row >= n_rows) return;
+  const int64_t r = limb_combine(p, rowsum[row], scale[row]);
+  if (acc_out) acc_out[row] = r;
+  else out[row] = requant(r);
 }
 
 // Decode GEMV reading the activations as limb planes in global memory (token
@@ -1245,6 +1358,29 @@ static void launch_lds_gemv(const DevMatrix& W, const void* act, uint64_t ld_act
 
 bool gemv_fits_lds(const DevMatrix& W, uint64_t m) { return m * 4 * (W.kpad + 32) <= kGemvLdsBudget; }
 
+// One-tile-per-workgroup batch-1 GEMV (k_gemv_tile) for int8 matrices of at
+// most kTileMaxTiles tiles; larger ones (the lm_head) amortise one activation
+// prologue over many tiles in k_gemv_i8_lds.
+constexpr uint64_t kTileMaxTiles = 4096;
+static bool gemv_tile_fits(const DevMatrix& W) { return W.storage == kInt8 && (W.rows + 15) / 16 <= kTileMaxTiles; }
+static void launch_gemv_tile(const DevMatrix& W, const void* act, bool in64, int32_t* o, int64_t* ao, hipStream_t s) {
+  const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
+  const int nw = nsteps <= 4 * kTileD ? 4 : (nsteps <= 8 * kTileD ? 8 : 16);
+#define DET_TILE_LAUNCH(NW, IN)                                                                                 \
+  hipLaunchKernelGGL((k_gemv_tile<NW, IN>), dim3(unsigned(ntiles)), dim3(64 * NW), 0, s, W.q, W.scale, W.rowsum, \
+                     act, W.cols, W.rows, W.kpad, o, ao)
+  if (in64) {
+    if (nw == 4) DET_TILE_LAUNCH(4, true);
+    else if (nw == 8) DET_TILE_LAUNCH(8, true);
+    else DET_TILE_LAUNCH(16, true);
+  } else {
+    if (nw == 4) DET_TILE_LAUNCH(4, false);
+    else if (nw == 8) DET_TILE_LAUNCH(8, false);
+    else DET_TILE_LAUNCH(16, false);
+  }
+#undef DET_TILE_LAUNCH
+}
+
 void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int epilogue, int32_t* out,
                         hipStream_t s) {
   if (act_i64) launch_lds_gemv<true, 0>(W, act, W.cols, 1, out, W.rows, nullptr, s);
@@ -1252,11 +1388,14 @@ void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int e
   else launch_lds_gemv<false, 0>(W, act, W.cols, 1, out, W.rows, nullptr, s);
 }
 
-// Decode GEMV into wrapping Q32.32 accumulators that are zero on entry. Eight
-// waves split K inside each workgroup; K is further split across workgroups
-// (doubling) until the launch has at least 512 workgroups, keeping at least
-// one K step per wave and at most 1024 workgroups.
+// Decode GEMV into wrapping Q32.32 accumulators that are zero on entry:
+// k_gemv_tile where the matrix is small enough (one workgroup per tile, plain
+// stores); otherwise eight waves split K inside each workgroup and K is
+// further split across workgroups (doubling) until the launch has at least
+// 512 workgroups, keeping at least one K step per wave and at most 1024
+// workgroups (atomic adds).
 void launch_gemv_decode_acc(const DevMatrix& W, const void* act, bool act_i64, int64_t* acc, hipStream_t s) {
+  if (gemv_tile_fits(W)) return launch_gemv_tile(W, act, act_i64, nullptr, acc, s);
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
   int ks = 8;
   while (ks > 1 && uint64_t(ks) > nsteps) ks >>= 1;
@@ -1436,7 +1575,9 @@ void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t 
       const uint32_t mm = uint32_t(m - t0 < 4 ? m - t0 : 4);
       int32_t* o = acc_out ? nullptr : out + t0 * ld_out;
       int64_t* ao = acc_out ? acc_out + t0 * ld_out : nullptr;
-      if (gemv_fits_lds(W, mm)) {
+      if (mm == 1 && gemv_tile_fits(W)) {
+        launch_gemv_tile(W, act + t0 * ld_act, false, o, ao, s);
+      } else if (gemv_fits_lds(W, mm)) {
         launch_lds_gemv<false, 0>(W, act + t0 * ld_act, ld_act, mm, o, ld_out, ao, s);
       } else {
         launch_act_limbs(act + t0 * ld_act, mm, W.cols, ld_act, W.kpad, limbs, s);

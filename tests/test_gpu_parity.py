@@ -56,7 +56,10 @@ def test_gemv_int8_every_tail_length(ctx, cols):
     assert np.array_equal(got, oracle_gemv(expand(q, s), act))
 
 
-@pytest.mark.parametrize("rows,cols", [(2560, 2560), (10240, 2560), (2560, 10240), (385, 64), (17, 4096)])
+# K of 12345 / 16384 takes two load batches per wave in the one-tile-per-
+# workgroup kernel; 65552 rows (4097 tiles) goes to the persistent kernel
+@pytest.mark.parametrize("rows,cols", [(2560, 2560), (10240, 2560), (2560, 10240), (385, 64), (17, 4096),
+                                       (2048, 2560), (33, 16384), (100, 12345), (65552, 128), (65536, 130)])
 def test_gemv_int8_decode_shapes(ctx, rows, cols):
     q, s, act = synthetic.gemv_problem(rows, cols, seed=rows * 7 + cols)
     mat = ctx.upload_matrix(q, s)
@@ -287,3 +290,4 @@ def test_gpu_tiny_baseline_model_matches_oracle(ctx):
     exp = om.capture(prompt, 8)
     got = gm.capture(prompt, 8)
     assert got == exp
+
