@@ -527,6 +527,134 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
   }
 }
 
+// Single-token form of k_gemv_dec (same arguments, outputs and K split) for
+// K shares of 4-5 steps per wave (E4B's gate/up projection): the four limb
+// planes of a wave's share are copied into a private LDS slice with
+// global_load_lds, so that they hold no registers while in flight and all
+// D = 5 weight steps of the share fit in registers at once, one weight round
+// trip (k_gemv_dec holds A and B in registers and takes 3 steps per trip).
+// Every load goes to a clamped address (none is predicated); steps past the
+// share meet zero A operands.
+template <int KS, int EPI>
+__global__ __launch_bounds__(256, 5) void k_gemv_dec1(
+    const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
+    const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, int32_t* __restrict__ out,
+    int64_t* __restrict__ acc_out, int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
+  constexpr int D = 5;
+  constexpr int kCopies = (4 * D * 128 + 1023) / 1024;  // 1 KB wave copies of 4 planes x D steps
+  __shared__ __attribute__((aligned(16))) int8_t al[4][kCopies * 1024];
+  __shared__ v4i part[KS > 1 ? 4 : 1][64];
+  constexpr int TPW = 4 / KS;
+  constexpr int kWaitLds = 15 | (7 << 4) | (0 << 8) | (3 << 14);  // lgkmcnt(0)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, i = lane & 15;
+  const int slot = wave / KS, kp = wave % KS;
+  const uint64_t nsteps = kpad / 128;
+  const uint32_t kc = blockIdx.x % kchunks;
+  const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
+  const uint64_t cs0 = kc * cper < nsteps ? kc * cper : nsteps;
+  const uint64_t cs1 = cs0 + cper < nsteps ? cs0 + cper : nsteps;
+  const uint64_t per = (cs1 - cs0 + KS - 1) / KS;
+  const uint64_t s0 = cs0 + kp * per < cs1 ? cs0 + kp * per : cs1;
+  const uint64_t s1 = s0 + per < cs1 ? s0 + per : cs1;
+  // A row i < 4 is limb i of the token: plane i, bytes [32 g, 32 g + 32) of each step
+  const bool a_on = i < 4;
+  const int8_t* aread = al[wave] + (i & 3) * (D * 128) + 32 * g;
+  const uint64_t ntiles = (n_rows + 15) / 16;
+  const uint64_t groups = gridDim.x / kchunks;
+  const v4i zero = {0, 0, 0, 0};
+  for (uint64_t base = uint64_t(blockIdx.x / kchunks) * TPW; base < ntiles; base += groups * TPW) {
+    const uint64_t tile = base + slot;
+    const uint64_t row = tile * 16 + i;
+    const bool t_on = tile < ntiles;
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : ntiles - 1) * nsteps * 2048 + lane * 32);
+    v4i acc = zero;
+    for (uint64_t sb = s0; sb < s1; sb += D) {
+      const uint64_t nu = s1 - sb < uint64_t(D) ? s1 - sb : uint64_t(D);
+      // the previous batch's operand reads are done before its slice is overwritten
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(kWaitLds);
+      asm volatile("" ::: "memory");
+      // A: copy r, lane l takes the 16-byte piece (64 r + l) % 8 of chunk (64 r + l) / 8 =
+      // (plane, step u) at slice offset 128 (D plane + u); chunks past the 4 D real ones
+      // re-read the last real one into the slice's slack
+#pragma unroll
+      for (int r = 0; r < kCopies; ++r) {
+        const uint32_t idx = 64 * r + lane, chunk = idx >> 3, piece = idx & 7;
+        const uint32_t c = chunk < uint32_t(4 * D) ? chunk : uint32_t(4 * D - 1);
+        const uint32_t plane = c / D, u = c % D;
+        const uint64_t st = sb + u < s1 ? sb + u : s1 - 1;
+        const int8_t* src = limbs + plane * kpad + st * 128 + piece * 16;
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
+                                         (void __attribute__((address_space(3)))*)(al[wave] + r * 1024), 16, 0, 0);
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      // B: the share's weight steps (past the share: its last step again)
+      v4i b[2 * D];
+#pragma unroll
+      for (int u = 0; u < D; ++u) {
+        const uint64_t st = sb + u < s1 ? sb + u : s1 - 1;
+        b[2 * u] = __builtin_nontemporal_load(bp + st * 128);
+        b[2 * u + 1] = __builtin_nontemporal_load(bp + st * 128 + 1);
+      }
+      // the copies have landed once every load of the batch has (the compiler does not
+      // order LDS reads after global_load_lds by itself; waiting for all loads holds
+      // whatever order it gives the weight loads)
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(0);
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int u = 0; u < D; ++u) {
+        // idle rows and steps past the share: a mask, not a branch, so the reads stay unconditional
+        const int m = (a_on && uint64_t(u) < nu) ? -1 : 0;
+        const v4i a0 = *reinterpret_cast<const v4i*>(aread + u * 128) & m;
+        const v4i a1 = *reinterpret_cast<const v4i*>(aread + u * 128 + 16) & m;
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b[2 * u], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b[2 * u + 1], acc, 0, 0, 0);
+      }
+    }
+    int64_t p[4] = {acc[0], acc[1], acc[2], acc[3]};
+    if (KS > 1) {
+      part[wave][lane] = acc;
+      __syncthreads();
+      if (kp == 0) {
+#pragma unroll
+        for (int w = 1; w < KS; ++w) {
+          const v4i v = part[wave + w][lane];
+          p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+        }
+      }
+      __syncthreads();
+    }
+    if (kp != 0 || !t_on) continue;
+    const bool r_on = row < n_rows;
+    const int32_t rs = r_on ? rowsum[row] : 0, sc = r_on ? scale[row] : 0;
+    // lanes 0-15 (g = 0) hold the token's four limb sums of row i
+    const bool ok = g == 0 && r_on;
+    if (acc_out) {
+      if (ok) {
+        const int64_t a = limb_combine(p, kc == 0 ? rs : 0, sc);
+        atomicAdd(reinterpret_cast<unsigned long long*>(acc_out + row), static_cast<unsigned long long>(a));
+      }
+    } else if (EPI == 1) {
+      const int32_t r = ok ? requant(limb_combine(p, rs, sc)) : 0;
+      const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
+      if (ok && i < 8) {
+        const uint64_t f = tile * 8 + i;
+        const int32_t h = mul_sat(gelu_act(r), up);
+        out[f] = h;
+        const uint32_t u = uint32_t(h) ^ 0x00808080u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out_limbs[j * out_kpad + f] = int8_t(uint8_t(u >> (8 * j)));
+      }
+    } else if (ok) {
+      out[row] = requant(limb_combine(p, rs, sc));
+    }
+  }
+}
+
 // Decode GEMV for 5-16 tokens (NG = 2 or 4 groups of 4): the A tiles of a K
 // step are as large as the weight tile or larger, so the four waves of a
 // workgroup take four consecutive weight tiles over the same K steps and
@@ -1429,8 +1557,15 @@ template <int KS, int EPI, int NG>
 static void launch_gemv_dec_ks(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, uint32_t kc, uint64_t groups,
                                int32_t* out, uint64_t out_ld, int64_t* acc, uint64_t acc_ld, int8_t* out_limbs,
                                uint64_t out_kpad, hipStream_t s) {
-  hipLaunchKernelGGL((k_gemv_dec<KS, EPI, NG>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,
-                     limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad);
+  // k_gemv_dec takes shares of up to 3 K steps in one round trip and is the
+  // faster of the two there (measured on E4B's qkv and down projections)
+  const uint64_t nsteps = W.kpad / 128, cper = (nsteps + kc - 1) / kc, per = (cper + KS - 1) / KS;
+  if (NG == 1 && ntok == 1 && per > 3)
+    hipLaunchKernelGGL((k_gemv_dec1<KS, EPI>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,
+                       limbs, W.rows, W.kpad, kc, out, acc, out_limbs, out_kpad);
+  else
+    hipLaunchKernelGGL((k_gemv_dec<KS, EPI, NG>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,
+                       limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad);
 }
 
 template <int NG>
@@ -1438,6 +1573,7 @@ static void launch_gemv_dec_ng(const DevMatrix& W, const int8_t* limbs, uint32_t
                                int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
                                hipStream_t s) {
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
+  // (k_gemv_dec1 has the same 5 workgroups per CU as k_gemv_dec<4, 0, 1>)
   const uint64_t cap = resident_blocks(reinterpret_cast<const void*>(&k_gemv_dec<4, 0, NG>), 256);
   auto groups = [&](int ks) { return (ntiles * ks + 3) / 4; };
   // in-workgroup K split: smallest that fills the device, keeping >= 4 K steps per wave
