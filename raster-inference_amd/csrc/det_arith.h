@@ -149,6 +149,30 @@ DET_HD int32_t inv_sqrt_acc(int64_t x) {
   // (2^31-1)^2 * x <= 2^64 exactly for x <= 4
   if (x <= 4) return INT32_MAX;  // includes x == 0 (negative x is rejected upstream)
   const uint64_t ux = uint64_t(x);
+#if defined(__HIP_DEVICE_COMPILE__)
+  {
+    // The result is lo = floor(Y), Y = 2^32 / sqrt(x), or lo + 1 when
+    // Y > T = sqrt(lo^2 + lo + 1/2) (the exact rule below: (lo^2 + hi^2) x
+    // against 2^65). Y = T is impossible: it needs x (2 lo^2 + 2 lo + 1) =
+    // 2^65 with an odd factor above 1 (lo = 0 would need x = 2^65). The
+    // estimate y (hardware rsq, two Newton steps; double x within 2^-53)
+    // has relative error below 2^-49.5 and y < 2^31.5, so |y - Y| < 2^-18;
+    // t is within 2^-20 of T. Both decisions are taken from y only when y
+    // is more than 2^-14 from the integer and from t; otherwise the exact
+    // integer search runs.
+    const double xd = double(ux);
+    double r = __builtin_amdgcn_rsq(xd);
+    r = r * (1.5 - 0.5 * xd * r * r);
+    r = r * (1.5 - 0.5 * xd * r * r);
+    const double y = 4294967296.0 * r;
+    const double fl = __builtin_floor(y);
+    const double fr = y - fl;  // exact
+    const double t = __builtin_sqrt(__builtin_fma(fl, fl, fl + 0.5));
+    const double gap = y - t;
+    const double m = 1.0 / 16384;
+    if (fr > m && fr < 1.0 - m && (gap > m || gap < -m)) return int32_t(uint32_t(fl) + (gap > 0 ? 1u : 0u));
+  }
+#endif
   uint64_t lo = inv_sqrt_estimate(ux);
   if (lo > 2147483646ull) lo = 2147483646ull;
   while (lo > 0 && !sq_times_le_2_64(lo, ux)) --lo;
@@ -165,6 +189,32 @@ DET_HD int32_t inv_sqrt_acc(int64_t x) {
 // estimate within two of the floor quotient for quotients below 2^51, then
 // the exact remainder; larger quotients use the integer division.
 DET_HD uint64_t div_rte_nonneg_u32(uint64_t v, uint32_t d) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // Branch-free on the GPU: rd = 1/d within 2^-51 (hardware rcp, two Newton
+  // steps), so v rd is within 2^-50 relative of v / d < 2^63 and q0 =
+  // trunc(v rd) within 2^13 + 1 of it; the exact remainder r = v - q0 d has
+  // |r| < 2^46 (an exact double). r rd is within 2^-36 of r / d, whose
+  // fractional part is 0 or at least 1/d > 2^-32, so trunc(r rd) leaves a
+  // remainder in [-d, d] that one step each way brings into [0, d); then
+  // round half to even.
+  const double dd = double(d);
+  double rd = __builtin_amdgcn_rcp(dd);
+  rd = rd * (2.0 - dd * rd);
+  rd = rd * (2.0 - dd * rd);
+  uint64_t q = uint64_t(double(v) * rd);
+  int64_t r = int64_t(v - q * uint64_t(d));
+  const int64_t adj = int64_t(double(r) * rd);
+  q += uint64_t(adj);
+  r -= adj * int64_t(d);
+  const bool neg = r < 0;
+  q -= uint64_t(neg);
+  r += neg ? int64_t(d) : 0;
+  const bool big = r >= int64_t(d);
+  q += uint64_t(big);
+  r -= big ? int64_t(d) : 0;
+  const uint64_t twice2 = uint64_t(r) << 1;
+  return q + uint64_t((twice2 > d) | ((twice2 == d) & (q & 1)));
+#else
   const double qd = double(v) / double(d);
   if (qd >= 2251799813685248.0) return udiv_rte(v, d);  // 2^51
   uint64_t q = uint64_t(qd);
@@ -179,6 +229,7 @@ DET_HD uint64_t div_rte_nonneg_u32(uint64_t v, uint32_t d) {
   }
   const uint64_t twice = uint64_t(r) << 1;
   return (twice > d || (twice == d && (q & 1))) ? q + 1 : q;
+#endif
 }
 
 // rms_norm_scale from a saturated sum of squares (ops.rs:406-425). The

@@ -28,6 +28,10 @@ __global__ void k_inv_sqrt(const int64_t* __restrict__ x, int32_t* __restrict__ 
   const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) out[i] = det::inv_sqrt_acc(x[i]);
 }
+__global__ void k_div(const int64_t* __restrict__ v, const uint32_t* __restrict__ d, int64_t* __restrict__ out, uint64_t n) {
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = int64_t(det::div_rte_nonneg_u32(uint64_t(v[i]), d[i]));
+}
 __global__ void k_rms_scale(const int64_t* __restrict__ ss, const uint32_t* __restrict__ cnt,
                             const int64_t* __restrict__ eps, int32_t* __restrict__ out, uint64_t n) {
   const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -52,13 +56,18 @@ int main(int argc, char** argv) {
   std::vector<int64_t> xs;
   for (int64_t x = 0; x < (1 << 16); ++x) xs.push_back(x);
   for (long i = 0; i < N; ++i) xs.push_back(int64_t(rng() >> 1) >> (rng() % 63));
+  // x next to the floor boundary c^2 x = 2^64 and the rounding boundary
+  // (2 c^2 + 2 c + 1) x = 2^65, for c at every magnitude
   for (long i = 0; i < N / 5; ++i) {
-    const uint64_t c = 2 + rng() % ((1ull << 31) - 3);
-    const long double target = 18446744073709551616.0L;
-    const long double cc = (rng() & 1) ? (long double)c * c : ((long double)c + 0.5L) * ((long double)c + 0.5L);
-    const int64_t x0 = int64_t(target / cc);
-    for (int64_t dx = -2; dx <= 2; ++dx)
-      if (x0 + dx >= 0) xs.push_back(x0 + dx);
+    const uint64_t c = 1 + (rng() >> (33 + rng() % 31)) % ((1ull << 31) - 2);
+    const unsigned __int128 den = (rng() & 1) ? (unsigned __int128)c * c : 2 * (unsigned __int128)c * c + 2 * c + 1;
+    const unsigned __int128 num = (rng() & 1) && den != (unsigned __int128)c * c ? ((unsigned __int128)1 << 65)
+                                                                                : ((unsigned __int128)1 << 64);
+    const unsigned __int128 x0 = num / den;
+    for (int dx = -2; dx <= 2; ++dx) {
+      const unsigned __int128 x = x0 + dx;
+      if (x0 + 2 >= 2 && x < ((unsigned __int128)1 << 63)) xs.push_back(int64_t(x));
+    }
   }
   {
     int64_t* dx = to_dev(xs);
@@ -77,6 +86,48 @@ int main(int argc, char** argv) {
     printf("gpu_inv_sqrt_acc %zu %ld\n", xs.size(), bad);
     failures += bad != 0;
     CK(hipFree(dx));
+    CK(hipFree(dout));
+  }
+  // div_rte_nonneg_u32: random v and d at every magnitude, exact multiples,
+  // halves (ties) and their neighbours
+  {
+    std::vector<int64_t> vs;
+    std::vector<uint32_t> ds;
+    for (long i = 0; i < N; ++i) {
+      uint32_t d = uint32_t(rng() >> (32 + rng() % 32));
+      if (d == 0) d = 1;
+      const int kind = int(rng() % 4);
+      uint64_t v = (rng() >> 1) >> (rng() % 63);
+      if (kind >= 2) {
+        const uint64_t q = v / d;
+        v = q * d + (kind == 3 ? d / 2 : 0) + (rng() % 3) - 1;
+        if (v >> 63) v = (rng() >> 1);
+      }
+      vs.push_back(int64_t(v));
+      ds.push_back(d);
+    }
+    vs.push_back(INT64_MAX); ds.push_back(1);
+    vs.push_back(INT64_MAX); ds.push_back(2);
+    vs.push_back(INT64_MAX); ds.push_back(0xffffffffu);
+    vs.push_back(0); ds.push_back(7);
+    int64_t* dv = to_dev(vs);
+    uint32_t* dd = to_dev(ds);
+    int64_t* dout = nullptr;
+    CK(hipMalloc(&dout, vs.size() * 8));
+    hipLaunchKernelGGL(k_div, dim3(unsigned((vs.size() + 255) / 256)), dim3(256), 0, 0, dv, dd, dout, uint64_t(vs.size()));
+    CK(hipGetLastError());
+    std::vector<int64_t> got(vs.size());
+    CK(hipMemcpy(got.data(), dout, vs.size() * 8, hipMemcpyDeviceToHost));
+    long bad = 0;
+    for (size_t i = 0; i < vs.size(); ++i) {
+      int64_t o;
+      orc_div_acc_by_u32(vs[i], ds[i], &o);
+      if (got[i] != o && ++bad < 5) printf("  div v=%lld d=%u gpu=%lld orc=%lld\n", (long long)vs[i], ds[i], (long long)got[i], (long long)o);
+    }
+    printf("gpu_div_rte_nonneg_u32 %zu %ld\n", vs.size(), bad);
+    failures += bad != 0;
+    CK(hipFree(dv));
+    CK(hipFree(dd));
     CK(hipFree(dout));
   }
   // rms_scale_from_sumsq on sums of squares of random rows (as the norms see them)

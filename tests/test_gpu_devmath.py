@@ -1,9 +1,13 @@
 """The product's integer arithmetic (det_arith.h) as the GPU executes it,
 against the oracle: the device build of inv_sqrt_acc takes its own path (a
-hardware reciprocal-square-root estimate refined by one Newton step, then the
-exact integer correction) and its own 64x64->128-bit products, which the host
-build of the same header never compiles. The driver (tests/devmath/
-gpu_devmath.hip) is built in-tree before the run."""
+hardware reciprocal-square-root estimate refined by Newton steps, decided in
+floating point away from the decision boundaries and by the exact integer
+search near them), the division of the mean its own branch-free reciprocal
+path, and both their own 64x64->128-bit products, which the host build of the
+same header never compiles. The driver (tests/devmath/
+gpu_devmath.hip) is built in-tree before the run. Its inputs include both
+decision boundaries of inv_sqrt_acc (c^2 x = 2^64 and (2 c^2 + 2 c + 1) x =
+2^65) and exact multiples and halves for the division."""
 import pathlib
 import subprocess
 
@@ -24,5 +28,5 @@ def test_device_inv_sqrt_and_rms_scale_match_oracle():
             name, n, bad = line.split()
             rows[name] = (int(n), int(bad))
     assert res.returncode == 0, res.stdout + res.stderr
-    assert set(rows) == {"gpu_inv_sqrt_acc", "gpu_rms_scale"}, res.stdout
+    assert set(rows) == {"gpu_inv_sqrt_acc", "gpu_div_rte_nonneg_u32", "gpu_rms_scale"}, res.stdout
     assert all(bad == 0 and n > 0 for n, bad in rows.values()), res.stdout
