@@ -181,23 +181,38 @@ __device__ __forceinline__ int64_t score_key(int32_t score, uint64_t j) {
 // here and cleared later), y = rmsnorm(x) * gain; the un-gained norm goes to
 // `plain` when given (k_eq_v values).
 // A head row's accumulators and gains as one lane reads them (element
-// lane + 64 k), so that they can be fetched before other loads are issued.
+// lane + 64 k, k < MAXHD / 64), so that they can be fetched before other loads
+// are issued. Every load goes to a clamped address (elements past hd re-read
+// the last one and are masked to zero; without gains the row itself is read
+// and masked), so that no load is predicated and the wait counts before the
+// first use stay exact.
+template <uint32_t MAXHD>
 struct HeadRowIn {
-  int64_t acc[kDecMaxHeadDim / 64];
-  int32_t gain[kDecMaxHeadDim / 64];
+  int64_t acc[MAXHD / 64];
+  int32_t gain[MAXHD / 64];
 };
+template <uint32_t MAXHD>
 __device__ __forceinline__ void load_head_row(const int64_t* __restrict__ src, uint32_t hd,
-                                              const int32_t* __restrict__ gain, uint32_t lane, HeadRowIn& in) {
+                                              const int32_t* __restrict__ gain, uint32_t lane, HeadRowIn<MAXHD>& in) {
+  const int32_t* gp = gain ? gain : reinterpret_cast<const int32_t*>(src);
 #pragma unroll
-  for (int k = 0; k < int(kDecMaxHeadDim / 64); ++k) {
+  for (int k = 0; k < int(MAXHD / 64); ++k) {
     const uint32_t d = lane + 64 * k;
-    in.acc[k] = d < hd ? src[d] : 0;
-    in.gain[k] = (gain && d < hd) ? gain[d] : 0;
+    const uint32_t dc = d < hd ? d : hd - 1;
+    in.acc[k] = src[dc];
+    in.gain[k] = gp[dc];
+  }
+#pragma unroll
+  for (int k = 0; k < int(MAXHD / 64); ++k) {
+    const bool on = lane + 64 * k < hd;
+    in.acc[k] = on ? in.acc[k] : 0;
+    in.gain[k] = (on && gain) ? in.gain[k] : 0;
   }
 }
-__device__ __forceinline__ void norm_head_row(const HeadRowIn& in, uint32_t hd, int64_t eps, bool has_gain,
-                                              int32_t* __restrict__ dst, int32_t* __restrict__ plain, uint32_t lane) {
-  constexpr int kPer = kDecMaxHeadDim / 64;
+template <uint32_t MAXHD, class DP, class PP>
+__device__ __forceinline__ void norm_head_row(const HeadRowIn<MAXHD>& in, uint32_t hd, int64_t eps, bool has_gain,
+                                              DP dst, PP plain, uint32_t lane) {
+  constexpr int kPer = MAXHD / 64;
   int32_t xv[kPer];
   int64_t ss = 0;
 #pragma unroll
@@ -217,16 +232,11 @@ __device__ __forceinline__ void norm_head_row(const HeadRowIn& in, uint32_t hd, 
     }
   }
 }
-__device__ __forceinline__ void norm_head_row(const int64_t* __restrict__ src, uint32_t hd, int64_t eps,
-                                              const int32_t* __restrict__ gain, int32_t* __restrict__ dst,
-                                              int32_t* __restrict__ plain, uint32_t lane) {
-  HeadRowIn in;
-  load_head_row(src, hd, gain, lane, in);
-  norm_head_row(in, hd, eps, gain != nullptr, dst, plain, lane);
-}
 
 // This workgroup's sequence view of a (possibly batched) launch: grid z picks
 // the sequence, its cache and its slices of the per-step buffers.
+// (The cache pointers may come from the per-sequence table, so the kernels
+// access the caches through global_ptr.)
 __device__ __forceinline__ void seq_view(AttnDecArgs& a) {
   const uint32_t seq = blockIdx.z;
   a.st += seq;
@@ -268,26 +278,29 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   // step's own row, and then go unused.
   const uint32_t wv = threadIdx.x >> 6;
   const uint32_t njobs_max = G + (a.own_cache ? (a.has_v ? 2u : 1u) : 0u);
-  HeadRowIn pre;
+  HeadRowIn<MAXHD> pre;
   auto job_src = [&](uint32_t job) {
     return job < G ? a.qkv + (uint64_t(kvh) * G + job) * hd
                    : a.qkv + (uint64_t(a.nh) + (job == G ? 0 : a.nkv) + kvh) * hd;
   };
   auto job_gain = [&](uint32_t job) { return job < G ? a.q_norm : (job == G ? a.k_norm : nullptr); };
-  if (wv < njobs_max) load_head_row(job_src(wv), hd, job_gain(wv), threadIdx.x & 63, pre);
+  const uint32_t pj = wv < njobs_max ? wv : 0;  // (idle waves read job 0's row and drop it)
+  load_head_row(job_src(pj), hd, job_gain(pj), threadIdx.x & 63, pre);
   // cos/sin of this thread's first two rotation slots, also read ahead of the
   // key rows (later slots, for rows x half > 1024, load theirs in the rotation
   // loop)
+  // (unconditional loads, straight into their registers: without rotation
+  // they read the accumulator row instead and go unused)
   const uint32_t half = uint32_t(a.rotary / 2);
-  int32_t tc[2] = {0, 0}, ts[2] = {0, 0};
-  if (half)
+  const int32_t* trig = half ? a.trig : reinterpret_cast<const int32_t*>(a.qkv);
+  const uint32_t hmod = half ? half : 1;
+  int32_t tc[2], ts[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const uint32_t idx = threadIdx.x + 512 * u;
-      const uint32_t i = idx % half;
-      tc[u] = a.trig[2 * i];
-      ts[u] = a.trig[2 * i + 1];
-    }
+  for (int u = 0; u < 2; ++u) {
+    const uint32_t i = (threadIdx.x + 512 * u) % hmod;
+    tc[u] = trig[2 * i];
+    ts[u] = trig[2 * i + 1];
+  }
   const Window win = attn_window(a);
   const uint64_t r0 = uint64_t(blockIdx.y) * P * kAttnScoreRows;
   const uint64_t qoff = uint64_t(kvh) * G * hd;
@@ -309,39 +322,48 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
     valid[p] = j < win.cnt;
     own_row[p] = has_new && j == cur;
     const bool kload = valid[p] && !own_row[p];
-    const int32_t* krow = a.k + (kload ? phys_row(a, win, j) : 0) * kvw + uint64_t(kvh) * hd;
+    // (clamped addresses, masked values: no predicated loads)
+    const global_ptr<const int32_t> krow = to_global(a.k) + (kload ? phys_row(a, win, j) : 0) * kvw + uint64_t(kvh) * hd;
     if (VEC) {
 #pragma unroll
       for (int t = 0; t < kPer / 4; ++t) {
         const uint32_t d = 4 * li + 64 * t;
-        int4 v = make_int4(0, 0, 0, 0);
-        if (kload && d < hd) v = *reinterpret_cast<const int4*>(krow + d);
-        kr[p][4 * t] = v.x, kr[p][4 * t + 1] = v.y, kr[p][4 * t + 2] = v.z, kr[p][4 * t + 3] = v.w;
+        const int4 v = load_int4(krow + (d < hd ? d : hd - 4));
+        const bool on = kload && d < hd;
+        kr[p][4 * t] = on ? v.x : 0, kr[p][4 * t + 1] = on ? v.y : 0;
+        kr[p][4 * t + 2] = on ? v.z : 0, kr[p][4 * t + 3] = on ? v.w : 0;
       }
     } else {
 #pragma unroll
       for (int t = 0; t < kPer; ++t) {
         const uint32_t d = li + 16 * t;
-        kr[p][t] = (kload && d < hd) ? krow[d] : 0;
+        const int32_t v = krow[d < hd ? d : hd - 1];
+        kr[p][t] = (kload && d < hd) ? v : 0;
       }
     }
   }
   // head rows: jobs 0..G-1 are the queries, then the new key (and value) rows
   const uint32_t nkeys = has_new ? (a.has_v ? 2 : 1) : 0;
-  int32_t* kslot = a.k + win.slot * kvw + uint64_t(kvh) * hd;
-  int32_t* vslot = a.v + win.slot * kvw + uint64_t(kvh) * hd;
-  for (uint32_t job = wave; job < G + nkeys; job += 8) {
-    HeadRowIn in;
-    if (job == wave) in = pre;
-    else load_head_row(job_src(job), hd, job_gain(job), lane, in);
+  const global_ptr<int32_t> kslot = to_global(a.k) + win.slot * kvw + uint64_t(kvh) * hd;
+  const global_ptr<int32_t> vslot = to_global(a.v) + win.slot * kvw + uint64_t(kvh) * hd;
+  const global_ptr<int32_t> no_row = nullptr;
+  auto norm_job = [&](uint32_t job, const HeadRowIn<MAXHD>& in) {
     const bool gained = job_gain(job) != nullptr;
     if (job < G) {
-      norm_head_row(in, hd, a.eps, gained, ql + job * hd, nullptr, lane);
+      norm_head_row(in, hd, a.eps, gained, ql + job * hd, no_row, lane);
     } else if (job == G) {
-      norm_head_row(in, hd, a.eps, gained, kn, a.has_v ? nullptr : vslot, lane);
+      norm_head_row(in, hd, a.eps, gained, kn, a.has_v ? no_row : vslot, lane);
     } else {
-      norm_head_row(in, hd, a.eps, gained, vslot, nullptr, lane);
+      norm_head_row(in, hd, a.eps, gained, vslot, no_row, lane);
     }
+  };
+  // the wave's first job straight from the preloaded registers (a copy into a
+  // loop variable would wait for every load in flight, key rows included)
+  if (wave < G + nkeys) norm_job(wave, pre);
+  for (uint32_t job = wave + 8; job < G + nkeys; job += 8) {
+    HeadRowIn<MAXHD> in;
+    load_head_row(job_src(job), hd, job_gain(job), lane, in);
+    norm_job(job, in);
   }
   __syncthreads();
   if (half && win.pos != 0) {
@@ -553,7 +575,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
       for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
         const uint32_t d = dl + 256 * jj;
         const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
-        vp[p][jj][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
+        vp[p][jj][k] = (d < hd && rr < nr) ? to_global(a.v)[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
       }
   for (uint32_t idx = threadIdx.x; idx < G * R; idx += 1024) {
     const uint32_t gg = idx / R, rr = idx % R;
@@ -664,7 +686,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
       for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
         const uint32_t d = dl + 256 * jj;
         const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
-        vp[p][jj][k] = (d < hd && rr < nr) ? a.v[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
+        vp[p][jj][k] = (d < hd && rr < nr) ? to_global(a.v)[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
       }
   // this wave's head and its rows r = wi * 64 + lane + stride * n
   const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;

@@ -1082,8 +1082,8 @@ constexpr uint64_t kMaxAttnRows = 16000;  // LDS: one int32 per window row
 // phys(r) = base + r, wrapped once around a ring of `wrap` rows (base < wrap,
 // r < count <= wrap).
 struct AttnWin {
-  const int32_t* k;
-  const int32_t* v;
+  global_ptr<const int32_t> k;
+  global_ptr<const int32_t> v;
   uint64_t base, wrap, count;
   __device__ uint64_t phys(uint64_t r) const {
     const uint64_t p = base + r;
@@ -1095,7 +1095,7 @@ __device__ inline AttnWin attn_window_of(const AttnArgs& a, uint32_t t) {
   if (a.seqs) {
     // one query per sequence, each over its own cache window
     const AttnSeq sq = a.seqs[t];
-    return {sq.k, sq.v, sq.base, sq.wrap ? sq.wrap : ~0ull, sq.count};
+    return {to_global(sq.k), to_global(sq.v), sq.base, sq.wrap ? sq.wrap : ~0ull, sq.count};
   }
   uint64_t start, count;
   if (a.causal) {
@@ -1109,7 +1109,7 @@ __device__ inline AttnWin attn_window_of(const AttnArgs& a, uint32_t t) {
     count = a.fix_count;
   }
   const uint64_t base = a.ring_cap ? (a.ring_start + start) % a.ring_cap : start;
-  return {a.k, a.v, base, a.ring_cap ? a.ring_cap : ~0ull, count};
+  return {to_global(a.k), to_global(a.v), base, a.ring_cap ? a.ring_cap : ~0ull, count};
 }
 
 __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
@@ -1126,7 +1126,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   int32_t* orow = a.out + uint64_t(t) * a.out_ld + uint64_t(h) * a.hd;
   // 1. scores (wave per row, lanes over head dims)
   for (uint64_t r = wave; r < count; r += kAttnWaves) {
-    const int32_t* krow = win.k + win.phys(r) * a.kv_ld + uint64_t(kvh) * a.hd;
+    const auto krow = win.k + win.phys(r) * a.kv_ld + uint64_t(kvh) * a.hd;
     int64_t acc = 0;
     for (uint32_t d = lane; d < a.hd; d += 64) acc = mac(acc, qrow[d], krow[d]);
     acc = wave_sum_wrap(acc);
@@ -1204,8 +1204,8 @@ __global__ __launch_bounds__(kAttnPThreads) void k_attention_prefill(AttnArgs a)
   const uint64_t count = win.count;
   if (count == 0) return;  // host validation makes every window non-empty
   const uint64_t cstride = attn_row_stride(a);
-  const int32_t* kc = win.k;
-  const int32_t* vc = win.v;
+  const auto kc = win.k;
+  const auto vc = win.v;
   auto phys = [&](uint64_t r) { return win.phys(r); };
   for (uint32_t i = threadIdx.x; i < HB * hd; i += kAttnPThreads)
     ql[i] = a.q[uint64_t(t) * a.q_ld + uint64_t(h0 + i / hd) * hd + i % hd];
@@ -1218,12 +1218,12 @@ __global__ __launch_bounds__(kAttnPThreads) void k_attention_prefill(AttnArgs a)
     for (int u = 0; u < U; ++u) {
       const uint64_t r = r0 + grp + 32 * u;
       const bool on = r < count;
-      const int32_t* krow = kc + (on ? phys(r) : 0) * a.kv_ld + uint64_t(kvh) * hd;
+      const auto krow = kc + (on ? phys(r) : 0) * a.kv_ld + uint64_t(kvh) * hd;
 #pragma unroll
       for (int tt = 0; tt < KPER / 4; ++tt) {
         const uint32_t d = 4 * li + 64 * tt;
         int4 v = make_int4(0, 0, 0, 0);
-        if (on && d < hd) v = *reinterpret_cast<const int4*>(krow + d);
+        if (on && d < hd) v = load_int4(krow + d);
         kr[u][4 * tt] = v.x, kr[u][4 * tt + 1] = v.y, kr[u][4 * tt + 2] = v.z, kr[u][4 * tt + 3] = v.w;
       }
     }

@@ -16,6 +16,26 @@
 
 namespace det {
 
+// Pointers typed as addressing global memory. Pointers read out of memory
+// (per-sequence cache tables) are not known to be global, and accesses
+// through them compile to FLAT instructions, which count against the
+// LDS/scalar wait counter as well: a wait for an LDS result then also waits
+// for every FLAT load in flight (an HBM round trip). Accesses through a
+// global_ptr compile to global loads and stores.
+template <class T>
+using global_ptr = __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ global_ptr<T> to_global(T* p) {
+  return (global_ptr<T>)p;
+}
+// A 16-byte global load of four int32 (HIP's int4 class cannot be assigned
+// from an address-space-qualified object, so the load goes through a vector).
+__device__ __forceinline__ int4 load_int4(global_ptr<const int32_t> p) {
+  typedef int v4 __attribute__((ext_vector_type(4)));
+  const v4 v = *(global_ptr<const v4>)p;
+  return make_int4(v.x, v.y, v.z, v.w);
+}
+
 template <int CTRL>
 __device__ __forceinline__ uint64_t dpp_move64(uint64_t v) {
   const uint32_t lo = uint32_t(__builtin_amdgcn_mov_dpp(int(uint32_t(v)), CTRL, 0xf, 0xf, false));
