@@ -563,10 +563,20 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
   if (r0 >= win.cnt) return;
   const uint64_t nr = win.cnt - r0 < R ? win.cnt - r0 : R;
   const uint64_t kvw = uint64_t(a.nkv) * hd;
+  // weight of row (gg, rr) = idx of the G x R block, R <= 1024 / G for P <= 8:
+  // this thread's statistics and score are read before the value rows (loads
+  // complete in issue order and the value rows are needed last), at clamped
+  // addresses so that no load is predicated
+  const uint32_t idx0 = threadIdx.x, gg0 = idx0 / R, rr0 = idx0 % R;
+  const uint64_t head0 = uint64_t(kvh) * G + (idx0 < G * R ? gg0 : 0);
+  const AttnStat st0 = a.stats[head0];
+  const int32_t sc0 = a.scores[head0 * a.max_rows + r0 + (rr0 < nr ? rr0 : nr - 1)];
+  asm volatile("" ::: "memory");
   // value rows: slice sl takes rows 8 sl .. 8 sl + 7 of every chunk, dims dl and dl + 256
   const uint32_t sl = threadIdx.x >> 8, dl = threadIdx.x & 255;
   constexpr int JJ = MAXHD > 256 ? 2 : 1;  // dims dl (and dl + 256)
   int32_t vp[P][JJ][kAttnWsumRows / 4];
+  const global_ptr<const int32_t> vcache = to_global(a.v) + uint64_t(kvh) * hd;
 #pragma unroll
   for (int p = 0; p < P; ++p)
 #pragma unroll
@@ -575,21 +585,30 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
       for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
         const uint32_t d = dl + 256 * jj;
         const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
-        vp[p][jj][k] = (d < hd && rr < nr) ? to_global(a.v)[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
+        vp[p][jj][k] = vcache[phys_row(a, win, r0 + (rr < nr ? rr : nr - 1)) * kvw + (d < hd ? d : hd - 1)];
       }
-  for (uint32_t idx = threadIdx.x; idx < G * R; idx += 1024) {
+  asm volatile("" ::: "memory");
+  auto weight = [&](const AttnStat& st, int32_t score, uint64_t r) {
+    const int64_t e = softmax_exp(score, st.mx);
+    int32_t w = st.rec ? softmax_weight_r(e, st.sum, st.rec) : softmax_weight(e, st.sum);
+    if (r == st.mi) w = add_sat(w, st.resid);
+    return w;
+  };
+  if (idx0 < G * R) wl[gg0][rr0] = rr0 < nr ? weight(st0, sc0, r0 + rr0) : 0;
+  for (uint32_t idx = threadIdx.x + 1024; idx < G * R; idx += 1024) {
     const uint32_t gg = idx / R, rr = idx % R;
     const uint64_t head = uint64_t(kvh) * G + gg;
-    int32_t w = 0;
-    if (rr < nr) {
-      const AttnStat st = a.stats[head];
-      const uint64_t r = r0 + rr;
-      const int64_t e = softmax_exp(a.scores[head * a.max_rows + r], st.mx);
-      w = st.rec ? softmax_weight_r(e, st.sum, st.rec) : softmax_weight(e, st.sum);
-      if (r == st.mi) w = add_sat(w, st.resid);
-    }
-    wl[gg][rr] = w;
+    wl[gg][rr] = rr < nr ? weight(a.stats[head], a.scores[head * a.max_rows + r0 + rr], r0 + rr) : 0;
   }
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int jj = 0; jj < JJ; ++jj)
+#pragma unroll
+      for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+        const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
+        if (!(dl + 256 * jj < hd && rr < nr)) vp[p][jj][k] = 0;
+      }
   __syncthreads();
   // weighted sums: 4 row slices per dim, combined in LDS for up to 1024 / dstr
   // heads per pass, one atomic per (head, dim)
@@ -674,10 +693,29 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t nr = win.cnt - r0 < R ? win.cnt - r0 : R;
   const uint64_t kvw = uint64_t(a.nkv) * hd;
+  // this wave's head and its rows r = wi * 64 + lane + stride * n
+  const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;
+  const bool active = g < G;
+  const uint64_t stride = 64 * uint64_t(wph);
+  const int32_t* scg = a.scores + (uint64_t(kvh) * G + (active ? g : 0)) * a.max_rows;
+  const bool lds = a.scores_in_lds;  // the window's scores (then exp terms) kept in LDS
+  int32_t* scl = sl_dyn + uint64_t(active ? g : 0) * a.lds_stride;  // (written only when lds)
+  // The first NS of this thread's scores are read before the value rows (loads
+  // complete in issue order, and the value rows are needed last); clamped
+  // addresses, so that no load is predicated.
+  constexpr int NS = 4;
+  int32_t sv[NS];
+#pragma unroll
+  for (int n = 0; n < NS; ++n) {
+    const uint64_t r = wi * 64 + lane + stride * n;
+    sv[n] = scg[r < win.cnt ? r : win.cnt - 1];
+  }
+  asm volatile("" ::: "memory");  // (keeps these loads ahead of the value rows)
   // value rows: slice sl takes rows 8 sl .. 8 sl + 7 of every chunk, dims dl and dl + 256
   const uint32_t sl = threadIdx.x >> 8, dl = threadIdx.x & 255;
   constexpr int JJ = MAXHD > 256 ? 2 : 1;  // dims dl (and dl + 256)
   int32_t vp[P][JJ][kAttnWsumRows / 4];
+  const global_ptr<const int32_t> vcache = to_global(a.v) + uint64_t(kvh) * hd;
 #pragma unroll
   for (int p = 0; p < P; ++p)
 #pragma unroll
@@ -686,24 +724,39 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
       for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
         const uint32_t d = dl + 256 * jj;
         const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
-        vp[p][jj][k] = (d < hd && rr < nr) ? to_global(a.v)[phys_row(a, win, r0 + rr) * kvw + uint64_t(kvh) * hd + d] : 0;
+        vp[p][jj][k] = vcache[phys_row(a, win, r0 + (rr < nr ? rr : nr - 1)) * kvw + (d < hd ? d : hd - 1)];
       }
-  // this wave's head and its rows r = wi * 64 + lane + stride * n
-  const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;
-  const bool active = g < G;
-  const uint64_t stride = 64 * uint64_t(wph);
-  const int32_t* scg = a.scores + (uint64_t(kvh) * G + (active ? g : 0)) * a.max_rows;
-  int32_t* scl = a.scores_in_lds ? sl_dyn + uint64_t(active ? g : 0) * a.lds_stride : nullptr;
+  asm volatile("" ::: "memory");
+  // (masked once the loads are all issued)
+  auto mask_values = [&]() {
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int jj = 0; jj < JJ; ++jj)
+#pragma unroll
+        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+          const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
+          if (!(dl + 256 * jj < hd && rr < nr)) vp[p][jj][k] = 0;
+        }
+  };
   // argmax (and the LDS copy of this thread's scores)
   int64_t best = INT64_MIN;
-  if (active)
-    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
+  if (active) {
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      const uint64_t r = wi * 64 + lane + stride * n;
+      const int64_t k = r < win.cnt ? score_key(sv[n], r) : INT64_MIN;
+      best = k > best ? k : best;
+      if (lds && r < win.cnt) scl[r] = sv[n];
+    }
+    for (uint64_t r = wi * 64 + lane + stride * NS; r < win.cnt; r += stride) {
       const int32_t v = scg[r];
-      if (scl) scl[r] = v;
+      if (lds) scl[r] = v;
       const int64_t k = score_key(v, r);
       best = k > best ? k : best;
     }
-  if (!scl) scl = const_cast<int32_t*>(scg);
+  }
+  mask_values();
   best = wmax(best);
   if (lane == 0) red[wave] = best;
   __syncthreads();
@@ -722,14 +775,23 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   // With the scores in LDS each exp term replaces its score there for the
   // residual pass (2^32, the argmax row's term, is stored as 0xffffffff: every
   // other term is at most 2^32 - 2^16).
-  const bool lds = a.scores_in_lds;
-  if (active)
+  // (the scores in LDS and in global memory take separate loops, so that
+  // neither compiles to FLAT accesses)
+  if (active && lds) {
+    int32_t* scs = sl_dyn + uint64_t(g) * a.lds_stride;
     for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
-      const int64_t e = softmax_exp(scl[r], mx);
+      const int64_t e = softmax_exp(scs[r], mx);
       s += e;
       if (r >= r0 && r < r0 + nr) el[g][r - r0] = e;
-      if (lds) scl[r] = int32_t(e == kOneAcc ? 0xffffffffu : uint32_t(e));
+      scs[r] = int32_t(e == kOneAcc ? 0xffffffffu : uint32_t(e));
     }
+  } else if (active) {
+    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
+      const int64_t e = softmax_exp(scg[r], mx);
+      s += e;
+      if (r >= r0 && r < r0 + nr) el[g][r - r0] = e;
+    }
+  }
   s = wsum_wrap(s);
   if (lane == 0) red[wave] = s;
   __syncthreads();
@@ -753,15 +815,18 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   if (owner) {
     const int64_t S = hsum[g];
     const uint64_t M = hrec[g];
-    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
-      int64_t e;
-      if (lds) {
-        const uint32_t u = uint32_t(scl[r]);
-        e = u == 0xffffffffu ? kOneAcc : int64_t(u);
-      } else {
-        e = softmax_exp(scl[r], mx);
+    if (lds) {
+      const int32_t* scs = sl_dyn + uint64_t(g) * a.lds_stride;
+      for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
+        const uint32_t u = uint32_t(scs[r]);
+        const int64_t e = u == 0xffffffffu ? kOneAcc : int64_t(u);
+        ws += M ? softmax_weight_r(e, S, M) : softmax_weight(e, S);
       }
-      ws += M ? softmax_weight_r(e, S, M) : softmax_weight(e, S);
+    } else {
+      for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
+        const int64_t e = softmax_exp(scg[r], mx);
+        ws += M ? softmax_weight_r(e, S, M) : softmax_weight(e, S);
+      }
     }
   }
   ws = wsum_wrap(ws);
