@@ -55,8 +55,11 @@ uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad);
 // matrices with the same input width.
 void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_act, uint64_t kpad, int8_t* a_tiled,
                        hipStream_t s);
+// gelu_pairs: W holds interleaved gate/up tiles (rows 0-7 gate f..f+7, rows
+// 8-15 up f..f+7 of every 16-row tile); out[t * ld_out + f] =
+// mul_sat(gelu(gate_f), up_f) for f < W.rows / 2.
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                       const int8_t* a_tiled, hipStream_t s);
+                       const int8_t* a_tiled, hipStream_t s, bool gelu_pairs = false);
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
                  int64_t* acc_out, int8_t* a_tiled, hipStream_t s);
 

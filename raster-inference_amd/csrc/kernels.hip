@@ -841,7 +841,7 @@ __global__ void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, u
 // and the 128-bit operand reads do not conflict on LDS banks. The MFMAs of a
 // step run as two passes over the wave's tile pairs (first 64 columns, then
 // the second 64), so consecutive MFMAs never share an accumulator.
-template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF>
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool GELU>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
                                                            const int32_t* __restrict__ scale,
                                                            const int32_t* __restrict__ rowsum, uint64_t n_rows,
@@ -952,9 +952,19 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     const uint64_t token = (at0 + wm * FA + ti) * 4 + g;
 #pragma unroll
     for (int tj = 0; tj < FB; ++tj) {
-      const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
-      if (token >= m_tokens || row >= n_rows) continue;
+      const uint64_t tile = bt0 + wn * FB + tj, row = tile * 16 + i;
       const int64_t p[4] = {acc[ti][tj][0], acc[ti][tj][1], acc[ti][tj][2], acc[ti][tj][3]};
+      if (GELU) {
+        // interleaved gate/up tiles (rows 0-7 gate f..f+7, rows 8-15 up):
+        // out[token][8 tile + i] = mul_sat(gelu(gate), up); every lane takes
+        // part in the shuffle (row >= n_rows only past the last whole tile)
+        const bool on = token < m_tokens && row < n_rows;
+        const int32_t r = on ? requant(limb_combine(p, rowsum[row], scale[row])) : 0;
+        const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
+        if (on && i < 8) out[token * ld_out + tile * 8 + i] = mul_sat(gelu_act(r), up);
+        continue;
+      }
+      if (token >= m_tokens || row >= n_rows) continue;
       const int64_t v = limb_combine(p, rowsum[row], scale[row]);
       if (acc_out) acc_out[token * ld_out + row] = v;
       else out[token * ld_out + row] = requant(v);
@@ -1654,17 +1664,17 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
 
 uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64 * 4 * kpad; }
 
-template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF>
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool GELU = false>
 static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
                                   const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s) {
   constexpr uint32_t lds = uint32_t(NBUF) * (TA + TB) * 2048u;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, GELU>), hipFuncAttributeMaxDynamicSharedMemorySize,
       int(lds));
   (void)attr;
   const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
   const uint64_t nblocks = ((W.rows + 15) / 16 + TB - 1) / TB;
-  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN), lds, s,
+  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, GELU>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN), lds, s,
                      a_tiled, W.q, W.scale, W.rowsum, W.rows, W.kpad, m, a_tiles, uint32_t(mblocks), out, ld_out,
                      acc_out);
 }
@@ -1680,9 +1690,12 @@ void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_a
 }
 
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                       const int8_t* a_tiled, hipStream_t s) {
+                       const int8_t* a_tiled, hipStream_t s, bool gelu_pairs) {
   if (W.rows == 0 || m == 0) return;
   const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
+  // GELU pairs take the 128 x 128 blocks only (the GELU epilogue does not fit
+  // the 256 x 256 block's registers)
+  if (gelu_pairs) return launch_gemm_lds_shape<8, 8, 2, 2, 8, 2, true>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   // 64 tokens x 256 rows on 8 waves (one block per CU) when its blocks fill
   // whole rounds of the device; otherwise 32 tokens x 128 rows on 4 waves
   // (two blocks per CU), whose finer grid leaves a smaller last round
