@@ -968,7 +968,23 @@ void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const
   det_ctx* ctx = s->m->ctx;
   hipStream_t st = ctx->stream;
   const uint64_t qw = L.num_heads * L.head_dim, kw = L.num_kv_heads * L.head_dim;
-  if (L.v) {
+  // with the fused [q; k; v] matrix of the decode step, one GEMM writes the
+  // three row buffers (its rows split at whole 16-row tiles)
+  const det_model* m = s->m;
+  const size_t li = size_t(&L - m->layers.data());
+  const det::DevMatrix* QKV = (m->fused_ok && li < m->fused.size()) ? &m->fused[li].qkv : nullptr;
+  if (L.v && QKV && M >= det_ctx::kGemmMinRows && QKV->storage == det::kInt8 && QKV->rows == qw + 2 * kw &&
+      L.q->rows == qw && L.k->rows == kw && L.v->rows == kw && qw % 16 == 0 && kw % 16 == 0) {
+    ctx->ensure_gemm_a(det::gemm_act_bytes(M, QKV->kpad));
+    det::launch_gemm_limbs(s->normed, M, QKV->cols, L.q->cols, QKV->kpad, ctx->gemm_a, st);
+    det::RowSplit sp;
+    sp.out1 = s->kb;
+    sp.out2 = s->vb;
+    sp.ld1 = sp.ld2 = kw;
+    sp.r1 = qw;
+    sp.r2 = qw + kw;
+    det::launch_gemm_tiled(*QKV, M, s->qb, qw, nullptr, ctx->gemm_a, st, false, &sp);
+  } else if (L.v) {
     ctx->linear_group({{L.q, s->qb}, {L.k, s->kb}, {L.v, s->vb}}, s->normed, M, L.q->cols);
   } else if (L.k_eq_v) {
     ctx->linear_group({{L.q, s->qb}, {L.k, s->kb}}, s->normed, M, L.q->cols);

@@ -58,8 +58,17 @@ void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_a
 // gelu_pairs: W holds interleaved gate/up tiles (rows 0-7 gate f..f+7, rows
 // 8-15 up f..f+7 of every 16-row tile); out[t * ld_out + f] =
 // mul_sat(gelu(gate_f), up_f) for f < W.rows / 2.
+// split: the rows of W go to three outputs (rows [0, r1) to out with stride
+// ld_out, [r1, r2) to out1, [r2, rows) to out2, each requantized), e.g. the
+// fused [q; k; v] projection into the q, k and v row buffers.
+struct RowSplit {
+  int32_t* out1 = nullptr;
+  int32_t* out2 = nullptr;
+  uint64_t ld1 = 0, ld2 = 0, r1 = 0, r2 = 0;
+};
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                       const int8_t* a_tiled, hipStream_t s, bool gelu_pairs = false);
+                       const int8_t* a_tiled, hipStream_t s, bool gelu_pairs = false,
+                       const RowSplit* split = nullptr);
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
                  int64_t* acc_out, int8_t* a_tiled, hipStream_t s);
 

@@ -841,13 +841,14 @@ __global__ void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, u
 // and the 128-bit operand reads do not conflict on LDS banks. The MFMAs of a
 // step run as two passes over the wave's tile pairs (first 64 columns, then
 // the second 64), so consecutive MFMAs never share an accumulator.
-template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool GELU>
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool GELU, bool SPLIT>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
                                                            const int32_t* __restrict__ scale,
                                                            const int32_t* __restrict__ rowsum, uint64_t n_rows,
                                                            uint64_t kpad, uint64_t m_tokens, uint64_t a_tiles,
                                                            uint32_t mblocks, int32_t* __restrict__ out,
-                                                           uint64_t ld_out, int64_t* __restrict__ acc_out) {
+                                                           uint64_t ld_out, int64_t* __restrict__ acc_out,
+                                                           RowSplit split) {
   constexpr int NW = WM * WN;                  // waves
   constexpr int TS = TA + TB;                  // tile-steps per K step
   constexpr int LPW = 2 * TS / NW;             // 1 KB wave copies per wave per K step
@@ -966,8 +967,18 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
       }
       if (token >= m_tokens || row >= n_rows) continue;
       const int64_t v = limb_combine(p, rowsum[row], scale[row]);
-      if (acc_out) acc_out[token * ld_out + row] = v;
-      else out[token * ld_out + row] = requant(v);
+      if (SPLIT) {
+        // rows [0, r1) to out, [r1, r2) to out1, [r2, n_rows) to out2
+        int32_t* o = out;
+        uint64_t ld = ld_out, rr = row;
+        if (row >= split.r2) o = split.out2, ld = split.ld2, rr = row - split.r2;
+        else if (row >= split.r1) o = split.out1, ld = split.ld1, rr = row - split.r1;
+        o[token * ld + rr] = requant(v);
+      } else if (acc_out) {
+        acc_out[token * ld_out + row] = v;
+      } else {
+        out[token * ld_out + row] = requant(v);
+      }
     }
   }
 }
@@ -1664,19 +1675,19 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
 
 uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64 * 4 * kpad; }
 
-template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool GELU = false>
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool GELU = false, bool SPLIT = false>
 static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                                  const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s) {
+                                  const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s, RowSplit split = {}) {
   constexpr uint32_t lds = uint32_t(NBUF) * (TA + TB) * 2048u;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, GELU>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, GELU, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
       int(lds));
   (void)attr;
   const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
   const uint64_t nblocks = ((W.rows + 15) / 16 + TB - 1) / TB;
-  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, GELU>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN), lds, s,
+  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, GELU, SPLIT>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN), lds, s,
                      a_tiled, W.q, W.scale, W.rowsum, W.rows, W.kpad, m, a_tiles, uint32_t(mblocks), out, ld_out,
-                     acc_out);
+                     acc_out, split);
 }
 
 void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_act, uint64_t kpad, int8_t* a_tiled,
@@ -1690,9 +1701,12 @@ void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_a
 }
 
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                       const int8_t* a_tiled, hipStream_t s, bool gelu_pairs) {
+                       const int8_t* a_tiled, hipStream_t s, bool gelu_pairs, const RowSplit* split) {
   if (W.rows == 0 || m == 0) return;
   const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
+  // row-split outputs likewise (128 x 128 blocks only)
+  if (split)
+    return launch_gemm_lds_shape<8, 8, 2, 2, 8, 2, false, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
   // GELU pairs take the 128 x 128 blocks only (the GELU epilogue does not fit
   // the 256 x 256 block's registers)
   if (gelu_pairs) return launch_gemm_lds_shape<8, 8, 2, 2, 8, 2, true>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
