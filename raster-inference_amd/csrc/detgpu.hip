@@ -983,7 +983,7 @@ void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const
     sp.ld1 = sp.ld2 = kw;
     sp.r1 = qw;
     sp.r2 = qw + kw;
-    det::launch_gemm_tiled(*QKV, M, s->qb, qw, nullptr, ctx->gemm_a, st, false, &sp);
+    det::launch_gemm_tiled(*QKV, M, s->qb, qw, nullptr, ctx->gemm_a, st, &sp);
   } else if (L.v) {
     ctx->linear_group({{L.q, s->qb}, {L.k, s->kb}, {L.v, s->vb}}, s->normed, M, L.q->cols);
   } else if (L.k_eq_v) {
@@ -1012,23 +1012,10 @@ void post_attention(det_session* s, const GLayer& L, uint64_t M, const int32_t* 
   hipStream_t st = ctx->stream;
   const uint64_t H = L.hidden;
   linear(ctx, *L.o, s->attn, M, s->x2);
-  det::launch_rmsnorm_add(s->x, s->x2, s->x, M, H, H, L.post_attn_ln, L.eps, st);  // x = add_sat(norm(o), x)
-  det::launch_rmsnorm_to(s->normed, s->x, M, H, H, L.pre_ff_ln, L.eps, st);
-  // with the interleaved gate/up matrix of the fused decode step, the prefill
-  // GEMM computes mul_sat(gelu(gate), up) in its epilogue
-  const det_model* m = s->m;
-  const size_t li = size_t(&L - m->layers.data());
-  const bool pairs = m->fused_ok && li < m->fused.size() && M >= det_ctx::kGemmMinRows &&
-                     m->fused[li].gateup.storage == det::kInt8 && m->fused[li].gateup.rows == 2 * L.gate->rows;
-  if (pairs) {
-    const det::DevMatrix& GU = m->fused[li].gateup;
-    ctx->ensure_gemm_a(det::gemm_act_bytes(M, GU.kpad));
-    det::launch_gemm_limbs(s->normed, M, GU.cols, H, GU.kpad, ctx->gemm_a, st);
-    det::launch_gemm_tiled(GU, M, s->gate, L.gate->rows, nullptr, ctx->gemm_a, st, true);
-  } else {
-    ctx->linear_group({{L.gate, s->gate}, {L.up, s->up}}, s->normed, M, H);
-    det::launch_gelu_mul(s->gate, s->up, M * L.gate->rows, st);
-  }
+  // x = add_sat(norm(o), x); normed = norm(x) (pre-FF)
+  det::launch_rmsnorm_add_norm(s->x, s->x2, s->normed, M, H, H, L.post_attn_ln, L.pre_ff_ln, L.eps, st);
+  ctx->linear_group({{L.gate, s->gate}, {L.up, s->up}}, s->normed, M, H);
+  det::launch_gelu_mul(s->gate, s->up, M * L.gate->rows, st);
   linear(ctx, *L.down, s->gate, M, s->x2);
   det::launch_rmsnorm_add(s->x, s->x2, s->x, M, H, H, L.post_ff_ln, L.eps, st);
   if (L.has_ple && ple_in) {

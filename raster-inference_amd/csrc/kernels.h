@@ -55,9 +55,6 @@ uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad);
 // matrices with the same input width.
 void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_act, uint64_t kpad, int8_t* a_tiled,
                        hipStream_t s);
-// gelu_pairs: W holds interleaved gate/up tiles (rows 0-7 gate f..f+7, rows
-// 8-15 up f..f+7 of every 16-row tile); out[t * ld_out + f] =
-// mul_sat(gelu(gate_f), up_f) for f < W.rows / 2.
 // split: the rows of W go to three outputs (rows [0, r1) to out with stride
 // ld_out, [r1, r2) to out1, [r2, rows) to out2, each requantized), e.g. the
 // fused [q; k; v] projection into the q, k and v row buffers.
@@ -67,8 +64,7 @@ struct RowSplit {
   uint64_t ld1 = 0, ld2 = 0, r1 = 0, r2 = 0;
 };
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                       const int8_t* a_tiled, hipStream_t s, bool gelu_pairs = false,
-                       const RowSplit* split = nullptr);
+                       const int8_t* a_tiled, hipStream_t s, const RowSplit* split = nullptr);
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
                  int64_t* acc_out, int8_t* a_tiled, hipStream_t s);
 
@@ -101,6 +97,10 @@ void launch_rmsnorm(int32_t* x, uint64_t rows, uint64_t cols, uint64_t ld, const
 void launch_rmsnorm_add(int32_t* dst, const int32_t* src, const int32_t* res, uint64_t rows, uint64_t cols,
                         uint64_t ld, const int32_t* w, int64_t eps, hipStream_t s);
 // dst = rmsnorm(src) row by row (dst may equal src).
+// x = add_sat(rmsnorm(src) * w1, x); normed = rmsnorm(x) * w2 (one pass for
+// rows of 2049-4096 columns, else the two launches above).
+void launch_rmsnorm_add_norm(int32_t* x, const int32_t* src, int32_t* normed, uint64_t rows, uint64_t cols,
+                             uint64_t ld, const int32_t* w1, const int32_t* w2, int64_t eps, hipStream_t s);
 void launch_rmsnorm_to(int32_t* dst, const int32_t* src, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
                        int64_t eps, hipStream_t s);
 void launch_rope(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t head_dim,

@@ -841,7 +841,7 @@ __global__ void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, u
 // and the 128-bit operand reads do not conflict on LDS banks. The MFMAs of a
 // step run as two passes over the wave's tile pairs (first 64 columns, then
 // the second 64), so consecutive MFMAs never share an accumulator.
-template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool GELU, bool SPLIT>
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
                                                            const int32_t* __restrict__ scale,
                                                            const int32_t* __restrict__ rowsum, uint64_t n_rows,
@@ -953,19 +953,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     const uint64_t token = (at0 + wm * FA + ti) * 4 + g;
 #pragma unroll
     for (int tj = 0; tj < FB; ++tj) {
-      const uint64_t tile = bt0 + wn * FB + tj, row = tile * 16 + i;
-      const int64_t p[4] = {acc[ti][tj][0], acc[ti][tj][1], acc[ti][tj][2], acc[ti][tj][3]};
-      if (GELU) {
-        // interleaved gate/up tiles (rows 0-7 gate f..f+7, rows 8-15 up):
-        // out[token][8 tile + i] = mul_sat(gelu(gate), up); every lane takes
-        // part in the shuffle (row >= n_rows only past the last whole tile)
-        const bool on = token < m_tokens && row < n_rows;
-        const int32_t r = on ? requant(limb_combine(p, rowsum[row], scale[row])) : 0;
-        const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
-        if (on && i < 8) out[token * ld_out + tile * 8 + i] = mul_sat(gelu_act(r), up);
-        continue;
-      }
+      const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
       if (token >= m_tokens || row >= n_rows) continue;
+      const int64_t p[4] = {acc[ti][tj][0], acc[ti][tj][1], acc[ti][tj][2], acc[ti][tj][3]};
       const int64_t v = limb_combine(p, rowsum[row], scale[row]);
       if (SPLIT) {
         // rows [0, r1) to out, [r1, r2) to out1, [r2, n_rows) to out2
@@ -1065,6 +1055,59 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_wide(const int32_t* src, int32_t
       const int32_t y = mul_sat(v[e], scale);
       const int32_t z = w ? mul_sat(y, g[e]) : y;
       yr[c] = res ? add_sat(z, res[row * ld + c]) : z;
+    }
+  }
+}
+
+// The residual add after a sub-block and the next input norm in one pass
+// over a wide row (the two k_rmsnorm_wide launches it replaces, in order):
+// x = add_sat(rmsnorm(src) * w1, x), then normed = rmsnorm(x) * w2 (w1, w2
+// optional). One workgroup of NT threads per row, as k_rmsnorm_wide.
+template <int NT, int EPT>
+__global__ __launch_bounds__(NT) void k_rmsnorm_add_norm(const int32_t* __restrict__ src, int32_t* __restrict__ x,
+                                                         int32_t* __restrict__ normed, uint64_t cols, uint64_t ld,
+                                                         const int32_t* __restrict__ w1,
+                                                         const int32_t* __restrict__ w2, int64_t eps) {
+  __shared__ int64_t red[2][NT / 64];
+  const uint64_t row = blockIdx.x;
+  int32_t v[EPT], xv[EPT], g1[EPT], g2[EPT];
+  int64_t ss = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    const bool in = c < cols;
+    v[e] = in ? src[row * ld + c] : 0;
+    xv[e] = in ? x[row * ld + c] : 0;
+    g1[e] = (w1 && in) ? w1[c] : 0;
+    g2[e] = (w2 && in) ? w2[c] : 0;
+    ss = add_sat64(ss, sq_term(v[e]));
+  }
+  auto block_scale = [&](int k, int64_t part) {
+    part = wave_sum_sat(part);
+    if ((threadIdx.x & 63) == 0) red[k][threadIdx.x >> 6] = part;
+    __syncthreads();
+    int64_t tot = 0;
+#pragma unroll
+    for (int j = 0; j < NT / 64; ++j) tot = add_sat64(tot, red[k][j]);
+    return rms_scale_from_sumsq(tot, uint32_t(cols), eps);
+  };
+  const int32_t s1 = block_scale(0, ss);
+  ss = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    const int32_t y = mul_sat(v[e], s1);
+    xv[e] = c < cols ? add_sat(w1 ? mul_sat(y, g1[e]) : y, xv[e]) : 0;
+    if (c < cols) x[row * ld + c] = xv[e];
+    ss = add_sat64(ss, sq_term(xv[e]));
+  }
+  const int32_t s2 = block_scale(1, ss);
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+    if (c < cols) {
+      const int32_t y = mul_sat(xv[e], s2);
+      normed[row * ld + c] = w2 ? mul_sat(y, g2[e]) : y;
     }
   }
 }
@@ -1675,17 +1718,17 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
 
 uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64 * 4 * kpad; }
 
-template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool GELU = false, bool SPLIT = false>
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT = false>
 static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
                                   const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s, RowSplit split = {}) {
   constexpr uint32_t lds = uint32_t(NBUF) * (TA + TB) * 2048u;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, GELU, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
       int(lds));
   (void)attr;
   const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
   const uint64_t nblocks = ((W.rows + 15) / 16 + TB - 1) / TB;
-  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, GELU, SPLIT>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN), lds, s,
+  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN), lds, s,
                      a_tiled, W.q, W.scale, W.rowsum, W.rows, W.kpad, m, a_tiles, uint32_t(mblocks), out, ld_out,
                      acc_out, split);
 }
@@ -1701,15 +1744,13 @@ void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_a
 }
 
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                       const int8_t* a_tiled, hipStream_t s, bool gelu_pairs, const RowSplit* split) {
+                       const int8_t* a_tiled, hipStream_t s, const RowSplit* split) {
   if (W.rows == 0 || m == 0) return;
   const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
-  // row-split outputs likewise (128 x 128 blocks only)
+  // row-split outputs take the 128 x 128 blocks only (their epilogue is kept
+  // out of the 256 x 256 block's registers)
   if (split)
-    return launch_gemm_lds_shape<8, 8, 2, 2, 8, 2, false, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
-  // GELU pairs take the 128 x 128 blocks only (the GELU epilogue does not fit
-  // the 256 x 256 block's registers)
-  if (gelu_pairs) return launch_gemm_lds_shape<8, 8, 2, 2, 8, 2, true>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
+    return launch_gemm_lds_shape<8, 8, 2, 2, 8, 2, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
   // 64 tokens x 256 rows on 8 waves (one block per CU) when its blocks fill
   // whole rounds of the device; otherwise 32 tokens x 128 rows on 4 waves
   // (two blocks per CU), whose finer grid leaves a smaller last round
@@ -1773,6 +1814,18 @@ void launch_rmsnorm_add(int32_t* dst, const int32_t* src, const int32_t* res, ui
     hipLaunchKernelGGL((k_rmsnorm_wide<1024, 16>), g, dim3(1024), 0, s, src, dst, cols, ld, w, eps, res);
   else
     hipLaunchKernelGGL(k_rmsnorm, dim3(blocks_for(rows, 4)), dim3(256), 0, s, src, dst, res, rows, cols, ld, w, eps);
+}
+
+void launch_rmsnorm_add_norm(int32_t* x, const int32_t* src, int32_t* normed, uint64_t rows, uint64_t cols,
+                             uint64_t ld, const int32_t* w1, const int32_t* w2, int64_t eps, hipStream_t s) {
+  if (rows == 0) return;
+  if (cols > 2048 && cols <= 4096) {
+    hipLaunchKernelGGL((k_rmsnorm_add_norm<256, 16>), dim3(unsigned(rows)), dim3(256), 0, s, src, x, normed, cols, ld,
+                       w1, w2, eps);
+  } else {
+    launch_rmsnorm_add(x, src, x, rows, cols, ld, w1, eps, s);
+    launch_rmsnorm_to(normed, x, rows, cols, ld, w2, eps, s);
+  }
 }
 
 void launch_rmsnorm_to(int32_t* dst, const int32_t* src, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
