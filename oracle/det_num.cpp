@@ -246,6 +246,11 @@ int64_t nth_root_acc(int64_t value, uint32_t degree) {
   if (degree == 0) contract_violation("nth_root_acc requires a positive degree");
   if (value <= 0) contract_violation("nth_root_acc requires a positive input");
   if (degree == 1 || value == kOneAcc) return value;
+  // ops.rs:578 evaluates `high_bits - low_bits + 1`, which overflows i64 on the
+  // first step when value == i64::MAX: the reference panics there ("attempt to
+  // add with overflow") in builds with overflow checks and, without them,
+  // wraps into a bisection that never terminates. The oracle reports the panic.
+  if (value == INT64_MAX) contract_violation("nth_root_acc: attempt to add with overflow (value i64::MAX)");
   int64_t low = 0;
   int64_t high = value > kOneAcc ? value : kOneAcc;
   while (low < high) {

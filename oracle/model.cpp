@@ -82,14 +82,28 @@ static void det_linear(const Matrix& W, const int32_t* act, size_t act_len, int3
   else gemv_dispatch(W.w32.data(), W.rows, W.cols, act, out, g_threads);
 }
 
-// det_kernels.rs:180-203 det_linear_slab: each token row is an independent GEMV.
+// det_kernels.rs:180-203 det_linear_slab: each token row is an independent
+// serial GEMV (det_linear_into); with a thread pool the token rows are spread
+// over the threads (par_chunks_mut over output rows), never the matrix rows.
+template <class T>
+static void slab_rows(const T* w, size_t rows, size_t cols, size_t m, const int32_t* act, int32_t* out,
+                      int threads) {
+  if (threads <= 1 || m <= 1) {
+    for (size_t t = 0; t < m; ++t) gemv_rows(w, cols, act + t * cols, 0, rows, out + t * rows);
+    return;
+  }
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+  for (long t = 0; t < long(m); ++t) gemv_rows(w, cols, act + size_t(t) * cols, 0, rows, out + size_t(t) * rows);
+}
+
 static std::vector<int32_t> det_linear_slab(const std::vector<int32_t>& in, size_t m, size_t k,
                                             const Matrix& W) {
   if (k != W.cols)
     bail("deterministic linear input row 0 has width " + std::to_string(k) + ", expected " +
          std::to_string(W.cols));
   std::vector<int32_t> out(m * W.rows);
-  for (size_t t = 0; t < m; ++t) det_linear(W, in.data() + t * k, k, out.data() + t * W.rows);
+  if (W.width == 16) slab_rows(W.w16.data(), W.rows, W.cols, m, in.data(), out.data(), g_threads);
+  else slab_rows(W.w32.data(), W.rows, W.cols, m, in.data(), out.data(), g_threads);
   return out;
 }
 
@@ -153,13 +167,10 @@ struct Hasher {
   Hasher() { SHA256_Init(&ctx); }
   void bytes(const void* p, size_t n) { SHA256_Update(&ctx, p, n); }
   void u64(uint64_t v) { uint8_t b[8]; for (int i = 0; i < 8; ++i) b[i] = uint8_t(v >> (8 * i)); bytes(b, 8); }
+  // i32 values as little-endian bytes: the host's own layout on x86-64.
   void i32s(const int32_t* v, size_t n) {
-    std::vector<uint8_t> b(n * 4);
-    for (size_t i = 0; i < n; ++i) {
-      const uint32_t u = uint32_t(v[i]);
-      b[4 * i] = uint8_t(u); b[4 * i + 1] = uint8_t(u >> 8); b[4 * i + 2] = uint8_t(u >> 16); b[4 * i + 3] = uint8_t(u >> 24);
-    }
-    bytes(b.data(), b.size());
+    static_assert(__BYTE_ORDER__ == __ORDER_LITTLE_ENDIAN__, "commitments hash little-endian i32 bytes");
+    bytes(v, n * 4);
   }
   std::string hex() {
     uint8_t d[32];
@@ -413,12 +424,19 @@ static void finalize_model(orc_model* m) {
 // ---------------------------------------------------------------------------
 // Elementwise drivers (det_kernels.rs:223-282)
 // ---------------------------------------------------------------------------
+// rms_norm_slab / apply_head_rms_norm_slab / apply_value_rms_norm_slab
+// (det_kernels.rs:231-250, 393-428): rows in parallel, each normalised alone.
 static void rms_rows(int32_t* x, size_t rows, size_t cols, const std::vector<int32_t>& w, int64_t eps) {
   if (w.size() != cols) bail("rms norm width mismatch: " + std::to_string(cols) + " vs " + std::to_string(w.size()));
-  for (size_t r = 0; r < rows; ++r) rms_norm_in_place(x + r * cols, w.data(), cols, eps);
+  // in parallel only when no row can fail a contract check
+  const bool par = g_threads > 1 && rows >= 16 && cols > 0 && cols <= UINT32_MAX && eps >= 0;
+#pragma omp parallel for num_threads(g_threads) schedule(static) if (par)
+  for (long r = 0; r < long(rows); ++r) rms_norm_in_place(x + size_t(r) * cols, w.data(), cols, eps);
 }
 static void value_rms_rows(int32_t* x, size_t rows, size_t cols, int64_t eps) {
-  for (size_t r = 0; r < rows; ++r) value_rms_norm_in_place(x + r * cols, cols, eps);
+  const bool par = g_threads > 1 && rows >= 16 && cols > 0 && cols <= UINT32_MAX && eps >= 0;
+#pragma omp parallel for num_threads(g_threads) schedule(static) if (par)
+  for (long r = 0; r < long(rows); ++r) value_rms_norm_in_place(x + size_t(r) * cols, cols, eps);
 }
 static void add_into(int32_t* dst, const int32_t* src, size_t n) { for (size_t i = 0; i < n; ++i) dst[i] = add_sat(dst[i], src[i]); }
 static void mul_into(int32_t* dst, const int32_t* src, size_t n) { for (size_t i = 0; i < n; ++i) dst[i] = mul_sat(dst[i], src[i]); }
@@ -480,11 +498,15 @@ static std::vector<int32_t> layer_prefill(const Layer& L, const std::vector<int3
   rms_rows(q.data(), L.num_heads * m, hd, L.q_norm, L.eps);
   rms_rows(k.data(), L.num_kv_heads * m, hd, L.k_norm, L.eps);
   value_rms_rows(v.data(), L.num_kv_heads * m, hd, L.eps);
-  if (L.partial_rotary_dim > 0) {  // apply_rope_slab, det_kernels.rs:430-468
-    for (size_t i = 0; i < L.num_heads * m; ++i)
-      rope_rotate_pairs_in_place(&q[i * hd], hd, L.partial_rotary_dim, L.rope_freq_base_dim, L.rope_base, i % m);
-    for (size_t i = 0; i < L.num_kv_heads * m; ++i)
-      rope_rotate_pairs_in_place(&k[i * hd], hd, L.partial_rotary_dim, L.rope_freq_base_dim, L.rope_base, i % m);
+  if (L.partial_rotary_dim > 0) {  // apply_rope_slab, det_kernels.rs:430-468: (head, row) items in parallel
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic, 4) if (g_threads > 1)
+    for (long i = 0; i < long(L.num_heads * m); ++i)
+      rope_rotate_pairs_in_place(&q[size_t(i) * hd], hd, L.partial_rotary_dim, L.rope_freq_base_dim, L.rope_base,
+                                 size_t(i) % m);
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic, 4) if (g_threads > 1)
+    for (long i = 0; i < long(L.num_kv_heads * m); ++i)
+      rope_rotate_pairs_in_place(&k[size_t(i) * hd], hd, L.partial_rotary_dim, L.rope_freq_base_dim, L.rope_base,
+                                 size_t(i) % m);
   }
   if (!donor) {  // DetKvCacheData::from_head_slabs (det_tensor.rs:250-268)
     const size_t retained = cache_window ? (m > *cache_window ? m - *cache_window : 0) : 0;
@@ -500,26 +522,38 @@ static std::vector<int32_t> layer_prefill(const Layer& L, const std::vector<int3
     cache_out->reset();
   }
   std::vector<int32_t> combined(m * L.num_heads * hd);
-  for (size_t h = 0; h < L.num_heads; ++h) {
+  // det_kernels.rs:584-646: one item per (head, query), head-major; items are
+  // independent and each writes its own output row, so the thread pool takes
+  // them in any order.
+  auto item_window = [&](size_t h, size_t t, const int32_t** kk, const int32_t** vv) -> size_t {
     const size_t kvh = h / groups;
-    for (size_t t = 0; t < m; ++t) {
-      size_t start = 0;
-      if (attn_window) start = (t + 1) > *attn_window ? t + 1 - *attn_window : 0;
-      size_t rows = t + 1 - start;
-      const int32_t *kk, *vv;
-      if (donor) {  // cache_windows (det_kernels.rs:297-311)
-        const size_t avail = donor->len();
-        start = std::min(start, avail);
-        rows = std::min(rows, avail - start);
-        kk = donor->keys[kvh].rows_window(start);
-        vv = donor->values[kvh].rows_window(start);
-      } else {
-        kk = &k[(kvh * m + start) * hd];
-        vv = &v[(kvh * m + start) * hd];
-      }
-      if (rows == 0) contract_violation("attention_softmax requires a non-empty logits slice");
-      attention_output(&q[(h * m + t) * hd], kk, vv, rows, hd, &combined[t * L.num_heads * hd + h * hd]);
+    size_t start = 0;
+    if (attn_window) start = (t + 1) > *attn_window ? t + 1 - *attn_window : 0;
+    size_t rows = t + 1 - start;
+    if (donor) {  // cache_windows (det_kernels.rs:297-311)
+      const size_t avail = donor->len();
+      start = std::min(start, avail);
+      rows = std::min(rows, avail - start);
+      *kk = donor->keys[kvh].rows_window(start);
+      *vv = donor->values[kvh].rows_window(start);
+    } else {
+      *kk = &k[(kvh * m + start) * hd];
+      *vv = &v[(kvh * m + start) * hd];
     }
+    return rows;
+  };
+  for (size_t h = 0; h < L.num_heads; ++h)
+    for (size_t t = 0; t < m; ++t) {
+      const int32_t *kk, *vv;
+      if (item_window(h, t, &kk, &vv) == 0) contract_violation("attention_softmax requires a non-empty logits slice");
+    }
+  const long items = long(L.num_heads * m);
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic, 8) if (g_threads > 1)
+  for (long it = 0; it < items; ++it) {
+    const size_t h = size_t(it) / m, t = size_t(it) % m;
+    const int32_t *kk, *vv;
+    const size_t rows = item_window(h, t, &kk, &vv);
+    attention_output(&q[(h * m + t) * hd], kk, vv, rows, hd, &combined[t * L.num_heads * hd + h * hd]);
   }
   std::vector<int32_t> attn = det_linear_slab(combined, m, L.num_heads * hd, *L.o);
   if (L.o->rows != H) bail("o_proj output width mismatch");
@@ -596,14 +630,16 @@ static std::vector<int32_t> layer_decode(const Layer& L, const std::vector<int32
   const size_t key_start = attn_window ? (cur > *attn_window ? cur - *attn_window : 0) : 0;
   const size_t window_len = ac.det->len() > key_start ? ac.det->len() - key_start : 0;
   std::vector<int32_t> combined(L.num_heads * hd);
-  for (size_t h = 0; h < L.num_heads; ++h) {
-    const size_t kvh = h / groups;
-    const size_t avail = ac.det->len();
-    const size_t start = std::min(key_start, avail);
-    const size_t rows = std::min(window_len, avail - start);
-    if (rows == 0) contract_violation("attention_softmax requires a non-empty logits slice");
-    attention_output(&q[h * hd], ac.det->keys[kvh].rows_window(start), ac.det->values[kvh].rows_window(start),
-                     rows, hd, &combined[h * hd]);
+  const size_t avail = ac.det->len();
+  const size_t start = std::min(key_start, avail);
+  const size_t rows = std::min(window_len, avail - start);
+  if (rows == 0) contract_violation("attention_softmax requires a non-empty logits slice");
+  // det_kernels.rs:1013-1036: heads in parallel, each into its own output chunk.
+#pragma omp parallel for num_threads(g_threads) schedule(static, 1) if (g_threads > 1 && L.num_heads > 1)
+  for (long h = 0; h < long(L.num_heads); ++h) {
+    const size_t kvh = size_t(h) / groups;
+    attention_output(&q[size_t(h) * hd], ac.det->keys[kvh].rows_window(start), ac.det->values[kvh].rows_window(start),
+                     rows, hd, &combined[size_t(h) * hd]);
   }
   std::vector<int32_t> attn(L.o->rows);
   det_linear(*L.o, combined.data(), combined.size(), attn.data());
@@ -938,10 +974,53 @@ int orc_det_linear_acc_i64(size_t rows, size_t cols, int w, const void* weight, 
 
 int orc_det_linear_slab(size_t m, size_t rows, size_t cols, int w, const void* weight, const int32_t* act, int32_t* out, int threads) {
   return guarded([&] {
-    for (size_t t = 0; t < m; ++t) {
-      if (w == 16) gemv_dispatch(static_cast<const int16_t*>(weight), rows, cols, act + t * cols, out + t * rows, threads);
-      else if (w == 32) gemv_dispatch(static_cast<const int32_t*>(weight), rows, cols, act + t * cols, out + t * rows, threads);
-      else bail("unsupported element width");
+    if (w == 16) slab_rows(static_cast<const int16_t*>(weight), rows, cols, m, act, out, threads);
+    else if (w == 32) slab_rows(static_cast<const int32_t*>(weight), rows, cols, m, act, out, threads);
+    else bail("unsupported element width");
+  });
+}
+
+// det_attention_prefill's attention items (det_kernels.rs:584-646) for caller
+// buffers: q [nq][nh*hd], k/v [nrows][nkv*hd] seq-major; query t attends key
+// rows [max(0, t+1-window), t+1) (window 0 = unbounded) of KV head h/groups.
+int orc_attention_causal(const int32_t* q, const int32_t* k, const int32_t* v, size_t nq, size_t nrows, size_t nh,
+                         size_t nkv, size_t hd, size_t window, int32_t* out, int threads) {
+  return guarded([&] {
+    if (nkv == 0 || nh / nkv == 0) bail("invalid Gemma head configuration");
+    if (nq == 0 || nh == 0 || hd == 0) bail("empty attention problem");
+    if (nrows < nq) contract_violation("attention_softmax requires a non-empty logits slice");
+    const size_t groups = nh / nkv;
+    if ((nh - 1) / groups >= nkv) contract_violation("query head maps past the last KV head");
+    // head-major copies of the key / value rows (HeadSlab layout, det_tensor.rs:12-146)
+    std::vector<int32_t> kh(nkv * nrows * hd), vh(nkv * nrows * hd);
+    for (size_t h = 0; h < nkv; ++h)
+      for (size_t r = 0; r < nrows; ++r) {
+        std::memcpy(&kh[(h * nrows + r) * hd], k + r * nkv * hd + h * hd, hd * 4);
+        std::memcpy(&vh[(h * nrows + r) * hd], v + r * nkv * hd + h * hd, hd * 4);
+      }
+    const long items = long(nh * nq);
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 8) if (threads > 1)
+    for (long it = 0; it < items; ++it) {
+      const size_t h = size_t(it) / nq, t = size_t(it) % nq, kvh = h / groups;
+      const size_t start = window && t + 1 > window ? t + 1 - window : 0;
+      attention_output(q + t * nh * hd + h * hd, &kh[(kvh * nrows + start) * hd], &vh[(kvh * nrows + start) * hd],
+                       t + 1 - start, hd, out + t * nh * hd + h * hd);
+    }
+  });
+}
+
+// The inverse-frequency chain of rope_rotate_pairs_in_place (ops.rs:184-195):
+// out[i] = inv_frequency before pair i, starting at one and multiplied by
+// rope_frequency_step(base, freq_base_dim) with acc_mul after every pair.
+int orc_rope_inv_frequencies(int64_t base, size_t freq_base_dim, size_t half, int64_t* out) {
+  return guarded([&] {
+    if (freq_base_dim < 2 || freq_base_dim % 2) contract_violation("rope_rotate_pairs requires an even freq_base_dim of at least 2");
+    if (base <= 0) contract_violation("rope_rotate_pairs requires a positive base");
+    int64_t inv_frequency = kOneAcc;
+    const int64_t step = rope_frequency_step(base, freq_base_dim);
+    for (size_t i = 0; i < half; ++i) {
+      out[i] = inv_frequency;
+      inv_frequency = acc_mul(inv_frequency, step);
     }
   });
 }
@@ -982,28 +1061,32 @@ int orc_model_set_tensor(orc_model* m, const char* name, size_t rank, const uint
       // Exact expansion q*s into canonical Wgt bits; i16 iff every value fits
       // (artifact.rs:250-256), as a detwgt v2 converter would store it.
       if (!row_scale) bail("int8 tensors need a row scale");
-      std::vector<int32_t> bits(n);
-      bool fits16 = true;
       const int8_t* q = static_cast<const int8_t*>(data);
-      for (size_t r = 0; r < rows; ++r) {
+      bool fits16 = true, fits32 = true, mass_ok = true;
+#pragma omp parallel for schedule(static) reduction(&& : fits16, fits32, mass_ok)
+      for (long r = 0; r < long(rows); ++r) {
         uint64_t mass = 0;
         for (size_t c = 0; c < cols; ++c) {
-          const int64_t v = int64_t(q[r * cols + c]) * int64_t(row_scale[r]);
-          if (v < INT32_MIN || v > INT32_MAX) bail("int8 x scale does not fit a Q16.16 weight");
-          bits[r * cols + c] = int32_t(v);
-          mass += uint64_t(v < 0 ? -v : v);
+          const int64_t v = int64_t(q[size_t(r) * cols + c]) * int64_t(row_scale[r]);
+          fits32 = fits32 && v >= INT32_MIN && v <= INT32_MAX;
           fits16 = fits16 && v >= INT16_MIN && v <= INT16_MAX;
+          mass += uint64_t(v < 0 ? -v : v);
         }
-        if (rank == 2 && mass >= (uint64_t(1) << 31)) bail("row mass violates the overflow bound");
+        mass_ok = mass_ok && !(rank == 2 && mass >= (uint64_t(1) << 31));
       }
-      if (fits16) {
-        t.m.width = 16;
-        t.m.w16.resize(n);
-        for (size_t i = 0; i < n; ++i) t.m.w16[i] = int16_t(bits[i]);
-      } else {
-        t.m.width = 32;
-        t.m.w32 = std::move(bits);
-      }
+      if (!fits32) bail("int8 x scale does not fit a Q16.16 weight");
+      if (!mass_ok) bail("row mass violates the overflow bound");
+      // Exact expansion q*s into canonical Wgt bits; i16 iff every value fits
+      // (artifact.rs:250-256), as a detwgt v2 converter would store it.
+      t.m.width = fits16 ? 16 : 32;
+      if (fits16) t.m.w16.resize(n); else t.m.w32.resize(n);
+#pragma omp parallel for schedule(static)
+      for (long r = 0; r < long(rows); ++r)
+        for (size_t c = 0; c < cols; ++c) {
+          const size_t i = size_t(r) * cols + c;
+          const int32_t v = int32_t(int64_t(q[i]) * int64_t(row_scale[r]));
+          if (fits16) t.m.w16[i] = int16_t(v); else t.m.w32[i] = v;
+        }
     } else if (w == 16) {
       t.m.width = 16;
       t.m.w16.assign(static_cast<const int16_t*>(data), static_cast<const int16_t*>(data) + n);

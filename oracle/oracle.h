@@ -100,8 +100,19 @@ int orc_det_linear(size_t rows, size_t cols, int elem_width, const void* weight,
                    const int32_t* act, int32_t* out, int threads);
 int orc_det_linear_acc_i64(size_t rows, size_t cols, int elem_width, const void* weight,
                            const int32_t* act, int64_t* acc_out);
+// threads > 1: token rows spread over the threads, each one serial GEMV
+// (det_linear_slab's parallel schedule).
 int orc_det_linear_slab(size_t m, size_t rows, size_t cols, int elem_width, const void* weight,
                         const int32_t* act, int32_t* out, int threads);
+
+// ---- attention / RoPE drivers ----
+// det_attention_prefill's (head, query) items without a donor cache
+// (det_kernels.rs:584-646): q [nq][nh*hd], k/v [nrows][nkv*hd]; query t attends
+// rows [max(0, t+1-window), t+1), window 0 = unbounded; out [nq][nh*hd].
+int orc_attention_causal(const int32_t* q, const int32_t* k, const int32_t* v, size_t nq, size_t nrows,
+                         size_t nh, size_t nkv, size_t hd, size_t window, int32_t* out, int threads);
+// RoPE inverse frequencies before each of `half` pairs (ops.rs:184-195).
+int orc_rope_inv_frequencies(int64_t base, size_t freq_base_dim, size_t half, int64_t* out);
 
 // ---- commitments (transformer_kernels.rs:1395-1482) ----
 void orc_commit_activation_rows(const int32_t* rows, size_t n_rows, size_t width, char out_hex[65]);

@@ -403,6 +403,8 @@ inline int64_t pow_acc(int64_t base, uint32_t e) {
   for (uint32_t i = 0; i < e; ++i) r = acc_mul(r, base);
   return r;
 }
+// Callers reject value == INT64_MAX first: the reference's bisection
+// overflows i64 there (ops.rs:578) and never returns a root.
 inline int64_t nth_root(int64_t value, uint32_t degree) {
   if (degree == 1 || value == kOneAcc) return value;
   int64_t lo = 0, hi = value > kOneAcc ? value : kOneAcc;

@@ -168,6 +168,9 @@ def lib() -> C.CDLL:
             ("orc_det_linear", C.c_int, [C.c_size_t, C.c_size_t, C.c_int, P, P, P, C.c_int]),
             ("orc_det_linear_acc_i64", C.c_int, [C.c_size_t, C.c_size_t, C.c_int, P, P, P]),
             ("orc_det_linear_slab", C.c_int, [C.c_size_t, C.c_size_t, C.c_size_t, C.c_int, P, P, P, C.c_int]),
+            ("orc_attention_causal", C.c_int, [P, P, P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t,
+                                               C.c_size_t, C.c_size_t, P, C.c_int]),
+            ("orc_rope_inv_frequencies", C.c_int, [C.c_int64, C.c_size_t, C.c_size_t, P]),
             ("orc_commit_activation_rows", None, [P, C.c_size_t, C.c_size_t, C.c_char_p]),
             ("orc_commit_vector", None, [P, C.c_size_t, C.c_char_p]),
             ("orc_model_create", C.c_int, [C.POINTER(OrcTextConfig), C.POINTER(P)]),
@@ -236,11 +239,59 @@ class OracleModel:
         check(lib().orc_capture(self.handle, ptr(ids), ids.size, decode_steps, buf, len(buf)))
         return json.loads(buf.value.decode())
 
+    def session(self, prompt: list[int]) -> "OracleSession":
+        """Prefills the prompt (pipeline::run_prefill_pass_with_mode) and returns the session."""
+        return OracleSession(self, prompt)
+
     def __del__(self):
         h = getattr(self, "handle", None)
         if h and _LIB is not None:
             _LIB.orc_model_free(h)
             self.handle = None
+
+
+class OracleSession:
+    """One sequence on the oracle: prefill, then greedy decode steps."""
+
+    def __init__(self, model: OracleModel, prompt: list[int]):
+        self.model = model  # keeps the weights alive
+        self.vocab = int(model.config["vocab_size"])
+        self.hidden = int(model.config["hidden_size"])
+        ids = np.asarray(prompt, dtype=np.uint32)
+        self.logits = np.empty(self.vocab, dtype=np.int32)
+        h = C.c_void_p()
+        check(lib().orc_session_prefill(model.handle, ptr(ids), ids.size, C.byref(h), ptr(self.logits)))
+        self.handle = h
+
+    def next_token(self) -> int:
+        return int(np.argmax(self.logits))  # argmax_first: numpy returns the first maximum
+
+    def decode(self, token: int) -> np.ndarray:
+        """One decode step; returns the activation row (logits in self.logits)."""
+        hidden = np.empty(self.hidden, dtype=np.int32)
+        check(lib().orc_session_decode(self.handle, int(token), ptr(self.logits), ptr(hidden)))
+        return hidden
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h and _LIB is not None:
+            _LIB.orc_session_free(h)
+            self.handle = None
+
+
+def attention_causal(q, k, v, n_queries, n_rows, num_heads, num_kv_heads, head_dim, window, threads=1):
+    """det_attention_prefill's items on seq-major q [nq][nh*hd], k/v [nrows][nkv*hd]."""
+    q, k, v = (np.ascontiguousarray(x, dtype=np.int32) for x in (q, k, v))
+    out = np.zeros((n_queries, num_heads * head_dim), dtype=np.int32)
+    check(lib().orc_attention_causal(ptr(q), ptr(k), ptr(v), n_queries, n_rows, num_heads, num_kv_heads, head_dim,
+                                     window, ptr(out), threads))
+    return out
+
+
+def rope_inv_frequencies(base_acc: int, freq_base_dim: int, half: int) -> np.ndarray:
+    out = np.empty(half, dtype=np.int64)
+    check(lib().orc_rope_inv_frequencies(base_acc, freq_base_dim, half, ptr(out)))
+    return out
 
 
 def set_threads(n: int) -> None:

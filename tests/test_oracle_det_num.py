@@ -332,9 +332,133 @@ def test_sin_cos_is_close_to_libm():
         assert abs(s.value / 65536 - math.sin(ang)) < 2e-3
 
 
-def test_nth_root_and_frequency_step():
-    for base, deg in [(16 << 32, 2), (10000 << 32, 8), (1_000_000 << 32, 128), (12345 << 32, 1)]:
-        r = out64(L.orc_nth_root_acc, base, deg)
-        assert abs(r / 2**32 - (base / 2**32) ** (1 / deg)) < 1e-6 * max(1, r / 2**32)
-        step = out64(L.orc_rope_frequency_step, base, 2 * deg)
-        assert abs(step / 2**32 - 1 / (r / 2**32)) < 1e-8
+# ---------------- nth_root_acc / RoPE frequencies, pinned exactly ----------------
+# The reference (ops.rs:555-611) takes the largest Q32.32 value m in
+# [0, max(value, one)] whose sequential power chain pow_acc_u32(m, degree)
+# (one, then acc_mul by m degree times, each product rounded half to even and
+# saturated to i64) does not exceed the value, then rounds to whichever of m and
+# m + 1 (saturating) has the power nearest the value, ties to the even one.
+# The restatement below shares no code with the oracle: acc_mul is the
+# closed-form rational rounding (pinned above), and the floor is found by
+# galloping from a floating-point estimate of the root instead of bisecting.
+ONE = 1 << 32
+I64MAX = (1 << 63) - 1
+
+
+def py_acc_mul(a, b):
+    return sat(rte(Fraction(a * b, ONE)), -(1 << 63), I64MAX)
+
+
+def py_pow(m, degree):
+    r = ONE
+    for _ in range(degree):
+        r = py_acc_mul(r, m)
+    return r
+
+
+def py_floor_root(value, degree):
+    """Largest m in [0, max(value, one)] with py_pow(m, degree) <= value.
+
+    py_pow is non-decreasing in m (acc_mul of non-negative operands is), so the
+    values that qualify form a prefix of [0, hi]."""
+    hi = max(value, ONE)
+    est = min(hi, max(0, int((value / ONE) ** (1.0 / degree) * ONE)))
+    m, step = est, 1
+    while py_pow(m, degree) > value:  # gallop down to a qualifying m
+        m, step = max(0, m - step), step * 2
+    step = 1
+    while m < hi and py_pow(min(hi, m + step), degree) <= value:  # gallop up
+        m, step = min(hi, m + step), step * 2
+    lo_ok, hi_bad = m, min(hi, m + step)  # py_pow(lo_ok) <= value, and hi_bad fails unless it is hi
+    if py_pow(hi_bad, degree) <= value:
+        return hi_bad
+    while hi_bad - lo_ok > 1:
+        mid = (lo_ok + hi_bad) // 2
+        if py_pow(mid, degree) <= value:
+            lo_ok = mid
+        else:
+            hi_bad = mid
+    return lo_ok
+
+
+def py_nth_root(value, degree):
+    if degree == 1 or value == ONE:
+        return value
+    lower = py_floor_root(value, degree)
+    upper = min(lower + 1, I64MAX)
+    el, eu = abs(value - py_pow(lower, degree)), abs(py_pow(upper, degree) - value)
+    if eu != el:
+        return upper if eu < el else lower
+    return lower if lower % 2 == 0 else upper
+
+
+NTH_ROOT_BASES = [10000 * ONE, 1_000_000 * ONE, 12345 * ONE, 16 * ONE, int(3.5 * ONE), ONE + 1, ONE - 1,
+                  ONE // 2, ONE // 1000, 7, I64MAX - 1, I64MAX - 12345, 5 * 10**17]
+
+
+@pytest.mark.parametrize("base", NTH_ROOT_BASES)
+def test_nth_root_equals_exact_restatement_for_every_degree(base):
+    chosen_upper = 0
+    for degree in list(range(1, 33)) + [47, 64, 100, 127, 128, 200, 256]:
+        got = out64(L.orc_nth_root_acc, base, degree)
+        exp = py_nth_root(base, degree)
+        assert got == exp, (base, degree)
+        if degree > 1 and got < I64MAX:
+            # nearest power: no worse than the neighbouring Q32.32 values
+            err = abs(base - py_pow(got, degree))
+            assert err <= abs(base - py_pow(got + 1, degree)), (base, degree)
+            assert got == 0 or err <= abs(base - py_pow(got - 1, degree)), (base, degree)
+            chosen_upper += got != py_floor_root(base, degree)
+    if base == 10000 * ONE:
+        assert chosen_upper > 0  # the set exercises rounding up as well as down
+
+
+def test_nth_root_saturating_search():
+    # near i64::MAX every large candidate's power chain saturates to i64::MAX,
+    # which exceeds the value, so the search stays below the saturation point
+    for v in (I64MAX - 1, I64MAX - (1 << 40)):
+        for degree in (2, 3, 128):
+            assert out64(L.orc_nth_root_acc, v, degree) == py_nth_root(v, degree)
+
+
+def test_nth_root_of_i64_max_is_the_reference_overflow_panic():
+    # ops.rs:578 computes high - low + 1 = i64::MAX + 1 on the first step: the
+    # reference panics (overflow checks) or bisects forever (wrapping), so the
+    # oracle reports the panic as a contract violation, status 2
+    o = C.c_int64()
+    for degree in (2, 3, 128):
+        assert L.orc_nth_root_acc(I64MAX, degree, C.byref(o)) == 2
+    assert out64(L.orc_nth_root_acc, I64MAX, 1) == I64MAX  # degree 1 returns before the search
+
+
+def test_nth_root_ties_go_to_the_even_candidate():
+    # degree 2: pow(m) = acc_mul(m, m). A value exactly halfway between the
+    # powers of consecutive candidates is a tie; both parities occur.
+    parities = set()
+    m = 3 * ONE // 2
+    while len(parities) < 2:
+        p0, p1 = py_pow(m, 2), py_pow(m + 1, 2)
+        if (p0 + p1) % 2 == 0 and p1 > p0:
+            v = (p0 + p1) // 2
+            assert py_floor_root(v, 2) == m
+            got = out64(L.orc_nth_root_acc, v, 2)
+            assert got == (m if m % 2 == 0 else m + 1), m
+            parities.add(m % 2)
+        m += 1
+
+
+@pytest.mark.parametrize("base", [10000 * ONE, 1_000_000 * ONE, 12345 * ONE, int(3.5 * ONE)])
+@pytest.mark.parametrize("freq_base_dim", [2, 4, 16, 64, 256, 512])
+def test_rope_frequency_step_and_inverse_frequency_chain(base, freq_base_dim):
+    # rope_frequency_step = div_acc(one, nth_root_acc(base, fbd / 2)) (ops.rs:555-559),
+    # div_acc rounding half to even; the chain multiplies by it after every pair
+    # (ops.rs:184-195). E4B tables: fbd 256 with 128 pairs (sliding) and 32 (full).
+    root = py_nth_root(base, freq_base_dim // 2)
+    step = sat(rte(Fraction(ONE * ONE, root)), -(1 << 63), I64MAX)
+    assert out64(L.orc_rope_frequency_step, base, freq_base_dim) == step
+    half = freq_base_dim // 2
+    chain, f = [], ONE
+    for _ in range(half):
+        chain.append(f)
+        f = py_acc_mul(f, step)
+    assert oracle_lib.rope_inv_frequencies(base, freq_base_dim, half).tolist() == chain
