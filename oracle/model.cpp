@@ -887,6 +887,7 @@ static void load_detwgt(orc_model* m, const uint8_t* b, size_t len) {
     const uint8_t* np = take(name_len);
     std::string name(reinterpret_cast<const char*>(np), name_len);
     const uint32_t rank = rd32();
+    if (rank > (len - cur) / 8) bail("artifact ended unexpectedly");  // before allocating the dims
     std::vector<uint64_t> shape(rank);
     uint64_t prod = 1;
     for (uint32_t r = 0; r < rank; ++r) {
@@ -899,7 +900,10 @@ static void load_detwgt(orc_model* m, const uint8_t* b, size_t len) {
     const uint32_t width = rd32();
     if (width != 16 && width != 32) bail("tensor `" + name + "` has an invalid element width");
     const uint64_t payload_len = rd64();
-    if (payload_len != element_count * (width / 8)) bail("tensor `" + name + "` payload length mismatch");
+    uint64_t expected_payload_len = 0;  // gemma/io.rs:327-331 checked_mul
+    if (__builtin_mul_overflow(element_count, uint64_t(width / 8), &expected_payload_len))
+      bail("tensor payload byte count overflowed");
+    if (payload_len != expected_payload_len) bail("tensor `" + name + "` payload length mismatch");
     const uint64_t mass = rd64();
     if (rank >= 2 && mass >= (uint64_t(1) << 31)) bail("tensor `" + name + "` max row mass violates the overflow bound");
     const size_t pad = (64 - cur % 64) % 64;

@@ -144,6 +144,9 @@ int guarded(det_ctx* ctx, F&& f) {
   } catch (const Status& e) {
     (ctx ? ctx->last_error : g_error) = e.what();
     return e.code;
+  } catch (const std::invalid_argument& e) {  // argument checks inside the kernel launchers
+    (ctx ? ctx->last_error : g_error) = e.what();
+    return 1;
   } catch (const std::exception& e) {
     (ctx ? ctx->last_error : g_error) = e.what();
     return 3;
@@ -240,6 +243,9 @@ void check_row_mass(uint64_t rows, uint64_t cols, const std::vector<int64_t>& ma
 
 DevMatrix upload_matrix(det_ctx* ctx, uint64_t rows, uint64_t cols, int width, const void* values,
                         const int32_t* row_scale) {
+  uint64_t elems = 0;
+  if (__builtin_mul_overflow(rows, cols, &elems) || elems > UINT64_MAX / 4) bail("tensor shape overflowed");
+  if (elems && !values) bail("matrix values pointer is null");
   if (width == 8) {
     if (!row_scale) bail("int8 matrices need a row scale");
     const int8_t* q = static_cast<const int8_t*>(values);
@@ -428,6 +434,9 @@ struct det_model {
   det::RopeTable* rope_tables_dev = nullptr;
   uint32_t trig_pairs = 0;
   bool fused_ok = false;
+  // a RoPE base of i64::MAX (theta >= 2^31): the reference's nth_root_acc
+  // overflows on it (ops.rs:578) at the first rotation of a position > 0
+  bool rope_overflow = false;
   BatchWs* batch = nullptr;  // row scratch of batched decode steps (grown on demand)
 
   ~det_model() {
@@ -616,8 +625,9 @@ void finalize(det_model* m) {
           L.trig_off = t.offset;
         }
       if (!L.inv_freq) {
-        std::vector<int64_t> tab(L.rotary / 2);
-        det::rope_inv_freq_table(L.rope_base, uint32_t(L.freq_base_dim), uint32_t(L.rotary / 2), tab.data());
+        std::vector<int64_t> tab(L.rotary / 2, 0);
+        if (L.rope_base == INT64_MAX && L.freq_base_dim / 2 > 1) m->rope_overflow = true;  // table never used
+        else det::rope_inv_freq_table(L.rope_base, uint32_t(L.freq_base_dim), uint32_t(L.rotary / 2), tab.data());
         HIPC(hipMalloc(&L.inv_freq, tab.size() * 8));
         HIPC(hipMemcpy(L.inv_freq, tab.data(), tab.size() * 8, hipMemcpyHostToDevice));
         m->owned_dev.push_back(L.inv_freq);
@@ -724,21 +734,28 @@ void load_detwgt(det_model* m, const uint8_t* b, size_t len) {
     const uint32_t nl = rd32();
     std::string name(reinterpret_cast<const char*>(take(nl)), nl);
     const uint32_t rank = rd32();
+    // every dimension is 8 bytes of the artifact: a rank the remaining bytes
+    // cannot hold ends the artifact before any allocation
+    if (rank > (len - cur) / 8) bail("artifact ended unexpectedly");
     std::vector<uint64_t> shape(rank);
     uint64_t prod = 1;
     for (auto& d : shape) {
       d = rd64();
-      if (d && prod > UINT64_MAX / d) bail("tensor shape overflowed");
-      prod *= d;
+      if (__builtin_mul_overflow(prod, d, &prod)) bail("tensor shape overflowed");
     }
     if (rd64() != prod) bail("tensor `" + name + "` element count mismatch");
     const uint32_t width = rd32();
     if (width != 16 && width != 32 && !(q8 && width == 8 && rank >= 2))
       bail("tensor `" + name + "` has an invalid element width");
-    if (rd64() != prod * (width / 8)) bail("tensor `" + name + "` payload length mismatch");
+    // gemma/io.rs:327-331: element_count.checked_mul(byte width)
+    uint64_t payload = 0;
+    if (__builtin_mul_overflow(prod, uint64_t(width / 8), &payload)) bail("tensor payload byte count overflowed");
+    if (rd64() != payload) bail("tensor `" + name + "` payload length mismatch");
     const uint64_t mass = rd64();
     if (rank >= 2 && mass >= (uint64_t(1) << 31)) bail("tensor `" + name + "` max row mass violates the overflow bound");
     const uint64_t rows = (width == 8 && shape.back()) ? prod / shape.back() : 0;
+    uint64_t scale_bytes = 0;
+    if (__builtin_mul_overflow(rows, uint64_t(4), &scale_bytes)) bail("tensor `" + name + "` scale byte count overflowed");
     if (width == 8 && rd64() != rows) bail("tensor `" + name + "` scale count mismatch");
     auto pad = [&]() {
       const size_t n = (64 - cur % 64) % 64;
@@ -747,12 +764,13 @@ void load_detwgt(det_model* m, const uint8_t* b, size_t len) {
         if (pp[k]) bail("tensor `" + name + "` has non-zero payload alignment padding");
     };
     pad();
-    const uint8_t* data = take(prod * (width / 8));
+    const uint8_t* data = take(payload);
     const int32_t* scale = nullptr;
     if (width == 8) {
       pad();
+      const uint8_t* sp = take(scale_bytes);
       scales.emplace_back(rows);
-      if (rows) std::memcpy(scales.back().data(), take(rows * 4), rows * 4);
+      if (rows) std::memcpy(scales.back().data(), sp, scale_bytes);
       scale = scales.back().data();
       // W = q * s must be a canonical (i32) Wgt value
       const uint64_t cols = shape.back();
@@ -1053,6 +1071,13 @@ void check_ids(det_model* m, const uint32_t* ids, uint64_t n) {
   }
 }
 
+// Rotations at positions up to max_position reach the reference's
+// nth_root_acc bisection, which overflows for a base of i64::MAX.
+void check_rope(const det_model* m, uint64_t max_position) {
+  if (m->rope_overflow && max_position > 0)
+    contract("nth_root_acc: attempt to add with overflow (RoPE base i64::MAX)");
+}
+
 void logits_from(det_session* s, const int32_t* hidden_row) {
   det_model* m = s->m;
   det_ctx* ctx = m->ctx;
@@ -1082,6 +1107,7 @@ bool prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
   if (n > s->max_tokens) bail("prompt longer than the session capacity");
   if (s->position != 0) bail("session already holds a prefilled sequence");
   check_ids(m, ids, n);
+  check_rope(m, n - 1);
   const uint64_t H = m->hidden;
   HIPC(hipMemcpyAsync(s->ids, ids, n * 4, hipMemcpyHostToDevice, st));
   det::launch_gather_rows(*m->embedding, s->ids, n, 0, H, m->embed_scale, s->x, H, st);
@@ -1183,6 +1209,7 @@ bool decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
   if (s->position == 0) bail("decode requires a prefilled session");
   if (s->position >= s->max_tokens) bail("session capacity exhausted");
   check_ids(m, &token, 1);
+  check_rope(m, s->position);
   const uint64_t H = m->hidden;
   HIPC(hipMemcpyAsync(s->ids, &token, 4, hipMemcpyHostToDevice, st));
   det::launch_gather_rows(*m->embedding, s->ids, 1, 0, H, m->embed_scale, s->dec_in, H, st);
@@ -1360,6 +1387,7 @@ void check_batch(det_session* const* ss, uint64_t n, const uint32_t* tokens) {
       if (ss[j] == s) bail("a session appears twice in one batch");
     if (s->position == 0) bail("decode requires a prefilled session");
     if (s->position >= s->max_tokens) bail("session capacity exhausted");
+    check_rope(m, s->position);
     for (size_t l = 0; l < m->layers.size(); ++l) {
       const GKv& c = s->kv[l];
       if (m->layers[l].donor) continue;
@@ -1777,6 +1805,7 @@ void decode_fused(det_session* s, uint32_t token, uint32_t flags, det_decode_res
   if (s->position == 0) bail("decode requires a prefilled session");
   if (s->position >= s->max_tokens) bail("session capacity exhausted");
   check_ids(m, &token, 1);
+  check_rope(m, s->position);
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GKv& c = s->kv[l];
     if (!m->layers[l].donor && !c.has) bail("deterministic decode cache append requires canonical key rows");
@@ -2425,6 +2454,13 @@ int det_rope(det_ctx_t* ctx, int32_t* x, uint64_t rows, uint64_t heads, uint64_t
     if (rotary > hd) contract("rope_rotate_pairs requires rotary_dim to fit within the input width");
     if (fbd < 2 || fbd % 2) contract("rope_rotate_pairs requires an even freq_base_dim of at least 2");
     if (base <= 0) contract("rope_rotate_pairs requires a positive base");
+    if (base == INT64_MAX && fbd / 2 > 1) {
+      // position 0 is the identity and returns before the frequency step;
+      // any later position reaches the overflowing bisection (ops.rs:578)
+      if (rows > 0 && (pos0 > 0 || (rows > 1 && pos_step > 0)))
+        contract("nth_root_acc: attempt to add with overflow (RoPE base i64::MAX)");
+      return;
+    }
     std::vector<int64_t> tab(rotary / 2);
     det::rope_inv_freq_table(base, uint32_t(fbd), uint32_t(rotary / 2), tab.data());
     int64_t* d = nullptr;

@@ -6,6 +6,8 @@
 // the reference's serial order regardless of the launch shape.
 #include <hip/hip_runtime.h>
 
+#include <stdexcept>
+
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -1858,7 +1860,9 @@ void launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.n_queries == 0 || a.num_heads == 0) return;
   uint64_t max_rows = a.causal ? (a.avail) : a.fix_count;
   if (max_rows == 0) max_rows = 1;
-  if (max_rows > kMaxAttnRows) return;  // callers validate against kMaxAttnRows
+  // callers validate against kMaxAttentionRows first; a window that still
+  // exceeds the LDS score rows fails here instead of leaving `out` stale
+  if (max_rows > kMaxAttnRows) throw std::invalid_argument("attention window longer than 16000 rows is not supported");
   // grouped-head kernel: 128-bit row loads need 4-aligned widths and strides
   const uint64_t stride = std::max<uint64_t>(attn_row_stride(a), 1);
   const bool aligned = a.hd % 4 == 0 && a.kv_ld % 4 == 0 && a.hd <= 512;

@@ -57,3 +57,19 @@ def test_loader_fails_closed():
         oracle_lib.OracleModel(cfg).load_detwgt(wgt + b"\0")  # trailing bytes
     with pytest.raises(oracle_lib.OracleError):
         oracle_lib.OracleModel(cfg).load_detwgt(wgt[:-2])  # truncated
+
+
+def test_loader_rejects_wrapping_and_oversized_headers():
+    # element count x width overflows u64 (2^62 x 4 = 2^64 wraps to 0): the
+    # reference's checked_mul rejects it (gemma/io.rs:327-331); a rank larger
+    # than the remaining bytes ends the artifact before any allocation
+    import struct
+    cfg, _, _, _ = fixtures.golden_fixture("no_donor_ple")
+    head = b"DNWGTV0\0" + struct.pack("<IIQ", 2, 1, 1)
+    rec = struct.pack("<I", 1) + b"w" + struct.pack("<I", 2) + struct.pack("<QQ", 1 << 31, 1 << 31)
+    rec += struct.pack("<QIQQ", 1 << 62, 32, 0, 0)
+    with pytest.raises(oracle_lib.OracleError, match="payload byte count overflowed") as e:
+        oracle_lib.OracleModel(cfg).load_detwgt(head + rec)
+    assert e.value.status == 1
+    with pytest.raises(oracle_lib.OracleError, match="ended unexpectedly"):
+        oracle_lib.OracleModel(cfg).load_detwgt(head + struct.pack("<I", 1) + b"w" + struct.pack("<I", 0xFFFFFFFF))
