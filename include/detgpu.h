@@ -37,6 +37,8 @@ typedef struct det_matrix det_matrix_t;
 typedef struct det_model det_model_t;
 typedef struct det_session det_session_t;
 typedef struct det_event det_event_t;
+typedef struct det_kv det_kv_t;
+typedef struct det_scratch det_scratch_t;
 
 /* ------------------------------------------------------------------------ */
 /* Context, memory, timing                                                   */
@@ -178,6 +180,69 @@ int det_model_load_detwgt(det_model_t* model, const uint8_t* bytes, size_t len);
 /* Resolves layers exactly like load_det_num_gemma4_layer_weights (gemma/io.rs:1896-2045). */
 int det_model_finalize(det_model_t* model);
 void det_model_free(det_model_t* model);
+
+/* ------------------------------------------------------------------------ */
+/* Layer-level operators: the reference's det_kernels.rs API                 */
+/* ------------------------------------------------------------------------ */
+/* These are the functions the routines' native deterministic tiles call per
+ * layer (prefill_range/native/deterministic_tiles.rs:69-199,
+ * decode_layer_range/native/tiles.rs:133-197), so an executor can run any
+ * layer range and emit its own checkpoints between layers. Activations are
+ * device buffers of Q16.16 int32 rows of the model's hidden width; work is
+ * enqueued on the model context's stream. */
+
+/* Reusable row buffers (DetDecodeScratch, det_kernels.rs:830-864), grown on
+ * demand; one scratch serves one caller at a time. det_layer_prefill
+ * allocates its scratch per call in the reference and takes one here. */
+int det_scratch_create(det_model_t* model, det_scratch_t** out);
+void det_scratch_free(det_scratch_t* scratch);
+
+/* LayerKvCache of one layer (shared/model/transformer.rs:278-337) with room
+ * for max_tokens appended tokens; a sliding-window layer that owns its cache
+ * keeps its last `window` rows. Starts without det data (None). */
+int det_kv_create(det_model_t* model, uint64_t layer, uint64_t max_tokens, det_kv_t** out);
+/* LayerKvCache::clone (e.g. to keep the pre-step caches a decode.layer_range
+ * commitment needs). */
+int det_kv_clone(const det_kv_t* src, det_kv_t** out);
+void det_kv_free(det_kv_t* kv);
+/* current_len, head count, head dim, and whether det data is present. */
+int det_kv_info(const det_kv_t* kv, uint64_t* len, uint64_t* heads, uint64_t* head_dim, int32_t* has_det);
+/* DetKvCacheData's rows in logical order (det_tensor.rs:147-397): keys and
+ * values host [heads][len][head_dim]; capacity = values each buffer holds. */
+int det_kv_read_logical(const det_kv_t* kv, int32_t* keys, int32_t* values, uint64_t capacity);
+/* build_det_kv_cache_commitment (transformer_kernels.rs:1460-1482) over
+ * caches[0..n) in order: *is_some = 0 and out = "" when one lacks det data. */
+int det_kv_commitment(const det_kv_t* const* caches, uint64_t n, char out[65], int32_t* is_some);
+
+/* decode_embedding_rows_for_token_ids_from_det_num + scale_act_row
+ * (gemma/io.rs:2446-2518): out [n][hidden]. */
+int det_embed_tokens(det_model_t* model, det_scratch_t* scratch, const uint32_t* ids, uint64_t n, int32_t* out_dev);
+/* compute_prefill_ple_inputs_det for one layer
+ * (prefill_prepare_aux/native/tiles.rs:111-240): out [n][ple_dim] from the
+ * token ids and the embedded rows input [n][hidden]; *produced = 0 (output
+ * untouched) when the layer has no per-layer input. */
+int det_prefill_ple_inputs(det_model_t* model, det_scratch_t* scratch, uint64_t layer, const uint32_t* ids, uint64_t n,
+                           const int32_t* input_dev, int32_t* out_dev, int32_t* produced);
+/* det_decode_ple_input (det_kernels.rs:1142-1150): the same for one token. */
+int det_decode_ple_input(det_model_t* model, det_scratch_t* scratch, uint32_t token, const int32_t* input_dev,
+                         uint64_t layer, int32_t* output_dev, int32_t* produced);
+/* det_layer_prefill (det_kernels.rs:678-683): xs [n][hidden] at positions
+ * 0..n-1 -> out [n][hidden] (may equal xs). per_layer_input [n][ple_dim] or
+ * NULL. With donor == NULL, `cache` (this layer's handle) receives the new
+ * cache (DetKvCacheData::from_head_slabs); with a donor, attention reads the
+ * donor's cache and `cache` (may be NULL) is left as it was, as the
+ * reference returns no cache. */
+int det_layer_prefill(det_model_t* model, det_scratch_t* scratch, uint64_t layer, const int32_t* xs_dev, uint64_t n,
+                      const int32_t* per_layer_input_dev, const det_kv_t* donor, det_kv_t* cache, int32_t* out_dev);
+/* det_layer_decode (det_kernels.rs:866-875): one row at `position`. Without a
+ * donor the token's K/V row is appended to `cache` (with the sliding-window
+ * trim); with a donor (already updated for this step) attention reads it. */
+int det_layer_decode(det_model_t* model, det_scratch_t* scratch, uint64_t layer, const int32_t* input_dev,
+                     const int32_t* per_layer_input_dev, det_kv_t* cache, const det_kv_t* donor, uint64_t position,
+                     int32_t* output_dev);
+/* det_hidden_to_logits (det_kernels.rs:1217-1225): final norm, the lm_head or
+ * tied embedding projection, optional softcap; logits [vocab]. */
+int det_hidden_to_logits(det_model_t* model, det_scratch_t* scratch, const int32_t* hidden_dev, int32_t* logits_dev);
 
 /* ------------------------------------------------------------------------ */
 /* Sessions: the prefill_layer / decode_transition routines on the GPU        */

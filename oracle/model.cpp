@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <memory>
 #include <optional>
@@ -740,8 +741,13 @@ static std::vector<const LayerCache*> ptrs(const std::vector<LayerCache>& v) {
   return p;
 }
 
+// Observer of each prefill layer: its output rows and the caches so far.
+using PrefillObserver = std::function<void(size_t layer, const std::vector<int32_t>& xs,
+                                           const std::vector<LayerCache>& caches)>;
+
 // pipeline.rs:70-98 (+ prefill_range deterministic_tiles.rs:69-199, prefill_finalize tiles.rs:11-107)
-static std::unique_ptr<orc_session> run_prefill(orc_model* m, const uint32_t* ids, size_t n) {
+static std::unique_ptr<orc_session> run_prefill(orc_model* m, const uint32_t* ids, size_t n,
+                                                const PrefillObserver* observe = nullptr) {
   if (!m->finalized) bail("model is not finalized");
   if (n == 0) bail("transformer layer execution requires at least one activation row");
   auto s = std::make_unique<orc_session>();
@@ -775,6 +781,7 @@ static std::unique_ptr<orc_session> run_prefill(orc_model* m, const uint32_t* id
     lc.num_kv_heads = L.num_kv_heads;
     lc.det = std::move(cache);
     s->caches.push_back(std::move(lc));
+    if (observe) (*observe)(l, xs, s->caches);
   }
   s->final_hidden_commit = commit_rows(xs.data(), n, H);
   s->logits = hidden_to_logits(m, &xs[(n - 1) * H]);
@@ -785,11 +792,15 @@ static std::unique_ptr<orc_session> run_prefill(orc_model* m, const uint32_t* id
 
 struct LayerCapture {
   std::string layer_output;
+  bool has_kv = false;  // the effective-cache commitment was taken after this layer
   std::optional<std::string> kv;
 };
 
 // decode_layer_range native tiles.rs:133-197 + decode_transition_finalize tiles.rs:9-65.
-static std::vector<int32_t> run_decode(orc_session* s, uint32_t token, std::vector<LayerCapture>* per_layer) {
+// per_layer: each layer's output commitment, and the effective caches'
+// commitment after every kv_every-th layer and after the last one.
+static std::vector<int32_t> run_decode(orc_session* s, uint32_t token, std::vector<LayerCapture>* per_layer,
+                                       size_t kv_every = 1) {
   orc_model* m = s->m;
   const size_t H = m->hidden;
   std::vector<int32_t> input = embed(m, &token, 1);
@@ -810,11 +821,17 @@ static std::vector<int32_t> run_decode(orc_session* s, uint32_t token, std::vect
     xs = layer_decode(L, xs, (m->has_ple && L.has_ple) ? &ple : nullptr, cache, donor, s->position);
     updated.push_back(std::move(cache));
     if (per_layer) {
-      // effective_layer_caches (decode_layer_range/mod.rs:497-506)
-      std::vector<const LayerCache*> eff;
-      for (auto& c : updated) eff.push_back(&c);
-      for (size_t j = updated.size(); j < s->caches.size(); ++j) eff.push_back(&s->caches[j]);
-      per_layer->push_back({commit_rows(xs.data(), 1, H), commit_kv(eff)});
+      LayerCapture c;
+      c.layer_output = commit_rows(xs.data(), 1, H);
+      if ((l + 1) % std::max<size_t>(kv_every, 1) == 0 || l + 1 == m->layers.size()) {
+        // effective_layer_caches (decode_layer_range/mod.rs:497-506)
+        std::vector<const LayerCache*> eff;
+        for (auto& uc : updated) eff.push_back(&uc);
+        for (size_t j = updated.size(); j < s->caches.size(); ++j) eff.push_back(&s->caches[j]);
+        c.has_kv = true;
+        c.kv = commit_kv(eff);
+      }
+      per_layer->push_back(std::move(c));
     }
   }
   s->caches = std::move(updated);
@@ -862,6 +879,46 @@ static std::string capture(orc_model* m, const uint32_t* ids, size_t n, size_t s
   h.bytes(ids_json.data(), ids_json.size());
   out += "],\"end_to_end\":{\"generated_token_ids\":" + ids_json + ",\"generated_token_ids_sha256\":\"" + h.hex() + "\"}}";
   return out;
+}
+
+// The commitments the native deterministic routines put into their
+// checkpoints (routines/prefill_range/mod.rs:36-88, prefill_range_finalize/mod.rs:17-73,
+// decode_layer_range/mod.rs:553-664): every prefill layer's output rows, its
+// token ranges of width `prefill_width` and the caches up to it; then per
+// greedy step every layer's output and, at the end of each layer range of
+// width `decode_width`, the effective caches.
+static std::string trace_capture(orc_model* m, const uint32_t* ids, size_t n, size_t steps, size_t prefill_width,
+                                 size_t decode_width) {
+  const size_t H = m->hidden, L = m->layers.size();
+  const size_t pw = std::min(std::max<size_t>(prefill_width ? prefill_width : SIZE_MAX, 1), n);
+  const size_t dw = std::min(std::max<size_t>(decode_width ? decode_width : SIZE_MAX, 1), std::max<size_t>(L, 1));
+  std::string layers_json;
+  PrefillObserver obs = [&](size_t l, const std::vector<int32_t>& xs, const std::vector<LayerCache>& caches) {
+    std::string ranges;
+    for (size_t a = 0; a < n; a += pw) {
+      const size_t b = std::min(n, a + pw);
+      ranges += (a ? ",\"" : "\"") + commit_rows(xs.data() + a * H, b - a, H) + "\"";
+    }
+    layers_json += std::string(l ? "," : "") + "{\"output\":\"" + commit_rows(xs.data(), n, H) + "\",\"ranges\":[" +
+                   ranges + "],\"kv\":" + json_opt(commit_kv(ptrs(caches))) + "}";
+  };
+  std::unique_ptr<orc_session> s = run_prefill(m, ids, n, &obs);
+  std::string out = "{\"prefill\":{\"embedding\":\"" + s->embedding_commit + "\",\"layers\":[" + layers_json +
+                    "],\"final_hidden\":\"" + s->final_hidden_commit + "\",\"logits\":\"" + s->logits_commit +
+                    "\",\"kv\":" + json_opt(commit_kv(ptrs(s->caches))) + "},\"steps\":[";
+  for (size_t i = 0; i < steps; ++i) {
+    const uint32_t tok = uint32_t(argmax_first(s->logits.data(), s->logits.size()));
+    std::vector<LayerCapture> per_layer;
+    run_decode(s.get(), tok, &per_layer, dw);
+    out += std::string(i ? "," : "") + "{\"token\":" + std::to_string(tok) + ",\"layers\":[";
+    for (size_t l = 0; l < per_layer.size(); ++l) {
+      out += std::string(l ? "," : "") + "{\"output\":\"" + per_layer[l].layer_output + "\"";
+      if (per_layer[l].has_kv) out += ",\"kv\":" + json_opt(per_layer[l].kv);
+      out += "}";
+    }
+    out += "],\"logits\":\"" + commit_vector(s->logits.data(), s->logits.size()) + "\"}";
+  }
+  return out + "]}";
 }
 
 // ---------------------------------------------------------------------------
@@ -1117,6 +1174,16 @@ void orc_model_free(orc_model* m) { delete m; }
 int orc_capture(orc_model* m, const uint32_t* prompt, size_t n, size_t steps, char* out, size_t cap) {
   return guarded([&] {
     std::string s = capture(m, prompt, n, steps);
+    if (s.size() + 1 > cap) bail("capture output buffer too small: need " + std::to_string(s.size() + 1));
+    std::memcpy(out, s.c_str(), s.size() + 1);
+  });
+}
+
+int orc_trace_capture(orc_model* m, const uint32_t* prompt, size_t n, size_t steps, size_t prefill_width,
+                      size_t decode_width, char* out, size_t cap) {
+  return guarded([&] {
+    if (!m->finalized) bail("model is not finalized");
+    std::string s = trace_capture(m, prompt, n, steps, prefill_width, decode_width);
     if (s.size() + 1 > cap) bail("capture output buffer too small: need " + std::to_string(s.size() + 1));
     std::memcpy(out, s.c_str(), s.size() + 1);
   });

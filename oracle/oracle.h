@@ -136,6 +136,15 @@ void orc_set_threads(int threads);
 int orc_capture(orc_model* m, const uint32_t* prompt, size_t prompt_len, size_t decode_steps,
                 char* out, size_t out_cap);
 
+// The commitments of the native deterministic routines' checkpoints as JSON:
+// prefill embedding, per layer its output rows, its token ranges of width
+// prefill_width (0 = one range) and the caches up to it; final hidden,
+// logits, caches; then per greedy step the token, every layer's output, the
+// effective caches at the end of each layer range of width decode_width
+// (0 = one range), and the logits.
+int orc_trace_capture(orc_model* m, const uint32_t* prompt, size_t prompt_len, size_t decode_steps,
+                      size_t prefill_width, size_t decode_width, char* out, size_t out_cap);
+
 // Stateful session for timing / incremental checks.
 typedef struct orc_session orc_session;
 int orc_session_prefill(orc_model* m, const uint32_t* prompt, size_t prompt_len,

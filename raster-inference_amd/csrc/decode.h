@@ -92,10 +92,11 @@ void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, ui
                       const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s,
                       uint32_t nseq = 1);
 // x = add_sat(x, rmsnorm(requant(src), w_post)) [* scalar]; normed = rmsnorm(x, w_next);
-// src (wrapping Q32.32 accumulators) is cleared after use.
+// src (wrapping Q32.32 accumulators) is cleared after use. x_out (optional)
+// receives a copy of the new x (row stride H per sequence).
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
-                              uint64_t kpad, hipStream_t s, uint32_t nseq = 1);
+                              uint64_t kpad, hipStream_t s, uint32_t nseq = 1, int32_t* x_out = nullptr);
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s);
 // Whether launch_dec_attention runs the statistics as a separate pass.
 bool dec_attention_split(const AttnDecArgs& a);
@@ -117,6 +118,17 @@ void launch_dec_set_trig(const StepState* st, uint32_t nseq, const RopeTable* ta
 // past k) for the O projection GEMV, and clears acc.
 void launch_dec_acc_limbs(int64_t* acc, uint64_t k, uint64_t ld, uint32_t nseq, int8_t* limbs, uint64_t kpad,
                           hipStream_t s);
+// Up to kMaxRowPtrs device rows gathered into one buffer: row i (width[i]
+// int32 values at src[i]) goes to dst + i * stride. Passed by value as the
+// kernel argument, so no descriptor upload precedes the launch.
+constexpr uint32_t kMaxRowPtrs = 128;
+struct RowPtrs {
+  const int32_t* src[kMaxRowPtrs];
+  uint32_t width[kMaxRowPtrs];
+  uint32_t n;
+  uint32_t stride;
+};
+void launch_gather_row_ptrs(const RowPtrs& g, int32_t* dst, hipStream_t s);
 // dst[i][0..w) = src[i * w ..] for i < n (device array of row pointers).
 void launch_copy_rows(const int32_t* src, uint64_t w, uint64_t n, int32_t* const* dst, hipStream_t s);
 

@@ -105,7 +105,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
                                                            const int32_t* __restrict__ w_post, int has_scalar,
                                                            int32_t scalar, const int32_t* __restrict__ w_next,
                                                            uint64_t H, int64_t eps, int8_t* __restrict__ limbs,
-                                                           uint64_t kpad) {
+                                                           uint64_t kpad, int32_t* __restrict__ x_out) {
   __shared__ int64_t red[NT / 64];
   __shared__ int32_t bc;
   const uint32_t seq = blockIdx.y;
@@ -113,6 +113,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
   x += uint64_t(seq) * H;
   normed += uint64_t(seq) * H;
   limbs += uint64_t(seq) * 4 * kpad;
+  if (x_out) x_out += uint64_t(seq) * H;
   int32_t o[EPT], xv[EPT], wp[EPT], wn[EPT];
   int64_t ss = 0;
 #pragma unroll
@@ -136,6 +137,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
     if (has_scalar) v = mul_sat(v, scalar);
     xv[e] = v;
     if (c < H) x[c] = v;
+    if (x_out && c < H) x_out[c] = v;
     ss = add_sat64(ss, sq_term(c < H ? v : 0));
   }
   const int32_t s2 = blk_rms_scale<NT>(ss, H, eps, red, &bc);
@@ -966,6 +968,15 @@ __global__ void k_copy_rows(const int32_t* __restrict__ src, uint64_t w, int32_t
   }
 }
 
+// Row i of the output (stride g.stride) = g.width[i] int32 values at g.src[i];
+// one workgroup per row.
+__global__ void k_gather_row_ptrs(RowPtrs g, int32_t* __restrict__ dst) {
+  const uint32_t r = blockIdx.x;
+  const int32_t* s = g.src[r];
+  int32_t* d = dst + uint64_t(r) * g.stride;
+  for (uint32_t c = threadIdx.x; c < g.width[r]; c += blockDim.x) d[c] = s[c];
+}
+
 __global__ void k_dec_softcap(int32_t* __restrict__ x, uint64_t n, int32_t cap) {
   const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) x[i] = softcap_act(x[i], cap);
@@ -994,8 +1005,9 @@ void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, ui
 }
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
-                              uint64_t kpad, hipStream_t s, uint32_t nseq) {
-  DET_ROW_DISPATCH(k_dec_residual_norm, src, x, normed, w_post, int(has_scalar), scalar, w_next, H, eps, limbs, kpad);
+                              uint64_t kpad, hipStream_t s, uint32_t nseq, int32_t* x_out) {
+  DET_ROW_DISPATCH(k_dec_residual_norm, src, x, normed, w_post, int(has_scalar), scalar, w_next, H, eps, limbs, kpad,
+                   x_out);
 }
 #undef DET_ROW_DISPATCH
 // Window chunks per attention workgroup: a.rows_mul when set (1, 2 or 4),
@@ -1076,6 +1088,9 @@ void launch_dec_set_step(StepState* st, uint64_t position, uint32_t token, const
                          uint32_t total_pairs, int32_t* trig, hipStream_t s) {
   hipLaunchKernelGGL(k_dec_set_step, dim3(total_pairs ? nblk(total_pairs, 256) : 1), dim3(256), 0, s, st, position,
                      token, tables, ntables, total_pairs, trig);
+}
+void launch_gather_row_ptrs(const RowPtrs& g, int32_t* dst, hipStream_t s) {
+  if (g.n) hipLaunchKernelGGL(k_gather_row_ptrs, dim3(g.n), dim3(256), 0, s, g, dst);
 }
 void launch_dec_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s) {
   hipLaunchKernelGGL(k_dec_softcap, dim3(nblk(n, 256)), dim3(256), 0, s, x, n, cap);

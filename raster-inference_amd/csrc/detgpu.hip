@@ -28,6 +28,7 @@
 #include "decode.h"
 #include "det_arith.h"
 #include "audit.h"
+#include "commit.h"
 #include "kernels.h"
 
 using det::DevMatrix;
@@ -320,44 +321,11 @@ int32_t* upload_vec(det_ctx* ctx, const std::vector<int32_t>& v) {
   return d;
 }
 
-// ---------------------------------------------------------------------------
-// SHA-256 commitments (transformer_kernels.rs:1395-1482)
-// ---------------------------------------------------------------------------
-struct Sha {
-  SHA256_CTX c;
-  Sha() { SHA256_Init(&c); }
-  void put(const void* p, size_t n) { SHA256_Update(&c, p, n); }
-  void u64(uint64_t v) {
-    uint8_t b[8];
-    for (int i = 0; i < 8; ++i) b[i] = uint8_t(v >> (8 * i));
-    put(b, 8);
-  }
-  // int32 values are little-endian on this host: hash the bytes directly.
-  void i32s(const int32_t* v, size_t n) { put(v, n * 4); }
-  void hex(char out[65]) {
-    uint8_t d[32];
-    SHA256_Final(d, &c);
-    static const char* H = "0123456789abcdef";
-    for (int i = 0; i < 32; ++i) { out[2 * i] = H[d[i] >> 4]; out[2 * i + 1] = H[d[i] & 15]; }
-    out[64] = 0;
-  }
-};
-void commit_rows(const int32_t* rows, uint64_t n, uint64_t width, char out[65]) {
-  Sha h;
-  static const char kDom[] = "raster-det-num-act-v1";
-  h.put(kDom, sizeof(kDom) - 1);
-  h.u64(n);
-  for (uint64_t r = 0; r < n; ++r) { h.u64(width); h.i32s(rows + r * width, width); }
-  h.hex(out);
-}
-void commit_vector(const int32_t* v, uint64_t n, char out[65]) {
-  Sha h;
-  static const char kDom[] = "raster-det-num-act-vector-v1";
-  h.put(kDom, sizeof(kDom) - 1);
-  h.u64(n);
-  h.i32s(v, n);
-  h.hex(out);
-}
+// SHA-256 commitments (transformer_kernels.rs:1395-1482) live in commit.cpp.
+using det_commit::commit_rows;
+using det_commit::commit_vector;
+using det_commit::Sha;
+using det_commit::sha_hex;
 
 }  // namespace
 
@@ -804,6 +772,7 @@ struct GKv {
   uint64_t cap = 0, row_w = 0, heads = 0, hd = 0;
   bool ring = false;  // sliding-window cache of capacity == window
   uint64_t start = 0, len = 0;
+  uint64_t total = 0;  // tokens appended so far; token t sits at slot t % cap (ring) or t
 };
 
 }  // namespace
@@ -835,6 +804,9 @@ struct det_session {
   int64_t* am_scratch = nullptr;
   uint32_t* am_out = nullptr;
   uint64_t score_stride = 0;
+  // checkpointed decode: every layer's output row of the last step ([layers][hidden])
+  bool capture_layers = false;
+  int32_t* layer_rows = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
 
@@ -856,9 +828,31 @@ struct det_session {
   }
 };
 
+// A layer's KV cache outside a session (LayerKvCache, shared/model/transformer.rs:278-337),
+// for the layer-level entry points.
+struct det_kv {
+  det_model* m = nullptr;
+  uint64_t layer = 0;
+  GKv c;
+  ~det_kv() {
+    if (c.k) (void)hipFree(c.k);
+    if (c.v) (void)hipFree(c.v);
+  }
+};
+
+// Row buffers reused by the layer-level entry points (DetDecodeScratch,
+// det_kernels.rs:830-864), grown on demand to the largest row count seen.
+struct det_scratch {
+  det_model* m = nullptr;
+  std::unique_ptr<det_session> ws;
+};
+
 namespace {
 
-void session_alloc(det_session* s) {
+// Allocates a session's row buffers for max_tokens rows; with_state adds the
+// per-layer KV caches and the fused decode step's buffers (a workspace for
+// the layer-level entry points has neither).
+void session_alloc(det_session* s, bool with_state = true) {
   det_model* m = s->m;
   const uint64_t T = s->max_tokens, H = m->hidden;
   uint64_t qw = 0, kw = 0, ffw = 0, plew = m->ple_dim;
@@ -883,6 +877,8 @@ void session_alloc(det_session* s) {
   s->logits = s->alloc<int32_t>(m->vocab);
   s->dec_in = s->alloc<int32_t>(H);
   s->kv.assign(m->layers.size(), GKv());
+  if (!with_state) return;
+  if (s->capture_layers) s->layer_rows = s->alloc<int32_t>(m->layers.size() * H);
   if (m->fused_ok) {
     uint64_t fr = 0, nhd = 0, ff = 0;
     for (size_t l = 0; l < m->layers.size(); ++l) {
@@ -932,37 +928,46 @@ void session_alloc(det_session* s) {
   }
 }
 
-// KV commitment (transformer_kernels.rs:1460-1482) over all layers' caches.
-bool commit_kv(det_session* s, const std::vector<const GKv*>& caches, char out[65]) {
+// The logical rows of a cache (oldest to newest) copied to the host as
+// [len][row_w]: at most two contiguous spans of a ring.
+std::vector<int32_t> host_rows(det_ctx* ctx, const GKv& c, int side) {
+  std::vector<int32_t> out(std::max<uint64_t>(c.len * c.row_w, 1));
+  const int32_t* base = side ? c.v : c.k;
+  const uint64_t first = c.ring ? std::min(c.len, c.cap - c.start) : c.len;
+  if (first)
+    HIPC(hipMemcpyAsync(out.data(), base + c.start * c.row_w, first * c.row_w * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (c.len > first)
+    HIPC(hipMemcpyAsync(out.data() + first * c.row_w, base, (c.len - first) * c.row_w * 4, hipMemcpyDeviceToHost,
+                        ctx->stream));
+  return out;
+}
+
+// build_det_kv_cache_commitment (transformer_kernels.rs:1460-1482) over the
+// given layers' caches; false (None) when one of them has no det data.
+bool commit_kv(det_ctx* ctx, const std::vector<const GKv*>& caches, char out[65]) {
   for (const GKv* c : caches)
     if (!c->has) { out[0] = 0; return false; }
-  hipStream_t st = s->m->ctx->stream;
-  HIPC(hipStreamSynchronize(st));
-  Sha h;
-  static const char kDom[] = "raster-det-num-kv-cache-v1";
-  h.put(kDom, sizeof(kDom) - 1);
-  h.u64(caches.size());
-  std::vector<int32_t> buf;
+  std::vector<std::vector<int32_t>> keys, vals;
   for (const GKv* c : caches) {
-    h.u64(c->heads);
-    for (int side = 0; side < 2; ++side) {
-      const char kind = side ? 'v' : 'k';
-      h.put(&kind, 1);
-      h.u64(c->heads);
-      buf.resize(std::max<uint64_t>(c->cap * c->row_w, 1));
-      HIPC(hipMemcpy(buf.data(), side ? c->v : c->k, c->cap * c->row_w * 4, hipMemcpyDeviceToHost));
-      const uint64_t w = std::max<uint64_t>(c->hd, 1);
-      for (uint64_t hh = 0; hh < c->heads; ++hh) {
-        h.u64(c->len);
-        for (uint64_t r = 0; r < c->len; ++r) {
-          const uint64_t phys = c->ring ? (c->start + r) % c->cap : r;
-          h.u64(w);
-          h.i32s(buf.data() + phys * c->row_w + hh * c->hd, c->hd);
-        }
-      }
-    }
+    keys.push_back(host_rows(ctx, *c, 0));
+    vals.push_back(host_rows(ctx, *c, 1));
   }
-  h.hex(out);
+  HIPC(hipStreamSynchronize(ctx->stream));
+  std::vector<det_commit::KvLayerView> views;
+  for (size_t i = 0; i < caches.size(); ++i) {
+    det_commit::KvLayerView v;
+    v.has = true;
+    v.heads = caches[i]->heads;
+    v.hd = caches[i]->hd;
+    v.len = caches[i]->len;
+    const int32_t* k = keys[i].data();
+    const int32_t* vv = vals[i].data();
+    const uint64_t w = caches[i]->row_w;
+    v.row = [k, vv, w](int side, uint64_t r) { return (side ? vv : k) + r * w; };
+    views.push_back(std::move(v));
+  }
+  const std::string h = det_commit::commit_kv(views);
+  std::memcpy(out, h.c_str(), 65);
   return true;
 }
 
@@ -1088,18 +1093,128 @@ void logits_from(det_session* s, const int32_t* hidden_row) {
   s->logits_valid = true;
 }
 
-// Observer of the prefill pass (checkpoint traces). Each callback returns
-// true to stop the pass there (a terminal checkpoint was reached).
-struct PrefillHook {
-  virtual bool after_embedding(det_session* s, uint64_t n) = 0;
-  virtual bool after_layer(det_session* s, uint64_t l, uint64_t n) = 0;
-  virtual ~PrefillHook() = default;
-};
+// Cache bookkeeping after n tokens with canonical slots (token t at t % cap
+// in a ring, t in a linear cache); equals push + trim-front of
+// DetKvCacheData::append_rows (det_tensor.rs:308-337).
+void kv_advance(GKv& c, uint64_t n) {
+  c.len = c.ring ? std::min(n, c.cap) : n;
+  c.start = c.ring ? (n - c.len) % c.cap : 0;
+  c.total = n;
+}
 
-// Returns false when the hook stopped the pass early (the session is then
-// left mid-prefill and must not be used further).
-bool prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, det_prefill_result_t* out,
-             PrefillHook* hook = nullptr) {
+// det_layer_prefill (det_kernels.rs:678-821) on the n activation rows in
+// ws->x, in place. With donor == nullptr the layer's own cache `own` receives
+// the rows its window keeps (DetKvCacheData::from_head_slabs,
+// det_tensor.rs:250-268); with a donor, attention reads the donor's cache and
+// `own` is left untouched (the reference returns no cache).
+void layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const GKv* donor, const int32_t* ple_in) {
+  det_model* m = ws->m;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  const uint64_t H = m->hidden;
+  if (n == 0) bail("transformer layer execution requires at least one activation row");
+  if (n > ws->max_tokens) bail("activation rows exceed the scratch capacity");
+  if (!donor && !own) bail("transformer prefill layer needs its own cache or a donor cache");
+  det::launch_rmsnorm_to(ws->normed, ws->x, n, H, H, L.in_ln, L.eps, st);
+  qkv_block(ws, L, n, 0);
+  const uint64_t kw = L.num_kv_heads * L.head_dim;
+  det::AttnArgs a{};
+  a.q = ws->qb; a.q_ld = L.num_heads * L.head_dim;
+  a.out = ws->attn; a.out_ld = L.num_heads * L.head_dim;
+  a.hd = uint32_t(L.head_dim); a.num_heads = uint32_t(L.num_heads);
+  a.groups = uint32_t(L.num_heads / L.num_kv_heads);
+  a.n_queries = uint32_t(n); a.causal = 1;
+  a.window = L.sliding ? *L.sliding_window : 0; a.causal_offset = 0;
+  if (donor) {
+    const GKv& d = *donor;
+    if (!d.has) bail("deterministic attention requires canonical key cache rows");
+    if (d.row_w != kw) bail("layer cache head count mismatch");
+    a.k = d.k; a.v = d.v; a.kv_ld = d.row_w;
+    a.ring_start = d.start; a.ring_cap = d.ring ? d.cap : 0; a.avail = d.len;
+    if (d.len < n) contract("attention_softmax requires a non-empty logits slice");
+  } else {
+    GKv& c = *own;
+    if (c.row_w != kw) bail("layer cache head count mismatch");
+    // DetKvCacheData::from_head_slabs: keep the last rows past the window.
+    const uint64_t retained = c.ring ? (n > c.cap ? n - c.cap : 0) : 0;
+    const uint64_t kept = n - retained;
+    if (kept > c.cap) bail("KV cache capacity exceeded");
+    // canonical slots: token t at t % cap (ring) or t (linear)
+    for (uint64_t t = retained; t < n;) {
+      const uint64_t slot = c.ring ? t % c.cap : t;
+      const uint64_t span = std::min<uint64_t>(n - t, c.cap - slot);
+      copy_d2d(ctx, c.k + slot * kw, ws->kb + t * kw, span * kw * 4);
+      copy_d2d(ctx, c.v + slot * kw, ws->vb + t * kw, span * kw * 4);
+      t += span;
+    }
+    kv_advance(c, n);
+    c.has = true;
+    a.k = ws->kb; a.v = ws->vb; a.kv_ld = kw; a.ring_start = 0; a.ring_cap = 0; a.avail = n;
+  }
+  if (a.avail > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
+  det::launch_attention(a, st);
+  post_attention(ws, L, n, ple_in);
+}
+
+// det_layer_decode (det_kernels.rs:866-1133) on the activation row in ws->x,
+// in place, with RoPE at `position`. Without a donor the token's K/V row is
+// appended to `own` (DetKvCacheData::append_rows with the sliding-window
+// trim, det_tensor.rs:308-337) and attention reads it; with a donor (already
+// updated for this step) attention reads the donor's cache.
+void layer_decode(det_session* ws, const GLayer& L, uint64_t position, GKv* own, const GKv* donor,
+                  const int32_t* ple_in) {
+  det_model* m = ws->m;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  const uint64_t H = m->hidden;
+  if (!donor && !own) bail("transformer decode layer needs its own cache or a donor cache");
+  det::launch_rmsnorm_to(ws->normed, ws->x, 1, H, H, L.in_ln, L.eps, st);
+  qkv_block(ws, L, 1, position);
+  const uint64_t kw = L.num_kv_heads * L.head_dim;
+  if (!donor) {
+    GKv& c = *own;
+    if (c.row_w != kw) bail("layer cache append head count mismatch");
+    if (!c.ring && c.total >= c.cap) bail("KV cache capacity exceeded");
+    const uint64_t slot = c.ring ? c.total % c.cap : c.total;
+    copy_d2d(ctx, c.k + slot * kw, ws->kb, kw * 4);
+    copy_d2d(ctx, c.v + slot * kw, ws->vb, kw * 4);
+    kv_advance(c, c.total + 1);
+    c.has = true;
+  }
+  const GKv& ac = donor ? *donor : *own;
+  if (!ac.has) bail("deterministic attention requires canonical key cache rows");
+  if (ac.row_w != kw) bail("layer cache head count mismatch");
+  const uint64_t cur = ac.len;
+  const uint64_t key_start = L.sliding ? (cur > *L.sliding_window ? cur - *L.sliding_window : 0) : 0;
+  const uint64_t count = cur > key_start ? cur - key_start : 0;
+  if (count == 0) contract("attention_softmax requires a non-empty logits slice");
+  det::AttnArgs a{};
+  a.q = ws->qb; a.q_ld = L.num_heads * L.head_dim;
+  a.k = ac.k; a.v = ac.v; a.kv_ld = kw;
+  a.ring_start = ac.start; a.ring_cap = ac.ring ? ac.cap : 0;
+  a.out = ws->attn; a.out_ld = L.num_heads * L.head_dim;
+  a.hd = uint32_t(L.head_dim); a.num_heads = uint32_t(L.num_heads);
+  a.groups = uint32_t(L.num_heads / L.num_kv_heads);
+  a.n_queries = 1; a.causal = 0; a.fix_start = key_start; a.fix_count = count;
+  if (count > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
+  det::launch_attention(a, st);
+  post_attention(ws, L, 1, ple_in);
+}
+
+// The layer's own cache in a session (nullptr for a layer that reads a
+// donor's cache) and the donor cache it reads.
+GKv* own_cache(det_session* s, const GLayer& L, uint64_t l) { return L.donor ? nullptr : &s->kv[l]; }
+const GKv* donor_cache(det_session* s, const GLayer& L) { return L.donor ? &s->kv[*L.donor] : nullptr; }
+
+// Embeds n token ids (already in s->ids) into s->x.
+void embed_ids(det_session* s, uint64_t n) {
+  det_model* m = s->m;
+  det::launch_gather_rows(*m->embedding, s->ids, n, 0, m->hidden, m->embed_scale, s->x, m->hidden, m->ctx->stream);
+}
+
+// pipeline::run_prefill_pass_with_mode (runtime/pipeline.rs:55-98): embedding,
+// PLE inputs, every layer's det_layer_prefill, prefill_finalize logits.
+void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, det_prefill_result_t* out) {
   det_model* m = s->m;
   det_ctx* ctx = m->ctx;
   hipStream_t st = ctx->stream;
@@ -1110,7 +1225,7 @@ bool prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
   check_rope(m, n - 1);
   const uint64_t H = m->hidden;
   HIPC(hipMemcpyAsync(s->ids, ids, n * 4, hipMemcpyHostToDevice, st));
-  det::launch_gather_rows(*m->embedding, s->ids, n, 0, H, m->embed_scale, s->x, H, st);
+  embed_ids(s, n);
   std::vector<int32_t> host;
   if (flags & DET_COMMIT_ACTIVATIONS) {
     host.resize(n * H);
@@ -1118,52 +1233,13 @@ bool prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
     HIPC(hipStreamSynchronize(st));
     commit_rows(host.data(), n, H, out->embedding);
   }
-  if (hook && hook->after_embedding(s, n)) return false;
   const uint64_t P = m->ple_dim;
   if (m->has_ple)
     for (uint64_t l = 0; l < m->layers.size(); ++l)
       if (m->layers[l].has_ple) ple_inputs(s, l, s->ids, s->x, n, s->ple_all + l * n * P);
   for (uint64_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
-    // det_layer_prefill (det_kernels.rs:678-821)
-    det::launch_rmsnorm_to(s->normed, s->x, n, H, H, L.in_ln, L.eps, st);
-    qkv_block(s, L, n, 0);
-    const uint64_t kw = L.num_kv_heads * L.head_dim;
-    GKv& c = s->kv[l];
-    det::AttnArgs a{};
-    a.q = s->qb; a.q_ld = L.num_heads * L.head_dim;
-    a.out = s->attn; a.out_ld = L.num_heads * L.head_dim;
-    a.hd = uint32_t(L.head_dim); a.num_heads = uint32_t(L.num_heads);
-    a.groups = uint32_t(L.num_heads / L.num_kv_heads);
-    a.n_queries = uint32_t(n); a.causal = 1;
-    a.window = L.sliding ? *L.sliding_window : 0; a.causal_offset = 0;
-    if (L.donor) {
-      const GKv& d = s->kv[*L.donor];
-      if (!d.has) bail("deterministic attention requires canonical key cache rows");
-      if (d.row_w != kw) bail("layer cache head count mismatch");
-      a.k = d.k; a.v = d.v; a.kv_ld = d.row_w;
-      a.ring_start = d.start; a.ring_cap = d.ring ? d.cap : 0; a.avail = d.len;
-      if (d.len < n) contract("attention_softmax requires a non-empty logits slice");
-    } else {
-      // DetKvCacheData::from_head_slabs: keep the last rows past the window.
-      const uint64_t retained = c.ring ? (n > *L.cache_sliding_window ? n - *L.cache_sliding_window : 0) : 0;
-      const uint64_t kept = n - retained;
-      if (kept > c.cap) bail("KV cache capacity exceeded");
-      // canonical slots: token t at t % cap (ring) or t (linear)
-      for (uint64_t t = retained; t < n;) {
-        const uint64_t slot = c.ring ? t % c.cap : t;
-        const uint64_t span = std::min<uint64_t>(n - t, c.cap - slot);
-        copy_d2d(ctx, c.k + slot * kw, s->kb + t * kw, span * kw * 4);
-        copy_d2d(ctx, c.v + slot * kw, s->vb + t * kw, span * kw * 4);
-        t += span;
-      }
-      c.start = c.ring ? retained % c.cap : 0; c.len = kept; c.has = true;
-      a.k = s->kb; a.v = s->vb; a.kv_ld = kw; a.ring_start = 0; a.ring_cap = 0; a.avail = n;
-    }
-    if (a.avail > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
-    det::launch_attention(a, st);
-    post_attention(s, L, n, (m->has_ple && L.has_ple) ? s->ple_all + l * n * P : nullptr);
-    if (hook && hook->after_layer(s, l, n)) return false;
+    layer_prefill(s, L, n, own_cache(s, L, l), donor_cache(s, L), (m->has_ple && L.has_ple) ? s->ple_all + l * n * P : nullptr);
   }
   if (flags & DET_COMMIT_ACTIVATIONS) {
     host.resize(n * H);
@@ -1180,29 +1256,23 @@ bool prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
     commit_vector(lg.data(), m->vocab, out->logits);
   }
   out->kv[0] = 0;
-  if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
+  if (flags & DET_COMMIT_KV) commit_kv(s->m->ctx, all_caches(s), out->kv);
   out->next_token = ctx->argmax(s->logits, m->vocab);
-  return true;
-}
-
-// Cache bookkeeping after n tokens with canonical slots (token t at t % cap
-// in a ring, t in a linear cache); equals push + trim-front of
-// DetKvCacheData::append_rows (det_tensor.rs:308-337).
-void kv_advance(GKv& c, uint64_t n) {
-  c.len = c.ring ? std::min(n, c.cap) : n;
-  c.start = c.ring ? (n - c.len) % c.cap : 0;
 }
 
 // Observer of a per-op decode step; after_layer returns true to stop the
-// step there (a terminal checkpoint was reached).
+// step there.
 struct LayerHook {
   virtual bool after_layer(det_session* s, uint64_t l) = 0;
   virtual ~LayerHook() = default;
 };
 
-// Returns false when the hook stopped the step early (the session is then
-// left mid-step and must not be used further).
-bool decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t* out, LayerHook* hook) {
+// One decode_step with one kernel sequence per layer. layer_rows (device,
+// [layers][hidden]) receives every layer's output row when non-null. Returns
+// false when the hook stopped the step early (the session is then left
+// mid-step and must not be used further).
+bool decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t* out, LayerHook* hook,
+            int32_t* layer_rows = nullptr) {
   det_model* m = s->m;
   det_ctx* ctx = m->ctx;
   hipStream_t st = ctx->stream;
@@ -1218,38 +1288,8 @@ bool decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
   for (uint64_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
     if (m->has_ple && L.has_ple) ple_inputs(s, l, s->ids, s->dec_in, 1, s->pe);
-    // det_layer_decode (det_kernels.rs:866-1133)
-    det::launch_rmsnorm_to(s->normed, s->x, 1, H, H, L.in_ln, L.eps, st);
-    qkv_block(s, L, 1, pos);
-    const uint64_t kw = L.num_kv_heads * L.head_dim;
-    GKv& own = s->kv[l];
-    if (!L.donor) {
-      // DetKvCacheData::append_rows with sliding-window trim (det_tensor.rs:308-337)
-      if (!own.ring && pos >= own.cap) bail("KV cache capacity exceeded");
-      const uint64_t slot = own.ring ? pos % own.cap : pos;
-      kv_advance(own, pos + 1);
-      copy_d2d(ctx, own.k + slot * kw, s->kb, kw * 4);
-      copy_d2d(ctx, own.v + slot * kw, s->vb, kw * 4);
-      own.has = true;
-    }
-    const GKv& ac = L.donor ? s->kv[*L.donor] : own;
-    if (!ac.has) bail("deterministic attention requires canonical key cache rows");
-    if (ac.row_w != kw) bail("layer cache head count mismatch");
-    const uint64_t cur = ac.len;
-    const uint64_t key_start = L.sliding ? (cur > *L.sliding_window ? cur - *L.sliding_window : 0) : 0;
-    const uint64_t count = cur > key_start ? cur - key_start : 0;
-    if (count == 0) contract("attention_softmax requires a non-empty logits slice");
-    det::AttnArgs a{};
-    a.q = s->qb; a.q_ld = L.num_heads * L.head_dim;
-    a.k = ac.k; a.v = ac.v; a.kv_ld = kw;
-    a.ring_start = ac.start; a.ring_cap = ac.ring ? ac.cap : 0;
-    a.out = s->attn; a.out_ld = L.num_heads * L.head_dim;
-    a.hd = uint32_t(L.head_dim); a.num_heads = uint32_t(L.num_heads);
-    a.groups = uint32_t(L.num_heads / L.num_kv_heads);
-    a.n_queries = 1; a.causal = 0; a.fix_start = key_start; a.fix_count = count;
-    if (count > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
-    det::launch_attention(a, st);
-    post_attention(s, L, 1, (m->has_ple && L.has_ple) ? s->pe : nullptr);
+    layer_decode(s, L, pos, own_cache(s, L, l), donor_cache(s, L), (m->has_ple && L.has_ple) ? s->pe : nullptr);
+    if (layer_rows) copy_d2d(ctx, layer_rows + l * H, s->x, H * 4);
     if (hook && hook->after_layer(s, l)) return false;
   }
   std::vector<int32_t> host;
@@ -1268,7 +1308,7 @@ bool decode(det_session* s, uint32_t token, uint32_t flags, det_decode_result_t*
     commit_vector(lg.data(), m->vocab, out->logits);
   }
   out->kv[0] = 0;
-  if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
+  if (flags & DET_COMMIT_KV) commit_kv(s->m->ctx, all_caches(s), out->kv);
   out->next_token = ctx->argmax(s->logits, m->vocab);
   return true;
 }
@@ -1502,7 +1542,7 @@ void decode_batch(det_session* const* ss, uint64_t n, const uint32_t* tokens, ui
   }
   for (uint64_t i = 0; i < n; ++i) {
     out[i].kv[0] = 0;
-    if (flags & DET_COMMIT_KV) commit_kv(ss[i], all_caches(ss[i]), out[i].kv);
+    if (flags & DET_COMMIT_KV) commit_kv(m->ctx, all_caches(ss[i]), out[i].kv);
     out[i].next_token = next[i];
   }
 }
@@ -1714,7 +1754,7 @@ void decode_batch_fused(det_session* const* ss, uint64_t n, const uint32_t* toke
   }
   for (uint64_t i = 0; i < n; ++i) {
     out[i].kv[0] = 0;
-    if (flags & DET_COMMIT_KV) commit_kv(ss[i], all_caches(ss[i]), out[i].kv);
+    if (flags & DET_COMMIT_KV) commit_kv(m->ctx, all_caches(ss[i]), out[i].kv);
     out[i].next_token = next[i];
   }
 }
@@ -1775,7 +1815,8 @@ void enqueue_fused_step(det_session* s) {
     det::launch_gemv_dec(*L.down, s->limbs_ff, nullptr, s->ff_acc, 0, nullptr, 0, st);
     const int32_t* w_next = l + 1 < m->layers.size() ? m->layers[l + 1].in_ln : m->final_norm;
     det::launch_dec_residual_norm(s->ff_acc, s->x, s->normed, L.post_ff_ln, L.layer_scalar.has_value(),
-                                  L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st);
+                                  L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st, 1,
+                                  s->layer_rows ? s->layer_rows + l * H : nullptr);
   }
   // the vocabulary projection streams best through the 8-wave LDS kernel
   det::launch_gemv_decode(*m->lm_head, s->normed, false, 0, s->logits, st);
@@ -1835,7 +1876,7 @@ void decode_fused(det_session* s, uint32_t token, uint32_t flags, det_decode_res
     commit_vector(lg.data(), m->vocab, out->logits);
   }
   out->kv[0] = 0;
-  if (flags & DET_COMMIT_KV) commit_kv(s, all_caches(s), out->kv);
+  if (flags & DET_COMMIT_KV) commit_kv(s->m->ctx, all_caches(s), out->kv);
   out->next_token = next;
 }
 
@@ -1849,7 +1890,7 @@ std::unique_ptr<det_session> clone_session(const det_session* src) {
   for (size_t l = 0; l < src->kv.size(); ++l) {
     const GKv& a = src->kv[l];
     GKv& b = s->kv[l];
-    b.has = a.has; b.start = a.start; b.len = a.len;
+    b.has = a.has; b.start = a.start; b.len = a.len; b.total = a.total;
     if (a.k) {
       copy_d2d(ctx, b.k, a.k, a.cap * a.row_w * 4);
       copy_d2d(ctx, b.v, a.v, a.cap * a.row_w * 4);
@@ -1875,7 +1916,7 @@ struct FirstStepHook : LayerHook {
     commit_rows(host.data(), 1, m->hidden, out);
     std::vector<const GKv*> eff;
     for (uint64_t j = 0; j < s->kv.size(); ++j) eff.push_back(j <= l ? &s->kv[j] : &original->kv[j]);
-    const bool has = commit_kv(s, eff, kv);
+    const bool has = commit_kv(m->ctx, eff, kv);
     if (!json.empty()) json += ",";
     json += std::string("{\"layer_output\":\"") + out + "\",\"kv\":" + (has ? "\"" + std::string(kv) + "\"" : "null") + "}";
     return false;
@@ -1976,8 +2017,6 @@ std::string json_u32s(const std::vector<uint32_t>& v) {
   return o + "]";
 }
 
-std::string json_hex_or_null(const char* hex, bool has) { return has ? json_str(hex) : "null"; }
-
 std::string json_obj(const std::map<std::string, std::string>& o) {
   std::string s = "{";
   bool first = true;
@@ -1989,16 +2028,23 @@ std::string json_obj(const std::map<std::string, std::string>& o) {
   return s + "}";
 }
 
-std::string sha_hex(const std::string& bytes) {
-  Sha h;
-  h.put(bytes.data(), bytes.size());
-  char out[65];
-  h.hex(out);
-  return out;
+using Fut = std::shared_future<std::string>;
+
+// A commitment future as a payload value: its quoted hex, or null for None ("").
+std::string json_fut(const Fut& f) {
+  const std::string v = f.get();
+  return v.empty() ? "null" : json_str(v);
+}
+std::string json_futs(const std::vector<Fut>& v, size_t n) {
+  std::string o = "[";
+  for (size_t i = 0; i < n; ++i) o += (i ? "," : "") + json_fut(v[i]);
+  return o + "]";
 }
 
 struct TraceCollector {
-  std::vector<std::pair<std::string, std::string>> entries;  // checkpoint, sha256 of its payload
+  // checkpoint name and the builder of its payload; builders run when the
+  // artifact is written, once the commitments they read have been hashed
+  std::vector<std::pair<std::string, std::function<std::string()>>> entries;
   bool has_terminal = false, reached = false;
   std::string terminal_id;
   uint64_t occurrence = 1, seen = 0;
@@ -2028,21 +2074,28 @@ struct TraceCollector {
     return reached;
   }
   // trace_checkpoint_lazy (trace.rs:266-288); layer_token checkpoints are
-  // never committed (trace.rs:451-454), so their payload is not built.
-  template <class F>
-  bool checkpoint(const std::string& name, F&& payload) {
+  // never committed (trace.rs:451-454), so their payload is not built. The
+  // payload builder must own (copy) everything it reads.
+  bool checkpoint(const std::string& name, std::function<std::string()> payload) {
     const bool commit = name.rfind("prefill.layer_token.", 0) != 0 && name.rfind("decode.layer_token.", 0) != 0;
     const bool r = mark(name);
-    if (commit) entries.push_back({name, sha_hex(payload())});
+    if (commit) entries.emplace_back(name, std::move(payload));
     return r;
+  }
+  // {checkpoint: sha256(payload)} for every committed checkpoint, in order
+  std::vector<std::pair<std::string, std::string>> committed() const {
+    std::vector<std::pair<std::string, std::string>> out;
+    for (const auto& e : entries) out.emplace_back(e.first, sha_hex(e.second()));
+    return out;
   }
   // serde_json::to_vec_pretty of the array of single-entry maps
   std::string artifact() const {
-    if (entries.empty()) return "[]";
+    const auto c = committed();
+    if (c.empty()) return "[]";
     std::string o = "[\n";
-    for (size_t i = 0; i < entries.size(); ++i) {
-      o += "  {\n    " + json_str(entries[i].first) + ": " + json_str(entries[i].second) + "\n  }";
-      o += i + 1 < entries.size() ? ",\n" : "\n";
+    for (size_t i = 0; i < c.size(); ++i) {
+      o += "  {\n    " + json_str(c[i].first) + ": " + json_str(c[i].second) + "\n  }";
+      o += i + 1 < c.size() ? ",\n" : "\n";
     }
     return o + "]";
   }
@@ -2050,135 +2103,40 @@ struct TraceCollector {
 
 const char* const kDetMode = "\"deterministic\"";
 
-// prefill.prepare_aux / input.embedding / prefill.range / range_finalize /
-// layer_token marks from the prefill pass
-// (runtime/executors/native.rs:60-263, routines/input_embedding/mod.rs:88-130,
-// routines/prefill_prepare_aux/mod.rs:175-210, routines/prefill_range/mod.rs:36-88,
-// routines/prefill_range_finalize/mod.rs:17-73,
-// routines/prefill_range/native/deterministic_tiles.rs:140-190).
-struct TracePrefill : PrefillHook {
-  TraceCollector& tc;
-  std::string ids_json, ids_sha;
-  uint64_t width;  // prefill token range width (0 = unbounded)
-  std::vector<std::string> completed;
-  std::vector<int32_t> host;
-  TracePrefill(TraceCollector& t, std::string ij, std::string is, uint64_t w)
-      : tc(t), ids_json(std::move(ij)), ids_sha(std::move(is)), width(w) {}
-  bool after_embedding(det_session* s, uint64_t n) override {
-    const uint64_t H = s->m->hidden;
-    host.resize(n * H);
-    HIPC(hipMemcpyAsync(host.data(), s->x, n * H * 4, hipMemcpyDeviceToHost, s->m->ctx->stream));
-    HIPC(hipStreamSynchronize(s->m->ctx->stream));
-    char emb[65];
-    commit_rows(host.data(), n, H, emb);
-    if (tc.checkpoint("input.embedding", [&] {
-          return json_obj({{"det_embedded_prompt_activations_sha256", json_str(emb)},
-                           {"prompt_token_ids", ids_json},
-                           {"prompt_token_ids_sha256", json_str(ids_sha)},
-                           {"raster", "null"}});
-        }))
-      return true;
-    return tc.checkpoint("prefill.prepare_aux", [&] {
-      return json_obj({{"det_embedded_prompt_activations_sha256", json_str(emb)},
-                       {"prompt_token_ids", ids_json},
-                       {"prompt_token_ids_sha256", json_str(ids_sha)}});
-    });
-  }
-  bool after_layer(det_session* s, uint64_t l, uint64_t n) override {
-    const uint64_t H = s->m->hidden;
-    host.resize(n * H);
-    HIPC(hipMemcpyAsync(host.data(), s->x, n * H * 4, hipMemcpyDeviceToHost, s->m->ctx->stream));
-    HIPC(hipStreamSynchronize(s->m->ctx->stream));
-    char all[65];
-    commit_rows(host.data(), n, H, all);
-    completed.push_back(all);
-    // range_bounds (prefill_range/mod.rs:25-34)
-    const uint64_t w = std::min<uint64_t>(std::max<uint64_t>(width ? width : UINT64_MAX, 1), std::max<uint64_t>(n, 1));
-    for (uint64_t a = 0; a < n; a += w) {
-      const uint64_t b = std::min(n, a + w);
-      if (tc.checkpoint("prefill.range", [&] {
-            char rc[65];
-            commit_rows(host.data() + a * H, b - a, H, rc);
-            return json_obj({{"det_range_activations_sha256", json_str(rc)},
-                             {"execution_mode", kDetMode},
-                             {"layer_idx", std::to_string(l)},
-                             {"range_end", std::to_string(b)},
-                             {"range_start", std::to_string(a)},
-                             {"token_count", std::to_string(n)}});
-          }))
-        return true;
-    }
-    if (tc.checkpoint("prefill.range_finalize", [&] {
-          std::vector<const GKv*> caches;
-          for (uint64_t j = 0; j <= l; ++j) caches.push_back(&s->kv[j]);
-          char kv[65];
-          const bool has = commit_kv(s, caches, kv);
-          std::string list = "[";
-          for (size_t i = 0; i < completed.size(); ++i) list += (i ? "," : "") + json_str(completed[i]);
-          list += "]";
-          return json_obj({{"completed_layer_output_det_sha256s", list},
-                           {"det_current_activations_sha256", json_str(all)},
-                           {"det_layer_caches_sha256", json_hex_or_null(kv, has)},
-                           {"execution_mode", kDetMode},
-                           {"next_layer_idx", std::to_string(l + 1)}});
-        }))
-      return true;
-    for (uint64_t t = 0; t < n; ++t)
-      if (tc.mark("prefill.layer_token.layer_" + std::to_string(l) + ".token_" + std::to_string(t))) return true;
-    return false;
-  }
-};
-
-// decode.layer_range checkpoints of one decode step
-// (routines/decode_layer_range/mod.rs:553-664, native/tiles.rs:35-70):
-// after each layer range, the current activation, the effective caches
-// (updated layers, then the untouched ones) and the layer outputs so far.
-struct TraceDecode : LayerHook {
-  TraceCollector& tc;
-  uint32_t token;
-  uint64_t position, layers, width, range_start = 0;
-  std::vector<std::string> completed;
-  std::vector<int32_t> host;
-  TraceDecode(TraceCollector& t, uint32_t tok, uint64_t pos, uint64_t nl, uint64_t w)
-      : tc(t), token(tok), position(pos), layers(nl), width(std::min<uint64_t>(std::max<uint64_t>(w ? w : UINT64_MAX, 1), std::max<uint64_t>(nl, 1))) {}
-  bool after_layer(det_session* s, uint64_t l) override {
-    const uint64_t H = s->m->hidden;
-    host.resize(H);
-    HIPC(hipMemcpyAsync(host.data(), s->x, H * 4, hipMemcpyDeviceToHost, s->m->ctx->stream));
-    HIPC(hipStreamSynchronize(s->m->ctx->stream));
-    char act[65];
-    commit_rows(host.data(), 1, H, act);
-    completed.push_back(act);
-    const uint64_t range_end = std::min(layers, range_start + width);
-    if (l + 1 != range_end) return false;
-    const uint64_t start = range_start;
-    range_start = range_end;
-    return tc.checkpoint("decode.layer_range", [&] {
-      char kv[65];
-      const bool has = commit_kv(s, all_caches(s), kv);
-      std::string list = "[";
-      for (size_t i = 0; i < completed.size(); ++i) list += (i ? "," : "") + json_str(completed[i]);
-      list += "]";
-      return json_obj({{"completed_layer_output_det_sha256s", list},
-                       {"decode_position", std::to_string(position)},
-                       {"decode_token_count", std::to_string(position)},
-                       {"det_current_activation_sha256", json_str(act)},
-                       {"det_layer_caches_sha256", json_hex_or_null(kv, has)},
-                       {"execution_mode", kDetMode},
-                       {"layer_count", std::to_string(layers)},
-                       {"layer_end", std::to_string(range_end)},
-                       {"layer_start", std::to_string(start)},
-                       {"next_token", std::to_string(token)}});
-    });
-  }
-};
-
 // SamplingConfig (shared/api/input.rs:45-50) as serialized into prompt.prepare.
 std::string sampling_json(const det_sampling_t& sp) {
   return std::string("{\"max_new_tokens\":") + (sp.has_max_new_tokens ? std::to_string(sp.max_new_tokens) : "null") +
          ",\"temperature\":" + (sp.has_temperature ? json_f32(sp.temperature) : "null") +
          ",\"top_k\":" + (sp.has_top_k ? std::to_string(sp.top_k) : "null") +
          ",\"top_p\":" + (sp.has_top_p ? json_f32(sp.top_p) : "null") + "}";
+}
+
+// Host buffers of one traced sequence. The hashing pool reads the KV mirror
+// and the row copies while the GPU runs ahead, so the pool is declared last
+// and drains before anything it reads is destroyed.
+struct TraceState {
+  det_session sess;
+  det_commit::KvMirror mirror;
+  int32_t* kv_stage = nullptr;  // device: the step's new K/V rows [own layers x 2][max width]
+  int32_t* host_stage = nullptr;  // pinned: layer rows | logits | K/V rows
+  uint64_t kv_rows = 0, kv_width = 0;
+  std::vector<int> own_layers;
+  std::unique_ptr<det_commit::HashPool> pool;
+  ~TraceState() {
+    pool.reset();  // finishes every queued hash before the buffers go
+    if (kv_stage) (void)hipFree(kv_stage);
+    if (host_stage) (void)hipHostFree(host_stage);
+  }
+};
+
+// build_det_kv_cache_commitment over the mirror: layer j after total[j] tokens.
+Fut commit_mirror(TraceState& ts, std::vector<uint64_t> totals) {
+  const det_commit::KvMirror* mirror = &ts.mirror;
+  return ts.pool->submit([mirror, totals] {
+    std::vector<det_commit::KvLayerView> views;
+    for (size_t j = 0; j < totals.size(); ++j) views.push_back(mirror->view(j, totals[j]));
+    return det_commit::commit_kv(views);
+  });
 }
 
 // Runs the traced sequence; returns true when it paused at the terminal
@@ -2191,33 +2149,145 @@ bool trace_run(det_model* m, const det_trace_request_t* rq, TraceCollector& tc) 
   if (!rq->prompt_token_ids || rq->prompt_token_count == 0)
     bail("transformer layer execution requires at least one activation row");
   const std::vector<uint32_t> ids(rq->prompt_token_ids, rq->prompt_token_ids + rq->prompt_token_count);
-  const uint64_t n = ids.size();
+  const uint64_t n = ids.size(), H = m->hidden, V = m->vocab, nl = m->layers.size();
   const std::string ids_json = json_u32s(ids), ids_sha = sha_hex(ids_json);
   // prompt.prepare (executors/native.rs:68-90): emitted when an authenticated
   // tokenizer source accompanies a deterministic run
-  if (rq->prompt_checkpoint &&
-      tc.checkpoint("prompt.prepare", [&] {
-        return json_obj({{"prompt_text", json_str(rq->prompt_text)},
-                         {"prompt_token_ids", ids_json},
-                         {"prompt_token_ids_sha256", json_str(ids_sha)},
-                         {"sampling", sampling_json(rq->sampling)}});
-      }))
-    return true;
+  if (rq->prompt_checkpoint) {
+    const std::string text = rq->prompt_text, sampling = sampling_json(rq->sampling);
+    if (tc.checkpoint("prompt.prepare", [text, ids_json, ids_sha, sampling] {
+          return json_obj({{"prompt_text", json_str(text)},
+                           {"prompt_token_ids", ids_json},
+                           {"prompt_token_ids_sha256", json_str(ids_sha)},
+                           {"sampling", sampling}});
+        }))
+      return true;
+  }
+  check_ids(m, ids.data(), n);
   const uint64_t max_new = rq->sampling.has_max_new_tokens ? rq->sampling.max_new_tokens : 0;
-  det_session sess;
+  det_ctx* ctx = m->ctx;
+  hipStream_t st = ctx->stream;
+  TraceState ts;
+  det_session& sess = ts.sess;
   sess.m = m;
   sess.max_tokens = n + max_new + 1;
+  sess.capture_layers = true;
   session_alloc(&sess);
-  TracePrefill ph(tc, ids_json, ids_sha, rq->prefill_token_range_width);
-  det_prefill_result_t pr{};
-  if (!prefill(&sess, ids.data(), n, DET_COMMIT_ALL, &pr, &ph)) return true;
-  // prefill.finalize (prefill_finalize/native/tiles.rs:68-94)
-  if (tc.checkpoint("prefill.finalize", [&] {
+  for (uint64_t l = 0; l < nl; ++l) {
+    const GLayer& L = m->layers[l];
+    ts.mirror.add_layer(!L.donor, L.num_kv_heads, L.head_dim, L.cache_sliding_window, sess.max_tokens);
+    if (!L.donor) {
+      ts.own_layers.push_back(int(l));
+      ts.kv_width = std::max(ts.kv_width, L.num_kv_heads * L.head_dim);
+    }
+  }
+  ts.kv_rows = 2 * ts.own_layers.size();
+  HIPC(hipMalloc(&ts.kv_stage, std::max<uint64_t>(ts.kv_rows * ts.kv_width, 1) * 4));
+  HIPC(hipHostMalloc(reinterpret_cast<void**>(&ts.host_stage), (nl * H + V + ts.kv_rows * ts.kv_width + 1) * 4,
+                     hipHostMallocDefault));
+  ts.pool.reset(new det_commit::HashPool(std::max(2u, std::min(16u, std::thread::hardware_concurrency()) - 1)));
+  det_commit::HashPool& pool = *ts.pool;
+  auto copy_rows = [&](const int32_t* dev, uint64_t count) {
+    auto h = std::make_shared<std::vector<int32_t>>(count);
+    if (count) HIPC(hipMemcpyAsync(h->data(), dev, count * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    return h;
+  };
+  auto rows_fut = [&](std::shared_ptr<std::vector<int32_t>> h, uint64_t first, uint64_t count, uint64_t width) {
+    return pool.submit([h, first, count, width] { return commit_rows(h->data() + first * width, count, width); });
+  };
+
+  // input.embedding / prefill.prepare_aux (routines/input_embedding/mod.rs:88-130,
+  // routines/prefill_prepare_aux/mod.rs:175-210)
+  HIPC(hipMemcpyAsync(sess.ids, ids.data(), n * 4, hipMemcpyHostToDevice, st));
+  embed_ids(&sess, n);
+  const Fut emb = rows_fut(copy_rows(sess.x, n * H), 0, n, H);
+  if (tc.checkpoint("input.embedding", [emb, ids_json, ids_sha] {
+        return json_obj({{"det_embedded_prompt_activations_sha256", json_fut(emb)},
+                         {"prompt_token_ids", ids_json},
+                         {"prompt_token_ids_sha256", json_str(ids_sha)},
+                         {"raster", "null"}});
+      }))
+    return true;
+  if (tc.checkpoint("prefill.prepare_aux", [emb, ids_json, ids_sha] {
+        return json_obj({{"det_embedded_prompt_activations_sha256", json_fut(emb)},
+                         {"prompt_token_ids", ids_json},
+                         {"prompt_token_ids_sha256", json_str(ids_sha)}});
+      }))
+    return true;
+  const uint64_t P = m->ple_dim;
+  if (m->has_ple)
+    for (uint64_t l = 0; l < nl; ++l)
+      if (m->layers[l].has_ple) ple_inputs(&sess, l, sess.ids, sess.x, n, sess.ple_all + l * n * P);
+  check_rope(m, n - 1);
+
+  // prefill.range per token range and prefill.range_finalize per layer
+  // (routines/prefill_range/mod.rs:25-88, routines/prefill_range_finalize/mod.rs:17-73,
+  // routines/prefill_range/native/deterministic_tiles.rs:140-190)
+  const uint64_t pw = std::min<uint64_t>(std::max<uint64_t>(rq->prefill_token_range_width ? rq->prefill_token_range_width
+                                                                                          : UINT64_MAX, 1), n);
+  std::vector<Fut> done;  // each layer's output commitment
+  for (uint64_t l = 0; l < nl; ++l) {
+    const GLayer& L = m->layers[l];
+    layer_prefill(&sess, L, n, own_cache(&sess, L, l), donor_cache(&sess, L),
+                  (m->has_ple && L.has_ple) ? sess.ple_all + l * n * P : nullptr);
+    if (!L.donor) {
+      // the rows this layer's cache keeps, from the projection rows (kb / vb
+      // hold all n rows until the next layer's projections)
+      auto& ml = ts.mirror.layer(l);
+      const uint64_t kept = ml.window ? std::min(n, *ml.window) : n, first = n - kept;
+      HIPC(hipMemcpyAsync(ml.k.get() + first * ml.width, sess.kb + first * ml.width, kept * ml.width * 4,
+                          hipMemcpyDeviceToHost, st));
+      HIPC(hipMemcpyAsync(ml.v.get() + first * ml.width, sess.vb + first * ml.width, kept * ml.width * 4,
+                          hipMemcpyDeviceToHost, st));
+    }
+    const auto rows = copy_rows(sess.x, n * H);
+    const Fut all = rows_fut(rows, 0, n, H);
+    done.push_back(all);
+    for (uint64_t a = 0; a < n; a += pw) {
+      const uint64_t b = std::min(n, a + pw);
+      const Fut rc = (a == 0 && b == n) ? all : rows_fut(rows, a, b - a, H);
+      if (tc.checkpoint("prefill.range", [rc, l, a, b, n] {
+            return json_obj({{"det_range_activations_sha256", json_fut(rc)},
+                             {"execution_mode", kDetMode},
+                             {"layer_idx", std::to_string(l)},
+                             {"range_end", std::to_string(b)},
+                             {"range_start", std::to_string(a)},
+                             {"token_count", std::to_string(n)}});
+          }))
+        return true;
+    }
+    const Fut kv = commit_mirror(ts, std::vector<uint64_t>(l + 1, n));
+    const std::vector<Fut> so_far = done;
+    if (tc.checkpoint("prefill.range_finalize", [so_far, all, kv, l] {
+          return json_obj({{"completed_layer_output_det_sha256s", json_futs(so_far, so_far.size())},
+                           {"det_current_activations_sha256", json_fut(all)},
+                           {"det_layer_caches_sha256", json_fut(kv)},
+                           {"execution_mode", kDetMode},
+                           {"next_layer_idx", std::to_string(l + 1)}});
+        }))
+      return true;
+    for (uint64_t t = 0; t < n; ++t)
+      if (tc.mark("prefill.layer_token.layer_" + std::to_string(l) + ".token_" + std::to_string(t))) return true;
+  }
+  // prefill.finalize (prefill_finalize/native/tiles.rs:68-94): the final
+  // hidden states are the last layer's output rows
+  logits_from(&sess, sess.x + (n - 1) * H);
+  sess.position = n;
+  const Fut final_hidden = done.back();
+  const Fut kv_all = commit_mirror(ts, std::vector<uint64_t>(nl, n));
+  uint32_t next = ctx->argmax(sess.logits, V);
+  Fut logits;
+  {
+    const auto lg = copy_rows(sess.logits, V);
+    logits = pool.submit([lg, V] { return commit_vector(lg->data(), V); });
+  }
+  if (tc.checkpoint("prefill.finalize", [n, final_hidden, kv_all, logits] {
         return json_obj({{"decode_position", std::to_string(n)},
                          {"decode_token_count", std::to_string(n)},
-                         {"det_final_hidden_states_sha256", json_str(pr.final_hidden)},
-                         {"det_layer_caches_sha256", json_hex_or_null(pr.kv, pr.kv[0] != 0)},
-                         {"det_prefill_logits_sha256", json_str(pr.logits)}});
+                         {"det_final_hidden_states_sha256", json_fut(final_hidden)},
+                         {"det_layer_caches_sha256", json_fut(kv_all)},
+                         {"det_prefill_logits_sha256", json_fut(logits)}});
       }))
     return true;
   // validate_sampling_config (runtime/pipeline.rs:22-40)
@@ -2226,11 +2296,14 @@ bool trace_run(det_model* m, const det_trace_request_t* rq, TraceCollector& tc) 
          json_f32(rq->sampling.temperature));
   if (rq->sampling.has_top_k) bail("output decode does not support top_k yet, got " + std::to_string(rq->sampling.top_k));
   if (rq->sampling.has_top_p) bail("output decode does not support top_p yet, got " + json_f32(rq->sampling.top_p));
+
   // the output decode loop (executors/native.rs:265-450)
   std::vector<uint32_t> full = ids, gen;
-  std::string logits = pr.logits;
-  uint32_t next = pr.next_token;
-  const uint64_t nl = m->layers.size();
+  const uint64_t dw = std::min<uint64_t>(std::max<uint64_t>(rq->decode_layer_range_width ? rq->decode_layer_range_width
+                                                                                         : UINT64_MAX, 1), std::max<uint64_t>(nl, 1));
+  int32_t* h_layers = ts.host_stage;
+  int32_t* h_logits = h_layers + nl * H;
+  int32_t* h_kv = h_logits + V;
   for (;;) {
     if (gen.size() >= max_new) {
       // output.finalize (output_finalize/mod.rs:18-52)
@@ -2249,11 +2322,12 @@ bool trace_run(det_model* m, const det_trace_request_t* rq, TraceCollector& tc) 
         }
       }
       const std::string full_json = json_u32s(full), gen_json = json_u32s(gen);
-      tc.checkpoint("output.finalize", [&] {
+      const uint64_t count = gen.size();
+      tc.checkpoint("output.finalize", [full_json, gen_json, text, count] {
         return json_obj({{"full_token_ids", full_json},
                          {"full_token_ids_sha256", json_str(sha_hex(full_json))},
                          {"generated_text", json_str(text)},
-                         {"generated_token_count", std::to_string(gen.size())},
+                         {"generated_token_count", std::to_string(count)},
                          {"generated_token_ids", gen_json},
                          {"generated_token_ids_sha256", json_str(sha_hex(gen_json))},
                          {"stop_reason", "\"max_new_tokens\""}});
@@ -2266,10 +2340,10 @@ bool trace_run(det_model* m, const det_trace_request_t* rq, TraceCollector& tc) 
     gen.push_back(t);
     const uint64_t pos = sess.position;
     const std::string full_json = json_u32s(full), gen_json = json_u32s(gen);
-    if (tc.checkpoint("decode.select_token", [&] {
+    if (tc.checkpoint("decode.select_token", [pos, logits, full_json, gen_json, max_new, t] {
           return json_obj({{"decode_position", std::to_string(pos)},
                            {"decode_token_count", std::to_string(pos)},
-                           {"det_current_logits_sha256", json_str(logits)},
+                           {"det_current_logits_sha256", json_fut(logits)},
                            {"full_token_ids", full_json},
                            {"full_token_ids_sha256", json_str(sha_hex(full_json))},
                            {"generated_token_ids", gen_json},
@@ -2278,17 +2352,69 @@ bool trace_run(det_model* m, const det_trace_request_t* rq, TraceCollector& tc) 
                            {"selected_next_token", std::to_string(t)}});
         }))
       return true;
-    // decode.layer_range(s), then decode.transition_finalize
-    // (decode_transition_finalize/mod.rs:67-99)
-    TraceDecode dh(tc, t, pos, nl, rq->decode_layer_range_width);
+    // one decode step; every layer's output row lands in sess.layer_rows
     det_decode_result_t dr{};
-    if (!decode(&sess, t, DET_COMMIT_ALL, &dr, &dh)) return true;
-    logits = dr.logits;
+    if (m->fused_ok) decode_fused(&sess, t, DET_COMMIT_NONE, &dr);
+    else decode(&sess, t, DET_COMMIT_NONE, &dr, nullptr, sess.layer_rows);
     next = dr.next_token;
-    if (tc.checkpoint("decode.transition_finalize", [&] {
+    // the token's K/V rows of every layer with its own cache
+    for (size_t i0 = 0; i0 < ts.own_layers.size(); i0 += det::kMaxRowPtrs / 2) {
+      det::RowPtrs g{};
+      const size_t i1 = std::min(ts.own_layers.size(), i0 + det::kMaxRowPtrs / 2);
+      for (size_t i = i0; i < i1; ++i) {
+        const GKv& c = sess.kv[size_t(ts.own_layers[i])];
+        const uint64_t slot = c.ring ? pos % c.cap : pos;
+        g.src[g.n] = c.k + slot * c.row_w;
+        g.width[g.n++] = uint32_t(c.row_w);
+        g.src[g.n] = c.v + slot * c.row_w;
+        g.width[g.n++] = uint32_t(c.row_w);
+      }
+      g.stride = uint32_t(ts.kv_width);
+      det::launch_gather_row_ptrs(g, ts.kv_stage + 2 * i0 * ts.kv_width, st);
+    }
+    HIPC(hipMemcpyAsync(h_layers, sess.layer_rows, nl * H * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipMemcpyAsync(h_logits, sess.logits, V * 4, hipMemcpyDeviceToHost, st));
+    if (ts.kv_rows) HIPC(hipMemcpyAsync(h_kv, ts.kv_stage, ts.kv_rows * ts.kv_width * 4, hipMemcpyDeviceToHost, st));
+    HIPC(hipStreamSynchronize(st));
+    for (size_t i = 0; i < ts.own_layers.size(); ++i) {
+      auto& ml = ts.mirror.layer(size_t(ts.own_layers[i]));
+      std::memcpy(ml.k.get() + pos * ml.width, h_kv + (2 * i) * ts.kv_width, ml.width * 4);
+      std::memcpy(ml.v.get() + pos * ml.width, h_kv + (2 * i + 1) * ts.kv_width, ml.width * 4);
+    }
+    auto outs = std::make_shared<std::vector<int32_t>>(h_layers, h_layers + nl * H);
+    auto lg = std::make_shared<std::vector<int32_t>>(h_logits, h_logits + V);
+    std::vector<Fut> layer_out;
+    for (uint64_t l = 0; l < nl; ++l) layer_out.push_back(rows_fut(outs, l, 1, H));
+    logits = pool.submit([lg, V] { return commit_vector(lg->data(), V); });
+    // decode.layer_range per layer range (routines/decode_layer_range/mod.rs:553-664,
+    // native/tiles.rs:35-70): the activation after the range, the effective
+    // caches (layers below the range end updated, the rest as before the step)
+    // and the layer outputs so far
+    for (uint64_t a = 0; a < nl; a += dw) {
+      const uint64_t b = std::min(nl, a + dw);
+      std::vector<uint64_t> totals(nl, pos);
+      for (uint64_t j = 0; j < b; ++j) totals[j] = pos + 1;
+      const Fut kv = commit_mirror(ts, totals);
+      const Fut act = layer_out[b - 1];
+      if (tc.checkpoint("decode.layer_range", [layer_out, act, kv, pos, nl, a, b, t] {
+            return json_obj({{"completed_layer_output_det_sha256s", json_futs(layer_out, b)},
+                             {"decode_position", std::to_string(pos)},
+                             {"decode_token_count", std::to_string(pos)},
+                             {"det_current_activation_sha256", json_fut(act)},
+                             {"det_layer_caches_sha256", json_fut(kv)},
+                             {"execution_mode", kDetMode},
+                             {"layer_count", std::to_string(nl)},
+                             {"layer_end", std::to_string(b)},
+                             {"layer_start", std::to_string(a)},
+                             {"next_token", std::to_string(t)}});
+          }))
+        return true;
+    }
+    // decode.transition_finalize (decode_transition_finalize/mod.rs:67-99)
+    if (tc.checkpoint("decode.transition_finalize", [pos, logits, full_json, gen_json] {
           return json_obj({{"decode_position", std::to_string(pos + 1)},
                            {"decode_token_count", std::to_string(pos + 1)},
-                           {"det_current_logits_sha256", json_str(logits)},
+                           {"det_current_logits_sha256", json_fut(logits)},
                            {"full_token_ids", full_json},
                            {"full_token_ids_sha256", json_str(sha_hex(full_json))},
                            {"generated_token_ids", gen_json},
@@ -2296,6 +2422,33 @@ bool trace_run(det_model* m, const det_trace_request_t* rq, TraceCollector& tc) 
         }))
       return true;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Layer-level operators (the reference's det_kernels.rs API) on caller buffers
+// ---------------------------------------------------------------------------
+det_session* scratch_rows(det_scratch* sc, uint64_t rows) {
+  if (!sc->ws || sc->ws->max_tokens < rows) {
+    HIPC(hipStreamSynchronize(sc->m->ctx->stream));
+    auto w = std::make_unique<det_session>();
+    w->m = sc->m;
+    w->max_tokens = std::max<uint64_t>(rows, sc->ws ? 2 * sc->ws->max_tokens : 16);
+    session_alloc(w.get(), false);
+    sc->ws = std::move(w);
+  }
+  return sc->ws.get();
+}
+
+const GLayer& need_layer(det_model* m, uint64_t layer) {
+  if (!m->finalized) bail("model is not finalized");
+  if (layer >= m->layers.size())
+    bail("layer index " + std::to_string(layer) + " out of range for " + std::to_string(m->layers.size()) + " layers");
+  return m->layers[layer];
+}
+
+void need_handles(det_model* m, det_scratch* sc, const det_kv* a, const det_kv* b) {
+  if (!sc || sc->m != m) bail("scratch belongs to another model");
+  if ((a && a->m != m) || (b && b->m != m)) bail("KV cache belongs to another model");
 }
 
 }  // namespace
@@ -2668,7 +2821,11 @@ int det_trace_run(det_model_t* m, const det_trace_request_t* request, char* out,
     if (!m->finalized) bail("model is not finalized");
     p = trace_run(m, request, tc);
   });
-  const std::string art = tc.artifact();
+  // the payloads of the checkpoints so far (also after an error); trace_run
+  // has drained its hashing pool, so every commitment they read is ready
+  std::string art;
+  const int st_art = guarded(m->ctx, [&] { art = tc.artifact(); });
+  if (st == 0) st = st_art;
   if (out_len) *out_len = art.size();
   if (paused) *paused = p ? 1 : 0;
   if (out && out_cap > art.size()) {
@@ -2716,9 +2873,230 @@ int det_audit_trace(det_model_t* m, const det_trace_request_t* request, const ch
     TraceCollector tc;
     if (trace_run(m, request, tc)) bail("challenger replay paused unexpectedly");
     bool d = false;
-    const std::string o = det_audit::outcome_json(c, det_audit::entries_of(tc.entries), &d);
+    const std::string o = det_audit::outcome_json(c, det_audit::entries_of(tc.committed()), &d);
     if (diverged) *diverged = d ? 1 : 0;
     put_text(o, out, out_cap, out_len, "audit outcome");
+  });
+}
+
+// ------------------------------------------------------------------------
+// Layer-level operators
+// ------------------------------------------------------------------------
+int det_scratch_create(det_model_t* m, det_scratch_t** out) {
+  if (!m || !out) {
+    g_error = "model and output pointer are required";
+    return 1;
+  }
+  return guarded(m->ctx, [&] {
+    if (!m->finalized) bail("model is not finalized");
+    auto sc = std::make_unique<det_scratch>();
+    sc->m = m;
+    *out = sc.release();
+  });
+}
+
+void det_scratch_free(det_scratch_t* sc) {
+  if (!sc) return;
+  (void)hipStreamSynchronize(sc->m->ctx->stream);
+  delete sc;
+}
+
+int det_kv_create(det_model_t* m, uint64_t layer, uint64_t max_tokens, det_kv_t** out) {
+  if (!m || !out) {
+    g_error = "model and output pointer are required";
+    return 1;
+  }
+  return guarded(m->ctx, [&] {
+    const GLayer& L = need_layer(m, layer);
+    if (max_tokens == 0) bail("a KV cache needs room for at least one token");
+    auto kv = std::make_unique<det_kv>();
+    kv->m = m;
+    kv->layer = layer;
+    GKv& c = kv->c;
+    c.heads = L.num_kv_heads;
+    c.hd = L.head_dim;
+    c.row_w = L.num_kv_heads * L.head_dim;
+    c.ring = L.cache_sliding_window.has_value();
+    c.cap = c.ring ? std::max<uint64_t>(std::min<uint64_t>(*L.cache_sliding_window, max_tokens), 1) : max_tokens;
+    HIPC(hipMalloc(&c.k, std::max<uint64_t>(c.cap * c.row_w, 1) * 4));
+    HIPC(hipMalloc(&c.v, std::max<uint64_t>(c.cap * c.row_w, 1) * 4));
+    *out = kv.release();
+  });
+}
+
+int det_kv_clone(const det_kv_t* src, det_kv_t** out) {
+  if (!src || !out) {
+    g_error = "source cache and output pointer are required";
+    return 1;
+  }
+  return guarded(src->m->ctx, [&] {
+    auto kv = std::make_unique<det_kv>();
+    kv->m = src->m;
+    kv->layer = src->layer;
+    kv->c = src->c;
+    kv->c.k = kv->c.v = nullptr;
+    const size_t bytes = std::max<uint64_t>(src->c.cap * src->c.row_w, 1) * 4;
+    HIPC(hipMalloc(&kv->c.k, bytes));
+    HIPC(hipMalloc(&kv->c.v, bytes));
+    hipStream_t st = src->m->ctx->stream;
+    HIPC(hipMemcpyAsync(kv->c.k, src->c.k, bytes, hipMemcpyDeviceToDevice, st));
+    HIPC(hipMemcpyAsync(kv->c.v, src->c.v, bytes, hipMemcpyDeviceToDevice, st));
+    *out = kv.release();
+  });
+}
+
+void det_kv_free(det_kv_t* kv) {
+  if (!kv) return;
+  (void)hipStreamSynchronize(kv->m->ctx->stream);
+  delete kv;
+}
+
+int det_kv_info(const det_kv_t* kv, uint64_t* len, uint64_t* heads, uint64_t* head_dim, int32_t* has_det) {
+  if (!kv) {
+    g_error = "cache is required";
+    return 1;
+  }
+  if (len) *len = kv->c.has ? kv->c.len : 0;
+  if (heads) *heads = kv->c.heads;
+  if (head_dim) *head_dim = kv->c.hd;
+  if (has_det) *has_det = kv->c.has ? 1 : 0;
+  return 0;
+}
+
+int det_kv_read_logical(const det_kv_t* kv, int32_t* keys, int32_t* values, uint64_t capacity) {
+  if (!kv) {
+    g_error = "cache is required";
+    return 1;
+  }
+  return guarded(kv->m->ctx, [&] {
+    const GKv& c = kv->c;
+    if (!c.has) bail("cache holds no det data");
+    if (c.len * c.row_w > capacity) bail("output buffers hold fewer values than the cache");
+    const auto k = host_rows(kv->m->ctx, c, 0);
+    const auto v = host_rows(kv->m->ctx, c, 1);
+    HIPC(hipStreamSynchronize(kv->m->ctx->stream));
+    // head-major [heads][len][head_dim], as DetKvCacheData keeps one buffer per head
+    for (uint64_t h = 0; h < c.heads; ++h)
+      for (uint64_t r = 0; r < c.len; ++r) {
+        std::memcpy(keys + (h * c.len + r) * c.hd, k.data() + r * c.row_w + h * c.hd, c.hd * 4);
+        std::memcpy(values + (h * c.len + r) * c.hd, v.data() + r * c.row_w + h * c.hd, c.hd * 4);
+      }
+  });
+}
+
+int det_kv_commitment(const det_kv_t* const* caches, uint64_t n, char out[65], int32_t* is_some) {
+  if (!caches || !out || n == 0 || !caches[0]) {
+    g_error = "at least one cache and an output buffer are required";
+    return 1;
+  }
+  det_model* m = caches[0]->m;
+  return guarded(m->ctx, [&] {
+    std::vector<const GKv*> list;
+    for (uint64_t i = 0; i < n; ++i) {
+      if (!caches[i]) bail("null cache in commitment list");
+      if (caches[i]->m != m) bail("KV cache belongs to another model");
+      list.push_back(&caches[i]->c);
+    }
+    const bool some = commit_kv(m->ctx, list, out);
+    if (!some) out[0] = 0;
+    if (is_some) *is_some = some ? 1 : 0;
+  });
+}
+
+int det_embed_tokens(det_model_t* m, det_scratch_t* sc, const uint32_t* ids, uint64_t n, int32_t* out_dev) {
+  if (!m) {
+    g_error = "model is required";
+    return 1;
+  }
+  return guarded(m->ctx, [&] {
+    if (!m->finalized) bail("model is not finalized");
+    need_handles(m, sc, nullptr, nullptr);
+    if (n == 0) bail("transformer layer execution requires at least one activation row");
+    check_ids(m, ids, n);
+    det_session* ws = scratch_rows(sc, n);
+    HIPC(hipMemcpyAsync(ws->ids, ids, n * 4, hipMemcpyHostToDevice, m->ctx->stream));
+    det::launch_gather_rows(*m->embedding, ws->ids, n, 0, m->hidden, m->embed_scale, out_dev, m->hidden, m->ctx->stream);
+  });
+}
+
+int det_prefill_ple_inputs(det_model_t* m, det_scratch_t* sc, uint64_t layer, const uint32_t* ids, uint64_t n,
+                           const int32_t* input_dev, int32_t* out_dev, int32_t* produced) {
+  if (!m) {
+    g_error = "model is required";
+    return 1;
+  }
+  return guarded(m->ctx, [&] {
+    const GLayer& L = need_layer(m, layer);
+    need_handles(m, sc, nullptr, nullptr);
+    if (produced) *produced = 0;
+    if (!m->has_ple || !L.has_ple) return;
+    if (n == 0) bail("transformer layer execution requires at least one activation row");
+    check_ids(m, ids, n);
+    det_session* ws = scratch_rows(sc, n);
+    HIPC(hipMemcpyAsync(ws->ids, ids, n * 4, hipMemcpyHostToDevice, m->ctx->stream));
+    ple_inputs(ws, layer, ws->ids, input_dev, n, out_dev);
+    if (produced) *produced = 1;
+  });
+}
+
+int det_decode_ple_input(det_model_t* m, det_scratch_t* sc, uint32_t token, const int32_t* input_dev, uint64_t layer,
+                         int32_t* output_dev, int32_t* produced) {
+  return det_prefill_ple_inputs(m, sc, layer, &token, 1, input_dev, output_dev, produced);
+}
+
+int det_layer_prefill(det_model_t* m, det_scratch_t* sc, uint64_t layer, const int32_t* xs_dev, uint64_t n,
+                      const int32_t* per_layer_input_dev, const det_kv_t* donor, det_kv_t* cache, int32_t* out_dev) {
+  if (!m) {
+    g_error = "model is required";
+    return 1;
+  }
+  return guarded(m->ctx, [&] {
+    const GLayer& L = need_layer(m, layer);
+    need_handles(m, sc, donor, cache);
+    if (!donor && !cache) bail("transformer prefill layer needs its own cache or a donor cache");
+    if (cache && cache->layer != layer) bail("KV cache belongs to another layer");
+    if (n == 0) bail("transformer layer execution requires at least one activation row");
+    check_rope(m, n - 1);
+    det_session* ws = scratch_rows(sc, n);
+    copy_d2d(m->ctx, ws->x, xs_dev, n * m->hidden * 4);
+    layer_prefill(ws, L, n, donor ? nullptr : &cache->c, donor ? &donor->c : nullptr, per_layer_input_dev);
+    copy_d2d(m->ctx, out_dev, ws->x, n * m->hidden * 4);
+  });
+}
+
+int det_layer_decode(det_model_t* m, det_scratch_t* sc, uint64_t layer, const int32_t* input_dev,
+                     const int32_t* per_layer_input_dev, det_kv_t* cache, const det_kv_t* donor, uint64_t position,
+                     int32_t* output_dev) {
+  if (!m) {
+    g_error = "model is required";
+    return 1;
+  }
+  return guarded(m->ctx, [&] {
+    const GLayer& L = need_layer(m, layer);
+    need_handles(m, sc, donor, cache);
+    if (!donor && !cache) bail("transformer decode layer needs its own cache or a donor cache");
+    if (cache && cache->layer != layer) bail("KV cache belongs to another layer");
+    check_rope(m, position);
+    det_session* ws = scratch_rows(sc, 1);
+    copy_d2d(m->ctx, ws->x, input_dev, m->hidden * 4);
+    layer_decode(ws, L, position, donor ? nullptr : &cache->c, donor ? &donor->c : nullptr, per_layer_input_dev);
+    copy_d2d(m->ctx, output_dev, ws->x, m->hidden * 4);
+  });
+}
+
+int det_hidden_to_logits(det_model_t* m, det_scratch_t* sc, const int32_t* hidden_dev, int32_t* logits_dev) {
+  if (!m) {
+    g_error = "model is required";
+    return 1;
+  }
+  return guarded(m->ctx, [&] {
+    if (!m->finalized) bail("model is not finalized");
+    need_handles(m, sc, nullptr, nullptr);
+    det_session* ws = scratch_rows(sc, 1);
+    hipStream_t st = m->ctx->stream;
+    det::launch_rmsnorm_to(ws->normed, hidden_dev, 1, m->hidden, m->hidden, m->final_norm, m->eps, st);
+    linear(m->ctx, *m->lm_head, ws->normed, 1, logits_dev);
+    if (m->softcap) det::launch_softcap(logits_dev, m->vocab, *m->softcap, st);
   });
 }
 

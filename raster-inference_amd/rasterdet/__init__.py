@@ -287,6 +287,20 @@ def lib() -> C.CDLL:
         "det_audit_trace": (C.c_int, [P, C.POINTER(TraceRequest), C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t,
                                       C.POINTER(C.c_size_t), C.POINTER(C.c_int32)]),
         "det_synthetic_int8": (C.c_int, [u64, u64, u64, C.c_int32, P, P]),
+        "det_scratch_create": (C.c_int, [P, C.POINTER(P)]),
+        "det_scratch_free": (None, [P]),
+        "det_kv_create": (C.c_int, [P, u64, u64, C.POINTER(P)]),
+        "det_kv_clone": (C.c_int, [P, C.POINTER(P)]),
+        "det_kv_free": (None, [P]),
+        "det_kv_info": (C.c_int, [P, C.POINTER(u64), C.POINTER(u64), C.POINTER(u64), C.POINTER(C.c_int32)]),
+        "det_kv_read_logical": (C.c_int, [P, P, P, u64]),
+        "det_kv_commitment": (C.c_int, [P, u64, C.c_char_p, C.POINTER(C.c_int32)]),
+        "det_embed_tokens": (C.c_int, [P, P, P, u64, P]),
+        "det_prefill_ple_inputs": (C.c_int, [P, P, u64, P, u64, P, P, C.POINTER(C.c_int32)]),
+        "det_decode_ple_input": (C.c_int, [P, P, C.c_uint32, P, u64, P, C.POINTER(C.c_int32)]),
+        "det_layer_prefill": (C.c_int, [P, P, u64, P, u64, P, P, P, P]),
+        "det_layer_decode": (C.c_int, [P, P, u64, P, P, P, P, u64, P]),
+        "det_hidden_to_logits": (C.c_int, [P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -340,7 +354,7 @@ class Context:
 
     def close(self) -> None:
         if getattr(self, "handle", None):
-            order = {"Session": 0, "Model": 1, "Matrix": 2, "DeviceBuffer": 3, "Event": 4}
+            order = {"Session": 0, "KvCache": 0, "Scratch": 0, "Model": 1, "Matrix": 2, "DeviceBuffer": 3, "Event": 4}
             for child in sorted(list(getattr(self, "_children", ())), key=lambda c: order.get(type(c).__name__, 5)):
                 child._release()
             self.lib.det_ctx_destroy(self.handle)
@@ -597,7 +611,11 @@ class Model:
         req, _keep, errors = self._trace_request(prompt_text, prompt_token_ids, max_new_tokens, temperature, top_k,
                                                  top_p, detokenize, prompt_checkpoint, terminal_checkpoint,
                                                  prefill_token_range_width, decode_layer_range_width)
-        cap = 1 << 16
+        # each committed checkpoint is one line of about 100 bytes
+        n_ids, layers, new = _keep[0].size, int(self.cfg.num_hidden_layers), max_new_tokens or 0
+        pw, dw = max(prefill_token_range_width or n_ids, 1), max(decode_layer_range_width or layers, 1)
+        entries = 4 + layers * (-(-n_ids // pw) + 1) + new * (2 + -(-layers // dw)) + 1
+        cap = entries * 128 + 4096
         while True:
             buf = C.create_string_buffer(cap)
             n = C.c_size_t()
@@ -698,6 +716,127 @@ class Session:
             self._release()
         except Exception:
             pass
+def _dptr(buf) -> C.c_void_p:
+    return C.c_void_p(buf.ptr) if buf is not None else None
+
+
+class Scratch:
+    """det_scratch_t: row buffers of the layer-level operators (DetDecodeScratch)."""
+
+    def __init__(self, model: "Model"):
+        self.model, self.ctx = model, model.ctx
+        h = C.c_void_p()
+        self.ctx.check(self.ctx.lib.det_scratch_create(model.handle, C.byref(h)))
+        self.handle = h
+        self.ctx._adopt(self)
+
+    def _release(self) -> None:
+        if self.handle and self.ctx.handle:
+            self.ctx.lib.det_scratch_free(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self._release()
+        except Exception:
+            pass
+
+
+class KvCache:
+    """det_kv_t: one layer's LayerKvCache on the device."""
+
+    def __init__(self, model: "Model", layer: int, max_tokens: int, _handle=None):
+        self.model, self.ctx, self.layer = model, model.ctx, layer
+        if _handle is None:
+            h = C.c_void_p()
+            self.ctx.check(self.ctx.lib.det_kv_create(model.handle, layer, max_tokens, C.byref(h)))
+            _handle = h
+        self.handle = _handle
+        self.ctx._adopt(self)
+
+    def info(self) -> tuple[int, int, int, bool]:
+        """(rows held, heads, head_dim, has det data)."""
+        n, h, d, has = C.c_uint64(), C.c_uint64(), C.c_uint64(), C.c_int32()
+        self.ctx.check(self.ctx.lib.det_kv_info(self.handle, C.byref(n), C.byref(h), C.byref(d), C.byref(has)))
+        return n.value, h.value, d.value, bool(has.value)
+
+    def read_logical(self) -> tuple[np.ndarray, np.ndarray]:
+        """Keys and values [heads][len][head_dim], oldest row first."""
+        n, h, d, _ = self.info()
+        k = np.empty((h, n, d), dtype=np.int32)
+        v = np.empty((h, n, d), dtype=np.int32)
+        self.ctx.check(self.ctx.lib.det_kv_read_logical(self.handle, _ptr(k), _ptr(v), k.size))
+        return k, v
+
+    def clone(self) -> "KvCache":
+        h = C.c_void_p()
+        self.ctx.check(self.ctx.lib.det_kv_clone(self.handle, C.byref(h)))
+        return KvCache(self.model, self.layer, 0, _handle=h)
+
+    def _release(self) -> None:
+        if self.handle and self.ctx.handle:
+            self.ctx.lib.det_kv_free(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self._release()
+        except Exception:
+            pass
+
+
+def kv_commitment(caches) -> str | None:
+    """build_det_kv_cache_commitment over the caches in order (None if one lacks det data)."""
+    caches = list(caches)
+    ctx = caches[0].ctx
+    handles = (C.c_void_p * len(caches))(*[c.handle for c in caches])
+    out = C.create_string_buffer(65)
+    some = C.c_int32()
+    ctx.check(ctx.lib.det_kv_commitment(C.cast(handles, C.c_void_p), len(caches), out, C.byref(some)))
+    return out.value.decode() if some.value else None
+
+
+class LayerOps:
+    """The layer-level operators (det_kernels.rs API) of one model on device buffers."""
+
+    def __init__(self, model: "Model"):
+        self.model, self.ctx = model, model.ctx
+        self.scratch = Scratch(model)
+
+    def embed(self, ids, out) -> None:
+        a = np.asarray(ids, dtype=np.uint32)
+        self.ctx.check(self.ctx.lib.det_embed_tokens(self.model.handle, self.scratch.handle, _ptr(a), a.size,
+                                                     _dptr(out)))
+
+    def prefill_ple_inputs(self, layer: int, ids, inp, out) -> bool:
+        a = np.asarray(ids, dtype=np.uint32)
+        produced = C.c_int32()
+        self.ctx.check(self.ctx.lib.det_prefill_ple_inputs(self.model.handle, self.scratch.handle, layer, _ptr(a),
+                                                           a.size, _dptr(inp), _dptr(out), C.byref(produced)))
+        return bool(produced.value)
+
+    def decode_ple_input(self, token: int, inp, layer: int, out) -> bool:
+        produced = C.c_int32()
+        self.ctx.check(self.ctx.lib.det_decode_ple_input(self.model.handle, self.scratch.handle, int(token),
+                                                         _dptr(inp), layer, _dptr(out), C.byref(produced)))
+        return bool(produced.value)
+
+    def layer_prefill(self, layer: int, xs, n: int, ple, donor: KvCache | None, cache: KvCache | None, out) -> None:
+        self.ctx.check(self.ctx.lib.det_layer_prefill(self.model.handle, self.scratch.handle, layer, _dptr(xs), n,
+                                                      _dptr(ple), donor.handle if donor else None,
+                                                      cache.handle if cache else None, _dptr(out)))
+
+    def layer_decode(self, layer: int, inp, ple, cache: KvCache | None, donor: KvCache | None, position: int,
+                     out) -> None:
+        self.ctx.check(self.ctx.lib.det_layer_decode(self.model.handle, self.scratch.handle, layer, _dptr(inp),
+                                                     _dptr(ple), cache.handle if cache else None,
+                                                     donor.handle if donor else None, position, _dptr(out)))
+
+    def hidden_to_logits(self, hidden, out) -> None:
+        self.ctx.check(self.ctx.lib.det_hidden_to_logits(self.model.handle, self.scratch.handle, _dptr(hidden),
+                                                         _dptr(out)))
+
+
 def decode_batch(sessions, tokens, flags: int = DET_COMMIT_ALL) -> list:
     """One decode step for each session (same model) in shared launches;
     results[i] is bit-identical to sessions[i].decode(tokens[i], flags)."""

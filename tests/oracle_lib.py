@@ -180,6 +180,8 @@ def lib() -> C.CDLL:
             ("orc_model_free", None, [P]),
             ("orc_set_threads", None, [C.c_int]),
             ("orc_capture", C.c_int, [P, P, C.c_size_t, C.c_size_t, C.c_char_p, C.c_size_t]),
+            ("orc_trace_capture", C.c_int, [P, P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, C.c_char_p,
+                                            C.c_size_t]),
             ("orc_session_prefill", C.c_int, [P, P, C.c_size_t, C.POINTER(P), P]),
             ("orc_session_decode", C.c_int, [P, C.c_uint32, P, P]),
             ("orc_session_free", None, [P]),
@@ -237,6 +239,18 @@ class OracleModel:
         cap = 1 << 20
         buf = C.create_string_buffer(cap + decode_steps * 512)
         check(lib().orc_capture(self.handle, ptr(ids), ids.size, decode_steps, buf, len(buf)))
+        return json.loads(buf.value.decode())
+
+    def trace_capture(self, prompt: list[int], decode_steps: int, prefill_width: int = 0,
+                      decode_width: int = 0) -> dict:
+        """Commitments of the routines' checkpoints (orc_trace_capture)."""
+        ids = np.asarray(prompt, dtype=np.uint32)
+        layers = int(self.config["num_hidden_layers"])
+        n_ranges = -(-ids.size // max(prefill_width or ids.size, 1))
+        cap = (1 << 16) + layers * (200 + 70 * n_ranges) + decode_steps * (400 + 200 * layers)
+        buf = C.create_string_buffer(cap)
+        check(lib().orc_trace_capture(self.handle, ptr(ids), ids.size, decode_steps, prefill_width, decode_width, buf,
+                                      len(buf)))
         return json.loads(buf.value.decode())
 
     def session(self, prompt: list[int]) -> "OracleSession":

@@ -20,7 +20,9 @@ def test_header_declares_the_boundary():
     names = declared_functions()
     for required in ["det_ctx_create", "det_matrix_upload", "det_linear", "det_linear_slab", "det_rms_norm",
                      "det_rope", "det_attention_causal", "det_model_load_detwgt", "det_session_prefill",
-                     "det_session_decode", "det_capture"]:
+                     "det_session_decode", "det_capture", "det_layer_prefill", "det_layer_decode",
+                     "det_decode_ple_input", "det_prefill_ple_inputs", "det_hidden_to_logits", "det_embed_tokens",
+                     "det_kv_create", "det_kv_read_logical", "det_kv_commitment", "det_scratch_create"]:
         assert required in names
 
 

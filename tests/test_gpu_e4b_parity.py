@@ -182,3 +182,54 @@ def test_e4b_42_layers_prompt_512_capture_matches_oracle(e4b_full):
     assert got["first_step_layers"] == exp["first_step_layers"]
     assert got["decode_steps"] == exp["decode_steps"]
     assert got["end_to_end"] == exp["end_to_end"]
+
+
+def test_e4b_42_layers_checkpoint_trace_matches_oracle(e4b_full):
+    # the claimer's trace (det_trace_run: fused decode with every layer's
+    # output captured, KV commitments hashed on the host pool from the
+    # append-only mirror) equals the payloads built from the oracle's
+    # checkpoint commitments, entry for entry
+    import trace_builder
+
+    om, gm = e4b_full
+    prompt = np.random.default_rng(77).integers(0, 262144, size=512).tolist()
+    steps = 8
+    text = lambda ids: ",".join(map(str, ids))  # noqa: E731
+    t0 = time.time()
+    got, paused = gm.trace("e4b prompt", prompt, max_new_tokens=steps, detokenize=text)
+    print(f"[e4b] GPU trace {time.time() - t0:.1f}s", flush=True)
+    t0 = time.time()
+    cap = om.trace_capture(prompt, steps)
+    print(f"[e4b] oracle trace capture {time.time() - t0:.1f}s", flush=True)
+    gen = [s["token"] for s in cap["steps"]]
+    exp = trace_builder.expected_trace(cap, "e4b prompt", prompt, steps, text(gen))
+    import json
+    assert not paused
+    assert [next(iter(e.items())) for e in json.loads(got)] == exp
+
+
+def test_e4b_42_layers_ragged_16_batch_matches_solo(e4b_full):
+    # config 5: 16 sequences with seeded prompt lengths in [32, 2048] decoded
+    # in shared batched steps; each sequence's activation and logits
+    # commitments every step, and its KV commitment at steps 0, 7 and 15,
+    # equal its solo decode (whose commitments are the oracle's, above)
+    _, gm = e4b_full
+    rng = np.random.default_rng(5)
+    lens = rng.integers(32, 2049, size=16)
+    prompts = [rng.integers(0, 262144, size=int(k)).tolist() for k in lens]
+    steps = 16
+    t0 = time.time()
+    batch = [gm.session(int(k) + steps + 1) for k in lens]
+    toks = [s.prefill(p, rd.DET_COMMIT_NONE).next_token for s, p in zip(batch, prompts)]
+    solo = [s.clone() for s in batch]
+    tok_s = list(toks)
+    print(f"[ragged16] prefilled {int(lens.sum())} tokens in {time.time() - t0:.1f}s", flush=True)
+    for step in range(steps):
+        flags = rd.DET_COMMIT_ALL if step in (0, 7, 15) else rd.DET_COMMIT_ACTIVATIONS
+        res = rd.decode_batch(batch, toks, flags)
+        for i, r in enumerate(res):
+            e = solo[i].decode(tok_s[i], flags)
+            assert (r.activation, r.logits, r.kv, r.next_token) == (e.activation, e.logits, e.kv, e.next_token), \
+                (step, i, int(lens[i]))
+            toks[i], tok_s[i] = r.next_token, e.next_token
+    print(f"[ragged16] {steps} batched steps checked against solo in {time.time() - t0:.1f}s", flush=True)

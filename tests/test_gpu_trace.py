@@ -108,3 +108,59 @@ def test_unsupported_sampling_fails_after_prefill_with_partial_trace(model, deto
     # prompt.prepare carries the sampling config, so only it differs
     assert [n for n, _ in got] == [n for n, _ in full[:12]]
     assert got[1:] == full[1:12] and got[0] != full[0]
+
+
+# ---------------------------------------------------------------------------
+# traces against the oracle's checkpoint commitments (tests/trace_builder.py
+# restates the payload builders; it reproduces both golden traces on the CPU)
+# ---------------------------------------------------------------------------
+def id_text(ids):
+    return ",".join(map(str, ids))
+
+
+@pytest.mark.parametrize("pw,dw", [(5, 3), (1, 1), (7, 2)])
+def test_per_op_trace_with_range_widths_matches_oracle(model, detokenize, pw, dw):
+    import oracle_lib
+    import trace_builder
+
+    cfg, blob = fixtures.tiny_gemma_dev()
+    om = oracle_lib.OracleModel(cfg).load_detwgt(blob).finalize()
+    ids = PROMPT["prompt_token_ids"]
+    cap = om.trace_capture(ids, 3, prefill_width=pw, decode_width=dw)
+    gen = [s["token"] for s in cap["steps"]]
+    exp = trace_builder.expected_trace(cap, PROMPT["prompt_text"], ids, 3, detokenize(gen), pw, dw)
+    got, paused = run(model, detokenize, max_new_tokens=3, prefill_token_range_width=pw, decode_layer_range_width=dw)
+    assert not paused
+    assert entries(got) == exp
+
+
+@pytest.fixture(scope="module")
+def e4b_two_layer():
+    import oracle_lib
+    from rasterdet import synthetic
+
+    c = rd.Context(0)
+    cfg = synthetic.e4b_config(layers=2, vocab=4096, sliding_window=8)
+    om, gm = fixtures.load_both(cfg, synthetic.synthetic_model_fast(cfg, seed=31, scale_max=256), c,
+                                threads=oracle_lib.cpu_count())
+    yield om, gm
+    del om, gm
+    c.close()
+
+
+@pytest.mark.parametrize("pw,dw", [(0, 0), (4, 1), (7, 2)])
+def test_fused_decode_trace_matches_oracle(e4b_two_layer, pw, dw):
+    # the fused, graph-captured step with every layer's output row captured and
+    # the KV commitments hashed on the host pool from the append-only mirror
+    import trace_builder
+
+    om, gm = e4b_two_layer
+    ids = list(range(40, 61))  # 21 tokens: the sliding ring (window 8) wraps
+    steps = 6
+    cap = om.trace_capture(ids, steps, prefill_width=pw, decode_width=dw)
+    gen = [s["token"] for s in cap["steps"]]
+    exp = trace_builder.expected_trace(cap, "e4b two-layer prompt", ids, steps, id_text(gen), pw, dw)
+    got, paused = gm.trace("e4b two-layer prompt", ids, max_new_tokens=steps, detokenize=id_text,
+                           prefill_token_range_width=pw, decode_layer_range_width=dw)
+    assert not paused
+    assert entries(got) == exp

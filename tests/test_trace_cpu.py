@@ -95,3 +95,36 @@ def test_oracle_commitments_reproduce_golden_entries():
     assert digest({"full_token_ids": full2, "full_token_ids_sha256": digest(full2), "generated_token_ids": gen2,
                    "generated_token_ids_sha256": digest(gen2), "generated_text": "", "generated_token_count": 2,
                    "stop_reason": "max_new_tokens"}) == g["output.finalize"][0][1]
+
+
+def test_trace_builder_over_oracle_reproduces_both_golden_traces():
+    # every entry of native-det-full.json (and its terminal prefix) from the
+    # restated payload builders over the oracle's checkpoint commitments
+    import trace_builder
+
+    cfg, blob = fixtures.tiny_gemma_dev()
+    om = oracle_lib.OracleModel(cfg).load_detwgt(blob).finalize()
+    ids = PROMPT["prompt_token_ids"]
+    cap = om.trace_capture(ids, 2)
+    # both generated ids are <bos>, which decodes (special tokens skipped) to ""
+    exp = trace_builder.expected_trace(cap, PROMPT["prompt_text"], ids, 2, "")
+    assert exp == golden("native-det-full")
+    assert exp[:12] == golden("native-det-terminal")
+
+
+def test_trace_capture_range_widths_agree_with_the_single_range():
+    import trace_builder
+
+    cfg, blob = fixtures.tiny_gemma_dev()
+    om = oracle_lib.OracleModel(cfg).load_detwgt(blob).finalize()
+    ids = PROMPT["prompt_token_ids"]
+    whole = om.trace_capture(ids, 2)
+    split = om.trace_capture(ids, 2, prefill_width=5, decode_width=3)
+    assert [len(l["ranges"]) for l in split["prefill"]["layers"]] == [4] * 4
+    for a, b in zip(whole["prefill"]["layers"], split["prefill"]["layers"]):
+        assert (a["output"], a["kv"]) == (b["output"], b["kv"])
+    # the effective caches after the last layer are the fully updated caches
+    assert whole["steps"][0]["layers"][-1]["kv"] == split["steps"][0]["layers"][-1]["kv"]
+    assert "kv" in split["steps"][0]["layers"][2] and "kv" not in split["steps"][0]["layers"][1]
+    names = [n for n, _ in trace_builder.expected_trace(split, PROMPT["prompt_text"], ids, 2, "", 5, 3)]
+    assert names.count("prefill.range") == 16 and names.count("decode.layer_range") == 4
