@@ -111,6 +111,14 @@ int det_attention_causal(det_ctx_t* ctx, const int32_t* q_dev, const int32_t* k_
                          uint64_t head_dim, uint64_t window, int32_t* out_dev);
 /* argmax_first (det_num/ops.rs:463-478); result written to *index (host). */
 int det_argmax_first(det_ctx_t* ctx, const int32_t* x_dev, uint64_t n, uint32_t* index);
+/* No counterpart in the reference: det_argmax_first for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops). It allocates
+ * and frees nothing, does not synchronize, and writes the index to the device
+ * word *index_dev. Its partial results live in a fixed per-GPU array sized for
+ * n <= 16777216 (larger n is rejected, status 1). All calls on one GPU share
+ * that array: calls that overlap on one GPU (other streams, other contexts)
+ * race and must be ordered by the caller. */
+int det_argmax_first_noalloc(det_ctx_t* ctx, const int32_t* x_dev, uint64_t n, uint32_t* index_dev);
 /* Elementwise saturating ops (det_kernels.rs:252-282, det_num/ops.rs:33-47, 377-403). */
 #define DET_EW_ADD 0      /* x = add_sat(x, y) */
 #define DET_EW_GELU_MUL 1 /* x = mul_sat(gelu_pytorch_tanh(x), y) */

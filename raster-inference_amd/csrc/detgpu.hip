@@ -16,6 +16,7 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <numeric>
 #include <optional>
 #include <stdexcept>
@@ -53,6 +54,7 @@ thread_local std::string g_error;  // errors before a context exists
 struct det_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
+  int64_t* noalloc_parts = nullptr;  // this device's address of the allocation-free argmax scratch
   std::string last_error;
   int8_t* limbs = nullptr;  // activation limb scratch for the int8 GEMV
   size_t limbs_bytes = 0;
@@ -2454,6 +2456,36 @@ void need_handles(det_model* m, det_scratch* sc, const det_kv* a, const det_kv* 
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Allocation-free argmax scratch: one int64 key per 1024-element part of the
+// input, in a file-scope device array (each GPU holds its own copy until the
+// process ends) instead of context memory allocated on demand. Every call on a
+// GPU shares that GPU's array, so calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+constexpr uint64_t kNoAllocArgmaxMax = uint64_t(1) << 24;  // elements per call
+static __device__ __align__(256) int64_t g_argmax_parts[kNoAllocArgmaxMax / 1024];
+
+namespace {
+
+std::mutex g_noalloc_mu;
+std::map<int, int64_t*> g_noalloc_parts;  // device -> address of g_argmax_parts on it
+
+// Address of this device's copy of g_argmax_parts (the device must be
+// current); looked up once per device. The array's name in host code is not
+// a device address, so kernels only ever receive this pointer.
+int64_t* noalloc_parts_on(int device) {
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  auto it = g_noalloc_parts.find(device);
+  if (it != g_noalloc_parts.end()) return it->second;
+  void* p = nullptr;
+  HIPC(hipGetSymbolAddress(&p, HIP_SYMBOL(g_argmax_parts)));
+  if (!p) throw Status(3, "hipGetSymbolAddress returned no address for the argmax scratch");
+  g_noalloc_parts[device] = static_cast<int64_t*>(p);
+  return static_cast<int64_t*>(p);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
 namespace {
@@ -2490,6 +2522,7 @@ int det_ctx_create(int device, det_ctx_t** out) {
     HIPC(hipSetDevice(device));
     HIPC(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
     HIPC(hipMalloc(&c->argmax_out, 4));
+    c->noalloc_parts = noalloc_parts_on(device);
     *out = c.release();
   });
 }
@@ -2644,6 +2677,20 @@ int det_argmax_first(det_ctx_t* ctx, const int32_t* x, uint64_t n, uint32_t* ind
   return guarded(ctx, [&] {
     if (n == 0) contract("argmax_first requires a non-empty slice");
     *index = ctx->argmax(x, n);
+  });
+}
+int det_argmax_first_noalloc(det_ctx_t* ctx, const int32_t* x, uint64_t n, uint32_t* index_dev) {
+  return guarded(ctx, [&] {
+    if (n == 0) contract("argmax_first requires a non-empty slice");
+    if (n > kNoAllocArgmaxMax)
+      bail("allocation-free argmax takes at most " + std::to_string(kNoAllocArgmaxMax) + " elements, got " +
+           std::to_string(n));
+    if (!x || !index_dev) bail("input and index device pointers are required");
+    // the same two kernels as det_argmax_first; the part keys go to the static
+    // array (every part is written before the final pass reads it, so nothing
+    // needs clearing) and nothing is allocated, copied to the host or waited on
+    det::launch_argmax(x, n, ctx->noalloc_parts, index_dev, ctx->stream);
+    HIPC(hipGetLastError());
   });
 }
 int det_elementwise(det_ctx_t* ctx, int op, int32_t* x, const int32_t* y, uint64_t n, int32_t scalar) {

@@ -265,6 +265,7 @@ def lib() -> C.CDLL:
         "det_rope": (C.c_int, [P, P, u64, u64, u64, u64, u64, C.c_int64, u64, u64]),
         "det_attention_causal": (C.c_int, [P, P, P, P, u64, u64, u64, u64, u64, u64, P]),
         "det_argmax_first": (C.c_int, [P, P, u64, C.POINTER(C.c_uint32)]),
+        "det_argmax_first_noalloc": (C.c_int, [P, P, u64, P]),
         "det_elementwise": (C.c_int, [P, C.c_int, P, P, u64, C.c_int32]),
         "det_model_create": (C.c_int, [P, C.POINTER(TextConfig), C.POINTER(P)]),
         "det_model_set_tensor": (C.c_int, [P, C.c_char_p, u64, P, C.c_int, P, P]),
@@ -425,6 +426,10 @@ class Context:
         r = C.c_uint32()
         self.check(self.lib.det_argmax_first(self.handle, C.c_void_p(x.ptr), n, C.byref(r)))
         return r.value
+
+    def argmax_first_noalloc(self, x: "DeviceBuffer", n: int, index: "DeviceBuffer") -> None:
+        """Allocation-free argmax_first into the device word `index` (no synchronization)."""
+        self.check(self.lib.det_argmax_first_noalloc(self.handle, C.c_void_p(x.ptr), n, C.c_void_p(index.ptr)))
 
     def elementwise(self, op: int, x: "DeviceBuffer", y: "DeviceBuffer | None", n: int, scalar: int = 0) -> None:
         yp = C.c_void_p(y.ptr) if y is not None else None
