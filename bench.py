@@ -13,6 +13,12 @@ per GEMV = N*K (int8) + 4N (scales) + 4K (activation) + 4N (output).
 is launched on. ``cpu_baseline`` = the oracle's restatement of the reference
 det_linear_into_par schedule on expanded i16 weights (what the reference CPU
 path streams), timed on this host on a bounded sample.
+
+Beside the headline: the config-3 prefill GEMM, the E4B-shaped (42-layer)
+greedy decode and 512-token prefill, the same decode with every checkpoint
+commitment of the routines (``decode_tok_s_checkpointed``), the oracle's E4B
+prefill / decode tok/s on this host's cores and on one thread
+(``e4b.cpu_baseline``), and 16 ragged sequences decoded in shared steps.
 """
 from __future__ import annotations
 
@@ -72,6 +78,124 @@ def cpu_baseline(problems, seconds: float, threads: int) -> dict:
     }
 
 
+E4B_SCALE_MAX = 256  # row scales in [1, 256]: expanded weights fit i16, row mass < 2^31
+
+
+def cpu_description() -> dict:
+    """nproc, the CPU model string and family/model numbers from /proc/cpuinfo."""
+    info = {"nproc": os.cpu_count()}
+    try:
+        fields = {}
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                fields.setdefault(k, v)
+        info["model"] = f"{fields.get('model name', '?')} (family {fields.get('cpu family', '?')}, " \
+                        f"model {fields.get('model', '?')})"
+        info["sha_ni"] = "sha_ni" in fields.get("flags", "")
+    except OSError:
+        pass
+    return info
+
+
+def e4b_cpu_baseline(rd, args, gpu_model) -> dict:
+    """The oracle (the reference's det path restated, reference schedule:
+    row-parallel GEMV for one token, token-parallel slab GEMV, item-parallel
+    attention; i16-expanded weights as the reference streams them) on the same
+    E4B-shaped weights: a bounded sample of prefill and greedy decode on all
+    host threads and on one thread. The GPU decodes the same prompt so the
+    sample is also a parity check of the tokens."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib  # the oracle is the checker / CPU baseline only
+    from rasterdet import synthetic
+
+    threads = oracle_lib.cpu_count()
+    cfg = synthetic.e4b_config(layers=args.e4b_layers)
+    t0 = time.perf_counter()
+    om = oracle_lib.OracleModel(cfg)
+    for name, v, sc in synthetic.synthetic_model_fast(cfg, seed=args.seed, scale_max=E4B_SCALE_MAX):
+        om.set_tensor(name, v, 32 if sc is None else 8, sc)
+    om.finalize()
+    load_s = time.perf_counter() - t0
+    rng = np.random.default_rng(args.seed + 11)
+    prompt = rng.integers(0, 262144, size=args.cpu_prompt).tolist()
+    out = {"cpu": cpu_description(), "threads": threads, "load_s": round(load_s, 1),
+           "sample": f"{args.cpu_prompt}-token prompt, then {args.cpu_steps} greedy steps (context "
+                     f"{args.cpu_prompt}..{args.cpu_prompt + args.cpu_steps}) on {threads} threads; one thread: "
+                     f"a {args.cpu_prompt_1t}-token prefill and {args.cpu_steps_1t} steps"}
+    oracle_lib.set_threads(threads)
+    t0 = time.perf_counter()
+    sess = om.session(prompt)
+    pre_s = time.perf_counter() - t0
+    toks, tok = [], sess.next_token()
+    t0 = time.perf_counter()
+    for _ in range(args.cpu_steps):
+        toks.append(tok)
+        sess.decode(tok)
+        tok = sess.next_token()
+    dec_s = time.perf_counter() - t0
+    out["prefill_tok_s"] = round(len(prompt) / pre_s, 2)
+    out["decode_tok_s"] = round(args.cpu_steps / dec_s, 3)
+    out["decode_ms_per_token"] = round(dec_s / args.cpu_steps * 1e3, 1)
+    # the GPU's greedy tokens for the same prompt
+    gs = gpu_model.session(len(prompt) + args.cpu_steps + 1)
+    g = gs.prefill(prompt, rd.DET_COMMIT_NONE).next_token
+    gpu_toks = []
+    for _ in range(args.cpu_steps):
+        gpu_toks.append(g)
+        g = gs.decode(g, rd.DET_COMMIT_NONE).next_token
+    out["gpu_tokens_identical"] = gpu_toks == toks
+    oracle_lib.set_threads(1)
+    t0 = time.perf_counter()
+    s1 = om.session(prompt[:args.cpu_prompt_1t])
+    pre1 = time.perf_counter() - t0
+    tok1 = s1.next_token()
+    t0 = time.perf_counter()
+    for _ in range(args.cpu_steps_1t):
+        s1.decode(tok1)
+        tok1 = s1.next_token()
+    dec1 = time.perf_counter() - t0
+    oracle_lib.set_threads(threads)
+    out["one_thread"] = {"prefill_tok_s": round(args.cpu_prompt_1t / pre1, 3),
+                         "decode_tok_s": round(args.cpu_steps_1t / dec1, 3)}
+    log(f"[bench] CPU E4B: prefill {out['prefill_tok_s']} tok/s, decode {out['decode_tok_s']} tok/s on {threads} "
+        f"threads; one thread {out['one_thread']}")
+    del s1, sess, om
+    return out
+
+
+def e4b_checkpointed(rd, args, model) -> dict:
+    """Greedy decode with every checkpoint commitment of the native
+    deterministic routines (det_trace_run: decode.select_token, one
+    decode.layer_range over all layers with the per-layer outputs and the KV
+    commitment of every cache, decode.transition_finalize) for the same
+    512-token prompt: tok/s = steps / (trace with the steps - trace of the
+    prompt alone). Hashing runs on host threads beside the GPU and is inside
+    the measured time."""
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, 262144, size=args.prompt_len).tolist()
+    steps = args.decode_steps
+
+    def text(ids):
+        return ""
+
+    t0 = time.perf_counter()
+    model.trace("bench prompt", prompt, max_new_tokens=0, detokenize=text)
+    pre_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    art, _ = model.trace("bench prompt", prompt, max_new_tokens=steps, detokenize=text)
+    full_s = time.perf_counter() - t0
+    n_entries = art.count(b'": "')
+    tok_s = steps / (full_s - pre_s)
+    log(f"[bench] E4B checkpointed decode: {steps} steps, {n_entries} checkpoints, {tok_s:.1f} tok/s "
+        f"(prompt trace {pre_s * 1e3:.0f} ms, full {full_s * 1e3:.0f} ms)")
+    return {"decode_tok_s_checkpointed": round(tok_s, 2),
+            "checkpointed": {"steps": steps, "checkpoints": n_entries, "prompt_trace_s": round(pre_s, 3),
+                             "full_trace_s": round(full_s, 3),
+                             "commitments": "every decode.layer_range (per-layer outputs, KV of all 42 caches), "
+                                            "select_token and transition_finalize (logits) checkpoint"}}
+
+
 def e4b_model(ctx, rd, args):
     """E4B-shaped model (42 layers, hidden 2560, 8/2 heads x 256, FF 10240,
     vocab 262144, alternating sliding/full) with counter-hash int8 weights."""
@@ -80,7 +204,7 @@ def e4b_model(ctx, rd, args):
     cfg = synthetic.e4b_config(layers=args.e4b_layers)
     t0 = time.perf_counter()
     model = rd.Model(ctx, cfg)
-    for name, v, s in synthetic.synthetic_model_fast(cfg, seed=args.seed):
+    for name, v, s in synthetic.synthetic_model_fast(cfg, seed=args.seed, scale_max=E4B_SCALE_MAX):
         model.set_tensor(name, v, s)
     model.finalize()
     load_s = time.perf_counter() - t0
@@ -131,8 +255,9 @@ def e4b_decode(ctx, rd, args, model, load_s) -> dict:
         "prefill_tok_s": round(args.prompt_len / prefill_s, 1),
         "e4b": {"layers": args.e4b_layers, "prompt": args.prompt_len, "decode_steps": steps,
                 "load_s": round(load_s, 1), "repeat_run_tokens_identical": bool(same),
-                "weights": "counter-hash int8 q, row scales in [1,16]",
-                "commitments": "decode_tok_s: none; with_commitments: activation+logits SHA-256 per step"},
+                "weights": f"counter-hash int8 q, row scales in [1,{E4B_SCALE_MAX}]",
+                "commitments": "decode_tok_s: none; with_commitments: activation+logits SHA-256 per step; "
+                               "checkpointed: every checkpoint of the routines (det_trace_run)"},
     }
 
 
@@ -152,10 +277,23 @@ def ragged_batch(ctx, rd, args, model) -> dict:
     toks = [s.prefill(p, rd.DET_COMMIT_NONE).next_token for s, p in zip(sess, prompts)]
     ctx.synchronize()
     prefill_s = time.perf_counter() - t0
-    # solo copies of the shortest and longest sequence, to check the batch against
-    check = [] if getattr(args, "no_solo_check", False) else [int(np.argmin(lens)), int(np.argmax(lens))]
-    solo = {i: sess[i].clone() for i in check}
-    first = toks[:]
+    # every sequence decoded in the batch and alone for 16 steps, on copies:
+    # activation and logits commitments every step, KV commitments at the last
+    n_check = min(steps, 16)
+    same = None
+    if not getattr(args, "no_solo_check", False):
+        same = True
+        bcopy = [s.clone() for s in sess]
+        solo = [s.clone() for s in sess]
+        tb, ts = toks[:], toks[:]
+        for j in range(n_check):
+            flags = rd.DET_COMMIT_ALL if j == n_check - 1 else rd.DET_COMMIT_ACTIVATIONS
+            res = rd.decode_batch(bcopy, tb, flags)
+            for i, r in enumerate(res):
+                e = solo[i].decode(ts[i], flags)
+                same &= (r.activation, r.logits, r.kv, r.next_token) == (e.activation, e.logits, e.kv, e.next_token)
+                tb[i], ts[i] = r.next_token, e.next_token
+        del bcopy, solo
     out = [[] for _ in range(n)]
     t0 = time.perf_counter()
     extra = rd.DET_DECODE_EAGER if getattr(args, "eager", False) else 0
@@ -166,13 +304,6 @@ def ragged_batch(ctx, rd, args, model) -> dict:
             out[i].append(t)
     ctx.synchronize()
     dec_s = time.perf_counter() - t0
-    n_check = min(steps, 16)
-    same = True
-    for i, s in solo.items():
-        t = first[i]
-        for j in range(n_check):
-            t = s.decode(t, rd.DET_COMMIT_NONE | extra).next_token
-            same &= t == out[i][j]
     log(f"[bench] ragged x{n}: prefill {int(lens.sum())} tokens in {prefill_s * 1e3:.0f} ms, "
         f"{steps} batched steps in {dec_s * 1e3:.0f} ms ({n * steps / dec_s:.1f} tok/s aggregate)")
     return {
@@ -180,8 +311,9 @@ def ragged_batch(ctx, rd, args, model) -> dict:
         "ms_per_batched_step": round(dec_s / steps * 1e3, 3),
         "sequences": n, "steps": steps, "prompt_lens": [int(k) for k in lens],
         "prefill_s": round(prefill_s, 3),
-        "solo_tokens_identical": bool(same) if solo else None,
-        "solo_check": f"shortest and longest sequence decoded alone for {n_check} steps" if solo else "skipped",
+        "solo_commitments_identical": bool(same) if same is not None else None,
+        "solo_check": (f"all {n} sequences decoded in the batch and alone for {n_check} steps: activation and "
+                       f"logits commitments every step, KV commitments at the last" if same is not None else "skipped"),
     }
 
 
@@ -296,11 +428,17 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true",
                     help="launch decode kernels directly instead of replaying graphs (for kernel tracing)")
     ap.add_argument("--no-solo-check", action="store_true",
-                    help="skip the solo re-decode of two ragged sequences (profiling runs)")
+                    help="skip the batch-vs-solo commitment check of the ragged sequences (profiling runs)")
     ap.add_argument("--ragged-seqs", type=int, default=16)
     ap.add_argument("--ragged-steps", type=int, default=128)
     ap.add_argument("--e4b-layers", type=int, default=42)
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--no-e4b-cpu", action="store_true", help="skip the oracle's E4B decode/prefill CPU baseline")
+    ap.add_argument("--no-checkpointed", action="store_true", help="skip the checkpointed (traced) decode")
+    ap.add_argument("--cpu-prompt", type=int, default=32)
+    ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--cpu-prompt-1t", type=int, default=4)
+    ap.add_argument("--cpu-steps-1t", type=int, default=2)
     ap.add_argument("--prompt-len", type=int, default=512)
     ap.add_argument("--decode-profile", action="store_true",
                     help="only the E4B-shaped model: prefill, then 32 greedy decode steps (for rocprofv3 runs)")
@@ -448,6 +586,10 @@ def main() -> int:
         model, load_s = e4b_model(ctx, rd, args)
         if not args.no_e4b:
             line.update(e4b_decode(ctx, rd, args, model, load_s))
+            if not args.no_checkpointed:
+                line.update(e4b_checkpointed(rd, args, model))
+            if not args.no_e4b_cpu and not args.no_cpu:
+                line["e4b"]["cpu_baseline"] = e4b_cpu_baseline(rd, args, model)
         if not args.no_ragged:
             line["ragged_batch"] = ragged_batch(ctx, rd, args, model)
     print(json.dumps(line), flush=True)
