@@ -212,6 +212,37 @@ def e4b_model(ctx, rd, args):
     return model, load_s
 
 
+def e4b_ple_decode(ctx, rd, args) -> dict:
+    """The E4B-shaped model with per-layer inputs of width 256 (Gemma-3n-style
+    PLE: a 262144 x 42*256 token table and a 42*256 x 2560 projection, a gate
+    and a projection GEMV per layer): greedy decode through the fused step."""
+    from rasterdet import synthetic
+
+    cfg = synthetic.e4b_config(layers=args.e4b_layers, ple=256)
+    model = rd.Model(ctx, cfg)
+    for name, v, s in synthetic.synthetic_model_fast(cfg, seed=args.seed + 1, scale_max=E4B_SCALE_MAX):
+        model.set_tensor(name, v, s)
+    model.finalize()
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, 262144, size=args.prompt_len).tolist()
+    steps = args.decode_steps
+    sess = model.session(args.prompt_len + steps + 1)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    tok = sess.prefill(prompt, rd.DET_COMMIT_NONE).next_token
+    ctx.synchronize()
+    prefill_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = sess.decode(tok, rd.DET_COMMIT_NONE).next_token
+    ctx.synchronize()
+    dec_s = time.perf_counter() - t0
+    log(f"[bench] E4B + PLE decode {steps} steps in {dec_s * 1e3:.1f} ms ({steps / dec_s:.1f} tok/s)")
+    return {"ple_width": 256, "fused_step": model.fused_decode, "decode_tok_s": round(steps / dec_s, 2),
+            "decode_ms_per_token": round(dec_s / steps * 1e3, 3), "prefill_tok_s": round(args.prompt_len / prefill_s, 1),
+            "prompt": args.prompt_len, "decode_steps": steps}
+
+
 def e4b_decode(ctx, rd, args, model, load_s) -> dict:
     """E4B-shaped greedy decode: prefill a seeded uniform-random prompt, then
     time greedy decode steps with the argmax token fed back each step."""
@@ -435,6 +466,7 @@ def main() -> int:
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--no-e4b-cpu", action="store_true", help="skip the oracle's E4B decode/prefill CPU baseline")
     ap.add_argument("--no-checkpointed", action="store_true", help="skip the checkpointed (traced) decode")
+    ap.add_argument("--no-ple", action="store_true", help="skip the E4B-shaped decode with per-layer inputs")
     ap.add_argument("--cpu-prompt", type=int, default=32)
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--cpu-prompt-1t", type=int, default=4)
@@ -592,6 +624,9 @@ def main() -> int:
                 line["e4b"]["cpu_baseline"] = e4b_cpu_baseline(rd, args, model)
         if not args.no_ragged:
             line["ragged_batch"] = ragged_batch(ctx, rd, args, model)
+        del model
+    if not args.no_e4b and not args.no_ple:
+        line["e4b_ple"] = e4b_ple_decode(ctx, rd, args)
     print(json.dumps(line), flush=True)
     return 0 if parity else 1
 

@@ -187,6 +187,12 @@ int det_model_set_tensor(det_model_t* model, const char* name, uint64_t rank, co
 int det_model_load_detwgt(det_model_t* model, const uint8_t* bytes, size_t len);
 /* Resolves layers exactly like load_det_num_gemma4_layer_weights (gemma/io.rs:1896-2045). */
 int det_model_finalize(det_model_t* model);
+/* 1 when the model's decode steps run the graph-captured fused step (int8
+ * matrices whose shapes fit its kernels, with or without per-layer inputs),
+ * 0 when they run one kernel sequence per operation, -1 before finalize. No
+ * counterpart in the reference (its executor has one CPU path); for callers
+ * and tests that need to know which GPU schedule a model takes. */
+int det_model_fused_decode(const det_model_t* model);
 void det_model_free(det_model_t* model);
 
 /* ------------------------------------------------------------------------ */

@@ -380,6 +380,7 @@ struct det_model {
   bool has_ple = false;
   uint64_t ple_dim = 0;
   const DevMatrix* ple_tok = nullptr;  // [ple_vocab x L*ple]
+  const DevMatrix* ple_proj_full = nullptr;  // [L*ple x hidden]: every layer's projection rows
   std::vector<DevMatrix> ple_proj_views;
   int32_t* ple_proj_norm = nullptr;
   int32_t ple_embedding_scale = 0, ple_projection_scalar = 0, ple_input_scale = 0;
@@ -618,6 +619,7 @@ void finalize(det_model* m) {
     for (uint64_t l = 0; l < c.num_hidden_layers; ++l) {
       m->ple_proj_views.push_back(extract_rows(m->ctx, *proj, l * ple, ple));
     }
+    m->ple_proj_full = proj;
     m->ple_proj_norm = m->need_vector("model.language_model.per_layer_projection_norm.weight", ple);
     m->ple_embedding_scale = det::f32_to_act(std::sqrt(float(ple)));
     m->ple_projection_scalar = det::f32_to_act(std::pow(float(c.hidden_size), -0.5f));
@@ -632,10 +634,16 @@ void finalize(det_model* m) {
     m->softcap = det::f32_to_act(c.final_logit_softcapping);
     if (*m->softcap <= 0) contract("softcap_act requires a strictly positive softcap");
   }
-  // The fused, graph-captured decode step covers int8 models without PLE
-  // whose shapes fit its kernels; everything else runs the per-op sequence.
-  bool ok = !m->has_ple && m->hidden <= det::kDecMaxHidden && m->lm_head->storage == det::kInt8 &&
-            det::gemv_fits_lds(*m->lm_head, 1);
+  // The fused, graph-captured decode step covers int8 models whose shapes
+  // fit its kernels, with or without PLE; everything else runs the per-op
+  // sequence.
+  auto gemv_ok = [](const DevMatrix* w) { return w->storage == det::kInt8 && det::gemv_fits_lds(*w, 1); };
+  bool ok = m->hidden <= det::kDecMaxHidden && gemv_ok(m->lm_head);
+  if (m->has_ple) {
+    ok = ok && gemv_ok(m->ple_proj_full);
+    for (const GLayer& L : m->layers)
+      if (L.has_ple && (!gemv_ok(L.ple_gate) || !gemv_ok(L.ple_proj))) ok = false;
+  }
   for (const GLayer& L : m->layers) {
     for (const DevMatrix* w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down})
       if (w && (w->storage != det::kInt8 || !det::gemv_fits_lds(*w, 1))) ok = false;
@@ -799,6 +807,11 @@ struct det_session {
   // limb planes (4 x kpad bytes) of the normalised row and of the MLP hidden row
   int8_t *limbs_x = nullptr, *limbs_ff = nullptr;
   uint64_t kpad_x = 0;
+  // PLE of the fused step: every layer's per-layer input of the step token
+  // ([L*ple], then the model projection rows), the gate row and the
+  // projection accumulators (cleared by their consumer)
+  int32_t *ple_in_all = nullptr, *ple_pp = nullptr, *ple_g = nullptr;
+  int64_t* ple_acc = nullptr;
   int64_t* attn_acc = nullptr;
   int64_t* attn_keys = nullptr;      // per-chunk argmax keys of the scores
   det::AttnStat* attn_stats = nullptr;  // per-head softmax statistics
@@ -914,6 +927,14 @@ void session_alloc(det_session* s, bool with_state = true) {
     s->am_out = s->alloc<uint32_t>(1);
     s->st_dev = s->alloc<det::StepState>(1);
     s->trig = s->alloc<int32_t>(2 * uint64_t(std::max<uint32_t>(m->trig_pairs, 1)));
+    if (m->has_ple) {
+      const uint64_t rows = std::max<uint64_t>(m->ple_proj_full->rows, m->layers.size() * m->ple_dim);
+      s->ple_in_all = s->alloc<int32_t>(rows);
+      s->ple_pp = s->alloc<int32_t>(rows);
+      s->ple_g = s->alloc<int32_t>(m->ple_dim);
+      s->ple_acc = s->alloc<int64_t>(H);
+      HIPC(hipMemsetAsync(s->ple_acc, 0, H * 8, zst));
+    }
   }
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
@@ -1804,6 +1825,17 @@ void enqueue_fused_step(det_session* s) {
   const uint64_t H = m->hidden;
   det::launch_dec_embed(*m->embedding, s->st_dev, m->embed_scale, H, s->x, s->dec_in, m->layers[0].in_ln, m->eps,
                         s->normed, s->limbs_x, s->kpad_x, st);
+  const uint64_t P = m->ple_dim, LP = m->layers.size() * P;
+  if (m->has_ple) {
+    // per-layer inputs of the step token for every layer at once
+    // (det_decode_ple_input, det_kernels.rs:1142-1208, one slice per layer)
+    det::launch_gather_rows(*m->ple_tok, &s->st_dev->token, 1, 0, LP, m->ple_embedding_scale, s->ple_in_all, LP, st);
+    det::launch_gemv_decode(*m->ple_proj_full, s->dec_in, false, 0, s->ple_pp, st);
+    det::launch_scale(s->ple_pp, LP, m->ple_projection_scalar, st);
+    det::launch_rmsnorm(s->ple_pp, m->layers.size(), P, P, m->ple_proj_norm, m->eps, st);
+    det::launch_add_sat(s->ple_in_all, s->ple_pp, LP, st);
+    det::launch_scale(s->ple_in_all, LP, m->ple_input_scale, st);
+  }
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
     const auto& F = m->fused[l];
@@ -1816,9 +1848,23 @@ void enqueue_fused_step(det_session* s) {
     det::launch_gemv_dec(F.gateup, s->limbs_x, s->hbuf, nullptr, 1, s->limbs_ff, L.down->kpad, st);
     det::launch_gemv_dec(*L.down, s->limbs_ff, nullptr, s->ff_acc, 0, nullptr, 0, st);
     const int32_t* w_next = l + 1 < m->layers.size() ? m->layers[l + 1].in_ln : m->final_norm;
-    det::launch_dec_residual_norm(s->ff_acc, s->x, s->normed, L.post_ff_ln, L.layer_scalar.has_value(),
-                                  L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st, 1,
-                                  s->layer_rows ? s->layer_rows + l * H : nullptr);
+    int32_t* row_out = s->layer_rows ? s->layer_rows + l * H : nullptr;
+    if (m->has_ple && L.has_ple) {
+      // x += norm(down); then the per-layer input block (det_kernels.rs:1108-1128):
+      // x += norm(proj(gelu(gate(x)) * ple_in)), then the layer scalar and the next norm
+      det::launch_dec_residual_norm(s->ff_acc, s->x, s->normed, L.post_ff_ln, false, 0, w_next, H, L.eps, s->limbs_x,
+                                    s->kpad_x, st);
+      det::launch_gemv_decode(*L.ple_gate, s->x, false, 0, s->ple_g, st);
+      det::launch_gelu_mul(s->ple_g, s->ple_in_all + l * P, P, st);
+      det::launch_gemv_decode_acc(*L.ple_proj, s->ple_g, false, s->ple_acc, st);
+      det::launch_dec_residual_norm(s->ple_acc, s->x, s->normed, L.ple_post_norm, L.layer_scalar.has_value(),
+                                    L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st, 1,
+                                    row_out);
+    } else {
+      det::launch_dec_residual_norm(s->ff_acc, s->x, s->normed, L.post_ff_ln, L.layer_scalar.has_value(),
+                                    L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st, 1,
+                                    row_out);
+    }
   }
   // the vocabulary projection streams best through the 8-wave LDS kernel
   det::launch_gemv_decode(*m->lm_head, s->normed, false, 0, s->logits, st);
@@ -2756,6 +2802,7 @@ int det_model_load_detwgt(det_model_t* m, const uint8_t* bytes, size_t len) {
   });
 }
 int det_model_finalize(det_model_t* m) { return guarded(m->ctx, [&] { finalize(m); }); }
+int det_model_fused_decode(const det_model_t* m) { return !m || !m->finalized ? -1 : (m->fused_ok ? 1 : 0); }
 void det_model_free(det_model_t* m) {
   if (!m) return;
   (void)hipStreamSynchronize(m->ctx->stream);
@@ -2802,7 +2849,8 @@ int det_session_decode_batch(det_session_t* const* sessions, uint64_t n, const u
   }
   return guarded(sessions[0]->m->ctx, [&] {
     std::vector<det_decode_result_t> tmp(out ? 0 : n);
-    if (sessions[0]->m->fused_ok && !(flags & DET_DECODE_PER_OP))
+    // (the batched fused step has no PLE stage: PLE models batch per op)
+    if (sessions[0]->m->fused_ok && !sessions[0]->m->has_ple && !(flags & DET_DECODE_PER_OP))
       decode_batch_fused(sessions, n, tokens, flags, out ? out : tmp.data());
     else
       decode_batch(sessions, n, tokens, flags, out ? out : tmp.data());

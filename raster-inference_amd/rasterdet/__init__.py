@@ -271,6 +271,7 @@ def lib() -> C.CDLL:
         "det_model_set_tensor": (C.c_int, [P, C.c_char_p, u64, P, C.c_int, P, P]),
         "det_model_load_detwgt": (C.c_int, [P, P, C.c_size_t]),
         "det_model_finalize": (C.c_int, [P]),
+        "det_model_fused_decode": (C.c_int, [P]),
         "det_model_free": (None, [P]),
         "det_session_create": (C.c_int, [P, u64, C.POINTER(P)]),
         "det_session_clone": (C.c_int, [P, C.POINTER(P)]),
@@ -565,6 +566,11 @@ class Model:
     def finalize(self) -> "Model":
         self.ctx.check(self.ctx.lib.det_model_finalize(self.handle))
         return self
+
+    @property
+    def fused_decode(self) -> bool:
+        """Whether decode steps run the graph-captured fused step."""
+        return self.ctx.lib.det_model_fused_decode(self.handle) == 1
 
     def session(self, max_tokens: int) -> "Session":
         return Session(self, max_tokens)

@@ -74,8 +74,10 @@ def tiny_config() -> dict:
     }}
 
 
-def e4b_config(layers: int = 42, vocab: int = 262144, sliding_window: int = 512) -> dict:
-    return {"text_config": {
+def e4b_config(layers: int = 42, vocab: int = 262144, sliding_window: int = 512, ple: int = 0) -> dict:
+    """E4B-shaped text config; ple > 0 adds per-layer inputs of that width
+    (hidden_size_per_layer_input, over the same vocabulary)."""
+    tc = {
         "enable_moe_block": False, "head_dim": 256, "hidden_activation": "gelu_pytorch_tanh",
         "hidden_size": 2560, "layer_types": [("sliding_attention" if l % 2 == 0 else "full_attention")
                                              for l in range(layers)],
@@ -83,17 +85,23 @@ def e4b_config(layers: int = 42, vocab: int = 262144, sliding_window: int = 512)
         "rms_norm_eps": 1e-6, "sliding_window": sliding_window, "tie_word_embeddings": False,
         "vocab_size": vocab,
         "intermediate_size": 10240,
-    }}
+    }
+    if ple:
+        tc.update({"hidden_size_per_layer_input": ple, "vocab_size_per_layer_input": vocab})
+    return {"text_config": tc}
 
 
 def model_tensor_shapes(cfg: dict) -> list[tuple[str, tuple[int, ...]]]:
-    """Tensor names/shapes of a Gemma-4 text decoder without PLE (gemma/io.rs naming)."""
+    """Tensor names/shapes of a Gemma-4 text decoder (gemma/io.rs naming), with
+    the per-layer-input tensors when hidden_size_per_layer_input is set
+    (gemma/io.rs:1183-1215, 1920-1940). Models without PLE keep their tensor order."""
     tc = cfg["text_config"]
     H, HD, NH, NKV = tc["hidden_size"], tc["head_dim"], tc["num_attention_heads"], tc["num_key_value_heads"]
     FF = tc.get("intermediate_size", 2 * H)
     V = tc["vocab_size"]
+    L, P = tc["num_hidden_layers"], tc.get("hidden_size_per_layer_input") or 0
     out = [("model.language_model.embed_tokens.weight", (V, H))]
-    for l in range(tc["num_hidden_layers"]):
+    for l in range(L):
         p = f"model.language_model.layers.{l}"
         out += [(f"{p}.self_attn.q_proj.weight", (NH * HD, H)), (f"{p}.self_attn.k_proj.weight", (NKV * HD, H)),
                 (f"{p}.self_attn.v_proj.weight", (NKV * HD, H)), (f"{p}.self_attn.o_proj.weight", (H, NH * HD)),
@@ -102,6 +110,14 @@ def model_tensor_shapes(cfg: dict) -> list[tuple[str, tuple[int, ...]]]:
                 (f"{p}.pre_feedforward_layernorm.weight", (H,)), (f"{p}.post_feedforward_layernorm.weight", (H,)),
                 (f"{p}.mlp.gate_proj.weight", (FF, H)), (f"{p}.mlp.up_proj.weight", (FF, H)),
                 (f"{p}.mlp.down_proj.weight", (H, FF))]
+        if P:
+            out += [(f"{p}.per_layer_input_gate.weight", (P, H)), (f"{p}.per_layer_projection.weight", (H, P)),
+                    (f"{p}.post_per_layer_input_norm.weight", (H,))]
+    if P:
+        PV = tc.get("vocab_size_per_layer_input") or V
+        out += [("model.language_model.embed_tokens_per_layer.weight", (PV, L * P)),
+                ("model.language_model.per_layer_model_projection.weight", (L * P, H)),
+                ("model.language_model.per_layer_projection_norm.weight", (P,))]
     out += [("model.language_model.norm.weight", (H,))]
     if not tc.get("tie_word_embeddings", True):
         out += [("model.language_model.lm_head.weight", (V, H))]

@@ -109,3 +109,45 @@ def test_fused_decode_long_context_split_softmax_matches_per_op(ctx):
         rb = b.decode(tb, rd.DET_COMMIT_ALL | rd.DET_DECODE_PER_OP)
         assert (ra.activation, ra.logits, ra.kv, ra.next_token) == (rb.activation, rb.logits, rb.kv, rb.next_token), step
         ta, tb = ra.next_token, rb.next_token
+
+
+def test_fused_decode_with_per_layer_inputs_matches_oracle(ctx):
+    # E4B-shaped layers with per-layer inputs (PLE width 256): the fused step
+    # computes every layer's per-layer input once per step and runs the PLE
+    # block (gate GEMV, GELU x input, projection GEMV, norm + residual)
+    # between the MLP and the next layer
+    cfg = synthetic.e4b_config(layers=2, vocab=4096, sliding_window=8, ple=256)
+    om, gm = fixtures.load_both(cfg, synthetic.synthetic_model_fast(cfg, seed=21, scale_max=256), ctx,
+                                threads=oracle_lib.cpu_count())
+    assert gm.fused_decode
+    prompt = list(range(40, 40 + 21))
+    exp = om.capture(prompt, 6)
+    got = gm.capture(prompt, 6)
+    assert got["prefill"] == exp["prefill"]
+    assert got["first_step_layers"] == exp["first_step_layers"]
+    assert got["decode_steps"] == exp["decode_steps"]
+    assert got["end_to_end"] == exp["end_to_end"]
+
+
+def test_fused_decode_with_per_layer_inputs_kv_sharing_and_scalars(ctx):
+    cfg = {"text_config": {
+        "enable_moe_block": False, "head_dim": 64, "hidden_activation": "gelu_pytorch_tanh", "hidden_size": 256,
+        "intermediate_size": 512, "layer_types": ["sliding_attention", "full_attention", "sliding_attention",
+                                                  "full_attention"],
+        "num_attention_heads": 4, "num_hidden_layers": 4, "num_key_value_heads": 2, "num_kv_shared_layers": 2,
+        "final_logit_softcapping": 30.0, "hidden_size_per_layer_input": 64, "vocab_size_per_layer_input": 1000,
+        "rms_norm_eps": 1e-6, "sliding_window": 5, "tie_word_embeddings": False, "vocab_size": 1000,
+    }}
+    om, gm = fixtures.load_both(cfg, fixtures.custom_model(cfg, seed=9, layer_scalars=True), ctx)
+    assert gm.fused_decode
+    prompt = [5, 900, 17, 3, 250, 64, 64, 1, 999, 12]
+    assert gm.capture(prompt, 12) == om.capture(prompt, 12)
+    # the same steps through the per-op schedule, step by step
+    a, b = gm.session(32), gm.session(32)
+    ta = a.prefill(prompt).next_token
+    tb = b.prefill(prompt).next_token
+    for step in range(10):
+        ra = a.decode(ta, rd.DET_COMMIT_ALL | (rd.DET_DECODE_EAGER if step % 2 else 0))
+        rb = b.decode(tb, rd.DET_COMMIT_ALL | rd.DET_DECODE_PER_OP)
+        assert (ra.activation, ra.logits, ra.kv, ra.next_token) == (rb.activation, rb.logits, rb.kv, rb.next_token), step
+        ta, tb = ra.next_token, rb.next_token
