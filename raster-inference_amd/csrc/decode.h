@@ -91,12 +91,14 @@ constexpr uint32_t kAttnWsumRows = 32;      // window rows per softmax / weighte
 void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, uint64_t H, int32_t* x, int32_t* dec_in,
                       const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s,
                       uint32_t nseq = 1);
-// x = add_sat(x, rmsnorm(requant(src), w_post)) [* scalar]; normed = rmsnorm(x, w_next);
-// src (wrapping Q32.32 accumulators) is cleared after use. x_out (optional)
-// receives a copy of the new x (row stride H per sequence).
+// x = add_sat(x_src, rmsnorm(requant(src), w_post)) [* scalar]; normed = rmsnorm(x, w_next);
+// src (wrapping Q32.32 accumulators) is cleared after use. x_src defaults to
+// x (in place). x_out (optional) receives a copy of the new x (row stride H
+// per sequence).
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
-                              uint64_t kpad, hipStream_t s, uint32_t nseq = 1, int32_t* x_out = nullptr);
+                              uint64_t kpad, hipStream_t s, uint32_t nseq = 1, int32_t* x_out = nullptr,
+                              const int32_t* x_src = nullptr);
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s);
 // Whether launch_dec_attention runs the statistics as a separate pass.
 bool dec_attention_split(const AttnDecArgs& a);

@@ -96,12 +96,13 @@ __global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* 
 }
 
 // Residual add of a normalised sub-block output, then the next input norm:
-// x = add_sat(x, rmsnorm(requant(src), w_post)) (times the layer scalar at the end of a
+// x = add_sat(x_src, rmsnorm(requant(src), w_post)) (times the layer scalar at the end of a
 // layer); normed = rmsnorm(x, w_next) (det_kernels.rs:1058-1075, 1108-1133).
 // src holds the projection's wrapping accumulators and is cleared after use.
+// x_src may equal x (each thread reads its elements before writing them).
 template <int NT, int EPT>
-__global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ src, int32_t* __restrict__ x,
-                                                           int32_t* __restrict__ normed,
+__global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ src, const int32_t* x_src,
+                                                           int32_t* x, int32_t* __restrict__ normed,
                                                            const int32_t* __restrict__ w_post, int has_scalar,
                                                            int32_t scalar, const int32_t* __restrict__ w_next,
                                                            uint64_t H, int64_t eps, int8_t* __restrict__ limbs,
@@ -110,6 +111,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
   __shared__ int32_t bc;
   const uint32_t seq = blockIdx.y;
   src += uint64_t(seq) * H;
+  x_src += uint64_t(seq) * H;
   x += uint64_t(seq) * H;
   normed += uint64_t(seq) * H;
   limbs += uint64_t(seq) * 4 * kpad;
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
     const bool in = c < H;
     o[e] = in ? requant(src[c]) : 0;
     if (in) src[c] = 0;
-    xv[e] = in ? x[c] : 0;
+    xv[e] = in ? x_src[c] : 0;
     wp[e] = in ? w_post[c] : 0;
     wn[e] = in ? w_next[c] : 0;
   }
@@ -1005,9 +1007,9 @@ void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, ui
 }
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
-                              uint64_t kpad, hipStream_t s, uint32_t nseq, int32_t* x_out) {
-  DET_ROW_DISPATCH(k_dec_residual_norm, src, x, normed, w_post, int(has_scalar), scalar, w_next, H, eps, limbs, kpad,
-                   x_out);
+                              uint64_t kpad, hipStream_t s, uint32_t nseq, int32_t* x_out, const int32_t* x_src) {
+  DET_ROW_DISPATCH(k_dec_residual_norm, src, x_src ? x_src : x, x, normed, w_post, int(has_scalar), scalar, w_next, H,
+                   eps, limbs, kpad, x_out);
 }
 #undef DET_ROW_DISPATCH
 // Window chunks per attention workgroup: a.rows_mul when set (1, 2 or 4),

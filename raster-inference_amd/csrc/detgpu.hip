@@ -405,6 +405,9 @@ struct det_model {
   det::RopeTable* rope_tables_dev = nullptr;
   uint32_t trig_pairs = 0;
   bool fused_ok = false;
+  // the fused step applies each residual norm inside the next projection
+  // (post-attention norm in gate/up, post-FF norm in the next layer's q/k/v)
+  bool norm_fused = false;
   // a RoPE base of i64::MAX (theta >= 2^31): the reference's nth_root_acc
   // overflows on it (ops.rs:578) at the first rotation of a position > 0
   bool rope_overflow = false;
@@ -678,6 +681,15 @@ void finalize(det_model* m) {
     HIPC(hipMemcpy(m->rope_tables_dev, tabs.data(), tabs.size() * sizeof(det::RopeTable), hipMemcpyHostToDevice));
   }
   m->fused_ok = ok;
+  // the O projection's accumulators are complete rows (plain stores), which
+  // the gate/up projection's norm reads from every workgroup
+  bool nf = ok;
+  if (ok)
+    for (size_t l = 0; l < m->layers.size(); ++l)
+      if (!det::gemv_norm_fits(m->fused[l].qkv, m->hidden) || !det::gemv_norm_fits(m->fused[l].gateup, m->hidden) ||
+          !det::gemv_decode_acc_plain(*m->layers[l].o))
+        nf = false;
+  m->norm_fused = nf;
   m->finalized = true;
 }
 
@@ -804,6 +816,9 @@ struct det_session {
   // projection accumulators (wrapping Q32.32); each consumer kernel clears
   // what it reads, so they are zero whenever a step starts
   int64_t *qkv_acc = nullptr, *o_acc = nullptr, *ff_acc = nullptr;
+  // the residual row alternates between x and x_alt where a projection
+  // applies the residual norm (its workgroups read one while one writes the other)
+  int32_t* x_alt = nullptr;
   // limb planes (4 x kpad bytes) of the normalised row and of the MLP hidden row
   int8_t *limbs_x = nullptr, *limbs_ff = nullptr;
   uint64_t kpad_x = 0;
@@ -907,6 +922,7 @@ void session_alloc(det_session* s, bool with_state = true) {
     s->qkv_acc = s->alloc<int64_t>(fr);
     s->o_acc = s->alloc<int64_t>(H);
     s->ff_acc = s->alloc<int64_t>(H);
+    s->x_alt = s->alloc<int32_t>(H);
     uint64_t kff = 0;
     for (const GLayer& L : m->layers) kff = std::max(kff, L.down->kpad);
     s->kpad_x = m->fused[0].qkv.kpad;
@@ -1836,34 +1852,85 @@ void enqueue_fused_step(det_session* s) {
     det::launch_add_sat(s->ple_in_all, s->ple_pp, LP, st);
     det::launch_scale(s->ple_in_all, LP, m->ple_input_scale, st);
   }
-  for (size_t l = 0; l < m->layers.size(); ++l) {
+  // The residual row: with norm_fused it alternates between s->x and
+  // s->x_alt at every projection that applies a residual norm, and the last
+  // layer's norm writes it back to s->x.
+  int32_t* xc = s->x;
+  auto flip = [&](const int32_t* p) { return p == s->x ? s->x_alt : s->x; };
+  const size_t nl = m->layers.size();
+  bool limbs_ready = true;  // limbs_x holds the normalised input of the next projection
+  for (size_t l = 0; l < nl; ++l) {
     const GLayer& L = m->layers[l];
     const auto& F = m->fused[l];
-    det::launch_gemv_dec(F.qkv, s->limbs_x, nullptr, s->qkv_acc, 0, nullptr, 0, st);
+    if (limbs_ready) {
+      det::launch_gemv_dec(F.qkv, s->limbs_x, nullptr, s->qkv_acc, 0, nullptr, 0, st);
+    } else {
+      // the previous layer's post-FF residual norm (and layer scalar), then this layer's input norm
+      const GLayer& Lp = m->layers[l - 1];
+      det::DecNormIn ni;
+      ni.src = s->ff_acc;
+      ni.x_in = xc;
+      ni.w_post = Lp.post_ff_ln;
+      ni.w_next = L.in_ln;
+      ni.x_out = flip(xc);
+      ni.row_out = s->layer_rows ? s->layer_rows + (l - 1) * H : nullptr;
+      ni.H = H;
+      ni.eps = Lp.eps;
+      ni.has_scalar = Lp.layer_scalar.has_value();
+      ni.scalar = Lp.layer_scalar.value_or(0);
+      det::launch_gemv_norm(ni, F.qkv, 0, s->qkv_acc, nullptr, nullptr, 0, st);
+      xc = ni.x_out;
+    }
     const det::AttnDecArgs aa = attn_args(s, l);
     det::launch_dec_attention(aa, st);
     det::launch_gemv_decode_acc(*L.o, s->attn_acc, true, s->o_acc, st);
-    det::launch_dec_residual_norm(s->o_acc, s->x, s->normed, L.post_attn_ln, false, 0, L.pre_ff_ln, H, L.eps,
-                                  s->limbs_x, s->kpad_x, st);
-    det::launch_gemv_dec(F.gateup, s->limbs_x, s->hbuf, nullptr, 1, s->limbs_ff, L.down->kpad, st);
+    if (m->norm_fused) {
+      // post-attention residual norm and pre-FF norm inside the gate/up
+      // projection, which also clears the down projection's accumulators
+      det::DecNormIn ni;
+      ni.src = s->o_acc;
+      ni.x_in = xc;
+      ni.w_post = L.post_attn_ln;
+      ni.w_next = L.pre_ff_ln;
+      ni.x_out = flip(xc);
+      ni.clear = s->ff_acc;
+      ni.clear_n = H;
+      ni.H = H;
+      ni.eps = L.eps;
+      det::launch_gemv_norm(ni, F.gateup, 1, nullptr, s->hbuf, s->limbs_ff, L.down->kpad, st);
+      xc = ni.x_out;
+    } else {
+      det::launch_dec_residual_norm(s->o_acc, xc, s->normed, L.post_attn_ln, false, 0, L.pre_ff_ln, H, L.eps,
+                                    s->limbs_x, s->kpad_x, st);
+      det::launch_gemv_dec(F.gateup, s->limbs_x, s->hbuf, nullptr, 1, s->limbs_ff, L.down->kpad, st);
+    }
     det::launch_gemv_dec(*L.down, s->limbs_ff, nullptr, s->ff_acc, 0, nullptr, 0, st);
-    const int32_t* w_next = l + 1 < m->layers.size() ? m->layers[l + 1].in_ln : m->final_norm;
+    const bool last = l + 1 == nl;
+    const int32_t* w_next = !last ? m->layers[l + 1].in_ln : m->final_norm;
     int32_t* row_out = s->layer_rows ? s->layer_rows + l * H : nullptr;
+    // the last layer's norm leaves the residual row in s->x
+    int32_t* x_dst = last ? s->x : xc;
     if (m->has_ple && L.has_ple) {
       // x += norm(down); then the per-layer input block (det_kernels.rs:1108-1128):
       // x += norm(proj(gelu(gate(x)) * ple_in)), then the layer scalar and the next norm
-      det::launch_dec_residual_norm(s->ff_acc, s->x, s->normed, L.post_ff_ln, false, 0, w_next, H, L.eps, s->limbs_x,
+      det::launch_dec_residual_norm(s->ff_acc, xc, s->normed, L.post_ff_ln, false, 0, w_next, H, L.eps, s->limbs_x,
                                     s->kpad_x, st);
-      det::launch_gemv_decode(*L.ple_gate, s->x, false, 0, s->ple_g, st);
+      det::launch_gemv_decode(*L.ple_gate, xc, false, 0, s->ple_g, st);
       det::launch_gelu_mul(s->ple_g, s->ple_in_all + l * P, P, st);
       det::launch_gemv_decode_acc(*L.ple_proj, s->ple_g, false, s->ple_acc, st);
-      det::launch_dec_residual_norm(s->ple_acc, s->x, s->normed, L.ple_post_norm, L.layer_scalar.has_value(),
+      det::launch_dec_residual_norm(s->ple_acc, x_dst, s->normed, L.ple_post_norm, L.layer_scalar.has_value(),
                                     L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st, 1,
-                                    row_out);
+                                    row_out, xc);
+      xc = x_dst;
+      limbs_ready = true;
+    } else if (last || !m->norm_fused) {
+      det::launch_dec_residual_norm(s->ff_acc, x_dst, s->normed, L.post_ff_ln, L.layer_scalar.has_value(),
+                                    L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st, 1,
+                                    row_out, xc);
+      xc = x_dst;
+      limbs_ready = true;
     } else {
-      det::launch_dec_residual_norm(s->ff_acc, s->x, s->normed, L.post_ff_ln, L.layer_scalar.has_value(),
-                                    L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st, 1,
-                                    row_out);
+      limbs_ready = false;  // the next layer's q/k/v projection applies this norm
     }
   }
   // the vocabulary projection streams best through the 8-wave LDS kernel

@@ -77,6 +77,9 @@ void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int e
 // Decode GEMV (one activation row) into wrapping Q32.32 accumulators that must
 // be zero on entry; K is split across workgroups with exact atomic adds.
 void launch_gemv_decode_acc(const DevMatrix& W, const void* act, bool act_i64, int64_t* acc, hipStream_t s);
+// Whether launch_gemv_decode_acc writes W's accumulators with plain stores
+// (complete rows, no zero needed on entry) rather than atomic partial sums.
+bool gemv_decode_acc_plain(const DevMatrix& W);
 // Decode GEMV from an activation given as limb planes (4 planes of W.kpad
 // bytes). acc != null: wrapping Q32.32 sums added atomically (zero on entry);
 // else requantized to out, or with epilogue 1 (interleaved gate/up matrix)
@@ -90,6 +93,33 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
 void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                            int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
                            hipStream_t s);
+
+// The residual norm that precedes a batch-1 decode GEMV, computed by the GEMV
+// itself: x' = add_sat(x_in, rmsnorm(requant(src)) * w_post) [* scalar], and
+// the GEMV's input is rmsnorm(x') * w_next. x' goes to x_out (and row_out when
+// set); x_out must not alias x_in. clear (optional) is zeroed by the launch.
+// All arrays hold H values (16-byte aligned), H % 4 == 0.
+struct DecNormIn {
+  const int64_t* src = nullptr;  // complete Q32.32 accumulators of the sub-block output
+  const int32_t* x_in = nullptr;
+  const int32_t* w_post = nullptr;
+  const int32_t* w_next = nullptr;
+  int32_t* x_out = nullptr;
+  int32_t* row_out = nullptr;
+  int64_t* clear = nullptr;
+  uint64_t clear_n = 0;
+  uint64_t H = 0;
+  int64_t eps = 0;
+  int32_t scalar = 0;
+  int has_scalar = 0;
+};
+// Whether W (int8, cols == H, K up to 4096, a few tiles per CU) fits the fused kernel.
+bool gemv_norm_fits(const DevMatrix& W, uint64_t H);
+// epilogue 0: Q32.32 accumulators to acc_out (plain stores); epilogue 1:
+// interleaved gate/up matrix, out[f] = mul_sat(gelu(gate_f), up_f) and its
+// limb planes (stride out_kpad) to out_limbs.
+void launch_gemv_norm(const DecNormIn& ni, const DevMatrix& W, int epilogue, int64_t* acc_out, int32_t* out,
+                      int8_t* out_limbs, uint64_t out_kpad, hipStream_t s);
 
 void launch_rmsnorm(int32_t* x, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
                     int64_t eps, hipStream_t s);

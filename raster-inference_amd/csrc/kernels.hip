@@ -657,6 +657,234 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
   }
 }
 
+// Residual norm + batch-1 decode GEMV in one kernel (the residual-norm row
+// kernel between a projection and the next GEMV is gone, with its launch and
+// its reads of the projection's output): every workgroup issues its weight
+// loads first, computes the whole residual norm of the row while they are in
+// flight (the row is 2-4 K values per thread; the two scale chains run once
+// per workgroup, on wave 0), builds the limb planes of the normalised row in
+// LDS and then runs its MFMAs.
+//   x' = add_sat(x_in, mul_sat(mul_sat(requant(src), s1), w_post)) [* scalar]
+//   a  = mul_sat(mul_sat(x', s2), w_next)
+// with s1, s2 the rms scales of requant(src) and x' (det_kernels.rs:1058-1075,
+// 1108-1133; the arithmetic of k_dec_residual_norm). Workgroup 0 writes x'.
+// Work: the grid's G workgroups take tiles b, b + G, ...; each of a tile's
+// K parts of kNormD steps (one weight round trip) is a job, and wave w takes
+// jobs w and w + NW of its workgroup. Partial tiles combine through LDS.
+// EPI 0: Q32.32 accumulators to acc_out (plain stores); EPI 1: interleaved
+// gate/up tiles, out[f] = mul_sat(gelu(gate_f), up_f) and its limb planes
+// (stride out_kpad) to out_limbs.
+constexpr int kNormD = 5;
+constexpr uint32_t kNormMaxK = 4096;
+// s_waitcnt lgkmcnt(0) with the vector-memory count left open
+constexpr int kWaitLdsOnly = 15 | (7 << 4) | (0 << 8) | (3 << 14);
+// LDS hand-over inside a workgroup that leaves its global loads in flight (a
+// __syncthreads fence would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// rms scale of a row spread over the workgroup from each thread's saturating
+// partial sum of squares (ops.rs:406-425): wave 0 reduces the wave totals and
+// runs the scale chain once.
+template <int NW>
+__device__ __forceinline__ int32_t wg_rms_scale(int64_t ss, uint64_t n, int64_t eps, int64_t* red, int32_t* bc,
+                                                int wave, int lane) {
+  ss = wave_sum_sat(ss);
+  if (lane == 0) red[wave] = ss;
+  lds_barrier();
+  if (wave == 0) {
+    int64_t t = lane < NW ? red[lane] : 0;
+    t = wave_sum_sat(t);
+    if (lane == 0) *bc = rms_scale_from_sumsq(t, uint32_t(n), eps);
+  }
+  lds_barrier();
+  return *bc;
+}
+template <int NW, int JM, int QPT, int EPI>
+__global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_t* __restrict__ q,
+                                                       const int32_t* __restrict__ scale,
+                                                       const int32_t* __restrict__ rowsum, uint64_t n_rows,
+                                                       uint64_t kpad, int64_t* __restrict__ acc_out,
+                                                       int32_t* __restrict__ out, int8_t* __restrict__ out_limbs,
+                                                       uint64_t out_kpad) {
+  constexpr int NT = 64 * NW, D = kNormD;
+  constexpr uint32_t kPlaneMax = kNormMaxK + 32;
+  typedef long long v2l __attribute__((ext_vector_type(2)));
+  __shared__ __attribute__((aligned(16))) uint8_t al[4 * kPlaneMax];
+  __shared__ v4i part[NW * JM][64];
+  __shared__ int64_t red[NW];
+  __shared__ int32_t bc;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, i = lane & 15;
+  const uint64_t nsteps = kpad / 128, np = (nsteps + D - 1) / D;
+  const uint64_t ntiles = (n_rows + 15) / 16, G = gridDim.x;
+  const uint64_t tpw = (ntiles + G - 1) / G, njobs = tpw * np;
+  const uint64_t plane = kpad + 32;  // limb plane stride in LDS (planes start 8 banks apart)
+  const uint64_t Q = ni.H / 4;      // activation quads (H % 4 == 0, H <= 4 NT QPT)
+  // 1. the norm's inputs, quad qd = tid + NT e (clamped addresses, masked
+  // below), and the row sum and scale of the tile whose epilogue this wave
+  // runs first
+  int64_t sv[QPT][4];
+  int32_t xv[QPT][4], wp[QPT][4], wn[QPT][4];
+#pragma unroll
+  for (int e = 0; e < QPT; ++e) {
+    const uint64_t qd = threadIdx.x + uint64_t(NT) * e, qc = qd < Q ? qd : Q - 1;
+    const v2l s0 = *reinterpret_cast<const v2l*>(ni.src + 4 * qc);
+    const v2l s1 = *reinterpret_cast<const v2l*>(ni.src + 4 * qc + 2);
+    const v4i x4 = *reinterpret_cast<const v4i*>(ni.x_in + 4 * qc);
+    const v4i p4 = *reinterpret_cast<const v4i*>(ni.w_post + 4 * qc);
+    const v4i n4 = *reinterpret_cast<const v4i*>(ni.w_next + 4 * qc);
+    sv[e][0] = s0.x, sv[e][1] = s0.y, sv[e][2] = s1.x, sv[e][3] = s1.y;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xv[e][k] = x4[k], wp[e][k] = p4[k], wn[e][k] = n4[k];
+  }
+  const uint64_t et = uint64_t(blockIdx.x) + G * uint64_t(wave);  // first epilogue tile of this wave
+  const uint64_t erow = (et < ntiles ? et : ntiles - 1) * 16 + i;
+  const uint64_t erc = erow < n_rows ? erow : n_rows - 1;
+  const int32_t ers = rowsum[erc], esc = scale[erc];
+  // 2. this wave's jobs: weight loads of up to D steps each (steps past the
+  // part re-read its last step and meet zero A operands). Slots past the
+  // workgroup's jobs load one line at q, never combined. The loads are
+  // unconditional and nothing is stored before the MFMAs, so every wait of
+  // the norm below counts only the loads above.
+  uint64_t js0[JM], jnu[JM];
+  v4i b[JM][2 * D];
+#pragma unroll
+  for (int u = 0; u < JM; ++u) {
+    const uint64_t jb = uint64_t(wave) + uint64_t(NW) * u;
+    const uint64_t tl = jb / np, p = jb % np;
+    const uint64_t tile = uint64_t(blockIdx.x) + G * tl;
+    const bool real = jb < njobs && tile < ntiles;  // wave-uniform
+    js0[u] = real ? p * D : 0;
+    jnu[u] = real ? (nsteps - js0[u] < uint64_t(D) ? nsteps - js0[u] : uint64_t(D)) : 1;
+    const v4i* bp = real ? reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 32)
+                         : reinterpret_cast<const v4i*>(q);
+    const uint64_t sstride = real ? 128 : 0;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const uint64_t st = js0[u] + (uint64_t(d) < jnu[u] ? uint64_t(d) : jnu[u] - 1);
+      b[u][2 * d] = __builtin_nontemporal_load(bp + st * sstride);
+      b[u][2 * d + 1] = __builtin_nontemporal_load(bp + st * sstride + (real ? 1 : 0));
+    }
+  }
+  // (the loads stay above the norm: nothing below may be hoisted over them or they sunk under it)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. residual norm of the whole row
+  int64_t ss = 0;
+#pragma unroll
+  for (int e = 0; e < QPT; ++e) {
+    const bool on = threadIdx.x + uint64_t(NT) * e < Q;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int32_t o = on ? requant(sv[e][k]) : 0;
+      sv[e][k] = o;
+      ss = add_sat64(ss, sq_term(o));
+    }
+  }
+  const int32_t s1 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane);
+  ss = 0;
+#pragma unroll
+  for (int e = 0; e < QPT; ++e) {
+    const bool on = threadIdx.x + uint64_t(NT) * e < Q;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      int32_t v = add_sat(xv[e][k], mul_sat(mul_sat(int32_t(sv[e][k]), s1), wp[e][k]));
+      if (ni.has_scalar) v = mul_sat(v, ni.scalar);
+      v = on ? v : 0;
+      xv[e][k] = v;
+      ss = add_sat64(ss, sq_term(v));
+    }
+  }
+  const int32_t s2 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane);
+  // limb planes of the normalised row (quads past H are zero, to kpad / 4)
+  const uint64_t kq = kpad / 4;
+#pragma unroll
+  for (int e = 0; e < QPT; ++e) {
+    const uint64_t qd = threadIdx.x + uint64_t(NT) * e;
+    const bool on = qd < Q;
+    if (qd < kq) {
+      uint32_t pk[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t u = on ? uint32_t(mul_sat(mul_sat(xv[e][k], s2), wn[e][k])) ^ 0x00808080u : 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pk[j] |= ((u >> (8 * j)) & 0xffu) << (8 * k);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(al + j * plane + 4 * qd) = pk[j];
+    }
+  }
+  lds_barrier();
+  // 4. MFMAs: A row i < 4 is limb i of the row (plane i, bytes [32 g, 32 g + 32) of each step)
+  const bool a_on = i < 4;
+  const uint8_t* aread = al + (i & 3) * plane + 32 * g;
+  const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+  for (int u = 0; u < JM; ++u) {
+    v4i acc = zero;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const uint64_t st = js0[u] + (uint64_t(d) < jnu[u] ? uint64_t(d) : jnu[u] - 1);
+      const int m = (a_on && uint64_t(d) < jnu[u]) ? -1 : 0;
+      const v4i a0 = *reinterpret_cast<const v4i*>(aread + st * 128) & m;
+      const v4i a1 = *reinterpret_cast<const v4i*>(aread + st * 128 + 16) & m;
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b[u][2 * d], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b[u][2 * d + 1], acc, 0, 0, 0);
+    }
+    part[wave + NW * u][lane] = acc;
+  }
+  __syncthreads();
+  // 5. one wave per tile: lanes 0-15 (g = 0) hold the row's four limb sums of row i
+  for (uint64_t tl = uint64_t(wave); tl < tpw; tl += NW) {
+    const uint64_t tile = uint64_t(blockIdx.x) + G * tl;
+    if (tile >= ntiles) break;
+    int64_t p[4] = {0, 0, 0, 0};
+    for (uint64_t pp = 0; pp < np; ++pp) {
+      const v4i v = part[tl * np + pp][lane];
+      p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+    }
+    const uint64_t row = tile * 16 + i;
+    const bool r_on = row < n_rows;
+    const bool ok = g == 0 && r_on;
+    const bool first = tl == uint64_t(wave);
+    const int32_t rs = first ? ers : (r_on ? rowsum[row] : 0);
+    const int32_t sc = first ? esc : (r_on ? scale[row] : 0);
+    const int64_t a = ok ? limb_combine(p, rs, sc) : 0;
+    if (EPI == 1) {
+      const int32_t r = requant(a);
+      const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
+      if (ok && i < 8) {
+        const uint64_t f = tile * 8 + i;
+        const int32_t h = mul_sat(gelu_act(r), up);
+        out[f] = h;
+        const uint32_t uh = uint32_t(h) ^ 0x00808080u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out_limbs[j * out_kpad + f] = int8_t(uint8_t(uh >> (8 * j)));
+      }
+    } else if (ok) {
+      acc_out[row] = a;
+    }
+  }
+  // 6. the new residual row (workgroup 0) and the cleared buffer
+  if (blockIdx.x == 0)
+#pragma unroll
+    for (int e = 0; e < QPT; ++e) {
+      const uint64_t qd = threadIdx.x + uint64_t(NT) * e;
+      if (qd < Q) {
+        const v4i x4 = {xv[e][0], xv[e][1], xv[e][2], xv[e][3]};
+        *reinterpret_cast<v4i*>(ni.x_out + 4 * qd) = x4;
+        if (ni.row_out) *reinterpret_cast<v4i*>(ni.row_out + 4 * qd) = x4;
+      }
+    }
+  if (ni.clear)
+    for (uint64_t idx = uint64_t(blockIdx.x) * NT + threadIdx.x; idx < ni.clear_n; idx += G * NT) ni.clear[idx] = 0;
+}
+
 // Decode GEMV for 5-16 tokens (NG = 2 or 4 groups of 4): the A tiles of a K
 // step are as large as the weight tile or larger, so the four waves of a
 // workgroup take four consecutive weight tiles over the same K steps and
@@ -1588,6 +1816,7 @@ void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int e
 // further split across workgroups (doubling) until the launch has at least
 // 512 workgroups, keeping at least one K step per wave and at most 1024
 // workgroups (atomic adds).
+bool gemv_decode_acc_plain(const DevMatrix& W) { return gemv_tile_fits(W); }
 void launch_gemv_decode_acc(const DevMatrix& W, const void* act, bool act_i64, int64_t* acc, hipStream_t s) {
   if (gemv_tile_fits(W)) return launch_gemv_tile(W, act, act_i64, nullptr, acc, s);
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
@@ -1716,6 +1945,60 @@ void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t nto
 void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int64_t* acc, int epilogue,
                      int8_t* out_limbs, uint64_t out_kpad, hipStream_t s) {
   launch_gemv_dec_ng<1>(W, limbs, 1, out, 0, acc, 0, epilogue, out_limbs, out_kpad, s);
+}
+
+// Work split of k_gemv_norm: one workgroup per CU (or per tile when fewer),
+// each taking ceil(tiles / G) tiles of ceil(steps / kNormD) jobs.
+struct NormSplit {
+  uint64_t grid, jobs;
+};
+static NormSplit norm_split(const DevMatrix& W) {
+  const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
+  const uint64_t grid = std::min<uint64_t>(ntiles, device_cus());
+  const uint64_t tpw = (ntiles + grid - 1) / grid;
+  return {grid, tpw * ((nsteps + kNormD - 1) / kNormD)};
+}
+bool gemv_norm_fits(const DevMatrix& W, uint64_t H) {
+  if (W.storage != kInt8 || W.rows == 0 || H == 0 || H % 4 != 0 || W.cols != H || W.kpad > kNormMaxK) return false;
+  return norm_split(W).jobs <= 32;
+}
+void launch_gemv_norm(const DecNormIn& ni, const DevMatrix& W, int epilogue, int64_t* acc_out, int32_t* out,
+                      int8_t* out_limbs, uint64_t out_kpad, hipStream_t s) {
+  if (!gemv_norm_fits(W, ni.H)) throw std::runtime_error("launch_gemv_norm: shape outside the fused kernel's range");
+  const NormSplit sp = norm_split(W);
+  // waves: one job each up to 16 jobs, else two, with as few idle job slots
+  // as the instances allow; quads per thread: the fewest that cover the
+  // kpad / 4 limb quads
+  const uint64_t kq = W.kpad / 4;
+  auto qpt = [&](int nw) { return (kq + 64 * nw - 1) / (64 * nw); };
+#define DET_NORM_LAUNCH(NW, JM, QPT)                                                                                 \
+  do {                                                                                                               \
+    if (epilogue == 1)                                                                                               \
+      hipLaunchKernelGGL((k_gemv_norm<NW, JM, QPT, 1>), dim3(unsigned(sp.grid)), dim3(64 * NW), 0, s, ni, W.q,      \
+                         W.scale, W.rowsum, W.rows, W.kpad, acc_out, out, out_limbs, out_kpad);                     \
+    else                                                                                                             \
+      hipLaunchKernelGGL((k_gemv_norm<NW, JM, QPT, 0>), dim3(unsigned(sp.grid)), dim3(64 * NW), 0, s, ni, W.q,      \
+                         W.scale, W.rowsum, W.rows, W.kpad, acc_out, out, out_limbs, out_kpad);                     \
+  } while (0)
+  if (sp.jobs <= 4) {
+    switch (qpt(4)) {
+      case 1: DET_NORM_LAUNCH(4, 1, 1); break;
+      case 2: DET_NORM_LAUNCH(4, 1, 2); break;
+      case 3: DET_NORM_LAUNCH(4, 1, 3); break;
+      default: DET_NORM_LAUNCH(4, 1, 4); break;
+    }
+  } else if (sp.jobs <= 10) {
+    if (qpt(10) == 1) DET_NORM_LAUNCH(10, 1, 1);
+    else DET_NORM_LAUNCH(10, 1, 2);
+  } else if (sp.jobs <= 16) {
+    DET_NORM_LAUNCH(16, 1, 1);
+  } else if (sp.jobs <= 20) {
+    if (qpt(10) == 1) DET_NORM_LAUNCH(10, 2, 1);
+    else DET_NORM_LAUNCH(10, 2, 2);
+  } else {
+    DET_NORM_LAUNCH(16, 2, 1);
+  }
+#undef DET_NORM_LAUNCH
 }
 
 uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64 * 4 * kpad; }
