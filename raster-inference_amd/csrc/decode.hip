@@ -85,7 +85,7 @@ __global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* 
       x[c] = v[e];
       dec_in[c] = v[e];
     }
-    ss = add_sat64(ss, sq_term(v[e]));
+    ss = add_sat64_nn(ss, sq_term(v[e]));
   }
   const int32_t sc = blk_rms_scale<NT>(ss, H, eps, red, &bc);
 #pragma unroll
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
     wn[e] = in ? w_next[c] : 0;
   }
 #pragma unroll
-  for (int e = 0; e < EPT; ++e) ss = add_sat64(ss, sq_term(o[e]));
+  for (int e = 0; e < EPT; ++e) ss = add_sat64_nn(ss, sq_term(o[e]));
   const int32_t s1 = blk_rms_scale<NT>(ss, H, eps, red, &bc);
   ss = 0;
 #pragma unroll
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
     xv[e] = v;
     if (c < H) x[c] = v;
     if (x_out && c < H) x_out[c] = v;
-    ss = add_sat64(ss, sq_term(c < H ? v : 0));
+    ss = add_sat64_nn(ss, sq_term(c < H ? v : 0));
   }
   const int32_t s2 = blk_rms_scale<NT>(ss, H, eps, red, &bc);
 #pragma unroll
@@ -222,7 +222,7 @@ __device__ __forceinline__ void norm_head_row(const HeadRowIn<MAXHD>& in, uint32
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     xv[k] = requant(in.acc[k]);  // zero past hd
-    ss = add_sat64(ss, sq_term(xv[k]));
+    ss = add_sat64_nn(ss, sq_term(xv[k]));
   }
   ss = wsum_sat(ss);
   const int32_t sc = rms_scale_from_sumsq(ss, hd, eps);

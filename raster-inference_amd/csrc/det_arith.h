@@ -25,14 +25,35 @@ typedef unsigned __int128 u128;
 DET_HD int32_t sat32(int64_t v) {
   return v > INT32_MAX ? INT32_MAX : (v < INT32_MIN ? INT32_MIN : int32_t(v));
 }
-DET_HD int32_t add_sat(int32_t a, int32_t b) { return sat32(int64_t(a) + int64_t(b)); }
-DET_HD int32_t sub_sat(int32_t a, int32_t b) { return sat32(int64_t(a) - int64_t(b)); }
+// (on the GPU: the clamping 32-bit add and subtract)
+DET_HD int32_t add_sat(int32_t a, int32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_elementwise_add_sat(a, b);
+#else
+  return sat32(int64_t(a) + int64_t(b));
+#endif
+}
+DET_HD int32_t sub_sat(int32_t a, int32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_elementwise_sub_sat(a, b);
+#else
+  return sat32(int64_t(a) - int64_t(b));
+#endif
+}
 DET_HD int32_t neg_sat32(int32_t a) { return a == INT32_MIN ? INT32_MAX : -a; }
 DET_HD int64_t neg_sat64(int64_t a) { return a == INT64_MIN ? INT64_MAX : -a; }
 DET_HD int64_t add_sat64(int64_t a, int64_t b) {
   int64_t r;
   if (__builtin_add_overflow(a, b, &r)) return a < 0 ? INT64_MIN : INT64_MAX;
   return r;
+}
+// add_sat64 for a, b >= 0: the unsigned sum stays below 2^64, and a set top
+// bit (a sum past i64::MAX) turns the result into i64::MAX.
+DET_HD int64_t add_sat64_nn(int64_t a, int64_t b) {
+  const uint64_t s = uint64_t(a) + uint64_t(b);
+  const uint32_t m = uint32_t(int32_t(uint32_t(s >> 32)) >> 31);  // all ones past i64::MAX
+  const uint32_t lo = uint32_t(s) | m, hi = (uint32_t(s >> 32) | m) & 0x7fffffffu;
+  return int64_t((uint64_t(hi) << 32) | lo);
 }
 // Wrapping i64 MAC (ops.rs:14-16).
 DET_HD int64_t mac(int64_t acc, int32_t a, int32_t w) {
@@ -50,8 +71,36 @@ DET_HD int64_t rshift_rte(int64_t x, unsigned s) {
 }
 
 // requantize: Q32.32 -> Q16.16, ties to even, saturating (ops.rs:445-448).
-DET_HD int32_t requant(int64_t acc) { return sat32(rshift_rte(acc, 16)); }
-DET_HD int32_t mul_sat(int32_t a, int32_t b) { return requant(int64_t(a) * int64_t(b)); }
+// On the GPU in 32-bit halves: with b = bit 16 of x (the low bit of the floor
+// quotient q), floor((x + 0x7fff + b) / 2^16) is q rounded half to even. For
+// x in [-2^47, 2^47) (high word in [-2^15, 2^15)) the sum y does not wrap and
+// the quotient is y's bits 16..47, exact when y's high word is in range as
+// well; every other x saturates with its sign.
+DET_HD int32_t requant(int64_t acc) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t xl = uint32_t(uint64_t(acc)), xh = uint32_t(uint64_t(acc) >> 32);
+  const uint64_t y = uint64_t(acc) + (0x7fffu + ((xl >> 16) & 1u));
+  const uint32_t yl = uint32_t(y), yh = uint32_t(y >> 32);
+  const int32_t q = int32_t(__builtin_amdgcn_alignbit(yh, yl, 16));
+  const bool ok = (xh + 0x8000u < 0x10000u) & (yh + 0x8000u < 0x10000u);
+  return ok ? q : int32_t((uint32_t(int32_t(xh) >> 31)) ^ 0x7fffffffu);
+#else
+  return sat32(rshift_rte(acc, 16));
+#endif
+}
+// |a b| <= 2^62, so the rounding sum of requant never wraps and the range
+// test needs y's high word only.
+DET_HD int32_t mul_sat(int32_t a, int32_t b) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint64_t p = uint64_t(int64_t(a) * int64_t(b));
+  const uint64_t y = p + (0x7fffu + ((uint32_t(p) >> 16) & 1u));
+  const uint32_t yl = uint32_t(y), yh = uint32_t(y >> 32);
+  const int32_t q = int32_t(__builtin_amdgcn_alignbit(yh, yl, 16));
+  return yh + 0x8000u < 0x10000u ? q : int32_t((uint32_t(int32_t(yh) >> 31)) ^ 0x7fffffffu);
+#else
+  return requant(int64_t(a) * int64_t(b));
+#endif
+}
 
 // Round |n| / d to nearest with ties to even on the magnitude, sign restored
 // (the reference's round_ties_even_division for |quotient| < 2^63).

@@ -783,7 +783,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
     for (int k = 0; k < 4; ++k) {
       const int32_t o = on ? requant(sv[e][k]) : 0;
       sv[e][k] = o;
-      ss = add_sat64(ss, sq_term(o));
+      ss = add_sat64_nn(ss, sq_term(o));
     }
   }
   const int32_t s1 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane);
@@ -797,7 +797,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
       if (ni.has_scalar) v = mul_sat(v, ni.scalar);
       v = on ? v : 0;
       xv[e][k] = v;
-      ss = add_sat64(ss, sq_term(v));
+      ss = add_sat64_nn(ss, sq_term(v));
     }
   }
   const int32_t s2 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane);
@@ -1237,7 +1237,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const int32_t* src, int32_t* ds
   if (row >= rows) return;
   const int32_t* xr = src + row * ld;
   int64_t ss = 0;
-  for (uint64_t c = lane; c < cols; c += 64) ss = add_sat64(ss, sq_term(xr[c]));
+  for (uint64_t c = lane; c < cols; c += 64) ss = add_sat64_nn(ss, sq_term(xr[c]));
   ss = wave_sum_sat(ss);
   const int32_t scale = rms_scale_from_sumsq(ss, uint32_t(cols), eps);
   // each element is read (src, res) and written (dst) by the same lane, so
@@ -1268,7 +1268,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_wide(const int32_t* src, int32_t
     const uint64_t c = threadIdx.x + uint64_t(NT) * e;
     v[e] = c < cols ? xr[c] : 0;
     g[e] = (w && c < cols) ? w[c] : 0;
-    ss = add_sat64(ss, sq_term(v[e]));
+    ss = add_sat64_nn(ss, sq_term(v[e]));
   }
   ss = wave_sum_sat(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
@@ -1310,7 +1310,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_add_norm(const int32_t* __restri
     xv[e] = in ? x[row * ld + c] : 0;
     g1[e] = (w1 && in) ? w1[c] : 0;
     g2[e] = (w2 && in) ? w2[c] : 0;
-    ss = add_sat64(ss, sq_term(v[e]));
+    ss = add_sat64_nn(ss, sq_term(v[e]));
   }
   auto block_scale = [&](int k, int64_t part) {
     part = wave_sum_sat(part);
@@ -1329,7 +1329,7 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_add_norm(const int32_t* __restri
     const int32_t y = mul_sat(v[e], s1);
     xv[e] = c < cols ? add_sat(w1 ? mul_sat(y, g1[e]) : y, xv[e]) : 0;
     if (c < cols) x[row * ld + c] = xv[e];
-    ss = add_sat64(ss, sq_term(xv[e]));
+    ss = add_sat64_nn(ss, sq_term(xv[e]));
   }
   const int32_t s2 = block_scale(1, ss);
 #pragma unroll

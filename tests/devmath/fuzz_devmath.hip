@@ -42,6 +42,7 @@ int main(int argc, char** argv) {
   long bad;
   bad = 0; for (long i = 0; i < N; ++i) { int64_t x = pick64(); if (det::requant(x) != orc_requantize(x)) bad++; } report("requant", N, bad);
   bad = 0; for (long i = 0; i < N; ++i) { int32_t a = pick32(), b = pick32(); if (det::mul_sat(a, b) != orc_mul_sat(a, b)) bad++; } report("mul_sat", N, bad);
+  bad = 0; for (long i = 0; i < N; ++i) { int64_t a = pick64(), b = pick64(); if (a < 0) a = -(a + 1); if (b < 0) b = -(b + 1); if (det::add_sat64_nn(a, b) != orc_acc_add_sat(a, b)) bad++; } report("add_sat64_nn", N, bad);
   bad = 0; for (long i = 0; i < N; ++i) { int32_t a = pick32(), b = pick32(); if (!b) continue; int32_t o; orc_div_act(a, b, &o); if (det::div_act(a, b) != o) bad++; } report("div_act", N, bad);
   bad = 0; for (long i = 0; i < N; ++i) { int64_t v = pick64(); uint32_t d = uint32_t(rng()) >> (rng() % 32); if (!d) d = 1; int64_t o; orc_div_acc_by_u32(v, d, &o); if (det::div_acc_u32(v, d) != o) bad++; } report("div_acc_u32", N, bad);
   bad = 0; for (long i = 0; i < N; ++i) { int64_t a = pick64(), b = pick64(); if (det::acc_mul(a, b) != orc_acc_mul(a, b)) bad++; } report("acc_mul", N, bad);

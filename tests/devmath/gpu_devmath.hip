@@ -38,6 +38,22 @@ __global__ void k_rms_scale(const int64_t* __restrict__ ss, const uint32_t* __re
   if (i < n) out[i] = det::rms_scale_from_sumsq(ss[i], cnt[i], eps[i]);
 }
 
+__global__ void k_requant(const int64_t* __restrict__ x, int32_t* __restrict__ out, uint64_t n) {
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = det::requant(x[i]);
+}
+// op 0: mul_sat, 1: add_sat, 2: sub_sat
+__global__ void k_binop(const int32_t* __restrict__ a, const int32_t* __restrict__ b, int op, int32_t* __restrict__ out,
+                        uint64_t n) {
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = op == 0 ? det::mul_sat(a[i], b[i]) : (op == 1 ? det::add_sat(a[i], b[i]) : det::sub_sat(a[i], b[i]));
+}
+__global__ void k_add_sat64_nn(const int64_t* __restrict__ a, const int64_t* __restrict__ b, int64_t* __restrict__ out,
+                               uint64_t n) {
+  const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = det::add_sat64_nn(a[i], b[i]);
+}
+
 static std::mt19937_64 rng(777);
 
 template <class T>
@@ -162,6 +178,120 @@ int main(int argc, char** argv) {
       if (got[i] != want[i] && ++bad < 5) printf("  rms_scale ss=%lld n=%u gpu=%d orc=%d\n", (long long)ss[i], cnt[i], got[i], want[i]);
     printf("gpu_rms_scale %ld %ld\n", M, bad);
     failures += bad != 0;
+  }
+  // requant (Q32.32 -> Q16.16, ties to even, saturating): every magnitude, the
+  // saturation edges +-2^47 with the rounding offsets around them, exact ties
+  // with odd and even quotients, and the i64 extremes
+  {
+    std::vector<int64_t> xs;
+    for (long i = 0; i < N; ++i) xs.push_back(int64_t(rng()) >> (rng() % 64));
+    const int64_t edge = int64_t(1) << 47;
+    for (int64_t base : {edge, -edge, int64_t(0), INT64_MAX, INT64_MIN, edge - 0x10000, -edge + 0x10000})
+      for (int64_t d = -0x18000; d <= 0x18000; d += 0x100) {
+        int64_t x;
+        if (!__builtin_add_overflow(base, d, &x)) xs.push_back(x);
+        for (int64_t e : {-1, 0, 1, 0x7fff, 0x8000, 0x8001})
+          if (!__builtin_add_overflow(base, d + e, &x)) xs.push_back(x);
+      }
+    for (long i = 0; i < N / 10; ++i) {  // ties
+      const int64_t q = int64_t(rng()) >> (17 + rng() % 40);
+      xs.push_back(q * 65536 + 0x8000);
+    }
+    int64_t* dx = to_dev(xs);
+    int32_t* dout = nullptr;
+    CK(hipMalloc(&dout, xs.size() * 4));
+    hipLaunchKernelGGL(k_requant, dim3(unsigned((xs.size() + 255) / 256)), dim3(256), 0, 0, dx, dout, uint64_t(xs.size()));
+    CK(hipGetLastError());
+    std::vector<int32_t> got(xs.size());
+    CK(hipMemcpy(got.data(), dout, xs.size() * 4, hipMemcpyDeviceToHost));
+    long bad = 0;
+    for (size_t i = 0; i < xs.size(); ++i) {
+      const int32_t o = orc_requantize(xs[i]);
+      if (got[i] != o && ++bad < 5) printf("  requant x=%lld gpu=%d orc=%d\n", (long long)xs[i], got[i], o);
+    }
+    printf("gpu_requant %zu %ld\n", xs.size(), bad);
+    failures += bad != 0;
+    CK(hipFree(dx));
+    CK(hipFree(dout));
+  }
+  // mul_sat / add_sat / sub_sat: random operands at every magnitude, the
+  // extremes, products next to the saturation edges and exact ties
+  {
+    std::vector<int32_t> as, bs;
+    const int32_t ext[] = {INT32_MIN, INT32_MIN + 1, -65536, -1, 0, 1, 65536, INT32_MAX - 1, INT32_MAX};
+    for (int32_t a : ext)
+      for (int32_t b : ext) as.push_back(a), bs.push_back(b);
+    for (long i = 0; i < N; ++i) {
+      as.push_back(int32_t(rng()) >> (rng() % 32));
+      bs.push_back(int32_t(rng()) >> (rng() % 32));
+    }
+    for (long i = 0; i < N / 4; ++i) {  // a b next to +-2^47 and +-2^47 - 2^15
+      int32_t a = int32_t(rng()) >> (rng() % 31);
+      if (a == 0) a = 3;
+      const int64_t t = ((rng() & 1) ? 1 : -1) * ((int64_t(1) << 47) - ((rng() & 1) ? 0x8000 : 0));
+      const int64_t b0 = t / a;
+      for (int64_t db = -2; db <= 2; ++db) {
+        const int64_t b = b0 + db;
+        if (b >= INT32_MIN && b <= INT32_MAX) as.push_back(a), bs.push_back(int32_t(b));
+      }
+    }
+    for (long i = 0; i < N / 10; ++i) {  // exact ties: a b = q 2^16 + 2^15 with a = 2^k
+      const int k = int(rng() % 16);
+      as.push_back(int32_t(1) << k);
+      bs.push_back(int32_t((int32_t(rng()) >> (rng() % 20)) | (1 << (15 - k))) & ~((1 << (15 - k)) - 1));
+    }
+    int32_t* da = to_dev(as);
+    int32_t* db = to_dev(bs);
+    int32_t* dout = nullptr;
+    CK(hipMalloc(&dout, as.size() * 4));
+    const char* names[] = {"gpu_mul_sat", "gpu_add_sat", "gpu_sub_sat"};
+    for (int op = 0; op < 3; ++op) {
+      hipLaunchKernelGGL(k_binop, dim3(unsigned((as.size() + 255) / 256)), dim3(256), 0, 0, da, db, op, dout,
+                         uint64_t(as.size()));
+      CK(hipGetLastError());
+      std::vector<int32_t> got(as.size());
+      CK(hipMemcpy(got.data(), dout, as.size() * 4, hipMemcpyDeviceToHost));
+      long bad = 0;
+      for (size_t i = 0; i < as.size(); ++i) {
+        const int32_t o = op == 0 ? orc_mul_sat(as[i], bs[i]) : (op == 1 ? orc_add_sat(as[i], bs[i]) : orc_sub_sat(as[i], bs[i]));
+        if (got[i] != o && ++bad < 5) printf("  %s a=%d b=%d gpu=%d orc=%d\n", names[op], as[i], bs[i], got[i], o);
+      }
+      printf("%s %zu %ld\n", names[op], as.size(), bad);
+      failures += bad != 0;
+    }
+    CK(hipFree(da));
+    CK(hipFree(db));
+    CK(hipFree(dout));
+  }
+  // add_sat64_nn: non-negative operands at every magnitude and around i64::MAX
+  {
+    std::vector<int64_t> as, bs;
+    for (long i = 0; i < N; ++i) {
+      as.push_back(int64_t(rng() >> 1) >> (rng() % 63));
+      bs.push_back(int64_t(rng() >> 1) >> (rng() % 63));
+    }
+    for (int64_t a : {int64_t(0), int64_t(1), INT64_MAX, INT64_MAX - 1, INT64_MAX / 2, INT64_MAX / 2 + 1, int64_t(1) << 62})
+      for (int64_t b : {int64_t(0), int64_t(1), INT64_MAX, INT64_MAX / 2, INT64_MAX / 2 + 1, int64_t(1) << 62})
+        as.push_back(a), bs.push_back(b);
+    int64_t* da = to_dev(as);
+    int64_t* db = to_dev(bs);
+    int64_t* dout = nullptr;
+    CK(hipMalloc(&dout, as.size() * 8));
+    hipLaunchKernelGGL(k_add_sat64_nn, dim3(unsigned((as.size() + 255) / 256)), dim3(256), 0, 0, da, db, dout,
+                       uint64_t(as.size()));
+    CK(hipGetLastError());
+    std::vector<int64_t> got(as.size());
+    CK(hipMemcpy(got.data(), dout, as.size() * 8, hipMemcpyDeviceToHost));
+    long bad = 0;
+    for (size_t i = 0; i < as.size(); ++i) {
+      const int64_t o = orc_acc_add_sat(as[i], bs[i]);
+      if (got[i] != o && ++bad < 5) printf("  add_sat64_nn a=%lld b=%lld gpu=%lld orc=%lld\n", (long long)as[i], (long long)bs[i], (long long)got[i], (long long)o);
+    }
+    printf("gpu_add_sat64_nn %zu %ld\n", as.size(), bad);
+    failures += bad != 0;
+    CK(hipFree(da));
+    CK(hipFree(db));
+    CK(hipFree(dout));
   }
   return failures ? 1 : 0;
 }

@@ -23,5 +23,5 @@ def test_device_arithmetic_matches_oracle():
     bad = {name: (int(n), int(b)) for name, n, b in rows if int(b)}
     assert res.returncode == 0 and not bad, res.stdout
     names = {r[0] for r in rows}
-    assert {"requant", "inv_sqrt_acc", "inv_sqrt_acc_edges", "softmax_exp_all_gaps", "softmax_weight",
+    assert {"requant", "add_sat64_nn", "inv_sqrt_acc", "inv_sqrt_acc_edges", "softmax_exp_all_gaps", "softmax_weight",
             "softmax_weight_recip", "div_rte_nonneg", "sin_cos", "rope", "gelu"} <= names
