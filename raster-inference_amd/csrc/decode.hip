@@ -663,20 +663,22 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
 // Single-kernel form for small grids (one sequence, short windows): integer
 // softmax (ops.rs:230-258) and weighted sum (ops.rs:336-351) over
 // P chunks of kAttnWsumRows window rows for every query head of one KV head,
-// 1024 threads. Each workgroup rebuilds the heads' argmax (first maximum) and exp
-// sum over the whole window from the scores, with 16 / G waves per head (each
-// thread keeps the scores it reads in LDS for the later passes when they
-// fit), weights its own rows, and adds its wrapping partial sums to the
-// accumulators atomically (exact in any order). The workgroup holding a
-// head's argmax row also sums every weight of the window and applies the
-// residual ONE - sum to that row, as the reference does before the weighted
-// sum. Workgroup 0 clears the projection accumulators read by the scores kernel.
+// 1024 threads. Each workgroup rebuilds the heads' statistics over the whole
+// window, with 16 / G waves per head: the first argmax from the scores
+// kernel's per-chunk argmax keys (every wave of a head reduces all of them,
+// so no barrier), the exp sum from the scores (the first NS of each thread's
+// rows held in registers from the start), then weights its own rows and
+// adds its wrapping partial sums to the accumulators atomically (exact in any
+// order). The workgroup holding a head's argmax row also sums every weight of
+// the window and applies the residual ONE - sum to that row, as the reference
+// does before the weighted sum. Workgroup 0 clears the projection
+// accumulators read by the scores kernel.
 template <int P, uint32_t MAXHD>
 __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   constexpr uint32_t R = P * kAttnWsumRows;  // window rows of this workgroup
-  extern __shared__ int32_t sl_dyn[];
+  constexpr int NS = 4;                       // score rows per thread held in registers
   __shared__ int64_t red[16];
-  __shared__ int64_t hkey[kDecMaxGroup], hsum[kDecMaxGroup];
+  __shared__ int64_t hsum[kDecMaxGroup];
   __shared__ uint64_t hrec[kDecMaxGroup];
   __shared__ int64_t el[kDecMaxGroup][R];
   __shared__ int32_t wl[kDecMaxGroup][R];
@@ -701,13 +703,14 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;
   const bool active = g < G;
   const uint64_t stride = 64 * uint64_t(wph);
-  const int32_t* scg = a.scores + (uint64_t(kvh) * G + (active ? g : 0)) * a.max_rows;
-  const bool lds = a.scores_in_lds;  // the window's scores (then exp terms) kept in LDS
-  int32_t* scl = sl_dyn + uint64_t(active ? g : 0) * a.lds_stride;  // (written only when lds)
-  // The first NS of this thread's scores are read before the value rows (loads
-  // complete in issue order, and the value rows are needed last); clamped
-  // addresses, so that no load is predicated.
-  constexpr int NS = 4;
+  const uint64_t head = uint64_t(kvh) * G + (active ? g : 0);
+  const int32_t* scg = a.scores + head * a.max_rows;
+  const uint64_t nch = (win.cnt + kAttnScoreRows - 1) / kAttnScoreRows;
+  // The chunk keys and the first NS of this thread's scores are read before
+  // the value rows (loads complete in issue order, and the value rows are
+  // needed last); clamped addresses, so that no load is predicated.
+  const int64_t* keys = a.keys + head * a.key_chunks;
+  const int64_t k0 = keys[lane < nch ? lane : nch - 1];
   int32_t sv[NS];
 #pragma unroll
   for (int n = 0; n < NS; ++n) {
@@ -731,66 +734,26 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
         vp[p][jj][k] = vcache[phys_row(a, win, r0 + (rr < nr ? rr : nr - 1)) * kvw + (d < hd ? d : hd - 1)];
       }
   asm volatile("" ::: "memory");
-  // (masked once the loads are all issued)
-  auto mask_values = [&]() {
-#pragma unroll
-    for (int p = 0; p < P; ++p)
-#pragma unroll
-      for (int jj = 0; jj < JJ; ++jj)
-#pragma unroll
-        for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
-          const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
-          if (!(dl + 256 * jj < hd && rr < nr)) vp[p][jj][k] = 0;
-        }
-  };
-  // argmax (and the LDS copy of this thread's scores)
-  int64_t best = INT64_MIN;
+  // the head's first argmax: the largest chunk key (every wave of the head
+  // reduces all of them)
+  int64_t best = lane < nch ? k0 : INT64_MIN;
+  for (uint64_t c = lane + 64; c < nch; c += 64) best = keys[c] > best ? keys[c] : best;
+  best = wmax(best);
+  const int32_t mx = int32_t(best >> 32);
+  const uint64_t mi = 0xffffffffull - (uint64_t(best) & 0xffffffffull);
+  // exp terms (non-negative, total below 2^63: the saturating sum is the plain
+  // sum); this workgroup's rows go to LDS
+  int64_t ev[NS];
+  int64_t s = 0;
   if (active) {
 #pragma unroll
     for (int n = 0; n < NS; ++n) {
       const uint64_t r = wi * 64 + lane + stride * n;
-      const int64_t k = r < win.cnt ? score_key(sv[n], r) : INT64_MIN;
-      best = k > best ? k : best;
-      if (lds && r < win.cnt) scl[r] = sv[n];
+      ev[n] = r < win.cnt ? softmax_exp(sv[n], mx) : 0;
+      s += ev[n];
+      if (r >= r0 && r < r0 + nr) el[g][r - r0] = ev[n];
     }
     for (uint64_t r = wi * 64 + lane + stride * NS; r < win.cnt; r += stride) {
-      const int32_t v = scg[r];
-      if (lds) scl[r] = v;
-      const int64_t k = score_key(v, r);
-      best = k > best ? k : best;
-    }
-  }
-  mask_values();
-  best = wmax(best);
-  if (lane == 0) red[wave] = best;
-  __syncthreads();
-  if (threadIdx.x < G) {
-    int64_t k = red[threadIdx.x * wph];
-    for (uint32_t w = 1; w < wph; ++w) k = red[threadIdx.x * wph + w] > k ? red[threadIdx.x * wph + w] : k;
-    hkey[threadIdx.x] = k;
-  }
-  __syncthreads();
-  const int64_t key = hkey[active ? g : 0];
-  const int32_t mx = int32_t(key >> 32);
-  const uint64_t mi = 0xffffffffull - (uint64_t(key) & 0xffffffffull);
-  // exp sum (non-negative terms with a total below 2^63: the saturating sum is
-  // the plain sum); this chunk's terms go to LDS
-  int64_t s = 0;
-  // With the scores in LDS each exp term replaces its score there for the
-  // residual pass (2^32, the argmax row's term, is stored as 0xffffffff: every
-  // other term is at most 2^32 - 2^16).
-  // (the scores in LDS and in global memory take separate loops, so that
-  // neither compiles to FLAT accesses)
-  if (active && lds) {
-    int32_t* scs = sl_dyn + uint64_t(g) * a.lds_stride;
-    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
-      const int64_t e = softmax_exp(scs[r], mx);
-      s += e;
-      if (r >= r0 && r < r0 + nr) el[g][r - r0] = e;
-      scs[r] = int32_t(e == kOneAcc ? 0xffffffffu : uint32_t(e));
-    }
-  } else if (active) {
-    for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
       const int64_t e = softmax_exp(scg[r], mx);
       s += e;
       if (r >= r0 && r < r0 + nr) el[g][r - r0] = e;
@@ -805,6 +768,16 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
     hsum[threadIdx.x] = t;
     hrec[threadIdx.x] = t < (int64_t(1) << 61) ? softmax_recip(t) : 0;  // 0: generic division
   }
+  // (masked once the loads are all issued)
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int jj = 0; jj < JJ; ++jj)
+#pragma unroll
+      for (int k = 0; k < int(kAttnWsumRows / 4); ++k) {
+        const uint64_t rr = p * kAttnWsumRows + sl * (kAttnWsumRows / 4) + k;
+        if (!(dl + 256 * jj < hd && rr < nr)) vp[p][jj][k] = 0;
+      }
   __syncthreads();
   // raw weights of this workgroup's rows
   for (uint32_t idx = threadIdx.x; idx < G * R; idx += 1024) {
@@ -819,31 +792,24 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   if (owner) {
     const int64_t S = hsum[g];
     const uint64_t M = hrec[g];
-    if (lds) {
-      const int32_t* scs = sl_dyn + uint64_t(g) * a.lds_stride;
-      for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
-        const uint32_t u = uint32_t(scs[r]);
-        const int64_t e = u == 0xffffffffu ? kOneAcc : int64_t(u);
-        ws += M ? softmax_weight_r(e, S, M) : softmax_weight(e, S);
-      }
-    } else {
-      for (uint64_t r = wi * 64 + lane; r < win.cnt; r += stride) {
-        const int64_t e = softmax_exp(scg[r], mx);
-        ws += M ? softmax_weight_r(e, S, M) : softmax_weight(e, S);
-      }
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+      const uint64_t r = wi * 64 + lane + stride * n;
+      if (r < win.cnt) ws += M ? softmax_weight_r(ev[n], S, M) : softmax_weight(ev[n], S);
+    }
+    for (uint64_t r = wi * 64 + lane + stride * NS; r < win.cnt; r += stride) {
+      const int64_t e = softmax_exp(scg[r], mx);
+      ws += M ? softmax_weight_r(e, S, M) : softmax_weight(e, S);
     }
   }
   ws = wsum_wrap(ws);
   __syncthreads();  // red[] from the exp sums has been read
   if (lane == 0) red[wave] = ws;
   __syncthreads();
-  if (threadIdx.x < G) {
-    const uint64_t m = 0xffffffffull - (uint64_t(hkey[threadIdx.x]) & 0xffffffffull);
-    if (m >= r0 && m < r0 + nr) {
-      int64_t t = 0;
-      for (uint32_t w = 0; w < wph; ++w) t += red[threadIdx.x * wph + w];
-      wl[threadIdx.x][m - r0] = add_sat(wl[threadIdx.x][m - r0], sub_sat(kOneAct, sat32(t)));
-    }
+  if (active && wi == 0 && lane == 0 && owner) {
+    int64_t t = 0;
+    for (uint32_t w = 0; w < wph; ++w) t += red[g * wph + w];
+    wl[g][mi - r0] = add_sat(wl[g][mi - r0], sub_sat(kOneAct, sat32(t)));
   }
   __syncthreads();
   // weighted sums: 4 row slices per dim, combined in LDS for up to 1024 / dstr
@@ -1064,9 +1030,7 @@ void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
   } else if (part == 2) {
     DET_ATTN_P(P, a.hd, k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, P * kAttnWsumRows), ns), dim3(1024), 0, s, a);
   } else {
-    const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.lds_stride * 4 : 0;
-    DET_ATTN_P(P, a.hd, k_dec_attn_softmax_wsum, dim3(a.nkv, nblk(a.cap, P * kAttnWsumRows), ns), dim3(1024), lds, s,
-               a);
+    DET_ATTN_P(P, a.hd, k_dec_attn_softmax_wsum, dim3(a.nkv, nblk(a.cap, P * kAttnWsumRows), ns), dim3(1024), 0, s, a);
   }
 }
 #undef DET_ATTN_P

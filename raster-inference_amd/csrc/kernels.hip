@@ -689,12 +689,14 @@ __device__ __forceinline__ void lds_barrier() {
 // rms scale of a row spread over the workgroup from each thread's saturating
 // partial sum of squares (ops.rs:406-425): wave 0 reduces the wave totals and
 // runs the scale chain once.
-template <int NW>
+// `between` runs in every wave once all waves have passed their partial sums.
+template <int NW, class F>
 __device__ __forceinline__ int32_t wg_rms_scale(int64_t ss, uint64_t n, int64_t eps, int64_t* red, int32_t* bc,
-                                                int wave, int lane) {
+                                                int wave, int lane, F&& between) {
   ss = wave_sum_sat(ss);
   if (lane == 0) red[wave] = ss;
   lds_barrier();
+  between();
   if (wave == 0) {
     int64_t t = lane < NW ? red[lane] : 0;
     t = wave_sum_sat(t);
@@ -748,32 +750,32 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
   const int32_t ers = rowsum[erc], esc = scale[erc];
   // 2. this wave's jobs: weight loads of up to D steps each (steps past the
   // part re-read its last step and meet zero A operands). Slots past the
-  // workgroup's jobs load one line at q, never combined. The loads are
-  // unconditional and nothing is stored before the MFMAs, so every wait of
-  // the norm below counts only the loads above.
+  // workgroup's jobs load one line at q, never combined. They are issued once
+  // every wave of the workgroup holds the norm's inputs: the inputs' reads
+  // are not queued behind the weight stream (whose bytes stay in flight
+  // through the rest of the norm).
   uint64_t js0[JM], jnu[JM];
   v4i b[JM][2 * D];
+  auto issue_weights = [&]() {
 #pragma unroll
-  for (int u = 0; u < JM; ++u) {
-    const uint64_t jb = uint64_t(wave) + uint64_t(NW) * u;
-    const uint64_t tl = jb / np, p = jb % np;
-    const uint64_t tile = uint64_t(blockIdx.x) + G * tl;
-    const bool real = jb < njobs && tile < ntiles;  // wave-uniform
-    js0[u] = real ? p * D : 0;
-    jnu[u] = real ? (nsteps - js0[u] < uint64_t(D) ? nsteps - js0[u] : uint64_t(D)) : 1;
-    const v4i* bp = real ? reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 32)
-                         : reinterpret_cast<const v4i*>(q);
-    const uint64_t sstride = real ? 128 : 0;
+    for (int u = 0; u < JM; ++u) {
+      const uint64_t jb = uint64_t(wave) + uint64_t(NW) * u;
+      const uint64_t tl = jb / np, p = jb % np;
+      const uint64_t tile = uint64_t(blockIdx.x) + G * tl;
+      const bool real = jb < njobs && tile < ntiles;  // wave-uniform
+      js0[u] = real ? p * D : 0;
+      jnu[u] = real ? (nsteps - js0[u] < uint64_t(D) ? nsteps - js0[u] : uint64_t(D)) : 1;
+      const v4i* bp = real ? reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 32)
+                           : reinterpret_cast<const v4i*>(q);
+      const uint64_t sstride = real ? 128 : 0;
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const uint64_t st = js0[u] + (uint64_t(d) < jnu[u] ? uint64_t(d) : jnu[u] - 1);
-      b[u][2 * d] = __builtin_nontemporal_load(bp + st * sstride);
-      b[u][2 * d + 1] = __builtin_nontemporal_load(bp + st * sstride + (real ? 1 : 0));
+      for (int d = 0; d < D; ++d) {
+        const uint64_t st = js0[u] + (uint64_t(d) < jnu[u] ? uint64_t(d) : jnu[u] - 1);
+        b[u][2 * d] = __builtin_nontemporal_load(bp + st * sstride);
+        b[u][2 * d + 1] = __builtin_nontemporal_load(bp + st * sstride + (real ? 1 : 0));
+      }
     }
-  }
-  // (the loads stay above the norm: nothing below may be hoisted over them or they sunk under it)
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
+  };
   // 3. residual norm of the whole row
   int64_t ss = 0;
 #pragma unroll
@@ -786,7 +788,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
       ss = add_sat64_nn(ss, sq_term(o));
     }
   }
-  const int32_t s1 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane);
+  const int32_t s1 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane, issue_weights);
   ss = 0;
 #pragma unroll
   for (int e = 0; e < QPT; ++e) {
@@ -800,7 +802,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
       ss = add_sat64_nn(ss, sq_term(v));
     }
   }
-  const int32_t s2 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane);
+  const int32_t s2 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane, [] {});
   // limb planes of the normalised row (quads past H are zero, to kpad / 4)
   const uint64_t kq = kpad / 4;
 #pragma unroll
