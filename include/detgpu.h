@@ -37,6 +37,7 @@ typedef struct det_matrix det_matrix_t;
 typedef struct det_model det_model_t;
 typedef struct det_session det_session_t;
 typedef struct det_event det_event_t;
+typedef struct det_graph det_graph_t;
 typedef struct det_kv det_kv_t;
 typedef struct det_scratch det_scratch_t;
 
@@ -61,6 +62,19 @@ int det_event_create(det_ctx_t* ctx, det_event_t** out);
 int det_event_record(det_ctx_t* ctx, det_event_t* ev);
 int det_event_elapsed_ms(det_ctx_t* ctx, det_event_t* start, det_event_t* stop, float* ms);
 void det_event_destroy(det_event_t* ev);
+
+/* A fixed sequence of calls on the context stream, recorded once and replayed
+   as one HIP graph (no counterpart in the reference: for callers that issue
+   the same short kernels repeatedly, where the per-call host launch cost
+   would exceed the GPU time). Between begin and end the calls are recorded,
+   not run; only calls that allocate nothing and do not synchronize may be
+   recorded (run each once beforehand so that their scratch exists), and the
+   buffers they name must outlive the graph. A failed or refused call ends
+   the capture. */
+int det_ctx_capture_begin(det_ctx_t* ctx);
+int det_ctx_capture_end(det_ctx_t* ctx, det_graph_t** out);
+int det_graph_launch(det_ctx_t* ctx, det_graph_t* g);
+void det_graph_destroy(det_graph_t* g);
 
 /* ------------------------------------------------------------------------ */
 /* Weights: DetNumMatrix (src/shared/model/transformer.rs:194-198)            */

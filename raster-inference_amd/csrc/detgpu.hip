@@ -64,6 +64,8 @@ struct det_ctx {
 
   int8_t* gemm_a = nullptr;  // tiled activation limb rows for the prefill GEMM
   size_t gemm_a_bytes = 0;
+  int64_t* gemm_planes = nullptr;  // K-range partial planes of split GEMMs
+  size_t gemm_planes_bytes = 0;
 
   void ensure_gemm_a(size_t bytes) {
     if (bytes <= gemm_a_bytes) return;
@@ -73,6 +75,19 @@ struct det_ctx {
     HIPC(hipMalloc(&gemm_a, bytes));
     gemm_a_bytes = bytes;
   }
+  // the partial planes a GEMM of W over m rows splits K into (null: no split)
+  int64_t* gemm_planes_for(const det::DevMatrix& W, uint64_t m) {
+    const size_t bytes = det::gemm_plane_bytes(W, m);
+    if (bytes == 0) return nullptr;
+    if (bytes > gemm_planes_bytes) {
+      HIPC(hipStreamSynchronize(stream));
+      if (gemm_planes) HIPC(hipFree(gemm_planes));
+      gemm_planes = nullptr;
+      HIPC(hipMalloc(&gemm_planes, bytes));
+      gemm_planes_bytes = bytes;
+    }
+    return gemm_planes;
+  }
   // Slab GEMM / GEMV dispatch: int8 weights with at least kGemmMinRows
   // activation rows take the MFMA GEMM, everything else the GEMV kernels.
   static constexpr uint64_t kGemmMinRows = 16;
@@ -80,7 +95,8 @@ struct det_ctx {
               int64_t* acc_out) {
     if (W.storage == det::kInt8 && m >= kGemmMinRows) {
       ensure_gemm_a(det::gemm_act_bytes(m, W.kpad));
-      det::launch_gemm(W, act, m, ld_act, out, ld_out, acc_out, gemm_a, stream);
+      int64_t* planes = gemm_planes_for(W, m);
+      det::launch_gemm(W, act, m, ld_act, out, ld_out, acc_out, gemm_a, stream, planes);
     } else {
       det::launch_linear(W, act, m, ld_act, out, ld_out, acc_out, limbs, stream);
     }
@@ -100,7 +116,10 @@ struct det_ctx {
     }
     ensure_gemm_a(det::gemm_act_bytes(m, first->kpad));
     det::launch_gemm_limbs(act, m, first->cols, ld_act, first->kpad, gemm_a, stream);
-    for (const auto& it : items) det::launch_gemm_tiled(*it.first, m, it.second, it.first->rows, nullptr, gemm_a, stream);
+    for (const auto& it : items) {
+      int64_t* planes = gemm_planes_for(*it.first, m);
+      det::launch_gemm_tiled(*it.first, m, it.second, it.first->rows, nullptr, gemm_a, stream, nullptr, planes);
+    }
   }
 
   void ensure_limbs(size_t bytes) {
@@ -135,6 +154,14 @@ struct det_matrix {
 
 struct det_event {
   hipEvent_t ev = nullptr;
+};
+struct det_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  ~det_graph() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+  }
 };
 
 namespace {
@@ -1045,7 +1072,7 @@ void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const
     sp.ld1 = sp.ld2 = kw;
     sp.r1 = qw;
     sp.r2 = qw + kw;
-    det::launch_gemm_tiled(*QKV, M, s->qb, qw, nullptr, ctx->gemm_a, st, &sp);
+    det::launch_gemm_tiled(*QKV, M, s->qb, qw, nullptr, ctx->gemm_a, st, &sp, ctx->gemm_planes_for(*QKV, M));
   } else if (L.v) {
     ctx->linear_group({{L.q, s->qb}, {L.k, s->kb}, {L.v, s->vb}}, s->normed, M, L.q->cols);
   } else if (L.k_eq_v) {
@@ -2645,6 +2672,7 @@ void det_ctx_destroy(det_ctx_t* ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->limbs) (void)hipFree(ctx->limbs);
   if (ctx->gemm_a) (void)hipFree(ctx->gemm_a);
+  if (ctx->gemm_planes) (void)hipFree(ctx->gemm_planes);
   if (ctx->argmax_scratch) (void)hipFree(ctx->argmax_scratch);
   if (ctx->argmax_out) (void)hipFree(ctx->argmax_out);
   (void)hipStreamDestroy(ctx->stream);
@@ -2692,6 +2720,26 @@ int det_event_create(det_ctx_t* ctx, det_event_t** out) {
 int det_event_record(det_ctx_t* ctx, det_event_t* ev) {
   return guarded(ctx, [&] { HIPC(hipEventRecord(ev->ev, ctx->stream)); });
 }
+int det_ctx_capture_begin(det_ctx_t* ctx) {
+  return guarded(ctx, [&] { HIPC(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal)); });
+}
+int det_ctx_capture_end(det_ctx_t* ctx, det_graph_t** out) {
+  return guarded(ctx, [&] {
+    if (!out) bail("det_ctx_capture_end requires an output handle");
+    *out = nullptr;
+    auto g = std::make_unique<det_graph>();
+    HIPC(hipStreamEndCapture(ctx->stream, &g->graph));
+    HIPC(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0));
+    *out = g.release();
+  });
+}
+int det_graph_launch(det_ctx_t* ctx, det_graph_t* g) {
+  return guarded(ctx, [&] {
+    if (!g || !g->exec) bail("det_graph_launch requires an instantiated graph");
+    HIPC(hipGraphLaunch(g->exec, ctx->stream));
+  });
+}
+void det_graph_destroy(det_graph_t* g) { delete g; }
 int det_event_elapsed_ms(det_ctx_t* ctx, det_event_t* a, det_event_t* b, float* ms) {
   return guarded(ctx, [&] {
     HIPC(hipEventSynchronize(b->ev));

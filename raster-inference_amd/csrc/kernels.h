@@ -63,10 +63,22 @@ struct RowSplit {
   int32_t* out2 = nullptr;
   uint64_t ld1 = 0, ld2 = 0, r1 = 0, r2 = 0;
 };
+// K split of grids that leave CUs idle (small m): chunk c of the K range
+// writes its wrapping Q32.32 share of every output to planes[c][m][rows]
+// (gemm_plane_bytes(W, m) bytes; the wrapping sum of the chunks is the
+// accumulator exactly), and a second kernel sums them into the outputs.
+// planes == nullptr keeps the single pass.
+struct KSplit {
+  uint32_t chunks = 1;
+  int64_t* planes = nullptr;
+};
+uint32_t gemm_kchunks(const DevMatrix& W, uint64_t m);
+uint64_t gemm_plane_bytes(const DevMatrix& W, uint64_t m);
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                       const int8_t* a_tiled, hipStream_t s, const RowSplit* split = nullptr);
+                       const int8_t* a_tiled, hipStream_t s, const RowSplit* split = nullptr,
+                       int64_t* planes = nullptr);
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
-                 int64_t* acc_out, int8_t* a_tiled, hipStream_t s);
+                 int64_t* acc_out, int8_t* a_tiled, hipStream_t s, int64_t* planes = nullptr);
 
 // Batch-1 int8 GEMV for the fused decode step (int8 storage, fits LDS):
 // act_i64 requantizes wrapped accumulators on load; epilogue 1 applies

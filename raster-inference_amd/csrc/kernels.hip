@@ -1080,7 +1080,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
                                                            uint64_t kpad, uint64_t m_tokens, uint64_t a_tiles,
                                                            uint32_t mblocks, int32_t* __restrict__ out,
                                                            uint64_t ld_out, int64_t* __restrict__ acc_out,
-                                                           RowSplit split) {
+                                                           RowSplit split, KSplit ks) {
   constexpr int NW = WM * WN;                  // waves
   constexpr int TS = TA + TB;                  // tile-steps per K step
   constexpr int LPW = 2 * TS / NW;             // 1 KB wave copies per wave per K step
@@ -1093,15 +1093,21 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   // range of logical blocks; logical blocks go in groups of GM m-blocks x all
   // n-blocks with m fastest, so the blocks resident on one XCD at a time form
   // a compact GM x (resident / GM) patch whose A and weight tiles share its L2.
-  const uint32_t nblk = gridDim.x;
+  // With K split into ks.chunks ranges, chunk c takes logical blocks
+  // [c nblk, (c + 1) nblk) and the same ordering inside them.
+  const uint32_t nall = gridDim.x, nblk = nall / ks.chunks;
   uint32_t logical = blockIdx.x;
-  if (nblk % 8 == 0) logical = (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8;
+  if (nall % 8 == 0) logical = (blockIdx.x % 8) * (nall / 8) + blockIdx.x / 8;
+  const uint32_t chunk = logical / nblk;
+  logical -= chunk * nblk;
   const uint32_t nblocks_n = nblk / mblocks;
   const uint32_t group = logical / (GM * nblocks_n), first_m = group * GM;
   const uint32_t gm = mblocks - first_m < GM ? mblocks - first_m : GM;
   const uint32_t in_group = logical - group * GM * nblocks_n;
   const uint32_t mb = first_m + in_group % gm, nb = in_group / gm;
-  const uint64_t nsteps = kpad / 128;
+  const uint64_t ksteps = kpad / 128, cper = (ksteps + ks.chunks - 1) / ks.chunks;
+  const uint64_t k0 = uint64_t(chunk) * cper < ksteps ? uint64_t(chunk) * cper : ksteps;
+  const uint64_t nsteps = (k0 + cper < ksteps ? k0 + cper : ksteps) - k0;  // this block's K steps
   const uint64_t ntiles = (n_rows + 15) / 16;
   const uint64_t at0 = uint64_t(mb) * TA, bt0 = uint64_t(nb) * TB;
   // this wave's copies: chunk c = wave * LPW + u is tile-step c / 2 (A tiles
@@ -1114,7 +1120,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     const bool is_a = ts < uint32_t(TA);
     uint64_t tile = is_a ? at0 + ts : bt0 + (ts - TA);
     if (is_a ? tile >= a_tiles : tile >= ntiles) tile = (is_a ? a_tiles : ntiles) - 1;
-    src[u] = (is_a ? a : q) + tile * nsteps * 2048 + lane * 32 + h * 16;
+    src[u] = (is_a ? a : q) + (tile * ksteps + k0) * 2048 + lane * 32 + h * 16;
   }
   auto copy_step = [&](uint64_t s, int buf) {
 #pragma unroll
@@ -1188,6 +1194,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
       const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
       if (token >= m_tokens || row >= n_rows) continue;
       const int64_t p[4] = {acc[ti][tj][0], acc[ti][tj][1], acc[ti][tj][2], acc[ti][tj][3]};
+      if (ks.chunks > 1) {
+        // this K range's wrapping share (the chunk holding column 0 adds the offset term)
+        ks.planes[(uint64_t(chunk) * m_tokens + token) * n_rows + row] = limb_combine(p, chunk == 0 ? rowsum[row] : 0, scale[row]);
+        continue;
+      }
       const int64_t v = limb_combine(p, rowsum[row], scale[row]);
       if (SPLIT) {
         // rows [0, r1) to out, [r1, r2) to out1, [r2, n_rows) to out2
@@ -1201,6 +1212,37 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
       } else {
         out[token * ld_out + row] = requant(v);
       }
+    }
+  }
+}
+
+// Sum of the K-range planes of a split GEMM (wrapping, so exactly the
+// accumulator), requantized to out (rows split as in k_gemm_lds) or written
+// to acc_out; two outputs per thread.
+__global__ __launch_bounds__(256) void k_gemm_reduce(const int64_t* __restrict__ planes, uint32_t chunks,
+                                                     uint64_t m_tokens, uint64_t n_rows, int32_t* __restrict__ out,
+                                                     uint64_t ld_out, int64_t* __restrict__ acc_out, RowSplit split) {
+  const uint64_t total = m_tokens * n_rows;
+  const uint64_t e0 = (uint64_t(blockIdx.x) * 256 + threadIdx.x) * 2;
+  if (e0 >= total) return;
+  const uint64_t plane = total;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint64_t e = e0 + h;
+    if (e >= total) break;
+    uint64_t v = 0;
+    for (uint32_t c = 0; c < chunks; ++c) v += uint64_t(planes[c * plane + e]);
+    const uint64_t token = e / n_rows, row = e % n_rows;
+    if (acc_out) {
+      acc_out[token * ld_out + row] = int64_t(v);
+    } else if (split.out1) {
+      int32_t* o = out;
+      uint64_t ld = ld_out, rr = row;
+      if (row >= split.r2) o = split.out2, ld = split.ld2, rr = row - split.r2;
+      else if (row >= split.r1) o = split.out1, ld = split.ld1, rr = row - split.r1;
+      o[token * ld + rr] = requant(int64_t(v));
+    } else {
+      out[token * ld_out + row] = requant(int64_t(v));
     }
   }
 }
@@ -2007,7 +2049,8 @@ uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64
 
 template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT = false>
 static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                                  const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s, RowSplit split = {}) {
+                                  const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s, RowSplit split = {},
+                                  KSplit ks = {}) {
   constexpr uint32_t lds = uint32_t(NBUF) * (TA + TB) * 2048u;
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -2015,9 +2058,33 @@ static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, 
   (void)attr;
   const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
   const uint64_t nblocks = ((W.rows + 15) / 16 + TB - 1) / TB;
-  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT>), dim3(unsigned(mblocks * nblocks)), dim3(64 * WM * WN), lds, s,
-                     a_tiled, W.q, W.scale, W.rowsum, W.rows, W.kpad, m, a_tiles, uint32_t(mblocks), out, ld_out,
-                     acc_out, split);
+  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT>), dim3(unsigned(mblocks * nblocks * ks.chunks)),
+                     dim3(64 * WM * WN), lds, s, a_tiled, W.q, W.scale, W.rowsum, W.rows, W.kpad, m, a_tiles,
+                     uint32_t(mblocks), out, ld_out, acc_out, split, ks);
+}
+
+// K split of a GEMM whose 128 x 128 blocks leave CUs idle: chunks of at least
+// four K steps, up to one block per CU (a second block on a CU shares its LDS
+// bandwidth, which bounds a block's K step), with their partial planes within
+// kGemmPlaneBudget bytes, and only where it saves at least kGemmSplitMinSteps
+// K steps per block: the planes' stores and the summing kernel cost about
+// that much (measured on E4B's projections at 128 rows).
+constexpr uint64_t kGemmPlaneBudget = uint64_t(16) << 20;
+constexpr uint64_t kGemmSplitMinSteps = 12;
+uint32_t gemm_kchunks(const DevMatrix& W, uint64_t m) {
+  if (W.storage != kInt8 || m == 0 || W.rows == 0) return 1;
+  const uint64_t blocks = ((m + 31) / 32) * (((W.rows + 15) / 16 + 7) / 8);
+  const uint64_t cus = device_cus();
+  if (blocks >= cus) return 1;
+  const uint64_t nsteps = W.kpad / 128;
+  uint64_t kc = std::min<uint64_t>(cus / blocks, nsteps / 4);
+  kc = std::min<uint64_t>(kc, kGemmPlaneBudget / (m * W.rows * 8));
+  if (kc < 2 || nsteps - (nsteps + kc - 1) / kc < kGemmSplitMinSteps) return 1;
+  return uint32_t(kc);
+}
+uint64_t gemm_plane_bytes(const DevMatrix& W, uint64_t m) {
+  const uint32_t kc = gemm_kchunks(W, m);
+  return kc > 1 ? uint64_t(kc) * m * W.rows * 8 : 0;
 }
 
 void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_act, uint64_t kpad, int8_t* a_tiled,
@@ -2031,9 +2098,20 @@ void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_a
 }
 
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
-                       const int8_t* a_tiled, hipStream_t s, const RowSplit* split) {
+                       const int8_t* a_tiled, hipStream_t s, const RowSplit* split, int64_t* planes) {
   if (W.rows == 0 || m == 0) return;
   const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
+  const uint32_t kc = planes ? gemm_kchunks(W, m) : 1;
+  if (kc > 1) {
+    KSplit ks;
+    ks.chunks = kc;
+    ks.planes = planes;
+    launch_gemm_lds_shape<8, 8, 2, 2, 8, 2>(W, m, nullptr, 0, nullptr, a_tiled, a_tiles, s, {}, ks);
+    const uint64_t total = m * W.rows;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3(unsigned((total + 511) / 512)), dim3(256), 0, s, planes, kc, m, W.rows,
+                       out, ld_out, acc_out, split ? *split : RowSplit{});
+    return;
+  }
   // row-split outputs take the 128 x 128 blocks only (their epilogue is kept
   // out of the 256 x 256 block's registers)
   if (split)
@@ -2051,10 +2129,10 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
 }
 
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
-                 int64_t* acc_out, int8_t* a_tiled, hipStream_t s) {
+                 int64_t* acc_out, int8_t* a_tiled, hipStream_t s, int64_t* planes) {
   if (W.rows == 0 || m == 0) return;
   launch_gemm_limbs(act, m, W.cols, ld_act, W.kpad, a_tiled, s);
-  launch_gemm_tiled(W, m, out, ld_out, acc_out, a_tiled, s);
+  launch_gemm_tiled(W, m, out, ld_out, acc_out, a_tiled, s, nullptr, planes);
 }
 
 void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out,

@@ -255,6 +255,10 @@ def lib() -> C.CDLL:
         "det_event_record": (C.c_int, [P, P]),
         "det_event_elapsed_ms": (C.c_int, [P, P, P, C.POINTER(C.c_float)]),
         "det_event_destroy": (None, [P]),
+        "det_ctx_capture_begin": (C.c_int, [P]),
+        "det_ctx_capture_end": (C.c_int, [P, C.POINTER(P)]),
+        "det_graph_launch": (C.c_int, [P, P]),
+        "det_graph_destroy": (None, [P]),
         "det_matrix_upload": (C.c_int, [P, u64, u64, C.c_int, P, P, C.POINTER(P)]),
         "det_matrix_info": (C.c_int, [P, C.POINTER(u64), C.POINTER(u64), C.POINTER(C.c_int)]),
         "det_matrix_free": (None, [P]),
@@ -356,7 +360,8 @@ class Context:
 
     def close(self) -> None:
         if getattr(self, "handle", None):
-            order = {"Session": 0, "KvCache": 0, "Scratch": 0, "Model": 1, "Matrix": 2, "DeviceBuffer": 3, "Event": 4}
+            order = {"Graph": 0, "Session": 0, "KvCache": 0, "Scratch": 0, "Model": 1, "Matrix": 2, "DeviceBuffer": 3,
+                     "Event": 4}
             for child in sorted(list(getattr(self, "_children", ())), key=lambda c: order.get(type(c).__name__, 5)):
                 child._release()
             self.lib.det_ctx_destroy(self.handle)
@@ -394,6 +399,17 @@ class Context:
     # -- events ---------------------------------------------------------------
     def event(self) -> "Event":
         return Event(self)
+
+    def capture(self, calls) -> "Graph":
+        """Records calls() (issued on the context stream) as a graph to replay."""
+        self.check(self.lib.det_ctx_capture_begin(self.handle))
+        try:
+            calls()
+        finally:
+            h = C.c_void_p()
+            status = self.lib.det_ctx_capture_end(self.handle, C.byref(h))
+        self.check(status)
+        return Graph(self, h)
 
     # -- weights --------------------------------------------------------------
     def upload_matrix(self, values: np.ndarray, row_scale: np.ndarray | None = None) -> "Matrix":
@@ -493,6 +509,27 @@ class Event:
     def _release(self) -> None:
         if self.handle and self.ctx.handle:
             self.ctx.lib.det_event_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self._release()
+        except Exception:
+            pass
+
+
+class Graph:
+    def __init__(self, ctx: Context, handle):
+        self.ctx = ctx
+        self.handle = handle
+        ctx._adopt(self)
+
+    def launch(self) -> None:
+        self.ctx.check(self.ctx.lib.det_graph_launch(self.ctx.handle, self.handle))
+
+    def _release(self) -> None:
+        if self.handle and self.ctx.handle:
+            self.ctx.lib.det_graph_destroy(self.handle)
         self.handle = None
 
     def __del__(self):

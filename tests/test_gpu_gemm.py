@@ -94,3 +94,36 @@ def test_gemm_e4b_shapes_match_gemv_rows(ctx, m, n, k):
     acts = act_slab(m, k, seed=n + k)
     mat = ctx.upload_matrix(q, s)
     assert np.array_equal(gpu_slab(ctx, mat, acts), gpu_rows(ctx, mat, acts))
+
+
+def test_captured_slab_calls_replay_exactly(ctx):
+    # det_ctx_capture_begin/end: the calls are recorded, not run, and every
+    # replay of the graph produces the direct calls' outputs (split-K GEMMs
+    # included: 16 x 512 x 2560 takes the partial-plane path)
+    shapes = [(512, 2560), (2560, 10240), (2048, 2560)]
+    m = 128
+    mats, acts, outs, want = [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        q, s = synthetic.fast_int8_matrix(900 + i, n, k, 256)
+        mats.append(ctx.upload_matrix(q, s))
+        acts.append(ctx.to_device(act_slab(m, k, seed=i)))
+        outs.append(ctx.empty((m, n)))
+    for mat, a, o in zip(mats, acts, outs):
+        ctx.det_linear_slab(mat, m, a, o)
+    want = [o.numpy().copy() for o in outs]
+
+    def calls():
+        for mat, a, o in zip(mats, acts, outs):
+            ctx.det_linear_slab(mat, m, a, o)
+
+    for o in outs:
+        o.upload(np.zeros(o.shape, np.int32))
+    graph = ctx.capture(calls)
+    ctx.synchronize()
+    assert all(not o.numpy().any() for o in outs)  # recorded, not run
+    for _ in range(3):
+        graph.launch()
+        ctx.synchronize()
+        assert all(np.array_equal(o.numpy(), w) for o, w in zip(outs, want))
+        for o in outs:
+            o.upload(np.zeros(o.shape, np.int32))
