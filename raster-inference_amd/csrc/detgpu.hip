@@ -208,6 +208,7 @@ void free_matrix(DevMatrix& m) {
   if (m.q) (void)hipFree(m.q);
   if (m.scale) (void)hipFree(m.scale);
   if (m.rowsum) (void)hipFree(m.rowsum);
+  if (m.rowsum_p) (void)hipFree(m.rowsum_p);
   if (m.w) (void)hipFree(m.w);
   m = DevMatrix();
 }
@@ -223,14 +224,18 @@ DevMatrix upload_int8(det_ctx* ctx, uint64_t rows, uint64_t cols, const int8_t* 
   m.kpad = round_up(std::max<uint64_t>(cols, 1), 128);
   const uint64_t prow = round_up(std::max<uint64_t>(rows, 1), 16);
   std::vector<int8_t> tiled(prow * m.kpad, 0);
-  std::vector<int32_t> rowsum(prow, 0), sc(prow, 0);
+  const uint64_t nparts = det::limb_parts(m.kpad);
+  std::vector<int32_t> rowsum(prow, 0), sc(prow, 0), rowsum_p(prow * nparts, 0);
   parallel_rows(rows, [&](uint64_t r0, uint64_t r1) {
     for (uint64_t r = r0; r < r1; ++r) {
       int32_t s = 0;
       for (uint64_t c0 = 0; c0 < cols; c0 += 32) {
         const uint64_t n = std::min<uint64_t>(32, cols - c0);
         std::memcpy(&tiled[det::tiled_offset(m.kpad, r, c0)], q + r * cols + c0, n);
-        for (uint64_t c = c0; c < c0 + n; ++c) s += q[r * cols + c];
+        int32_t sp = 0;
+        for (uint64_t c = c0; c < c0 + n; ++c) sp += q[r * cols + c];
+        s += sp;
+        rowsum_p[(c0 / det::kLimbPartCols) * prow + r] += sp;
       }
       rowsum[r] = s;
       sc[r] = scale[r];
@@ -239,9 +244,12 @@ DevMatrix upload_int8(det_ctx* ctx, uint64_t rows, uint64_t cols, const int8_t* 
   HIPC(hipMalloc(&m.q, tiled.size()));
   HIPC(hipMalloc(&m.scale, prow * 4));
   HIPC(hipMalloc(&m.rowsum, prow * 4));
+  HIPC(hipMalloc(&m.rowsum_p, rowsum_p.size() * 4));
+  m.rowsum_p_ld = prow;
   HIPC(hipMemcpyAsync(m.q, tiled.data(), tiled.size(), hipMemcpyHostToDevice, ctx->stream));
   HIPC(hipMemcpyAsync(m.scale, sc.data(), prow * 4, hipMemcpyHostToDevice, ctx->stream));
   HIPC(hipMemcpyAsync(m.rowsum, rowsum.data(), prow * 4, hipMemcpyHostToDevice, ctx->stream));
+  HIPC(hipMemcpyAsync(m.rowsum_p, rowsum_p.data(), rowsum_p.size() * 4, hipMemcpyHostToDevice, ctx->stream));
   HIPC(hipStreamSynchronize(ctx->stream));
   ctx->ensure_limbs(4 * 4 * m.kpad);
   return m;

@@ -21,10 +21,21 @@ struct DevMatrix {
   int8_t* q = nullptr;
   int32_t* scale = nullptr;
   int32_t* rowsum = nullptr;
+  // row sums over each column part of kLimbPartCols (the prefill GEMM's
+  // limb decomposition is chosen per part): part p of row r at
+  // rowsum_p[p * rowsum_p_ld + r]
+  int32_t* rowsum_p = nullptr;
+  uint64_t rowsum_p_ld = 0;
   // wide form: w[rows][cols] as int16 or int32 Wgt bits.
   void* w = nullptr;
   bool owns = true;  // false for row-range views
 };
+
+// Columns per part of the prefill GEMM's per-part limb decomposition.
+constexpr uint64_t kLimbPartCols = 512;
+// More parts than this (K above 32768) take four limbs throughout.
+constexpr uint64_t kLimbMaxParts = 64;
+__host__ __device__ inline uint64_t limb_parts(uint64_t kpad) { return (kpad + kLimbPartCols - 1) / kLimbPartCols; }
 
 // A view of rows [r0, r0+n) of a matrix (shares storage). For int8 storage
 // r0 must be a multiple of 16 (tile aligned).

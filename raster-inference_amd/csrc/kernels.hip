@@ -1011,44 +1011,61 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
 // row i) in lane 16g + i, which are combined exactly as in the GEMV.
 // ---------------------------------------------------------------------------
 
-// Activation limbs in the tiled layout for a_tiles 16-row tiles (4 tokens
-// each); tokens >= m and columns >= k are zero. One thread per token and 32
-// columns: its four limb rows are four consecutive 32-byte lane slots of the
-// tile-step (lanes 16 g + 4 (t % 4) + j), so it writes 128 contiguous bytes,
-// and the four tokens of a tile go to consecutive threads (512 contiguous
-// bytes). vec: act rows are 16-byte aligned (base and ld), so a thread's 32
-// columns load as eight 128-bit reads.
-__global__ void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, uint64_t k, uint64_t ld,
-                                  uint64_t kpad, uint64_t tokens_pad, int vec, int8_t* __restrict__ out) {
-  const uint64_t id = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  const uint64_t nsteps = kpad / 128;
-  const uint64_t tq = id & 3, g = (id >> 2) & 3, rest = id >> 4;
-  const uint64_t step = rest % nsteps, tile = rest / nsteps;
-  const uint64_t t = 4 * tile + tq;
-  if (t >= tokens_pad) return;
+// Prefill GEMM A operand: activation rows as limb-major token groups. Token
+// group T (tokens 16 T .. 16 T + 15) has four limb tiles T 4 + j; tile-step
+// (tile, s) is 2048 bytes in the lane order of the weight tiles (lane 16 g + i:
+// token 16 T + i, columns [128 s + 32 g, +32)), so an MFMA A operand is one
+// limb of 16 tokens and the four limb products of (token, row) land in the
+// same lane of four accumulators.
+// The decomposition is chosen per token group and column part of
+// kLimbPartCols: where the part's activations all lie in [-2^23, 2^23), three
+// limbs: with u = (a + 2^23) ^ 0x808080, a = sum_{j<3} c_j 256^j + 32896 (c_j
+// the signed bytes of u; its top byte is 0, so the fourth limb tile is zero
+// and the GEMM skips it); otherwise u = a ^ 0x808080, a = sum_{j<4} c_j 256^j
+// + 8421504. flags[T * parts + p] = 1 marks the four-limb parts.
+// One workgroup per (group, part): thread (step, g, token i) holds 32 columns
+// of one token, the workgroup decides the part's decomposition, and every
+// thread writes its four limbs as four 32-byte lane slots (16 tokens of a limb
+// tile-step are 512 contiguous bytes). vec: act rows are 16-byte aligned (base
+// and ld), so a thread's 32 columns load as eight 128-bit reads. Tokens past m
+// and columns past k are zero.
+__global__ __launch_bounds__(256) void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, uint64_t k,
+                                                          uint64_t ld, uint64_t kpad, int vec,
+                                                          uint32_t* __restrict__ flags, int8_t* __restrict__ out) {
+  constexpr uint64_t PS = kLimbPartCols / 128;  // K steps per part
+  const uint64_t nsteps = kpad / 128, parts = limb_parts(kpad);
+  const uint64_t T = blockIdx.x, part = blockIdx.y;
+  const uint64_t i = threadIdx.x & 15, g = (threadIdx.x >> 4) & 3;
+  const uint64_t step = part * PS + (threadIdx.x >> 6);
+  const uint64_t t = 16 * T + i;
+  const bool on = step < nsteps;
   const uint64_t c0 = 128 * step + 32 * g;
-  uint32_t u[32];
-  if (vec && t < m && c0 + 32 <= k) {
+  uint32_t a[32];
+  if (vec && on && t < m && c0 + 32 <= k) {
     const int4* src = reinterpret_cast<const int4*>(act + t * ld + c0);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int4 v = src[q];
-      u[4 * q] = uint32_t(v.x) ^ 0x00808080u;
-      u[4 * q + 1] = uint32_t(v.y) ^ 0x00808080u;
-      u[4 * q + 2] = uint32_t(v.z) ^ 0x00808080u;
-      u[4 * q + 3] = uint32_t(v.w) ^ 0x00808080u;
+      a[4 * q] = uint32_t(v.x), a[4 * q + 1] = uint32_t(v.y), a[4 * q + 2] = uint32_t(v.z), a[4 * q + 3] = uint32_t(v.w);
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const bool live = t < m && c0 + e < k;
-      u[e] = live ? uint32_t(act[t * ld + c0 + e]) ^ 0x00808080u : 0u;
-    }
+    for (int e = 0; e < 32; ++e) a[e] = (on && t < m && c0 + e < k) ? uint32_t(act[t * ld + c0 + e]) : 0u;
   }
-  // lane slot 16 g + 4 tq + j of tile-step (tile, step)
-  int4* dst = reinterpret_cast<int4*>(out + ((tile * nsteps + step) * 64 + 16 * g + 4 * tq) * 32);
+  uint32_t wide = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int e = 0; e < 32; ++e) wide |= a[e] + 0x800000u >= 0x1000000u;
+  const bool four = __syncthreads_or(int(wide)) != 0 || parts > kLimbMaxParts;
+  if (threadIdx.x == 0) flags[T * parts + part] = four ? 1u : 0u;
+  if (!on) return;
+  const uint32_t off = four ? 0u : 0x800000u;
+  uint32_t u[32];
+#pragma unroll
+  for (int e = 0; e < 32; ++e) u[e] = (t < m && c0 + e < k) ? (a[e] + off) ^ 0x00808080u : 0u;
+  // lane slot 16 g + i of tile-step (4 T + j, step)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    int4* dst = reinterpret_cast<int4*>(out + (((4 * T + j) * nsteps + step) * 64 + 16 * g + i) * 32);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       uint32_t w[4];
@@ -1058,12 +1075,15 @@ __global__ void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, u
 #pragma unroll
         for (int b = 0; b < 4; ++b) w[q] |= ((u[16 * h + 4 * q + b] >> (8 * j)) & 0xffu) << (8 * b);
       }
-      dst[2 * j + h] = make_int4(int(w[0]), int(w[1]), int(w[2]), int(w[3]));
+      dst[h] = make_int4(int(w[0]), int(w[1]), int(w[2]), int(w[3]));
     }
+  }
 }
 
-// Block: TA A tiles (4 TA tokens) x TB weight tiles on WM x WN waves, each
-// wave (TA / WM) x (TB / WN) MFMA tiles. Every 128-column K step, the block's
+// Block: TA A tiles (TA / 4 token groups of 16 tokens, four limb tiles each)
+// x TB weight tiles on WM x WN waves, each wave (TA / WM) x (TB / WN) MFMA
+// tiles (whole token groups). A block whose token groups all take three limbs
+// copies and multiplies no fourth-limb tile. Every 128-column K step, the block's
 // TA + TB tile-steps (2 KB each) are copied straight from global memory into
 // one of NBUF LDS buffers with global_load_lds_dwordx4 (no register staging):
 // the copies of the next NBUF - 1 steps are in flight while step s's MFMAs
@@ -1076,8 +1096,10 @@ __global__ void k_act_limbs_tiled(const int32_t* __restrict__ act, uint64_t m, u
 template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
                                                            const int32_t* __restrict__ scale,
-                                                           const int32_t* __restrict__ rowsum, uint64_t n_rows,
-                                                           uint64_t kpad, uint64_t m_tokens, uint64_t a_tiles,
+                                                           const int32_t* __restrict__ rowsum,
+                                                           const int32_t* __restrict__ rowsum_p, uint64_t rowsum_p_ld,
+                                                           uint64_t n_rows, uint64_t kpad, uint64_t m_tokens,
+                                                           uint64_t a_tiles, const uint32_t* __restrict__ a_flags,
                                                            uint32_t mblocks, int32_t* __restrict__ out,
                                                            uint64_t ld_out, int64_t* __restrict__ acc_out,
                                                            RowSplit split, KSplit ks) {
@@ -1086,6 +1108,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   constexpr int LPW = 2 * TS / NW;             // 1 KB wave copies per wave per K step
   constexpr int FA = TA / WM, FB = TB / WN;    // MFMA tiles per wave
   static_assert(2 * TS % NW == 0, "copies must divide evenly");
+  static_assert(FA % 4 == 0 && NBUF == 2, "whole token groups per wave; every step waits for all its copies");
   extern __shared__ __attribute__((aligned(16))) int8_t lds_gemm[];
   // the wave index as a scalar, so that copy addresses and LDS targets stay in SGPRs
   const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1110,10 +1133,29 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   const uint64_t nsteps = (k0 + cper < ksteps ? k0 + cper : ksteps) - k0;  // this block's K steps
   const uint64_t ntiles = (n_rows + 15) / 16;
   const uint64_t at0 = uint64_t(mb) * TA, bt0 = uint64_t(nb) * TB;
+  // per column part: four limbs when any of the block's token groups needs
+  // them there (block-uniform bit mask, parts <= 64)
+  const uint64_t parts = limb_parts(kpad);
+  constexpr uint64_t PS = kLimbPartCols / 128;
+  const bool many = parts > kLimbMaxParts;  // (every part of every group takes four limbs)
+  uint64_t fourmask = many ? 1 : 0;
+#pragma unroll
+  for (int t = 0; t < TA / 4; ++t) {
+    const uint64_t grp = at0 / 4 + t;
+    if (grp < a_tiles / 4 && !many)
+      for (uint64_t p = 0; p < parts; ++p) fourmask |= uint64_t(a_flags[grp * parts + p] != 0) << p;
+  }
+  // (one limb count for the block's whole K range: a loop that switches
+  // between the two forms per part needs more registers than the larger
+  // block has)
+  const bool four = fourmask != 0;
+  (void)PS;
   // this wave's copies: chunk c = wave * LPW + u is tile-step c / 2 (A tiles
   // first), half c % 2; tiles past the matrix re-read its last tile (their
-  // results are never stored)
+  // results are never stored); fourth-limb A tiles are not copied in a
+  // three-limb block
   const int8_t* src[LPW];
+  bool limb3[LPW];
 #pragma unroll
   for (int u = 0; u < LPW; ++u) {
     const uint32_t c = wave * LPW + u, ts = c >> 1, h = c & 1;
@@ -1121,14 +1163,16 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     uint64_t tile = is_a ? at0 + ts : bt0 + (ts - TA);
     if (is_a ? tile >= a_tiles : tile >= ntiles) tile = (is_a ? a_tiles : ntiles) - 1;
     src[u] = (is_a ? a : q) + (tile * ksteps + k0) * 2048 + lane * 32 + h * 16;
+    limb3[u] = is_a && (ts & 3) == 3;
   }
   auto copy_step = [&](uint64_t s, int buf) {
 #pragma unroll
     for (int u = 0; u < LPW; ++u) {
       const uint32_t c = wave * LPW + u;
-      __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[u] + s * 2048),
-                                       (void __attribute__((address_space(3)))*)(lds_gemm + (buf * TS * 2 + c) * 1024),
-                                       16, 0, 0);
+      if (four || !limb3[u])
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[u] + s * 2048),
+                                         (void __attribute__((address_space(3)))*)(lds_gemm + (buf * TS * 2 + c) * 1024),
+                                         16, 0, 0);
     }
   };
   const uint32_t wm = wave / WN, wn = wave % WN;
@@ -1159,47 +1203,73 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     asm volatile("" ::: "memory");
   };
   step_barrier(nsteps >= uint64_t(NBUF - 1));
-  for (uint64_t s = 0; s < nsteps; ++s) {
-    const int buf = int(s % NBUF);
-    const int8_t* base = lds_gemm + buf * TS * 2048 + lane * 16;
-    // the first half's operands, the copies, the second half's operands
-    // (read while the first half's MFMAs run), then the MFMAs
-    v4i ao[2][FA], bo[2][FB];
-    auto read_half = [&](int h) {
+  // the K loop with L limbs (A tiles with i % 4 >= L are neither read nor multiplied)
+  auto kloop = [&](auto Lc) {
+    constexpr int L = decltype(Lc)::value;
+    for (uint64_t s = 0; s < nsteps; ++s) {
+      const int buf = int(s % NBUF);
+      const int8_t* base = lds_gemm + buf * TS * 2048 + lane * 16;
+      // the first half's operands, the copies, the second half's operands
+      // (read while the first half's MFMAs run), then the MFMAs
+      v4i ao[2][FA], bo[2][FB];
+      auto read_half = [&](int h) {
 #pragma unroll
-      for (int j = 0; j < FB; ++j) bo[h][j] = *reinterpret_cast<const v4i*>(base + (TA + wn * FB + j) * 2048 + 1024 * h);
+        for (int j = 0; j < FB; ++j) bo[h][j] = *reinterpret_cast<const v4i*>(base + (TA + wn * FB + j) * 2048 + 1024 * h);
 #pragma unroll
-      for (int i = 0; i < FA; ++i) ao[h][i] = *reinterpret_cast<const v4i*>(base + (wm * FA + i) * 2048 + 1024 * h);
-    };
-    read_half(0);
-    if (s + NBUF - 1 < nsteps) copy_step(s + NBUF - 1, int((s + NBUF - 1) % NBUF));
-    read_half(1);
+        for (int i = 0; i < FA; ++i)
+          if ((i & 3) < L) ao[h][i] = *reinterpret_cast<const v4i*>(base + (wm * FA + i) * 2048 + 1024 * h);
+      };
+      read_half(0);
+      if (s + NBUF - 1 < nsteps) copy_step(s + NBUF - 1, int((s + NBUF - 1) % NBUF));
+      read_half(1);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int i = 0; i < FA; ++i)
+        for (int i = 0; i < FA; ++i)
 #pragma unroll
-        for (int j = 0; j < FB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ao[h][i], bo[h][j], acc[i][j], 0, 0, 0);
-    // step s + 1's copies are complete when no more than the later steps' are outstanding
-    step_barrier(s + NBUF - 1 < nsteps);
-  }
-  // epilogue: lane 16g + i holds the limb sums of token 4 tile + g, weight row 16 tile + i
+          for (int j = 0; j < FB; ++j)
+            if ((i & 3) < L) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ao[h][i], bo[h][j], acc[i][j], 0, 0, 0);
+      // step s + 1's copies are complete when no more than the later steps' are outstanding
+      step_barrier(s + NBUF - 1 < nsteps);
+    }
+  };
+  if (four) kloop(std::integral_constant<int, 4>());
+  else kloop(std::integral_constant<int, 3>());
+  // epilogue: lane 16 g + i holds, in component r of the four limb tiles of a
+  // token group, the limb sums of token 16 group + 4 g + r and weight row 16 tile + i
   const uint32_t g = lane >> 4, i = lane & 15;
 #pragma unroll
-  for (int ti = 0; ti < FA; ++ti) {
-    const uint64_t token = (at0 + wm * FA + ti) * 4 + g;
+  for (int tg = 0; tg < FA / 4; ++tg) {
+    const uint64_t grp = (at0 + wm * FA) / 4 + tg;
+    // the decomposition's constant per part: sum_p c_p S_p (S_p the part's row sum)
+    uint64_t gmask = 0;
+    if (grp < a_tiles / 4 && !many)
+      for (uint64_t p = 0; p < parts; ++p) gmask |= uint64_t(a_flags[grp * parts + p] != 0) << p;
 #pragma unroll
     for (int tj = 0; tj < FB; ++tj) {
-      const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
+    const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
+    const uint64_t rc = row < n_rows ? row : n_rows - 1;
+    // the chunk holding column 0 adds the constant term (wrapping i64)
+    // (32896 S, plus 8388608 S_p for every four-limb part p)
+    uint64_t cterm = 0;
+    if (chunk == 0) {
+      cterm = uint64_t(int64_t(many ? 8421504 : 32896) * rowsum[rc]);
+      for (uint64_t gm = gmask; gm; gm &= gm - 1)
+        cterm += uint64_t(int64_t(8388608) * rowsum_p[uint64_t(__builtin_ctzll(gm)) * rowsum_p_ld + rc]);
+    }
+    const uint64_t sc = uint64_t(int64_t(scale[rc]));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint64_t token = grp * 16 + 4 * g + r;
       if (token >= m_tokens || row >= n_rows) continue;
-      const int64_t p[4] = {acc[ti][tj][0], acc[ti][tj][1], acc[ti][tj][2], acc[ti][tj][3]};
+      const int64_t p[4] = {acc[4 * tg][tj][r], acc[4 * tg + 1][tj][r], acc[4 * tg + 2][tj][r], acc[4 * tg + 3][tj][r]};
+      const int64_t dot = p[0] + p[1] * 256 + p[2] * 65536 + p[3] * 16777216 + int64_t(cterm);
+      const int64_t v = int64_t(uint64_t(dot) * sc);
       if (ks.chunks > 1) {
-        // this K range's wrapping share (the chunk holding column 0 adds the offset term)
-        ks.planes[(uint64_t(chunk) * m_tokens + token) * n_rows + row] = limb_combine(p, chunk == 0 ? rowsum[row] : 0, scale[row]);
+        // this K range's wrapping share
+        ks.planes[(uint64_t(chunk) * m_tokens + token) * n_rows + row] = v;
         continue;
       }
-      const int64_t v = limb_combine(p, rowsum[row], scale[row]);
       if (SPLIT) {
         // rows [0, r1) to out, [r1, r2) to out1, [r2, n_rows) to out2
         int32_t* o = out;
@@ -1212,6 +1282,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
       } else {
         out[token * ld_out + row] = requant(v);
       }
+    }
     }
   }
 }
@@ -1776,6 +1847,7 @@ DevMatrix row_view(const DevMatrix& m, uint64_t r0, uint64_t n) {
     v.q = m.q + (r0 / 16) * (m.kpad / 128) * 2048;  // r0 is tile aligned
     v.scale = m.scale + r0;
     v.rowsum = m.rowsum + r0;
+    v.rowsum_p = m.rowsum_p ? m.rowsum_p + r0 : nullptr;  // (rowsum_p_ld is the parent's)
   } else if (m.storage == kI16) {
     v.w = static_cast<int16_t*>(m.w) + r0 * m.cols;
   } else {
@@ -2045,7 +2117,16 @@ void launch_gemv_norm(const DecNormIn& ni, const DevMatrix& W, int epilogue, int
 #undef DET_NORM_LAUNCH
 }
 
-uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64 * 4 * kpad; }
+// a_tiled holds the limb tiles of (m rounded up to 64) tokens, then the
+// four-limb flag of every (token group, column part).
+static uint64_t gemm_tile_bytes(uint64_t m, uint64_t kpad) { return ((m + 63) / 64) * 64 * 4 * kpad; }
+static uint32_t* gemm_flags(const int8_t* a_tiled, uint64_t m, uint64_t kpad) {
+  return reinterpret_cast<uint32_t*>(const_cast<int8_t*>(a_tiled) + gemm_tile_bytes(m, kpad));
+}
+uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) {
+  const uint64_t groups = (m + 63) / 64 * 4;
+  return gemm_tile_bytes(m, kpad) + 4 * groups * limb_parts(kpad);
+}
 
 template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT = false>
 static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
@@ -2059,8 +2140,9 @@ static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, 
   const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
   const uint64_t nblocks = ((W.rows + 15) / 16 + TB - 1) / TB;
   hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT>), dim3(unsigned(mblocks * nblocks * ks.chunks)),
-                     dim3(64 * WM * WN), lds, s, a_tiled, W.q, W.scale, W.rowsum, W.rows, W.kpad, m, a_tiles,
-                     uint32_t(mblocks), out, ld_out, acc_out, split, ks);
+                     dim3(64 * WM * WN), lds, s, a_tiled, W.q, W.scale, W.rowsum, W.rowsum_p, W.rowsum_p_ld, W.rows,
+                     W.kpad, m, a_tiles, gemm_flags(a_tiled, m, W.kpad), uint32_t(mblocks), out, ld_out, acc_out,
+                     split, ks);
 }
 
 // K split of a GEMM whose 128 x 128 blocks leave CUs idle: chunks of at least
@@ -2090,11 +2172,11 @@ uint64_t gemm_plane_bytes(const DevMatrix& W, uint64_t m) {
 void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_act, uint64_t kpad, int8_t* a_tiled,
                        hipStream_t s) {
   if (m == 0) return;
-  const uint64_t tokens_pad = (m + 63) / 64 * 64;  // the larger block's 16 A tiles
+  const uint64_t groups = (m + 63) / 64 * 4;  // the larger block's 4 token groups
   const int vec = (reinterpret_cast<uintptr_t>(act) % 16 == 0 && ld_act % 4 == 0) ? 1 : 0;
-  const uint64_t threads = tokens_pad * (kpad / 128) * 4;
-  hipLaunchKernelGGL(k_act_limbs_tiled, dim3(blocks_for(threads, 256)), dim3(256), 0, s, act, m, k, ld_act, kpad,
-                     tokens_pad, vec, a_tiled);
+  hipLaunchKernelGGL(k_act_limbs_tiled, dim3(unsigned(groups), unsigned(limb_parts(kpad))),
+                     dim3(unsigned(64 * (kLimbPartCols / 128))), 0, s, act, m, k, ld_act, kpad, vec,
+                     gemm_flags(a_tiled, m, kpad), a_tiled);
 }
 
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,

@@ -87,6 +87,25 @@ def test_gemm_adversarial_values(ctx):
     assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("m,n,k", [(100, 300, 2600), (200, 1000, 777), (64, 128, 4096)])
+def test_gemm_three_and_four_limb_groups(ctx, m, n, k):
+    # token groups of 16 whose activations all lie in [-2^23, 2^23) take three
+    # limbs, the others four: values at both edges of the range, one group
+    # with a single value just outside it, blocks mixing both kinds
+    rng = np.random.default_rng(m + n + k)
+    q, s = synthetic.random_int8_matrix(rng, n, k, scale_max=256)
+    acts = act_slab(m, k, seed=k)
+    acts[0, :4] = [2**23 - 1, -(2**23), 2**23 - 1, -(2**23)]     # group 0: three limbs, at the edges
+    acts[17, k // 2] = 2**23                                       # group 1: four limbs (one value)
+    acts[40, k - 1] = -(2**23) - 1                                  # group 2: four limbs (last column)
+    if m > 64:
+        acts[64:80, :] = rng.integers(-(2**31), 2**31, size=(16, k), dtype=np.int64).astype(np.int32)
+    mat = ctx.upload_matrix(q, s)
+    got = gpu_slab(ctx, mat, acts)
+    exp = oracle_lib.det_linear_slab(expand(q, s), acts, threads=oracle_lib.cpu_count())
+    assert np.array_equal(got, exp)
+
+
 @pytest.mark.parametrize("m,n,k", [(128, 3072, 2560), (64, 2560, 10240), (48, 2560, 2048),
                                    (256, 16384, 512), (300, 13100, 2600)])
 def test_gemm_e4b_shapes_match_gemv_rows(ctx, m, n, k):
