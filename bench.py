@@ -443,6 +443,27 @@ def gemm_profile(ctx, rd, seed: int) -> int:
     return 0
 
 
+def gemm_sets_profile(ctx, rd, seed: int) -> int:
+    """Kernel-trace workload for the prefill GEMM: the seven E4B projections
+    through det_linear_slab at M = 128, 512 and 2048 rows, 3 layer-sets each
+    (the per-projection limb expansions, GEMMs and partial-plane sums)."""
+    from rasterdet import synthetic
+
+    mats = [ctx.upload_matrix(*synthetic.fast_int8_matrix(seed * 7 + i, n, k, 256))
+            for i, (n, k) in enumerate(PREFILL_SHAPES)]
+    rng = np.random.default_rng(seed)
+    for m in (128, 512, 2048):
+        acts = {k: ctx.to_device(synthetic.f32_to_act(rng.standard_normal((m, k)).astype(np.float32)))
+                for k in {k for _, k in PREFILL_SHAPES}}
+        outs = [ctx.empty((m, n)) for n, _ in PREFILL_SHAPES]
+        for _ in range(3):
+            for mat, (n, k), o in zip(mats, PREFILL_SHAPES, outs):
+                ctx.det_linear_slab(mat, m, acts[k], o)
+        ctx.synchronize()
+    print(json.dumps({"gemm_sets_profile": True, "m": [128, 512, 2048], "layer_sets": 3}), flush=True)
+    return 0
+
+
 def profile_pass(ctx, rd, seed: int) -> int:
     """Counter-collection workload: the lm_head GEMV and a device copy of the
     same weight byte count, so FETCH_SIZE / WRITE_SIZE of the GEMV can be scaled
@@ -494,6 +515,8 @@ def main() -> int:
                     help="only the E4B-shaped model: prefill, then 32 greedy decode steps (for rocprofv3 runs)")
     ap.add_argument("--gemm-profile", action="store_true",
                     help="only 10 prefill GEMMs (gate 10240x2560, M 2048) for rocprofv3 runs")
+    ap.add_argument("--gemm-sets-profile", action="store_true",
+                    help="only the seven E4B projections at M = 128/512/2048, 3 layer-sets each (for rocprofv3 runs)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only 5 lm_head GEMV launches + 5 same-size device copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
@@ -509,6 +532,8 @@ def main() -> int:
         return profile_pass(ctx, rd, args.seed)
     if args.gemm_profile:
         return gemm_profile(ctx, rd, args.seed)
+    if args.gemm_sets_profile:
+        return gemm_sets_profile(ctx, rd, args.seed)
     if args.decode_profile:
         args.decode_steps = 32
         args.eager = True  # profiler kernel tracing of graph replays is not used

@@ -1253,9 +1253,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     // (32896 S, plus 8388608 S_p for every four-limb part p)
     uint64_t cterm = 0;
     if (chunk == 0) {
-      cterm = uint64_t(int64_t(many ? 8421504 : 32896) * rowsum[rc]);
-      for (uint64_t gm = gmask; gm; gm &= gm - 1)
-        cterm += uint64_t(int64_t(8388608) * rowsum_p[uint64_t(__builtin_ctzll(gm)) * rowsum_p_ld + rc]);
+      const bool all4 = many || gmask == (parts >= 64 ? ~uint64_t(0) : (uint64_t(1) << parts) - 1);
+      cterm = uint64_t(int64_t(all4 ? 8421504 : 32896) * rowsum[rc]);
+      if (!all4)
+        for (uint64_t gm = gmask; gm; gm &= gm - 1)
+          cterm += uint64_t(int64_t(8388608) * rowsum_p[uint64_t(__builtin_ctzll(gm)) * rowsum_p_ld + rc]);
     }
     const uint64_t sc = uint64_t(int64_t(scale[rc]));
 #pragma unroll
