@@ -68,9 +68,11 @@ void det_event_destroy(det_event_t* ev);
    the same short kernels repeatedly, where the per-call host launch cost
    would exceed the GPU time). Between begin and end the calls are recorded,
    not run; only calls that allocate nothing and do not synchronize may be
-   recorded (run each once beforehand so that their scratch exists), and the
-   buffers they name must outlive the graph. A failed or refused call ends
-   the capture. */
+   recorded (run each once beforehand so that their scratch exists; a call
+   whose scratch would grow is refused), and the buffers they name must
+   outlive the graph. A failed or refused call ends the capture and discards
+   what was recorded; det_ctx_capture_end then reports that no capture is in
+   progress. */
 int det_ctx_capture_begin(det_ctx_t* ctx);
 int det_ctx_capture_end(det_ctx_t* ctx, det_graph_t** out);
 int det_graph_launch(det_ctx_t* ctx, det_graph_t* g);

@@ -66,9 +66,17 @@ struct det_ctx {
   size_t gemm_a_bytes = 0;
   int64_t* gemm_planes = nullptr;  // K-range partial planes of split GEMMs
   size_t gemm_planes_bytes = 0;
+  bool capturing = false;  // between det_ctx_capture_begin and _end
 
+  // scratch that has to grow cannot be allocated while the stream records
+  void grow_check(const char* what) const {
+    if (capturing)
+      bail(std::string("det_ctx capture: ") + what +
+           " scratch would grow inside the capture; run the call once before capturing");
+  }
   void ensure_gemm_a(size_t bytes) {
     if (bytes <= gemm_a_bytes) return;
+    grow_check("GEMM activation");
     HIPC(hipStreamSynchronize(stream));
     if (gemm_a) HIPC(hipFree(gemm_a));
     gemm_a = nullptr;
@@ -80,6 +88,7 @@ struct det_ctx {
     const size_t bytes = det::gemm_plane_bytes(W, m);
     if (bytes == 0) return nullptr;
     if (bytes > gemm_planes_bytes) {
+      grow_check("GEMM partial-plane");
       HIPC(hipStreamSynchronize(stream));
       if (gemm_planes) HIPC(hipFree(gemm_planes));
       gemm_planes = nullptr;
@@ -124,6 +133,7 @@ struct det_ctx {
 
   void ensure_limbs(size_t bytes) {
     if (bytes <= limbs_bytes) return;
+    grow_check("GEMV limb");
     HIPC(hipStreamSynchronize(stream));
     if (limbs) HIPC(hipFree(limbs));
     limbs = nullptr;
@@ -131,6 +141,7 @@ struct det_ctx {
     limbs_bytes = bytes;
   }
   uint32_t argmax(const int32_t* x, uint64_t n) {
+    if (capturing) bail("det_ctx capture: the argmax returns its index to the host and cannot be recorded");
     const size_t parts = (n + 1023) / 1024;
     if (parts > argmax_parts) {
       HIPC(hipStreamSynchronize(stream));
@@ -166,6 +177,16 @@ struct det_graph {
 
 namespace {
 
+// A call that fails while the context's stream is recording ends the
+// capture: the partial recording is discarded and the stream runs again.
+void abort_capture(det_ctx* ctx) {
+  if (!ctx || !ctx->capturing) return;
+  ctx->capturing = false;
+  hipGraph_t g = nullptr;
+  (void)hipStreamEndCapture(ctx->stream, &g);
+  if (g) (void)hipGraphDestroy(g);
+}
+
 template <class F>
 int guarded(det_ctx* ctx, F&& f) {
   try {
@@ -173,12 +194,15 @@ int guarded(det_ctx* ctx, F&& f) {
     return 0;
   } catch (const Status& e) {
     (ctx ? ctx->last_error : g_error) = e.what();
+    abort_capture(ctx);
     return e.code;
   } catch (const std::invalid_argument& e) {  // argument checks inside the kernel launchers
     (ctx ? ctx->last_error : g_error) = e.what();
+    abort_capture(ctx);
     return 1;
   } catch (const std::exception& e) {
     (ctx ? ctx->last_error : g_error) = e.what();
+    abort_capture(ctx);
     return 3;
   }
 }
@@ -2729,12 +2753,18 @@ int det_event_record(det_ctx_t* ctx, det_event_t* ev) {
   return guarded(ctx, [&] { HIPC(hipEventRecord(ev->ev, ctx->stream)); });
 }
 int det_ctx_capture_begin(det_ctx_t* ctx) {
-  return guarded(ctx, [&] { HIPC(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal)); });
+  return guarded(ctx, [&] {
+    if (ctx->capturing) bail("det_ctx_capture_begin: the context is already capturing");
+    HIPC(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+  });
 }
 int det_ctx_capture_end(det_ctx_t* ctx, det_graph_t** out) {
   return guarded(ctx, [&] {
     if (!out) bail("det_ctx_capture_end requires an output handle");
     *out = nullptr;
+    if (!ctx->capturing) bail("det_ctx_capture_end: no capture in progress (a failed call ends it)");
+    ctx->capturing = false;
     auto g = std::make_unique<det_graph>();
     HIPC(hipStreamEndCapture(ctx->stream, &g->graph));
     HIPC(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0));
@@ -2744,6 +2774,7 @@ int det_ctx_capture_end(det_ctx_t* ctx, det_graph_t** out) {
 int det_graph_launch(det_ctx_t* ctx, det_graph_t* g) {
   return guarded(ctx, [&] {
     if (!g || !g->exec) bail("det_graph_launch requires an instantiated graph");
+    if (ctx->capturing) bail("det_graph_launch: the context is capturing");
     HIPC(hipGraphLaunch(g->exec, ctx->stream));
   });
 }

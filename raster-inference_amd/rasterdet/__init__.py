@@ -405,10 +405,15 @@ class Context:
         self.check(self.lib.det_ctx_capture_begin(self.handle))
         try:
             calls()
-        finally:
+        except BaseException:
+            # a failed C call has ended the capture already; anything else
+            # leaves it open: end it and drop the partial graph
             h = C.c_void_p()
-            status = self.lib.det_ctx_capture_end(self.handle, C.byref(h))
-        self.check(status)
+            if self.lib.det_ctx_capture_end(self.handle, C.byref(h)) == 0 and h.value:
+                self.lib.det_graph_destroy(h)
+            raise
+        h = C.c_void_p()
+        self.check(self.lib.det_ctx_capture_end(self.handle, C.byref(h)))
         return Graph(self, h)
 
     # -- weights --------------------------------------------------------------

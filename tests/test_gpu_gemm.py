@@ -146,3 +146,27 @@ def test_captured_slab_calls_replay_exactly(ctx):
         assert all(np.array_equal(o.numpy(), w) for o, w in zip(outs, want))
         for o in outs:
             o.upload(np.zeros(o.shape, np.int32))
+
+
+def test_capture_refuses_growing_scratch_and_ends():
+    # a fresh context has no GEMM scratch yet: the recorded call would have to
+    # allocate it, so it is refused, the capture ends and the stream runs again
+    c = rd.Context(0)
+    try:
+        q, s = synthetic.fast_int8_matrix(5, 512, 2560, 256)
+        mat = c.upload_matrix(q, s)
+        a = c.to_device(act_slab(128, 2560, seed=3))
+        o = c.empty((128, 512))
+        with pytest.raises(rd.DetError, match="run the call once before capturing"):
+            c.capture(lambda: c.det_linear_slab(mat, 128, a, o))
+        c.det_linear_slab(mat, 128, a, o)
+        want = o.numpy().copy()
+        assert np.array_equal(want, gpu_rows(c, mat, act_slab(128, 2560, seed=3)))
+        o.upload(np.zeros(o.shape, np.int32))
+        graph = c.capture(lambda: c.det_linear_slab(mat, 128, a, o))
+        for _ in range(2):
+            graph.launch()
+            c.synchronize()
+            assert np.array_equal(o.numpy(), want)
+    finally:
+        c.close()
