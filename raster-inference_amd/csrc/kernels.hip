@@ -1124,6 +1124,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   const uint32_t chunk = logical / nblk;
   logical -= chunk * nblk;
   const uint32_t nblocks_n = nblk / mblocks;
+  const uint32_t wm = wave / WN, wn = wave % WN;
   const uint32_t group = logical / (GM * nblocks_n), first_m = group * GM;
   const uint32_t gm = mblocks - first_m < GM ? mblocks - first_m : GM;
   const uint32_t in_group = logical - group * GM * nblocks_n;
@@ -1133,27 +1134,23 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   const uint64_t nsteps = (k0 + cper < ksteps ? k0 + cper : ksteps) - k0;  // this block's K steps
   const uint64_t ntiles = (n_rows + 15) / 16;
   const uint64_t at0 = uint64_t(mb) * TA, bt0 = uint64_t(nb) * TB;
-  // per column part: four limbs when any of the block's token groups needs
-  // them there (block-uniform bit mask, parts <= 64)
+  // The block's decomposition flags, one vector load per token group (lane p
+  // reads part p's flag, at clamped addresses), issued ahead of the first
+  // step's copies so that waiting for them leaves the copies in flight.
   const uint64_t parts = limb_parts(kpad);
-  constexpr uint64_t PS = kLimbPartCols / 128;
   const bool many = parts > kLimbMaxParts;  // (every part of every group takes four limbs)
-  uint64_t fourmask = many ? 1 : 0;
+  constexpr int NG = TA / 4;                // the block's token groups
+  const uint64_t ngroups = a_tiles / 4;
+  uint32_t flag[NG];
 #pragma unroll
-  for (int t = 0; t < TA / 4; ++t) {
-    const uint64_t grp = at0 / 4 + t;
-    if (grp < a_tiles / 4 && !many)
-      for (uint64_t p = 0; p < parts; ++p) fourmask |= uint64_t(a_flags[grp * parts + p] != 0) << p;
+  for (int t = 0; t < NG; ++t) {
+    const uint64_t grp = at0 / 4 + t < ngroups ? at0 / 4 + t : ngroups - 1;
+    flag[t] = a_flags[grp * parts + (lane < parts ? lane : parts - 1)];
   }
-  // (one limb count for the block's whole K range: a loop that switches
-  // between the two forms per part needs more registers than the larger
-  // block has)
-  const bool four = fourmask != 0;
-  (void)PS;
   // this wave's copies: chunk c = wave * LPW + u is tile-step c / 2 (A tiles
   // first), half c % 2; tiles past the matrix re-read its last tile (their
   // results are never stored); fourth-limb A tiles are not copied in a
-  // three-limb block
+  // three-limb block (the first step copies them before the flags are known)
   const int8_t* src[LPW];
   bool limb3[LPW];
 #pragma unroll
@@ -1165,6 +1162,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     src[u] = (is_a ? a : q) + (tile * ksteps + k0) * 2048 + lane * 32 + h * 16;
     limb3[u] = is_a && (ts & 3) == 3;
   }
+  bool four = true;
   auto copy_step = [&](uint64_t s, int buf) {
 #pragma unroll
     for (int u = 0; u < LPW; ++u) {
@@ -1175,7 +1173,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
                                          16, 0, 0);
     }
   };
-  const uint32_t wm = wave / WN, wn = wave % WN;
   const v4i zero = {0, 0, 0, 0};
   v4i acc[FA][FB];
 #pragma unroll
@@ -1186,6 +1183,29 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
 #pragma unroll
   for (int p = 0; p < NBUF - 1; ++p)
     if (uint64_t(p) < nsteps) copy_step(p, p);
+  // the epilogue's row sums and scales, loaded while the K loop runs
+  const uint32_t g = lane >> 4, i = lane & 15;
+  int32_t ep_rowsum[FB], ep_scale[FB];
+#pragma unroll
+  for (int tj = 0; tj < FB; ++tj) {
+    const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
+    const uint64_t rc = row < n_rows ? row : n_rows - 1;
+    ep_rowsum[tj] = rowsum[rc];
+    ep_scale[tj] = scale[rc];
+  }
+  // per token group, the parts that take four limbs (bit p); the block runs
+  // four limbs when any group needs them anywhere (one limb count for the
+  // whole K range: a loop that switches between the two forms per part needs
+  // more registers than the larger block has)
+  uint64_t gmask[NG];
+  uint64_t fourmask = many ? 1 : 0;
+#pragma unroll
+  for (int t = 0; t < NG; ++t) {
+    const uint64_t bits = __ballot(lane < parts && flag[t] != 0);
+    gmask[t] = !many && at0 / 4 + t < ngroups ? bits : 0;
+    fourmask |= gmask[t];
+  }
+  four = fourmask != 0;
   // vmcnt immediate: wait until at most (NBUF - 2) steps of copies are outstanding
   constexpr int kWait = (NBUF - 2) * LPW;
   static_assert(kWait < 64, "vmcnt range");
@@ -1237,29 +1257,30 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   else kloop(std::integral_constant<int, 3>());
   // epilogue: lane 16 g + i holds, in component r of the four limb tiles of a
   // token group, the limb sums of token 16 group + 4 g + r and weight row 16 tile + i
-  const uint32_t g = lane >> 4, i = lane & 15;
 #pragma unroll
   for (int tg = 0; tg < FA / 4; ++tg) {
     const uint64_t grp = (at0 + wm * FA) / 4 + tg;
-    // the decomposition's constant per part: sum_p c_p S_p (S_p the part's row sum)
-    uint64_t gmask = 0;
-    if (grp < a_tiles / 4 && !many)
-      for (uint64_t p = 0; p < parts; ++p) gmask |= uint64_t(a_flags[grp * parts + p] != 0) << p;
+    // this group's four-limb parts (a uniform select among the block's groups)
+    uint64_t wmask = 0;
+#pragma unroll
+    for (int t = 0; t < NG; ++t)
+      if (uint32_t(t) == wm * (FA / 4) + tg) wmask = gmask[t];
 #pragma unroll
     for (int tj = 0; tj < FB; ++tj) {
     const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
     const uint64_t rc = row < n_rows ? row : n_rows - 1;
-    // the chunk holding column 0 adds the constant term (wrapping i64)
-    // (32896 S, plus 8388608 S_p for every four-limb part p)
+    // the chunk holding column 0 adds the constant term (wrapping i64): the
+    // decomposition's sum_p c_p S_p (S_p the row sum of part p), i.e. 32896 S
+    // plus 8388608 S_p for every four-limb part p
     uint64_t cterm = 0;
     if (chunk == 0) {
-      const bool all4 = many || gmask == (parts >= 64 ? ~uint64_t(0) : (uint64_t(1) << parts) - 1);
-      cterm = uint64_t(int64_t(all4 ? 8421504 : 32896) * rowsum[rc]);
+      const bool all4 = many || wmask == (parts >= 64 ? ~uint64_t(0) : (uint64_t(1) << parts) - 1);
+      cterm = uint64_t(int64_t(all4 ? 8421504 : 32896) * ep_rowsum[tj]);
       if (!all4)
-        for (uint64_t gm = gmask; gm; gm &= gm - 1)
+        for (uint64_t gm = wmask; gm; gm &= gm - 1)
           cterm += uint64_t(int64_t(8388608) * rowsum_p[uint64_t(__builtin_ctzll(gm)) * rowsum_p_ld + rc]);
     }
-    const uint64_t sc = uint64_t(int64_t(scale[rc]));
+    const uint64_t sc = uint64_t(int64_t(ep_scale[tj]));
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint64_t token = grp * 16 + 4 * g + r;
