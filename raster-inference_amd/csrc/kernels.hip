@@ -2211,7 +2211,7 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
     KSplit ks;
     ks.chunks = kc;
     ks.planes = planes;
-    launch_gemm_lds_shape<8, 8, 2, 2, 8, 2>(W, m, nullptr, 0, nullptr, a_tiled, a_tiles, s, {}, ks);
+    launch_gemm_lds_shape<8, 8, 2, 4, 8, 2>(W, m, nullptr, 0, nullptr, a_tiled, a_tiles, s, {}, ks);
     const uint64_t total = m * W.rows;
     hipLaunchKernelGGL(k_gemm_reduce, dim3(unsigned((total + 511) / 512)), dim3(256), 0, s, planes, kc, m, W.rows,
                        out, ld_out, acc_out, split ? *split : RowSplit{});
@@ -2220,17 +2220,18 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
   // row-split outputs take the 128 x 128 blocks only (their epilogue is kept
   // out of the 256 x 256 block's registers)
   if (split)
-    return launch_gemm_lds_shape<8, 8, 2, 2, 8, 2, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
+    return launch_gemm_lds_shape<8, 8, 2, 4, 8, 2, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
   // 64 tokens x 256 rows on 8 waves (one block per CU) when its blocks fill
-  // whole rounds of the device; otherwise 32 tokens x 128 rows on 4 waves
-  // (two blocks per CU), whose finer grid leaves a smaller last round
+  // whole rounds of the device; otherwise 32 tokens x 128 rows on 8 waves
+  // (two blocks per CU, so two waves per SIMD hide each other's LDS and
+  // MFMA latency), whose finer grid leaves a smaller last round
   const uint64_t cus = device_cus();
   const uint64_t big = ((m + 63) / 64) * (((W.rows + 15) / 16 + 15) / 16);
   const uint64_t rounds = (big + cus - 1) / cus;
   if (big >= cus && big * 10 >= rounds * cus * 9)
     launch_gemm_lds_shape<16, 16, 2, 4, 4, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   else
-    launch_gemm_lds_shape<8, 8, 2, 2, 8, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
+    launch_gemm_lds_shape<8, 8, 2, 4, 8, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
 }
 
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,

@@ -88,18 +88,36 @@ def test_gemm_adversarial_values(ctx):
 
 
 @pytest.mark.parametrize("m,n,k", [(100, 300, 2600), (200, 1000, 777), (64, 128, 4096)])
-def test_gemm_three_and_four_limb_groups(ctx, m, n, k):
-    # token groups of 16 whose activations all lie in [-2^23, 2^23) take three
-    # limbs, the others four: values at both edges of the range, one group
-    # with a single value just outside it, blocks mixing both kinds
+def test_gemm_limb_decompositions(ctx, m, n, k):
+    # token groups of 16 whose activations lie in [-2^23, 2^23) over a
+    # 512-column part take three limbs there, the others four: values at both
+    # edges of the range, groups with a single value outside it, values at the
+    # top of the int32 range, blocks mixing both kinds
     rng = np.random.default_rng(m + n + k)
     q, s = synthetic.random_int8_matrix(rng, n, k, scale_max=256)
     acts = act_slab(m, k, seed=k)
     acts[0, :4] = [2**23 - 1, -(2**23), 2**23 - 1, -(2**23)]     # group 0: three limbs, at the edges
     acts[17, k // 2] = 2**23                                       # group 1: four limbs (one value)
     acts[40, k - 1] = -(2**23) - 1                                  # group 2: four limbs (last column)
+    acts[50, 3] = 2**31 - 2**23                                     # group 3: top of the int32 range
+    acts[51, k // 3] = 2**31 - 2**23 - 1
+    acts[52, 130] = 2**31 - 1
     if m > 64:
         acts[64:80, :] = rng.integers(-(2**31), 2**31, size=(16, k), dtype=np.int64).astype(np.int32)
+    mat = ctx.upload_matrix(q, s)
+    got = gpu_slab(ctx, mat, acts)
+    exp = oracle_lib.det_linear_slab(expand(q, s), acts, threads=oracle_lib.cpu_count())
+    assert np.array_equal(got, exp)
+
+
+def test_gemm_unaligned_activation_rows(ctx):
+    # rows whose stride is not a multiple of 16 bytes take the per-element loads
+    m, n, k = 40, 96, 301
+    rng = np.random.default_rng(5)
+    q, s = synthetic.random_int8_matrix(rng, n, k, scale_max=256)
+    acts = act_slab(m, k, seed=9)
+    acts[3, 7] = 2**31 - 1
+    acts[20, 300] = -(2**31)
     mat = ctx.upload_matrix(q, s)
     got = gpu_slab(ctx, mat, acts)
     exp = oracle_lib.det_linear_slab(expand(q, s), acts, threads=oracle_lib.cpu_count())
