@@ -66,6 +66,8 @@ struct det_ctx {
   size_t gemm_a_bytes = 0;
   int64_t* gemm_planes = nullptr;  // K-range partial planes of split GEMMs
   size_t gemm_planes_bytes = 0;
+  void* attn_work = nullptr;  // work area of the MFMA form of causal attention
+  size_t attn_work_bytes = 0;
   bool capturing = false;  // between det_ctx_capture_begin and _end
 
   // scratch that has to grow cannot be allocated while the stream records
@@ -96,6 +98,26 @@ struct det_ctx {
       gemm_planes_bytes = bytes;
     }
     return gemm_planes;
+  }
+  // The MFMA attention's work area for a (null where that form does not
+  // apply or would need more than kAttnWorkMax bytes: the vector-ALU kernel
+  // runs then).
+  static constexpr uint64_t kAttnWorkMax = uint64_t(512) << 20;
+  void attach_attn_work(det::AttnArgs& a) {
+    const uint64_t bytes = det::attn_mfma_bytes(a);
+    a.work = nullptr;
+    a.work_bytes = 0;
+    if (bytes == 0 || bytes > kAttnWorkMax) return;
+    if (bytes > attn_work_bytes) {
+      grow_check("attention");
+      HIPC(hipStreamSynchronize(stream));
+      if (attn_work) HIPC(hipFree(attn_work));
+      attn_work = nullptr;
+      HIPC(hipMalloc(&attn_work, bytes));
+      attn_work_bytes = bytes;
+    }
+    a.work = attn_work;
+    a.work_bytes = attn_work_bytes;
   }
   // Slab GEMM / GEMV dispatch: int8 weights with at least kGemmMinRows
   // activation rows take the MFMA GEMM, everything else the GEMV kernels.
@@ -1250,6 +1272,7 @@ void layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const
     a.k = ws->kb; a.v = ws->vb; a.kv_ld = kw; a.ring_start = 0; a.ring_cap = 0; a.avail = n;
   }
   if (a.avail > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
+  ctx->attach_attn_work(a);
   det::launch_attention(a, st);
   post_attention(ws, L, n, ple_in);
 }
@@ -2705,6 +2728,7 @@ void det_ctx_destroy(det_ctx_t* ctx) {
   if (ctx->limbs) (void)hipFree(ctx->limbs);
   if (ctx->gemm_a) (void)hipFree(ctx->gemm_a);
   if (ctx->gemm_planes) (void)hipFree(ctx->gemm_planes);
+  if (ctx->attn_work) (void)hipFree(ctx->attn_work);
   if (ctx->argmax_scratch) (void)hipFree(ctx->argmax_scratch);
   if (ctx->argmax_out) (void)hipFree(ctx->argmax_out);
   (void)hipStreamDestroy(ctx->stream);
@@ -2870,6 +2894,7 @@ int det_attention_causal(det_ctx_t* ctx, const int32_t* q, const int32_t* k, con
     a.out = out; a.out_ld = nh * hd; a.hd = uint32_t(hd); a.num_heads = uint32_t(nh);
     a.groups = uint32_t(nh / nkv); a.n_queries = uint32_t(nq); a.causal = 1; a.window = window;
     a.causal_offset = 0; a.avail = nrows;
+    ctx->attach_attn_work(a);
     det::launch_attention(a, ctx->stream);
   });
 }

@@ -189,10 +189,37 @@ struct AttnArgs {
   // batched decode: query t uses seqs[t] (k, v, window) instead of the fields
   // above; fix_count then holds the longest window of the batch
   const AttnSeq* seqs;
+  // work area for the MFMA form of causal attention (attn_mfma_bytes(*this)
+  // bytes; without it the vector-ALU kernel runs)
+  void* work;
+  uint64_t work_bytes;
 };
 // Windows longer than kMaxAttentionRows are rejected by the callers.
 constexpr uint64_t kMaxAttentionRows = 16000;
 void launch_attention(const AttnArgs& a, hipStream_t s);
+
+// Causal attention over a linear cache on int8 MFMA (attention.hip): the
+// work area it needs (0 where it does not apply: ring caches, batched
+// windows, head dims not a multiple of 64 or above 512, fewer than 16
+// queries, unaligned rows), and the launch, false when it does not apply.
+uint64_t attn_mfma_bytes(const AttnArgs& a);
+bool launch_attention_mfma(const AttnArgs& a, void* work, uint64_t work_bytes, hipStream_t s);
+struct AttnMfmaArgs {
+  uint32_t hd, groups;
+  uint64_t n_queries, avail, window, causal_offset;
+  uint64_t nqt, nkt, nks, srow;  // query / key tiles of 16, key substeps of 64, score row stride
+  int32_t* out;
+  uint64_t out_ld;
+  int8_t* qlimbs;
+  int8_t* klimbs;
+  int8_t* vlimbs;
+  int64_t* qsum;
+  int64_t* ksum;
+  int64_t* vblk;
+  int32_t* scores;
+  int32_t* resid;
+  uint32_t* argm;
+};
 
 // Elementwise ops (saturating Q16.16).
 void launch_add_sat(int32_t* dst, const int32_t* src, uint64_t n, hipStream_t s);

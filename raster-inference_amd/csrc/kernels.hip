@@ -2327,6 +2327,7 @@ void launch_rope_rows(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, ui
 
 void launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.n_queries == 0 || a.num_heads == 0) return;
+  if (launch_attention_mfma(a, a.work, a.work_bytes, s)) return;
   uint64_t max_rows = a.causal ? (a.avail) : a.fix_count;
   if (max_rows == 0) max_rows = 1;
   // callers validate against kMaxAttentionRows first; a window that still

@@ -206,7 +206,12 @@ def oracle_attention(q, k, v, nq, nrows, nh, nkv, hd, window):
 
 
 @pytest.mark.parametrize("nq,nh,nkv,hd,window,mag", [(9, 4, 1, 16, 0, 18), (12, 2, 1, 2, 4, 16), (20, 8, 2, 256, 5, 16),
-                                                     (7, 2, 2, 64, 0, 31)])
+                                                     (7, 2, 2, 64, 0, 31),
+                                                     # 16 queries or more, head dims a multiple of 64:
+                                                     # the MFMA form, int32 extremes included
+                                                     (40, 4, 2, 64, 0, 31), (33, 4, 4, 128, 7, 31),
+                                                     (48, 2, 1, 512, 0, 24), (17, 8, 1, 64, 16, 31),
+                                                     (70, 6, 3, 192, 0, 20)])
 def test_attention_causal(ctx, nq, nh, nkv, hd, window, mag):
     rng = np.random.default_rng(nq * hd + mag)
     lim = 1 << mag
