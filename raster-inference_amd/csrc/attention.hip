@@ -286,141 +286,109 @@ __global__ __launch_bounds__(256) void k_attn_softmax_rows(AttnMfmaArgs a) {
   }
 }
 
-// Weighted sums: block (kv head, query tile T, dim tile D, pass of GB query
-// heads); wave w takes the key substeps ks0 + w, ks0 + w + 4, ... of the
-// tile's window and the waves' partial accumulators meet in LDS, where wave
-// 0 finishes. The weights (zero outside a query's window, the residual added
-// at its first argmax row) are split into three limbs per key substep; lane
-// l holds, in component r, query 16 T + 4 (l >> 4) + r and dim
-// 16 D + (l & 15). grid (kv heads, query tiles, dim tiles x G / GB), block 256.
+// Weighted sums: block (kv head, query tile T, group of 8 dim tiles), wave w
+// on dim tile 8 dg + w for all GB (= group size, at most 4) query heads.
+// Each key substep of the tile's union window, waves 0 .. GB-1 turn one
+// head's weights (zero outside a query's window, the residual added at its
+// first argmax row) into three limb operands in LDS (double-buffered), and
+// every wave multiplies them with its dim tile's V limbs. Lane l holds, in
+// component r, query 16 T + 4 (l >> 4) + r and dim 16 D + (l & 15).
+// grid (kv heads, query tiles, ceil(dim tiles / 8)), block 512.
 template <int GB>
-__global__ __launch_bounds__(256) void k_attn_wsum_mfma(AttnMfmaArgs a) {
-  __shared__ v4i part[3][GB][6][64];
-  __shared__ int64_t wpart[3][GB][64];
+__global__ __launch_bounds__(512) void k_attn_wsum_mfma(AttnMfmaArgs a) {
+  __shared__ v4i wlimb[2][GB][3][64];
+  __shared__ int64_t wq[GB][16];
   const uint32_t kvh = blockIdx.x, T = blockIdx.y, wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const uint32_t G = a.groups, ndt = a.hd / 16;
-  const uint32_t D = blockIdx.z % ndt, g0 = (blockIdx.z / ndt) * GB;
+  const uint32_t ndt = a.hd / 16, D = blockIdx.z * 8 + wave;
+  const bool d_on = D < ndt;
+  const uint32_t G = a.groups;
   const uint64_t t_lo = uint64_t(T) * 16;
   const uint64_t t_hi = t_lo + 15 < a.n_queries ? t_lo + 15 : a.n_queries - 1;
   const uint64_t kmin = attn_range(a, t_lo).start, kmax = attn_range(a, t_hi).end;
   const uint64_t ks0 = kmin / 64, ks1 = (kmax + 63) / 64;  // key substeps of the tile's union window
-  // this lane's A-operand query (row l & 15) and its window
+  // converting waves (wave < GB): head g = wave, query tq = lane & 15
+  const bool conv = wave < uint32_t(GB);
   const uint64_t tq = t_lo + (l & 15);
   const bool tq_on = tq < a.n_queries;
-  const AttnRange wq = attn_range(a, tq_on ? tq : a.n_queries - 1);
-  const int8_t* vb = a.vlimbs + (uint64_t(kvh) * ndt + D) * a.nks * 4 * kOp + l * 16;
-  int32_t res[GB];
-  uint32_t am[GB];
+  const AttnRange wr = attn_range(a, tq_on ? tq : a.n_queries - 1);
+  const uint64_t hq = uint64_t(kvh * G + (conv ? wave : 0)) * a.n_queries + (tq_on ? tq : 0);
+  const int32_t res = conv && tq_on ? a.resid[hq] : 0;
+  const uint32_t am = conv && tq_on ? a.argm[hq] : 0xffffffffu;
+  const int32_t* wrow = a.scores + hq * a.srow;
+  int64_t wsm = 0;
+  auto convert = [&](uint64_t ks, int buf) {
+    const uint64_t kb = ks * 64 + 16 * (l >> 4);
+    const int4* wp = reinterpret_cast<const int4*>(wrow + kb);
+    uint32_t wl[3][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-  for (int g = 0; g < GB; ++g) {
-    const uint64_t hq = uint64_t(kvh * G + g0 + g) * a.n_queries + tq;
-    res[g] = tq_on ? a.resid[hq] : 0;
-    am[g] = tq_on ? a.argm[hq] : 0xffffffffu;
-  }
-  // wave 0's epilogue sum over the union window of v - C4 for its lane's dim
-  // (read ahead of the loop)
-  const uint32_t dim = 16 * D + (l & 15);
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int4 x = wp[q4];
+      const int32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t key = kb + 4 * q4 + e;
+        int32_t wt = (tq_on && key >= wr.start && key < wr.end) ? xs[e] : 0;
+        if (key == am) wt = add_sat(wt, res);
+        wsm += int64_t(wt) - kC3;
+        const uint32_t u = (uint32_t(wt) + 0x800000u) ^ 0x00808080u;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) wl[i][q4] |= ((u >> (8 * i)) & 0xffu) << (8 * e);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      wlimb[buf][wave][i][l] = v4i{int(wl[i][0]), int(wl[i][1]), int(wl[i][2]), int(wl[i][3])};
+  };
+  const uint32_t dim = 16 * (d_on ? D : ndt - 1) + (l & 15);
+  const int8_t* vb = a.vlimbs + (uint64_t(kvh) * ndt + (d_on ? D : ndt - 1)) * a.nks * 4 * kOp + l * 16;
   int64_t vs = 0;
-  if (wave == 0)
-    for (uint64_t ks = ks0; ks < ks1; ++ks) vs += a.vblk[(uint64_t(kvh) * a.nks + ks) * a.hd + dim];
+  for (uint64_t ks = ks0; ks < ks1; ++ks) vs += a.vblk[(uint64_t(kvh) * a.nks + ks) * a.hd + dim];
   v4i acc[GB][6];
-  int64_t wsm[GB];
 #pragma unroll
-  for (int g = 0; g < GB; ++g) {
-    wsm[g] = 0;
+  for (int g = 0; g < GB; ++g)
 #pragma unroll
     for (int s = 0; s < 6; ++s) acc[g][s] = v4i{0, 0, 0, 0};
-  }
-  // a key substep's operands: the V limb blocks and the weights of the pass's heads
-  auto load_step = [&](uint64_t ks, v4i (&b)[4], int4 (&x)[GB][4]) {
+  if (conv && ks0 < ks1) convert(ks0, 0);
+  __syncthreads();
+  for (uint64_t ks = ks0; ks < ks1; ++ks) {
+    const int buf = int((ks - ks0) & 1);
+    v4i b[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4i*>(vb + (ks * 4 + j) * kOp);
-    const uint64_t kb = ks * 64 + 16 * (l >> 4);
+    // the next substep's limbs go to the other buffer while this one's MFMAs run
+    if (conv && ks + 1 < ks1) convert(ks + 1, buf ^ 1);
 #pragma unroll
-    for (int g = 0; g < GB; ++g) {
-      const uint64_t rq = (uint64_t(kvh * G + g0 + g) * a.n_queries + (tq_on ? tq : 0)) * a.srow;
-      const int4* wp = reinterpret_cast<const int4*>(a.scores + rq + kb);
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) x[g][q4] = wp[q4];
-    }
-  };
-  // this wave's first two substeps' loads issue together (a substep past the
-  // window reads the window's last substep and is not used)
-  const uint64_t kl = ks1 > ks0 ? ks1 - 1 : ks0;
-  v4i b0[4], b1[4];
-  int4 x0[GB][4], x1[GB][4];
-  load_step(ks0 + wave < kl ? ks0 + wave : kl, b0, x0);
-  load_step(ks0 + wave + 4 < kl ? ks0 + wave + 4 : kl, b1, x1);
-  auto process = [&](uint64_t ks, const v4i (&b)[4], const int4 (&x)[GB][4]) {
-    const uint64_t kb = ks * 64 + 16 * (l >> 4);
-#pragma unroll
-    for (int g = 0; g < GB; ++g) {
-      uint32_t wl[3][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int32_t xs[4] = {x[g][q4].x, x[g][q4].y, x[g][q4].z, x[g][q4].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint64_t key = kb + 4 * q4 + e;
-          int32_t wt = (tq_on && key >= wq.start && key < wq.end) ? xs[e] : 0;
-          if (key == am[g]) wt = add_sat(wt, res[g]);
-          wsm[g] += int64_t(wt) - kC3;
-          const uint32_t u = (uint32_t(wt) + 0x800000u) ^ 0x00808080u;
-#pragma unroll
-          for (int i = 0; i < 3; ++i) wl[i][q4] |= ((u >> (8 * i)) & 0xffu) << (8 * e);
-        }
-      }
+    for (int g = 0; g < GB; ++g)
 #pragma unroll
       for (int i = 0; i < 3; ++i) {
-        const v4i ai = {int(wl[i][0]), int(wl[i][1]), int(wl[i][2]), int(wl[i][3])};
+        const v4i ai = wlimb[buf][g][i][l];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           acc[g][i + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ai, b[j], acc[g][i + j], 0, 0, 0);
       }
-    }
-  };
-  const uint64_t kf = ks0 + wave;
-  if (kf < ks1) process(kf, b0, x0);
-  if (kf + 4 < ks1) process(kf + 4, b1, x1);
-  for (uint64_t ks = kf + 8; ks < ks1; ks += 4) {
-    v4i b[4];
-    int4 x[GB][4];
-    load_step(ks, b, x);
-    process(ks, b, x);
+    __syncthreads();
   }
-  if (wave > 0)
-#pragma unroll
-    for (int g = 0; g < GB; ++g) {
-      wpart[wave - 1][g][l] = wsm[g];
-#pragma unroll
-      for (int s = 0; s < 6; ++s) part[wave - 1][g][s][l] = acc[g][s];
-    }
+  // sum of w - 32896 per query and head, over the four key groups of the converting wave
+  if (conv) {
+    int64_t sq = wsm;
+    sq += __shfl_xor(sq, 16, 64);
+    sq += __shfl_xor(sq, 32, 64);
+    if (l < 16) wq[wave][l] = sq;
+  }
   __syncthreads();
-  if (wave != 0) return;
+  if (!d_on) return;
   const uint64_t rconst = (ks1 - ks0) * 64 * uint64_t(kC3) * uint64_t(kC4);
 #pragma unroll
   for (int g = 0; g < GB; ++g) {
-    // (each partial sum, and so their total, is below 2^31 in magnitude)
-#pragma unroll
-    for (int w = 0; w < 3; ++w) {
-      wsm[g] += wpart[w][g][l];
-#pragma unroll
-      for (int s = 0; s < 6; ++s) acc[g][s] += part[w][g][s][l];
-    }
-    // sum of w - 32896 per query: lanes l & 15 = query, over the four key groups
-    int64_t sq = wsm[g];
-    sq += __shfl_xor(sq, 16, 64);
-    sq += __shfl_xor(sq, 32, 64);
-    const uint32_t h = kvh * G + g0 + g;
+    const uint32_t h = kvh * G + g;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t qi = 4 * (l >> 4) + r;
-      const int64_t wq_sum = __shfl(sq, int(qi), 64);
       const uint64_t t = t_lo + qi;
       uint64_t dot = 0;
 #pragma unroll
       for (int s = 0; s < 6; ++s) dot += uint64_t(int64_t(acc[g][s][r])) << (8 * s);
-      dot += uint64_t(kC4) * uint64_t(wq_sum) + uint64_t(kC3) * uint64_t(vs) + rconst;
+      dot += uint64_t(kC4) * uint64_t(wq[g][qi]) + uint64_t(kC3) * uint64_t(vs) + rconst;
       if (t < a.n_queries) a.out[t * a.out_ld + uint64_t(h) * a.hd + dim] = requant(int64_t(dot));
     }
   }
@@ -432,7 +400,7 @@ __global__ __launch_bounds__(256) void k_attn_wsum_mfma(AttnMfmaArgs a) {
 // K and V, their offset sums, the score rows and the per-row residuals.
 uint64_t attn_mfma_bytes(const AttnArgs& a) {
   if (a.seqs || !a.causal || a.ring_cap || a.hd % 64 != 0 || a.hd > 512 || a.num_heads == 0 || a.groups == 0 ||
-      a.num_heads % a.groups != 0 ||
+      a.num_heads % a.groups != 0 || a.groups > 4 ||
       a.n_queries < 16 || a.avail == 0 || a.q_ld % 4 != 0 || a.kv_ld % 4 != 0 ||
       reinterpret_cast<uintptr_t>(a.q) % 16 != 0 || reinterpret_cast<uintptr_t>(a.k) % 16 != 0)
     return 0;
@@ -491,7 +459,7 @@ bool launch_attention_mfma(const AttnArgs& a, void* work, uint64_t work_bytes, h
                      a.hd, m.nks, m.vlimbs, m.vblk);
   const uint32_t gb = a.groups % 2 == 0 ? 2 : 1;
   const dim3 sgrid(unsigned(nkv), unsigned(m.nqt), unsigned((m.nkt + 3) / 4));
-  const dim3 wgrid(unsigned(nkv), unsigned(m.nqt), unsigned((a.hd / 16) * (a.groups / gb)));
+  const dim3 wgrid(unsigned(nkv), unsigned(m.nqt), unsigned((a.hd / 16 + 7) / 8));
 #define DET_SCORES(GB)                                                                                          \
   switch (nsub) {                                                                                               \
     case 1: hipLaunchKernelGGL((k_attn_scores_mfma<GB, 1>), sgrid, dim3(256), 0, s, m); break;                  \
@@ -510,10 +478,11 @@ bool launch_attention_mfma(const AttnArgs& a, void* work, uint64_t work_bytes, h
   }
 #undef DET_SCORES
   hipLaunchKernelGGL(k_attn_softmax_rows, dim3(unsigned(nh), unsigned((a.n_queries + 3) / 4)), dim3(256), 0, s, m);
-  if (gb == 2) {
-    hipLaunchKernelGGL(k_attn_wsum_mfma<2>, wgrid, dim3(256), 0, s, m);
-  } else {
-    hipLaunchKernelGGL(k_attn_wsum_mfma<1>, wgrid, dim3(256), 0, s, m);
+  switch (a.groups) {
+    case 1: hipLaunchKernelGGL(k_attn_wsum_mfma<1>, wgrid, dim3(512), 0, s, m); break;
+    case 2: hipLaunchKernelGGL(k_attn_wsum_mfma<2>, wgrid, dim3(512), 0, s, m); break;
+    case 3: hipLaunchKernelGGL(k_attn_wsum_mfma<3>, wgrid, dim3(512), 0, s, m); break;
+    default: hipLaunchKernelGGL(k_attn_wsum_mfma<4>, wgrid, dim3(512), 0, s, m); break;
   }
   return true;
 }
