@@ -149,70 +149,80 @@ __global__ __launch_bounds__(1024) void k_attn_split_v(const int32_t* __restrict
   }
 }
 
-// Scores: block (kv head, query tile T, group of 4 key tiles), wave w on key
-// tile 4 kg + w, GB query heads per pass, the NSUB head-dim substeps unrolled
-// (their loads issue together). Lane l holds, in component r, query
-// 16 T + 4 (l >> 4) + r and key 16 J + (l & 15). Scores outside a query's
-// window are not written. grid (kv heads, query tiles, ceil(key tiles / 4)),
-// block 256.
-template <int GB, int NSUB>
-__global__ __launch_bounds__(256) void k_attn_scores_mfma(AttnMfmaArgs a) {
+// Scores: block (kv head, query tile T, group of 8 key tiles), wave w on key
+// tile 8 kg + w. The block's query limb blocks (all G heads, 4 KB per head
+// and head-dim substep) are read once into LDS and shared by the waves; each
+// wave holds its key tile's limb blocks in registers and goes through the
+// heads. Lane l holds, in component r, query 16 T + 4 (l >> 4) + r and key
+// 16 J + (l & 15). Scores outside a query's window are not written.
+// grid (kv heads, query tiles, ceil(key tiles / 8)), block 512, LDS
+// G * NSUB * 4 KB.
+template <int NSUB>
+__global__ __launch_bounds__(512) void k_attn_scores_mfma(AttnMfmaArgs a) {
+  extern __shared__ v4i qsh[];  // [g][s][i][lane]
   const uint32_t kvh = blockIdx.x, T = blockIdx.y, wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const uint32_t J = blockIdx.z * 4 + wave;
   const uint32_t G = a.groups;
   const uint64_t t_lo = uint64_t(T) * 16;
   const uint64_t t_hi = t_lo + 15 < a.n_queries ? t_lo + 15 : a.n_queries - 1;
   const uint64_t kmin = attn_range(a, t_lo).start, kmax = attn_range(a, t_hi).end;
+  const uint64_t kg0 = uint64_t(blockIdx.z) * 128;  // the group's first key
+  if (kg0 >= kmax || kg0 + 128 <= kmin) return;    // (workgroup-uniform)
+  // the query limb blocks of the G heads
+  constexpr uint32_t per_head = NSUB * 4 * 64;  // v4i per head
+  for (uint32_t idx = threadIdx.x; idx < G * per_head; idx += 512) {
+    const uint32_t g = idx / per_head, rest = idx % per_head;
+    const uint64_t h = uint64_t(kvh) * G + g;
+    qsh[idx] = reinterpret_cast<const v4i*>(a.qlimbs + (h * a.nqt + T) * NSUB * 4 * kOp)[rest];
+  }
+  __syncthreads();
+  const uint32_t J = blockIdx.z * 8 + wave;
   const uint64_t key0 = uint64_t(J) * 16;
-  if (key0 >= kmax || key0 + 16 <= kmin || key0 >= a.avail) return;  // (no barriers in this kernel)
+  if (J >= a.nkt || key0 >= kmax || key0 + 16 <= kmin) return;  // (no barriers below)
   const uint64_t key = key0 + (l & 15);
   const int64_t ks = a.ksum[uint64_t(kvh) * a.nkt * 16 + key];
   const uint64_t cconst = uint64_t(NSUB) * 64 * uint64_t(kC4) * uint64_t(kC4);
   const int8_t* kb = a.klimbs + (uint64_t(kvh) * a.nkt + J) * NSUB * 4 * kOp + l * 16;
-  for (uint32_t g0 = 0; g0 < G; g0 += GB) {
-    v4i acc[GB][7];
+  v4i b[NSUB][4];
 #pragma unroll
-    for (int g = 0; g < GB; ++g)
+  for (int s = 0; s < NSUB; ++s)
 #pragma unroll
-      for (int s = 0; s < 7; ++s) acc[g][s] = v4i{0, 0, 0, 0};
+    for (int j = 0; j < 4; ++j) b[s][j] = *reinterpret_cast<const v4i*>(kb + (s * 4 + j) * kOp);
+  for (uint32_t g = 0; g < G; ++g) {
+    v4i acc[7];
 #pragma unroll
-    for (int s = 0; s < NSUB; ++s) {
-      v4i b[4], q[GB][4];
+    for (int s = 0; s < 7; ++s) acc[s] = v4i{0, 0, 0, 0};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4i*>(kb + (s * 4 + j) * kOp);
+    for (int s = 0; s < NSUB; ++s)
 #pragma unroll
-      for (int g = 0; g < GB; ++g) {
-        const uint32_t h = kvh * G + g0 + g;
-        const int8_t* qb = a.qlimbs + ((uint64_t(h) * a.nqt + T) * NSUB + s) * 4 * kOp + l * 16;
+      for (int i = 0; i < 4; ++i) {
+        const v4i q = qsh[((g * NSUB + s) * 4 + i) * 64 + l];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q[g][i] = *reinterpret_cast<const v4i*>(qb + i * kOp);
+        for (int j = 0; j < 4; ++j) acc[i + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(q, b[s][j], acc[i + j], 0, 0, 0);
       }
+    const uint32_t h = kvh * G + g;
 #pragma unroll
-      for (int g = 0; g < GB; ++g)
+    for (int r = 0; r < 4; ++r) {
+      const uint64_t t = t_lo + 4 * (l >> 4) + r;
+      if (t >= a.n_queries) continue;
+      const AttnRange w = attn_range(a, t);
+      if (key < w.start || key >= w.end) continue;
+      uint64_t dot = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[g][i + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(q[g][i], b[j], acc[g][i + j], 0, 0, 0);
-    }
-#pragma unroll
-    for (int g = 0; g < GB; ++g) {
-      const uint32_t h = kvh * G + g0 + g;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint64_t t = t_lo + 4 * (l >> 4) + r;
-        if (t >= a.n_queries) continue;
-        const AttnRange w = attn_range(a, t);
-        if (key < w.start || key >= w.end) continue;
-        uint64_t dot = 0;
-#pragma unroll
-        for (int s = 0; s < 7; ++s) dot += uint64_t(int64_t(acc[g][s][r])) << (8 * s);
-        dot += uint64_t(kC4) * uint64_t(ks) + uint64_t(kC4) * uint64_t(a.qsum[uint64_t(h) * a.nqt * 16 + t]) +
-               cconst;
-        a.scores[(uint64_t(h) * a.n_queries + t) * a.srow + key] = requant(int64_t(dot));
-      }
+      for (int s = 0; s < 7; ++s) dot += uint64_t(int64_t(acc[s][r])) << (8 * s);
+      dot += uint64_t(kC4) * uint64_t(ks) + uint64_t(kC4) * uint64_t(a.qsum[uint64_t(h) * a.nqt * 16 + t]) + cconst;
+      a.scores[(uint64_t(h) * a.n_queries + t) * a.srow + key] = requant(int64_t(dot));
     }
   }
+}
+
+template <int NSUB>
+void launch_scores_nsub(const AttnMfmaArgs& m, uint64_t nkv, hipStream_t s) {
+  const uint32_t lds = m.groups * NSUB * 4 * kOp;
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_scores_mfma<NSUB>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 4 * NSUB * 4 * kOp);
+  (void)attr;
+  const dim3 grid(unsigned(nkv), unsigned(m.nqt), unsigned((m.nkt + 7) / 8));
+  hipLaunchKernelGGL(k_attn_scores_mfma<NSUB>, grid, dim3(512), lds, s, m);
 }
 
 // Softmax of every (head, query) row in place, one wave per row (the
@@ -457,26 +467,17 @@ bool launch_attention_mfma(const AttnArgs& a, void* work, uint64_t work_bytes, h
   const unsigned vth = unsigned(64 * std::min<uint64_t>(a.hd / 16, 16));
   hipLaunchKernelGGL(k_attn_split_v, dim3(unsigned(nkv), unsigned(m.nks)), dim3(vth), 0, s, a.v, a.kv_ld, a.avail,
                      a.hd, m.nks, m.vlimbs, m.vblk);
-  const uint32_t gb = a.groups % 2 == 0 ? 2 : 1;
-  const dim3 sgrid(unsigned(nkv), unsigned(m.nqt), unsigned((m.nkt + 3) / 4));
   const dim3 wgrid(unsigned(nkv), unsigned(m.nqt), unsigned((a.hd / 16 + 7) / 8));
-#define DET_SCORES(GB)                                                                                          \
-  switch (nsub) {                                                                                               \
-    case 1: hipLaunchKernelGGL((k_attn_scores_mfma<GB, 1>), sgrid, dim3(256), 0, s, m); break;                  \
-    case 2: hipLaunchKernelGGL((k_attn_scores_mfma<GB, 2>), sgrid, dim3(256), 0, s, m); break;                  \
-    case 3: hipLaunchKernelGGL((k_attn_scores_mfma<GB, 3>), sgrid, dim3(256), 0, s, m); break;                  \
-    case 4: hipLaunchKernelGGL((k_attn_scores_mfma<GB, 4>), sgrid, dim3(256), 0, s, m); break;                  \
-    case 5: hipLaunchKernelGGL((k_attn_scores_mfma<GB, 5>), sgrid, dim3(256), 0, s, m); break;                  \
-    case 6: hipLaunchKernelGGL((k_attn_scores_mfma<GB, 6>), sgrid, dim3(256), 0, s, m); break;                  \
-    case 7: hipLaunchKernelGGL((k_attn_scores_mfma<GB, 7>), sgrid, dim3(256), 0, s, m); break;                  \
-    default: hipLaunchKernelGGL((k_attn_scores_mfma<GB, 8>), sgrid, dim3(256), 0, s, m); break;                 \
+  switch (nsub) {
+    case 1: launch_scores_nsub<1>(m, nkv, s); break;
+    case 2: launch_scores_nsub<2>(m, nkv, s); break;
+    case 3: launch_scores_nsub<3>(m, nkv, s); break;
+    case 4: launch_scores_nsub<4>(m, nkv, s); break;
+    case 5: launch_scores_nsub<5>(m, nkv, s); break;
+    case 6: launch_scores_nsub<6>(m, nkv, s); break;
+    case 7: launch_scores_nsub<7>(m, nkv, s); break;
+    default: launch_scores_nsub<8>(m, nkv, s); break;
   }
-  if (gb == 2) {
-    DET_SCORES(2)
-  } else {
-    DET_SCORES(1)
-  }
-#undef DET_SCORES
   hipLaunchKernelGGL(k_attn_softmax_rows, dim3(unsigned(nh), unsigned((a.n_queries + 3) / 4)), dim3(256), 0, s, m);
   switch (a.groups) {
     case 1: hipLaunchKernelGGL(k_attn_wsum_mfma<1>, wgrid, dim3(512), 0, s, m); break;
