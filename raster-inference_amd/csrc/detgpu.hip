@@ -1107,7 +1107,11 @@ void copy_d2d(det_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
 
 // Q/K/V projections + head norms + RoPE for M rows at positions pos0.. (det_kernels.rs:499-566, 930-985).
 // positions: one device position per row (batched decode) instead of pos0 + row.
-void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const uint64_t* positions = nullptr) {
+// With `cache`, the final K/V rows of tokens t >= cache_from are also written
+// to their canonical slots (t % cap on a ring, else t) when the head-norm
+// kernel takes the shape; returns whether it did.
+bool qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const uint64_t* positions = nullptr,
+               const GKv* cache = nullptr, uint64_t cache_from = 0) {
   det_ctx* ctx = s->m->ctx;
   hipStream_t st = ctx->stream;
   const uint64_t qw = L.num_heads * L.head_dim, kw = L.num_kv_heads * L.head_dim;
@@ -1135,6 +1139,29 @@ void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const
   } else {
     bail("Gemma layer is missing v_proj without attention_k_eq_v enabled");
   }
+  // head norms and RoPE in one launch where the shape allows
+  det::HeadNormRope hn;
+  hn.q = s->qb;
+  hn.k = s->kb;
+  hn.v = s->vb;
+  hn.q_gain = L.q_norm;
+  hn.k_gain = L.k_norm;
+  hn.nh = uint32_t(L.num_heads);
+  hn.nkv = uint32_t(L.num_kv_heads);
+  hn.hd = uint32_t(L.head_dim);
+  hn.half = uint32_t(L.rotary / 2);
+  hn.eps = L.eps;
+  hn.inv_freq = L.inv_freq;
+  hn.pos0 = pos0;
+  hn.positions = positions;
+  if (cache) {
+    hn.kc = cache->k;
+    hn.vc = cache->v;
+    hn.kv_from = cache_from;
+    hn.kv_cap = cache->cap;
+    hn.kv_ring = cache->ring ? 1 : 0;
+  }
+  if (det::launch_head_norm_rope(hn, M, st)) return cache != nullptr;
   det::launch_rmsnorm(s->qb, M * L.num_heads, L.head_dim, L.head_dim, L.q_norm, L.eps, st);
   det::launch_rmsnorm(s->kb, M * L.num_kv_heads, L.head_dim, L.head_dim, L.k_norm, L.eps, st);
   det::launch_rmsnorm(s->vb, M * L.num_kv_heads, L.head_dim, L.head_dim, nullptr, L.eps, st);
@@ -1145,6 +1172,7 @@ void qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const
     det::launch_rope(s->qb, M, qw, L.num_heads, L.head_dim, L.rotary / 2, L.inv_freq, pos0, 1, st);
     det::launch_rope(s->kb, M, kw, L.num_kv_heads, L.head_dim, L.rotary / 2, L.inv_freq, pos0, 1, st);
   }
+  return false;
 }
 
 // Everything after attention: O proj, norms, residuals, MLP, PLE, scalar
@@ -1236,8 +1264,14 @@ void layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const
   if (n > ws->max_tokens) bail("activation rows exceed the scratch capacity");
   if (!donor && !own) bail("transformer prefill layer needs its own cache or a donor cache");
   det::launch_rmsnorm_to(ws->normed, ws->x, n, H, H, L.in_ln, L.eps, st);
-  qkv_block(ws, L, n, 0);
   const uint64_t kw = L.num_kv_heads * L.head_dim;
+  // DetKvCacheData::from_head_slabs: keep the last rows past the window.
+  const uint64_t retained = (!donor && own && own->ring) ? (n > own->cap ? n - own->cap : 0) : 0;
+  if (!donor && own) {
+    if (own->row_w != kw) bail("layer cache head count mismatch");
+    if (n - retained > own->cap) bail("KV cache capacity exceeded");
+  }
+  const bool cached = qkv_block(ws, L, n, 0, nullptr, donor ? nullptr : own, retained);
   det::AttnArgs a{};
   a.q = ws->qb; a.q_ld = L.num_heads * L.head_dim;
   a.out = ws->attn; a.out_ld = L.num_heads * L.head_dim;
@@ -1254,13 +1288,9 @@ void layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const
     if (d.len < n) contract("attention_softmax requires a non-empty logits slice");
   } else {
     GKv& c = *own;
-    if (c.row_w != kw) bail("layer cache head count mismatch");
-    // DetKvCacheData::from_head_slabs: keep the last rows past the window.
-    const uint64_t retained = c.ring ? (n > c.cap ? n - c.cap : 0) : 0;
-    const uint64_t kept = n - retained;
-    if (kept > c.cap) bail("KV cache capacity exceeded");
-    // canonical slots: token t at t % cap (ring) or t (linear)
-    for (uint64_t t = retained; t < n;) {
+    // canonical slots: token t at t % cap (ring) or t (linear), unless the
+    // head-norm kernel wrote them
+    for (uint64_t t = cached ? n : retained; t < n;) {
       const uint64_t slot = c.ring ? t % c.cap : t;
       const uint64_t span = std::min<uint64_t>(n - t, c.cap - slot);
       copy_d2d(ctx, c.k + slot * kw, ws->kb + t * kw, span * kw * 4);

@@ -231,6 +231,28 @@ void launch_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s);
 // RoPE with one position per row (positions on the device).
 void launch_rope_rows(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t hd, uint64_t half,
                       const int64_t* inv_freq, const uint64_t* positions, hipStream_t s);
+
+// Head norms of M tokens' q / k / v rows and RoPE of the q and k rows in one
+// launch (q: [M][nh * hd], k and v: [M][nkv * hd]; v may be null); the same
+// results as launch_rmsnorm over each row set followed by launch_rope /
+// launch_rope_rows. Returns false (nothing launched) for shapes it does not
+// take: head dim above 512 or a rotation of more than 256 pairs.
+constexpr uint32_t kHeadRopeMaxHalf = 256;
+struct HeadNormRope {
+  int32_t *q, *k, *v;
+  const int32_t *q_gain, *k_gain;  // null: no gain
+  uint32_t nh, nkv, hd, half;      // half: rotated pairs per head (0: no rotation)
+  int64_t eps;
+  const int64_t* inv_freq;
+  uint64_t pos0;                   // token t at position pos0 + t, unless
+  const uint64_t* positions;       // one device position per token
+  // optional cache copies of the final k and v rows: token t >= kv_from to
+  // row t % kv_cap (kv_ring) or t of kc / vc (row width nkv * hd)
+  int32_t *kc = nullptr, *vc = nullptr;
+  uint64_t kv_from = 0, kv_cap = 0;
+  int kv_ring = 0;
+};
+bool launch_head_norm_rope(const HeadNormRope& a, uint64_t m, hipStream_t s);
 // Row i of k and v (width w) to kdst[i] / vdst[i] (device arrays of row pointers).
 void launch_kv_append(const int32_t* k, const int32_t* v, uint64_t w, uint64_t n, int32_t* const* kdst,
                       int32_t* const* vdst, hipStream_t s);

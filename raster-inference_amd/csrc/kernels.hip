@@ -1502,6 +1502,122 @@ __global__ void k_rope(int32_t* __restrict__ x, uint64_t rows, uint64_t ld, uint
   base[i + half] = add_sat(mul_sat(rhs, c), mul_sat(lhs, s));
 }
 
+// LDS hand-over between the lanes of one wave (no other wave involved)
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// The head norms of a token's q, k and v rows and the rotation of its q and
+// k rows in one pass (the arithmetic of k_rmsnorm over every head row, q rows
+// times q_gain, k rows times k_gain, v rows without gain, then k_rope on the
+// q and k rows): one workgroup per token computes the token's cos/sin pairs
+// once into LDS; each wave loads up to four of the token's head rows at a
+// time (rows wave, wave + 4, ...), normalises them, and writes a rotated
+// row through its own LDS row so that each pair's two elements meet in one
+// lane. E: elements per lane (head dim <= 64 E).
+template <int E>
+__global__ __launch_bounds__(256) void k_head_norm_rope(HeadNormRope a) {
+  constexpr int RPW = 4;  // head rows per wave in flight
+  __shared__ int32_t tcs[2][kHeadRopeMaxHalf];
+  __shared__ int32_t rowbuf[4][64 * E];
+  const uint64_t t = blockIdx.x;
+  const uint64_t pos = a.positions ? a.positions[t] : a.pos0 + t;
+  const bool rot = a.half != 0 && pos != 0;  // position 0 is the identity (ops.rs:179-181)
+  if (rot)
+    for (uint32_t i = threadIdx.x; i < a.half; i += 256) {
+      int32_t c, s;
+      sin_cos(rope_angle(pos, a.inv_freq[i]), &c, &s);
+      tcs[0][i] = c;
+      tcs[1][i] = s;
+    }
+  __syncthreads();
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hd = a.hd, half = a.half;
+  const uint32_t nv = a.v ? a.nkv : 0, nrows = a.nh + a.nkv + nv;
+  int32_t* rb = rowbuf[wave];
+  // this lane's q and k gains (every q row shares one gain vector, every k row another)
+  int32_t gq[E], gk[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
+    const uint32_t c = lane + 64 * k;
+    gq[k] = (a.q_gain && c < hd) ? a.q_gain[c] : 0;
+    gk[k] = (a.k_gain && c < hd) ? a.k_gain[c] : 0;
+  }
+  auto row_of = [&](uint32_t r) {
+    return r < a.nh ? a.q + (t * a.nh + r) * hd
+                    : (r < a.nh + a.nkv ? a.k + (t * a.nkv + (r - a.nh)) * hd
+                                        : a.v + (t * a.nkv + (r - a.nh - a.nkv)) * hd);
+  };
+  // this token's cache rows (k and v rows also go there)
+  const bool cached = a.kc && t >= a.kv_from;
+  const uint64_t slot = a.kv_ring ? t % a.kv_cap : t;
+  auto cache_of = [&](uint32_t r) -> int32_t* {
+    if (!cached || r < a.nh) return nullptr;
+    return r < a.nh + a.nkv ? a.kc + (slot * a.nkv + (r - a.nh)) * hd : a.vc + (slot * a.nkv + (r - a.nh - a.nkv)) * hd;
+  };
+  for (uint32_t r0 = wave; r0 < nrows; r0 += 4 * RPW) {
+    int32_t x[RPW][E];
+#pragma unroll
+    for (int u = 0; u < RPW; ++u) {
+      const uint32_t r = r0 + 4 * u;
+      const int32_t* row = row_of(r < nrows ? r : r0);
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        const uint32_t c = lane + 64 * k;
+        x[u][k] = (r < nrows && c < hd) ? row[c] : 0;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < RPW; ++u) {
+      const uint32_t r = r0 + 4 * u;
+      if (r >= nrows) break;  // (wave-uniform)
+      int32_t* row = row_of(r);
+      int32_t* crow = cache_of(r);
+      const bool is_q = r < a.nh, is_k = !is_q && r < a.nh + a.nkv;
+      const bool gained = is_q ? a.q_gain != nullptr : (is_k && a.k_gain != nullptr);
+      const bool rotate = rot && (is_q || is_k);
+      int64_t ss = 0;
+#pragma unroll
+      for (int k = 0; k < E; ++k) ss = add_sat64_nn(ss, sq_term(x[u][k]));
+      ss = wave_sum_sat(ss);
+      const int32_t sc = rms_scale_from_sumsq(ss, hd, a.eps);
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        const uint32_t c = lane + 64 * k;
+        if (c < hd) {
+          const int32_t y = mul_sat(x[u][k], sc);
+          const int32_t z = gained ? mul_sat(y, is_q ? gq[k] : gk[k]) : y;
+          if (rotate) {
+            rb[c] = z;
+          } else {
+            row[c] = z;
+            if (crow) crow[c] = z;
+          }
+        }
+      }
+      if (rotate) {
+        wave_lds_sync();  // the wave's LDS row is complete before its lanes read each other's elements
+        for (uint32_t i = lane; i < half; i += 64) {
+          const int32_t c = tcs[0][i], s = tcs[1][i];
+          const int32_t lhs = rb[i], rhs = rb[i + half];
+          const int32_t y0 = sub_sat(mul_sat(lhs, c), mul_sat(rhs, s));
+          const int32_t y1 = add_sat(mul_sat(rhs, c), mul_sat(lhs, s));
+          row[i] = y0;
+          row[i + half] = y1;
+          if (crow) crow[i] = y0, crow[i + half] = y1;
+        }
+        for (uint32_t c = 2 * half + lane; c < hd; c += 64) {
+          row[c] = rb[c];
+          if (crow) crow[c] = rb[c];
+        }
+        wave_lds_sync();  // every lane's reads of this row precede the next row's writes
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Attention for one (head, query): score dots -> integer softmax -> weighted
 // sum (det_kernels.rs:340-367, ops.rs:230-258).
@@ -2323,6 +2439,14 @@ void launch_rope_rows(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, ui
   if (total == 0) return;
   hipLaunchKernelGGL(k_rope, dim3(blocks_for(total, 256)), dim3(256), 0, s, x, rows, ld, heads, hd, half, inv_freq,
                      0, 0, positions);
+}
+
+bool launch_head_norm_rope(const HeadNormRope& a, uint64_t m, hipStream_t s) {
+  if (a.hd == 0 || a.hd > 512 || a.half > kHeadRopeMaxHalf || 2 * uint64_t(a.half) > a.hd) return false;
+  if (m == 0) return true;
+  if (a.hd <= 256) hipLaunchKernelGGL(k_head_norm_rope<4>, dim3(unsigned(m)), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(k_head_norm_rope<8>, dim3(unsigned(m)), dim3(256), 0, s, a);
+  return true;
 }
 
 void launch_attention(const AttnArgs& a, hipStream_t s) {

@@ -124,10 +124,11 @@ def model_tensor_shapes(cfg: dict) -> list[tuple[str, tuple[int, ...]]]:
     return out
 
 
-def tiny_model(seed: int = 0x5EED):
+def tiny_model(seed: int = 0x5EED, head_dim: int = 16):
     """Config + tensors of the tiny parity model: list of (name, values, row_scale)."""
     cfg = tiny_config()
     cfg["text_config"]["intermediate_size"] = 128
+    cfg["text_config"]["head_dim"] = head_dim
     tensors = []
     stream_seed = seed
     for name, shape in model_tensor_shapes(cfg):

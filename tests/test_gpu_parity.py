@@ -232,9 +232,10 @@ def test_argmax_first(ctx, n):
     assert ctx.argmax_first(ctx.to_device(x), n) == int(np.argmax(x))
 
 
-def test_elementwise_ops(ctx):
+@pytest.mark.parametrize("n", [3, 5000, 5003, 20483])
+def test_elementwise_ops(ctx, n):
+    # (n % 4 != 0: the quad-vector GELU kernel's scalar tail)
     rng = np.random.default_rng(1)
-    n = 5000
     x = rng.integers(-(1 << 31), 1 << 31, size=n, dtype=np.int64).astype(np.int32)
     y = rng.integers(-(1 << 20), 1 << 20, size=n).astype(np.int32)
     L = oracle_lib.lib()
@@ -282,8 +283,11 @@ def test_gpu_tiny_gemma_dev_matches_oracle(ctx):
     assert got == exp
 
 
-def test_gpu_tiny_baseline_model_matches_oracle(ctx):
-    cfg, tensors = synthetic.tiny_model()
+@pytest.mark.parametrize("head_dim", [16, 40, 384])
+def test_gpu_tiny_baseline_model_matches_oracle(ctx, head_dim):
+    # head dims up to 256 and 257-512 take the two forms of the prefill head
+    # norm + RoPE kernel (40: rows that are not whole waves)
+    cfg, tensors = synthetic.tiny_model(head_dim=head_dim)
     om = oracle_lib.OracleModel(cfg)
     gm = rd.Model(ctx, cfg)
     for name, v, s in tensors:
