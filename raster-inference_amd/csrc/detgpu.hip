@@ -1178,7 +1178,11 @@ bool qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const
 // Everything after attention: O proj, norms, residuals, MLP, PLE, scalar
 // (det_kernels.rs:733-818 / 1054-1128). Input residual in s->x, combined
 // attention heads in s->attn; result in s->x.
-void post_attention(det_session* s, const GLayer& L, uint64_t M, const int32_t* ple_in) {
+// With `next`, the last residual norm of the layer, the layer scalar and the
+// next layer's input norm run as one pass that also leaves next's normalised
+// rows in s->normed; returns whether it did.
+bool post_attention(det_session* s, const GLayer& L, uint64_t M, const int32_t* ple_in,
+                    const GLayer* next = nullptr) {
   det_ctx* ctx = s->m->ctx;
   hipStream_t st = ctx->stream;
   const uint64_t H = L.hidden;
@@ -1188,15 +1192,29 @@ void post_attention(det_session* s, const GLayer& L, uint64_t M, const int32_t* 
   ctx->linear_group({{L.gate, s->gate}, {L.up, s->up}}, s->normed, M, H);
   det::launch_gelu_mul(s->gate, s->up, M * L.gate->rows, st);
   linear(ctx, *L.down, s->gate, M, s->x2);
-  det::launch_rmsnorm_add(s->x, s->x2, s->x, M, H, H, L.post_ff_ln, L.eps, st);
-  if (L.has_ple && ple_in) {
-    const uint64_t P = L.ple_gate->rows;
-    linear(ctx, *L.ple_gate, s->x, M, s->gate);
-    det::launch_gelu_mul(s->gate, ple_in, M * P, st);
-    linear(ctx, *L.ple_proj, s->gate, M, s->x2);
-    det::launch_rmsnorm_add(s->x, s->x2, s->x, M, H, H, L.ple_post_norm, L.eps, st);
+  const bool ple = L.has_ple && ple_in;
+  const bool fuse_next = next && next->hidden == H && next->eps == L.eps;
+  // x = add_sat(norm(x2) * w, x), times the layer scalar; then next's input norm
+  auto last_norm = [&](const int32_t* w) {
+    if (fuse_next) {
+      det::launch_rmsnorm_add_norm(s->x, s->x2, s->normed, M, H, H, w, next->in_ln, L.eps, st,
+                                   L.layer_scalar.has_value(), L.layer_scalar.value_or(0));
+    } else {
+      det::launch_rmsnorm_add(s->x, s->x2, s->x, M, H, H, w, L.eps, st);
+      if (L.layer_scalar) det::launch_scale(s->x, M * H, *L.layer_scalar, st);
+    }
+  };
+  if (!ple) {
+    last_norm(L.post_ff_ln);
+    return fuse_next;
   }
-  if (L.layer_scalar) det::launch_scale(s->x, M * H, *L.layer_scalar, st);
+  det::launch_rmsnorm_add(s->x, s->x2, s->x, M, H, H, L.post_ff_ln, L.eps, st);
+  const uint64_t P = L.ple_gate->rows;
+  linear(ctx, *L.ple_gate, s->x, M, s->gate);
+  det::launch_gelu_mul(s->gate, ple_in, M * P, st);
+  linear(ctx, *L.ple_proj, s->gate, M, s->x2);
+  last_norm(L.ple_post_norm);
+  return fuse_next;
 }
 
 // PLE inputs for M tokens of one layer into out [M x P]
@@ -1255,7 +1273,11 @@ void kv_advance(GKv& c, uint64_t n) {
 // the rows its window keeps (DetKvCacheData::from_head_slabs,
 // det_tensor.rs:250-268); with a donor, attention reads the donor's cache and
 // `own` is left untouched (the reference returns no cache).
-void layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const GKv* donor, const int32_t* ple_in) {
+// `normed_ready`: the previous layer's last pass already wrote this layer's
+// input norm of ws->x into ws->normed. With `next`, this layer leaves next's
+// input norm there (returned true) or not (false).
+bool layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const GKv* donor, const int32_t* ple_in,
+                   const GLayer* next = nullptr, bool normed_ready = false) {
   det_model* m = ws->m;
   det_ctx* ctx = m->ctx;
   hipStream_t st = ctx->stream;
@@ -1263,7 +1285,7 @@ void layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const
   if (n == 0) bail("transformer layer execution requires at least one activation row");
   if (n > ws->max_tokens) bail("activation rows exceed the scratch capacity");
   if (!donor && !own) bail("transformer prefill layer needs its own cache or a donor cache");
-  det::launch_rmsnorm_to(ws->normed, ws->x, n, H, H, L.in_ln, L.eps, st);
+  if (!normed_ready) det::launch_rmsnorm_to(ws->normed, ws->x, n, H, H, L.in_ln, L.eps, st);
   const uint64_t kw = L.num_kv_heads * L.head_dim;
   // DetKvCacheData::from_head_slabs: keep the last rows past the window.
   const uint64_t retained = (!donor && own && own->ring) ? (n > own->cap ? n - own->cap : 0) : 0;
@@ -1304,7 +1326,7 @@ void layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const
   if (a.avail > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
   ctx->attach_attn_work(a);
   det::launch_attention(a, st);
-  post_attention(ws, L, n, ple_in);
+  return post_attention(ws, L, n, ple_in, next);
 }
 
 // det_layer_decode (det_kernels.rs:866-1133) on the activation row in ws->x,
@@ -1388,9 +1410,12 @@ void prefill(det_session* s, const uint32_t* ids, uint64_t n, uint32_t flags, de
   if (m->has_ple)
     for (uint64_t l = 0; l < m->layers.size(); ++l)
       if (m->layers[l].has_ple) ple_inputs(s, l, s->ids, s->x, n, s->ple_all + l * n * P);
+  bool ready = false;  // the layer's input norm was written by the previous layer
   for (uint64_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
-    layer_prefill(s, L, n, own_cache(s, L, l), donor_cache(s, L), (m->has_ple && L.has_ple) ? s->ple_all + l * n * P : nullptr);
+    const GLayer* next = l + 1 < m->layers.size() ? &m->layers[l + 1] : nullptr;
+    ready = layer_prefill(s, L, n, own_cache(s, L, l), donor_cache(s, L),
+                          (m->has_ple && L.has_ple) ? s->ple_all + l * n * P : nullptr, next, ready);
   }
   if (flags & DET_COMMIT_ACTIVATIONS) {
     host.resize(n * H);
@@ -2454,10 +2479,12 @@ bool trace_run(det_model* m, const det_trace_request_t* rq, TraceCollector& tc) 
   const uint64_t pw = std::min<uint64_t>(std::max<uint64_t>(rq->prefill_token_range_width ? rq->prefill_token_range_width
                                                                                           : UINT64_MAX, 1), n);
   std::vector<Fut> done;  // each layer's output commitment
+  bool ready = false;  // the layer's input norm was written by the previous layer
   for (uint64_t l = 0; l < nl; ++l) {
     const GLayer& L = m->layers[l];
-    layer_prefill(&sess, L, n, own_cache(&sess, L, l), donor_cache(&sess, L),
-                  (m->has_ple && L.has_ple) ? sess.ple_all + l * n * P : nullptr);
+    ready = layer_prefill(&sess, L, n, own_cache(&sess, L, l), donor_cache(&sess, L),
+                          (m->has_ple && L.has_ple) ? sess.ple_all + l * n * P : nullptr,
+                          l + 1 < nl ? &m->layers[l + 1] : nullptr, ready);
     if (!L.donor) {
       // the rows this layer's cache keeps, from the projection rows (kb / vb
       // hold all n rows until the next layer's projections)

@@ -153,7 +153,8 @@ void launch_rmsnorm_add(int32_t* dst, const int32_t* src, const int32_t* res, ui
 // x = add_sat(rmsnorm(src) * w1, x); normed = rmsnorm(x) * w2 (one pass for
 // rows of 2049-4096 columns, else the two launches above).
 void launch_rmsnorm_add_norm(int32_t* x, const int32_t* src, int32_t* normed, uint64_t rows, uint64_t cols,
-                             uint64_t ld, const int32_t* w1, const int32_t* w2, int64_t eps, hipStream_t s);
+                             uint64_t ld, const int32_t* w1, const int32_t* w2, int64_t eps, hipStream_t s,
+                             bool has_scalar = false, int32_t scalar = 0);
 void launch_rmsnorm_to(int32_t* dst, const int32_t* src, uint64_t rows, uint64_t cols, uint64_t ld, const int32_t* w,
                        int64_t eps, hipStream_t s);
 void launch_rope(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, uint64_t head_dim,

@@ -1429,13 +1429,16 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_wide(const int32_t* src, int32_t
 
 // The residual add after a sub-block and the next input norm in one pass
 // over a wide row (the two k_rmsnorm_wide launches it replaces, in order):
-// x = add_sat(rmsnorm(src) * w1, x), then normed = rmsnorm(x) * w2 (w1, w2
-// optional). One workgroup of NT threads per row, as k_rmsnorm_wide.
+// x = add_sat(rmsnorm(src) * w1, x) [then x = mul_sat(x, scalar) with
+// has_scalar, the layer scalar between two layers], then normed =
+// rmsnorm(x) * w2 (w1, w2 optional). One workgroup of NT threads per row, as
+// k_rmsnorm_wide.
 template <int NT, int EPT>
 __global__ __launch_bounds__(NT) void k_rmsnorm_add_norm(const int32_t* __restrict__ src, int32_t* __restrict__ x,
                                                          int32_t* __restrict__ normed, uint64_t cols, uint64_t ld,
                                                          const int32_t* __restrict__ w1,
-                                                         const int32_t* __restrict__ w2, int64_t eps) {
+                                                         const int32_t* __restrict__ w2, int64_t eps,
+                                                         int has_scalar, int32_t scalar) {
   __shared__ int64_t red[2][NT / 64];
   const uint64_t row = blockIdx.x;
   int32_t v[EPT], xv[EPT], g1[EPT], g2[EPT];
@@ -1465,7 +1468,9 @@ __global__ __launch_bounds__(NT) void k_rmsnorm_add_norm(const int32_t* __restri
   for (int e = 0; e < EPT; ++e) {
     const uint64_t c = threadIdx.x + uint64_t(NT) * e;
     const int32_t y = mul_sat(v[e], s1);
-    xv[e] = c < cols ? add_sat(w1 ? mul_sat(y, g1[e]) : y, xv[e]) : 0;
+    int32_t nx = add_sat(w1 ? mul_sat(y, g1[e]) : y, xv[e]);
+    if (has_scalar) nx = mul_sat(nx, scalar);
+    xv[e] = c < cols ? nx : 0;
     if (c < cols) x[row * ld + c] = xv[e];
     ss = add_sat64_nn(ss, sq_term(xv[e]));
   }
@@ -2404,13 +2409,18 @@ void launch_rmsnorm_add(int32_t* dst, const int32_t* src, const int32_t* res, ui
 }
 
 void launch_rmsnorm_add_norm(int32_t* x, const int32_t* src, int32_t* normed, uint64_t rows, uint64_t cols,
-                             uint64_t ld, const int32_t* w1, const int32_t* w2, int64_t eps, hipStream_t s) {
+                             uint64_t ld, const int32_t* w1, const int32_t* w2, int64_t eps, hipStream_t s,
+                             bool has_scalar, int32_t scalar) {
   if (rows == 0) return;
   if (cols > 2048 && cols <= 4096) {
     hipLaunchKernelGGL((k_rmsnorm_add_norm<256, 16>), dim3(unsigned(rows)), dim3(256), 0, s, src, x, normed, cols, ld,
-                       w1, w2, eps);
+                       w1, w2, eps, has_scalar ? 1 : 0, scalar);
   } else {
     launch_rmsnorm_add(x, src, x, rows, cols, ld, w1, eps, s);
+    if (has_scalar) {
+      if (ld != cols) throw std::runtime_error("rmsnorm_add_norm: the layer scalar needs contiguous rows");
+      launch_scale(x, rows * cols, scalar, s);
+    }
     launch_rmsnorm_to(normed, x, rows, cols, ld, w2, eps, s);
   }
 }

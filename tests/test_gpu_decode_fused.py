@@ -151,3 +151,18 @@ def test_fused_decode_with_per_layer_inputs_kv_sharing_and_scalars(ctx):
         rb = b.decode(tb, rd.DET_COMMIT_ALL | rd.DET_DECODE_PER_OP)
         assert (ra.activation, ra.logits, ra.kv, ra.next_token) == (rb.activation, rb.logits, rb.kv, rb.next_token), step
         ta, tb = ra.next_token, rb.next_token
+
+
+def test_e4b_shaped_layers_with_scalars_and_per_layer_inputs_match_oracle(ctx):
+    # hidden 2560: between prefill layers the last residual norm, the layer
+    # scalar and the next layer's input norm run as one row pass (two layer
+    # boundaries here, one after a PLE block)
+    cfg = synthetic.e4b_config(layers=3, vocab=4096, sliding_window=8, ple=256)
+    om, gm = fixtures.load_both(cfg, fixtures.custom_model(cfg, seed=5, scale_max=256, layer_scalars=True), ctx,
+                                threads=oracle_lib.cpu_count())
+    prompt = list(range(300, 300 + 19))
+    exp = om.capture(prompt, 3)
+    got = gm.capture(prompt, 3)
+    assert got["prefill"] == exp["prefill"]
+    assert got["first_step_layers"] == exp["first_step_layers"]
+    assert got["decode_steps"] == exp["decode_steps"]
