@@ -1189,8 +1189,20 @@ bool post_attention(det_session* s, const GLayer& L, uint64_t M, const int32_t* 
   linear(ctx, *L.o, s->attn, M, s->x2);
   // x = add_sat(norm(o), x); normed = norm(x) (pre-FF)
   det::launch_rmsnorm_add_norm(s->x, s->x2, s->normed, M, H, H, L.post_attn_ln, L.pre_ff_ln, L.eps, st);
-  ctx->linear_group({{L.gate, s->gate}, {L.up, s->up}}, s->normed, M, H);
-  det::launch_gelu_mul(s->gate, s->up, M * L.gate->rows, st);
+  // with the decode step's interleaved gate/up matrix, one GEMM whose
+  // epilogue forms gelu(gate) * up
+  const det_model* m = s->m;
+  const size_t li = size_t(&L - m->layers.data());
+  const det::DevMatrix* GU = (m->fused_ok && li < m->fused.size()) ? &m->fused[li].gateup : nullptr;
+  if (GU && M >= det_ctx::kGemmMinRows && GU->storage == det::kInt8 && GU->rows == 2 * L.gate->rows &&
+      GU->cols == H && L.gate->rows % 8 == 0) {
+    ctx->ensure_gemm_a(det::gemm_act_bytes(M, GU->kpad));
+    det::launch_gemm_limbs(s->normed, M, H, H, GU->kpad, ctx->gemm_a, st);
+    det::launch_gemm_tiled_gelu(*GU, M, s->gate, L.gate->rows, ctx->gemm_a, st);
+  } else {
+    ctx->linear_group({{L.gate, s->gate}, {L.up, s->up}}, s->normed, M, H);
+    det::launch_gelu_mul(s->gate, s->up, M * L.gate->rows, st);
+  }
   linear(ctx, *L.down, s->gate, M, s->x2);
   const bool ple = L.has_ple && ple_in;
   const bool fuse_next = next && next->hidden == H && next->eps == L.eps;

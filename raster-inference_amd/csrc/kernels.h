@@ -90,6 +90,12 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
                        int64_t* planes = nullptr);
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
                  int64_t* acc_out, int8_t* a_tiled, hipStream_t s, int64_t* planes = nullptr);
+// The gate/up projection with the GELU product in the GEMM epilogue: W holds
+// tiles of 8 gate rows followed by the matching 8 up rows (the decode step's
+// interleaved gate/up matrix), and out[t][f] = mul_sat(gelu(gate_f), up_f)
+// for f < W.rows / 2 (stride ld_out); a_tiled from launch_gemm_limbs.
+void launch_gemm_tiled_gelu(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, const int8_t* a_tiled,
+                            hipStream_t s);
 
 // Batch-1 int8 GEMV for the fused decode step (int8 storage, fits LDS):
 // act_i64 requantizes wrapped accumulators on load; epilogue 1 applies

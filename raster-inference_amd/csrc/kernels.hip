@@ -1093,7 +1093,11 @@ __global__ __launch_bounds__(256) void k_act_limbs_tiled(const int32_t* __restri
 // and the 128-bit operand reads do not conflict on LDS banks. The MFMAs of a
 // step run as two passes over the wave's tile pairs (first 64 columns, then
 // the second 64), so consecutive MFMAs never share an accumulator.
-template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT>
+// GELU: W holds tiles of 8 gate rows and the matching 8 up rows (rows
+// 16 t + i, i < 8: gate row 8 t + i; rows 16 t + 8 + i: up row 8 t + i) and
+// out[token][8 t + i] = mul_sat(gelu(gate), up) (the decode step's gate/up
+// epilogue; no other output form).
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT, bool GELU = false>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
                                                            const int32_t* __restrict__ scale,
                                                            const int32_t* __restrict__ rowsum,
@@ -1281,6 +1285,30 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
           cterm += uint64_t(int64_t(8388608) * rowsum_p[uint64_t(__builtin_ctzll(gm)) * rowsum_p_ld + rc]);
     }
     const uint64_t sc = uint64_t(int64_t(ep_scale[tj]));
+    if constexpr (GELU) {
+      int32_t val[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t p[4] = {acc[4 * tg][tj][r], acc[4 * tg + 1][tj][r], acc[4 * tg + 2][tj][r], acc[4 * tg + 3][tj][r]};
+        const int64_t dot = p[0] + p[1] * 256 + p[2] * 65536 + p[3] * 16777216 + int64_t(cterm);
+        val[r] = requant(int64_t(uint64_t(dot) * sc));
+      }
+      // lane i < 8 holds gate row i, lane i + 8 its up row: the lower lanes
+      // take tokens 4 g and 4 g + 1, the upper lanes 4 g + 2 and 4 g + 3, each
+      // receiving the other half's values of its tokens
+      const bool lo = i < 8;
+      const int32_t send0 = lo ? val[2] : val[0], send1 = lo ? val[3] : val[1];
+      const int32_t recv0 = __shfl(send0, int(lane ^ 8u), 64), recv1 = __shfl(send1, int(lane ^ 8u), 64);
+      const int32_t g0 = lo ? val[0] : recv0, u0 = lo ? recv0 : val[2];
+      const int32_t g1 = lo ? val[1] : recv1, u1 = lo ? recv1 : val[3];
+      const uint64_t f = (bt0 + wn * FB + tj) * 8 + (i & 7);
+      const uint64_t t0 = grp * 16 + 4 * g + (lo ? 0 : 2);
+      if (row < n_rows) {  // (whole tiles: the up row is there too)
+        if (t0 < m_tokens) out[t0 * ld_out + f] = mul_sat(gelu_act(g0), u0);
+        if (t0 + 1 < m_tokens) out[(t0 + 1) * ld_out + f] = mul_sat(gelu_act(g1), u1);
+      }
+      continue;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint64_t token = grp * 16 + 4 * g + r;
@@ -2272,18 +2300,18 @@ uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) {
   return gemm_tile_bytes(m, kpad) + 4 * groups * limb_parts(kpad);
 }
 
-template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT = false>
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT = false, bool GELU = false>
 static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
                                   const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s, RowSplit split = {},
                                   KSplit ks = {}) {
   constexpr uint32_t lds = uint32_t(NBUF) * (TA + TB) * 2048u;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT>), hipFuncAttributeMaxDynamicSharedMemorySize,
-      int(lds));
+      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
   (void)attr;
   const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
   const uint64_t nblocks = ((W.rows + 15) / 16 + TB - 1) / TB;
-  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT>), dim3(unsigned(mblocks * nblocks * ks.chunks)),
+  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU>), dim3(unsigned(mblocks * nblocks * ks.chunks)),
                      dim3(64 * WM * WN), lds, s, a_tiled, W.q, W.scale, W.rowsum, W.rowsum_p, W.rowsum_p_ld, W.rows,
                      W.kpad, m, a_tiles, gemm_flags(a_tiled, m, W.kpad), uint32_t(mblocks), out, ld_out, acc_out,
                      split, ks);
@@ -2353,6 +2381,16 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
     launch_gemm_lds_shape<16, 16, 2, 4, 4, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   else
     launch_gemm_lds_shape<8, 8, 2, 4, 8, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
+}
+
+void launch_gemm_tiled_gelu(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, const int8_t* a_tiled,
+                            hipStream_t s) {
+  if (W.rows == 0 || m == 0) return;
+  if (W.rows % 16) throw std::invalid_argument("gate/up GEMM: rows must be whole tiles of 8 gate + 8 up rows");
+  const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
+  // 128 x 128 blocks at every m (no K split): with the GELU arithmetic in its
+  // epilogue the 256 x 256 block does not fit its registers
+  launch_gemm_lds_shape<8, 8, 2, 4, 8, 2, false, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s);
 }
 
 void launch_gemm(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t ld_act, int32_t* out, uint64_t ld_out,
