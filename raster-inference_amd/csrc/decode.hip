@@ -673,7 +673,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_wsum(AttnDecArgs a) {
 // the window and applies the residual ONE - sum to that row, as the reference
 // does before the weighted sum. Workgroup 0 clears the projection
 // accumulators read by the scores kernel.
-template <int P, uint32_t MAXHD>
+template <int P, uint32_t MAXHD, bool OH = false>
 __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   constexpr uint32_t R = P * kAttnWsumRows;  // window rows of this workgroup
   constexpr int NS = 4;                       // score rows per thread held in registers
@@ -685,10 +685,14 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   __shared__ int64_t part[3][1024];
   seq_view(a);
   const Window win = attn_window(a);
-  const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
+  // OH: one query head per workgroup (grid x = query head); else every
+  // query head of KV head blockIdx.x. GW heads from h_first.
+  const uint32_t G = a.nh / a.nkv, hd = a.hd;
+  const uint32_t kvh = OH ? blockIdx.x / G : blockIdx.x;
+  const uint32_t GW = OH ? 1u : G, h_first = OH ? blockIdx.x : kvh * G;
   if (blockIdx.y == 0) {
-    for (uint32_t i = threadIdx.x; i < G * hd; i += 1024) a.qkv[uint64_t(kvh) * G * hd + i] = 0;
-    if (a.own_cache)
+    for (uint32_t i = threadIdx.x; i < GW * hd; i += 1024) a.qkv[uint64_t(h_first) * hd + i] = 0;
+    if (a.own_cache && (!OH || blockIdx.x % G == 0))
       for (uint32_t i = threadIdx.x; i < hd; i += 1024) {
         a.qkv[(uint64_t(a.nh) + kvh) * hd + i] = 0;
         if (a.has_v) a.qkv[(uint64_t(a.nh) + a.nkv + kvh) * hd + i] = 0;
@@ -700,10 +704,10 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   const uint64_t nr = win.cnt - r0 < R ? win.cnt - r0 : R;
   const uint64_t kvw = uint64_t(a.nkv) * hd;
   // this wave's head and its rows r = wi * 64 + lane + stride * n
-  const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;
-  const bool active = g < G;
+  const uint32_t wph = 16 / GW, g = wave / wph, wi = wave % wph;
+  const bool active = g < GW;
   const uint64_t stride = 64 * uint64_t(wph);
-  const uint64_t head = uint64_t(kvh) * G + (active ? g : 0);
+  const uint64_t head = uint64_t(h_first) + (active ? g : 0);
   const int32_t* scg = a.scores + head * a.max_rows;
   const uint64_t nch = (win.cnt + kAttnScoreRows - 1) / kAttnScoreRows;
   // The chunk keys and the first NS of this thread's scores are read before
@@ -762,7 +766,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   s = wsum_wrap(s);
   if (lane == 0) red[wave] = s;
   __syncthreads();
-  if (threadIdx.x < G) {
+  if (threadIdx.x < GW) {
     int64_t t = 0;
     for (uint32_t w = 0; w < wph; ++w) t += red[threadIdx.x * wph + w];
     hsum[threadIdx.x] = t;
@@ -780,7 +784,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
       }
   __syncthreads();
   // raw weights of this workgroup's rows
-  for (uint32_t idx = threadIdx.x; idx < G * R; idx += 1024) {
+  for (uint32_t idx = threadIdx.x; idx < GW * R; idx += 1024) {
     const uint32_t gg = idx / R, rr = idx % R;
     const uint64_t M = hrec[gg];
     wl[gg][rr] = rr < nr ? (M ? softmax_weight_r(el[gg][rr], hsum[gg], M) : softmax_weight(el[gg][rr], hsum[gg])) : 0;
@@ -816,8 +820,8 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
   // heads per pass, one atomic per (head, dim)
   const uint32_t dstr = hd > 256 ? 512 : 256;
   const uint32_t hpp = 1024 / dstr;
-  for (uint32_t h0 = 0; h0 < G; h0 += hpp) {
-    const uint32_t hn = G - h0 < hpp ? G - h0 : hpp;
+  for (uint32_t h0 = 0; h0 < GW; h0 += hpp) {
+    const uint32_t hn = GW - h0 < hpp ? GW - h0 : hpp;
     if (sl > 0)
       for (uint32_t hh = 0; hh < hn; ++hh) {
         int64_t p0 = 0, p1 = 0;
@@ -849,7 +853,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_softmax_wsum(AttnDecArgs a) {
           p0 = int64_t(uint64_t(p0) + uint64_t(part[q][hh * dstr + dl]));
           if (dstr == 512) p1 = int64_t(uint64_t(p1) + uint64_t(part[q][hh * dstr + 256 + dl]));
         }
-        int64_t* out = a.acc + (uint64_t(kvh) * G + h0 + hh) * hd;
+        int64_t* out = a.acc + (uint64_t(h_first) + h0 + hh) * hd;
         if (dl < hd) atomicAdd(reinterpret_cast<unsigned long long*>(out + dl), static_cast<unsigned long long>(p0));
         if (dl + 256 < hd)
           atomicAdd(reinterpret_cast<unsigned long long*>(out + dl + 256), static_cast<unsigned long long>(p1));
@@ -1029,6 +1033,19 @@ void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
     hipLaunchKernelGGL(k_dec_attn_stats, dim3(a.nkv, 1, ns), dim3(1024), lds, s, a);
   } else if (part == 2) {
     DET_ATTN_P(P, a.hd, k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, P * kAttnWsumRows), ns), dim3(1024), 0, s, a);
+  } else if (uint64_t(a.nh) * nblk(a.cap, P * kAttnWsumRows) * ns <= 256) {
+    // one query head per workgroup while that grid still fits the device in
+    // one pass: each workgroup's exp terms (the window of its heads, vector
+    // ALU bound) are those of one head instead of all heads of a KV head
+    const dim3 grid(a.nh, nblk(a.cap, P * kAttnWsumRows), ns);
+    if (a.hd <= 256) {
+      if (P == 4) hipLaunchKernelGGL((k_dec_attn_softmax_wsum<4, 256, true>), grid, dim3(1024), 0, s, a);
+      else if (P == 2) hipLaunchKernelGGL((k_dec_attn_softmax_wsum<2, 256, true>), grid, dim3(1024), 0, s, a);
+      else hipLaunchKernelGGL((k_dec_attn_softmax_wsum<1, 256, true>), grid, dim3(1024), 0, s, a);
+    } else {
+      if (P == 2) hipLaunchKernelGGL((k_dec_attn_softmax_wsum<2, kDecMaxHeadDim, true>), grid, dim3(1024), 0, s, a);
+      else hipLaunchKernelGGL((k_dec_attn_softmax_wsum<1, kDecMaxHeadDim, true>), grid, dim3(1024), 0, s, a);
+    }
   } else {
     DET_ATTN_P(P, a.hd, k_dec_attn_softmax_wsum, dim3(a.nkv, nblk(a.cap, P * kAttnWsumRows), ns), dim3(1024), 0, s, a);
   }

@@ -676,16 +676,6 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
 // (stride out_kpad) to out_limbs.
 constexpr int kNormD = 5;
 constexpr uint32_t kNormMaxK = 4096;
-// s_waitcnt lgkmcnt(0) with the vector-memory count left open
-constexpr int kWaitLdsOnly = 15 | (7 << 4) | (0 << 8) | (3 << 14);
-// LDS hand-over inside a workgroup that leaves its global loads in flight (a
-// __syncthreads fence would wait for them).
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 // rms scale of a row spread over the workgroup from each thread's saturating
 // partial sum of squares (ops.rs:406-425): wave 0 reduces the wave totals and
 // runs the scale chain once.
@@ -1533,14 +1523,6 @@ __global__ void k_rope(int32_t* __restrict__ x, uint64_t rows, uint64_t ld, uint
   const int32_t lhs = base[i], rhs = base[i + half];
   base[i] = sub_sat(mul_sat(lhs, c), mul_sat(rhs, s));
   base[i + half] = add_sat(mul_sat(rhs, c), mul_sat(lhs, s));
-}
-
-// LDS hand-over between the lanes of one wave (no other wave involved)
-__device__ __forceinline__ void wave_lds_sync() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
-  __builtin_amdgcn_wave_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // The head norms of a token's q, k and v rows and the rotation of its q and

@@ -36,6 +36,25 @@ __device__ __forceinline__ int4 load_int4(global_ptr<const int32_t> p) {
   return make_int4(v.x, v.y, v.z, v.w);
 }
 
+// s_waitcnt lgkmcnt(0) with the vector-memory count left open
+constexpr int kWaitLdsOnly = 15 | (7 << 4) | (0 << 8) | (3 << 14);
+// LDS hand-over inside a workgroup that leaves its global loads in flight (a
+// __syncthreads fence would wait for them). Only LDS contents are handed over:
+// global memory written by one wave is not made visible to the others.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// LDS hand-over between the lanes of one wave (no other wave involved)
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <int CTRL>
 __device__ __forceinline__ uint64_t dpp_move64(uint64_t v) {
   const uint32_t lo = uint32_t(__builtin_amdgcn_mov_dpp(int(uint32_t(v)), CTRL, 0xf, 0xf, false));
