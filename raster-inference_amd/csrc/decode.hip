@@ -268,26 +268,33 @@ __device__ __forceinline__ void seq_view(AttnDecArgs& a) {
 // Sixteen lanes share one key row per chunk; the key rows of all P chunks are
 // fetched at the start. Workgroup 0 also zeroes the heads' weighted-sum
 // accumulators. The argmax key of every chunk goes to keys.
-template <bool VEC, int P, uint32_t MAXHD>
+template <bool VEC, int P, uint32_t MAXHD, bool OH = false>
 __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   __shared__ int32_t ql[kDecMaxGroup * kDecMaxHeadDim];
   __shared__ int32_t kn[kDecMaxHeadDim];
   __shared__ int64_t ck[P][kDecMaxGroup][kAttnScoreRows];
   seq_view(a);
-  const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv, hd = a.hd;
-  // head-norm jobs: 0..G-1 the queries, G the new key, G + 1 the new value.
+  // OH: one query head per workgroup (grid x = query head), else every query
+  // head of KV head blockIdx.x: GW heads from h_first. Only the writer (the
+  // first head's workgroup under OH) stores the new key and value rows.
+  const uint32_t G = a.nh / a.nkv, hd = a.hd;
+  const uint32_t kvh = OH ? blockIdx.x / G : blockIdx.x;
+  const uint32_t GW = OH ? 1u : G, h_first = OH ? blockIdx.x : kvh * G;
+  const bool writer = !OH || blockIdx.x % G == 0;
+  // head-norm jobs: 0..GW-1 the queries, GW the new key, GW + 1 the new value
+  // (the writer only).
   // This wave's first job's accumulators are read before anything else (the
   // key-row loads below would otherwise be waited for first); the key and
   // value rows are read even where this workgroup turns out not to hold the
   // step's own row, and then go unused.
   const uint32_t wv = threadIdx.x >> 6;
-  const uint32_t njobs_max = G + (a.own_cache ? (a.has_v ? 2u : 1u) : 0u);
+  const uint32_t njobs_max = GW + (a.own_cache ? ((a.has_v && writer) ? 2u : 1u) : 0u);
   HeadRowIn<MAXHD> pre;
   auto job_src = [&](uint32_t job) {
-    return job < G ? a.qkv + (uint64_t(kvh) * G + job) * hd
-                   : a.qkv + (uint64_t(a.nh) + (job == G ? 0 : a.nkv) + kvh) * hd;
+    return job < GW ? a.qkv + (uint64_t(h_first) + job) * hd
+                    : a.qkv + (uint64_t(a.nh) + (job == GW ? 0 : a.nkv) + kvh) * hd;
   };
-  auto job_gain = [&](uint32_t job) { return job < G ? a.q_norm : (job == G ? a.k_norm : nullptr); };
+  auto job_gain = [&](uint32_t job) { return job < GW ? a.q_norm : (job == GW ? a.k_norm : nullptr); };
   const uint32_t pj = wv < njobs_max ? wv : 0;  // (idle waves read job 0's row and drop it)
   load_head_row(job_src(pj), hd, job_gain(pj), threadIdx.x & 63, pre);
   // cos/sin of this thread's first two rotation slots, also read ahead of the
@@ -307,9 +314,9 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   }
   const Window win = attn_window(a);
   const uint64_t r0 = uint64_t(blockIdx.y) * P * kAttnScoreRows;
-  const uint64_t qoff = uint64_t(kvh) * G * hd;
+  const uint64_t qoff = uint64_t(h_first) * hd;
   if (blockIdx.y == 0)
-    for (uint32_t i = threadIdx.x; i < G * hd; i += 512) a.acc[qoff + i] = 0;
+    for (uint32_t i = threadIdx.x; i < GW * hd; i += 512) a.acc[qoff + i] = 0;
   if (r0 >= win.cnt) return;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t cur = win.cnt - 1;  // window row of the step's own token
@@ -346,35 +353,35 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
       }
     }
   }
-  // head rows: jobs 0..G-1 are the queries, then the new key (and value) rows
-  const uint32_t nkeys = has_new ? (a.has_v ? 2 : 1) : 0;
+  // head rows: jobs 0..GW-1 are the queries, then the new key (and value) rows
+  const uint32_t nkeys = has_new ? ((a.has_v && writer) ? 2 : 1) : 0;
   const global_ptr<int32_t> kslot = to_global(a.k) + win.slot * kvw + uint64_t(kvh) * hd;
   const global_ptr<int32_t> vslot = to_global(a.v) + win.slot * kvw + uint64_t(kvh) * hd;
   const global_ptr<int32_t> no_row = nullptr;
   auto norm_job = [&](uint32_t job, const HeadRowIn<MAXHD>& in) {
     const bool gained = job_gain(job) != nullptr;
-    if (job < G) {
+    if (job < GW) {
       norm_head_row(in, hd, a.eps, gained, ql + job * hd, no_row, lane);
-    } else if (job == G) {
-      norm_head_row(in, hd, a.eps, gained, kn, a.has_v ? no_row : vslot, lane);
+    } else if (job == GW) {
+      norm_head_row(in, hd, a.eps, gained, kn, (a.has_v || !writer) ? no_row : vslot, lane);
     } else {
       norm_head_row(in, hd, a.eps, gained, vslot, no_row, lane);
     }
   };
   // the wave's first job straight from the preloaded registers (a copy into a
   // loop variable would wait for every load in flight, key rows included)
-  if (wave < G + nkeys) norm_job(wave, pre);
-  for (uint32_t job = wave + 8; job < G + nkeys; job += 8) {
+  if (wave < GW + nkeys) norm_job(wave, pre);
+  for (uint32_t job = wave + 8; job < GW + nkeys; job += 8) {
     HeadRowIn<MAXHD> in;
     load_head_row(job_src(job), hd, job_gain(job), lane, in);
     norm_job(job, in);
   }
   __syncthreads();
   if (half && win.pos != 0) {
-    const uint32_t rows = G + (has_new ? 1 : 0);
+    const uint32_t rows = GW + (has_new ? 1 : 0);
     for (uint32_t idx = threadIdx.x, u = 0; idx < rows * half; idx += 512, ++u) {
       const uint32_t r = idx / half, i = idx % half;
-      int32_t* y = r < G ? ql + r * hd : kn;
+      int32_t* y = r < GW ? ql + r * hd : kn;
       const int32_t c = u == 0 ? tc[0] : (u == 1 ? tc[1] : a.trig[2 * i]);
       const int32_t s = u == 0 ? ts[0] : (u == 1 ? ts[1] : a.trig[2 * i + 1]);
       const int32_t lhs = y[i], rhs = y[i + half];
@@ -383,7 +390,7 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
     }
     __syncthreads();
   }
-  if (has_new)
+  if (has_new && writer)
     for (uint32_t d = threadIdx.x; d < hd; d += 512) kslot[d] = kn[d];
 #pragma unroll
   for (int p = 0; p < P; ++p)
@@ -403,7 +410,7 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
         }
       }
     }
-  for (uint32_t g = 0; g < G; ++g) {
+  for (uint32_t g = 0; g < GW; ++g) {
     const int32_t* qg = ql + g * hd;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -431,7 +438,7 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
       if (li == 0) {
         const uint64_t j = r0 + p * kAttnScoreRows + grp;
         const int32_t sc = requant(acc);
-        if (valid[p]) a.scores[(uint64_t(kvh) * G + g) * a.max_rows + j] = sc;
+        if (valid[p]) a.scores[(uint64_t(h_first) + g) * a.max_rows + j] = sc;
         ck[p][g][grp] = valid[p] ? score_key(sc, j) : INT64_MIN;
       }
     }
@@ -439,13 +446,13 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
   __syncthreads();
   // every chunk's argmax key per head (the maximum of the chunk maxima is the
   // window's first argmax); chunks past the window are never read
-  if (threadIdx.x < P * G) {
-    const uint32_t p = threadIdx.x / G, g = threadIdx.x % G;
+  if (threadIdx.x < P * GW) {
+    const uint32_t p = threadIdx.x / GW, g = threadIdx.x % GW;
     const uint64_t c = uint64_t(blockIdx.y) * P + p;
     if (c * kAttnScoreRows < win.cnt) {
       int64_t best = ck[p][g][0];
       for (uint32_t r = 1; r < kAttnScoreRows; ++r) best = ck[p][g][r] > best ? ck[p][g][r] : best;
-      a.keys[(uint64_t(kvh) * G + g) * a.key_chunks + c] = best;
+      a.keys[(uint64_t(h_first) + g) * a.key_chunks + c] = best;
     }
   }
 }
@@ -1009,15 +1016,15 @@ static uint32_t attn_rows_mul(const AttnDecArgs& a) {
       else hipLaunchKernelGGL((KERNEL<1, kDecMaxHeadDim>), __VA_ARGS__);                     \
     }                                                                                        \
   } while (0)
-template <bool VEC>
+template <bool VEC, bool OH>
 static void launch_scores(const AttnDecArgs& a, uint32_t P, dim3 grid, hipStream_t s) {
   if (a.hd <= 256) {
-    if (P == 4) hipLaunchKernelGGL((k_dec_attn_scores<VEC, 4, 256>), grid, dim3(512), 0, s, a);
-    else if (P == 2) hipLaunchKernelGGL((k_dec_attn_scores<VEC, 2, 256>), grid, dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((k_dec_attn_scores<VEC, 1, 256>), grid, dim3(512), 0, s, a);
+    if (P == 4) hipLaunchKernelGGL((k_dec_attn_scores<VEC, 4, 256, OH>), grid, dim3(512), 0, s, a);
+    else if (P == 2) hipLaunchKernelGGL((k_dec_attn_scores<VEC, 2, 256, OH>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((k_dec_attn_scores<VEC, 1, 256, OH>), grid, dim3(512), 0, s, a);
   } else {
-    if (P == 2) hipLaunchKernelGGL((k_dec_attn_scores<VEC, 2, kDecMaxHeadDim>), grid, dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((k_dec_attn_scores<VEC, 1, kDecMaxHeadDim>), grid, dim3(512), 0, s, a);
+    if (P == 2) hipLaunchKernelGGL((k_dec_attn_scores<VEC, 2, kDecMaxHeadDim, OH>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((k_dec_attn_scores<VEC, 1, kDecMaxHeadDim, OH>), grid, dim3(512), 0, s, a);
   }
 }
 void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
@@ -1025,9 +1032,19 @@ void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
   const uint32_t ns = a.nseq ? a.nseq : 1;
   const uint32_t P = attn_rows_mul(a);
   if (part == 0) {
-    const dim3 grid(a.nkv, nblk(a.cap, P * kAttnScoreRows), ns);
-    if (a.hd % 64 == 0) launch_scores<true>(a, P, grid, s);
-    else launch_scores<false>(a, P, grid, s);
+    // one query head per workgroup while that grid fits the device in one
+    // pass (each workgroup's dot products cover one head instead of all heads
+    // of a KV head)
+    const uint64_t chunks = nblk(a.cap, P * kAttnScoreRows);
+    const bool oh = uint64_t(a.nh) * chunks * ns <= 256;
+    const dim3 grid(oh ? a.nh : a.nkv, unsigned(chunks), ns);
+    if (a.hd % 64 == 0) {
+      if (oh) launch_scores<true, true>(a, P, grid, s);
+      else launch_scores<true, false>(a, P, grid, s);
+    } else {
+      if (oh) launch_scores<false, true>(a, P, grid, s);
+      else launch_scores<false, false>(a, P, grid, s);
+    }
   } else if (part == 1) {
     const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.lds_stride * 4 : 0;
     hipLaunchKernelGGL(k_dec_attn_stats, dim3(a.nkv, 1, ns), dim3(1024), lds, s, a);
