@@ -465,6 +465,7 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
 // complement to ONE the reference adds to the argmax row's weight. With room
 // in LDS each exp term is kept there for the weight pass (2^32, the argmax
 // row's term, stored as 0xffffffff: every other term is at most 2^32 - 2^16).
+template <bool OH = false>
 __global__ __launch_bounds__(1024) void k_dec_attn_stats(AttnDecArgs a) {
   extern __shared__ int32_t sl_dyn[];
   __shared__ int64_t red[16];
@@ -472,12 +473,15 @@ __global__ __launch_bounds__(1024) void k_dec_attn_stats(AttnDecArgs a) {
   __shared__ uint64_t hrec[kDecMaxGroup];
   seq_view(a);
   const Window win = attn_window(a);
-  const uint32_t kvh = blockIdx.x, G = a.nh / a.nkv;
+  // OH: one query head per workgroup (grid x = query head); else every query
+  // head of KV head blockIdx.x: GW heads from h_first
+  const uint32_t G = a.nh / a.nkv;
+  const uint32_t GW = OH ? 1u : G, h_first = OH ? blockIdx.x : blockIdx.x * G;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t wph = 16 / G, g = wave / wph, wi = wave % wph;
-  const bool active = g < G;
+  const uint32_t wph = 16 / GW, g = wave / wph, wi = wave % wph;
+  const bool active = g < GW;
   const uint64_t stride = 64 * uint64_t(wph);
-  const uint64_t head = uint64_t(kvh) * G + (active ? g : 0);
+  const uint64_t head = uint64_t(h_first) + (active ? g : 0);
   const uint64_t nch = (win.cnt + kAttnScoreRows - 1) / kAttnScoreRows;
   int64_t best = INT64_MIN;
   if (active)
@@ -488,7 +492,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_stats(AttnDecArgs a) {
   best = wmax(best);
   if (lane == 0) red[wave] = best;
   __syncthreads();
-  if (threadIdx.x < G) {
+  if (threadIdx.x < GW) {
     int64_t k = red[threadIdx.x * wph];
     for (uint32_t w = 1; w < wph; ++w) k = red[threadIdx.x * wph + w] > k ? red[threadIdx.x * wph + w] : k;
     hkey[threadIdx.x] = k;
@@ -508,7 +512,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_stats(AttnDecArgs a) {
   __syncthreads();  // red[] from the argmax has been read
   if (lane == 0) red[wave] = s;
   __syncthreads();
-  if (threadIdx.x < G) {
+  if (threadIdx.x < GW) {
     int64_t t = 0;
     for (uint32_t w = 0; w < wph; ++w) t += red[threadIdx.x * wph + w];
     hsum[threadIdx.x] = t;
@@ -534,7 +538,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_stats(AttnDecArgs a) {
   __syncthreads();  // red[] from the exp sums has been read
   if (lane == 0) red[wave] = ws;
   __syncthreads();
-  if (threadIdx.x < G) {
+  if (threadIdx.x < GW) {
     int64_t t = 0;
     for (uint32_t w = 0; w < wph; ++w) t += red[threadIdx.x * wph + w];
     const int64_t key = hkey[threadIdx.x];
@@ -545,7 +549,7 @@ __global__ __launch_bounds__(1024) void k_dec_attn_stats(AttnDecArgs a) {
     st.rec = hrec[threadIdx.x];
     st.resid = sub_sat(kOneAct, sat32(t));
     st.pad = 0;
-    a.stats[uint64_t(kvh) * G + threadIdx.x] = st;
+    a.stats[uint64_t(h_first) + threadIdx.x] = st;
   }
 }
 
@@ -1046,8 +1050,18 @@ void launch_dec_attention_part(const AttnDecArgs& a, int part, hipStream_t s) {
       else launch_scores<false, false>(a, P, grid, s);
     }
   } else if (part == 1) {
-    const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.lds_stride * 4 : 0;
-    hipLaunchKernelGGL(k_dec_attn_stats, dim3(a.nkv, 1, ns), dim3(1024), lds, s, a);
+    if (uint64_t(a.nh) * ns <= 256) {
+      // one query head per workgroup: a quarter of the exp terms per
+      // workgroup for four heads per KV head, and one head's terms fit in LDS
+      // for windows up to 8192 rows
+      AttnDecArgs b = a;
+      b.scores_in_lds = b.lds_stride * 4 <= 32768;
+      hipLaunchKernelGGL(k_dec_attn_stats<true>, dim3(a.nh, 1, ns), dim3(1024), b.scores_in_lds ? b.lds_stride * 4 : 0,
+                         s, b);
+    } else {
+      const size_t lds = a.scores_in_lds ? size_t(a.nh / a.nkv) * a.lds_stride * 4 : 0;
+      hipLaunchKernelGGL(k_dec_attn_stats<false>, dim3(a.nkv, 1, ns), dim3(1024), lds, s, a);
+    }
   } else if (part == 2) {
     DET_ATTN_P(P, a.hd, k_dec_attn_wsum, dim3(a.nkv, nblk(a.cap, P * kAttnWsumRows), ns), dim3(1024), 0, s, a);
   } else if (uint64_t(a.nh) * nblk(a.cap, P * kAttnWsumRows) * ns <= 256) {
