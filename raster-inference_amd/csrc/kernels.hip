@@ -746,9 +746,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
   // through the rest of the norm).
   uint64_t js0[JM], jnu[JM];
   v4i b[JM][2 * D];
-  auto issue_weights = [&]() {
+  // jobs [u0, u1) of this wave
+  auto issue_weights = [&](auto u0c, auto u1c) {
+    constexpr int u0 = decltype(u0c)::value, u1 = decltype(u1c)::value;
 #pragma unroll
-    for (int u = 0; u < JM; ++u) {
+    for (int u = u0; u < u1; ++u) {
       const uint64_t jb = uint64_t(wave) + uint64_t(NW) * u;
       const uint64_t tl = jb / np, p = jb % np;
       const uint64_t tile = uint64_t(blockIdx.x) + G * tl;
@@ -778,7 +780,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
       ss = add_sat64_nn(ss, sq_term(o));
     }
   }
-  const int32_t s1 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane, issue_weights);
+  // the first job's weights go out once the norm inputs are in, the others
+  // after the first scale: the first job's loads are in flight while the scale
+  // chain and the residual run, instead of every wave waiting to issue all its
+  // loads before any of that arithmetic
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using IJ = std::integral_constant<int, JM>;
+  const int32_t s1 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane, [&] { issue_weights(I0(), I1()); });
   ss = 0;
 #pragma unroll
   for (int e = 0; e < QPT; ++e) {
@@ -792,7 +801,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
       ss = add_sat64_nn(ss, sq_term(v));
     }
   }
-  const int32_t s2 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane, [] {});
+  const int32_t s2 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane, [&] { issue_weights(I1(), IJ()); });
   // limb planes of the normalised row (quads past H are zero, to kpad / 4)
   const uint64_t kq = kpad / 4;
 #pragma unroll
