@@ -677,8 +677,11 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
 constexpr int kNormD = 5;
 constexpr uint32_t kNormMaxK = 4096;
 // rms scale of a row spread over the workgroup from each thread's saturating
-// partial sum of squares (ops.rs:406-425): wave 0 reduces the wave totals and
-// runs the scale chain once.
+// partial sum of squares (ops.rs:406-425). With at most four waves every wave
+// reduces the wave totals and runs the scale chain itself (one per SIMD, no
+// second barrier); with more, wave 0 does and broadcasts the scale through
+// LDS. red holds this call's wave totals (a separate array per call, so that
+// one call's reads never meet the next call's writes).
 // `between` runs in every wave once all waves have passed their partial sums.
 template <int NW, class F>
 __device__ __forceinline__ int32_t wg_rms_scale(int64_t ss, uint64_t n, int64_t eps, int64_t* red, int32_t* bc,
@@ -687,13 +690,19 @@ __device__ __forceinline__ int32_t wg_rms_scale(int64_t ss, uint64_t n, int64_t 
   if (lane == 0) red[wave] = ss;
   lds_barrier();
   between();
-  if (wave == 0) {
+  if constexpr (NW <= 4) {
     int64_t t = lane < NW ? red[lane] : 0;
     t = wave_sum_sat(t);
-    if (lane == 0) *bc = rms_scale_from_sumsq(t, uint32_t(n), eps);
+    return rms_scale_from_sumsq(t, uint32_t(n), eps);
+  } else {
+    if (wave == 0) {
+      int64_t t = lane < NW ? red[lane] : 0;
+      t = wave_sum_sat(t);
+      if (lane == 0) *bc = rms_scale_from_sumsq(t, uint32_t(n), eps);
+    }
+    lds_barrier();
+    return *bc;
   }
-  lds_barrier();
-  return *bc;
 }
 template <int NW, int JM, int QPT, int EPI>
 __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_t* __restrict__ q,
@@ -707,7 +716,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
   typedef long long v2l __attribute__((ext_vector_type(2)));
   __shared__ __attribute__((aligned(16))) uint8_t al[4 * kPlaneMax];
   __shared__ v4i part[NW * JM][64];
-  __shared__ int64_t red[NW];
+  __shared__ int64_t red[2][NW];
   __shared__ int32_t bc;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -787,7 +796,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using IJ = std::integral_constant<int, JM>;
-  const int32_t s1 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane, [&] { issue_weights(I0(), I1()); });
+  const int32_t s1 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red[0], &bc, wave, lane, [&] { issue_weights(I0(), I1()); });
   ss = 0;
 #pragma unroll
   for (int e = 0; e < QPT; ++e) {
@@ -801,7 +810,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
       ss = add_sat64_nn(ss, sq_term(v));
     }
   }
-  const int32_t s2 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red, &bc, wave, lane, [&] { issue_weights(I1(), IJ()); });
+  const int32_t s2 = wg_rms_scale<NW>(ss, ni.H, ni.eps, red[1], &bc, wave, lane, [&] { issue_weights(I1(), IJ()); });
   // limb planes of the normalised row (quads past H are zero, to kpad / 4)
   const uint64_t kq = kpad / 4;
 #pragma unroll
