@@ -275,8 +275,9 @@ DevMatrix upload_int8(det_ctx* ctx, uint64_t rows, uint64_t cols, const int8_t* 
   parallel_rows(rows, [&](uint64_t r0, uint64_t r1) {
     for (uint64_t r = r0; r < r1; ++r) {
       int32_t s = 0;
-      for (uint64_t c0 = 0; c0 < cols; c0 += 32) {
-        const uint64_t n = std::min<uint64_t>(32, cols - c0);
+      // (16 columns at a time: the run of one row that is contiguous in the tile-step)
+      for (uint64_t c0 = 0; c0 < cols; c0 += 16) {
+        const uint64_t n = std::min<uint64_t>(16, cols - c0);
         std::memcpy(&tiled[det::tiled_offset(m.kpad, r, c0)], q + r * cols + c0, n);
         int32_t sp = 0;
         for (uint64_t c = c0; c < c0 + n; ++c) sp += q[r * cols + c];
@@ -535,8 +536,8 @@ void untile(det_ctx* ctx, const DevMatrix& M, std::vector<int8_t>& q, std::vecto
   q.resize(M.rows * M.cols);
   parallel_rows(M.rows, [&](uint64_t r0, uint64_t r1) {
     for (uint64_t r = r0; r < r1; ++r)
-      for (uint64_t c0 = 0; c0 < M.cols; c0 += 32)
-        std::memcpy(&q[r * M.cols + c0], &tiled[det::tiled_offset(M.kpad, r, c0)], std::min<uint64_t>(32, M.cols - c0));
+      for (uint64_t c0 = 0; c0 < M.cols; c0 += 16)
+        std::memcpy(&q[r * M.cols + c0], &tiled[det::tiled_offset(M.kpad, r, c0)], std::min<uint64_t>(16, M.cols - c0));
   });
 }
 

@@ -21,6 +21,8 @@
 namespace det {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+// the second 16-byte half of a lane's weight operand, in v4i units
+constexpr int kHalfV4 = int(kTileHalfBytes / 16);
 
 // ---------------------------------------------------------------------------
 // wave / block reductions
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
   const uint64_t per = (nsteps + NW - 1) / NW;
   const uint64_t s0 = wave * per;
   const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
-  const v4i* bp = reinterpret_cast<const v4i*>(q + uint64_t(blockIdx.x) * nsteps * 2048 + lane * 32);
+  const v4i* bp = reinterpret_cast<const v4i*>(q + uint64_t(blockIdx.x) * nsteps * 2048 + lane * 16);
   const v4i* ap = reinterpret_cast<const v4i*>(limbs + (a_on ? (uint64_t(at) * 4 + aj) : 0) * kpad + 32 * g);
   const v4i zero = {0, 0, 0, 0};
   v4i acc = zero;
@@ -106,7 +108,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       b[2 * u] = __builtin_nontemporal_load(bp + (s + u) * 128);
-      b[2 * u + 1] = __builtin_nontemporal_load(bp + (s + u) * 128 + 1);
+      b[2 * u + 1] = __builtin_nontemporal_load(bp + (s + u) * 128 + kHalfV4);
       a[2 * u] = a_on ? ap[(s + u) * 8] : zero;
       a[2 * u + 1] = a_on ? ap[(s + u) * 8 + 1] : zero;
     }
@@ -115,7 +117,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
   }
   for (; s < s1; ++s) {
     const v4i b0 = __builtin_nontemporal_load(bp + s * 128);
-    const v4i b1 = __builtin_nontemporal_load(bp + s * 128 + 1);
+    const v4i b1 = __builtin_nontemporal_load(bp + s * 128 + kHalfV4);
     const v4i a0 = a_on ? ap[s * 8] : zero;
     const v4i a1 = a_on ? ap[s * 8 + 1] : zero;
     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
@@ -219,7 +221,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles;
     const bool b_on = t_on && row < n_rows;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 32);
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 16);
     v4i acc = zero;
     uint64_t s = s0;
     for (; s + 4 <= s1; s += 4) {
@@ -227,7 +229,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         b[2 * u] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128) : zero;
-        b[2 * u + 1] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128 + 1) : zero;
+        b[2 * u + 1] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128 + kHalfV4) : zero;
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -239,7 +241,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     }
     for (; s < s1; ++s) {
       const v4i b0 = t_on ? __builtin_nontemporal_load(bp + s * 128) : zero;
-      const v4i b1 = t_on ? __builtin_nontemporal_load(bp + s * 128 + 1) : zero;
+      const v4i b1 = t_on ? __builtin_nontemporal_load(bp + s * 128 + kHalfV4) : zero;
       const v4i a0 = a_on ? *reinterpret_cast<const v4i*>(abase + (s - cs0) * 128) : zero;
       const v4i a1 = a_on ? *reinterpret_cast<const v4i*>(abase + (s - cs0) * 128 + 16) : zero;
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict_
   const uint64_t per = (nsteps + NW - 1) / NW;
   const uint64_t s0 = uint64_t(wave) * per < nsteps ? uint64_t(wave) * per : nsteps;
   const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
-  const v4i* bp = reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 32);
+  const v4i* bp = reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 16);
   const bool a_on = i < 4;  // A row i = limb i of the one token
   const uint8_t* aread = al[wave] + (i & 3) * kPlane + 32 * g;
   const v4i zero = {0, 0, 0, 0};
@@ -335,7 +337,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict_
     for (int u = 0; u < D; ++u) {
       const uint64_t st = sb + u < s1 ? sb + u : s1 - 1;
       b[2 * u] = __builtin_nontemporal_load(bp + st * 128);
-      b[2 * u + 1] = __builtin_nontemporal_load(bp + st * 128 + 1);
+      b[2 * u + 1] = __builtin_nontemporal_load(bp + st * 128 + kHalfV4);
     }
     __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the conversion waits
     // limb planes of the batch: byte j of a ^ 0x00808080, 0 past k (where the
@@ -443,7 +445,7 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
     const uint64_t tile = base + slot;
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 32);
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 16);
     v4i acc[NG];
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
 #pragma unroll
       for (int u = 0; u < D; ++u) {
         b[2 * u] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128) : zero;
-        b[2 * u + 1] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128 + 1) : zero;
+        b[2 * u + 1] = t_on ? __builtin_nontemporal_load(bp + (s + u) * 128 + kHalfV4) : zero;
 #pragma unroll
         for (int tg = 0; tg < NG; ++tg) {
           a[tg][2 * u] = a_on[tg] ? ap[tg][(s + u) * 8] : zero;
@@ -467,7 +469,7 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
     }
     for (; s < s1; ++s) {
       const v4i b0 = t_on ? __builtin_nontemporal_load(bp + s * 128) : zero;
-      const v4i b1 = t_on ? __builtin_nontemporal_load(bp + s * 128 + 1) : zero;
+      const v4i b1 = t_on ? __builtin_nontemporal_load(bp + s * 128 + kHalfV4) : zero;
 #pragma unroll
       for (int tg = 0; tg < NG; ++tg) {
         const v4i a0 = a_on[tg] ? ap[tg][s * 8] : zero;
@@ -570,7 +572,7 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
     const uint64_t tile = base + slot;
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : ntiles - 1) * nsteps * 2048 + lane * 32);
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : ntiles - 1) * nsteps * 2048 + lane * 16);
     v4i acc = zero;
     for (uint64_t sb = s0; sb < s1; sb += D) {
       const uint64_t nu = s1 - sb < uint64_t(D) ? s1 - sb : uint64_t(D);
@@ -599,7 +601,7 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
       for (int u = 0; u < D; ++u) {
         const uint64_t st = sb + u < s1 ? sb + u : s1 - 1;
         b[2 * u] = __builtin_nontemporal_load(bp + st * 128);
-        b[2 * u + 1] = __builtin_nontemporal_load(bp + st * 128 + 1);
+        b[2 * u + 1] = __builtin_nontemporal_load(bp + st * 128 + kHalfV4);
       }
       // the copies have landed once every load of the batch has (the compiler does not
       // order LDS reads after global_load_lds by itself; waiting for all loads holds
@@ -766,14 +768,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
       const bool real = jb < njobs && tile < ntiles;  // wave-uniform
       js0[u] = real ? p * D : 0;
       jnu[u] = real ? (nsteps - js0[u] < uint64_t(D) ? nsteps - js0[u] : uint64_t(D)) : 1;
-      const v4i* bp = real ? reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 32)
+      const v4i* bp = real ? reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 16)
                            : reinterpret_cast<const v4i*>(q);
       const uint64_t sstride = real ? 128 : 0;
 #pragma unroll
       for (int d = 0; d < D; ++d) {
         const uint64_t st = js0[u] + (uint64_t(d) < jnu[u] ? uint64_t(d) : jnu[u] - 1);
         b[u][2 * d] = __builtin_nontemporal_load(bp + st * sstride);
-        b[u][2 * d + 1] = __builtin_nontemporal_load(bp + st * sstride + (real ? 1 : 0));
+        b[u][2 * d + 1] = __builtin_nontemporal_load(bp + st * sstride + (real ? kHalfV4 : 0));
       }
     }
   };
@@ -939,14 +941,14 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
   for (uint64_t base = uint64_t(blockIdx.x / kchunks) * 4; base < ntiles; base += groups * 4) {
     const uint64_t tile = base + wave;
     const bool t_on = tile < ntiles;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 32);
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 16);
     v4i acc[NG];
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
     v4i b0 = zero, b1 = zero, ar[CH];
     if (cs0 < cs1) {
       b0 = __builtin_nontemporal_load(bp + cs0 * 128);
-      b1 = __builtin_nontemporal_load(bp + cs0 * 128 + 1);
+      b1 = __builtin_nontemporal_load(bp + cs0 * 128 + kHalfV4);
 #pragma unroll
       for (int c = 0; c < CH; ++c) ar[c] = asrc[c][cs0 * 8];
     }
@@ -958,7 +960,7 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
       v4i n0 = zero, n1 = zero;
       if (s + 1 < cs1) {
         n0 = __builtin_nontemporal_load(bp + (s + 1) * 128);
-        n1 = __builtin_nontemporal_load(bp + (s + 1) * 128 + 1);
+        n1 = __builtin_nontemporal_load(bp + (s + 1) * 128 + kHalfV4);
 #pragma unroll
         for (int c = 0; c < CH; ++c) ar[c] = asrc[c][(s + 1) * 8];
       }
@@ -1171,7 +1173,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     const bool is_a = ts < uint32_t(TA);
     uint64_t tile = is_a ? at0 + ts : bt0 + (ts - TA);
     if (is_a ? tile >= a_tiles : tile >= ntiles) tile = (is_a ? a_tiles : ntiles) - 1;
-    src[u] = (is_a ? a : q) + (tile * ksteps + k0) * 2048 + lane * 32 + h * 16;
+    // (weight tile-steps hold each half of the lanes' operands contiguously;
+    // the activation limb tiles keep the 32-byte lane slots)
+    src[u] = (is_a ? a : q) + (tile * ksteps + k0) * 2048 + (is_a ? lane * 32 + h * 16 : h * kTileHalfBytes + lane * 16);
     limb3[u] = is_a && (ts & 3) == 3;
   }
   bool four = true;
