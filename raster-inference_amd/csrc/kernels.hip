@@ -1014,17 +1014,19 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
 //
 // The activations enter as limb rows: row 4m + j holds byte j of
 // act[m][k] ^ 0x00808080 (the four int8 limbs c_j with
-// act = sum_j c_j 256^j + 8421504), laid out exactly like the tile-major
-// weights (16-row tiles x 128-column steps of 2 KB; lane 16g + i of a step
-// holds row i, bytes [32g, 32g + 32)). A 16x16x64 MFMA of an A tile (4 tokens
-// x 4 limbs) with a weight tile leaves the four limb sums of (token g, weight
+// act = sum_j c_j 256^j + 8421504), in tiles like the tile-major weights
+// (16-row tiles x 128-column steps of 2 KB; MFMA lane 16g + i of a step takes
+// row i, columns [32g, 32g + 32)). A 16x16x64 MFMA of an A tile (4 tokens x
+// 4 limbs) with a weight tile leaves the four limb sums of (token g, weight
 // row i) in lane 16g + i, which are combined exactly as in the GEMV.
 // ---------------------------------------------------------------------------
 
 // Prefill GEMM A operand: activation rows as limb-major token groups. Token
 // group T (tokens 16 T .. 16 T + 15) has four limb tiles T 4 + j; tile-step
-// (tile, s) is 2048 bytes in the lane order of the weight tiles (lane 16 g + i:
-// token 16 T + i, columns [128 s + 32 g, +32)), so an MFMA A operand is one
+// (tile, s) is 2048 bytes of 32-byte lane slots (slot 16 g + i: token 16 T + i,
+// columns [128 s + 32 g, +32); the weights store the two 16-byte halves of a
+// lane's columns 1 KB apart instead, which only the copy addresses see), so an
+// MFMA A operand is one
 // limb of 16 tokens and the four limb products of (token, row) land in the
 // same lane of four accumulators.
 // The decomposition is chosen per token group and column part of
@@ -1098,8 +1100,10 @@ __global__ __launch_bounds__(256) void k_act_limbs_tiled(const int32_t* __restri
 // one of NBUF LDS buffers with global_load_lds_dwordx4 (no register staging):
 // the copies of the next NBUF - 1 steps are in flight while step s's MFMAs
 // run, and one barrier per step hands a buffer over. Copy h of a tile-step
-// takes bytes [16 h, 16 h + 16) of every lane's 32 (a 32-byte source stride),
-// so each 1 KB LDS half holds one MFMA operand of all 64 lanes contiguously
+// takes the 16-byte half h of every lane's 32 columns (a weight tile-step's
+// contiguous half h; bytes [16 h, 16 h + 16) of each 32-byte slot of an
+// activation tile-step), so each 1 KB LDS half holds one MFMA operand of all
+// 64 lanes contiguously
 // and the 128-bit operand reads do not conflict on LDS banks. The MFMAs of a
 // step run as two passes over the wave's tile pairs (first 64 columns, then
 // the second 64), so consecutive MFMAs never share an accumulator.
