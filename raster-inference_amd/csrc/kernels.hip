@@ -745,7 +745,8 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
 #pragma unroll
     for (int k = 0; k < 4; ++k) xv[e][k] = x4[k], wp[e][k] = p4[k], wn[e][k] = n4[k];
   }
-  const uint64_t et = uint64_t(blockIdx.x) + G * uint64_t(wave);  // first epilogue tile of this wave
+  // first epilogue tile of this lane group (lanes 16 g + i of wave w take tile 4 w + g)
+  const uint64_t et = uint64_t(blockIdx.x) + G * (4 * uint64_t(wave) + uint64_t(g));
   const uint64_t erow = (et < ntiles ? et : ntiles - 1) * 16 + i;
   const uint64_t erc = erow < n_rows ? erow : n_rows - 1;
   const int32_t ers = rowsum[erc], esc = scale[erc];
@@ -851,21 +852,24 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
     part[wave + NW * u][lane] = acc;
   }
   __syncthreads();
-  // 5. one wave per tile: lanes 0-15 (g = 0) hold the row's four limb sums of row i
-  for (uint64_t tl = uint64_t(wave); tl < tpw; tl += NW) {
+  // 5. lanes 16 g + i of wave w take row i of tile 4 w + g (four tiles per
+  // wave, so the GELU epilogue runs on every lane group): the row's four limb
+  // sums sit in lane i (g = 0) of each of the tile's part slots
+  for (uint64_t tl0 = 4 * uint64_t(wave); tl0 < tpw; tl0 += 4 * uint64_t(NW)) {
+    const uint64_t tl = tl0 + uint64_t(g);
     const uint64_t tile = uint64_t(blockIdx.x) + G * tl;
-    if (tile >= ntiles) break;
+    const bool t_ok = tl < tpw && tile < ntiles;
     int64_t p[4] = {0, 0, 0, 0};
-    for (uint64_t pp = 0; pp < np; ++pp) {
-      const v4i v = part[tl * np + pp][lane];
-      p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
-    }
+    if (t_ok)
+      for (uint64_t pp = 0; pp < np; ++pp) {
+        const v4i v = part[tl * np + pp][i];
+        p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+      }
     const uint64_t row = tile * 16 + i;
-    const bool r_on = row < n_rows;
-    const bool ok = g == 0 && r_on;
-    const bool first = tl == uint64_t(wave);
-    const int32_t rs = first ? ers : (r_on ? rowsum[row] : 0);
-    const int32_t sc = first ? esc : (r_on ? scale[row] : 0);
+    const bool ok = t_ok && row < n_rows;
+    const bool first = tl0 == 4 * uint64_t(wave);
+    const int32_t rs = first ? ers : (ok ? rowsum[row] : 0);
+    const int32_t sc = first ? esc : (ok ? scale[row] : 0);
     const int64_t a = ok ? limb_combine(p, rs, sc) : 0;
     if (EPI == 1) {
       const int32_t r = requant(a);
