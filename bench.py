@@ -529,8 +529,8 @@ def main() -> int:
                     help="only 5 lm_head GEMV launches + 5 same-size device copies (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the det path's sharding "
-              "is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py: measures one GPU only (asked for {args.gpus}); multi-GPU runs of the det path "
+              "are not measured", file=sys.stderr)
         return 2
 
     import rasterdet as rd
