@@ -36,9 +36,9 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int64_t kC4 = 8421504;  // offset of the four-limb split
-constexpr int64_t kC3 = 32896;    // offset of the three-limb split
-constexpr uint32_t kOp = 1024;    // one MFMA operand block: 64 lanes x 16 bytes
+constexpr int64_t kC4 = kAttnC4;  // offset of the four-limb split
+constexpr int64_t kC3 = 32896;     // offset of the three-limb split
+constexpr uint32_t kOp = kAttnOp;  // one MFMA operand block: 64 lanes x 16 bytes
 
 // Sortable key for "max value, first index": larger value wins, then smaller index.
 __device__ inline int64_t first_max_key(int32_t value, uint32_t index) {
@@ -59,19 +59,8 @@ __device__ inline AttnRange attn_range(const AttnMfmaArgs& a, uint64_t t) {
 
 // 16 int32 -> four 16-byte limb vectors (byte j of x ^ 0x808080) and the sum of x - C4
 __device__ inline int64_t split4(const int32_t (&x)[16], v4i (&limb)[4]) {
-  int64_t s = 0;
   uint32_t w[4][4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int d = 0; d < 4; ++d) w[j][d] = 0;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const uint32_t u = uint32_t(x[e]) ^ 0x00808080u;
-    s += int64_t(x[e]) - kC4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j][e >> 2] |= ((u >> (8 * j)) & 0xffu) << (8 * (e & 3));
-  }
+  const int64_t s = attn_split16(x, w);
 #pragma unroll
   for (int j = 0; j < 4; ++j) limb[j] = v4i{int(w[j][0]), int(w[j][1]), int(w[j][2]), int(w[j][3])};
   return s;
@@ -427,10 +416,11 @@ uint64_t attn_mfma_bytes(const AttnArgs& a) {
   return b + 4096;
 }
 
-bool launch_attention_mfma(const AttnArgs& a, void* work, uint64_t work_bytes, hipStream_t s) {
+bool attn_mfma_plan(const AttnArgs& a, AttnMfmaArgs& m) {
   const uint64_t need = attn_mfma_bytes(a);
-  if (need == 0 || !work || work_bytes < need) return false;
-  AttnMfmaArgs m{};
+  void* work = a.work;
+  if (need == 0 || !work || a.work_bytes < need) return false;
+  m = AttnMfmaArgs{};
   const uint64_t nh = a.num_heads, nkv = nh / a.groups, nsub = a.hd / 64;
   m.hd = a.hd;
   m.groups = a.groups;
@@ -458,12 +448,25 @@ bool launch_attention_mfma(const AttnArgs& a, void* work, uint64_t work_bytes, h
   m.scores = reinterpret_cast<int32_t*>(carve(nh * a.n_queries * m.srow * 4));
   m.resid = reinterpret_cast<int32_t*>(carve(nh * a.n_queries * 4));
   m.argm = reinterpret_cast<uint32_t*>(carve(nh * a.n_queries * 4));
+  return true;
+}
+
+bool launch_attention_mfma(const AttnArgs& a, void* work, uint64_t work_bytes, hipStream_t s) {
+  AttnArgs aw = a;
+  aw.work = work;
+  aw.work_bytes = work_bytes;
+  AttnMfmaArgs m;
+  if (!attn_mfma_plan(aw, m)) return false;
+  const uint64_t nh = a.num_heads, nkv = nh / a.groups, nsub = a.hd / 64;
   const unsigned th = unsigned(64 * nsub);
-  // Q rows: heads are the row segments of q; K rows: kv heads of k
-  hipLaunchKernelGGL(k_attn_split_rows, dim3(unsigned(nh), unsigned(m.nqt)), dim3(th), 0, s, a.q, a.q_ld,
-                     uint64_t(a.n_queries), a.hd, m.nqt, m.qlimbs, m.qsum);
-  hipLaunchKernelGGL(k_attn_split_rows, dim3(unsigned(nkv), unsigned(m.nkt)), dim3(th), 0, s, a.k, a.kv_ld, a.avail,
-                     a.hd, m.nkt, m.klimbs, m.ksum);
+  // Q rows: heads are the row segments of q; K rows: kv heads of k (unless
+  // the rows' producer wrote their blocks)
+  if (!(a.split_done & 1))
+    hipLaunchKernelGGL(k_attn_split_rows, dim3(unsigned(nh), unsigned(m.nqt)), dim3(th), 0, s, a.q, a.q_ld,
+                       uint64_t(a.n_queries), a.hd, m.nqt, m.qlimbs, m.qsum);
+  if (!(a.split_done & 2))
+    hipLaunchKernelGGL(k_attn_split_rows, dim3(unsigned(nkv), unsigned(m.nkt)), dim3(th), 0, s, a.k, a.kv_ld,
+                       a.avail, a.hd, m.nkt, m.klimbs, m.ksum);
   const unsigned vth = unsigned(64 * std::min<uint64_t>(a.hd / 16, 16));
   hipLaunchKernelGGL(k_attn_split_v, dim3(unsigned(nkv), unsigned(m.nks)), dim3(vth), 0, s, a.v, a.kv_ld, a.avail,
                      a.hd, m.nks, m.vlimbs, m.vblk);

@@ -1111,8 +1111,13 @@ void copy_d2d(det_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
 // With `cache`, the final K/V rows of tokens t >= cache_from are also written
 // to their canonical slots (t % cap on a ring, else t) when the head-norm
 // kernel takes the shape; returns whether it did.
+// With `plan` (the MFMA attention's work area), the head-norm kernel also
+// writes the Q operand blocks, and the K blocks with `k_blocks`; *split_done
+// receives the blocks it wrote (1: Q, 2: K) for AttnArgs::split_done.
 bool qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const uint64_t* positions = nullptr,
-               const GKv* cache = nullptr, uint64_t cache_from = 0) {
+               const GKv* cache = nullptr, uint64_t cache_from = 0, const det::AttnMfmaArgs* plan = nullptr,
+               bool k_blocks = false, uint32_t* split_done = nullptr) {
+  if (split_done) *split_done = 0;
   det_ctx* ctx = s->m->ctx;
   hipStream_t st = ctx->stream;
   const uint64_t qw = L.num_heads * L.head_dim, kw = L.num_kv_heads * L.head_dim;
@@ -1162,7 +1167,20 @@ bool qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const
     hn.kv_cap = cache->cap;
     hn.kv_ring = cache->ring ? 1 : 0;
   }
-  if (det::launch_head_norm_rope(hn, M, st)) return cache != nullptr;
+  if (plan) {
+    hn.qlimbs = plan->qlimbs;
+    hn.qsum = plan->qsum;
+    hn.nqt = plan->nqt;
+    if (k_blocks) {
+      hn.klimbs = plan->klimbs;
+      hn.ksum = plan->ksum;
+      hn.nkt = plan->nkt;
+    }
+  }
+  if (det::launch_head_norm_rope(hn, M, st)) {
+    if (split_done && plan) *split_done = k_blocks ? 3u : 1u;
+    return cache != nullptr;
+  }
   det::launch_rmsnorm(s->qb, M * L.num_heads, L.head_dim, L.head_dim, L.q_norm, L.eps, st);
   det::launch_rmsnorm(s->kb, M * L.num_kv_heads, L.head_dim, L.head_dim, L.k_norm, L.eps, st);
   det::launch_rmsnorm(s->vb, M * L.num_kv_heads, L.head_dim, L.head_dim, nullptr, L.eps, st);
@@ -1306,7 +1324,9 @@ bool layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const
     if (own->row_w != kw) bail("layer cache head count mismatch");
     if (n - retained > own->cap) bail("KV cache capacity exceeded");
   }
-  const bool cached = qkv_block(ws, L, n, 0, nullptr, donor ? nullptr : own, retained);
+  // the attention's arguments and work area first: the head-norm kernel then
+  // writes the MFMA form's Q (and, with this layer's own K rows, K) operand
+  // blocks itself
   det::AttnArgs a{};
   a.q = ws->qb; a.q_ld = L.num_heads * L.head_dim;
   a.out = ws->attn; a.out_ld = L.num_heads * L.head_dim;
@@ -1322,6 +1342,17 @@ bool layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const
     a.ring_start = d.start; a.ring_cap = d.ring ? d.cap : 0; a.avail = d.len;
     if (d.len < n) contract("attention_softmax requires a non-empty logits slice");
   } else {
+    a.k = ws->kb; a.v = ws->vb; a.kv_ld = kw; a.ring_start = 0; a.ring_cap = 0; a.avail = n;
+  }
+  if (a.avail > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
+  ctx->attach_attn_work(a);
+  det::AttnMfmaArgs plan;
+  const bool mfma = det::attn_mfma_plan(a, plan);
+  uint32_t split = 0;
+  const bool cached = qkv_block(ws, L, n, 0, nullptr, donor ? nullptr : own, retained, mfma ? &plan : nullptr,
+                                donor == nullptr, &split);
+  a.split_done = split;
+  if (!donor) {
     GKv& c = *own;
     // canonical slots: token t at t % cap (ring) or t (linear), unless the
     // head-norm kernel wrote them
@@ -1334,10 +1365,7 @@ bool layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const
     }
     kv_advance(c, n);
     c.has = true;
-    a.k = ws->kb; a.v = ws->vb; a.kv_ld = kw; a.ring_start = 0; a.ring_cap = 0; a.avail = n;
   }
-  if (a.avail > det::kMaxAttentionRows) bail("attention window longer than 16000 rows is not supported");
-  ctx->attach_attn_work(a);
   det::launch_attention(a, st);
   return post_attention(ws, L, n, ple_in, next);
 }

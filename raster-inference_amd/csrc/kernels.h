@@ -206,6 +206,9 @@ struct AttnArgs {
   // bytes; without it the vector-ALU kernel runs)
   void* work;
   uint64_t work_bytes;
+  // limb blocks already written into that work area by the producer of the
+  // rows (attn_mfma_plan's qlimbs / klimbs): 1 the Q blocks, 2 the K blocks
+  uint32_t split_done;
 };
 // Windows longer than kMaxAttentionRows are rejected by the callers.
 constexpr uint64_t kMaxAttentionRows = 16000;
@@ -217,6 +220,31 @@ void launch_attention(const AttnArgs& a, hipStream_t s);
 // queries, unaligned rows), and the launch, false when it does not apply.
 uint64_t attn_mfma_bytes(const AttnArgs& a);
 bool launch_attention_mfma(const AttnArgs& a, void* work, uint64_t work_bytes, hipStream_t s);
+struct AttnMfmaArgs;
+// The MFMA form's layout of a.work (false where the form does not apply).
+bool attn_mfma_plan(const AttnArgs& a, AttnMfmaArgs& m);
+// MFMA operand limb blocks of Q / K rows (one 1 KB block per 16-row tile,
+// 64-dim substep and limb: lane 16 g + i holds row i, dims [64 s + 16 g, +16)
+// as bytes j of x ^ 0x808080, the four-limb split x = sum_j c_j 256^j + C4).
+constexpr int64_t kAttnC4 = 8421504;
+constexpr uint32_t kAttnOp = 1024;
+// 16 consecutive values of a row -> limb j's 16 bytes as four words w[j][0..3]
+// (byte j of x ^ 0x808080, four values per word) and the sum of x - C4
+__device__ inline int64_t attn_split16(const int32_t (&x)[16], uint32_t (&w)[4][4]) {
+  int64_t s = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) w[j][d] = 0;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const uint32_t u = uint32_t(x[e]) ^ 0x00808080u;
+    s += int64_t(x[e]) - kAttnC4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j][e >> 2] |= ((u >> (8 * j)) & 0xffu) << (8 * (e & 3));
+  }
+  return s;
+}
 struct AttnMfmaArgs {
   uint32_t hd, groups;
   uint64_t n_queries, avail, window, causal_offset;
@@ -264,6 +292,14 @@ struct HeadNormRope {
   int32_t *kc = nullptr, *vc = nullptr;
   uint64_t kv_from = 0, kv_cap = 0;
   int kv_ring = 0;
+  // optional MFMA attention operands of the final rows (attn_mfma_plan):
+  // q rows to qlimbs / qsum (nqt tiles per head), k rows to klimbs / ksum
+  // (nkt tiles per KV head); rows from m up to whole tiles are written as
+  // zero blocks and zero sums
+  int8_t *qlimbs = nullptr, *klimbs = nullptr;
+  int64_t *qsum = nullptr, *ksum = nullptr;
+  uint64_t nqt = 0, nkt = 0;
+  uint64_t rows = 0;  // tokens with rows (the grid covers nqt * 16 when qlimbs is set)
 };
 bool launch_head_norm_rope(const HeadNormRope& a, uint64_t m, hipStream_t s);
 // Row i of k and v (width w) to kdst[i] / vdst[i] (device arrays of row pointers).

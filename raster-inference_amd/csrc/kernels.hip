@@ -1567,8 +1567,56 @@ template <int E>
 __global__ __launch_bounds__(256) void k_head_norm_rope(HeadNormRope a) {
   constexpr int RPW = 4;  // head rows per wave in flight
   __shared__ int32_t tcs[2][kHeadRopeMaxHalf];
-  __shared__ int32_t rowbuf[4][64 * E];
+  __shared__ __attribute__((aligned(16))) int32_t rowbuf[4][RPW][64 * E];
   const uint64_t t = blockIdx.x;
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hd = a.hd, half = a.half;
+  const uint32_t nsub = hd / 64;
+  // One 16-dim slot of the 1 KB MFMA operand blocks of head row hidx (of the q
+  // or k blocks): dims [16 sl, 16 sl + 16) go to limb j's block
+  // ((hidx * nt + t / 16) * nsub + sl / 4) * 4 + j, bytes (16 (sl % 4) + t % 16) * 16;
+  // returns the slot's sum of x - C4 (src null: a padding row, x = C4)
+  auto put_slot = [&](int8_t* limbs, uint64_t nt, uint32_t hidx, uint32_t sl, const int32_t* src) {
+    int32_t x16[16];
+    if (src) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int4 v = reinterpret_cast<const int4*>(src + 16 * sl)[q];
+        x16[4 * q] = v.x, x16[4 * q + 1] = v.y, x16[4 * q + 2] = v.z, x16[4 * q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) x16[q] = int32_t(kAttnC4);
+    }
+    uint32_t w[4][4];
+    const int64_t sm = attn_split16(x16, w);
+    int8_t* blk = limbs + ((uint64_t(hidx) * nt + t / 16) * nsub + sl / 4) * 4 * kAttnOp + (16 * (sl % 4) + t % 16) * 16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<uint4*>(blk + j * kAttnOp) = make_uint4(w[j][0], w[j][1], w[j][2], w[j][3]);
+    return sm;
+  };
+  // sum over the spr lanes of a row's slots (every lane takes part): segments
+  // of a power-of-two width share the wave, any other width takes one row per
+  // pass and the whole wave (lanes past its slots add zero)
+  const uint32_t spr = hd / 16;  // slots per row
+  const bool pow2 = (spr & (spr - 1)) == 0;
+  const uint32_t rpp = pow2 ? 64 / spr : 1;  // rows per 64-lane pass
+  auto seg_sum = [&](int64_t sm) {
+    if (!pow2) return wave_sum_wrap64(sm);
+    for (uint32_t off = 1; off < spr; off <<= 1) sm += __shfl_xor(sm, int(off), 64);
+    return sm;
+  };
+  auto put_blocks = [&](int8_t* limbs, int64_t* sums, uint64_t nt, uint32_t hidx, const int32_t* src) {
+    const int64_t sm = seg_sum(lane < spr ? put_slot(limbs, nt, hidx, lane, src) : 0);
+    if (lane == 0) sums[uint64_t(hidx) * nt * 16 + t] = sm;
+  };
+  if (t >= a.rows) {
+    // rows past the tokens up to whole tiles of the MFMA blocks
+    for (uint32_t h = wave; h < a.nh; h += 4) put_blocks(a.qlimbs, a.qsum, a.nqt, h, nullptr);
+    if (a.klimbs)
+      for (uint32_t h = wave; h < a.nkv; h += 4) put_blocks(a.klimbs, a.ksum, a.nkt, h, nullptr);
+    return;
+  }
   const uint64_t pos = a.positions ? a.positions[t] : a.pos0 + t;
   const bool rot = a.half != 0 && pos != 0;  // position 0 is the identity (ops.rs:179-181)
   if (rot)
@@ -1579,9 +1627,8 @@ __global__ __launch_bounds__(256) void k_head_norm_rope(HeadNormRope a) {
       tcs[1][i] = s;
     }
   __syncthreads();
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, hd = a.hd, half = a.half;
   const uint32_t nv = a.v ? a.nkv : 0, nrows = a.nh + a.nkv + nv;
-  int32_t* rb = rowbuf[wave];
+
   // this lane's q and k gains (every q row shares one gain vector, every k row another)
   int32_t gq[E], gk[E];
 #pragma unroll
@@ -1603,6 +1650,7 @@ __global__ __launch_bounds__(256) void k_head_norm_rope(HeadNormRope a) {
     return r < a.nh + a.nkv ? a.kc + (slot * a.nkv + (r - a.nh)) * hd : a.vc + (slot * a.nkv + (r - a.nh - a.nkv)) * hd;
   };
   for (uint32_t r0 = wave; r0 < nrows; r0 += 4 * RPW) {
+    uint32_t blk_mask = 0;  // rows of this group whose blocks are written after the group
     int32_t x[RPW][E];
 #pragma unroll
     for (int u = 0; u < RPW; ++u) {
@@ -1620,9 +1668,13 @@ __global__ __launch_bounds__(256) void k_head_norm_rope(HeadNormRope a) {
       if (r >= nrows) break;  // (wave-uniform)
       int32_t* row = row_of(r);
       int32_t* crow = cache_of(r);
+      int32_t* rb = rowbuf[wave][u];
       const bool is_q = r < a.nh, is_k = !is_q && r < a.nh + a.nkv;
       const bool gained = is_q ? a.q_gain != nullptr : (is_k && a.k_gain != nullptr);
       const bool rotate = rot && (is_q || is_k);
+      // the final row also goes to the MFMA attention's operand blocks (through this wave's LDS row)
+      const bool blocks = (is_q && a.qlimbs) || (is_k && a.klimbs);
+      if (blocks) blk_mask |= 1u << u;
       int64_t ss = 0;
 #pragma unroll
       for (int k = 0; k < E; ++k) ss = add_sat64_nn(ss, sq_term(x[u][k]));
@@ -1634,9 +1686,8 @@ __global__ __launch_bounds__(256) void k_head_norm_rope(HeadNormRope a) {
         if (c < hd) {
           const int32_t y = mul_sat(x[u][k], sc);
           const int32_t z = gained ? mul_sat(y, is_q ? gq[k] : gk[k]) : y;
-          if (rotate) {
-            rb[c] = z;
-          } else {
+          if (rotate || blocks) rb[c] = z;
+          if (!rotate) {
             row[c] = z;
             if (crow) crow[c] = z;
           }
@@ -1652,14 +1703,33 @@ __global__ __launch_bounds__(256) void k_head_norm_rope(HeadNormRope a) {
           row[i] = y0;
           row[i + half] = y1;
           if (crow) crow[i] = y0, crow[i + half] = y1;
+          if (blocks) rb[i] = y0, rb[i + half] = y1;  // (this lane's own pair: read above)
         }
         for (uint32_t c = 2 * half + lane; c < hd; c += 64) {
           row[c] = rb[c];
           if (crow) crow[c] = rb[c];
         }
-        wave_lds_sync();  // every lane's reads of this row precede the next row's writes
       }
     }
+    // the group's operand blocks, rpp rows per pass of the wave's 64 lanes
+    if (blk_mask) {
+      wave_lds_sync();  // the final rows are in the wave's LDS rows
+      for (uint32_t p0 = 0; p0 < RPW; p0 += rpp) {
+        const uint32_t u = p0 + lane / spr, sl = lane % spr;
+        const uint32_t r = r0 + 4 * u;
+        const bool on = lane < rpp * spr && u < RPW && ((blk_mask >> u) & 1u);
+        const bool is_q = r < a.nh;
+        int64_t sm = 0;
+        if (on) sm = is_q ? put_slot(a.qlimbs, a.nqt, r, sl, rowbuf[wave][u])
+                          : put_slot(a.klimbs, a.nkt, r - a.nh, sl, rowbuf[wave][u]);
+        sm = seg_sum(sm);
+        if (on && sl == 0) {
+          if (is_q) a.qsum[uint64_t(r) * a.nqt * 16 + t] = sm;
+          else a.ksum[uint64_t(r - a.nh) * a.nkt * 16 + t] = sm;
+        }
+      }
+    }
+    wave_lds_sync();  // every read of the group's LDS rows precedes the next group's writes
   }
 }
 
@@ -2501,11 +2571,16 @@ void launch_rope_rows(int32_t* x, uint64_t rows, uint64_t ld, uint64_t heads, ui
                      0, 0, positions);
 }
 
-bool launch_head_norm_rope(const HeadNormRope& a, uint64_t m, hipStream_t s) {
-  if (a.hd == 0 || a.hd > 512 || a.half > kHeadRopeMaxHalf || 2 * uint64_t(a.half) > a.hd) return false;
+bool launch_head_norm_rope(const HeadNormRope& a0, uint64_t m, hipStream_t s) {
+  if (a0.hd == 0 || a0.hd > 512 || a0.half > kHeadRopeMaxHalf || 2 * uint64_t(a0.half) > a0.hd) return false;
+  if ((a0.qlimbs || a0.klimbs) && (a0.hd % 64 != 0 || !a0.qlimbs || a0.nqt * 16 < m || (a0.klimbs && a0.nkt != a0.nqt)))
+    return false;
   if (m == 0) return true;
-  if (a.hd <= 256) hipLaunchKernelGGL(k_head_norm_rope<4>, dim3(unsigned(m)), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(k_head_norm_rope<8>, dim3(unsigned(m)), dim3(256), 0, s, a);
+  HeadNormRope a = a0;
+  a.rows = m;
+  const uint64_t grid = a.qlimbs ? a.nqt * 16 : m;  // (padding rows of the last tile write zero blocks)
+  if (a.hd <= 256) hipLaunchKernelGGL(k_head_norm_rope<4>, dim3(unsigned(grid)), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(k_head_norm_rope<8>, dim3(unsigned(grid)), dim3(256), 0, s, a);
   return true;
 }
 
