@@ -969,11 +969,13 @@ __global__ void k_dec_softcap(int32_t* __restrict__ x, uint64_t n, int32_t cap) 
 static inline unsigned nblk(uint64_t n, unsigned per) { return unsigned((n + per - 1) / per); }
 
 // Row kernels run 1024 threads with the fewest elements per thread that
-// cover the row (2, 4, 8 or 15; up to kDecMaxHidden).
+// cover the row (2, 3, 4, 8 or 15; up to kDecMaxHidden).
 #define DET_ROW_DISPATCH(KERNEL, ...)                                                     \
   do {                                                                                    \
     if (H <= 2048)                                                                        \
       hipLaunchKernelGGL((KERNEL<1024, 2>), dim3(1, nseq), dim3(1024), 0, s, __VA_ARGS__); \
+    else if (H <= 3072)                                                                   \
+      hipLaunchKernelGGL((KERNEL<1024, 3>), dim3(1, nseq), dim3(1024), 0, s, __VA_ARGS__); \
     else if (H <= 4096)                                                                   \
       hipLaunchKernelGGL((KERNEL<1024, 4>), dim3(1, nseq), dim3(1024), 0, s, __VA_ARGS__); \
     else if (H <= 8192)                                                                   \
