@@ -2093,8 +2093,7 @@ void enqueue_fused_step(det_session* s) {
       // x += norm(proj(gelu(gate(x)) * ple_in)), then the layer scalar and the next norm
       det::launch_dec_residual_norm(s->ff_acc, xc, s->normed, L.post_ff_ln, false, 0, w_next, H, L.eps, s->limbs_x,
                                     s->kpad_x, st);
-      det::launch_gemv_decode(*L.ple_gate, xc, false, 0, s->ple_g, st);
-      det::launch_gelu_mul(s->ple_g, s->ple_in_all + l * P, P, st);
+      det::launch_gemv_decode(*L.ple_gate, xc, false, 2, s->ple_g, st, s->ple_in_all + l * P);
       det::launch_gemv_decode_acc(*L.ple_proj, s->ple_g, false, s->ple_acc, st);
       det::launch_dec_residual_norm(s->ple_acc, x_dst, s->normed, L.ple_post_norm, L.layer_scalar.has_value(),
                                     L.layer_scalar.value_or(0), w_next, H, L.eps, s->limbs_x, s->kpad_x, st, 1,

@@ -105,10 +105,11 @@ void launch_gemm_tiled_gelu(const DevMatrix& W, uint64_t m, int32_t* out, uint64
 
 // Batch-1 int8 GEMV for the fused decode step (int8 storage, fits LDS):
 // act_i64 requantizes wrapped accumulators on load; epilogue 1 applies
-// mul_sat(gelu(gate), up) to an interleaved gate/up matrix (out has rows/2).
+// mul_sat(gelu(gate), up) to an interleaved gate/up matrix (out has rows/2);
+// epilogue 2 writes mul_sat(gelu(row), mul[row]) (int32 activations only).
 bool gemv_fits_lds(const DevMatrix& W, uint64_t m);
 void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int epilogue, int32_t* out,
-                        hipStream_t s);
+                        hipStream_t s, const int32_t* mul = nullptr);
 // Decode GEMV (one activation row) into wrapping Q32.32 accumulators that must
 // be zero on entry; K is split across workgroups with exact atomic adds.
 void launch_gemv_decode_acc(const DevMatrix& W, const void* act, bool act_i64, int64_t* acc, hipStream_t s);

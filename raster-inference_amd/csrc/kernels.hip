@@ -157,7 +157,9 @@ __device__ __forceinline__ int64_t limb_combine(const int64_t p[4], int32_t rows
 // load (the attention weighted sums feeding the O projection).
 // EPI 0: requantize (or raw accumulators to acc_out). EPI 1: rows are
 // interleaved gate/up pairs per tile (rows 0-7 gate f..f+7, rows 8-15 up
-// f..f+7); out[f] = mul_sat(gelu(gate_f), up_f).
+// f..f+7); out[f] = mul_sat(gelu(gate_f), up_f). EPI 2: out[row] =
+// mul_sat(gelu(requant(acc)), mulv[row]) (a gate projection times a given
+// row, as k_gelu_mul after the GEMV; single-chunk launches only).
 // kchunks > 1 splits K across workgroups as well (block b takes K chunk
 // b % kchunks): each adds its wrapping share of the Q32.32 accumulator to
 // acc_out atomically (the sum over chunks is the accumulator exactly, since
@@ -166,7 +168,8 @@ template <int KSPLIT, bool IN64, int EPI>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const void* __restrict__ act_v, uint64_t ld_act, uint64_t k, uint64_t n_rows, uint64_t kpad, uint32_t m,
-    int32_t* __restrict__ out, uint64_t ld_out, int64_t* __restrict__ acc_out, uint32_t kchunks) {
+    int32_t* __restrict__ out, uint64_t ld_out, int64_t* __restrict__ acc_out, uint32_t kchunks,
+    const int32_t* __restrict__ mulv) {
   extern __shared__ __attribute__((aligned(16))) int8_t lds_limbs[];
   __shared__ v4i part[KSPLIT > 1 ? 8 : 1][64];
   constexpr int TPW = 8 / KSPLIT;
@@ -275,6 +278,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
         const int32_t r = requant(a);
         const int32_t up = __shfl(r, (lane & 48) | ((i + 8) & 15), 64);
         if (ok && i < 8) out[uint64_t(g) * ld_out + tile * 8 + i] = mul_sat(gelu_act(r), up);
+      } else if (EPI == 2) {
+        if (ok) out[uint64_t(g) * ld_out + row] = mul_sat(gelu_act(requant(a)), mulv[uint64_t(g) * ld_out + row]);
       } else if (ok) {
         if (acc_out) acc_out[uint64_t(g) * ld_out + row] = a;
         else out[uint64_t(g) * ld_out + row] = requant(a);
@@ -2127,7 +2132,8 @@ static int pick_ksplit(uint64_t ntiles, uint64_t nsteps) {
 
 template <bool IN64, int EPI>
 static void launch_lds_gemv(const DevMatrix& W, const void* act, uint64_t ld_act, uint32_t mm, int32_t* o,
-                            uint64_t ld_out, int64_t* ao, hipStream_t s, int ks = 0, uint32_t kchunks = 1) {
+                            uint64_t ld_out, int64_t* ao, hipStream_t s, int ks = 0, uint32_t kchunks = 1,
+                            const int32_t* mulv = nullptr) {
   const uint64_t ntiles = (W.rows + 15) / 16;
   const uint64_t nsteps = W.kpad / 128;
   const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
@@ -2138,7 +2144,7 @@ static void launch_lds_gemv(const DevMatrix& W, const void* act, uint64_t ld_act
   const uint64_t grid = groups * kchunks;
 #define DET_GEMV_LAUNCH(KS)                                                                                     \
   hipLaunchKernelGGL((k_gemv_i8_lds<KS, IN64, EPI>), dim3(unsigned(grid)), dim3(kGemvThreads), size_t(lds), s, W.q, \
-                     W.scale, W.rowsum, act, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao, kchunks)
+                     W.scale, W.rowsum, act, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao, kchunks, mulv)
   switch (ks) {
     case 8: DET_GEMV_LAUNCH(8); break;
     case 4: DET_GEMV_LAUNCH(4); break;
@@ -2174,8 +2180,9 @@ static void launch_gemv_tile(const DevMatrix& W, const void* act, bool in64, int
 }
 
 void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int epilogue, int32_t* out,
-                        hipStream_t s) {
+                        hipStream_t s, const int32_t* mul) {
   if (act_i64) launch_lds_gemv<true, 0>(W, act, W.cols, 1, out, W.rows, nullptr, s);
+  else if (epilogue == 2) launch_lds_gemv<false, 2>(W, act, W.cols, 1, out, W.rows, nullptr, s, 0, 1, mul);
   else if (epilogue == 1) launch_lds_gemv<false, 1>(W, act, W.cols, 1, out, W.rows / 2, nullptr, s);
   else launch_lds_gemv<false, 0>(W, act, W.cols, 1, out, W.rows, nullptr, s);
 }
