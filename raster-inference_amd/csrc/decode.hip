@@ -100,6 +100,7 @@ __global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* 
 // layer); normed = rmsnorm(x, w_next) (det_kernels.rs:1058-1075, 1108-1133).
 // src holds the projection's wrapping accumulators and is cleared after use.
 // x_src may equal x (each thread reads its elements before writing them).
+// Without w_next only x is written (the next norm is left to a later kernel).
 template <int NT, int EPT>
 __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ src, const int32_t* x_src,
                                                            int32_t* x, int32_t* __restrict__ normed,
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
     if (in) src[c] = 0;
     xv[e] = in ? x_src[c] : 0;
     wp[e] = in ? w_post[c] : 0;
-    wn[e] = in ? w_next[c] : 0;
+    wn[e] = in && w_next ? w_next[c] : 0;
   }
 #pragma unroll
   for (int e = 0; e < EPT; ++e) ss = add_sat64_nn(ss, sq_term(o[e]));
@@ -142,6 +143,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
     if (x_out && c < H) x_out[c] = v;
     ss = add_sat64_nn(ss, sq_term(c < H ? v : 0));
   }
+  if (!w_next) return;  // uniform over the workgroup
   const int32_t s2 = blk_rms_scale<NT>(ss, H, eps, red, &bc);
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {

@@ -2091,7 +2091,8 @@ void enqueue_fused_step(det_session* s) {
     if (m->has_ple && L.has_ple) {
       // x += norm(down); then the per-layer input block (det_kernels.rs:1108-1128):
       // x += norm(proj(gelu(gate(x)) * ple_in)), then the layer scalar and the next norm
-      det::launch_dec_residual_norm(s->ff_acc, xc, s->normed, L.post_ff_ln, false, 0, w_next, H, L.eps, s->limbs_x,
+      // (the first residual norm writes x only: the second writes the next norm)
+      det::launch_dec_residual_norm(s->ff_acc, xc, s->normed, L.post_ff_ln, false, 0, nullptr, H, L.eps, s->limbs_x,
                                     s->kpad_x, st);
       det::launch_gemv_decode(*L.ple_gate, xc, false, 2, s->ple_g, st, s->ple_in_all + l * P);
       det::launch_gemv_decode_acc(*L.ple_proj, s->ple_g, false, s->ple_acc, st);
