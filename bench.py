@@ -49,6 +49,9 @@ def log(msg: str) -> None:
 
 
 def cpu_baseline(problems, seconds: float, threads: int) -> dict:
+    """The oracle's det_linear_into_par schedule over the four GEMV shapes
+    (one step), timed step by step on `threads` host threads for `seconds`
+    (at least 20 steps) and for 20 steps on one thread: medians."""
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib  # the oracle is the checker / CPU baseline only
 
@@ -56,25 +59,24 @@ def cpu_baseline(problems, seconds: float, threads: int) -> dict:
     step_bytes = sum(alg_bytes(*w.shape) for w, _ in expanded)
 
     def one_step(nthreads):
+        t = time.perf_counter()
         for w, a in expanded:
             oracle_lib.det_linear(w, a, threads=nthreads)
+        return time.perf_counter() - t
 
     one_step(threads)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        one_step(threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and reps >= 2:
-            break
-    t1 = time.perf_counter()
-    one_step(1)
-    single = time.perf_counter() - t1
+    times, t0 = [], time.perf_counter()
+    while len(times) < 20 or time.perf_counter() - t0 < seconds:
+        times.append(one_step(threads))
+    single = [one_step(1) for _ in range(20)]
+    med, med1 = float(np.median(times)), float(np.median(single))
     return {
-        "value": round(step_bytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": f"{reps} full steps (4 decode-shape GEMVs, i16-expanded weights) in {el:.1f}s; "
-                  f"1-thread step {single * 1e3:.1f} ms ({step_bytes / single / 1e9:.2f} GB/s)",
-        "ms_per_step": round(el / reps * 1e3, 3),
+        "value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"median of {len(times)} full steps (4 decode-shape GEMVs, i16-expanded weights, "
+                  f"{step_bytes} algorithmic bytes each) on {threads} threads; one thread: median of 20 steps, "
+                  f"{med1 * 1e3:.1f} ms ({step_bytes / med1 / 1e9:.2f} GB/s)",
+        "ms_per_step": round(med * 1e3, 3),
+        "one_thread_gbs": round(step_bytes / med1 / 1e9, 3),
     }
 
 
@@ -102,9 +104,12 @@ def e4b_cpu_baseline(rd, args, gpu_model) -> dict:
     """The oracle (the reference's det path restated, reference schedule:
     row-parallel GEMV for one token, token-parallel slab GEMV, item-parallel
     attention; i16-expanded weights as the reference streams them) on the same
-    E4B-shaped weights: a bounded sample of prefill and greedy decode on all
-    host threads and on one thread. The GPU decodes the same prompt so the
-    sample is also a parity check of the tokens."""
+    E4B-shaped weights at the configuration's own context: the 512-token
+    prompt prefilled, then greedy decode steps at context 512.., on all host
+    threads, `cpu_e4b_runs` times (medians). One thread: decode steps from a
+    copy of the prefilled session (same context) and a short prefill. The GPU
+    decodes the same prompt, so the sample is also a parity check of the
+    tokens."""
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib  # the oracle is the checker / CPU baseline only
     from rasterdet import synthetic
@@ -117,50 +122,65 @@ def e4b_cpu_baseline(rd, args, gpu_model) -> dict:
         om.set_tensor(name, v, 32 if sc is None else 8, sc)
     om.finalize()
     load_s = time.perf_counter() - t0
-    rng = np.random.default_rng(args.seed + 11)
-    prompt = rng.integers(0, 262144, size=args.cpu_prompt).tolist()
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, 262144, size=args.prompt_len).tolist()  # the GPU decode's prompt
+    runs, steps = args.cpu_e4b_runs, args.cpu_steps
     out = {"cpu": cpu_description(), "threads": threads, "load_s": round(load_s, 1),
-           "sample": f"{args.cpu_prompt}-token prompt, then {args.cpu_steps} greedy steps (context "
-                     f"{args.cpu_prompt}..{args.cpu_prompt + args.cpu_steps}) on {threads} threads; one thread: "
-                     f"a {args.cpu_prompt_1t}-token prefill and {args.cpu_steps_1t} steps"}
+           "sample": f"{runs} runs of a {len(prompt)}-token prefill then {steps} greedy steps (context "
+                     f"{len(prompt)}..{len(prompt) + steps}) on {threads} threads, medians over the runs (prefill) "
+                     f"and over every step (decode); one thread: {args.cpu_steps_1t} steps from a copy of the "
+                     f"prefilled session (same context), median, and a {args.cpu_prompt_1t}-token prefill"}
     oracle_lib.set_threads(threads)
-    t0 = time.perf_counter()
-    sess = om.session(prompt)
-    pre_s = time.perf_counter() - t0
-    toks, tok = [], sess.next_token()
-    t0 = time.perf_counter()
-    for _ in range(args.cpu_steps):
-        toks.append(tok)
-        sess.decode(tok)
-        tok = sess.next_token()
-    dec_s = time.perf_counter() - t0
-    out["prefill_tok_s"] = round(len(prompt) / pre_s, 2)
-    out["decode_tok_s"] = round(args.cpu_steps / dec_s, 3)
-    out["decode_ms_per_token"] = round(dec_s / args.cpu_steps * 1e3, 1)
+    pre_times, step_times, toks, first = [], [], [], None
+    for r in range(runs):
+        t0 = time.perf_counter()
+        sess = om.session(prompt)
+        pre_times.append(time.perf_counter() - t0)
+        if first is None:
+            first = sess.clone()
+        tok, run_toks = sess.next_token(), []
+        for _ in range(steps):
+            run_toks.append(tok)
+            t0 = time.perf_counter()
+            sess.decode(tok)
+            step_times.append(time.perf_counter() - t0)
+            tok = sess.next_token()
+        toks.append(run_toks)
+        log(f"[bench] CPU E4B run {r}: prefill {pre_times[-1]:.1f} s, {steps} steps "
+            f"{sum(step_times[-steps:]):.2f} s")
+        del sess
+    pre_med, step_med = float(np.median(pre_times)), float(np.median(step_times))
+    out["prefill_tok_s"] = round(len(prompt) / pre_med, 2)
+    out["prefill_s_runs"] = [round(t, 2) for t in pre_times]
+    out["decode_tok_s"] = round(1.0 / step_med, 3)
+    out["decode_ms_per_token"] = round(step_med * 1e3, 1)
+    out["runs_tokens_identical"] = all(t == toks[0] for t in toks)
     # the GPU's greedy tokens for the same prompt
-    gs = gpu_model.session(len(prompt) + args.cpu_steps + 1)
+    gs = gpu_model.session(len(prompt) + steps + 1)
     g = gs.prefill(prompt, rd.DET_COMMIT_NONE).next_token
     gpu_toks = []
-    for _ in range(args.cpu_steps):
+    for _ in range(steps):
         gpu_toks.append(g)
         g = gs.decode(g, rd.DET_COMMIT_NONE).next_token
-    out["gpu_tokens_identical"] = gpu_toks == toks
+    out["gpu_tokens_identical"] = gpu_toks == toks[0]
     oracle_lib.set_threads(1)
+    tok1, t1 = first.next_token(), []
+    for _ in range(args.cpu_steps_1t):
+        t0 = time.perf_counter()
+        first.decode(tok1)
+        t1.append(time.perf_counter() - t0)
+        tok1 = first.next_token()
     t0 = time.perf_counter()
     s1 = om.session(prompt[:args.cpu_prompt_1t])
     pre1 = time.perf_counter() - t0
-    tok1 = s1.next_token()
-    t0 = time.perf_counter()
-    for _ in range(args.cpu_steps_1t):
-        s1.decode(tok1)
-        tok1 = s1.next_token()
-    dec1 = time.perf_counter() - t0
     oracle_lib.set_threads(threads)
-    out["one_thread"] = {"prefill_tok_s": round(args.cpu_prompt_1t / pre1, 3),
-                         "decode_tok_s": round(args.cpu_steps_1t / dec1, 3)}
+    out["one_thread"] = {"decode_tok_s": round(1.0 / float(np.median(t1)), 3),
+                         "decode_context": len(prompt),
+                         "prefill_tok_s": round(args.cpu_prompt_1t / pre1, 3),
+                         "prefill_tokens": args.cpu_prompt_1t}
     log(f"[bench] CPU E4B: prefill {out['prefill_tok_s']} tok/s, decode {out['decode_tok_s']} tok/s on {threads} "
         f"threads; one thread {out['one_thread']}")
-    del s1, sess, om
+    del s1, first, om
     return out
 
 
@@ -252,7 +272,7 @@ def e4b_decode(ctx, rd, args, model, load_s) -> dict:
     # the first prefill on the model also grows its scratch areas (attention
     # work area, limb buffers) and loads the kernels: timed apart; the
     # reported rate is the second prefill's (the commitment session's prompt)
-    sess2 = model.session(args.prompt_len + 17)
+    sess2 = model.session(args.prompt_len + steps + 1)
     ctx.synchronize()
     t0 = time.perf_counter()
     pr2 = sess2.prefill(prompt, rd.DET_COMMIT_NONE)
@@ -275,9 +295,10 @@ def e4b_decode(ctx, rd, args, model, load_s) -> dict:
         tokens.append(tok)
     ctx.synchronize()
     dec_s = time.perf_counter() - t0
-    # same decode with activation/logit commitments hashed on the host each step
+    # the same decode again with activation/logit commitments hashed on the
+    # host every step: every token must repeat
     tok2 = pr2.next_token
-    n_commit = 16
+    n_commit = steps
     t0 = time.perf_counter()
     same = True
     for i in range(n_commit):
@@ -316,9 +337,10 @@ def ragged_batch(ctx, rd, args, model) -> dict:
     toks = [s.prefill(p, rd.DET_COMMIT_NONE).next_token for s, p in zip(sess, prompts)]
     ctx.synchronize()
     prefill_s = time.perf_counter() - t0
-    # every sequence decoded in the batch and alone for 16 steps, on copies:
-    # activation and logits commitments every step, KV commitments at the last
-    n_check = min(steps, 16)
+    # every sequence decoded in the batch and alone for all the steps, on
+    # copies: activation and logits commitments every step, KV commitments
+    # every 32nd step and at the last
+    n_check = steps
     same = None
     if not getattr(args, "no_solo_check", False):
         same = True
@@ -326,7 +348,7 @@ def ragged_batch(ctx, rd, args, model) -> dict:
         solo = [s.clone() for s in sess]
         tb, ts = toks[:], toks[:]
         for j in range(n_check):
-            flags = rd.DET_COMMIT_ALL if j == n_check - 1 else rd.DET_COMMIT_ACTIVATIONS
+            flags = rd.DET_COMMIT_ALL if (j % 32 == 0 or j == n_check - 1) else rd.DET_COMMIT_ACTIVATIONS
             res = rd.decode_batch(bcopy, tb, flags)
             for i, r in enumerate(res):
                 e = solo[i].decode(ts[i], flags)
@@ -352,7 +374,8 @@ def ragged_batch(ctx, rd, args, model) -> dict:
         "prefill_s": round(prefill_s, 3),
         "solo_commitments_identical": bool(same) if same is not None else None,
         "solo_check": (f"all {n} sequences decoded in the batch and alone for {n_check} steps: activation and "
-                       f"logits commitments every step, KV commitments at the last" if same is not None else "skipped"),
+                       f"logits commitments every step, KV commitments every 32nd step and at the last"
+                       if same is not None else "skipped"),
     }
 
 
@@ -409,9 +432,22 @@ def prefill_gemm(ctx, rd, args) -> dict:
         c1.record()
         ms_calls = c0.elapsed_ms(c1) / reps
         tops = 2 * m * weights / (ms / 1e3) / 1e12
+        # int8 MFMA ops the GEMMs issue: 3 activation limbs per (16-token
+        # group, 512-column part) whose values lie in [-2^23, 2^23), else 4
+        # (a block with any four-limb part runs four throughout: counted as
+        # four for the whole projection); rows past 32768 columns take four
+        host_acts = {k: v.numpy().reshape(m, k) for k, v in acts.items()}
+        limbs = []
+        for n, k in PREFILL_SHAPES:
+            a = host_acts[k]
+            wide = k > 32768 or bool(((a < -(1 << 23)) | (a >= (1 << 23))).any())
+            limbs.append(4 if wide else 3)
+        hw_tops = sum(2 * m * n * k * l for (n, k), l in zip(PREFILL_SHAPES, limbs)) / (ms / 1e3) / 1e12
         out[f"M{m}"] = {"ms_per_layer_set": round(ms, 4), "alg_tops": round(tops, 1),
                         "frac_of_int8_peak": round(tops / MFMA_INT8_PEAK_TOPS, 4),
-                        "hw_frac_with_4_limbs": round(4 * tops / MFMA_INT8_PEAK_TOPS, 4),
+                        "limbs_per_projection": limbs,
+                        "hw_tops": round(hw_tops, 1),
+                        "hw_frac_of_int8_peak": round(hw_tops / MFMA_INT8_PEAK_TOPS, 4),
                         "ms_per_layer_set_calls": round(ms_calls, 4)}
         log(f"[bench] prefill GEMM M={m}: {ms:.3f} ms per layer-set (graph replay), {ms_calls:.3f} ms through "
             f"per-call launches, {tops:.1f} algorithmic TOPS")
@@ -514,10 +550,10 @@ def main() -> int:
     ap.add_argument("--no-e4b-cpu", action="store_true", help="skip the oracle's E4B decode/prefill CPU baseline")
     ap.add_argument("--no-checkpointed", action="store_true", help="skip the checkpointed (traced) decode")
     ap.add_argument("--no-ple", action="store_true", help="skip the E4B-shaped decode with per-layer inputs")
-    ap.add_argument("--cpu-prompt", type=int, default=32)
-    ap.add_argument("--cpu-steps", type=int, default=16)
-    ap.add_argument("--cpu-prompt-1t", type=int, default=4)
-    ap.add_argument("--cpu-steps-1t", type=int, default=2)
+    ap.add_argument("--cpu-e4b-runs", type=int, default=3, help="oracle E4B prefill+decode runs (medians)")
+    ap.add_argument("--cpu-steps", type=int, default=4, help="oracle E4B decode steps per run")
+    ap.add_argument("--cpu-prompt-1t", type=int, default=16, help="tokens of the one-thread oracle prefill")
+    ap.add_argument("--cpu-steps-1t", type=int, default=3, help="one-thread oracle decode steps at the prompt's context")
     ap.add_argument("--prompt-len", type=int, default=512)
     ap.add_argument("--decode-profile", action="store_true",
                     help="only the E4B-shaped model: prefill, then 32 greedy decode steps (for rocprofv3 runs)")
@@ -657,6 +693,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
+            "traffic_source": "profiles/gemv_lm_head_traffic.md: rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE of this "
+                              "kernel at this shape, scaled by a same-size copy; committed, not measured in this run",
             "avg_launch_us": round(lm_avg * 1e3, 2),
             "alg_bytes_per_launch": lm_bytes,
         },

@@ -209,6 +209,10 @@ int det_model_finalize(det_model_t* model);
  * counterpart in the reference (its executor has one CPU path); for callers
  * and tests that need to know which GPU schedule a model takes. */
 int det_model_fused_decode(const det_model_t* model);
+/* Sessions, KV caches and scratches may be freed before or after their model
+ * (they keep their own device memory and the context's stream); the context
+ * must outlive all of them, and a model must not be freed while a call on one
+ * of its sessions, caches or scratches is running. */
 void det_model_free(det_model_t* model);
 
 /* ------------------------------------------------------------------------ */
@@ -229,7 +233,11 @@ void det_scratch_free(det_scratch_t* scratch);
 
 /* LayerKvCache of one layer (shared/model/transformer.rs:278-337) with room
  * for max_tokens appended tokens; a sliding-window layer that owns its cache
- * keeps its last `window` rows. Starts without det data (None). */
+ * keeps its last `window` rows. Starts without det data (None). A prefill of
+ * more than max_tokens rows, or an append past max_tokens tokens, fails with
+ * "KV cache capacity exceeded" (status 1), except on a sliding-window cache
+ * created with max_tokens >= window, which keeps taking tokens as the
+ * reference's trimmed cache does. */
 int det_kv_create(det_model_t* model, uint64_t layer, uint64_t max_tokens, det_kv_t** out);
 /* LayerKvCache::clone (e.g. to keep the pre-step caches a decode.layer_range
  * commitment needs). */

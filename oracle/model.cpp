@@ -28,6 +28,11 @@ namespace oracle {
 
 static thread_local std::string g_last_error;
 static int g_threads = 1;
+// Token rows per slab work item: 1 is the reference's schedule (one serial
+// GEMV per token row). Tests may take several token rows per item, each
+// weight row then read once for the group while it is in cache; every output
+// element still adds its terms in column order, so the results are the same.
+static int g_slab_group = 1;
 
 struct InvalidArgument : std::runtime_error {
   using std::runtime_error::runtime_error;
@@ -87,8 +92,30 @@ static void det_linear(const Matrix& W, const int32_t* act, size_t act_len, int3
 // serial GEMV (det_linear_into); with a thread pool the token rows are spread
 // over the threads (par_chunks_mut over output rows), never the matrix rows.
 template <class T>
+static void slab_group(const T* w, size_t rows, size_t cols, size_t t0, size_t t1, const int32_t* act,
+                       int32_t* out) {
+  for (size_t r = 0; r < rows; ++r) {
+    const T* row = w + r * cols;
+    for (size_t t = t0; t < t1; ++t) {
+      const int32_t* a = act + t * cols;
+      int64_t acc = 0;
+      for (size_t c = 0; c < cols; ++c) acc = mac_bits(acc, a[c], int32_t(row[c]));
+      out[t * rows + r] = requantize(acc);
+    }
+  }
+}
+
+template <class T>
 static void slab_rows(const T* w, size_t rows, size_t cols, size_t m, const int32_t* act, int32_t* out,
                       int threads) {
+  if (g_slab_group > 1 && m > 1) {
+    const size_t G = size_t(g_slab_group);
+    const long groups = long((m + G - 1) / G);
+#pragma omp parallel for num_threads(threads > 1 ? threads : 1) schedule(dynamic, 1)
+    for (long g = 0; g < groups; ++g)
+      slab_group(w, rows, cols, size_t(g) * G, std::min(m, size_t(g + 1) * G), act, out);
+    return;
+  }
   if (threads <= 1 || m <= 1) {
     for (size_t t = 0; t < m; ++t) gemv_rows(w, cols, act + t * cols, 0, rows, out + t * rows);
     return;
@@ -1009,6 +1036,7 @@ extern "C" {
 
 const char* orc_last_error(void) { return g_last_error.c_str(); }
 void orc_set_threads(int threads) { g_threads = threads < 1 ? 1 : threads; }
+void orc_set_slab_group(int tokens) { g_slab_group = tokens < 1 ? 1 : tokens; }
 
 int orc_det_linear(size_t rows, size_t cols, int w, const void* weight, const int32_t* act, int32_t* out, int threads) {
   return guarded([&] {
@@ -1205,6 +1233,11 @@ int orc_session_decode(orc_session* s, uint32_t token, int32_t* logits_out, int3
   });
 }
 
+int orc_session_clone(const orc_session* src, orc_session** out) {
+  if (!src || !out) return 1;
+  *out = new orc_session(*src);
+  return 0;
+}
 void orc_session_free(orc_session* s) { delete s; }
 
 }  // extern "C"

@@ -130,6 +130,9 @@ int orc_model_load_detwgt(orc_model* m, const uint8_t* bytes, size_t len);
 int orc_model_finalize(orc_model* m);
 void orc_model_free(orc_model* m);
 void orc_set_threads(int threads);
+/* Token rows per slab work item (default 1, the reference's schedule); more
+ * read each weight row once per group. Results are identical for any value. */
+void orc_set_slab_group(int tokens);
 
 // Runs the det_goldens capture (src/runtime/det_goldens.rs:90-185) for the
 // given prompt ids and writes it as compact JSON into `out` (NUL-terminated).
@@ -150,6 +153,8 @@ typedef struct orc_session orc_session;
 int orc_session_prefill(orc_model* m, const uint32_t* prompt, size_t prompt_len,
                         orc_session** out, int32_t* logits_out);
 int orc_session_decode(orc_session* s, uint32_t token, int32_t* logits_out, int32_t* hidden_out);
+/* An independent copy of a session (its caches, position and last logits). */
+int orc_session_clone(const orc_session* src, orc_session** out);
 void orc_session_free(orc_session* s);
 
 #ifdef __cplusplus

@@ -133,5 +133,9 @@ struct RowPtrs {
 void launch_gather_row_ptrs(const RowPtrs& g, int32_t* dst, hipStream_t s);
 // dst[i][0..w) = src[i * w ..] for i < n (device array of row pointers).
 void launch_copy_rows(const int32_t* src, uint64_t w, uint64_t n, int32_t* const* dst, hipStream_t s);
+// Writes `bytes` (a multiple of 8) of host data to device memory at dst by
+// kernel arguments, 3.5 KB per launch: stream-ordered, nothing staged in
+// host memory the device reads later.
+void launch_set_bytes(void* dst, const void* src, size_t bytes, hipStream_t s);
 
 }  // namespace det

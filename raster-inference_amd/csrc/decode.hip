@@ -10,6 +10,9 @@
 // reduction is an integer reduction whose result does not depend on order.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cstring>
+
 #include "decode.h"
 #include "det_arith.h"
 #include "kernels.h"
@@ -941,6 +944,15 @@ __global__ __launch_bounds__(256) void k_dec_acc_limbs(int64_t* __restrict__ acc
   for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(limbs + (t * 4 + j) * kpad + c0) = packed[j];
 }
 
+// Up to kSetWords 64-bit words by value (within the 4 KB of kernel arguments).
+constexpr uint32_t kSetWords = 448;
+struct SetWords {
+  uint64_t w[kSetWords];
+};
+__global__ __launch_bounds__(256) void k_set_words(uint64_t* __restrict__ dst, uint32_t n, SetWords v) {
+  for (uint32_t i = threadIdx.x; i < n; i += 256) dst[i] = v.w[i];
+}
+
 __global__ void k_copy_rows(const int32_t* __restrict__ src, uint64_t w, int32_t* const* __restrict__ dst) {
   const uint64_t c = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (c >= w) return;
@@ -1125,6 +1137,16 @@ void launch_dec_acc_limbs(int64_t* acc, uint64_t k, uint64_t ld, uint32_t nseq, 
 }
 void launch_copy_rows(const int32_t* src, uint64_t w, uint64_t n, int32_t* const* dst, hipStream_t s) {
   if (n && w) hipLaunchKernelGGL(k_copy_rows, dim3(nblk((w + 3) / 4, 256), unsigned(n)), dim3(256), 0, s, src, w, dst);
+}
+void launch_set_bytes(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  const auto* w = static_cast<const uint8_t*>(src);
+  auto* d = static_cast<uint64_t*>(dst);
+  for (size_t off = 0; off < bytes / 8; off += kSetWords) {
+    const uint32_t n = uint32_t(std::min<size_t>(kSetWords, bytes / 8 - off));
+    SetWords v{};
+    std::memcpy(v.w, w + off * 8, size_t(n) * 8);
+    hipLaunchKernelGGL(k_set_words, dim3(1), dim3(256), 0, s, d + off, n, v);
+  }
 }
 
 }  // namespace det

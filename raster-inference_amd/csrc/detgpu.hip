@@ -877,12 +877,17 @@ struct GKv {
   bool ring = false;  // sliding-window cache of capacity == window
   uint64_t start = 0, len = 0;
   uint64_t total = 0;  // tokens appended so far; token t sits at slot t % cap (ring) or t
+  // tokens the cache may take in all: a ring smaller than its window (a
+  // layer-level cache created for fewer tokens than the window) would
+  // otherwise overwrite rows the window still reads
+  uint64_t limit = UINT64_MAX;
 };
 
 }  // namespace
 
 struct det_session {
   det_model* m = nullptr;
+  det_ctx* ctx = nullptr;  // m->ctx, kept so that freeing the session does not read the model
   uint64_t max_tokens = 0, position = 0;
   std::vector<GKv> kv;
   // device scratch (sized for max_tokens rows)
@@ -944,6 +949,7 @@ struct det_session {
 // for the layer-level entry points.
 struct det_kv {
   det_model* m = nullptr;
+  det_ctx* ctx = nullptr;  // m->ctx, kept so that freeing the cache does not read the model
   uint64_t layer = 0;
   GKv c;
   ~det_kv() {
@@ -956,6 +962,7 @@ struct det_kv {
 // det_kernels.rs:830-864), grown on demand to the largest row count seen.
 struct det_scratch {
   det_model* m = nullptr;
+  det_ctx* ctx = nullptr;  // m->ctx, kept so that freeing the scratch does not read the model
   std::unique_ptr<det_session> ws;
 };
 
@@ -966,6 +973,7 @@ namespace {
 // the layer-level entry points has neither).
 void session_alloc(det_session* s, bool with_state = true) {
   det_model* m = s->m;
+  s->ctx = m->ctx;
   const uint64_t T = s->max_tokens, H = m->hidden;
   uint64_t qw = 0, kw = 0, ffw = 0, plew = m->ple_dim;
   for (const GLayer& L : m->layers) {
@@ -1063,33 +1071,74 @@ std::vector<int32_t> host_rows(det_ctx* ctx, const GKv& c, int side) {
   return out;
 }
 
-// build_det_kv_cache_commitment (transformer_kernels.rs:1460-1482) over the
-// given layers' caches; false (None) when one of them has no det data.
-bool commit_kv(det_ctx* ctx, const std::vector<const GKv*>& caches, char out[65]) {
-  for (const GKv* c : caches)
-    if (!c->has) { out[0] = 0; return false; }
+// The rows of the given layers' caches on the host, for one KV commitment:
+// the copies are enqueued here and complete at the next stream synchronize.
+struct KvHost {
+  bool some = true;  // every cache holds det data
+  std::vector<const GKv*> caches;
   std::vector<std::vector<int32_t>> keys, vals;
+};
+
+KvHost fetch_kv(det_ctx* ctx, const std::vector<const GKv*>& caches) {
+  KvHost h;
+  for (const GKv* c : caches)
+    if (!c->has) {
+      h.some = false;
+      return h;
+    }
+  h.caches = caches;
   for (const GKv* c : caches) {
-    keys.push_back(host_rows(ctx, *c, 0));
-    vals.push_back(host_rows(ctx, *c, 1));
+    h.keys.push_back(host_rows(ctx, *c, 0));
+    h.vals.push_back(host_rows(ctx, *c, 1));
   }
-  HIPC(hipStreamSynchronize(ctx->stream));
+  return h;
+}
+
+// build_det_kv_cache_commitment (transformer_kernels.rs:1460-1482) over
+// fetched rows (after the synchronize); false (None) when a cache has no det data.
+bool hash_kv(const KvHost& h, char out[65]) {
+  if (!h.some) {
+    out[0] = 0;
+    return false;
+  }
   std::vector<det_commit::KvLayerView> views;
-  for (size_t i = 0; i < caches.size(); ++i) {
+  for (size_t i = 0; i < h.caches.size(); ++i) {
     det_commit::KvLayerView v;
     v.has = true;
-    v.heads = caches[i]->heads;
-    v.hd = caches[i]->hd;
-    v.len = caches[i]->len;
-    const int32_t* k = keys[i].data();
-    const int32_t* vv = vals[i].data();
-    const uint64_t w = caches[i]->row_w;
+    v.heads = h.caches[i]->heads;
+    v.hd = h.caches[i]->hd;
+    v.len = h.caches[i]->len;
+    const int32_t* k = h.keys[i].data();
+    const int32_t* vv = h.vals[i].data();
+    const uint64_t w = h.caches[i]->row_w;
     v.row = [k, vv, w](int side, uint64_t r) { return (side ? vv : k) + r * w; };
     views.push_back(std::move(v));
   }
-  const std::string h = det_commit::commit_kv(views);
-  std::memcpy(out, h.c_str(), 65);
+  const std::string d = det_commit::commit_kv(views);
+  std::memcpy(out, d.c_str(), 65);
   return true;
+}
+
+bool commit_kv(det_ctx* ctx, const std::vector<const GKv*>& caches, char out[65]) {
+  const KvHost h = fetch_kv(ctx, caches);
+  HIPC(hipStreamSynchronize(ctx->stream));
+  return hash_kv(h, out);
+}
+
+// The KV commitments of several sessions' caches: one synchronize for all
+// the copies, then one hashing thread per session (at most the host's cores).
+void commit_kv_sessions(det_ctx* ctx, const std::vector<std::vector<const GKv*>>& sets, std::vector<char*> outs) {
+  std::vector<KvHost> hs;
+  for (const auto& set : sets) hs.push_back(fetch_kv(ctx, set));
+  HIPC(hipStreamSynchronize(ctx->stream));
+  const size_t n = hs.size();
+  const size_t nt = std::max<size_t>(1, std::min<size_t>(n, std::max(1u, std::thread::hardware_concurrency())));
+  std::vector<std::thread> pool;
+  for (size_t t = 0; t < nt; ++t)
+    pool.emplace_back([&, t] {
+      for (size_t i = t; i < n; i += nt) hash_kv(hs[i], outs[i]);
+    });
+  for (auto& th : pool) th.join();
 }
 
 std::vector<const GKv*> all_caches(det_session* s) {
@@ -1322,7 +1371,7 @@ bool layer_prefill(det_session* ws, const GLayer& L, uint64_t n, GKv* own, const
   const uint64_t retained = (!donor && own && own->ring) ? (n > own->cap ? n - own->cap : 0) : 0;
   if (!donor && own) {
     if (own->row_w != kw) bail("layer cache head count mismatch");
-    if (n - retained > own->cap) bail("KV cache capacity exceeded");
+    if (n - retained > own->cap || n > own->limit) bail("KV cache capacity exceeded");
   }
   // the attention's arguments and work area first: the head-norm kernel then
   // writes the MFMA form's Q (and, with this layer's own K rows, K) operand
@@ -1388,7 +1437,7 @@ void layer_decode(det_session* ws, const GLayer& L, uint64_t position, GKv* own,
   if (!donor) {
     GKv& c = *own;
     if (c.row_w != kw) bail("layer cache append head count mismatch");
-    if (!c.ring && c.total >= c.cap) bail("KV cache capacity exceeded");
+    if ((!c.ring && c.total >= c.cap) || c.total >= c.limit) bail("KV cache capacity exceeded");
     const uint64_t slot = c.ring ? c.total % c.cap : c.total;
     copy_d2d(ctx, c.k + slot * kw, ws->kb, kw * 4);
     copy_d2d(ctx, c.v + slot * kw, ws->vb, kw * 4);
@@ -1546,8 +1595,10 @@ struct BatchWs {
   uint32_t* next = nullptr;   // [cap] greedy tokens
   int64_t* am_keys = nullptr;  // argmax partial keys of cap logits rows
   uint8_t* desc = nullptr;    // device: positions, per-layer windows and append targets
-  uint8_t* desc_host = nullptr;  // pinned staging of desc
   size_t desc_bytes = 0;
+  // fused step: the cache and logits-row part of desc as last written (it
+  // changes only with the batch's sessions; the step states every step)
+  std::vector<uint8_t> desc_tail;
   // fused batched step: per-sequence rows of the fused decode buffers
   bool fused = false;
   uint64_t grid_cap = 0;  // cache rows the captured attention grids cover
@@ -1582,7 +1633,6 @@ struct BatchWs {
                     static_cast<void*>(attn_keys)})
       if (p) (void)hipFree(p);
     for (void* p : owned) (void)hipFree(p);
-    if (desc_host) (void)hipHostFree(desc_host);
   }
 };
 
@@ -1628,7 +1678,6 @@ BatchWs& ensure_batch(det_model* m, uint64_t n) {
   HIPC(hipMalloc(&b->am_keys, det::argmax_rows_scratch(b->cap, m->vocab) * 8));
   b->desc_bytes = std::max(BatchDesc(b->cap, m->layers.size()).bytes, FusedDesc(b->cap, m->layers.size()).bytes);
   HIPC(hipMalloc(&b->desc, b->desc_bytes));
-  HIPC(hipHostMalloc(reinterpret_cast<void**>(&b->desc_host), b->desc_bytes, hipHostMallocDefault));
   m->batch = b.release();
   return *m->batch;
 }
@@ -1666,7 +1715,8 @@ void decode_batch(det_session* const* ss, uint64_t n, const uint32_t* tokens, ui
   det_session* w = b.rows.get();
   // host bookkeeping: cache state after this step's append, then the windows
   const BatchDesc D(n, nl);
-  uint8_t* hb = b.desc_host;
+  std::vector<uint8_t> hbv(D.bytes);
+  uint8_t* hb = hbv.data();
   auto* pos = reinterpret_cast<uint64_t*>(hb + D.pos);
   auto* seqs = reinterpret_cast<det::AttnSeq*>(hb + D.seqs);
   auto* kdst = reinterpret_cast<int32_t**>(hb + D.kdst);
@@ -1708,7 +1758,8 @@ void decode_batch(det_session* const* ss, uint64_t n, const uint32_t* tokens, ui
     }
   }
   uint8_t* dd = b.desc;
-  HIPC(hipMemcpyAsync(dd, hb, D.bytes, hipMemcpyHostToDevice, st));
+  det::launch_set_bytes(dd, hb, D.bytes, st);
+  b.desc_tail.clear();  // desc now holds this layout, not the fused step's cache table
   HIPC(hipMemcpyAsync(w->ids, tokens, n * 4, hipMemcpyHostToDevice, st));
   const auto* pos_dev = reinterpret_cast<const uint64_t*>(dd + D.pos);
   det::launch_gather_rows(*m->embedding, w->ids, n, 0, H, m->embed_scale, b.dec_in, H, st);
@@ -1759,8 +1810,16 @@ void decode_batch(det_session* const* ss, uint64_t n, const uint32_t* tokens, ui
   }
   for (uint64_t i = 0; i < n; ++i) {
     out[i].kv[0] = 0;
-    if (flags & DET_COMMIT_KV) commit_kv(m->ctx, all_caches(ss[i]), out[i].kv);
     out[i].next_token = next[i];
+  }
+  if (flags & DET_COMMIT_KV) {
+    std::vector<std::vector<const GKv*>> sets;
+    std::vector<char*> outs;
+    for (uint64_t i = 0; i < n; ++i) {
+      sets.push_back(all_caches(ss[i]));
+      outs.push_back(out[i].kv);
+    }
+    commit_kv_sessions(m->ctx, sets, outs);
   }
 }
 
@@ -1909,7 +1968,8 @@ void decode_batch_fused(det_session* const* ss, uint64_t n, const uint32_t* toke
   for (uint64_t i = 0; i < n; ++i) need = std::max(need, ss[i]->max_tokens);
   ensure_fused_batch(m, b, need);
   const FusedDesc D(n, nl);
-  uint8_t* hb = b.desc_host;
+  std::vector<uint8_t> hbv(D.bytes);
+  uint8_t* hb = hbv.data();
   auto* sts = reinterpret_cast<det::StepState*>(hb + D.st);
   auto* caches = reinterpret_cast<det::DecSeqCache*>(hb + D.caches);
   auto* dst = reinterpret_cast<int32_t**>(hb + D.logit_dst);
@@ -1927,7 +1987,15 @@ void decode_batch_fused(det_session* const* ss, uint64_t n, const uint32_t* toke
       caches[l * n + i] = det::DecSeqCache{c.k, c.v, c.cap};
     }
   }
-  HIPC(hipMemcpyAsync(b.desc, hb, D.bytes, hipMemcpyHostToDevice, st));
+  // descriptors by kernel arguments, stream-ordered before the step: the
+  // step states every step, the cache table when the batch changes
+  det::launch_set_bytes(b.desc + D.st, hb + D.st, D.caches - D.st, st);
+  if (b.desc_tail.size() != D.bytes - D.caches ||
+      std::memcmp(b.desc_tail.data(), hb + D.caches, D.bytes - D.caches) != 0) {
+    det::launch_set_bytes(b.desc + D.caches, hb + D.caches, D.bytes - D.caches, st);
+    b.desc_tail.assign(hb + D.caches, hb + D.bytes);
+  }
+  HIPC(hipGetLastError());
   const bool eager = flags & DET_DECODE_EAGER;
   if (eager) {
     enqueue_fused_batch(m, b, uint32_t(n));
@@ -1971,8 +2039,16 @@ void decode_batch_fused(det_session* const* ss, uint64_t n, const uint32_t* toke
   }
   for (uint64_t i = 0; i < n; ++i) {
     out[i].kv[0] = 0;
-    if (flags & DET_COMMIT_KV) commit_kv(m->ctx, all_caches(ss[i]), out[i].kv);
     out[i].next_token = next[i];
+  }
+  if (flags & DET_COMMIT_KV) {
+    std::vector<std::vector<const GKv*>> sets;
+    std::vector<char*> outs;
+    for (uint64_t i = 0; i < n; ++i) {
+      sets.push_back(all_caches(ss[i]));
+      outs.push_back(out[i].kv);
+    }
+    commit_kv_sessions(m->ctx, sets, outs);
   }
 }
 
@@ -3102,7 +3178,7 @@ int det_session_clone(const det_session_t* src, det_session_t** out) {
 }
 void det_session_free(det_session_t* s) {
   if (!s) return;
-  (void)hipStreamSynchronize(s->m->ctx->stream);
+  (void)hipStreamSynchronize(s->ctx->stream);
   delete s;
 }
 int det_session_prefill(det_session_t* s, const uint32_t* ids, uint64_t n, uint32_t flags, det_prefill_result_t* out) {
@@ -3263,13 +3339,14 @@ int det_scratch_create(det_model_t* m, det_scratch_t** out) {
     if (!m->finalized) bail("model is not finalized");
     auto sc = std::make_unique<det_scratch>();
     sc->m = m;
+    sc->ctx = m->ctx;
     *out = sc.release();
   });
 }
 
 void det_scratch_free(det_scratch_t* sc) {
   if (!sc) return;
-  (void)hipStreamSynchronize(sc->m->ctx->stream);
+  (void)hipStreamSynchronize(sc->ctx->stream);
   delete sc;
 }
 
@@ -3283,6 +3360,7 @@ int det_kv_create(det_model_t* m, uint64_t layer, uint64_t max_tokens, det_kv_t*
     if (max_tokens == 0) bail("a KV cache needs room for at least one token");
     auto kv = std::make_unique<det_kv>();
     kv->m = m;
+    kv->ctx = m->ctx;
     kv->layer = layer;
     GKv& c = kv->c;
     c.heads = L.num_kv_heads;
@@ -3290,6 +3368,7 @@ int det_kv_create(det_model_t* m, uint64_t layer, uint64_t max_tokens, det_kv_t*
     c.row_w = L.num_kv_heads * L.head_dim;
     c.ring = L.cache_sliding_window.has_value();
     c.cap = c.ring ? std::max<uint64_t>(std::min<uint64_t>(*L.cache_sliding_window, max_tokens), 1) : max_tokens;
+    if (c.ring && max_tokens < *L.cache_sliding_window) c.limit = max_tokens;
     HIPC(hipMalloc(&c.k, std::max<uint64_t>(c.cap * c.row_w, 1) * 4));
     HIPC(hipMalloc(&c.v, std::max<uint64_t>(c.cap * c.row_w, 1) * 4));
     *out = kv.release();
@@ -3304,6 +3383,7 @@ int det_kv_clone(const det_kv_t* src, det_kv_t** out) {
   return guarded(src->m->ctx, [&] {
     auto kv = std::make_unique<det_kv>();
     kv->m = src->m;
+    kv->ctx = src->ctx;
     kv->layer = src->layer;
     kv->c = src->c;
     kv->c.k = kv->c.v = nullptr;
@@ -3319,7 +3399,7 @@ int det_kv_clone(const det_kv_t* src, det_kv_t** out) {
 
 void det_kv_free(det_kv_t* kv) {
   if (!kv) return;
-  (void)hipStreamSynchronize(kv->m->ctx->stream);
+  (void)hipStreamSynchronize(kv->ctx->stream);
   delete kv;
 }
 

@@ -179,11 +179,13 @@ def lib() -> C.CDLL:
             ("orc_model_finalize", C.c_int, [P]),
             ("orc_model_free", None, [P]),
             ("orc_set_threads", None, [C.c_int]),
+            ("orc_set_slab_group", None, [C.c_int]),
             ("orc_capture", C.c_int, [P, P, C.c_size_t, C.c_size_t, C.c_char_p, C.c_size_t]),
             ("orc_trace_capture", C.c_int, [P, P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, C.c_char_p,
                                             C.c_size_t]),
             ("orc_session_prefill", C.c_int, [P, P, C.c_size_t, C.POINTER(P), P]),
             ("orc_session_decode", C.c_int, [P, C.c_uint32, P, P]),
+            ("orc_session_clone", C.c_int, [P, P]),
             ("orc_session_free", None, [P]),
         ]:
             fn = getattr(L, name)
@@ -280,6 +282,16 @@ class OracleSession:
     def next_token(self) -> int:
         return int(np.argmax(self.logits))  # argmax_first: numpy returns the first maximum
 
+    def clone(self) -> "OracleSession":
+        """An independent copy (caches, position, last logits)."""
+        c = OracleSession.__new__(OracleSession)
+        c.model, c.vocab, c.hidden = self.model, self.vocab, self.hidden
+        c.logits = self.logits.copy()
+        h = C.c_void_p()
+        check(lib().orc_session_clone(self.handle, C.byref(h)))
+        c.handle = h
+        return c
+
     def decode(self, token: int) -> np.ndarray:
         """One decode step; returns the activation row (logits in self.logits)."""
         hidden = np.empty(self.hidden, dtype=np.int32)
@@ -310,6 +322,13 @@ def rope_inv_frequencies(base_acc: int, freq_base_dim: int, half: int) -> np.nda
 
 def set_threads(n: int) -> None:
     lib().orc_set_threads(int(n))
+
+
+def set_slab_group(tokens: int) -> None:
+    """Token rows per slab work item: 1 is the reference's schedule; larger
+    groups read each weight row once per group (the same sums, faster for the
+    long prompts of the E4B tests)."""
+    lib().orc_set_slab_group(int(tokens))
 
 
 def det_linear(weight: np.ndarray, act: np.ndarray, threads: int = 1) -> np.ndarray:

@@ -8,12 +8,16 @@
 * 16 sequences of 300-700 tokens decoded in shared batched steps, each
   sequence's commitments equal to the oracle's capture of that sequence alone
   (multi-chunk workgroups and the separate softmax statistics pass);
-* the full 42-layer E4B-shaped model (config 4): 512-token prompt, then greedy
-  decode, every capture entry equal to the oracle's.
+* the full 42-layer E4B-shaped model (config 4): 512-token prompt, then all
+  256 greedy decode steps, every capture entry equal to the oracle's;
+* the longest prompt of the ragged 16-sequence set (config 5, 1643 tokens)
+  through the 42 layers, equal to the oracle's capture (full-attention
+  windows past 1600 rows), and all 16 sequences decoded in shared batched
+  steps for the 128 steps of config 5, equal to their solo decodes.
 
 The oracle runs on all host cores with the reference's parallel schedule
-(token-parallel slab GEMV, item-parallel attention); it is itself pinned by
-test_oracle_*.py.
+(token-parallel slab GEMV in groups of 16 token rows, item-parallel
+attention); it is itself pinned by test_oracle_*.py.
 """
 import time
 
@@ -28,6 +32,16 @@ rd = pytest.importorskip("rasterdet")
 from rasterdet import synthetic  # noqa: E402
 
 THREADS = oracle_lib.cpu_count()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def grouped_oracle_slabs():
+    # the oracle's slab GEMVs take 16 token rows per work item here (the same
+    # sums as the reference's one-row items, test_oracle_goldens.py), so the
+    # long prompts' prefills read each weight row once per 16 tokens
+    oracle_lib.set_slab_group(16)
+    yield
+    oracle_lib.set_slab_group(1)
 
 
 @pytest.fixture(scope="module")
@@ -162,7 +176,7 @@ def e4b_full(ctx):
     del om, gm
 
 
-E4B_DECODE_STEPS = 24
+E4B_DECODE_STEPS = 256  # config 4's greedy steps (contexts 512..767)
 
 
 def test_e4b_42_layers_prompt_512_capture_matches_oracle(e4b_full):
@@ -208,16 +222,47 @@ def test_e4b_42_layers_checkpoint_trace_matches_oracle(e4b_full):
     assert [next(iter(e.items())) for e in json.loads(got)] == exp
 
 
+def ragged_prompts():
+    # config 5: 16 prompts with seeded lengths uniform in [32, 2048] (the
+    # ragged set bench.py decodes: seed 2029, lengths 91-1643)
+    rng = np.random.default_rng(2029)
+    lens = rng.integers(32, 2049, size=16)
+    return lens, [rng.integers(0, 262144, size=int(k)).tolist() for k in lens]
+
+
+def test_e4b_42_layers_longest_ragged_prompt_matches_oracle(e4b_full):
+    # the solo decode that the batched steps are compared with below, anchored
+    # to the oracle at config 5's longest prompt: full-attention windows of
+    # 1643-1651 rows, sliding rings wrapped three times
+    om, gm = e4b_full
+    lens, prompts = ragged_prompts()
+    prompt = prompts[int(np.argmax(lens))]
+    assert len(prompt) == 1643
+    steps = 8
+    t0 = time.time()
+    got = gm.capture(prompt, steps)
+    print(f"[e4b-1643] GPU capture {time.time() - t0:.1f}s", flush=True)
+    t0 = time.time()
+    exp = om.capture(prompt, steps)
+    print(f"[e4b-1643] oracle capture {time.time() - t0:.1f}s", flush=True)
+    assert got["prefill"] == exp["prefill"]
+    assert got["first_step_layers"] == exp["first_step_layers"]
+    assert got["decode_steps"] == exp["decode_steps"]
+    assert got["end_to_end"] == exp["end_to_end"]
+
+
+RAGGED_STEPS = 128  # config 5's greedy steps
+
+
 def test_e4b_42_layers_ragged_16_batch_matches_solo(e4b_full):
     # config 5: 16 sequences with seeded prompt lengths in [32, 2048] decoded
-    # in shared batched steps; each sequence's activation and logits
-    # commitments every step, and its KV commitment at steps 0, 7 and 15,
-    # equal its solo decode (whose commitments are the oracle's, above)
+    # in shared batched steps for all 128 steps; each sequence's activation
+    # and logits commitments every step, and its KV commitment every 16th
+    # step and at the last, equal its solo decode (whose commitments are the
+    # oracle's at 512 and 1643 tokens, above)
     _, gm = e4b_full
-    rng = np.random.default_rng(5)
-    lens = rng.integers(32, 2049, size=16)
-    prompts = [rng.integers(0, 262144, size=int(k)).tolist() for k in lens]
-    steps = 16
+    lens, prompts = ragged_prompts()
+    steps = RAGGED_STEPS
     t0 = time.time()
     batch = [gm.session(int(k) + steps + 1) for k in lens]
     toks = [s.prefill(p, rd.DET_COMMIT_NONE).next_token for s, p in zip(batch, prompts)]
@@ -225,11 +270,14 @@ def test_e4b_42_layers_ragged_16_batch_matches_solo(e4b_full):
     tok_s = list(toks)
     print(f"[ragged16] prefilled {int(lens.sum())} tokens in {time.time() - t0:.1f}s", flush=True)
     for step in range(steps):
-        flags = rd.DET_COMMIT_ALL if step in (0, 7, 15) else rd.DET_COMMIT_ACTIVATIONS
+        kv = step % 16 == 0 or step == steps - 1
+        flags = rd.DET_COMMIT_ALL if kv else rd.DET_COMMIT_ACTIVATIONS
         res = rd.decode_batch(batch, toks, flags)
         for i, r in enumerate(res):
             e = solo[i].decode(tok_s[i], flags)
             assert (r.activation, r.logits, r.kv, r.next_token) == (e.activation, e.logits, e.kv, e.next_token), \
                 (step, i, int(lens[i]))
             toks[i], tok_s[i] = r.next_token, e.next_token
+        if kv:
+            print(f"[ragged16] step {step} checked (with KV) at {time.time() - t0:.1f}s", flush=True)
     print(f"[ragged16] {steps} batched steps checked against solo in {time.time() - t0:.1f}s", flush=True)

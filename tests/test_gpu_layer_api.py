@@ -202,3 +202,38 @@ def test_kv_handles_read_logical_rows_and_reject_misuse(ctx):
         loop.ops.layer_decode(0, x, None, None, None, 7, x)
     with pytest.raises(rd.DetError):
         rd.KvCache(gm, 2, 8)  # no such layer
+
+
+def test_kv_handle_smaller_than_window_fails_closed(ctx):
+    # a sliding-window cache created for fewer tokens than its window holds
+    # max_tokens rows: a prefill or append past max_tokens must fail (the
+    # reference's cache would still hold the last `window` rows) instead of
+    # overwriting rows the window reads; a linear cache fails the same way,
+    # and a ring sized at its window keeps taking tokens
+    cfg = synthetic.e4b_config(layers=2, vocab=512, sliding_window=8)
+    cfg["text_config"].update({"hidden_size": 128, "intermediate_size": 256, "head_dim": 32,
+                               "num_attention_heads": 4, "num_key_value_heads": 2})
+    gm = rd.Model(ctx, cfg)
+    for name, v, s in fixtures.custom_model(cfg, seed=6):
+        gm.set_tensor(name, v, s)
+    gm.finalize()
+    ops = rd.LayerOps(gm)
+    x = ctx.to_device(np.zeros((6, 128), dtype=np.int32))
+    small = rd.KvCache(gm, 0, 5)  # layer 0 is sliding (window 8), room for 5 tokens
+    with pytest.raises(rd.DetError, match="KV cache capacity exceeded"):
+        ops.layer_prefill(0, x, 6, None, None, small, x)
+    small = rd.KvCache(gm, 0, 5)
+    ops.layer_prefill(0, x, 5, None, None, small, x)
+    assert small.info()[0] == 5
+    row = ctx.to_device(np.zeros(128, dtype=np.int32))
+    with pytest.raises(rd.DetError, match="KV cache capacity exceeded"):
+        ops.layer_decode(0, row, None, small, None, 5, row)
+    linear = rd.KvCache(gm, 1, 5)  # layer 1 is full attention
+    ops.layer_prefill(1, x, 5, None, None, linear, x)
+    with pytest.raises(rd.DetError, match="KV cache capacity exceeded"):
+        ops.layer_decode(1, row, None, linear, None, 5, row)
+    ring = rd.KvCache(gm, 0, 8)  # sized at the window: the trim keeps it going
+    ops.layer_prefill(0, x, 5, None, None, ring, x)
+    for pos in range(5, 12):
+        ops.layer_decode(0, row, None, ring, None, pos, row)
+    assert ring.info()[0] == 8

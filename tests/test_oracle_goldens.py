@@ -48,6 +48,45 @@ def test_thread_count_invariance(threads):
     assert got["decode_steps"] == exp["decode_steps"][:4]
 
 
+@pytest.mark.parametrize("group,threads", [(2, 1), (5, 3), (16, 8)])
+def test_slab_group_invariance(group, threads):
+    # token rows grouped per slab work item (each weight row read once per
+    # group) give the reference schedule's commitments: every output element
+    # adds its terms in column order either way
+    cfg, wgt, prompt, _ = fixtures.golden_fixture("donor_ple")
+    oracle_lib.set_threads(threads)
+    oracle_lib.set_slab_group(group)
+    try:
+        got = oracle_lib.OracleModel(cfg).load_detwgt(wgt).finalize().capture(prompt, 4)
+    finally:
+        oracle_lib.set_threads(1)
+        oracle_lib.set_slab_group(1)
+    exp = fixtures.golden_expected("donor_ple")
+    assert got["prefill"] == exp["prefill"]
+    assert got["first_step_layers"] == exp["first_step_layers"]
+    assert got["decode_steps"] == exp["decode_steps"][:4]
+
+
+@pytest.mark.parametrize("width", [16, 32])
+def test_slab_group_matches_per_token_gemv(width):
+    # the grouped slab against one GEMV per token row, ragged token counts
+    # and row lengths, values at the ends of the storage range
+    import numpy as np
+    rng = np.random.default_rng(width)
+    info = np.iinfo(np.int16 if width == 16 else np.int32)
+    for m, n, k in [(1, 7, 5), (17, 33, 129), (40, 64, 1000)]:
+        w = rng.integers(info.min, info.max, size=(n, k), endpoint=True).astype(info.dtype)
+        a = rng.integers(-(1 << 31), 1 << 31, size=(m, k)).astype(np.int32)
+        exp = np.stack([oracle_lib.det_linear(w, a[t]) for t in range(m)])
+        for group, threads in [(3, 1), (16, 4)]:
+            oracle_lib.set_slab_group(group)
+            try:
+                got = oracle_lib.det_linear_slab(w, a, threads=threads)
+            finally:
+                oracle_lib.set_slab_group(1)
+            assert np.array_equal(got, exp), (m, n, k, group)
+
+
 def test_loader_fails_closed():
     cfg, wgt, _, _ = fixtures.golden_fixture("no_donor_ple")
     bad_version = wgt[:8] + (1).to_bytes(4, "little") + wgt[12:]
