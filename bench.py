@@ -321,6 +321,97 @@ def e4b_decode(ctx, rd, args, model, load_s) -> dict:
     }
 
 
+I16_LIM = 4096  # i16 Wgt bits uniform in [-4096, 4096] (|w| < 1/16) plus extreme entries
+
+
+def i16_gemv(ctx, rd, args) -> dict:
+    """The lm_head GEMV (262144 x 2560) over i16 Wgt bits that do not factor
+    into int8 x scale (the reference's own artifact storage, det_num/
+    artifact.rs:57-63), held as two int8 digit planes: parity against the
+    oracle's i16 dot product, then 10 launches timed with HIP events on the
+    context stream (1.34 GB of weights: every launch reads them cold from
+    HBM). Algorithmic bytes = 2 N K (i16 weights) + 4 K (activation) + 4 N
+    (output)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib  # the oracle is the checker only
+
+    from rasterdet import synthetic
+
+    n, k = SHAPES[-1]
+    w = rd.synthetic_i16(args.seed + 77, n, k, I16_LIM)
+    act = synthetic.f32_to_act(np.random.default_rng(args.seed + 78).standard_normal(k).astype(np.float32))
+    mat = ctx.upload_matrix(w)
+    a, o = ctx.to_device(act), ctx.empty(n)
+    ctx.det_linear_into(mat, a, o)
+    parity = bool(np.array_equal(o.numpy(), oracle_lib.det_linear(w, act, threads=oracle_lib.cpu_count())))
+    del w
+    for _ in range(3):
+        ctx.det_linear_into(mat, a, o)
+    reps = 10
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record()
+    for _ in range(reps):
+        ctx.det_linear_into(mat, a, o)
+    e1.record()
+    us = e0.elapsed_ms(e1) / reps * 1e3
+    alg = 2 * n * k + 4 * k + 4 * n
+    gbs = alg / (us / 1e6) / 1e9
+    log(f"[bench] i16 lm_head GEMV: {us:.1f} us per launch, {gbs:.0f} GB/s (parity {'ok' if parity else 'MISMATCH'})")
+    return {"shape": f"{n}x{k}", "storage": mat.storage, "parity_bit_exact": parity, "us_per_launch": round(us, 2),
+            "alg_bytes_per_launch": alg, "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "weights": f"i16 Wgt bits uniform in [-{I16_LIM}, {I16_LIM}] with 32767 / -32768 entries "
+                       "(two int8 digit planes)"}
+
+
+def e4b_i16_decode(ctx, rd, args) -> dict:
+    """The E4B-shaped model (42 layers) with i16 Wgt bits that do not factor
+    (every matrix as two int8 digit planes, the reference's own i16 storage):
+    512-token prefill and greedy decode through the fused step; tokens of a
+    second decode of the same prompt must repeat. Bytes per token are the
+    i16 weights (2 x 4.52 G) plus the KV rows read."""
+    from rasterdet import synthetic
+
+    cfg = synthetic.e4b_config(layers=args.e4b_layers)
+    t0 = time.perf_counter()
+    model = rd.Model(ctx, cfg)
+    for name, v, s in synthetic.synthetic_model_i16(cfg, seed=args.seed + 3, lim=I16_LIM):
+        model.set_tensor(name, v, s)
+    model.finalize()
+    load_s = time.perf_counter() - t0
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, 262144, size=args.prompt_len).tolist()
+    steps = args.i16_steps
+    sess = model.session(args.prompt_len + steps + 1)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    tok = sess.prefill(prompt, rd.DET_COMMIT_NONE).next_token
+    ctx.synchronize()
+    prefill_s = time.perf_counter() - t0
+    tokens = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tokens.append(tok)
+        tok = sess.decode(tok, rd.DET_COMMIT_NONE).next_token
+    ctx.synchronize()
+    dec_s = time.perf_counter() - t0
+    s2 = model.session(args.prompt_len + 17)
+    t2 = s2.prefill(prompt, rd.DET_COMMIT_NONE).next_token
+    same = True
+    for i in range(16):
+        same &= t2 == tokens[i]
+        t2 = s2.decode(t2, rd.DET_COMMIT_ACTIVATIONS).next_token
+    out = {"fused_step": model.fused_decode, "decode_tok_s": round(steps / dec_s, 2),
+           "decode_ms_per_token": round(dec_s / steps * 1e3, 3), "prefill_tok_s": round(args.prompt_len / prefill_s, 1),
+           "prompt": args.prompt_len, "decode_steps": steps, "load_s": round(load_s, 1),
+           "repeat_run_tokens_identical": bool(same),
+           "weights": f"i16 Wgt bits uniform in [-{I16_LIM}, {I16_LIM}] with 32767 / -32768 entries "
+                      "(two int8 digit planes per matrix)"}
+    log(f"[bench] E4B i16 decode {steps} steps in {dec_s * 1e3:.1f} ms ({steps / dec_s:.1f} tok/s), prefill "
+        f"{args.prompt_len / prefill_s:.0f} tok/s, load {load_s:.1f} s")
+    del sess, s2, model
+    return out
+
+
 def ragged_batch(ctx, rd, args, model) -> dict:
     """E4B-shaped decode of several independent sequences with ragged prompt
     lengths (seeded uniform in [32, 2048]): each prompt is prefilled on its
@@ -550,6 +641,9 @@ def main() -> int:
     ap.add_argument("--no-e4b-cpu", action="store_true", help="skip the oracle's E4B decode/prefill CPU baseline")
     ap.add_argument("--no-checkpointed", action="store_true", help="skip the checkpointed (traced) decode")
     ap.add_argument("--no-ple", action="store_true", help="skip the E4B-shaped decode with per-layer inputs")
+    ap.add_argument("--no-i16", action="store_true", help="skip the i16-weight GEMV and E4B decode")
+    ap.add_argument("--i16-steps", type=int, default=128, help="greedy steps of the i16 E4B decode")
+    ap.add_argument("--i16-only", action="store_true", help="only the i16-weight GEMV and E4B decode")
     ap.add_argument("--cpu-e4b-runs", type=int, default=3, help="oracle E4B prefill+decode runs (medians)")
     ap.add_argument("--cpu-steps", type=int, default=4, help="oracle E4B decode steps per run")
     ap.add_argument("--cpu-prompt-1t", type=int, default=16, help="tokens of the one-thread oracle prefill")
@@ -582,6 +676,12 @@ def main() -> int:
         args.decode_steps = 32
         args.eager = True  # profiler kernel tracing of graph replays is not used
         print(json.dumps(e4b_decode(ctx, rd, args, *e4b_model(ctx, rd, args))), flush=True)
+        return 0
+    if args.i16_only:
+        out = {"i16_gemv": i16_gemv(ctx, rd, args)}
+        if not args.no_e4b:
+            out["e4b_i16"] = e4b_i16_decode(ctx, rd, args)
+        print(json.dumps(out), flush=True)
         return 0
     if args.ragged_only:
         model, _ = e4b_model(ctx, rd, args)
@@ -716,6 +816,10 @@ def main() -> int:
         del model
     if not args.no_e4b and not args.no_ple:
         line["e4b_ple"] = e4b_ple_decode(ctx, rd, args)
+    if not args.no_i16:
+        line["i16_gemv"] = i16_gemv(ctx, rd, args)
+        if not args.no_e4b:
+            line["e4b_i16"] = e4b_i16_decode(ctx, rd, args)
     print(json.dumps(line), flush=True)
     return 0 if parity else 1
 

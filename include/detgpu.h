@@ -83,14 +83,22 @@ void det_graph_destroy(det_graph_t* g);
 /* ------------------------------------------------------------------------ */
 /* Storage after upload (det_matrix_info): */
 #define DET_STORAGE_INT8 8   /* int8 q with per-row integer scale: W = q * s exactly */
-#define DET_STORAGE_I16 16   /* canonical Wgt bits stored as int16 (detwgt v2 i16) */
-#define DET_STORAGE_I32 32   /* canonical Wgt bits stored as int32 (detwgt v2 i32) */
+#define DET_STORAGE_I16 16   /* Wgt bits of int16 range (detwgt v2 i16) that do not factor */
+#define DET_STORAGE_I32 32   /* Wgt bits of int32 range (detwgt v2 i32) that do not factor */
 
 /* Uploads a rows x cols row-major weight matrix.
  *  elem_width 8 : `values` is int8 q, `row_scale` int32[rows] (W = q*s);
  *  elem_width 16/32 : `values` are detwgt v2 Wgt bits (row_scale ignored);
  *                     rows are stored as int8 x scale whenever that
- *                     factorization is exact for the whole matrix, else wide.
+ *                     factorization is exact for the whole matrix. Else
+ *                     each row is held as s * sum_p 256^p d_p with int8
+ *                     digits d_p (balanced, in [-128, 127]) and s = +1 or -1:
+ *                     two digit planes when every row fits them (i16 data
+ *                     without rows that hold values near both ends of the
+ *                     range), four otherwise. Every GEMV and GEMM then runs
+ *                     on the int8 MFMA path (the planes' products combine
+ *                     with shifts, exactly). Rows longer than 130000 columns
+ *                     are stored as the Wgt bits (vector-ALU path).
  * Rejects matrices whose max row mass sum_c |W[r][c]| >= 2^31
  * (det_num/mod.rs:39-42, gemma/io.rs:327-335). */
 int det_matrix_upload(det_ctx_t* ctx, uint64_t rows, uint64_t cols, int elem_width, const void* values,
@@ -430,6 +438,11 @@ int det_audit_trace(det_model_t* model, const det_trace_request_t* request, cons
  * s in [1, scale_max]. Host memory; multi-threaded. Same definition as
  * rasterdet.synthetic.fast_int8_matrix. */
 int det_synthetic_int8(uint64_t seed, uint64_t rows, uint64_t cols, int32_t scale_max, int8_t* q, int32_t* s);
+/* Counter-hash i16 Wgt bits uniform in [-lim, lim] that do not factor into
+ * int8 x scale (column 0 holds 1; every 7th row holds 32767 and rows 3 mod 11
+ * not among them hold -32768, at hashed columns): the benchmark's i16 model
+ * weights, multi-threaded. No reference counterpart (synthetic data). */
+int det_synthetic_i16(uint64_t seed, uint64_t rows, uint64_t cols, int32_t lim, int16_t* w);
 
 #ifdef __cplusplus
 }

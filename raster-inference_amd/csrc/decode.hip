@@ -45,7 +45,11 @@ __device__ __forceinline__ int32_t blk_rms_scale(int64_t ss, uint64_t n, int64_t
 }
 
 __device__ __forceinline__ int32_t wgt_bits(const DevMatrix& M, uint64_t r, uint64_t c) {
-  if (M.storage == kInt8) return int32_t(M.q[tiled_offset(M.kpad, r, c)]) * M.scale[r];
+  if (M.storage == kInt8) {
+    uint32_t v = 0;
+    for (int p = 0; p < M.planes; ++p) v += uint32_t(int32_t(M.q[tiled_offset(M.kpad, digit_row(r, M.planes, p), c)])) << (8 * p);
+    return int32_t(v * uint32_t(M.scale[r]));
+  }
   if (M.storage == kI16) return int32_t(static_cast<const int16_t*>(M.w)[r * M.cols + c]);
   return static_cast<const int32_t*>(M.w)[r * M.cols + c];
 }

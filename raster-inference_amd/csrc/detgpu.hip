@@ -259,35 +259,56 @@ void free_matrix(DevMatrix& m) {
   m = DevMatrix();
 }
 
-// Uploads int8 q (rows x cols) with per-row scales, padding rows to a multiple
-// of 128 bytes and computing the row sums used by the limb correction.
-DevMatrix upload_int8(det_ctx* ctx, uint64_t rows, uint64_t cols, const int8_t* q, const int32_t* scale) {
+// Uploads a digit-plane matrix: W[r][c] = scale[r] * sum_p 256^p d[p][r][c]
+// (d plane-major [planes][rows][cols]) in the tile-major layout, each tile's
+// planes consecutive (virtual rows digit_row(r, planes, p)), rows padded to a
+// multiple of 16 and columns to kpad, with the row sums (of sum_p 256^p d_p)
+// used by the limb correction, whole and per column part.
+DevMatrix upload_digits(det_ctx* ctx, uint64_t rows, uint64_t cols, int planes, const int8_t* d,
+                        const int32_t* scale) {
   if (cols > 130000) bail("int8 rows longer than 130000 columns are not supported");
   DevMatrix m;
   m.rows = rows;
   m.cols = cols;
   m.storage = det::kInt8;
+  m.planes = planes;
   m.kpad = round_up(std::max<uint64_t>(cols, 1), 128);
   const uint64_t prow = round_up(std::max<uint64_t>(rows, 1), 16);
-  std::vector<int8_t> tiled(prow * m.kpad, 0);
+  std::vector<int8_t> tiled(prow * uint64_t(planes) * m.kpad, 0);
   const uint64_t nparts = det::limb_parts(m.kpad);
   std::vector<int32_t> rowsum(prow, 0), sc(prow, 0), rowsum_p(prow * nparts, 0);
+  bool sums_fit = true;
+  std::mutex mu;
   parallel_rows(rows, [&](uint64_t r0, uint64_t r1) {
+    bool fit = true;
     for (uint64_t r = r0; r < r1; ++r) {
-      int32_t s = 0;
+      int64_t s = 0;
       // (16 columns at a time: the run of one row that is contiguous in the tile-step)
       for (uint64_t c0 = 0; c0 < cols; c0 += 16) {
         const uint64_t n = std::min<uint64_t>(16, cols - c0);
-        std::memcpy(&tiled[det::tiled_offset(m.kpad, r, c0)], q + r * cols + c0, n);
-        int32_t sp = 0;
-        for (uint64_t c = c0; c < c0 + n; ++c) sp += q[r * cols + c];
+        int64_t sp = 0;
+        for (int p = 0; p < planes; ++p) {
+          const int8_t* src = d + (uint64_t(p) * rows + r) * cols + c0;
+          std::memcpy(&tiled[det::tiled_offset(m.kpad, det::digit_row(r, planes, p), c0)], src, n);
+          int64_t dp = 0;
+          for (uint64_t c = 0; c < n; ++c) dp += src[c];
+          sp += dp * (int64_t(1) << (8 * p));
+        }
         s += sp;
-        rowsum_p[(c0 / det::kLimbPartCols) * prow + r] += sp;
+        const int64_t acc = int64_t(rowsum_p[(c0 / det::kLimbPartCols) * prow + r]) + sp;
+        fit &= acc >= INT32_MIN && acc <= INT32_MAX;
+        rowsum_p[(c0 / det::kLimbPartCols) * prow + r] = int32_t(acc);
       }
-      rowsum[r] = s;
+      fit &= s >= INT32_MIN && s <= INT32_MAX;
+      rowsum[r] = int32_t(s);
       sc[r] = scale[r];
     }
+    if (!fit) {
+      std::lock_guard<std::mutex> lock(mu);
+      sums_fit = false;
+    }
   });
+  if (!sums_fit) bail("weight row mass violates the 2^31 overflow bound");
   HIPC(hipMalloc(&m.q, tiled.size()));
   HIPC(hipMalloc(&m.scale, prow * 4));
   HIPC(hipMalloc(&m.rowsum, prow * 4));
@@ -302,21 +323,66 @@ DevMatrix upload_int8(det_ctx* ctx, uint64_t rows, uint64_t cols, const int8_t* 
   return m;
 }
 
+// Uploads int8 q (rows x cols) with per-row scales: one digit plane.
+DevMatrix upload_int8(det_ctx* ctx, uint64_t rows, uint64_t cols, const int8_t* q, const int32_t* scale) {
+  return upload_digits(ctx, rows, cols, 1, q, scale);
+}
+
+// A digit-plane matrix on the host: d plane-major [planes][rows][cols].
+struct HostDigits {
+  uint64_t rows = 0, cols = 0;
+  int planes = 1;
+  std::vector<int8_t> d;
+  std::vector<int32_t> scale;
+};
+
+// Downloads a digit-plane matrix back to row-major planes + scales.
+HostDigits untile(det_ctx* ctx, const DevMatrix& M) {
+  HostDigits h;
+  h.rows = M.rows;
+  h.cols = M.cols;
+  h.planes = M.planes;
+  const uint64_t prow = round_up(std::max<uint64_t>(M.rows, 1), 16);
+  std::vector<int8_t> tiled(prow * uint64_t(M.planes) * M.kpad);
+  HIPC(hipMemcpy(tiled.data(), M.q, tiled.size(), hipMemcpyDeviceToHost));
+  h.scale.resize(M.rows);
+  HIPC(hipMemcpy(h.scale.data(), M.scale, M.rows * 4, hipMemcpyDeviceToHost));
+  h.d.resize(uint64_t(M.planes) * M.rows * M.cols);
+  parallel_rows(M.rows, [&](uint64_t r0, uint64_t r1) {
+    for (uint64_t r = r0; r < r1; ++r)
+      for (int p = 0; p < M.planes; ++p)
+        for (uint64_t c0 = 0; c0 < M.cols; c0 += 16)
+          std::memcpy(&h.d[(uint64_t(p) * M.rows + r) * M.cols + c0],
+                      &tiled[det::tiled_offset(M.kpad, det::digit_row(r, M.planes, p), c0)],
+                      std::min<uint64_t>(16, M.cols - c0));
+  });
+  return h;
+}
+
 // Copies rows [r0, r0+n) of a device matrix into a new matrix (host round trip;
 // load time only). Used for row slices that are not tile aligned.
 DevMatrix extract_rows(det_ctx* ctx, const DevMatrix& src, uint64_t r0, uint64_t n) {
   if (r0 + n > src.rows) bail("matrix row slice out of bounds");
   if (src.storage != det::kInt8) return det::row_view(src, r0, n);
   if (r0 % 16 == 0) return det::row_view(src, r0, n);
-  const uint64_t prow = round_up(src.rows, 16);
-  std::vector<int8_t> tiled(prow * src.kpad);
-  std::vector<int32_t> sc(prow);
-  HIPC(hipMemcpy(tiled.data(), src.q, tiled.size(), hipMemcpyDeviceToHost));
-  HIPC(hipMemcpy(sc.data(), src.scale, prow * 4, hipMemcpyDeviceToHost));
-  std::vector<int8_t> q(n * src.cols);
-  for (uint64_t r = 0; r < n; ++r)
-    for (uint64_t c = 0; c < src.cols; ++c) q[r * src.cols + c] = tiled[det::tiled_offset(src.kpad, r0 + r, c)];
-  return upload_int8(ctx, n, src.cols, q.data(), sc.data() + r0);
+  const HostDigits h = untile(ctx, src);
+  std::vector<int8_t> d(uint64_t(h.planes) * n * h.cols);
+  for (int p = 0; p < h.planes; ++p)
+    std::memcpy(&d[uint64_t(p) * n * h.cols], &h.d[(uint64_t(p) * h.rows + r0) * h.cols], n * h.cols);
+  DevMatrix m = upload_digits(ctx, n, src.cols, h.planes, d.data(), h.scale.data() + r0);
+  m.value_width = src.value_width;
+  return m;
+}
+
+// Balanced base-256 digits of v, each in [-128, 127]: false when v needs
+// more than `planes` of them.
+bool balanced_digits(int64_t v, int planes, int8_t* d) {
+  for (int p = 0; p < planes; ++p) {
+    const int64_t lo = ((v + 128) & 255) - 128;
+    d[p] = int8_t(lo);
+    v = (v - lo) / 256;
+  }
+  return v == 0;
 }
 
 // Row mass bound (det_num/mod.rs:39-42).
@@ -353,34 +419,86 @@ DevMatrix upload_matrix(det_ctx* ctx, uint64_t rows, uint64_t cols, int width, c
   // every |q| <= 127. Products q*s reproduce the Wgt bits exactly.
   std::vector<int32_t> scale(rows, 1);
   std::vector<int64_t> mass(rows, 0);
-  bool factor = true;
-  for (uint64_t r = 0; r < rows; ++r) {
-    uint64_t g = 0, mx = 0;
-    int64_t ms = 0;
-    for (uint64_t c = 0; c < cols; ++c) {
-      const uint64_t a = uint64_t(std::abs(int64_t(at(r * cols + c))));
-      g = std::gcd(g, a);
-      mx = std::max(mx, a);
-      ms += int64_t(a);
+  std::vector<uint8_t> row_factors(rows, 1), row_fits16(rows, 1);
+  parallel_rows(rows, [&](uint64_t r0, uint64_t r1) {
+    for (uint64_t r = r0; r < r1; ++r) {
+      uint64_t g = 0, mx = 0;
+      int64_t ms = 0;
+      bool f16 = true;
+      for (uint64_t c = 0; c < cols; ++c) {
+        const int32_t v = at(r * cols + c);
+        const uint64_t a = uint64_t(std::abs(int64_t(v)));
+        g = std::gcd(g, a);
+        mx = std::max(mx, a);
+        ms += int64_t(a);
+        f16 &= v >= INT16_MIN && v <= INT16_MAX;
+      }
+      mass[r] = ms;
+      if (g == 0) g = 1;
+      row_factors[r] = mx / g <= 127;
+      row_fits16[r] = f16;
+      scale[r] = int32_t(g);
     }
-    mass[r] = ms;
-    if (g == 0) g = 1;
-    if (mx / g > 127) factor = false;
-    scale[r] = int32_t(g);
-  }
+  });
   check_row_mass(rows, cols, mass);
+  const bool factor = std::all_of(row_factors.begin(), row_factors.end(), [](uint8_t b) { return b != 0; });
   if (factor) {
     std::vector<int8_t> q(rows * cols);
-    for (uint64_t r = 0; r < rows; ++r)
-      for (uint64_t c = 0; c < cols; ++c) q[r * cols + c] = int8_t(at(r * cols + c) / scale[r]);
+    parallel_rows(rows, [&](uint64_t r0, uint64_t r1) {
+      for (uint64_t r = r0; r < r1; ++r)
+        for (uint64_t c = 0; c < cols; ++c) q[r * cols + c] = int8_t(at(r * cols + c) / scale[r]);
+    });
     return upload_int8(ctx, rows, cols, q.data(), scale.data());
   }
+  const bool fits16 = std::all_of(row_fits16.begin(), row_fits16.end(), [](uint8_t b) { return b != 0; });
+  if (cols <= 130000) {
+    // Digit planes on the int8 MFMA path: each row as s * sum_p 256^p d_p
+    // with balanced digits and s = +1 or -1 (whichever sign the row's values
+    // fit). Two planes hold every i16 row unless it has values near both
+    // ends of the range; four hold every i32 row within the row-mass bound.
+    // The products s * (digits) are the Wgt bits exactly.
+    for (int planes : {2, 4}) {
+      if (planes == 2 && !fits16) continue;
+      std::vector<int8_t> d(uint64_t(planes) * rows * cols);
+      std::vector<int32_t> sgn(rows, 1);
+      bool ok = true;
+      std::mutex mu;
+      parallel_rows(rows, [&](uint64_t r0, uint64_t r1) {
+        bool all = true;
+        int8_t dg[4];
+        for (uint64_t r = r0; r < r1 && all; ++r) {
+          bool row_ok = false;
+          for (int32_t sign : {1, -1}) {
+            row_ok = true;
+            for (uint64_t c = 0; c < cols && row_ok; ++c) {
+              row_ok = balanced_digits(int64_t(sign) * at(r * cols + c), planes, dg);
+              for (int p = 0; p < planes && row_ok; ++p) d[(uint64_t(p) * rows + r) * cols + c] = dg[p];
+            }
+            if (row_ok) {
+              sgn[r] = sign;
+              break;
+            }
+          }
+          all = row_ok;
+        }
+        if (!all) {
+          std::lock_guard<std::mutex> lock(mu);
+          ok = false;
+        }
+      });
+      if (!ok) continue;
+      DevMatrix m = upload_digits(ctx, rows, cols, planes, d.data(), sgn.data());
+      m.value_width = fits16 ? 16 : 32;
+      return m;
+    }
+    contract("weight row fits no digit-plane form");
+  }
+  // rows longer than the MFMA path takes: wide storage on the vector ALUs
   DevMatrix m;
   m.rows = rows;
   m.cols = cols;
-  bool fits16 = true;
-  for (uint64_t i = 0; i < rows * cols && fits16; ++i) fits16 = at(i) >= INT16_MIN && at(i) <= INT16_MAX;
   m.storage = fits16 ? det::kI16 : det::kI32;
+  m.value_width = fits16 ? 16 : 32;
   const size_t esz = fits16 ? 2 : 4;
   HIPC(hipMalloc(&m.w, std::max<size_t>(rows * cols * esz, 4)));
   if ((width == 16) == fits16) {
@@ -526,39 +644,30 @@ struct det_model {
 
 namespace {
 
-// Downloads a tile-major int8 matrix back to row-major q + scales.
-void untile(det_ctx* ctx, const DevMatrix& M, std::vector<int8_t>& q, std::vector<int32_t>& sc) {
-  const uint64_t prow = round_up(std::max<uint64_t>(M.rows, 1), 16);
-  std::vector<int8_t> tiled(prow * M.kpad);
-  HIPC(hipMemcpy(tiled.data(), M.q, tiled.size(), hipMemcpyDeviceToHost));
-  sc.resize(M.rows);
-  HIPC(hipMemcpy(sc.data(), M.scale, M.rows * 4, hipMemcpyDeviceToHost));
-  q.resize(M.rows * M.cols);
-  parallel_rows(M.rows, [&](uint64_t r0, uint64_t r1) {
-    for (uint64_t r = r0; r < r1; ++r)
-      for (uint64_t c0 = 0; c0 < M.cols; c0 += 16)
-        std::memcpy(&q[r * M.cols + c0], &tiled[det::tiled_offset(M.kpad, r, c0)], std::min<uint64_t>(16, M.cols - c0));
-  });
-}
-
-// Stacks int8 matrices of equal width row-wise; with interleave8 (two inputs
-// of equal height) rows alternate in blocks of 8: a[0..8), b[0..8), a[8..16), ...
+// Stacks digit-plane matrices of equal width row-wise (the result takes the
+// largest plane count; a row with fewer planes gets zero digits above its
+// own); with interleave8 (two inputs of equal height) rows alternate in
+// blocks of 8: a[0..8), b[0..8), a[8..16), ...
 DevMatrix fuse_rows(det_ctx* ctx, const std::vector<const DevMatrix*>& ms, bool interleave8) {
   const uint64_t cols = ms[0]->cols;
   uint64_t rows = 0;
-  std::vector<std::vector<int8_t>> qs(ms.size());
-  std::vector<std::vector<int32_t>> ss(ms.size());
-  for (size_t i = 0; i < ms.size(); ++i) {
-    if (ms[i]->cols != cols || ms[i]->storage != det::kInt8) bail("cannot fuse matrices of different widths");
-    untile(ctx, *ms[i], qs[i], ss[i]);
-    rows += ms[i]->rows;
+  int planes = 1, vw = 8;
+  std::vector<HostDigits> hs;
+  for (const DevMatrix* m : ms) {
+    if (m->cols != cols || m->storage != det::kInt8) bail("cannot fuse matrices of different widths");
+    hs.push_back(untile(ctx, *m));
+    rows += m->rows;
+    planes = std::max(planes, m->planes);
+    vw = std::max(vw, m->value_width);
   }
-  std::vector<int8_t> q(rows * cols);
+  std::vector<int8_t> d(uint64_t(planes) * rows * cols, 0);
   std::vector<int32_t> sc(rows);
   uint64_t r = 0;
   auto put = [&](size_t i, uint64_t src_row) {
-    std::memcpy(&q[r * cols], &qs[i][src_row * cols], cols);
-    sc[r] = ss[i][src_row];
+    const HostDigits& h = hs[i];
+    for (int p = 0; p < h.planes; ++p)
+      std::memcpy(&d[(uint64_t(p) * rows + r) * cols], &h.d[(uint64_t(p) * h.rows + src_row) * cols], cols);
+    sc[r] = h.scale[src_row];
     ++r;
   };
   if (interleave8) {
@@ -570,7 +679,9 @@ DevMatrix fuse_rows(det_ctx* ctx, const std::vector<const DevMatrix*>& ms, bool 
     for (size_t i = 0; i < ms.size(); ++i)
       for (uint64_t j = 0; j < ms[i]->rows; ++j) put(i, j);
   }
-  return upload_int8(ctx, rows, cols, q.data(), sc.data());
+  DevMatrix m = upload_digits(ctx, rows, cols, planes, d.data(), sc.data());
+  m.value_width = vw;
+  return m;
 }
 
 // gemma/io.rs:165-190
@@ -1175,7 +1286,7 @@ bool qkv_block(det_session* s, const GLayer& L, uint64_t M, uint64_t pos0, const
   const det_model* m = s->m;
   const size_t li = size_t(&L - m->layers.data());
   const det::DevMatrix* QKV = (m->fused_ok && li < m->fused.size()) ? &m->fused[li].qkv : nullptr;
-  if (L.v && QKV && M >= det_ctx::kGemmMinRows && QKV->storage == det::kInt8 && QKV->rows == qw + 2 * kw &&
+  if (L.v && QKV && M >= det_ctx::kGemmMinRows && QKV->storage == det::kInt8 && QKV->planes <= 2 && QKV->rows == qw + 2 * kw &&
       L.q->rows == qw && L.k->rows == kw && L.v->rows == kw && qw % 16 == 0 && kw % 16 == 0) {
     ctx->ensure_gemm_a(det::gemm_act_bytes(M, QKV->kpad));
     det::launch_gemm_limbs(s->normed, M, QKV->cols, L.q->cols, QKV->kpad, ctx->gemm_a, st);
@@ -1262,7 +1373,7 @@ bool post_attention(det_session* s, const GLayer& L, uint64_t M, const int32_t* 
   const det_model* m = s->m;
   const size_t li = size_t(&L - m->layers.data());
   const det::DevMatrix* GU = (m->fused_ok && li < m->fused.size()) ? &m->fused[li].gateup : nullptr;
-  if (GU && M >= det_ctx::kGemmMinRows && GU->storage == det::kInt8 && GU->rows == 2 * L.gate->rows &&
+  if (GU && M >= det_ctx::kGemmMinRows && GU->storage == det::kInt8 && GU->planes <= 2 && GU->rows == 2 * L.gate->rows &&
       GU->cols == H && L.gate->rows % 8 == 0) {
     ctx->ensure_gemm_a(det::gemm_act_bytes(M, GU->kpad));
     det::launch_gemm_limbs(s->normed, M, H, H, GU->kpad, ctx->gemm_a, st);
@@ -3003,7 +3114,8 @@ int det_matrix_info(const det_matrix_t* m, uint64_t* rows, uint64_t* cols, int* 
   if (!m) return 1;
   if (rows) *rows = m->m.rows;
   if (cols) *cols = m->m.cols;
-  if (storage) *storage = m->m.storage;
+  // int8 x scale, or the width class of values held as digit planes / wide
+  if (storage) *storage = m->m.storage == det::kInt8 && m->m.planes == 1 ? det::kInt8 : m->m.value_width;
   return 0;
 }
 void det_matrix_free(det_matrix_t* m) {
@@ -3244,6 +3356,33 @@ int det_synthetic_int8(uint64_t seed, uint64_t rows, uint64_t cols, int32_t scal
       const uint64_t h = synth_mix(sbase + r / 2);
       const uint32_t u = uint32_t(h >> (32 * (r & 1)));
       s[r] = int32_t(u % uint32_t(scale_max)) + 1;
+    }
+  });
+}
+
+int det_synthetic_i16(uint64_t seed, uint64_t rows, uint64_t cols, int32_t lim, int16_t* w) {
+  return guarded(nullptr, [&] {
+    if (lim < 1 || lim > 32767) bail("lim must be in [1, 32767]");
+    const uint64_t base = seed * 0x9E3779B97F4A7C15ull;
+    const uint64_t n = rows * cols;
+    const uint32_t span = uint32_t(2 * lim + 1);
+    parallel_rows((n + 3) / 4, [&](uint64_t w0, uint64_t w1) {
+      for (uint64_t u = w0; u < w1; ++u) {
+        const uint64_t h = synth_mix(base + u);
+        for (int k = 0; k < 4 && u * 4 + k < n; ++k)
+          w[u * 4 + k] = int16_t(int32_t(uint32_t(uint16_t(h >> (16 * k))) % span) - lim);
+      }
+    });
+    for (uint64_t r = 0; r < rows; ++r) w[r * cols] = 1;
+    if (cols > 1) {
+      const uint64_t cbase = (seed ^ 0xE7ull) * 0x9E3779B97F4A7C15ull;
+      for (uint64_t r = 0; r < rows; ++r) {
+        const bool hi = r % 7 == 0, lo = r % 11 == 3 && !hi;
+        if (!hi && !lo) continue;
+        const uint32_t u = uint32_t(synth_mix(cbase + r / 2) >> (32 * (r & 1)));
+        const uint64_t c = u % uint32_t(cols - 1) + 1;
+        w[r * cols + c] = hi ? int16_t(32767) : int16_t(-32768);
+      }
     }
   });
 }

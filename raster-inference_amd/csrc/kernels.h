@@ -26,6 +26,16 @@ struct DevMatrix {
   // rowsum_p[p * rowsum_p_ld + r]
   int32_t* rowsum_p = nullptr;
   uint64_t rowsum_p_ld = 0;
+  // Digit planes: W[r][c] = scale[r] * sum_p 256^p d_p[r][c] with int8
+  // digits d_p (planes = 1: the int8 form above). Plane p of tile t is the
+  // virtual tile t * planes + p in the tile-major layout (each tile's planes
+  // are consecutive, every plane kpad/128 tile-steps), so kernels read a
+  // planes-digit matrix as an int8 matrix of planes * 16 rows per tile and
+  // combine a row's planes with shifts of 8 p bits. rowsum is the row sum of
+  // sum_p 256^p d_p (within int32 by the row-mass bound).
+  int planes = 1;
+  // width class of the uploaded values (8: factored int8 x scale, 16, 32)
+  int value_width = 8;
   // wide form: w[rows][cols] as int16 or int32 Wgt bits.
   void* w = nullptr;
   bool owns = true;  // false for row-range views
@@ -50,6 +60,10 @@ constexpr uint64_t kTileHalfBytes = 1024;
 __host__ __device__ inline uint64_t tiled_offset(uint64_t kpad, uint64_t r, uint64_t c) {
   const uint64_t tile = r >> 4, i = r & 15, step = c >> 7, g = (c >> 5) & 3, h = (c >> 4) & 1, b = c & 15;
   return (tile * (kpad >> 7) + step) * 2048 + h * kTileHalfBytes + (g * 16 + i) * 16 + b;
+}
+// The virtual row of digit plane p of row r in a planes-digit matrix.
+__host__ __device__ inline uint64_t digit_row(uint64_t r, int planes, int p) {
+  return (((r >> 4) * uint64_t(planes) + uint64_t(p)) << 4) | (r & 15);
 }
 
 // Activation limb planes for the int8 path: for each token row, four int8

@@ -80,13 +80,15 @@ __global__ void k_act_limbs(const int32_t* __restrict__ act, uint64_t m, uint64_
 // limb row i = 4*token + limb (A operand). The 16x16 i32 result tile puts all
 // four limb sums of (token g, row i) in the four accumulator registers of
 // lane l, so the combine is lane-local.
+// planes > 1 (a digit-plane matrix, planes dividing NW): NW / planes waves
+// per plane split K; wave 0 combines the planes' partial tiles with shifts.
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ q,
                                                     const int32_t* __restrict__ scale,
                                                     const int32_t* __restrict__ rowsum,
                                                     const int8_t* __restrict__ limbs, uint64_t n_rows,
                                                     uint64_t kpad, uint32_t m, int32_t* __restrict__ out,
-                                                    uint64_t ld_out, int64_t* __restrict__ acc_out) {
+                                                    uint64_t ld_out, int64_t* __restrict__ acc_out, int planes) {
   __shared__ v4i part[NW][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
@@ -95,10 +97,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
   const bool a_on = uint32_t(at) < m;
   const bool b_on = row < n_rows;
   const uint64_t nsteps = kpad / 128;
-  const uint64_t per = (nsteps + NW - 1) / NW;
-  const uint64_t s0 = wave * per;
+  const int wpp = NW / planes, plane = wave / wpp, pw = wave % wpp;
+  const uint64_t per = (nsteps + wpp - 1) / wpp;
+  const uint64_t s0 = pw * per < nsteps ? pw * per : nsteps;
   const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
-  const v4i* bp = reinterpret_cast<const v4i*>(q + uint64_t(blockIdx.x) * nsteps * 2048 + lane * 16);
+  const v4i* bp = reinterpret_cast<const v4i*>(
+      q + (uint64_t(blockIdx.x) * planes + plane) * nsteps * 2048 + lane * 16);
   const v4i* ap = reinterpret_cast<const v4i*>(limbs + (a_on ? (uint64_t(at) * 4 + aj) : 0) * kpad + 32 * g);
   const v4i zero = {0, 0, 0, 0};
   v4i acc = zero;
@@ -131,7 +135,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     const v4i v = part[w][lane];
-    p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+    const int sh = 8 * (w / wpp);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
   }
   if (uint32_t(g) >= m || !b_on) return;
   const int64_t dot = p[0] + p[1] * 256 + p[2] * 65536 + p[3] * 16777216 + int64_t(8421504) * rowsum[row];
@@ -164,15 +170,19 @@ __device__ __forceinline__ int64_t limb_combine(const int64_t p[4], int32_t rows
 // b % kchunks): each adds its wrapping share of the Q32.32 accumulator to
 // acc_out atomically (the sum over chunks is the accumulator exactly, since
 // the row scale distributes over wrapping sums); acc_out starts at zero.
+// A digit-plane matrix (KSPLIT * planes <= 8) gives each of a tile's planes
+// KSPLIT waves; the tile's KSPLIT * planes partial tiles combine through LDS
+// with shifts of 8 bits per plane.
 template <int KSPLIT, bool IN64, int EPI>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const void* __restrict__ act_v, uint64_t ld_act, uint64_t k, uint64_t n_rows, uint64_t kpad, uint32_t m,
     int32_t* __restrict__ out, uint64_t ld_out, int64_t* __restrict__ acc_out, uint32_t kchunks,
-    const int32_t* __restrict__ mulv) {
+    const int32_t* __restrict__ mulv, int planes) {
   extern __shared__ __attribute__((aligned(16))) int8_t lds_limbs[];
-  __shared__ v4i part[KSPLIT > 1 ? 8 : 1][64];
-  constexpr int TPW = 8 / KSPLIT;
+  __shared__ v4i part[8][64];
+  const int S = KSPLIT * planes;  // waves per tile
+  const int TPW = 8 / S;
   const uint64_t nsteps = kpad / 128;
   const uint32_t kc = blockIdx.x % kchunks;
   const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
@@ -208,7 +218,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
-  const int slot = wave / KSPLIT, kp = wave % KSPLIT;
+  const int slot = wave / S, within = wave % S, plane = within / KSPLIT, kp = within % KSPLIT;
   const int at = i >> 2, aj = i & 3;
   const bool a_on = uint32_t(at) < m;
   // LDS column (s - cs0) * 128 of this lane's limb plane
@@ -222,9 +232,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
   for (uint64_t base = uint64_t(blockIdx.x / kchunks) * TPW; base < ntiles; base += groups * TPW) {
     const uint64_t tile = base + slot;
     const uint64_t row = tile * 16 + i;
-    const bool t_on = tile < ntiles;
+    const bool t_on = tile < ntiles && slot < TPW;
     const bool b_on = t_on && row < n_rows;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 16);
+    const v4i* bp = reinterpret_cast<const v4i*>(q + ((t_on ? tile : 0) * planes + plane) * nsteps * 2048 + lane * 16);
     v4i acc = zero;
     uint64_t s = s0;
     for (; s + 4 <= s1; s += 4) {
@@ -251,19 +261,20 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
       acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
     }
     int64_t p[4] = {acc[0], acc[1], acc[2], acc[3]};
-    if (KSPLIT > 1) {
+    if (S > 1) {
       part[wave][lane] = acc;
       __syncthreads();
-      if (kp == 0) {
-#pragma unroll
-        for (int w = 1; w < KSPLIT; ++w) {
+      if (within == 0) {
+        for (int w = 1; w < S; ++w) {
           const v4i v = part[wave + w][lane];
-          p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+          const int sh = 8 * (w / KSPLIT);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
         }
       }
       __syncthreads();
     }
-    if (kp == 0) {
+    if (within == 0) {
       const bool ok = uint32_t(g) < m && b_on;
       if (kchunks > 1) {
         if (ok) {
@@ -299,11 +310,14 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
 // IN64: the activation row is a wrapped Q32.32 accumulator row, requantized
 // on load.
 constexpr int kTileD = 5;
+// A digit-plane matrix (planes dividing NW) gives NW / planes waves to each
+// plane; the partial tiles combine with shifts of 8 bits per plane.
 template <int NW, bool IN64>
 __global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict__ q, const int32_t* __restrict__ scale,
                                                        const int32_t* __restrict__ rowsum, const void* __restrict__ act_v,
                                                        uint64_t k, uint64_t n_rows, uint64_t kpad,
-                                                       int32_t* __restrict__ out, int64_t* __restrict__ acc_out) {
+                                                       int32_t* __restrict__ out, int64_t* __restrict__ acc_out,
+                                                       int planes) {
   constexpr int D = kTileD;
   constexpr int kPass = (D * 32 + 63) / 64;             // activation quads per lane and batch
   constexpr uint32_t kPlane = kPass * 256 + 32;          // limb plane stride of a wave slice
@@ -313,10 +327,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict_
   const int g = lane >> 4, i = lane & 15;
   const uint64_t tile = blockIdx.x;
   const uint64_t nsteps = kpad / 128;
-  const uint64_t per = (nsteps + NW - 1) / NW;
-  const uint64_t s0 = uint64_t(wave) * per < nsteps ? uint64_t(wave) * per : nsteps;
+  const int wpp = NW / planes, plane = wave / wpp, pw = wave % wpp;
+  const uint64_t per = (nsteps + wpp - 1) / wpp;
+  const uint64_t s0 = uint64_t(pw) * per < nsteps ? uint64_t(pw) * per : nsteps;
   const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
-  const v4i* bp = reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 16);
+  const v4i* bp = reinterpret_cast<const v4i*>(q + (tile * planes + plane) * nsteps * 2048 + lane * 16);
   const bool a_on = i < 4;  // A row i = limb i of the one token
   const uint8_t* aread = al[wave] + (i & 3) * kPlane + 32 * g;
   const v4i zero = {0, 0, 0, 0};
@@ -391,7 +406,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict_
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     const v4i v = reinterpret_cast<const v4i*>(al[w])[lane];
-    p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+    const int sh = 8 * (w / wpp);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
   }
   const uint64_t row = tile * 16 + i;
   if (row >= n_rows) return;
@@ -418,16 +435,17 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
     int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
-    int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
-  __shared__ v4i part[KS > 1 ? 4 : 1][NG][64];
-  constexpr int TPW = 4 / KS;
+    int8_t* __restrict__ out_limbs, uint64_t out_kpad, int planes) {
+  __shared__ v4i part[4][NG][64];
+  const int S = KS * planes;  // waves per tile (digit planes x K shares)
+  const int TPW = 4 / S;
   // K steps per load batch: three for one token group (a wave's 5-step share
   // of K 2560 split four ways takes two load round trips either way), two when
   // the A tiles of several groups share the registers
   constexpr int D = NG == 1 ? 3 : 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
-  const int slot = wave / KS, kp = wave % KS;
+  const int slot = wave / S, within = wave % S, plane = within / KS, kp = within % KS;
   const uint64_t nsteps = kpad / 128;
   const uint32_t kc = blockIdx.x % kchunks;
   const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
@@ -450,7 +468,7 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
     const uint64_t tile = base + slot;
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 16);
+    const v4i* bp = reinterpret_cast<const v4i*>(q + ((t_on ? tile : 0) * planes + plane) * nsteps * 2048 + lane * 16);
     v4i acc[NG];
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
@@ -488,22 +506,24 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
     for (int tg = 0; tg < NG; ++tg)
 #pragma unroll
       for (int e = 0; e < 4; ++e) p[tg][e] = acc[tg][e];
-    if (KS > 1) {
+    if (S > 1) {
 #pragma unroll
       for (int tg = 0; tg < NG; ++tg) part[wave][tg][lane] = acc[tg];
       __syncthreads();
-      if (kp == 0) {
-#pragma unroll
-        for (int w = 1; w < KS; ++w)
+      if (within == 0) {
+        for (int w = 1; w < S; ++w) {
+          const int sh = 8 * (w / KS);
 #pragma unroll
           for (int tg = 0; tg < NG; ++tg) {
             const v4i v = part[wave + w][tg][lane];
-            p[tg][0] += v[0]; p[tg][1] += v[1]; p[tg][2] += v[2]; p[tg][3] += v[3];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[tg][j] += int64_t(uint64_t(int64_t(v[j])) << sh);
           }
+        }
       }
       __syncthreads();
     }
-    if (kp != 0 || !t_on) continue;
+    if (within != 0 || !t_on) continue;
     const bool r_on = row < n_rows;
     const int32_t rs = r_on ? rowsum[row] : 0, sc = r_on ? scale[row] : 0;
     // lane 16 g + i of group tg holds the limb sums of token 4 tg + g, row i
@@ -548,17 +568,18 @@ template <int KS, int EPI>
 __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, int32_t* __restrict__ out,
-    int64_t* __restrict__ acc_out, int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
+    int64_t* __restrict__ acc_out, int8_t* __restrict__ out_limbs, uint64_t out_kpad, int planes) {
   constexpr int D = 5;
   constexpr int kCopies = (4 * D * 128 + 1023) / 1024;  // 1 KB wave copies of 4 planes x D steps
   __shared__ __attribute__((aligned(16))) int8_t al[4][kCopies * 1024];
-  __shared__ v4i part[KS > 1 ? 4 : 1][64];
-  constexpr int TPW = 4 / KS;
+  __shared__ v4i part[4][64];
+  const int S = KS * planes;  // waves per tile (digit planes x K shares)
+  const int TPW = 4 / S;
   constexpr int kWaitLds = 15 | (7 << 4) | (0 << 8) | (3 << 14);  // lgkmcnt(0)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, i = lane & 15;
-  const int slot = wave / KS, kp = wave % KS;
+  const int slot = wave / S, within = wave % S, plane = within / KS, kp = within % KS;
   const uint64_t nsteps = kpad / 128;
   const uint32_t kc = blockIdx.x % kchunks;
   const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
@@ -577,7 +598,8 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
     const uint64_t tile = base + slot;
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : ntiles - 1) * nsteps * 2048 + lane * 16);
+    const v4i* bp = reinterpret_cast<const v4i*>(q + ((t_on ? tile : ntiles - 1) * planes + plane) * nsteps * 2048 +
+                                                 lane * 16);
     v4i acc = zero;
     for (uint64_t sb = s0; sb < s1; sb += D) {
       const uint64_t nu = s1 - sb < uint64_t(D) ? s1 - sb : uint64_t(D);
@@ -625,19 +647,20 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
       }
     }
     int64_t p[4] = {acc[0], acc[1], acc[2], acc[3]};
-    if (KS > 1) {
+    if (S > 1) {
       part[wave][lane] = acc;
       __syncthreads();
-      if (kp == 0) {
-#pragma unroll
-        for (int w = 1; w < KS; ++w) {
+      if (within == 0) {
+        for (int w = 1; w < S; ++w) {
           const v4i v = part[wave + w][lane];
-          p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+          const int sh = 8 * (w / KS);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
         }
       }
       __syncthreads();
     }
-    if (kp != 0 || !t_on) continue;
+    if (within != 0 || !t_on) continue;
     const bool r_on = row < n_rows;
     const int32_t rs = r_on ? rowsum[row] : 0, sc = r_on ? scale[row] : 0;
     // lanes 0-15 (g = 0) hold the token's four limb sums of row i
@@ -717,7 +740,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
                                                        const int32_t* __restrict__ rowsum, uint64_t n_rows,
                                                        uint64_t kpad, int64_t* __restrict__ acc_out,
                                                        int32_t* __restrict__ out, int8_t* __restrict__ out_limbs,
-                                                       uint64_t out_kpad) {
+                                                       uint64_t out_kpad, int planes) {
   constexpr int NT = 64 * NW, D = kNormD;
   constexpr uint32_t kPlaneMax = kNormMaxK + 32;
   typedef long long v2l __attribute__((ext_vector_type(2)));
@@ -728,9 +751,10 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, i = lane & 15;
-  const uint64_t nsteps = kpad / 128, np = (nsteps + D - 1) / D;
+  // a tile's jobs: its digit planes x K parts of D steps (job pp: plane pp / np)
+  const uint64_t nsteps = kpad / 128, np = (nsteps + D - 1) / D, npt = np * uint64_t(planes);
   const uint64_t ntiles = (n_rows + 15) / 16, G = gridDim.x;
-  const uint64_t tpw = (ntiles + G - 1) / G, njobs = tpw * np;
+  const uint64_t tpw = (ntiles + G - 1) / G, njobs = tpw * npt;
   const uint64_t plane = kpad + 32;  // limb plane stride in LDS (planes start 8 banks apart)
   const uint64_t Q = ni.H / 4;      // activation quads (H % 4 == 0, H <= 4 NT QPT)
   // 1. the norm's inputs, quad qd = tid + NT e (clamped addresses, masked
@@ -769,12 +793,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
 #pragma unroll
     for (int u = u0; u < u1; ++u) {
       const uint64_t jb = uint64_t(wave) + uint64_t(NW) * u;
-      const uint64_t tl = jb / np, p = jb % np;
+      const uint64_t tl = jb / npt, pl = (jb % npt) / np, p = jb % np;
       const uint64_t tile = uint64_t(blockIdx.x) + G * tl;
       const bool real = jb < njobs && tile < ntiles;  // wave-uniform
       js0[u] = real ? p * D : 0;
       jnu[u] = real ? (nsteps - js0[u] < uint64_t(D) ? nsteps - js0[u] : uint64_t(D)) : 1;
-      const v4i* bp = real ? reinterpret_cast<const v4i*>(q + tile * nsteps * 2048 + lane * 16)
+      const v4i* bp = real ? reinterpret_cast<const v4i*>(q + (tile * planes + pl) * nsteps * 2048 + lane * 16)
                            : reinterpret_cast<const v4i*>(q);
       const uint64_t sstride = real ? 128 : 0;
 #pragma unroll
@@ -866,9 +890,11 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
     const bool t_ok = tl < tpw && tile < ntiles;
     int64_t p[4] = {0, 0, 0, 0};
     if (t_ok)
-      for (uint64_t pp = 0; pp < np; ++pp) {
-        const v4i v = part[tl * np + pp][i];
-        p[0] += v[0]; p[1] += v[1]; p[2] += v[2]; p[3] += v[3];
+      for (uint64_t pp = 0; pp < npt; ++pp) {
+        const v4i v = part[tl * npt + pp][i];
+        const int sh = int(8 * (pp / np));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
       }
     const uint64_t row = tile * 16 + i;
     const bool ok = t_ok && row < n_rows;
@@ -918,7 +944,7 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
     int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
-    int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
+    int8_t* __restrict__ out_limbs, uint64_t out_kpad, int planes) {
   __shared__ v4i al[2][NG][2][64];  // [buffer][token group][half][lane]
   constexpr int CH = (NG * 2 * 64 + 255) / 256;  // A chunks per thread and step
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -947,10 +973,15 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
     asrc[c] = reinterpret_cast<const v4i*>(limbs + (on ? uint64_t(16 * tg + (ln & 15)) * kpad : 0) +
                                            32 * (ln >> 4) + 16 * h);
   }
-  for (uint64_t base = uint64_t(blockIdx.x / kchunks) * 4; base < ntiles; base += groups * 4) {
-    const uint64_t tile = base + wave;
-    const bool t_on = tile < ntiles;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? tile : 0) * nsteps * 2048 + lane * 16);
+  // the four waves take four consecutive virtual tiles (digit plane p of tile
+  // t is virtual tile t * planes + p), whole tiles per workgroup pass
+  const uint64_t vtiles = ntiles * uint64_t(planes);
+  for (uint64_t base = uint64_t(blockIdx.x / kchunks) * 4; base < vtiles; base += groups * 4) {
+    const uint64_t vt = base + wave;
+    const bool t_on = vt < vtiles;
+    const uint64_t tile = vt / uint64_t(planes);
+    const int plane = int(vt % uint64_t(planes));
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? vt : 0) * nsteps * 2048 + lane * 16);
     v4i acc[NG];
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
@@ -982,14 +1013,36 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
       b1 = n1;
     }
     __syncthreads();  // both buffers are read before the next tile group refills them
-    if (!t_on) continue;
+    // a tile's digit planes: the plane-0 wave adds the others' partial tiles
+    // (through the A buffers, free until the next pass) with shifts
+    int64_t pt[NG][4];
+#pragma unroll
+    for (int tg = 0; tg < NG; ++tg)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pt[tg][j] = acc[tg][j];
+    if (planes > 1) {
+      v4i* xs = &al[0][0][0][0];
+#pragma unroll
+      for (int tg = 0; tg < NG; ++tg) xs[(wave * NG + tg) * 64 + lane] = acc[tg];
+      __syncthreads();
+      if (plane == 0)
+        for (int w = 1; w < planes; ++w)
+#pragma unroll
+          for (int tg = 0; tg < NG; ++tg) {
+            const v4i v = xs[((wave + w) * NG + tg) * 64 + lane];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pt[tg][j] += int64_t(uint64_t(int64_t(v[j])) << (8 * w));
+          }
+      __syncthreads();
+    }
+    if (!t_on || plane != 0) continue;
     const uint64_t row = tile * 16 + i;
     const bool r_on = row < n_rows;
     const int32_t rs = r_on ? rowsum[row] : 0, sc = r_on ? scale[row] : 0;
     // lane 16 g + i of group tg holds the limb sums of token 4 tg + g, row i
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg) {
-      const int64_t p[4] = {acc[tg][0], acc[tg][1], acc[tg][2], acc[tg][3]};
+      const int64_t p[4] = {pt[tg][0], pt[tg][1], pt[tg][2], pt[tg][3]};
       const uint32_t tok = 4 * tg + g;
       const bool ok = tok < ntok && r_on;
       if (acc_out) {
@@ -1129,7 +1182,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
                                                            uint64_t a_tiles, const uint32_t* __restrict__ a_flags,
                                                            uint32_t mblocks, int32_t* __restrict__ out,
                                                            uint64_t ld_out, int64_t* __restrict__ acc_out,
-                                                           RowSplit split, KSplit ks) {
+                                                           RowSplit split, KSplit ks, int planes) {
   constexpr int NW = WM * WN;                  // waves
   constexpr int TS = TA + TB;                  // tile-steps per K step
   constexpr int LPW = 2 * TS / NW;             // 1 KB wave copies per wave per K step
@@ -1159,7 +1212,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   const uint64_t ksteps = kpad / 128, cper = (ksteps + ks.chunks - 1) / ks.chunks;
   const uint64_t k0 = uint64_t(chunk) * cper < ksteps ? uint64_t(chunk) * cper : ksteps;
   const uint64_t nsteps = (k0 + cper < ksteps ? k0 + cper : ksteps) - k0;  // this block's K steps
-  const uint64_t ntiles = (n_rows + 15) / 16;
+  // weight tiles are virtual: digit plane p of tile t is tile t * planes + p
+  // (a block's FB tiles per wave hold whole tiles' planes)
+  const uint64_t ntiles = (n_rows + 15) / 16 * uint64_t(planes);
   const uint64_t at0 = uint64_t(mb) * TA, bt0 = uint64_t(nb) * TB;
   // The block's decomposition flags, one vector load per token group (lane p
   // reads part p's flag, at clamped addresses), issued ahead of the first
@@ -1217,7 +1272,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   int32_t ep_rowsum[FB], ep_scale[FB];
 #pragma unroll
   for (int tj = 0; tj < FB; ++tj) {
-    const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
+    const uint64_t row = (bt0 + wn * FB + tj) / uint64_t(planes) * 16 + i;
     const uint64_t rc = row < n_rows ? row : n_rows - 1;
     ep_rowsum[tj] = rowsum[rc];
     ep_scale[tj] = scale[rc];
@@ -1294,9 +1349,23 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
 #pragma unroll
     for (int t = 0; t < NG; ++t)
       if (uint32_t(t) == wm * (FA / 4) + tg) wmask = gmask[t];
+    // a tile's digit planes are consecutive virtual tiles of this wave: their
+    // limb sums accumulate (shifted 8 bits per plane) until the last plane
+    int64_t run[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int tj = 0; tj < FB; ++tj) {
-    const uint64_t row = (bt0 + wn * FB + tj) * 16 + i;
+    const uint64_t vt = bt0 + wn * FB + tj;
+    const int plane = int(vt % uint64_t(planes));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t d = int64_t(acc[4 * tg][tj][r]) + int64_t(acc[4 * tg + 1][tj][r]) * 256 +
+                        int64_t(acc[4 * tg + 2][tj][r]) * 65536 + int64_t(acc[4 * tg + 3][tj][r]) * 16777216;
+      run[r] = int64_t(uint64_t(run[r]) + (uint64_t(d) << (8 * plane)));
+    }
+    if (plane != planes - 1) continue;
+    int64_t dsum[4] = {run[0], run[1], run[2], run[3]};
+    run[0] = run[1] = run[2] = run[3] = 0;
+    const uint64_t row = vt / uint64_t(planes) * 16 + i;
     const uint64_t rc = row < n_rows ? row : n_rows - 1;
     // the chunk holding column 0 adds the constant term (wrapping i64): the
     // decomposition's sum_p c_p S_p (S_p the row sum of part p), i.e. 32896 S
@@ -1314,8 +1383,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
       int32_t val[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t p[4] = {acc[4 * tg][tj][r], acc[4 * tg + 1][tj][r], acc[4 * tg + 2][tj][r], acc[4 * tg + 3][tj][r]};
-        const int64_t dot = p[0] + p[1] * 256 + p[2] * 65536 + p[3] * 16777216 + int64_t(cterm);
+        const int64_t dot = int64_t(uint64_t(dsum[r]) + cterm);
         val[r] = requant(int64_t(uint64_t(dot) * sc));
       }
       // lane i < 8 holds gate row i, lane i + 8 its up row: the lower lanes
@@ -1326,7 +1394,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
       const int32_t recv0 = __shfl(send0, int(lane ^ 8u), 64), recv1 = __shfl(send1, int(lane ^ 8u), 64);
       const int32_t g0 = lo ? val[0] : recv0, u0 = lo ? recv0 : val[2];
       const int32_t g1 = lo ? val[1] : recv1, u1 = lo ? recv1 : val[3];
-      const uint64_t f = (bt0 + wn * FB + tj) * 8 + (i & 7);
+      const uint64_t f = vt / uint64_t(planes) * 8 + (i & 7);
       const uint64_t t0 = grp * 16 + 4 * g + (lo ? 0 : 2);
       if (row < n_rows) {  // (whole tiles: the up row is there too)
         if (t0 < m_tokens) out[t0 * ld_out + f] = mul_sat(gelu_act(g0), u0);
@@ -1338,8 +1406,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     for (int r = 0; r < 4; ++r) {
       const uint64_t token = grp * 16 + 4 * g + r;
       if (token >= m_tokens || row >= n_rows) continue;
-      const int64_t p[4] = {acc[4 * tg][tj][r], acc[4 * tg + 1][tj][r], acc[4 * tg + 2][tj][r], acc[4 * tg + 3][tj][r]};
-      const int64_t dot = p[0] + p[1] * 256 + p[2] * 65536 + p[3] * 16777216 + int64_t(cterm);
+      const int64_t dot = int64_t(uint64_t(dsum[r]) + cterm);
       const int64_t v = int64_t(uint64_t(dot) * sc);
       if (ks.chunks > 1) {
         // this K range's wrapping share
@@ -2060,7 +2127,11 @@ __global__ void k_softcap(int32_t* __restrict__ x, uint64_t n, int32_t cap) {
 }
 
 __device__ __forceinline__ int32_t wgt_at(const DevMatrix& M, uint64_t r, uint64_t c) {
-  if (M.storage == kInt8) return int32_t(M.q[tiled_offset(M.kpad, r, c)]) * M.scale[r];
+  if (M.storage == kInt8) {
+    uint32_t v = 0;
+    for (int p = 0; p < M.planes; ++p) v += uint32_t(int32_t(M.q[tiled_offset(M.kpad, digit_row(r, M.planes, p), c)])) << (8 * p);
+    return int32_t(v * uint32_t(M.scale[r]));
+  }
   if (M.storage == kI16) return int32_t(static_cast<const int16_t*>(M.w)[r * M.cols + c]);
   return static_cast<const int32_t*>(M.w)[r * M.cols + c];
 }
@@ -2103,7 +2174,7 @@ DevMatrix row_view(const DevMatrix& m, uint64_t r0, uint64_t n) {
   v.rows = n;
   v.owns = false;
   if (m.storage == kInt8) {
-    v.q = m.q + (r0 / 16) * (m.kpad / 128) * 2048;  // r0 is tile aligned
+    v.q = m.q + (r0 / 16) * uint64_t(m.planes) * (m.kpad / 128) * 2048;  // r0 is tile aligned
     v.scale = m.scale + r0;
     v.rowsum = m.rowsum + r0;
     v.rowsum_p = m.rowsum_p ? m.rowsum_p + r0 : nullptr;  // (rowsum_p_ld is the parent's)
@@ -2139,12 +2210,13 @@ static void launch_lds_gemv(const DevMatrix& W, const void* act, uint64_t ld_act
   const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
   const uint64_t lds = uint64_t(mm) * 4 * (cper * 128 + 32);
   if (ks == 0) ks = pick_ksplit(ntiles, nsteps);
-  const uint64_t tpw = 8 / ks;
+  while (ks * W.planes > 8) ks /= 2;
+  const uint64_t tpw = 8 / (uint64_t(ks) * W.planes);
   const uint64_t groups = std::min<uint64_t>((ntiles + tpw - 1) / tpw, std::max<uint64_t>(1024 / kchunks, 1));
   const uint64_t grid = groups * kchunks;
 #define DET_GEMV_LAUNCH(KS)                                                                                     \
   hipLaunchKernelGGL((k_gemv_i8_lds<KS, IN64, EPI>), dim3(unsigned(grid)), dim3(kGemvThreads), size_t(lds), s, W.q, \
-                     W.scale, W.rowsum, act, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao, kchunks, mulv)
+                     W.scale, W.rowsum, act, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao, kchunks, mulv, W.planes)
   switch (ks) {
     case 8: DET_GEMV_LAUNCH(8); break;
     case 4: DET_GEMV_LAUNCH(4); break;
@@ -2162,11 +2234,11 @@ bool gemv_fits_lds(const DevMatrix& W, uint64_t m) { return m * 4 * (W.kpad + 32
 constexpr uint64_t kTileMaxTiles = 4096;
 static bool gemv_tile_fits(const DevMatrix& W) { return W.storage == kInt8 && (W.rows + 15) / 16 <= kTileMaxTiles; }
 static void launch_gemv_tile(const DevMatrix& W, const void* act, bool in64, int32_t* o, int64_t* ao, hipStream_t s) {
-  const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
+  const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128 * uint64_t(W.planes);
   const int nw = nsteps <= 4 * kTileD ? 4 : (nsteps <= 8 * kTileD ? 8 : 16);
 #define DET_TILE_LAUNCH(NW, IN)                                                                                 \
   hipLaunchKernelGGL((k_gemv_tile<NW, IN>), dim3(unsigned(ntiles)), dim3(64 * NW), 0, s, W.q, W.scale, W.rowsum, \
-                     act, W.cols, W.rows, W.kpad, o, ao)
+                     act, W.cols, W.rows, W.kpad, o, ao, W.planes)
   if (in64) {
     if (nw == 4) DET_TILE_LAUNCH(4, true);
     else if (nw == 8) DET_TILE_LAUNCH(8, true);
@@ -2234,10 +2306,10 @@ static void launch_gemv_dec_ks(const DevMatrix& W, const int8_t* limbs, uint32_t
   const uint64_t nsteps = W.kpad / 128, cper = (nsteps + kc - 1) / kc, per = (cper + KS - 1) / KS;
   if (NG == 1 && ntok == 1 && per > 3)
     hipLaunchKernelGGL((k_gemv_dec1<KS, EPI>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,
-                       limbs, W.rows, W.kpad, kc, out, acc, out_limbs, out_kpad);
+                       limbs, W.rows, W.kpad, kc, out, acc, out_limbs, out_kpad, W.planes);
   else
     hipLaunchKernelGGL((k_gemv_dec<KS, EPI, NG>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,
-                       limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad);
+                       limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, W.planes);
 }
 
 template <int NG>
@@ -2247,10 +2319,12 @@ static void launch_gemv_dec_ng(const DevMatrix& W, const int8_t* limbs, uint32_t
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
   // (k_gemv_dec1 has the same 5 workgroups per CU as k_gemv_dec<4, 0, 1>)
   const uint64_t cap = resident_blocks(reinterpret_cast<const void*>(&k_gemv_dec<4, 0, NG>), 256);
-  auto groups = [&](int ks) { return (ntiles * ks + 3) / 4; };
+  // a tile's waves: K shares x digit planes, at most the workgroup's four
+  const uint64_t P = uint64_t(W.planes);
+  auto groups = [&](int ks) { return (ntiles * ks * P + 3) / 4; };
   // in-workgroup K split: smallest that fills the device, keeping >= 4 K steps per wave
   int ks = 1;
-  while (ks < 4 && groups(ks) < cap && nsteps >= uint64_t(ks) * 2 * 4) ks *= 2;
+  while (uint64_t(ks) * 2 * P <= 4 && groups(ks) < cap && nsteps >= uint64_t(ks) * 2 * 4) ks *= 2;
   // K chunks across workgroups (atomic outputs only) while the launch stays resident
   uint32_t kc = 1;
   if (acc)
@@ -2285,7 +2359,7 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
   const void* fn = epilogue == 1 ? reinterpret_cast<const void*>(&k_gemv_dec_wg<1, NG>)
                                  : reinterpret_cast<const void*>(&k_gemv_dec_wg<0, NG>);
   const uint64_t cap = resident_blocks(fn, 256);
-  const uint64_t groups = (ntiles + 3) / 4;
+  const uint64_t groups = (ntiles * uint64_t(W.planes) + 3) / 4;
   // K chunks across workgroups (atomic outputs only) up to about 2.5
   // workgroups per CU (measured best at E4B shapes), keeping at least two K
   // steps per chunk
@@ -2296,10 +2370,10 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
   const uint64_t g = std::min<uint64_t>(groups, std::max<uint64_t>(cap / kc, 1));
   if (epilogue == 1)
     hipLaunchKernelGGL((k_gemv_dec_wg<1, NG>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum, limbs,
-                       W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad);
+                       W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, W.planes);
   else
     hipLaunchKernelGGL((k_gemv_dec_wg<0, NG>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum, limbs,
-                       W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad);
+                       W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, W.planes);
 }
 
 void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
@@ -2333,7 +2407,7 @@ static NormSplit norm_split(const DevMatrix& W) {
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
   const uint64_t grid = std::min<uint64_t>(ntiles, device_cus());
   const uint64_t tpw = (ntiles + grid - 1) / grid;
-  return {grid, tpw * ((nsteps + kNormD - 1) / kNormD)};
+  return {grid, tpw * ((nsteps + kNormD - 1) / kNormD) * uint64_t(W.planes)};
 }
 bool gemv_norm_fits(const DevMatrix& W, uint64_t H) {
   if (W.storage != kInt8 || W.rows == 0 || H == 0 || H % 4 != 0 || W.cols != H || W.kpad > kNormMaxK) return false;
@@ -2352,10 +2426,10 @@ void launch_gemv_norm(const DecNormIn& ni, const DevMatrix& W, int epilogue, int
   do {                                                                                                               \
     if (epilogue == 1)                                                                                               \
       hipLaunchKernelGGL((k_gemv_norm<NW, JM, QPT, 1>), dim3(unsigned(sp.grid)), dim3(64 * NW), 0, s, ni, W.q,      \
-                         W.scale, W.rowsum, W.rows, W.kpad, acc_out, out, out_limbs, out_kpad);                     \
+                         W.scale, W.rowsum, W.rows, W.kpad, acc_out, out, out_limbs, out_kpad, W.planes);           \
     else                                                                                                             \
       hipLaunchKernelGGL((k_gemv_norm<NW, JM, QPT, 0>), dim3(unsigned(sp.grid)), dim3(64 * NW), 0, s, ni, W.q,      \
-                         W.scale, W.rowsum, W.rows, W.kpad, acc_out, out, out_limbs, out_kpad);                     \
+                         W.scale, W.rowsum, W.rows, W.kpad, acc_out, out, out_limbs, out_kpad, W.planes);           \
   } while (0)
   if (sp.jobs <= 4) {
     switch (qpt(4)) {
@@ -2398,12 +2472,14 @@ static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, 
       reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU>),
       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
   (void)attr;
+  static_assert(TB / WN >= 1, "weight tiles per wave");
+  if ((TB / WN) % W.planes) throw std::invalid_argument("GEMM block: a wave's weight tiles must hold whole digit-plane tiles");
   const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
-  const uint64_t nblocks = ((W.rows + 15) / 16 + TB - 1) / TB;
+  const uint64_t nblocks = ((W.rows + 15) / 16 * uint64_t(W.planes) + TB - 1) / TB;
   hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU>), dim3(unsigned(mblocks * nblocks * ks.chunks)),
                      dim3(64 * WM * WN), lds, s, a_tiled, W.q, W.scale, W.rowsum, W.rowsum_p, W.rowsum_p_ld, W.rows,
                      W.kpad, m, a_tiles, gemm_flags(a_tiled, m, W.kpad), uint32_t(mblocks), out, ld_out, acc_out,
-                     split, ks);
+                     split, ks, W.planes);
 }
 
 // K split of a GEMM whose 128 x 128 blocks leave CUs idle: chunks of at least
@@ -2415,8 +2491,8 @@ static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, 
 constexpr uint64_t kGemmPlaneBudget = uint64_t(16) << 20;
 constexpr uint64_t kGemmSplitMinSteps = 12;
 uint32_t gemm_kchunks(const DevMatrix& W, uint64_t m) {
-  if (W.storage != kInt8 || m == 0 || W.rows == 0) return 1;
-  const uint64_t blocks = ((m + 31) / 32) * (((W.rows + 15) / 16 + 7) / 8);
+  if (W.storage != kInt8 || m == 0 || W.rows == 0 || W.planes > 2) return 1;
+  const uint64_t blocks = ((m + 31) / 32) * (((W.rows + 15) / 16 * uint64_t(W.planes) + 7) / 8);
   const uint64_t cus = device_cus();
   if (blocks >= cus) return 1;
   const uint64_t nsteps = W.kpad / 128;
@@ -2457,16 +2533,19 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
   }
   // row-split outputs take the 128 x 128 blocks only (their epilogue is kept
   // out of the 256 x 256 block's registers)
-  if (split)
+  if (split) {
+    if (W.planes > 2) throw std::invalid_argument("row-split GEMM: at most two digit planes");
     return launch_gemm_lds_shape<8, 8, 2, 4, 8, 2, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
+  }
   // 64 tokens x 256 rows on 8 waves (one block per CU) when its blocks fill
   // whole rounds of the device; otherwise 32 tokens x 128 rows on 8 waves
   // (two blocks per CU, so two waves per SIMD hide each other's LDS and
-  // MFMA latency), whose finer grid leaves a smaller last round
+  // MFMA latency), whose finer grid leaves a smaller last round. Four digit
+  // planes take the larger block (four weight tiles per wave).
   const uint64_t cus = device_cus();
-  const uint64_t big = ((m + 63) / 64) * (((W.rows + 15) / 16 + 15) / 16);
+  const uint64_t big = ((m + 63) / 64) * (((W.rows + 15) / 16 * uint64_t(W.planes) + 15) / 16);
   const uint64_t rounds = (big + cus - 1) / cus;
-  if (big >= cus && big * 10 >= rounds * cus * 9)
+  if (W.planes > 2 || (big >= cus && big * 10 >= rounds * cus * 9))
     launch_gemm_lds_shape<16, 16, 2, 4, 4, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   else
     launch_gemm_lds_shape<8, 8, 2, 4, 8, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
@@ -2476,6 +2555,7 @@ void launch_gemm_tiled_gelu(const DevMatrix& W, uint64_t m, int32_t* out, uint64
                             hipStream_t s) {
   if (W.rows == 0 || m == 0) return;
   if (W.rows % 16) throw std::invalid_argument("gate/up GEMM: rows must be whole tiles of 8 gate + 8 up rows");
+  if (W.planes > 2) throw std::invalid_argument("gate/up GEMM: at most two digit planes");
   const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
   // 128 x 128 blocks at every m (no K split): with the GELU arithmetic in its
   // epilogue the 256 x 256 block does not fit its registers
@@ -2505,7 +2585,7 @@ void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t 
       } else {
         launch_act_limbs(act + t0 * ld_act, mm, W.cols, ld_act, W.kpad, limbs, s);
         hipLaunchKernelGGL(k_gemv_i8<8>, dim3(blocks_for(W.rows, 16)), dim3(512), 0, s, W.q, W.scale, W.rowsum,
-                           limbs, W.rows, W.kpad, mm, o, ld_out, ao);
+                           limbs, W.rows, W.kpad, mm, o, ld_out, ao, W.planes);
       }
     }
   } else if (W.storage == kI16) {

@@ -293,6 +293,7 @@ def lib() -> C.CDLL:
         "det_audit_trace": (C.c_int, [P, C.POINTER(TraceRequest), C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t,
                                       C.POINTER(C.c_size_t), C.POINTER(C.c_int32)]),
         "det_synthetic_int8": (C.c_int, [u64, u64, u64, C.c_int32, P, P]),
+        "det_synthetic_i16": (C.c_int, [u64, u64, u64, C.c_int32, P]),
         "det_scratch_create": (C.c_int, [P, C.POINTER(P)]),
         "det_scratch_free": (None, [P]),
         "det_kv_create": (C.c_int, [P, u64, u64, C.POINTER(P)]),
@@ -335,6 +336,16 @@ def synthetic_int8(seed: int, rows: int, cols: int, scale_max: int):
     if st:
         raise DetError(st, lib().det_ctx_last_error(None).decode())
     return q, s
+
+
+def synthetic_i16(seed: int, rows: int, cols: int, lim: int) -> np.ndarray:
+    """Counter-hash i16 Wgt bits (det_synthetic_i16; same values as
+    synthetic.fast_i16_matrix, generated by multi-threaded native code)."""
+    w = np.empty((rows, cols), dtype=np.int16)
+    st = lib().det_synthetic_i16(seed & ((1 << 64) - 1), rows, cols, lim, _ptr(w))
+    if st:
+        raise DetError(st, lib().det_ctx_last_error(None).decode())
+    return w
 
 
 class Context:

@@ -183,6 +183,41 @@ def fast_int8_matrix(seed: int, rows: int, cols: int, scale_max: int):
     return q, s
 
 
+def fast_i16_matrix(seed: int, rows: int, cols: int, lim: int = 4096, extremes: bool = True) -> np.ndarray:
+    """Wgt bits uniform in [-lim, lim] from counter hashes (int16; with
+    gcd 1 and values past 127 they do not factor into int8 x scale). With
+    `extremes`, every 7th row holds 32767 and every 11th row -32768 at a
+    hashed column, never both in one row (rows that need the negated or the
+    plain two-digit form)."""
+    b = hash_bytes(seed, rows * cols * 2).view(np.uint16).astype(np.int32)
+    w = (b % (2 * lim + 1) - lim).astype(np.int16).reshape(rows, cols)
+    w[:, 0] = 1
+    if extremes and cols > 1:
+        c = hash_bytes(seed ^ 0xE7, rows * 4).view(np.uint32) % np.uint32(cols - 1) + 1
+        r = np.arange(rows)
+        hi = r % 7 == 0
+        lo = (r % 11 == 3) & ~hi
+        w[r[hi], c[hi]] = 32767
+        w[r[lo], c[lo]] = -32768
+    return w
+
+
+def synthetic_model_i16(cfg: dict, seed: int, lim: int = 4096):
+    """The model of synthetic_model_fast with i16 Wgt bits that do not
+    factor into int8 x scale (every matrix from fast_i16_matrix)."""
+    for idx, (name, shape) in enumerate(model_tensor_shapes(cfg)):
+        ts = (seed * 1000003 + idx) & MASK64
+        if len(shape) == 1:
+            b = hash_bytes(ts, shape[0]).astype(np.int32) % 33 - 16
+            yield name, (65536 + b * 1024).astype(np.int32), None
+        else:
+            try:
+                from . import synthetic_i16  # native generator (same values)
+                yield name, synthetic_i16(ts, shape[0], shape[1], lim), None
+            except RuntimeError:
+                yield name, fast_i16_matrix(ts, shape[0], shape[1], lim), None
+
+
 def synthetic_model_fast(cfg: dict, seed: int, scale_max: int = 16):
     """Like synthetic_model but with counter-hash weights (fast enough for E4B scale)."""
     for idx, (name, shape) in enumerate(model_tensor_shapes(cfg)):

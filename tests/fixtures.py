@@ -169,7 +169,7 @@ def load_both(cfg, tensors, ctx, threads=8):
     om = oracle_lib.OracleModel(cfg)
     gm = rd.Model(ctx, cfg)
     for name, v, s in tensors:
-        om.set_tensor(name, v, 32 if s is None else 8, s)
+        om.set_tensor(name, v, 8 if s is not None else {np.dtype(np.int16): 16}.get(np.asarray(v).dtype, 32), s)
         gm.set_tensor(name, v, s)
     oracle_lib.set_threads(threads)
     return om.finalize(), gm.finalize()

@@ -57,3 +57,13 @@ def test_native_synthetic_generator_matches_python_definition():
         q2, s2 = synthetic.fast_int8_matrix(seed, rows, cols, smax)
         assert (q == q2).all() and (s == s2).all()
         assert q.min() >= -127 and q.max() <= 127 and s.min() >= 1 and s.max() <= smax
+
+
+@pytest.mark.skipif(not LIB.exists(), reason="libdetgpu.so not built")
+@pytest.mark.parametrize("rows,cols,lim", [(1, 1, 5), (23, 17, 4096), (77, 300, 32767), (4, 3, 1)])
+def test_native_i16_generator_equals_numpy(rows, cols, lim):
+    # host-only: det_synthetic_i16 reproduces synthetic.fast_i16_matrix
+    import rasterdet
+    from rasterdet import synthetic
+    seed = rows * 1000 + cols
+    assert (rasterdet.synthetic_i16(seed, rows, cols, lim) == synthetic.fast_i16_matrix(seed, rows, cols, lim)).all()
