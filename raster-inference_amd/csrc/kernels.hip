@@ -88,7 +88,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
                                                     const int32_t* __restrict__ rowsum,
                                                     const int8_t* __restrict__ limbs, uint64_t n_rows,
                                                     uint64_t kpad, uint32_t m, int32_t* __restrict__ out,
-                                                    uint64_t ld_out, int64_t* __restrict__ acc_out, int planes) {
+                                                    uint64_t ld_out, int64_t* __restrict__ acc_out, int lp) {
   __shared__ v4i part[NW][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
@@ -97,12 +97,15 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
   const bool a_on = uint32_t(at) < m;
   const bool b_on = row < n_rows;
   const uint64_t nsteps = kpad / 128;
-  const int wpp = NW / planes, plane = wave / wpp, pw = wave % wpp;
-  const uint64_t per = (nsteps + wpp - 1) / wpp;
+  // lp = log2(planes): NW >> lp waves per plane (shifts, no divisions)
+  constexpr int LNW = NW == 16 ? 4 : (NW == 8 ? 3 : (NW == 4 ? 2 : (NW == 2 ? 1 : 0)));
+  static_assert((1 << LNW) == NW, "NW is a power of two");
+  const int lw = LNW - lp, wpp = 1 << lw, plane = wave >> lw, pw = wave & (wpp - 1);
+  const uint64_t per = (nsteps + wpp - 1) >> lw;
   const uint64_t s0 = pw * per < nsteps ? pw * per : nsteps;
   const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
   const v4i* bp = reinterpret_cast<const v4i*>(
-      q + (uint64_t(blockIdx.x) * planes + plane) * nsteps * 2048 + lane * 16);
+      q + ((uint64_t(blockIdx.x) << lp) + plane) * nsteps * 2048 + lane * 16);
   const v4i* ap = reinterpret_cast<const v4i*>(limbs + (a_on ? (uint64_t(at) * 4 + aj) : 0) * kpad + 32 * g);
   const v4i zero = {0, 0, 0, 0};
   v4i acc = zero;
@@ -135,7 +138,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_i8(const int8_t* __restrict__ 
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     const v4i v = part[w][lane];
-    const int sh = 8 * (w / wpp);
+    const int sh = 8 * (w >> lw);
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
   }
@@ -173,16 +176,18 @@ __device__ __forceinline__ int64_t limb_combine(const int64_t p[4], int32_t rows
 // A digit-plane matrix (KSPLIT * planes <= 8) gives each of a tile's planes
 // KSPLIT waves; the tile's KSPLIT * planes partial tiles combine through LDS
 // with shifts of 8 bits per plane.
-template <int KSPLIT, bool IN64, int EPI>
+template <int KSPLIT, bool IN64, int EPI, bool DG>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const void* __restrict__ act_v, uint64_t ld_act, uint64_t k, uint64_t n_rows, uint64_t kpad, uint32_t m,
     int32_t* __restrict__ out, uint64_t ld_out, int64_t* __restrict__ acc_out, uint32_t kchunks,
-    const int32_t* __restrict__ mulv, int planes) {
+    const int32_t* __restrict__ mulv, int lp_arg) {
+  const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   extern __shared__ __attribute__((aligned(16))) int8_t lds_limbs[];
   __shared__ v4i part[8][64];
-  const int S = KSPLIT * planes;  // waves per tile
-  const int TPW = 8 / S;
+  constexpr int LKS = KSPLIT == 8 ? 3 : (KSPLIT == 4 ? 2 : (KSPLIT == 2 ? 1 : 0));
+  const int ls = LKS + lp, S = 1 << ls;  // waves per tile: KSPLIT << lp (lp = log2 of the digit planes)
+  const int TPW = 8 >> ls;
   const uint64_t nsteps = kpad / 128;
   const uint32_t kc = blockIdx.x % kchunks;
   const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
@@ -218,7 +223,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
-  const int slot = wave / S, within = wave % S, plane = within / KSPLIT, kp = within % KSPLIT;
+  const int slot = wave >> ls, within = wave & (S - 1), plane = within >> LKS, kp = within & (KSPLIT - 1);
   const int at = i >> 2, aj = i & 3;
   const bool a_on = uint32_t(at) < m;
   // LDS column (s - cs0) * 128 of this lane's limb plane
@@ -234,7 +239,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles && slot < TPW;
     const bool b_on = t_on && row < n_rows;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + ((t_on ? tile : 0) * planes + plane) * nsteps * 2048 + lane * 16);
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (((t_on ? tile : 0) << lp) + plane) * nsteps * 2048 + lane * 16);
     v4i acc = zero;
     uint64_t s = s0;
     for (; s + 4 <= s1; s += 4) {
@@ -267,7 +272,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
       if (within == 0) {
         for (int w = 1; w < S; ++w) {
           const v4i v = part[wave + w][lane];
-          const int sh = 8 * (w / KSPLIT);
+          const int sh = 8 * (w >> LKS);
 #pragma unroll
           for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
         }
@@ -312,12 +317,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_i8_lds(
 constexpr int kTileD = 5;
 // A digit-plane matrix (planes dividing NW) gives NW / planes waves to each
 // plane; the partial tiles combine with shifts of 8 bits per plane.
-template <int NW, bool IN64>
+template <int NW, bool IN64, bool DG>
 __global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict__ q, const int32_t* __restrict__ scale,
                                                        const int32_t* __restrict__ rowsum, const void* __restrict__ act_v,
                                                        uint64_t k, uint64_t n_rows, uint64_t kpad,
                                                        int32_t* __restrict__ out, int64_t* __restrict__ acc_out,
-                                                       int planes) {
+                                                       int lp_arg) {
+  const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   constexpr int D = kTileD;
   constexpr int kPass = (D * 32 + 63) / 64;             // activation quads per lane and batch
   constexpr uint32_t kPlane = kPass * 256 + 32;          // limb plane stride of a wave slice
@@ -327,11 +333,14 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict_
   const int g = lane >> 4, i = lane & 15;
   const uint64_t tile = blockIdx.x;
   const uint64_t nsteps = kpad / 128;
-  const int wpp = NW / planes, plane = wave / wpp, pw = wave % wpp;
-  const uint64_t per = (nsteps + wpp - 1) / wpp;
+  // lp = log2(planes): NW >> lp waves per digit plane (shifts, no divisions)
+  constexpr int LNW = NW == 16 ? 4 : (NW == 8 ? 3 : 2);
+  static_assert((1 << LNW) == NW, "NW is 4, 8 or 16");
+  const int lw = LNW - lp, wpp = 1 << lw, plane = wave >> lw, pw = wave & (wpp - 1);
+  const uint64_t per = (nsteps + wpp - 1) >> lw;
   const uint64_t s0 = uint64_t(pw) * per < nsteps ? uint64_t(pw) * per : nsteps;
   const uint64_t s1 = s0 + per < nsteps ? s0 + per : nsteps;
-  const v4i* bp = reinterpret_cast<const v4i*>(q + (tile * planes + plane) * nsteps * 2048 + lane * 16);
+  const v4i* bp = reinterpret_cast<const v4i*>(q + ((tile << lp) + plane) * nsteps * 2048 + lane * 16);
   const bool a_on = i < 4;  // A row i = limb i of the one token
   const uint8_t* aread = al[wave] + (i & 3) * kPlane + 32 * g;
   const v4i zero = {0, 0, 0, 0};
@@ -406,7 +415,7 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict_
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
     const v4i v = reinterpret_cast<const v4i*>(al[w])[lane];
-    const int sh = 8 * (w / wpp);
+    const int sh = 8 * (w >> lw);
 #pragma unroll
     for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
   }
@@ -430,22 +439,24 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_tile(const int8_t* __restrict_
 // out[t * out_ld + row] = requant; EPI 1: interleaved gate/up tiles,
 // out[t * out_ld + f] = mul_sat(gelu(gate_f), up_f), also written as limb
 // planes 4t..4t+3 of out_limbs (plane stride out_kpad) for the next GEMV.
-template <int KS, int EPI, int NG>
+template <int KS, int EPI, int NG, bool DG>
 __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_dec(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
     int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
-    int8_t* __restrict__ out_limbs, uint64_t out_kpad, int planes) {
+    int8_t* __restrict__ out_limbs, uint64_t out_kpad, int lp_arg) {
+  const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   __shared__ v4i part[4][NG][64];
-  const int S = KS * planes;  // waves per tile (digit planes x K shares)
-  const int TPW = 4 / S;
+  constexpr int LKS = KS == 4 ? 2 : (KS == 2 ? 1 : 0);
+  const int ls = LKS + lp, S = 1 << ls;  // waves per tile: K shares x digit planes (lp = log2 planes)
+  const int TPW = 4 >> ls;
   // K steps per load batch: three for one token group (a wave's 5-step share
   // of K 2560 split four ways takes two load round trips either way), two when
   // the A tiles of several groups share the registers
   constexpr int D = NG == 1 ? 3 : 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
-  const int slot = wave / S, within = wave % S, plane = within / KS, kp = within % KS;
+  const int slot = wave >> ls, within = wave & (S - 1), plane = within >> LKS, kp = within & (KS - 1);
   const uint64_t nsteps = kpad / 128;
   const uint32_t kc = blockIdx.x % kchunks;
   const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
@@ -468,7 +479,7 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
     const uint64_t tile = base + slot;
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + ((t_on ? tile : 0) * planes + plane) * nsteps * 2048 + lane * 16);
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (((t_on ? tile : 0) << lp) + plane) * nsteps * 2048 + lane * 16);
     v4i acc[NG];
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
@@ -512,7 +523,7 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
       __syncthreads();
       if (within == 0) {
         for (int w = 1; w < S; ++w) {
-          const int sh = 8 * (w / KS);
+          const int sh = 8 * (w >> LKS);
 #pragma unroll
           for (int tg = 0; tg < NG; ++tg) {
             const v4i v = part[wave + w][tg][lane];
@@ -564,22 +575,24 @@ __global__ __launch_bounds__(256, NG == 1 ? 5 : (NG == 2 ? 4 : 3)) void k_gemv_d
 // trip (k_gemv_dec holds A and B in registers and takes 3 steps per trip).
 // Every load goes to a clamped address (none is predicated); steps past the
 // share meet zero A operands.
-template <int KS, int EPI>
+template <int KS, int EPI, bool DG>
 __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, int32_t* __restrict__ out,
-    int64_t* __restrict__ acc_out, int8_t* __restrict__ out_limbs, uint64_t out_kpad, int planes) {
+    int64_t* __restrict__ acc_out, int8_t* __restrict__ out_limbs, uint64_t out_kpad, int lp_arg) {
+  const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   constexpr int D = 5;
   constexpr int kCopies = (4 * D * 128 + 1023) / 1024;  // 1 KB wave copies of 4 planes x D steps
   __shared__ __attribute__((aligned(16))) int8_t al[4][kCopies * 1024];
   __shared__ v4i part[4][64];
-  const int S = KS * planes;  // waves per tile (digit planes x K shares)
-  const int TPW = 4 / S;
+  constexpr int LKS = KS == 4 ? 2 : (KS == 2 ? 1 : 0);
+  const int ls = LKS + lp, S = 1 << ls;  // waves per tile: K shares x digit planes (lp = log2 planes)
+  const int TPW = 4 >> ls;
   constexpr int kWaitLds = 15 | (7 << 4) | (0 << 8) | (3 << 14);  // lgkmcnt(0)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, i = lane & 15;
-  const int slot = wave / S, within = wave % S, plane = within / KS, kp = within % KS;
+  const int slot = wave >> ls, within = wave & (S - 1), plane = within >> LKS, kp = within & (KS - 1);
   const uint64_t nsteps = kpad / 128;
   const uint32_t kc = blockIdx.x % kchunks;
   const uint64_t cper = (nsteps + kchunks - 1) / kchunks;
@@ -598,7 +611,7 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
     const uint64_t tile = base + slot;
     const uint64_t row = tile * 16 + i;
     const bool t_on = tile < ntiles;
-    const v4i* bp = reinterpret_cast<const v4i*>(q + ((t_on ? tile : ntiles - 1) * planes + plane) * nsteps * 2048 +
+    const v4i* bp = reinterpret_cast<const v4i*>(q + (((t_on ? tile : ntiles - 1) << lp) + plane) * nsteps * 2048 +
                                                  lane * 16);
     v4i acc = zero;
     for (uint64_t sb = s0; sb < s1; sb += D) {
@@ -653,7 +666,7 @@ __global__ __launch_bounds__(256, 5) void k_gemv_dec1(
       if (within == 0) {
         for (int w = 1; w < S; ++w) {
           const v4i v = part[wave + w][lane];
-          const int sh = 8 * (w / KS);
+          const int sh = 8 * (w >> LKS);
 #pragma unroll
           for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
         }
@@ -734,13 +747,14 @@ __device__ __forceinline__ int32_t wg_rms_scale(int64_t ss, uint64_t n, int64_t 
     return *bc;
   }
 }
-template <int NW, int JM, int QPT, int EPI>
+template <int NW, int JM, int QPT, int EPI, bool DG>
 __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_t* __restrict__ q,
                                                        const int32_t* __restrict__ scale,
                                                        const int32_t* __restrict__ rowsum, uint64_t n_rows,
                                                        uint64_t kpad, int64_t* __restrict__ acc_out,
                                                        int32_t* __restrict__ out, int8_t* __restrict__ out_limbs,
-                                                       uint64_t out_kpad, int planes) {
+                                                       uint64_t out_kpad, int lp_arg) {
+  const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   constexpr int NT = 64 * NW, D = kNormD;
   constexpr uint32_t kPlaneMax = kNormMaxK + 32;
   typedef long long v2l __attribute__((ext_vector_type(2)));
@@ -751,8 +765,9 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, i = lane & 15;
-  // a tile's jobs: its digit planes x K parts of D steps (job pp: plane pp / np)
-  const uint64_t nsteps = kpad / 128, np = (nsteps + D - 1) / D, npt = np * uint64_t(planes);
+  // a tile's jobs: its digit planes x K parts of D steps (job pp: plane pp / np,
+  // lp = log2 of the planes)
+  const uint64_t nsteps = kpad / 128, np = (nsteps + D - 1) / D, npt = np << lp;
   const uint64_t ntiles = (n_rows + 15) / 16, G = gridDim.x;
   const uint64_t tpw = (ntiles + G - 1) / G, njobs = tpw * npt;
   const uint64_t plane = kpad + 32;  // limb plane stride in LDS (planes start 8 banks apart)
@@ -793,12 +808,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
 #pragma unroll
     for (int u = u0; u < u1; ++u) {
       const uint64_t jb = uint64_t(wave) + uint64_t(NW) * u;
-      const uint64_t tl = jb / npt, pl = (jb % npt) / np, p = jb % np;
+      const uint64_t jq = jb / np, p = jb - jq * np, tl = jq >> lp, pl = jq & ((uint64_t(1) << lp) - 1);
       const uint64_t tile = uint64_t(blockIdx.x) + G * tl;
       const bool real = jb < njobs && tile < ntiles;  // wave-uniform
       js0[u] = real ? p * D : 0;
       jnu[u] = real ? (nsteps - js0[u] < uint64_t(D) ? nsteps - js0[u] : uint64_t(D)) : 1;
-      const v4i* bp = real ? reinterpret_cast<const v4i*>(q + (tile * planes + pl) * nsteps * 2048 + lane * 16)
+      const v4i* bp = real ? reinterpret_cast<const v4i*>(q + ((tile << lp) + pl) * nsteps * 2048 + lane * 16)
                            : reinterpret_cast<const v4i*>(q);
       const uint64_t sstride = real ? 128 : 0;
 #pragma unroll
@@ -890,12 +905,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
     const bool t_ok = tl < tpw && tile < ntiles;
     int64_t p[4] = {0, 0, 0, 0};
     if (t_ok)
-      for (uint64_t pp = 0; pp < npt; ++pp) {
-        const v4i v = part[tl * npt + pp][i];
-        const int sh = int(8 * (pp / np));
+      for (int pl = 0; pl < (1 << lp); ++pl)
+        for (uint64_t pp = 0; pp < np; ++pp) {
+          const v4i v = part[tl * npt + pl * np + pp][i];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << sh);
-      }
+          for (int j = 0; j < 4; ++j) p[j] += int64_t(uint64_t(int64_t(v[j])) << (8 * pl));
+        }
     const uint64_t row = tile * 16 + i;
     const bool ok = t_ok && row < n_rows;
     const bool first = tl0 == 4 * uint64_t(wave);
@@ -939,13 +954,15 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
 // and A loads are issued before the current step's MFMAs, one barrier per
 // step). Outputs as in k_gemv_dec; kchunks splits K across workgroups
 // (atomic outputs only).
-template <int EPI, int NG>
+template <int EPI, int NG, bool DG>
 __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
     int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
-    int8_t* __restrict__ out_limbs, uint64_t out_kpad, int planes) {
+    int8_t* __restrict__ out_limbs, uint64_t out_kpad, int lp_arg) {
+  const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   __shared__ v4i al[2][NG][2][64];  // [buffer][token group][half][lane]
+  const int planes = 1 << lp;  // digit planes
   constexpr int CH = (NG * 2 * 64 + 255) / 256;  // A chunks per thread and step
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
@@ -975,12 +992,12 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
   }
   // the four waves take four consecutive virtual tiles (digit plane p of tile
   // t is virtual tile t * planes + p), whole tiles per workgroup pass
-  const uint64_t vtiles = ntiles * uint64_t(planes);
+  const uint64_t vtiles = ntiles << lp;
   for (uint64_t base = uint64_t(blockIdx.x / kchunks) * 4; base < vtiles; base += groups * 4) {
     const uint64_t vt = base + wave;
     const bool t_on = vt < vtiles;
-    const uint64_t tile = vt / uint64_t(planes);
-    const int plane = int(vt % uint64_t(planes));
+    const uint64_t tile = vt >> lp;
+    const int plane = int(vt & uint64_t(planes - 1));
     const v4i* bp = reinterpret_cast<const v4i*>(q + (t_on ? vt : 0) * nsteps * 2048 + lane * 16);
     v4i acc[NG];
 #pragma unroll
@@ -1083,6 +1100,7 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
 // row i) in lane 16g + i, which are combined exactly as in the GEMV.
 // ---------------------------------------------------------------------------
 
+
 // Prefill GEMM A operand: activation rows as limb-major token groups. Token
 // group T (tokens 16 T .. 16 T + 15) has four limb tiles T 4 + j; tile-step
 // (tile, s) is 2048 bytes of 32-byte lane slots (slot 16 g + i: token 16 T + i,
@@ -1173,7 +1191,7 @@ __global__ __launch_bounds__(256) void k_act_limbs_tiled(const int32_t* __restri
 // 16 t + i, i < 8: gate row 8 t + i; rows 16 t + 8 + i: up row 8 t + i) and
 // out[token][8 t + i] = mul_sat(gelu(gate), up) (the decode step's gate/up
 // epilogue; no other output form).
-template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT, bool GELU = false>
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT, bool GELU, bool DG>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restrict__ a, const int8_t* __restrict__ q,
                                                            const int32_t* __restrict__ scale,
                                                            const int32_t* __restrict__ rowsum,
@@ -1182,7 +1200,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
                                                            uint64_t a_tiles, const uint32_t* __restrict__ a_flags,
                                                            uint32_t mblocks, int32_t* __restrict__ out,
                                                            uint64_t ld_out, int64_t* __restrict__ acc_out,
-                                                           RowSplit split, KSplit ks, int planes) {
+                                                           RowSplit split, KSplit ks, int lp_arg) {
+  const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   constexpr int NW = WM * WN;                  // waves
   constexpr int TS = TA + TB;                  // tile-steps per K step
   constexpr int LPW = 2 * TS / NW;             // 1 KB wave copies per wave per K step
@@ -1214,7 +1233,8 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   const uint64_t nsteps = (k0 + cper < ksteps ? k0 + cper : ksteps) - k0;  // this block's K steps
   // weight tiles are virtual: digit plane p of tile t is tile t * planes + p
   // (a block's FB tiles per wave hold whole tiles' planes)
-  const uint64_t ntiles = (n_rows + 15) / 16 * uint64_t(planes);
+  const uint64_t ntiles = (n_rows + 15) / 16 << lp;  // (lp = log2 of the digit planes)
+  const int planes = 1 << lp;
   const uint64_t at0 = uint64_t(mb) * TA, bt0 = uint64_t(nb) * TB;
   // The block's decomposition flags, one vector load per token group (lane p
   // reads part p's flag, at clamped addresses), issued ahead of the first
@@ -1272,7 +1292,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   int32_t ep_rowsum[FB], ep_scale[FB];
 #pragma unroll
   for (int tj = 0; tj < FB; ++tj) {
-    const uint64_t row = (bt0 + wn * FB + tj) / uint64_t(planes) * 16 + i;
+    const uint64_t row = ((bt0 + wn * FB + tj) >> lp) * 16 + i;
     const uint64_t rc = row < n_rows ? row : n_rows - 1;
     ep_rowsum[tj] = rowsum[rc];
     ep_scale[tj] = scale[rc];
@@ -1355,7 +1375,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
 #pragma unroll
     for (int tj = 0; tj < FB; ++tj) {
     const uint64_t vt = bt0 + wn * FB + tj;
-    const int plane = int(vt % uint64_t(planes));
+    const int plane = int(vt & uint64_t(planes - 1));
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t d = int64_t(acc[4 * tg][tj][r]) + int64_t(acc[4 * tg + 1][tj][r]) * 256 +
@@ -1365,7 +1385,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     if (plane != planes - 1) continue;
     int64_t dsum[4] = {run[0], run[1], run[2], run[3]};
     run[0] = run[1] = run[2] = run[3] = 0;
-    const uint64_t row = vt / uint64_t(planes) * 16 + i;
+    const uint64_t row = (vt >> lp) * 16 + i;
     const uint64_t rc = row < n_rows ? row : n_rows - 1;
     // the chunk holding column 0 adds the constant term (wrapping i64): the
     // decomposition's sum_p c_p S_p (S_p the row sum of part p), i.e. 32896 S
@@ -1394,7 +1414,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
       const int32_t recv0 = __shfl(send0, int(lane ^ 8u), 64), recv1 = __shfl(send1, int(lane ^ 8u), 64);
       const int32_t g0 = lo ? val[0] : recv0, u0 = lo ? recv0 : val[2];
       const int32_t g1 = lo ? val[1] : recv1, u1 = lo ? recv1 : val[3];
-      const uint64_t f = vt / uint64_t(planes) * 8 + (i & 7);
+      const uint64_t f = (vt >> lp) * 8 + (i & 7);
       const uint64_t t0 = grp * 16 + 4 * g + (lo ? 0 : 2);
       if (row < n_rows) {  // (whole tiles: the up row is there too)
         if (t0 < m_tokens) out[t0 * ld_out + f] = mul_sat(gelu_act(g0), u0);
@@ -2168,6 +2188,11 @@ __global__ __launch_bounds__(256) void k_argmax_final(const int64_t* __restrict_
 // launchers
 // ---------------------------------------------------------------------------
 static inline unsigned blocks_for(uint64_t n, unsigned per) { return unsigned((n + per - 1) / per); }
+// log2 of a matrix's digit planes (1, 2 or 4), the kernels' shift amount
+static inline int plane_log2(const DevMatrix& W) {
+  if (W.planes != 1 && W.planes != 2 && W.planes != 4) throw std::invalid_argument("digit planes must be 1, 2 or 4");
+  return W.planes >> 1;
+}
 
 DevMatrix row_view(const DevMatrix& m, uint64_t r0, uint64_t n) {
   DevMatrix v = m;
@@ -2214,9 +2239,15 @@ static void launch_lds_gemv(const DevMatrix& W, const void* act, uint64_t ld_act
   const uint64_t tpw = 8 / (uint64_t(ks) * W.planes);
   const uint64_t groups = std::min<uint64_t>((ntiles + tpw - 1) / tpw, std::max<uint64_t>(1024 / kchunks, 1));
   const uint64_t grid = groups * kchunks;
+#define DET_GEMV_LAUNCH_DG(KS, DG)                                                                              \
+  hipLaunchKernelGGL((k_gemv_i8_lds<KS, IN64, EPI, DG>), dim3(unsigned(grid)), dim3(kGemvThreads), size_t(lds), s, \
+                     W.q, W.scale, W.rowsum, act, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao, kchunks, mulv,   \
+                     plane_log2(W))
 #define DET_GEMV_LAUNCH(KS)                                                                                     \
-  hipLaunchKernelGGL((k_gemv_i8_lds<KS, IN64, EPI>), dim3(unsigned(grid)), dim3(kGemvThreads), size_t(lds), s, W.q, \
-                     W.scale, W.rowsum, act, ld_act, W.cols, W.rows, W.kpad, mm, o, ld_out, ao, kchunks, mulv, W.planes)
+  do {                                                                                                          \
+    if (W.planes == 1) DET_GEMV_LAUNCH_DG(KS, false);                                                           \
+    else DET_GEMV_LAUNCH_DG(KS, true);                                                                          \
+  } while (0)
   switch (ks) {
     case 8: DET_GEMV_LAUNCH(8); break;
     case 4: DET_GEMV_LAUNCH(4); break;
@@ -2224,6 +2255,7 @@ static void launch_lds_gemv(const DevMatrix& W, const void* act, uint64_t ld_act
     default: DET_GEMV_LAUNCH(1); break;
   }
 #undef DET_GEMV_LAUNCH
+#undef DET_GEMV_LAUNCH_DG
 }
 
 bool gemv_fits_lds(const DevMatrix& W, uint64_t m) { return m * 4 * (W.kpad + 32) <= kGemvLdsBudget; }
@@ -2236,9 +2268,14 @@ static bool gemv_tile_fits(const DevMatrix& W) { return W.storage == kInt8 && (W
 static void launch_gemv_tile(const DevMatrix& W, const void* act, bool in64, int32_t* o, int64_t* ao, hipStream_t s) {
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128 * uint64_t(W.planes);
   const int nw = nsteps <= 4 * kTileD ? 4 : (nsteps <= 8 * kTileD ? 8 : 16);
+#define DET_TILE_LAUNCH_DG(NW, IN, DG)                                                                          \
+  hipLaunchKernelGGL((k_gemv_tile<NW, IN, DG>), dim3(unsigned(ntiles)), dim3(64 * NW), 0, s, W.q, W.scale,        \
+                     W.rowsum, act, W.cols, W.rows, W.kpad, o, ao, plane_log2(W))
 #define DET_TILE_LAUNCH(NW, IN)                                                                                 \
-  hipLaunchKernelGGL((k_gemv_tile<NW, IN>), dim3(unsigned(ntiles)), dim3(64 * NW), 0, s, W.q, W.scale, W.rowsum, \
-                     act, W.cols, W.rows, W.kpad, o, ao, W.planes)
+  do {                                                                                                          \
+    if (W.planes == 1) DET_TILE_LAUNCH_DG(NW, IN, false);                                                       \
+    else DET_TILE_LAUNCH_DG(NW, IN, true);                                                                      \
+  } while (0)
   if (in64) {
     if (nw == 4) DET_TILE_LAUNCH(4, true);
     else if (nw == 8) DET_TILE_LAUNCH(8, true);
@@ -2249,6 +2286,7 @@ static void launch_gemv_tile(const DevMatrix& W, const void* act, bool in64, int
     else DET_TILE_LAUNCH(16, false);
   }
 #undef DET_TILE_LAUNCH
+#undef DET_TILE_LAUNCH_DG
 }
 
 void launch_gemv_decode(const DevMatrix& W, const void* act, bool act_i64, int epilogue, int32_t* out,
@@ -2304,12 +2342,22 @@ static void launch_gemv_dec_ks(const DevMatrix& W, const int8_t* limbs, uint32_t
   // k_gemv_dec takes shares of up to 3 K steps in one round trip and is the
   // faster of the two there (measured on E4B's qkv and down projections)
   const uint64_t nsteps = W.kpad / 128, cper = (nsteps + kc - 1) / kc, per = (cper + KS - 1) / KS;
-  if (NG == 1 && ntok == 1 && per > 3)
-    hipLaunchKernelGGL((k_gemv_dec1<KS, EPI>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,
-                       limbs, W.rows, W.kpad, kc, out, acc, out_limbs, out_kpad, W.planes);
-  else
-    hipLaunchKernelGGL((k_gemv_dec<KS, EPI, NG>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,
-                       limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, W.planes);
+  const bool dg = W.planes > 1;
+  if (NG == 1 && ntok == 1 && per > 3) {
+    if (dg)
+      hipLaunchKernelGGL((k_gemv_dec1<KS, EPI, true>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale,
+                         W.rowsum, limbs, W.rows, W.kpad, kc, out, acc, out_limbs, out_kpad, plane_log2(W));
+    else
+      hipLaunchKernelGGL((k_gemv_dec1<KS, EPI, false>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale,
+                         W.rowsum, limbs, W.rows, W.kpad, kc, out, acc, out_limbs, out_kpad, 0);
+  } else if (dg) {
+    hipLaunchKernelGGL((k_gemv_dec<KS, EPI, NG, true>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale,
+                       W.rowsum, limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad,
+                       plane_log2(W));
+  } else {
+    hipLaunchKernelGGL((k_gemv_dec<KS, EPI, NG, false>), dim3(unsigned(groups * kc)), dim3(256), 0, s, W.q, W.scale,
+                       W.rowsum, limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, 0);
+  }
 }
 
 template <int NG>
@@ -2318,7 +2366,7 @@ static void launch_gemv_dec_ng(const DevMatrix& W, const int8_t* limbs, uint32_t
                                hipStream_t s) {
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
   // (k_gemv_dec1 has the same 5 workgroups per CU as k_gemv_dec<4, 0, 1>)
-  const uint64_t cap = resident_blocks(reinterpret_cast<const void*>(&k_gemv_dec<4, 0, NG>), 256);
+  const uint64_t cap = resident_blocks(reinterpret_cast<const void*>(&k_gemv_dec<4, 0, NG, false>), 256);
   // a tile's waves: K shares x digit planes, at most the workgroup's four
   const uint64_t P = uint64_t(W.planes);
   auto groups = [&](int ks) { return (ntiles * ks * P + 3) / 4; };
@@ -2356,8 +2404,8 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
                                int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
                                hipStream_t s) {
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
-  const void* fn = epilogue == 1 ? reinterpret_cast<const void*>(&k_gemv_dec_wg<1, NG>)
-                                 : reinterpret_cast<const void*>(&k_gemv_dec_wg<0, NG>);
+  const void* fn = epilogue == 1 ? reinterpret_cast<const void*>(&k_gemv_dec_wg<1, NG, false>)
+                                 : reinterpret_cast<const void*>(&k_gemv_dec_wg<0, NG, false>);
   const uint64_t cap = resident_blocks(fn, 256);
   const uint64_t groups = (ntiles * uint64_t(W.planes) + 3) / 4;
   // K chunks across workgroups (atomic outputs only) up to about 2.5
@@ -2368,12 +2416,17 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
   if (acc)
     while (groups * kc * 2 <= target && nsteps >= uint64_t(kc) * 2 * 2) kc *= 2;
   const uint64_t g = std::min<uint64_t>(groups, std::max<uint64_t>(cap / kc, 1));
-  if (epilogue == 1)
-    hipLaunchKernelGGL((k_gemv_dec_wg<1, NG>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum, limbs,
-                       W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, W.planes);
-  else
-    hipLaunchKernelGGL((k_gemv_dec_wg<0, NG>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum, limbs,
-                       W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, W.planes);
+#define DET_DEC_WG(E, DG)                                                                                       \
+  hipLaunchKernelGGL((k_gemv_dec_wg<E, NG, DG>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,  \
+                     limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, plane_log2(W))
+  if (epilogue == 1) {
+    if (W.planes == 1) DET_DEC_WG(1, false);
+    else DET_DEC_WG(1, true);
+  } else {
+    if (W.planes == 1) DET_DEC_WG(0, false);
+    else DET_DEC_WG(0, true);
+  }
+#undef DET_DEC_WG
 }
 
 void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
@@ -2422,14 +2475,19 @@ void launch_gemv_norm(const DecNormIn& ni, const DevMatrix& W, int epilogue, int
   // kpad / 4 limb quads
   const uint64_t kq = W.kpad / 4;
   auto qpt = [&](int nw) { return (kq + 64 * nw - 1) / (64 * nw); };
+#define DET_NORM_LAUNCH_DG(NW, JM, QPT, E, DG)                                                                       \
+  hipLaunchKernelGGL((k_gemv_norm<NW, JM, QPT, E, DG>), dim3(unsigned(sp.grid)), dim3(64 * NW), 0, s, ni, W.q,       \
+                     W.scale, W.rowsum, W.rows, W.kpad, acc_out, out, out_limbs, out_kpad, plane_log2(W))
 #define DET_NORM_LAUNCH(NW, JM, QPT)                                                                                 \
   do {                                                                                                               \
-    if (epilogue == 1)                                                                                               \
-      hipLaunchKernelGGL((k_gemv_norm<NW, JM, QPT, 1>), dim3(unsigned(sp.grid)), dim3(64 * NW), 0, s, ni, W.q,      \
-                         W.scale, W.rowsum, W.rows, W.kpad, acc_out, out, out_limbs, out_kpad, W.planes);           \
-    else                                                                                                             \
-      hipLaunchKernelGGL((k_gemv_norm<NW, JM, QPT, 0>), dim3(unsigned(sp.grid)), dim3(64 * NW), 0, s, ni, W.q,      \
-                         W.scale, W.rowsum, W.rows, W.kpad, acc_out, out, out_limbs, out_kpad, W.planes);           \
+    const bool dg = W.planes > 1;                                                                                    \
+    if (epilogue == 1) {                                                                                             \
+      if (dg) DET_NORM_LAUNCH_DG(NW, JM, QPT, 1, true);                                                              \
+      else DET_NORM_LAUNCH_DG(NW, JM, QPT, 1, false);                                                                \
+    } else {                                                                                                         \
+      if (dg) DET_NORM_LAUNCH_DG(NW, JM, QPT, 0, true);                                                              \
+      else DET_NORM_LAUNCH_DG(NW, JM, QPT, 0, false);                                                                \
+    }                                                                                                                \
   } while (0)
   if (sp.jobs <= 4) {
     switch (qpt(4)) {
@@ -2450,6 +2508,7 @@ void launch_gemv_norm(const DecNormIn& ni, const DevMatrix& W, int epilogue, int
     DET_NORM_LAUNCH(16, 2, 1);
   }
 #undef DET_NORM_LAUNCH
+#undef DET_NORM_LAUNCH_DG
 }
 
 // a_tiled holds the limb tiles of (m rounded up to 64) tokens, then the
@@ -2463,23 +2522,34 @@ uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) {
   return gemm_tile_bytes(m, kpad) + 4 * groups * limb_parts(kpad);
 }
 
+template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT, bool GELU, bool DG>
+static void launch_gemm_lds_dg(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
+                               const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s, RowSplit split, KSplit ks) {
+  constexpr uint32_t lds = uint32_t(NBUF) * (TA + TB) * 2048u;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU, DG>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+  (void)attr;
+  const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
+  const uint64_t nblocks = ((W.rows + 15) / 16 * uint64_t(W.planes) + TB - 1) / TB;
+  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU, DG>),
+                     dim3(unsigned(mblocks * nblocks * ks.chunks)), dim3(64 * WM * WN), lds, s, a_tiled, W.q, W.scale,
+                     W.rowsum, W.rowsum_p, W.rowsum_p_ld, W.rows, W.kpad, m, a_tiles, gemm_flags(a_tiled, m, W.kpad),
+                     uint32_t(mblocks), out, ld_out, acc_out, split, ks, plane_log2(W));
+}
+
 template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT = false, bool GELU = false>
 static void launch_gemm_lds_shape(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
                                   const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s, RowSplit split = {},
                                   KSplit ks = {}) {
-  constexpr uint32_t lds = uint32_t(NBUF) * (TA + TB) * 2048u;
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-  (void)attr;
   static_assert(TB / WN >= 1, "weight tiles per wave");
   if ((TB / WN) % W.planes) throw std::invalid_argument("GEMM block: a wave's weight tiles must hold whole digit-plane tiles");
-  const uint64_t mblocks = (m + 4 * TA - 1) / (4 * TA);
-  const uint64_t nblocks = ((W.rows + 15) / 16 * uint64_t(W.planes) + TB - 1) / TB;
-  hipLaunchKernelGGL((k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU>), dim3(unsigned(mblocks * nblocks * ks.chunks)),
-                     dim3(64 * WM * WN), lds, s, a_tiled, W.q, W.scale, W.rowsum, W.rowsum_p, W.rowsum_p_ld, W.rows,
-                     W.kpad, m, a_tiles, gemm_flags(a_tiled, m, W.kpad), uint32_t(mblocks), out, ld_out, acc_out,
-                     split, ks, W.planes);
+  if (W.planes == 1)
+    launch_gemm_lds_dg<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU, false>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s,
+                                                                     split, ks);
+  else
+    launch_gemm_lds_dg<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU, true>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s,
+                                                                    split, ks);
 }
 
 // K split of a GEMM whose 128 x 128 blocks leave CUs idle: chunks of at least
@@ -2585,7 +2655,7 @@ void launch_linear(const DevMatrix& W, const int32_t* act, uint64_t m, uint64_t 
       } else {
         launch_act_limbs(act + t0 * ld_act, mm, W.cols, ld_act, W.kpad, limbs, s);
         hipLaunchKernelGGL(k_gemv_i8<8>, dim3(blocks_for(W.rows, 16)), dim3(512), 0, s, W.q, W.scale, W.rowsum,
-                           limbs, W.rows, W.kpad, mm, o, ld_out, ao, W.planes);
+                           limbs, W.rows, W.kpad, mm, o, ld_out, ao, plane_log2(W));
       }
     }
   } else if (W.storage == kI16) {
