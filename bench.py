@@ -388,10 +388,11 @@ def e4b_i16_decode(ctx, rd, args) -> dict:
     ctx.synchronize()
     prefill_s = time.perf_counter() - t0
     tokens = []
+    extra = rd.DET_DECODE_EAGER if getattr(args, "eager", False) else 0
     t0 = time.perf_counter()
     for _ in range(steps):
         tokens.append(tok)
-        tok = sess.decode(tok, rd.DET_COMMIT_NONE).next_token
+        tok = sess.decode(tok, rd.DET_COMMIT_NONE | extra).next_token
     ctx.synchronize()
     dec_s = time.perf_counter() - t0
     s2 = model.session(args.prompt_len + 17)
