@@ -421,29 +421,50 @@ __global__ __launch_bounds__(512) void k_dec_attn_scores(AttnDecArgs a) {
     }
   for (uint32_t g = 0; g < GW; ++g) {
     const int32_t* qg = ql + g * hd;
+    int64_t accs[P];
+    if (VEC) {
+      // every chunk's products from one read of each query quad, in four
+      // independent wrapping chains per chunk (the sum is exact in any order);
+      // past hd the key values are zero, and the query read is clamped into
+      // the row
+      int64_t part[P][4];
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      int64_t acc = 0;
-      if (VEC) {
+      for (int p = 0; p < P; ++p)
 #pragma unroll
-        for (int t = 0; t < kPer / 4; ++t) {
-          const uint32_t d = 4 * li + 64 * t;
-          if (d < hd) {
-            const int4 q = *reinterpret_cast<const int4*>(qg + d);
-            acc = mac(acc, q.x, kr[p][4 * t]);
-            acc = mac(acc, q.y, kr[p][4 * t + 1]);
-            acc = mac(acc, q.z, kr[p][4 * t + 2]);
-            acc = mac(acc, q.w, kr[p][4 * t + 3]);
-          }
+        for (int c = 0; c < 4; ++c) part[p][c] = 0;
+#pragma unroll
+      for (int t = 0; t < kPer / 4; ++t) {
+        const uint32_t d = 4 * li + 64 * t;
+        const int4 q = *reinterpret_cast<const int4*>(qg + (d < hd ? d : 0));
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          const int c = t & 3;
+          part[p][c] = mac(part[p][c], q.x, kr[p][4 * t]);
+          part[p][c] = mac(part[p][c], q.y, kr[p][4 * t + 1]);
+          part[p][c] = mac(part[p][c], q.z, kr[p][4 * t + 2]);
+          part[p][c] = mac(part[p][c], q.w, kr[p][4 * t + 3]);
         }
-      } else {
+      }
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        accs[p] = int64_t(uint64_t(part[p][0]) + uint64_t(part[p][1]) + uint64_t(part[p][2]) + uint64_t(part[p][3]));
+    } else {
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        int64_t acc = 0;
 #pragma unroll
         for (int t = 0; t < kPer; ++t) {
           const uint32_t d = li + 16 * t;
           if (d < hd) acc = mac(acc, qg[d], kr[p][t]);
         }
+        accs[p] = acc;
       }
-      acc = int64_t(row16_reduce(uint64_t(acc), OpWrapAdd()));  // the 16 lanes of this key row
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) accs[p] = int64_t(row16_reduce(uint64_t(accs[p]), OpWrapAdd()));  // the 16 lanes of a key row
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t acc = accs[p];
       if (li == 0) {
         const uint64_t j = r0 + p * kAttnScoreRows + grp;
         const int32_t sc = requant(acc);

@@ -2051,8 +2051,14 @@ void enqueue_fused_batch(det_model* m, BatchWs& b, uint32_t n) {
     const auto& F = m->fused[l];
     det::launch_gemv_dec_batch(F.qkv, b.limbs_x, n, nullptr, 0, b.qkv_acc, b.qkv_stride, 0, nullptr, 0, st);
     det::launch_dec_attention(batch_attn_args(m, b, l, n), st);
-    det::launch_dec_acc_limbs(b.attn_acc, L.num_heads * L.head_dim, b.attn_stride, n, b.limbs_o, L.o->kpad, st);
-    det::launch_gemv_dec_batch(*L.o, b.limbs_o, n, nullptr, 0, b.o_acc, H, 0, nullptr, 0, st);
+    // the O projection reads the weighted-sum accumulators directly where
+    // its kernel takes them (the scores kernel clears them at the next layer)
+    if (det::gemv_dec_batch_in64_ok(*L.o, n, b.attn_stride)) {
+      det::launch_gemv_dec_batch_in64(*L.o, b.attn_acc, b.attn_stride, n, b.o_acc, H, st);
+    } else {
+      det::launch_dec_acc_limbs(b.attn_acc, L.num_heads * L.head_dim, b.attn_stride, n, b.limbs_o, L.o->kpad, st);
+      det::launch_gemv_dec_batch(*L.o, b.limbs_o, n, nullptr, 0, b.o_acc, H, 0, nullptr, 0, st);
+    }
     det::launch_dec_residual_norm(b.o_acc, b.x, b.normed, L.post_attn_ln, false, 0, L.pre_ff_ln, H, L.eps, b.limbs_x,
                                   kpad_x, st, n);
     det::launch_gemv_dec_batch(F.gateup, b.limbs_x, n, b.hbuf, b.ff_stride, nullptr, 0, 1, b.limbs_ff, L.down->kpad, st);

@@ -143,6 +143,14 @@ void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int6
 void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                            int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
                            hipStream_t s);
+// The same into Q32.32 accumulators (acc + t * acc_ld, added atomically)
+// from activation rows given as wrapped Q32.32 accumulators (acc_in + t *
+// in_ld, requantized on load): no limb planes in between. Applies when
+// gemv_dec_batch_in64_ok: int8 or digit-plane weights with K a multiple of
+// 128, in_ld even, at least 5 tokens in every pass of 16.
+bool gemv_dec_batch_in64_ok(const DevMatrix& W, uint32_t ntok, uint64_t in_ld);
+void launch_gemv_dec_batch_in64(const DevMatrix& W, const int64_t* acc_in, uint64_t in_ld, uint32_t ntok,
+                                int64_t* acc, uint64_t acc_ld, hipStream_t s);
 
 // The residual norm that precedes a batch-1 decode GEMV, computed by the GEMV
 // itself: x' = add_sat(x_in, rmsnorm(requant(src)) * w_post) [* scalar], and

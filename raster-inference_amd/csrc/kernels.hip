@@ -954,16 +954,22 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_norm(DecNormIn ni, const int8_
 // and A loads are issued before the current step's MFMAs, one barrier per
 // step). Outputs as in k_gemv_dec; kchunks splits K across workgroups
 // (atomic outputs only).
-template <int EPI, int NG, bool DG>
+// IN64: the activation rows are wrapped Q32.32 accumulator rows (row stride
+// in_ld, even; K a multiple of 128 and equal to kpad), requantized and split
+// into limbs while a step's A tiles are written to LDS: each thread loads
+// 2 NG consecutive accumulators of one token (16-byte loads) and writes their
+// four limb bytes.
+template <int EPI, int NG, bool DG, bool IN64 = false>
 __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
     int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
-    int8_t* __restrict__ out_limbs, uint64_t out_kpad, int lp_arg) {
+    int8_t* __restrict__ out_limbs, uint64_t out_kpad, int lp_arg, const int64_t* __restrict__ acc_in = nullptr,
+    uint64_t in_ld = 0) {
   const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   __shared__ v4i al[2][NG][2][64];  // [buffer][token group][half][lane]
   const int planes = 1 << lp;  // digit planes
-  constexpr int CH = (NG * 2 * 64 + 255) / 256;  // A chunks per thread and step
+  constexpr int CH = IN64 ? NG : (NG * 2 * 64 + 255) / 256;  // A loads (16 bytes) per thread and step
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
   const uint64_t nsteps = kpad / 128;
@@ -982,14 +988,58 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
   // never written), so the loads issue back to back without exec-masked
   // branches between them.
   const v4i* asrc[CH];
+  // IN64: token itok, columns icol .. icol + 2 NG - 1 of every K step
+  constexpr uint32_t VPT = 2 * NG, TPR = 128 / VPT;
+  const uint32_t itok = threadIdx.x / TPR, icol = (threadIdx.x % TPR) * VPT;
+  if (IN64) {
+    const int64_t* row = acc_in + uint64_t(itok < ntok ? itok : 0) * in_ld + icol;
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const uint32_t e = threadIdx.x + 256 * c;
-    const uint32_t ln = e & 63, h = (e >> 6) & 1, tg = e >> 7;
-    const bool on = 4 * tg + ((ln & 15) >> 2) < ntok;
-    asrc[c] = reinterpret_cast<const v4i*>(limbs + (on ? uint64_t(16 * tg + (ln & 15)) * kpad : 0) +
-                                           32 * (ln >> 4) + 16 * h);
+    for (int c = 0; c < CH; ++c) asrc[c] = reinterpret_cast<const v4i*>(row + 2 * c);
+  } else {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const uint32_t e = threadIdx.x + 256 * c;
+      const uint32_t ln = e & 63, h = (e >> 6) & 1, tg = e >> 7;
+      const bool on = 4 * tg + ((ln & 15) >> 2) < ntok;
+      asrc[c] = reinterpret_cast<const v4i*>(limbs + (on ? uint64_t(16 * tg + (ln & 15)) * kpad : 0) +
+                                             32 * (ln >> 4) + 16 * h);
+    }
   }
+  // a K step's A loads sit 128 columns apart: 8 v4i of limb bytes, 64 of accumulators
+  constexpr uint64_t ASTEP = IN64 ? 64 : 8;
+  // LDS bytes of limb 0 of this thread's columns (lane 16 g + 4 ti + j of
+  // token group tg, half h, byte b; limb j adds 16 j)
+  const uint32_t lds_in64 = (((itok >> 2) * 2 + ((icol >> 4) & 1)) * 64 + 16 * (icol >> 5) + 4 * (itok & 3)) * 16 +
+                            (icol & 15);
+  auto store_a = [&](int buf, const v4i* ar) {
+    if (IN64) {
+      uint32_t u[VPT];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        u[2 * c] = uint32_t(requant(int64_t(uint64_t(uint32_t(ar[c][0])) | uint64_t(uint32_t(ar[c][1])) << 32))) ^
+                   0x00808080u;
+        u[2 * c + 1] =
+            uint32_t(requant(int64_t(uint64_t(uint32_t(ar[c][2])) | uint64_t(uint32_t(ar[c][3])) << 32))) ^
+            0x00808080u;
+      }
+      char* dst = reinterpret_cast<char*>(&al[buf][0][0][0]) + lds_in64;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t w[VPT / 4];
+#pragma unroll
+        for (int v = 0; v < int(VPT / 4); ++v)
+          w[v] = ((u[4 * v] >> (8 * j)) & 0xffu) | ((u[4 * v + 1] >> (8 * j)) & 0xffu) << 8 |
+                 ((u[4 * v + 2] >> (8 * j)) & 0xffu) << 16 | ((u[4 * v + 3] >> (8 * j)) & 0xffu) << 24;
+        if (VPT == 8)
+          *reinterpret_cast<uint2*>(dst + 16 * j) = make_uint2(w[0], w[VPT / 4 - 1]);
+        else
+          *reinterpret_cast<uint32_t*>(dst + 16 * j) = w[0];
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) (&al[buf][0][0][0])[threadIdx.x + 256 * c] = ar[c];
+    }
+  };
   // the four waves take four consecutive virtual tiles (digit plane p of tile
   // t is virtual tile t * planes + p), whole tiles per workgroup pass
   const uint64_t vtiles = ntiles << lp;
@@ -1007,19 +1057,18 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
       b0 = __builtin_nontemporal_load(bp + cs0 * 128);
       b1 = __builtin_nontemporal_load(bp + cs0 * 128 + kHalfV4);
 #pragma unroll
-      for (int c = 0; c < CH; ++c) ar[c] = asrc[c][cs0 * 8];
+      for (int c = 0; c < CH; ++c) ar[c] = asrc[c][cs0 * ASTEP];
     }
     for (uint64_t s = cs0; s < cs1; ++s) {
       const int buf = int((s - cs0) & 1);
-#pragma unroll
-      for (int c = 0; c < CH; ++c) (&al[buf][0][0][0])[threadIdx.x + 256 * c] = ar[c];
+      store_a(buf, ar);
       __syncthreads();
       v4i n0 = zero, n1 = zero;
       if (s + 1 < cs1) {
         n0 = __builtin_nontemporal_load(bp + (s + 1) * 128);
         n1 = __builtin_nontemporal_load(bp + (s + 1) * 128 + kHalfV4);
 #pragma unroll
-        for (int c = 0; c < CH; ++c) ar[c] = asrc[c][(s + 1) * 8];
+        for (int c = 0; c < CH; ++c) ar[c] = asrc[c][(s + 1) * ASTEP];
       }
 #pragma unroll
       for (int tg = 0; tg < NG; ++tg) {
@@ -2402,7 +2451,7 @@ static uint64_t device_cus() {
 template <int NG>
 static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                                int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
-                               hipStream_t s) {
+                               hipStream_t s, const int64_t* acc_in = nullptr, uint64_t in_ld = 0) {
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
   const void* fn = epilogue == 1 ? reinterpret_cast<const void*>(&k_gemv_dec_wg<1, NG, false>)
                                  : reinterpret_cast<const void*>(&k_gemv_dec_wg<0, NG, false>);
@@ -2416,17 +2465,40 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
   if (acc)
     while (groups * kc * 2 <= target && nsteps >= uint64_t(kc) * 2 * 2) kc *= 2;
   const uint64_t g = std::min<uint64_t>(groups, std::max<uint64_t>(cap / kc, 1));
-#define DET_DEC_WG(E, DG)                                                                                       \
-  hipLaunchKernelGGL((k_gemv_dec_wg<E, NG, DG>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale, W.rowsum,  \
-                     limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, plane_log2(W))
-  if (epilogue == 1) {
-    if (W.planes == 1) DET_DEC_WG(1, false);
-    else DET_DEC_WG(1, true);
+#define DET_DEC_WG(E, DG, IN)                                                                                    \
+  hipLaunchKernelGGL((k_gemv_dec_wg<E, NG, DG, IN>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale,        \
+                     W.rowsum, limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad,      \
+                     plane_log2(W), acc_in, in_ld)
+  if (acc_in) {
+    if (W.planes == 1) DET_DEC_WG(0, false, true);
+    else DET_DEC_WG(0, true, true);
+  } else if (epilogue == 1) {
+    if (W.planes == 1) DET_DEC_WG(1, false, false);
+    else DET_DEC_WG(1, true, false);
   } else {
-    if (W.planes == 1) DET_DEC_WG(0, false);
-    else DET_DEC_WG(0, true);
+    if (W.planes == 1) DET_DEC_WG(0, false, false);
+    else DET_DEC_WG(0, true, false);
   }
 #undef DET_DEC_WG
+}
+
+bool gemv_dec_batch_in64_ok(const DevMatrix& W, uint32_t ntok, uint64_t in_ld) {
+  const uint32_t tail = ntok % 16;
+  return W.storage == kInt8 && W.rows > 0 && W.cols == W.kpad && in_ld % 2 == 0 && ntok >= 5 &&
+         (tail == 0 || tail >= 5);
+}
+
+void launch_gemv_dec_batch_in64(const DevMatrix& W, const int64_t* acc_in, uint64_t in_ld, uint32_t ntok,
+                                int64_t* acc, uint64_t acc_ld, hipStream_t s) {
+  if (!gemv_dec_batch_in64_ok(W, ntok, in_ld) || !acc)
+    throw std::invalid_argument("launch_gemv_dec_batch_in64: shape outside the kernel's range");
+  for (uint32_t t0 = 0; t0 < ntok; t0 += 16) {
+    const uint32_t nt = ntok - t0 < 16 ? ntok - t0 : 16;
+    const int64_t* a_in = acc_in + uint64_t(t0) * in_ld;
+    int64_t* a = acc + uint64_t(t0) * acc_ld;
+    if (nt <= 8) launch_gemv_dec_wg<2>(W, nullptr, nt, nullptr, 0, a, acc_ld, 0, nullptr, 0, s, a_in, in_ld);
+    else launch_gemv_dec_wg<4>(W, nullptr, nt, nullptr, 0, a, acc_ld, 0, nullptr, 0, s, a_in, in_ld);
+  }
 }
 
 void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
