@@ -258,9 +258,47 @@ def e4b_ple_decode(ctx, rd, args) -> dict:
     ctx.synchronize()
     dec_s = time.perf_counter() - t0
     log(f"[bench] E4B + PLE decode {steps} steps in {dec_s * 1e3:.1f} ms ({steps / dec_s:.1f} tok/s)")
+    del sess
+    # 16 sequences with ragged prompts (seeded uniform in [32, 512]) batched:
+    # the first steps through the fused and the per-op batched schedules on
+    # copies of the same sessions (commitments compared), then timed fused steps
+    n, bsteps, cmp_steps = 16, 32, 4
+    lens = rng.integers(32, 513, size=n)
+    prompts = [rng.integers(0, 262144, size=int(k)).tolist() for k in lens]
+    bs = [model.session(int(k) + bsteps + cmp_steps + 1) for k in lens]
+    toks = [s.prefill(p, rd.DET_COMMIT_NONE).next_token for s, p in zip(bs, prompts)]
+    fa, pa = [s.clone() for s in bs], [s.clone() for s in bs]
+    ta, tp = toks[:], toks[:]
+    same = True
+    ctx.synchronize()
+    per_op_s = 0.0
+    for _ in range(cmp_steps):
+        ra = rd.decode_batch(fa, ta, rd.DET_COMMIT_ACTIVATIONS)
+        t0 = time.perf_counter()
+        rp = rd.decode_batch(pa, tp, rd.DET_COMMIT_ACTIVATIONS | rd.DET_DECODE_PER_OP)
+        per_op_s += time.perf_counter() - t0
+        same &= [(r.activation, r.logits, r.next_token) for r in ra] == [(r.activation, r.logits, r.next_token)
+                                                                       for r in rp]
+        ta, tp = [r.next_token for r in ra], [r.next_token for r in rp]
+    del fa, pa
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(bsteps):
+        toks = [r.next_token for r in rd.decode_batch(bs, toks, rd.DET_COMMIT_NONE)]
+    ctx.synchronize()
+    bat_s = time.perf_counter() - t0
+    log(f"[bench] E4B + PLE ragged x{n}: {bsteps} fused batched steps in {bat_s * 1e3:.0f} ms "
+        f"({n * bsteps / bat_s:.1f} tok/s aggregate); per-op batched steps {n * cmp_steps / per_op_s:.1f} tok/s; "
+        f"identical commitments: {same}")
     return {"ple_width": 256, "fused_step": model.fused_decode, "decode_tok_s": round(steps / dec_s, 2),
             "decode_ms_per_token": round(dec_s / steps * 1e3, 3), "prefill_tok_s": round(args.prompt_len / prefill_s, 1),
-            "prompt": args.prompt_len, "decode_steps": steps}
+            "prompt": args.prompt_len, "decode_steps": steps,
+            "ragged": {"sequences": n, "steps": bsteps, "prompt_lens": [int(k) for k in lens],
+                       "fused_aggregate_tok_s": round(n * bsteps / bat_s, 1),
+                       "per_op_aggregate_tok_s": round(n * cmp_steps / per_op_s, 1),
+                       "fused_equals_per_op": bool(same),
+                       "compared": f"activation and logits commitments and tokens of the first {cmp_steps} steps "
+                                   f"of every sequence, fused batched step against the per-op batched step"}}
 
 
 def e4b_decode(ctx, rd, args, model, load_s) -> dict:

@@ -95,10 +95,16 @@ void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, ui
 // src (wrapping Q32.32 accumulators) is cleared after use. x_src defaults to
 // x (in place). x_out (optional) receives a copy of the new x (row stride H
 // per sequence).
+// Without w_next, x_limbs also writes x's limb planes to limbs.
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
                               uint64_t kpad, hipStream_t s, uint32_t nseq = 1, int32_t* x_out = nullptr,
-                              const int32_t* x_src = nullptr);
+                              const int32_t* x_src = nullptr, bool x_limbs = false);
+// Limb planes (plane stride kpad, 4 planes per row) of nseq int32 rows of k
+// columns (row stride ld); with gate_in, of mul_sat(gelu(x), gate_in) per
+// element (gate_in row stride in_ld): the per-layer input gate.
+void launch_dec_row_limbs(const int32_t* x, uint64_t k, uint64_t ld, uint32_t nseq, int8_t* limbs, uint64_t kpad,
+                          hipStream_t s, const int32_t* gate_in = nullptr, uint64_t in_ld = 0);
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s);
 // Whether launch_dec_attention runs the statistics as a separate pass.
 bool dec_attention_split(const AttnDecArgs& a);

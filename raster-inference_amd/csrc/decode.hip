@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <stdexcept>
 
 #include "decode.h"
 #include "det_arith.h"
@@ -107,14 +108,15 @@ __global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* 
 // layer); normed = rmsnorm(x, w_next) (det_kernels.rs:1058-1075, 1108-1133).
 // src holds the projection's wrapping accumulators and is cleared after use.
 // x_src may equal x (each thread reads its elements before writing them).
-// Without w_next only x is written (the next norm is left to a later kernel).
+// Without w_next only x is written (the next norm is left to a later kernel),
+// and with x_limbs also x's limb planes (the input of a GEMV on x itself).
 template <int NT, int EPT>
 __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ src, const int32_t* x_src,
                                                            int32_t* x, int32_t* __restrict__ normed,
                                                            const int32_t* __restrict__ w_post, int has_scalar,
                                                            int32_t scalar, const int32_t* __restrict__ w_next,
                                                            uint64_t H, int64_t eps, int8_t* __restrict__ limbs,
-                                                           uint64_t kpad, int32_t* __restrict__ x_out) {
+                                                           uint64_t kpad, int32_t* __restrict__ x_out, int x_limbs) {
   __shared__ int64_t red[NT / 64];
   __shared__ int32_t bc;
   const uint32_t seq = blockIdx.y;
@@ -150,7 +152,19 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
     if (x_out && c < H) x_out[c] = v;
     ss = add_sat64_nn(ss, sq_term(c < H ? v : 0));
   }
-  if (!w_next) return;  // uniform over the workgroup
+  if (!w_next) {  // uniform over the workgroup
+    if (x_limbs)
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const uint64_t c = threadIdx.x + uint64_t(NT) * e;
+        if (c < H) {
+          const uint32_t u = uint32_t(xv[e]) ^ 0x00808080u;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) limbs[j * kpad + c] = int8_t(uint8_t(u >> (8 * j)));
+        }
+      }
+    return;
+  }
   const int32_t s2 = blk_rms_scale<NT>(ss, H, eps, red, &bc);
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
@@ -969,6 +983,33 @@ __global__ __launch_bounds__(256) void k_dec_acc_limbs(int64_t* __restrict__ acc
   for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(limbs + (t * 4 + j) * kpad + c0) = packed[j];
 }
 
+// Limb planes of n int32 rows (grid y = row t, x at x + t * ld), 4 columns
+// per thread; with GATE the row is first the per-layer input gate's
+// mul_sat(gelu(x), in) (det_kernels.rs:1108-1128) with in at in + t * in_ld.
+// Columns k..kpad-1 get zero bytes (their weights are zero).
+template <bool GATE>
+__global__ __launch_bounds__(256) void k_dec_row_limbs(const int32_t* __restrict__ x, uint64_t k, uint64_t ld,
+                                                       const int32_t* __restrict__ in, uint64_t in_ld,
+                                                       int8_t* __restrict__ limbs, uint64_t kpad) {
+  const uint64_t c0 = (uint64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (c0 >= kpad) return;
+  const uint64_t t = blockIdx.y;
+  uint32_t packed[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint64_t c = c0 + e;
+    if (c < k) {
+      int32_t v = x[t * ld + c];
+      if (GATE) v = mul_sat(gelu_act(v), in[t * in_ld + c]);
+      const uint32_t u = uint32_t(v) ^ 0x00808080u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) packed[j] |= ((u >> (8 * j)) & 0xffu) << (8 * e);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(limbs + (t * 4 + j) * kpad + c0) = packed[j];
+}
+
 // Up to kSetWords 64-bit words by value (within the 4 KB of kernel arguments).
 constexpr uint32_t kSetWords = 448;
 struct SetWords {
@@ -1029,9 +1070,10 @@ void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, ui
 }
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
-                              uint64_t kpad, hipStream_t s, uint32_t nseq, int32_t* x_out, const int32_t* x_src) {
+                              uint64_t kpad, hipStream_t s, uint32_t nseq, int32_t* x_out, const int32_t* x_src,
+                              bool x_limbs) {
   DET_ROW_DISPATCH(k_dec_residual_norm, src, x_src ? x_src : x, x, normed, w_post, int(has_scalar), scalar, w_next, H,
-                   eps, limbs, kpad, x_out);
+                   eps, limbs, kpad, x_out, int(x_limbs && !w_next));
 }
 #undef DET_ROW_DISPATCH
 // Window chunks per attention workgroup: a.rows_mul when set (1, 2 or 4),
@@ -1159,6 +1201,17 @@ void launch_dec_set_trig(const StepState* st, uint32_t nseq, const RopeTable* ta
 void launch_dec_acc_limbs(int64_t* acc, uint64_t k, uint64_t ld, uint32_t nseq, int8_t* limbs, uint64_t kpad,
                           hipStream_t s) {
   if (nseq && kpad) hipLaunchKernelGGL(k_dec_acc_limbs, dim3(nblk(kpad / 4, 256), nseq), dim3(256), 0, s, acc, k, ld, limbs, kpad);
+}
+void launch_dec_row_limbs(const int32_t* x, uint64_t k, uint64_t ld, uint32_t nseq, int8_t* limbs, uint64_t kpad,
+                          hipStream_t s, const int32_t* gate_in, uint64_t in_ld) {
+  if (!nseq || !kpad) return;
+  if (kpad % 4) throw std::invalid_argument("launch_dec_row_limbs: kpad must be a multiple of 4");
+  if (gate_in)
+    hipLaunchKernelGGL(k_dec_row_limbs<true>, dim3(nblk(kpad / 4, 256), nseq), dim3(256), 0, s, x, k, ld, gate_in,
+                       in_ld, limbs, kpad);
+  else
+    hipLaunchKernelGGL(k_dec_row_limbs<false>, dim3(nblk(kpad / 4, 256), nseq), dim3(256), 0, s, x, k, ld, x, 0,
+                       limbs, kpad);
 }
 void launch_copy_rows(const int32_t* src, uint64_t w, uint64_t n, int32_t* const* dst, hipStream_t s) {
   if (n && w) hipLaunchKernelGGL(k_copy_rows, dim3(nblk((w + 3) / 4, 256), unsigned(n)), dim3(256), 0, s, src, w, dst);

@@ -1719,6 +1719,13 @@ struct BatchWs {
   det::AttnStat* attn_stats = nullptr;  // [cap][score_heads]
   int64_t *qkv_acc = nullptr, *attn_acc = nullptr, *o_acc = nullptr, *ff_acc = nullptr;
   int8_t *limbs_x = nullptr, *limbs_o = nullptr, *limbs_ff = nullptr;
+  // per-layer inputs (PLE models): every layer's inputs of each sequence's
+  // token [cap][L*P], the model projection rows [cap][L*P], the gate rows
+  // [cap][P], the projection accumulators [cap][hidden] and the limb planes
+  // of the embedded row (model projection) or of the gate (layer projection)
+  int32_t *ple_in = nullptr, *ple_pp = nullptr, *ple_g = nullptr;
+  int64_t* ple_acc = nullptr;
+  int8_t* limbs_p = nullptr;
   std::vector<void*> owned;
   uint32_t graph_n = 0;
   hipGraph_t graph = nullptr;
@@ -1976,6 +1983,18 @@ void ensure_fused_batch(det_model* m, BatchWs& b, uint64_t need) {
     HIPC(hipMemsetAsync(b.limbs_o, 0, T * 4 * kpo, zst));
     HIPC(hipMemsetAsync(b.limbs_ff, 0, T * 4 * kff, zst));
     HIPC(hipMemsetAsync(b.limbs_x, 0, T * 4 * m->fused[0].qkv.kpad, zst));
+    if (m->has_ple) {
+      const uint64_t LP = m->layers.size() * m->ple_dim;
+      uint64_t kp = m->ple_proj_full->kpad;
+      for (const GLayer& L : m->layers)
+        if (L.has_ple) kp = std::max(kp, L.ple_proj->kpad);
+      b.ple_in = b.alloc<int32_t>(T * LP);
+      b.ple_pp = b.alloc<int32_t>(T * LP);
+      b.ple_g = b.alloc<int32_t>(T * m->ple_dim);
+      b.ple_acc = b.alloc<int64_t>(T * H);
+      b.limbs_p = b.alloc<int8_t>(T * 4 * kp);
+      HIPC(hipMemsetAsync(b.ple_acc, 0, T * H * 8, zst));
+    }
     b.fused = true;
   }
   if (need > b.grid_cap) {
@@ -2046,6 +2065,19 @@ void enqueue_fused_batch(det_model* m, BatchWs& b, uint32_t n) {
   det::launch_dec_set_trig(st_dev, n, m->rope_tables_dev, uint32_t(m->rope_tables.size()), m->trig_pairs, b.trig, st);
   det::launch_dec_embed(*m->embedding, st_dev, m->embed_scale, H, b.x, b.dec_in, m->layers[0].in_ln, m->eps, b.normed,
                         b.limbs_x, kpad_x, st, n);
+  const uint64_t P = m->ple_dim, LP = m->layers.size() * P;
+  if (m->has_ple) {
+    // every layer's per-layer input of each sequence's token (det_decode_ple_input,
+    // det_kernels.rs:1142-1208), rows [n][L*P] as in the single-sequence step
+    const uint64_t id_stride = sizeof(det::StepState) / sizeof(uint32_t);
+    det::launch_gather_rows(*m->ple_tok, &st_dev->token, n, 0, LP, m->ple_embedding_scale, b.ple_in, LP, st, id_stride);
+    det::launch_dec_row_limbs(b.dec_in, H, H, n, b.limbs_p, m->ple_proj_full->kpad, st);
+    det::launch_gemv_dec_batch(*m->ple_proj_full, b.limbs_p, n, b.ple_pp, LP, nullptr, 0, 0, nullptr, 0, st);
+    det::launch_scale(b.ple_pp, n * LP, m->ple_projection_scalar, st);
+    det::launch_rmsnorm(b.ple_pp, n * m->layers.size(), P, P, m->ple_proj_norm, m->eps, st);
+    det::launch_add_sat(b.ple_in, b.ple_pp, n * LP, st);
+    det::launch_scale(b.ple_in, n * LP, m->ple_input_scale, st);
+  }
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
     const auto& F = m->fused[l];
@@ -2064,13 +2096,34 @@ void enqueue_fused_batch(det_model* m, BatchWs& b, uint32_t n) {
     det::launch_gemv_dec_batch(F.gateup, b.limbs_x, n, b.hbuf, b.ff_stride, nullptr, 0, 1, b.limbs_ff, L.down->kpad, st);
     det::launch_gemv_dec_batch(*L.down, b.limbs_ff, n, nullptr, 0, b.ff_acc, H, 0, nullptr, 0, st);
     const int32_t* w_next = l + 1 < m->layers.size() ? m->layers[l + 1].in_ln : m->final_norm;
-    det::launch_dec_residual_norm(b.ff_acc, b.x, b.normed, L.post_ff_ln, L.layer_scalar.has_value(),
-                                  L.layer_scalar.value_or(0), w_next, H, L.eps, b.limbs_x, kpad_x, st, n);
+    if (m->has_ple && L.has_ple) {
+      // x += norm(down) (with x's limb planes); then the per-layer input block
+      // (det_kernels.rs:1108-1128): x += norm(proj(gelu(gate(x)) * ple_in)),
+      // the layer scalar and the next norm
+      det::launch_dec_residual_norm(b.ff_acc, b.x, b.normed, L.post_ff_ln, false, 0, nullptr, H, L.eps, b.limbs_x,
+                                    kpad_x, st, n, nullptr, nullptr, true);
+      det::launch_gemv_dec_batch(*L.ple_gate, b.limbs_x, n, b.ple_g, P, nullptr, 0, 0, nullptr, 0, st);
+      det::launch_dec_row_limbs(b.ple_g, P, P, n, b.limbs_p, L.ple_proj->kpad, st, b.ple_in + l * P, LP);
+      det::launch_gemv_dec_batch(*L.ple_proj, b.limbs_p, n, nullptr, 0, b.ple_acc, H, 0, nullptr, 0, st);
+      det::launch_dec_residual_norm(b.ple_acc, b.x, b.normed, L.ple_post_norm, L.layer_scalar.has_value(),
+                                    L.layer_scalar.value_or(0), w_next, H, L.eps, b.limbs_x, kpad_x, st, n);
+    } else {
+      det::launch_dec_residual_norm(b.ff_acc, b.x, b.normed, L.post_ff_ln, L.layer_scalar.has_value(),
+                                    L.layer_scalar.value_or(0), w_next, H, L.eps, b.limbs_x, kpad_x, st, n);
+    }
   }
   det::launch_gemv_dec_batch(*m->lm_head, b.limbs_x, n, b.logits, V, nullptr, 0, 0, nullptr, 0, st);
   if (m->softcap) det::launch_dec_softcap(b.logits, n * V, *m->softcap, st);
   det::launch_copy_rows(b.logits, V, n, reinterpret_cast<int32_t* const*>(b.desc + D.logit_dst), st);
   det::launch_argmax_rows(b.logits, n, V, b.am_keys, b.next, st);
+}
+
+// Whether a model's batched steps take the fused schedule: the single-sequence
+// fused step's conditions, and for per-layer inputs a model projection of
+// exactly L*P rows (the per-sequence rows [L*P] of the step's PLE buffers).
+bool batch_fused_ok(const det_model* m) {
+  if (!m->fused_ok) return false;
+  return !m->has_ple || m->ple_proj_full->rows == m->layers.size() * m->ple_dim;
 }
 
 void decode_batch_fused(det_session* const* ss, uint64_t n, const uint32_t* tokens, uint32_t flags,
@@ -3321,7 +3374,7 @@ int det_session_decode_batch(det_session_t* const* sessions, uint64_t n, const u
   return guarded(sessions[0]->m->ctx, [&] {
     std::vector<det_decode_result_t> tmp(out ? 0 : n);
     // (the batched fused step has no PLE stage: PLE models batch per op)
-    if (sessions[0]->m->fused_ok && !sessions[0]->m->has_ple && !(flags & DET_DECODE_PER_OP))
+    if (batch_fused_ok(sessions[0]->m) && !(flags & DET_DECODE_PER_OP))
       decode_batch_fused(sessions, n, tokens, flags, out ? out : tmp.data());
     else
       decode_batch(sessions, n, tokens, flags, out ? out : tmp.data());

@@ -333,7 +333,8 @@ void launch_kv_append(const int32_t* k, const int32_t* v, uint64_t w, uint64_t n
 uint64_t argmax_rows_scratch(uint64_t rows, uint64_t n);
 void launch_argmax_rows(const int32_t* x, uint64_t rows, uint64_t n, int64_t* scratch, uint32_t* out, hipStream_t s);
 void launch_gather_rows(const DevMatrix& M, const uint32_t* ids, uint64_t m, uint64_t col0,
-                        uint64_t ncols, int32_t scale, int32_t* out, uint64_t ld_out, hipStream_t s);
+                        uint64_t ncols, int32_t scale, int32_t* out, uint64_t ld_out, hipStream_t s,
+                        uint64_t ids_stride = 1);
 
 // First index of the maximum; `scratch` holds >= 2*ceil(n/1024) int64 values.
 void launch_argmax(const int32_t* x, uint64_t n, int64_t* scratch, uint32_t* out, hipStream_t s);

@@ -2204,12 +2204,13 @@ __device__ __forceinline__ int32_t wgt_at(const DevMatrix& M, uint64_t r, uint64
   if (M.storage == kI16) return int32_t(static_cast<const int16_t*>(M.w)[r * M.cols + c]);
   return static_cast<const int32_t*>(M.w)[r * M.cols + c];
 }
-__global__ void k_gather_rows(DevMatrix M, const uint32_t* __restrict__ ids, uint64_t m, uint64_t col0,
-                              uint64_t ncols, int32_t scale, int32_t* __restrict__ out, uint64_t ld_out) {
+__global__ void k_gather_rows(DevMatrix M, const uint32_t* __restrict__ ids, uint64_t ids_stride, uint64_t m,
+                              uint64_t col0, uint64_t ncols, int32_t scale, int32_t* __restrict__ out,
+                              uint64_t ld_out) {
   const uint64_t c = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint64_t t = blockIdx.y;
   if (c >= ncols || t >= m) return;
-  out[t * ld_out + c] = mul_sat(wgt_at(M, ids[t], col0 + c), scale);
+  out[t * ld_out + c] = mul_sat(wgt_at(M, ids[t * ids_stride], col0 + c), scale);
 }
 
 __global__ __launch_bounds__(256) void k_argmax_partial(const int32_t* __restrict__ x, uint64_t n,
@@ -2875,10 +2876,10 @@ void launch_softcap(int32_t* x, uint64_t n, int32_t cap, hipStream_t s) {
   if (n) hipLaunchKernelGGL(k_softcap, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, n, cap);
 }
 void launch_gather_rows(const DevMatrix& M, const uint32_t* ids, uint64_t m, uint64_t col0, uint64_t ncols,
-                        int32_t scale, int32_t* out, uint64_t ld_out, hipStream_t s) {
+                        int32_t scale, int32_t* out, uint64_t ld_out, hipStream_t s, uint64_t ids_stride) {
   if (!m || !ncols) return;
-  hipLaunchKernelGGL(k_gather_rows, dim3(blocks_for(ncols, 256), unsigned(m)), dim3(256), 0, s, M, ids, m, col0,
-                     ncols, scale, out, ld_out);
+  hipLaunchKernelGGL(k_gather_rows, dim3(blocks_for(ncols, 256), unsigned(m)), dim3(256), 0, s, M, ids, ids_stride, m,
+                     col0, ncols, scale, out, ld_out);
 }
 void launch_kv_append(const int32_t* k, const int32_t* v, uint64_t w, uint64_t n, int32_t* const* kdst,
                       int32_t* const* vdst, hipStream_t s) {

@@ -173,3 +173,54 @@ def test_batch_of_16_long_windows_split_softmax(ctx):
     gm = sharing_model(ctx)
     prompts = ragged_prompts(16, 300, 640, 1000, seed=33)
     run_batch_vs_solo(gm, 1000, prompts, steps=3, max_tokens=700, solo_flags=rd.DET_DECODE_PER_OP)
+
+
+def ple_sharing_model(ctx):
+    """Per-layer inputs (width 64) with KV-sharing donors, softcap and layer scalars."""
+    cfg = {"text_config": {
+        "enable_moe_block": False, "head_dim": 64, "hidden_activation": "gelu_pytorch_tanh", "hidden_size": 256,
+        "intermediate_size": 512, "layer_types": ["sliding_attention", "full_attention", "sliding_attention",
+                                                  "full_attention"],
+        "num_attention_heads": 4, "num_hidden_layers": 4, "num_key_value_heads": 2, "num_kv_shared_layers": 2,
+        "final_logit_softcapping": 30.0, "hidden_size_per_layer_input": 64, "vocab_size_per_layer_input": 1000,
+        "rms_norm_eps": 1e-6, "sliding_window": 5, "tie_word_embeddings": False, "vocab_size": 1000,
+    }}
+    return build(ctx, cfg, fixtures.custom_model(cfg, seed=9, layer_scalars=True))
+
+
+@pytest.mark.parametrize("mode", ["graph", "eager"])
+@pytest.mark.parametrize("n", [3, 5, 16, 19])
+def test_per_layer_input_model_batch_matches_solo(ctx, n, mode):
+    # the fused batched step with the per-layer input stage (every layer's
+    # inputs of each sequence's token, then per layer the gate GEMV over the
+    # residual rows, GELU x input, the projection GEMV and the second residual
+    # norm) against solo steps through the fused single-sequence step, whose
+    # PLE block is pinned to the oracle in test_gpu_decode_fused.py
+    gm = ple_sharing_model(ctx)
+    assert gm.fused_decode
+    prompts = ragged_prompts(n, 1, 14, 1000, seed=40 + n)
+    run_batch_vs_solo(gm, 1000, prompts, steps=4, max_tokens=24, flags=rd.DET_COMMIT_ALL | MODES[mode])
+
+
+def test_per_layer_input_model_fused_batch_matches_per_op_batch(ctx):
+    gm = ple_sharing_model(ctx)
+    prompts = ragged_prompts(6, 2, 12, 1000, seed=77)
+    a = [gm.session(24) for _ in prompts]
+    b = [gm.session(24) for _ in prompts]
+    ta = [s.prefill(p).next_token for s, p in zip(a, prompts)]
+    tb = [s.prefill(p).next_token for s, p in zip(b, prompts)]
+    for step in range(5):
+        ra = rd.decode_batch(a, ta, rd.DET_COMMIT_ALL)
+        rb = rd.decode_batch(b, tb, rd.DET_COMMIT_ALL | rd.DET_DECODE_PER_OP)
+        assert [key(r) for r in ra] == [key(r) for r in rb], step
+        ta, tb = [r.next_token for r in ra], [r.next_token for r in rb]
+
+
+def test_e4b_shaped_per_layer_input_batch_of_16_matches_solo(ctx):
+    # hidden 2560, PLE width 256: the 16-token GEMVs over the model projection
+    # (L*P x H), the per-layer gate (P x H) and projection (H x P)
+    cfg = synthetic.e4b_config(layers=2, vocab=4096, sliding_window=8, ple=256)
+    gm = build(ctx, cfg, synthetic.synthetic_model_fast(cfg, seed=21, scale_max=256))
+    assert gm.fused_decode
+    prompts = ragged_prompts(16, 1, 40, 4096, seed=6)
+    run_batch_vs_solo(gm, 4096, prompts, steps=3, max_tokens=48)
