@@ -1136,6 +1136,126 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
   }
 }
 
+// Decode GEMV for 5-16 tokens (NG = 2 or 4 groups of 4) with the activation
+// limbs resident in registers. The NW waves of a workgroup split a K chunk of
+// NW * HPW half-steps (64 columns: half h of 128-column step s is half-step
+// 2 s + h); each wave loads the A operands of its HPW half-steps for all NG
+// token groups once, then streams its K share of the workgroup's weight
+// tiles: a tile's half-step operands are HPW contiguous 1 KB blocks, and the
+// next tile's are in flight while this tile's MFMAs run (no barrier between
+// the K steps). The waves' partial limb sums of a tile (int32; a limb times a
+// weight is at most 128 * 127 in magnitude, so K chunks up to 130000 columns
+// cannot wrap) are added through LDS, one LDS-only barrier per tile, and wave
+// tg (< NG) combines token group tg's sums as k_gemv_dec_wg does. Workgroup b
+// takes K chunk b % kchunks (kchunks > 1: atomic acc_out only) and tiles
+// b / kchunks + groups * j. Half-steps past kpad are read clamped to the last
+// one with zero A operands.
+template <int EPI, int NG, int NW, int HPW>
+__global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
+    const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
+    const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
+    int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
+    int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
+  __shared__ v4i red[2][NW][NG][64];  // [tile parity][wave][token group][lane]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4, i = lane & 15;
+  const uint64_t nhs = kpad / 64;
+  const uint32_t kc = blockIdx.x % kchunks;
+  const uint64_t hs0 = (uint64_t(kc) * NW + uint64_t(wave)) * HPW;
+  const uint64_t ntiles = (n_rows + 15) / 16;
+  const uint64_t groups = gridDim.x / kchunks;
+  const uint64_t t0 = blockIdx.x / kchunks;
+  const v4i zero = {0, 0, 0, 0};
+  // A operand of (half-step hs, token group tg) in lane 16 g + i: limb row
+  // 16 tg + i (token 4 tg + i / 4, limb i % 4), columns 128 s + 32 g + 16 h
+  // (clamped addresses, masked values: no predicated loads)
+  v4i ar[HPW][NG];
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    const uint64_t hs = hs0 + h;
+    const bool k_on = hs < nhs;
+    const uint64_t col = k_on ? 128 * (hs >> 1) + 32 * g + 16 * (hs & 1) : 0;
+#pragma unroll
+    for (int tg = 0; tg < NG; ++tg) {
+      const bool on = k_on && uint32_t(4 * tg + (i >> 2)) < ntok;
+      const v4i v = *reinterpret_cast<const v4i*>(limbs + uint64_t(on ? 16 * tg + i : 0) * kpad + col);
+      ar[h][tg] = on ? v : zero;
+    }
+  }
+  const uint64_t my_tiles = t0 < ntiles ? (ntiles - t0 + groups - 1) / groups : 0;
+  // this wave's first half-step operand of tile j (tiles past the end read the last tile)
+  const v4i* qw = reinterpret_cast<const v4i*>(q) + lane;
+  auto tile_of = [&](uint64_t j) {
+    const uint64_t t = t0 + groups * j;
+    return t < ntiles ? t : ntiles - 1;
+  };
+  auto hs_of = [&](int h) { return hs0 + h < nhs ? hs0 + h : nhs - 1; };
+  v4i wb[2][HPW];
+  int32_t rsr[2], scr[2];
+  // the epilogue's row sum and scale of tile j, loaded just ahead of its weights
+  auto issue = [&](int r, uint64_t j) {
+    const uint64_t t = tile_of(j);
+    const uint64_t row = t * 16 + uint64_t(i) < n_rows ? t * 16 + uint64_t(i) : n_rows - 1;
+    rsr[r] = rowsum[row];
+    scr[r] = scale[row];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) wb[r][h] = __builtin_nontemporal_load(qw + (t * nhs + hs_of(h)) * 64);
+  };
+  issue(0, 0);
+  issue(1, 1);
+  for (uint64_t j0 = 0; j0 < my_tiles; j0 += 2) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint64_t j = j0 + r;
+      if (j < my_tiles) {
+        v4i acc[NG];
+#pragma unroll
+        for (int tg = 0; tg < NG; ++tg) acc[tg] = zero;
+#pragma unroll
+        for (int h = 0; h < HPW; ++h)
+#pragma unroll
+          for (int tg = 0; tg < NG; ++tg)
+            acc[tg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ar[h][tg], wb[r][h], acc[tg], 0, 0, 0);
+        const int32_t rs = rsr[r], sc = scr[r];
+        issue(r, j + 2);
+#pragma unroll
+        for (int tg = 0; tg < NG; ++tg) red[r][wave][tg][lane] = acc[tg];
+        lds_barrier();
+        if (wave < NG) {
+          // token group tg = wave; lane 16 g + i holds the limb sums of token 4 tg + g, row i
+          v4i s = red[r][0][wave][lane];
+#pragma unroll
+          for (int w = 1; w < NW; ++w) s += red[r][w][wave][lane];
+          const int64_t p[4] = {s[0], s[1], s[2], s[3]};
+          const uint64_t tile = t0 + groups * j;
+          const uint64_t row = tile * 16 + uint64_t(i);
+          const uint32_t tok = 4 * uint32_t(wave) + uint32_t(g);
+          const bool ok = tok < ntok && row < n_rows;
+          if (acc_out) {
+            if (ok)
+              atomicAdd(reinterpret_cast<unsigned long long*>(acc_out + tok * acc_ld + row),
+                        static_cast<unsigned long long>(limb_combine(p, kc == 0 ? rs : 0, sc)));
+          } else if (EPI == 1) {
+            const int32_t rq = ok ? requant(limb_combine(p, rs, sc)) : 0;
+            const int32_t up = __shfl(rq, (lane & 48) | ((i + 8) & 15), 64);
+            if (ok && i < 8) {
+              const uint64_t f = tile * 8 + uint64_t(i);
+              const int32_t hv = mul_sat(gelu_act(rq), up);
+              out[tok * out_ld + f] = hv;
+              const uint32_t u = uint32_t(hv) ^ 0x00808080u;
+              int8_t* ol = out_limbs + uint64_t(tok) * 4 * out_kpad + f;
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj) ol[jj * out_kpad] = int8_t(uint8_t(u >> (8 * jj)));
+            }
+          } else if (ok) {
+            out[tok * out_ld + row] = requant(limb_combine(p, rs, sc));
+          }
+        }
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Prefill GEMM (det_linear_slab, det_kernels.rs:180-203): C[m][n] =
 // requantize(sum_k act[m][k] * W[n][k]) for a slab of M activation rows.
@@ -2483,6 +2603,35 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
 #undef DET_DEC_WG
 }
 
+// 5-16 tokens over single-plane weights with K of at least 24 half-steps
+// (1536 columns): k_gemv_rega, K chunks of at most 8 waves x 5 half-steps,
+// one workgroup of 8 waves per CU. False where the shape is outside its range
+// (digit planes, short K, or a K split without atomic outputs).
+template <int NG>
+static bool launch_gemv_rega(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
+                             int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
+                             hipStream_t s) {
+  const uint64_t nhs = W.kpad / 64;
+  if (W.planes != 1 || nhs < 24) return false;
+  const uint64_t kc = (nhs + 39) / 40;
+  if (kc > 1 && (!acc || epilogue != 0)) return false;
+  const uint64_t hpw = (nhs + 8 * kc - 1) / (8 * kc);
+  if (hpw < 3 || hpw > 5) return false;
+  const uint64_t ntiles = (W.rows + 15) / 16;
+  const uint64_t groups = std::min<uint64_t>(ntiles, std::max<uint64_t>(device_cus() / kc, 1));
+  const dim3 grid(unsigned(groups * kc)), block(512);
+#define DET_REGA(E, H)                                                                                          \
+  hipLaunchKernelGGL((k_gemv_rega<E, NG, 8, H>), grid, block, 0, s, W.q, W.scale, W.rowsum, limbs, W.rows, W.kpad, \
+                     uint32_t(kc), ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad)
+  if (epilogue == 1) {
+    if (hpw == 5) DET_REGA(1, 5); else if (hpw == 4) DET_REGA(1, 4); else DET_REGA(1, 3);
+  } else {
+    if (hpw == 5) DET_REGA(0, 5); else if (hpw == 4) DET_REGA(0, 4); else DET_REGA(0, 3);
+  }
+#undef DET_REGA
+  return true;
+}
+
 bool gemv_dec_batch_in64_ok(const DevMatrix& W, uint32_t ntok, uint64_t in_ld) {
   const uint32_t tail = ntok % 16;
   return W.storage == kInt8 && W.rows > 0 && W.cols == W.kpad && in_ld % 2 == 0 && ntok >= 5 &&
@@ -2514,8 +2663,12 @@ void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t nto
     int64_t* a = acc ? acc + uint64_t(t0) * acc_ld : nullptr;
     int8_t* ol = out_limbs ? out_limbs + uint64_t(t0) * 4 * out_kpad : nullptr;
     if (nt <= 4) launch_gemv_dec_ng<1>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
-    else if (nt <= 8) launch_gemv_dec_wg<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
-    else launch_gemv_dec_wg<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
+    else if (nt <= 8) {
+      if (!launch_gemv_rega<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s))
+        launch_gemv_dec_wg<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
+    } else if (!launch_gemv_rega<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s)) {
+      launch_gemv_dec_wg<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
+    }
   }
 }
 

@@ -141,6 +141,16 @@ def test_e4b_shaped_layers_batch_of_16_matches_solo(ctx, mode):
     run_batch_vs_solo(gm, 4096, prompts, steps=3, max_tokens=48, flags=rd.DET_COMMIT_ALL | MODES[mode])
 
 
+@pytest.mark.parametrize("n", [5, 7, 13])
+def test_e4b_shaped_layers_partial_batches_match_solo(ctx, n):
+    """Batches of 5-8 tokens take the two-token-group GEMV instances and
+    13 tokens a partly filled last group (E4B widths: K of 2048-10240)."""
+    cfg = synthetic.e4b_config(layers=2, vocab=4096, sliding_window=8)
+    gm = build(ctx, cfg, synthetic.synthetic_model_fast(cfg, seed=11))
+    prompts = ragged_prompts(n, 1, 40, 4096, seed=n)
+    run_batch_vs_solo(gm, 4096, prompts, steps=3, max_tokens=48, flags=rd.DET_COMMIT_ALL)
+
+
 def test_batch_rejects_bad_inputs_without_touching_state(ctx):
     gm = sharing_model(ctx)
     a, b, full = gm.session(8), gm.session(8), gm.session(4)
