@@ -1143,20 +1143,28 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
 // token groups once, then streams its K share of the workgroup's weight
 // tiles: a tile's half-step operands are HPW contiguous 1 KB blocks, and the
 // next tile's are in flight while this tile's MFMAs run (no barrier between
-// the K steps). The waves' partial limb sums of a tile (int32; a limb times a
-// weight is at most 128 * 127 in magnitude, so K chunks up to 130000 columns
-// cannot wrap) are added through LDS, one LDS-only barrier per tile, and wave
-// tg (< NG) combines token group tg's sums as k_gemv_dec_wg does. Workgroup b
-// takes K chunk b % kchunks (kchunks > 1: atomic acc_out only) and tiles
-// b / kchunks + groups * j. Half-steps past kpad are read clamped to the last
-// one with zero A operands.
+// the K steps). The waves' partial limb sums of a tile
+// (int32; a limb times a weight is at most 128 * 127 in magnitude, so K
+// chunks up to 130000 columns cannot wrap) are added through LDS, one
+// LDS-only barrier per tile, and wave w combines token groups w, w + NW, ...
+// as k_gemv_dec_wg does. Workgroup b takes K chunk b % kchunks
+// (kchunks > 1: atomic acc_out only) and tiles b / kchunks + groups * j.
+// Half-steps past kpad are read clamped to the last one with zero A operands.
+// EPI 1 (gate/up rows interleaved per tile, kchunks 1): the combining waves
+// stage each tile's requantized values in LDS, and every kStage tiles (and at
+// the end) all the workgroup's lanes form the mul_sat(gelu(gate), up)
+// products, one product per lane, rather than half the lanes of NG waves
+// between two tiles' barriers.
 template <int EPI, int NG, int NW, int HPW>
 __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
     int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
     int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
+  constexpr int kStage = 8;
   __shared__ v4i red[2][NW][NG][64];  // [tile parity][wave][token group][lane]
+  __shared__ int32_t stage[EPI == 1 ? kStage : 1][NG][64];
+  __shared__ uint64_t stage_tile[kStage];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane >> 4, i = lane & 15;
   const uint64_t nhs = kpad / 64;
@@ -1166,22 +1174,6 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
   const uint64_t groups = gridDim.x / kchunks;
   const uint64_t t0 = blockIdx.x / kchunks;
   const v4i zero = {0, 0, 0, 0};
-  // A operand of (half-step hs, token group tg) in lane 16 g + i: limb row
-  // 16 tg + i (token 4 tg + i / 4, limb i % 4), columns 128 s + 32 g + 16 h
-  // (clamped addresses, masked values: no predicated loads)
-  v4i ar[HPW][NG];
-#pragma unroll
-  for (int h = 0; h < HPW; ++h) {
-    const uint64_t hs = hs0 + h;
-    const bool k_on = hs < nhs;
-    const uint64_t col = k_on ? 128 * (hs >> 1) + 32 * g + 16 * (hs & 1) : 0;
-#pragma unroll
-    for (int tg = 0; tg < NG; ++tg) {
-      const bool on = k_on && uint32_t(4 * tg + (i >> 2)) < ntok;
-      const v4i v = *reinterpret_cast<const v4i*>(limbs + uint64_t(on ? 16 * tg + i : 0) * kpad + col);
-      ar[h][tg] = on ? v : zero;
-    }
-  }
   const uint64_t my_tiles = t0 < ntiles ? (ntiles - t0 + groups - 1) / groups : 0;
   // this wave's first half-step operand of tile j (tiles past the end read the last tile)
   const v4i* qw = reinterpret_cast<const v4i*>(q) + lane;
@@ -1201,8 +1193,47 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
 #pragma unroll
     for (int h = 0; h < HPW; ++h) wb[r][h] = __builtin_nontemporal_load(qw + (t * nhs + hs_of(h)) * 64);
   };
+  // A operand of (half-step hs, token group tg) in lane 16 g + i: limb row
+  // 16 tg + i (token 4 tg + i / 4, limb i % 4), columns 128 s + 32 g + 16 h
+  // (clamped addresses, masked values: no predicated loads)
+  v4i ar[HPW][NG];
+#pragma unroll
+  for (int h = 0; h < HPW; ++h) {
+    const uint64_t hs = hs0 + h;
+    const bool k_on = hs < nhs;
+    const uint64_t col = k_on ? 128 * (hs >> 1) + 32 * g + 16 * (hs & 1) : 0;
+#pragma unroll
+    for (int tg = 0; tg < NG; ++tg) {
+      const bool on = k_on && uint32_t(4 * tg + (i >> 2)) < ntok;
+      const v4i v = *reinterpret_cast<const v4i*>(limbs + uint64_t(on ? 16 * tg + i : 0) * kpad + col);
+      ar[h][tg] = on ? v : zero;
+    }
+  }
   issue(0, 0);
   issue(1, 1);
+  // EPI 1: the staged tiles' products, lane by lane (token-major within a
+  // tile: product p = tok * 8 + f of staged tile slot)
+  auto flush = [&](uint32_t cnt) {
+    lds_barrier();
+    for (uint32_t idx = threadIdx.x; idx < cnt * NG * 32; idx += 64 * NW) {
+      const uint32_t slot = idx / (NG * 32), rem = idx % (NG * 32);
+      const uint32_t tok = rem >> 3, f8 = rem & 7;
+      const uint64_t tile = stage_tile[slot];
+      const uint32_t ln = 16 * (tok & 3) + f8;
+      const int32_t gate = stage[slot][tok >> 2][ln], up = stage[slot][tok >> 2][ln + 8];
+      if (tok < ntok && tile * 16 + f8 < n_rows) {
+        const uint64_t f = tile * 8 + f8;
+        const int32_t hv = mul_sat(gelu_act(gate), up);
+        out[tok * out_ld + f] = hv;
+        const uint32_t u = uint32_t(hv) ^ 0x00808080u;
+        int8_t* ol = out_limbs + uint64_t(tok) * 4 * out_kpad + f;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) ol[jj * out_kpad] = int8_t(uint8_t(u >> (8 * jj)));
+      }
+    }
+    lds_barrier();
+  };
+  uint32_t nst = 0;
   for (uint64_t j0 = 0; j0 < my_tiles; j0 += 2) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -1221,39 +1252,36 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
 #pragma unroll
         for (int tg = 0; tg < NG; ++tg) red[r][wave][tg][lane] = acc[tg];
         lds_barrier();
-        if (wave < NG) {
-          // token group tg = wave; lane 16 g + i holds the limb sums of token 4 tg + g, row i
-          v4i s = red[r][0][wave][lane];
+        const uint64_t tile = t0 + groups * j;
+        if (EPI == 1 && wave == 0 && lane == 0) stage_tile[nst] = tile;
 #pragma unroll
-          for (int w = 1; w < NW; ++w) s += red[r][w][wave][lane];
+        for (int tg = wave; tg < NG; tg += NW) {
+          // lane 16 g + i holds the limb sums of token 4 tg + g, row i
+          v4i s = red[r][0][tg][lane];
+#pragma unroll
+          for (int w = 1; w < NW; ++w) s += red[r][w][tg][lane];
           const int64_t p[4] = {s[0], s[1], s[2], s[3]};
-          const uint64_t tile = t0 + groups * j;
           const uint64_t row = tile * 16 + uint64_t(i);
-          const uint32_t tok = 4 * uint32_t(wave) + uint32_t(g);
+          const uint32_t tok = 4 * uint32_t(tg) + uint32_t(g);
           const bool ok = tok < ntok && row < n_rows;
           if (acc_out) {
             if (ok)
               atomicAdd(reinterpret_cast<unsigned long long*>(acc_out + tok * acc_ld + row),
                         static_cast<unsigned long long>(limb_combine(p, kc == 0 ? rs : 0, sc)));
           } else if (EPI == 1) {
-            const int32_t rq = ok ? requant(limb_combine(p, rs, sc)) : 0;
-            const int32_t up = __shfl(rq, (lane & 48) | ((i + 8) & 15), 64);
-            if (ok && i < 8) {
-              const uint64_t f = tile * 8 + uint64_t(i);
-              const int32_t hv = mul_sat(gelu_act(rq), up);
-              out[tok * out_ld + f] = hv;
-              const uint32_t u = uint32_t(hv) ^ 0x00808080u;
-              int8_t* ol = out_limbs + uint64_t(tok) * 4 * out_kpad + f;
-#pragma unroll
-              for (int jj = 0; jj < 4; ++jj) ol[jj * out_kpad] = int8_t(uint8_t(u >> (8 * jj)));
-            }
+            stage[nst][tg][lane] = ok ? requant(limb_combine(p, rs, sc)) : 0;
           } else if (ok) {
             out[tok * out_ld + row] = requant(limb_combine(p, rs, sc));
           }
         }
+        if (EPI == 1 && ++nst == kStage) {
+          flush(kStage);
+          nst = 0;
+        }
       }
     }
   }
+  if (EPI == 1 && nst > 0) flush(nst);
 }
 
 // ---------------------------------------------------------------------------
@@ -2604,25 +2632,54 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
 }
 
 // 5-16 tokens over single-plane weights with K of at least 24 half-steps
-// (1536 columns): k_gemv_rega, K chunks of at most 8 waves x 5 half-steps,
-// one workgroup of 8 waves per CU. False where the shape is outside its range
-// (digit planes, short K, or a K split without atomic outputs).
+// (1536 columns): k_gemv_rega. False where the shape is outside its range
+// (digit planes, short K, or a K split without atomic outputs) or where the
+// tiles cannot give every workgroup two or more: a workgroup loads its K
+// chunk's activation limbs of all tokens once, which only several tiles
+// amortise.
+// - Atomic outputs: workgroups of 2 waves x HPW half-steps, so K splits into
+//   many chunks and each workgroup loads a small share of the activations
+//   (HPW from 5, 4, 3, whichever leaves the fewest idle half-steps), about
+//   512 workgroups with at least three tiles each. Measured on E4B shapes at
+//   16 tokens: down 2560 x 10240 8.9 us in 16 chunks against 12.0 us for
+//   k_gemv_dec_wg and 12.0 us with 8 waves x 5 half-steps in 4 chunks;
+//   q/k/v 3072 x 2560 5.6 us in 4 chunks against 6.7 us.
+// - One K chunk (requantized outputs, the GELU epilogue): 8 waves x up to 5
+//   half-steps cover K = 2560 in one workgroup per CU (gate/up 20480 x 2560
+//   17.2 us against 25.3 us; lm_head 262144 x 2560 122 us against 185 us).
 template <int NG>
 static bool launch_gemv_rega(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                              int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
                              hipStream_t s) {
   const uint64_t nhs = W.kpad / 64;
   if (W.planes != 1 || nhs < 24) return false;
-  const uint64_t kc = (nhs + 39) / 40;
-  if (kc > 1 && (!acc || epilogue != 0)) return false;
-  const uint64_t hpw = (nhs + 8 * kc - 1) / (8 * kc);
-  if (hpw < 3 || hpw > 5) return false;
   const uint64_t ntiles = (W.rows + 15) / 16;
-  const uint64_t groups = std::min<uint64_t>(ntiles, std::max<uint64_t>(device_cus() / kc, 1));
-  const dim3 grid(unsigned(groups * kc)), block(512);
+  const uint64_t cus = device_cus();
+  if (acc && epilogue == 0) {
+    uint64_t hpw = 5, best = ~uint64_t(0);
+    for (uint64_t h = 5; h >= 3; --h) {
+      const uint64_t idle = (nhs + 2 * h - 1) / (2 * h) * 2 * h - nhs;
+      if (idle < best) best = idle, hpw = h;
+    }
+    const uint64_t kc = (nhs + 2 * hpw - 1) / (2 * hpw);
+    if (ntiles * kc < 2 * cus) return false;
+    const uint64_t groups =
+        std::max<uint64_t>(1, std::min<uint64_t>({ntiles, std::max<uint64_t>(2 * cus / kc, 1), ntiles / 3}));
+    const dim3 grid(unsigned(groups * kc)), block(128);
+#define DET_REGA2(H)                                                                                              \
+    hipLaunchKernelGGL((k_gemv_rega<0, NG, 2, H>), grid, block, 0, s, W.q, W.scale, W.rowsum, limbs, W.rows, W.kpad, \
+                       uint32_t(kc), ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad)
+    if (hpw == 5) DET_REGA2(5); else if (hpw == 4) DET_REGA2(4); else DET_REGA2(3);
+#undef DET_REGA2
+    return true;
+  }
+  if (acc || nhs > 40 || ntiles < 2 * cus) return false;
+  const uint64_t hpw = (nhs + 7) / 8;
+  const uint64_t groups = std::min<uint64_t>(ntiles, cus);
+  const dim3 grid{unsigned(groups)}, block{512};
 #define DET_REGA(E, H)                                                                                          \
   hipLaunchKernelGGL((k_gemv_rega<E, NG, 8, H>), grid, block, 0, s, W.q, W.scale, W.rowsum, limbs, W.rows, W.kpad, \
-                     uint32_t(kc), ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad)
+                     1u, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad)
   if (epilogue == 1) {
     if (hpw == 5) DET_REGA(1, 5); else if (hpw == 4) DET_REGA(1, 4); else DET_REGA(1, 3);
   } else {
