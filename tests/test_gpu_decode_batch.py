@@ -141,6 +141,19 @@ def test_e4b_shaped_layers_batch_of_16_matches_solo(ctx, mode):
     run_batch_vs_solo(gm, 4096, prompts, steps=3, max_tokens=48, flags=rd.DET_COMMIT_ALL | MODES[mode])
 
 
+@pytest.mark.parametrize("hidden,ff", [(1536, 6144), (2048, 8192)])
+@pytest.mark.parametrize("n", [6, 16])
+def test_other_widths_batch_matches_solo(ctx, hidden, ff, n):
+    """Widths whose batched GEMVs take 3 and 4 half-steps per wave: K 1536 /
+    2048 for q/k/v, gate/up and the vocabulary projection, 6144 / 8192 for
+    down (12 and 16 K chunks)."""
+    cfg = synthetic.e4b_config(layers=2, vocab=8192, sliding_window=8)
+    cfg["text_config"].update({"hidden_size": hidden, "intermediate_size": ff})
+    gm = build(ctx, cfg, synthetic.synthetic_model_fast(cfg, seed=hidden + n))
+    prompts = ragged_prompts(n, 1, 40, 8192, seed=hidden // 64 + n)
+    run_batch_vs_solo(gm, 8192, prompts, steps=3, max_tokens=48, flags=rd.DET_COMMIT_ALL)
+
+
 @pytest.mark.parametrize("n", [5, 7, 13])
 def test_e4b_shaped_layers_partial_batches_match_solo(ctx, n):
     """Batches of 5-8 tokens take the two-token-group GEMV instances and
