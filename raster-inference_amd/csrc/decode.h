@@ -85,26 +85,28 @@ constexpr uint32_t kAttnScoreRows = 32;     // window rows per scores workgroup 
 constexpr uint32_t kAttnWsumRows = 32;      // window rows per softmax / weighted-sum workgroup
 
 // The normalised rows are written as int32 (normed) and as limb planes
-// (limbs, plane stride kpad) for the decode GEMV.
+// (limbs, plane stride kpad) for the decode GEMV; with om (optional) also in
+// the batched GEMV's operand-major layout (om_offset, row i = token i).
 // With nseq > 1, sequence i uses st[i] and rows i of x, dec_in and normed
 // (stride H) and limb planes 4i..4i+3 (stride kpad).
 void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, uint64_t H, int32_t* x, int32_t* dec_in,
                       const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s,
-                      uint32_t nseq = 1);
+                      uint32_t nseq = 1, int8_t* om = nullptr);
 // x = add_sat(x_src, rmsnorm(requant(src), w_post)) [* scalar]; normed = rmsnorm(x, w_next);
 // src (wrapping Q32.32 accumulators) is cleared after use. x_src defaults to
 // x (in place). x_out (optional) receives a copy of the new x (row stride H
 // per sequence).
-// Without w_next, x_limbs also writes x's limb planes to limbs.
+// Without w_next, x_limbs also writes x's limb planes to limbs. om as for
+// launch_dec_embed.
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
                               uint64_t kpad, hipStream_t s, uint32_t nseq = 1, int32_t* x_out = nullptr,
-                              const int32_t* x_src = nullptr, bool x_limbs = false);
+                              const int32_t* x_src = nullptr, bool x_limbs = false, int8_t* om = nullptr);
 // Limb planes (plane stride kpad, 4 planes per row) of nseq int32 rows of k
 // columns (row stride ld); with gate_in, of mul_sat(gelu(x), gate_in) per
 // element (gate_in row stride in_ld): the per-layer input gate.
 void launch_dec_row_limbs(const int32_t* x, uint64_t k, uint64_t ld, uint32_t nseq, int8_t* limbs, uint64_t kpad,
-                          hipStream_t s, const int32_t* gate_in = nullptr, uint64_t in_ld = 0);
+                          hipStream_t s, const int32_t* gate_in = nullptr, uint64_t in_ld = 0, int8_t* om = nullptr);
 void launch_dec_attention(const AttnDecArgs& a, hipStream_t s);
 // Whether launch_dec_attention runs the statistics as a separate pass.
 bool dec_attention_split(const AttnDecArgs& a);

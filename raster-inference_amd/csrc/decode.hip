@@ -58,12 +58,21 @@ __device__ __forceinline__ int32_t wgt_bits(const DevMatrix& M, uint64_t r, uint
 // Row kernels: one workgroup of NT threads, element c = tid + NT * e held in
 // registers (e < EPT, so rows up to NT * EPT), every global read issued first.
 // The normalised row is written as int32 and as the four limb planes (plane
-// stride kpad) that the next decode GEMV reads.
-__device__ __forceinline__ void put_row(int32_t* row, int8_t* limbs, uint64_t kpad, uint64_t c, int32_t v) {
-  row[c] = v;
+// stride kpad) that the next decode GEMV reads; with om also in the batched
+// GEMV's operand-major layout (om_offset, token t of the batch).
+__device__ __forceinline__ void put_limbs(int8_t* limbs, uint64_t kpad, uint64_t c, int32_t v, int8_t* om,
+                                          uint64_t t) {
   const uint32_t u = uint32_t(v) ^ 0x00808080u;
 #pragma unroll
   for (int j = 0; j < 4; ++j) limbs[j * kpad + c] = int8_t(uint8_t(u >> (8 * j)));
+  if (om)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) om[om_offset(kpad, t, c, j)] = int8_t(uint8_t(u >> (8 * j)));
+}
+__device__ __forceinline__ void put_row(int32_t* row, int8_t* limbs, uint64_t kpad, uint64_t c, int32_t v, int8_t* om,
+                                        uint64_t t) {
+  row[c] = v;
+  put_limbs(limbs, kpad, c, v, om, t);
 }
 
 // Embed the step token (gemma/io.rs:2446-2518) and normalise it for layer 0.
@@ -72,7 +81,7 @@ __global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* 
                                                    uint64_t H, int32_t* __restrict__ x, int32_t* __restrict__ dec_in,
                                                    const int32_t* __restrict__ w_in, int64_t eps,
                                                    int32_t* __restrict__ normed, int8_t* __restrict__ limbs,
-                                                   uint64_t kpad) {
+                                                   uint64_t kpad, int8_t* __restrict__ om) {
   __shared__ int64_t red[NT / 64];
   __shared__ int32_t bc;
   const uint32_t seq = blockIdx.y;
@@ -99,7 +108,7 @@ __global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* 
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const uint64_t c = threadIdx.x + uint64_t(NT) * e;
-    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(v[e], sc), w[e]));
+    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(v[e], sc), w[e]), om, seq);
   }
 }
 
@@ -116,7 +125,8 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
                                                            const int32_t* __restrict__ w_post, int has_scalar,
                                                            int32_t scalar, const int32_t* __restrict__ w_next,
                                                            uint64_t H, int64_t eps, int8_t* __restrict__ limbs,
-                                                           uint64_t kpad, int32_t* __restrict__ x_out, int x_limbs) {
+                                                           uint64_t kpad, int32_t* __restrict__ x_out, int x_limbs,
+                                                           int8_t* __restrict__ om) {
   __shared__ int64_t red[NT / 64];
   __shared__ int32_t bc;
   const uint32_t seq = blockIdx.y;
@@ -157,11 +167,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         const uint64_t c = threadIdx.x + uint64_t(NT) * e;
-        if (c < H) {
-          const uint32_t u = uint32_t(xv[e]) ^ 0x00808080u;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) limbs[j * kpad + c] = int8_t(uint8_t(u >> (8 * j)));
-        }
+        if (c < H) put_limbs(limbs, kpad, c, xv[e], om, seq);
       }
     return;
   }
@@ -169,7 +175,7 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const uint64_t c = threadIdx.x + uint64_t(NT) * e;
-    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(xv[e], s2), wn[e]));
+    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(xv[e], s2), wn[e]), om, seq);
   }
 }
 
@@ -990,7 +996,8 @@ __global__ __launch_bounds__(256) void k_dec_acc_limbs(int64_t* __restrict__ acc
 template <bool GATE>
 __global__ __launch_bounds__(256) void k_dec_row_limbs(const int32_t* __restrict__ x, uint64_t k, uint64_t ld,
                                                        const int32_t* __restrict__ in, uint64_t in_ld,
-                                                       int8_t* __restrict__ limbs, uint64_t kpad) {
+                                                       int8_t* __restrict__ limbs, uint64_t kpad,
+                                                       int8_t* __restrict__ om) {
   const uint64_t c0 = (uint64_t(blockIdx.x) * 256 + threadIdx.x) * 4;
   if (c0 >= kpad) return;
   const uint64_t t = blockIdx.y;
@@ -1008,6 +1015,10 @@ __global__ __launch_bounds__(256) void k_dec_row_limbs(const int32_t* __restrict
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(limbs + (t * 4 + j) * kpad + c0) = packed[j];
+  // (columns c0 .. c0 + 3 are four consecutive bytes of one operand)
+  if (om)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(om + om_offset(kpad, t, c0, j)) = packed[j];
 }
 
 // Up to kSetWords 64-bit words by value (within the 4 KB of kernel arguments).
@@ -1065,15 +1076,15 @@ static inline unsigned nblk(uint64_t n, unsigned per) { return unsigned((n + per
   } while (0)
 void launch_dec_embed(const DevMatrix& E, const StepState* st, int32_t scale, uint64_t H, int32_t* x, int32_t* dec_in,
                       const int32_t* w_in, int64_t eps, int32_t* normed, int8_t* limbs, uint64_t kpad, hipStream_t s,
-                      uint32_t nseq) {
-  DET_ROW_DISPATCH(k_dec_embed, E, st, scale, H, x, dec_in, w_in, eps, normed, limbs, kpad);
+                      uint32_t nseq, int8_t* om) {
+  DET_ROW_DISPATCH(k_dec_embed, E, st, scale, H, x, dec_in, w_in, eps, normed, limbs, kpad, om);
 }
 void launch_dec_residual_norm(int64_t* src, int32_t* x, int32_t* normed, const int32_t* w_post, bool has_scalar,
                               int32_t scalar, const int32_t* w_next, uint64_t H, int64_t eps, int8_t* limbs,
                               uint64_t kpad, hipStream_t s, uint32_t nseq, int32_t* x_out, const int32_t* x_src,
-                              bool x_limbs) {
+                              bool x_limbs, int8_t* om) {
   DET_ROW_DISPATCH(k_dec_residual_norm, src, x_src ? x_src : x, x, normed, w_post, int(has_scalar), scalar, w_next, H,
-                   eps, limbs, kpad, x_out, int(x_limbs && !w_next));
+                   eps, limbs, kpad, x_out, int(x_limbs && !w_next), om);
 }
 #undef DET_ROW_DISPATCH
 // Window chunks per attention workgroup: a.rows_mul when set (1, 2 or 4),
@@ -1203,15 +1214,15 @@ void launch_dec_acc_limbs(int64_t* acc, uint64_t k, uint64_t ld, uint32_t nseq, 
   if (nseq && kpad) hipLaunchKernelGGL(k_dec_acc_limbs, dim3(nblk(kpad / 4, 256), nseq), dim3(256), 0, s, acc, k, ld, limbs, kpad);
 }
 void launch_dec_row_limbs(const int32_t* x, uint64_t k, uint64_t ld, uint32_t nseq, int8_t* limbs, uint64_t kpad,
-                          hipStream_t s, const int32_t* gate_in, uint64_t in_ld) {
+                          hipStream_t s, const int32_t* gate_in, uint64_t in_ld, int8_t* om) {
   if (!nseq || !kpad) return;
   if (kpad % 4) throw std::invalid_argument("launch_dec_row_limbs: kpad must be a multiple of 4");
   if (gate_in)
     hipLaunchKernelGGL(k_dec_row_limbs<true>, dim3(nblk(kpad / 4, 256), nseq), dim3(256), 0, s, x, k, ld, gate_in,
-                       in_ld, limbs, kpad);
+                       in_ld, limbs, kpad, om);
   else
     hipLaunchKernelGGL(k_dec_row_limbs<false>, dim3(nblk(kpad / 4, 256), nseq), dim3(256), 0, s, x, k, ld, x, 0,
-                       limbs, kpad);
+                       limbs, kpad, om);
 }
 void launch_copy_rows(const int32_t* src, uint64_t w, uint64_t n, int32_t* const* dst, hipStream_t s) {
   if (n && w) hipLaunchKernelGGL(k_copy_rows, dim3(nblk((w + 3) / 4, 256), unsigned(n)), dim3(256), 0, s, src, w, dst);

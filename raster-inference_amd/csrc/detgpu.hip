@@ -1719,6 +1719,10 @@ struct BatchWs {
   det::AttnStat* attn_stats = nullptr;  // [cap][score_heads]
   int64_t *qkv_acc = nullptr, *attn_acc = nullptr, *o_acc = nullptr, *ff_acc = nullptr;
   int8_t *limbs_x = nullptr, *limbs_o = nullptr, *limbs_ff = nullptr;
+  // the same activations in the batched GEMV's operand-major layout
+  // (det::om_offset, passes of 16 rows), written by every kernel that writes
+  // limbs_x / limbs_ff / limbs_p
+  int8_t *om_x = nullptr, *om_ff = nullptr, *om_p = nullptr;
   // per-layer inputs (PLE models): every layer's inputs of each sequence's
   // token [cap][L*P], the model projection rows [cap][L*P], the gate rows
   // [cap][P], the projection accumulators [cap][hidden] and the limb planes
@@ -1972,6 +1976,9 @@ void ensure_fused_batch(det_model* m, BatchWs& b, uint64_t need) {
     b.limbs_x = b.alloc<int8_t>(T * 4 * m->fused[0].qkv.kpad);
     b.limbs_o = b.alloc<int8_t>(T * 4 * kpo);
     b.limbs_ff = b.alloc<int8_t>(T * 4 * kff);
+    const uint64_t T16 = (T + 15) / 16 * 16;
+    b.om_x = b.alloc<int8_t>(T16 * 4 * m->fused[0].qkv.kpad);
+    b.om_ff = b.alloc<int8_t>(T16 * 4 * kff);
     b.attn_stats = b.alloc<det::AttnStat>(T * nh);
     // every accumulator is cleared by the kernel that consumes it, so they
     // only need to start at zero (stream-ordered, outside any graph)
@@ -1983,6 +1990,8 @@ void ensure_fused_batch(det_model* m, BatchWs& b, uint64_t need) {
     HIPC(hipMemsetAsync(b.limbs_o, 0, T * 4 * kpo, zst));
     HIPC(hipMemsetAsync(b.limbs_ff, 0, T * 4 * kff, zst));
     HIPC(hipMemsetAsync(b.limbs_x, 0, T * 4 * m->fused[0].qkv.kpad, zst));
+    HIPC(hipMemsetAsync(b.om_x, 0, T16 * 4 * m->fused[0].qkv.kpad, zst));
+    HIPC(hipMemsetAsync(b.om_ff, 0, T16 * 4 * kff, zst));
     if (m->has_ple) {
       const uint64_t LP = m->layers.size() * m->ple_dim;
       uint64_t kp = m->ple_proj_full->kpad;
@@ -1993,6 +2002,7 @@ void ensure_fused_batch(det_model* m, BatchWs& b, uint64_t need) {
       b.ple_g = b.alloc<int32_t>(T * m->ple_dim);
       b.ple_acc = b.alloc<int64_t>(T * H);
       b.limbs_p = b.alloc<int8_t>(T * 4 * kp);
+      b.om_p = b.alloc<int8_t>(T16 * 4 * kp);
       HIPC(hipMemsetAsync(b.ple_acc, 0, T * H * 8, zst));
     }
     b.fused = true;
@@ -2064,15 +2074,15 @@ void enqueue_fused_batch(det_model* m, BatchWs& b, uint32_t n) {
   const uint64_t kpad_x = m->fused[0].qkv.kpad;
   det::launch_dec_set_trig(st_dev, n, m->rope_tables_dev, uint32_t(m->rope_tables.size()), m->trig_pairs, b.trig, st);
   det::launch_dec_embed(*m->embedding, st_dev, m->embed_scale, H, b.x, b.dec_in, m->layers[0].in_ln, m->eps, b.normed,
-                        b.limbs_x, kpad_x, st, n);
+                        b.limbs_x, kpad_x, st, n, b.om_x);
   const uint64_t P = m->ple_dim, LP = m->layers.size() * P;
   if (m->has_ple) {
     // every layer's per-layer input of each sequence's token (det_decode_ple_input,
     // det_kernels.rs:1142-1208), rows [n][L*P] as in the single-sequence step
     const uint64_t id_stride = sizeof(det::StepState) / sizeof(uint32_t);
     det::launch_gather_rows(*m->ple_tok, &st_dev->token, n, 0, LP, m->ple_embedding_scale, b.ple_in, LP, st, id_stride);
-    det::launch_dec_row_limbs(b.dec_in, H, H, n, b.limbs_p, m->ple_proj_full->kpad, st);
-    det::launch_gemv_dec_batch(*m->ple_proj_full, b.limbs_p, n, b.ple_pp, LP, nullptr, 0, 0, nullptr, 0, st);
+    det::launch_dec_row_limbs(b.dec_in, H, H, n, b.limbs_p, m->ple_proj_full->kpad, st, nullptr, 0, b.om_p);
+    det::launch_gemv_dec_batch(*m->ple_proj_full, b.limbs_p, n, b.ple_pp, LP, nullptr, 0, 0, nullptr, 0, st, b.om_p);
     det::launch_scale(b.ple_pp, n * LP, m->ple_projection_scalar, st);
     det::launch_rmsnorm(b.ple_pp, n * m->layers.size(), P, P, m->ple_proj_norm, m->eps, st);
     det::launch_add_sat(b.ple_in, b.ple_pp, n * LP, st);
@@ -2081,7 +2091,7 @@ void enqueue_fused_batch(det_model* m, BatchWs& b, uint32_t n) {
   for (size_t l = 0; l < m->layers.size(); ++l) {
     const GLayer& L = m->layers[l];
     const auto& F = m->fused[l];
-    det::launch_gemv_dec_batch(F.qkv, b.limbs_x, n, nullptr, 0, b.qkv_acc, b.qkv_stride, 0, nullptr, 0, st);
+    det::launch_gemv_dec_batch(F.qkv, b.limbs_x, n, nullptr, 0, b.qkv_acc, b.qkv_stride, 0, nullptr, 0, st, b.om_x);
     det::launch_dec_attention(batch_attn_args(m, b, l, n), st);
     // the O projection reads the weighted-sum accumulators directly where
     // its kernel takes them (the scores kernel clears them at the next layer)
@@ -2092,27 +2102,30 @@ void enqueue_fused_batch(det_model* m, BatchWs& b, uint32_t n) {
       det::launch_gemv_dec_batch(*L.o, b.limbs_o, n, nullptr, 0, b.o_acc, H, 0, nullptr, 0, st);
     }
     det::launch_dec_residual_norm(b.o_acc, b.x, b.normed, L.post_attn_ln, false, 0, L.pre_ff_ln, H, L.eps, b.limbs_x,
-                                  kpad_x, st, n);
-    det::launch_gemv_dec_batch(F.gateup, b.limbs_x, n, b.hbuf, b.ff_stride, nullptr, 0, 1, b.limbs_ff, L.down->kpad, st);
-    det::launch_gemv_dec_batch(*L.down, b.limbs_ff, n, nullptr, 0, b.ff_acc, H, 0, nullptr, 0, st);
+                                  kpad_x, st, n, nullptr, nullptr, false, b.om_x);
+    det::launch_gemv_dec_batch(F.gateup, b.limbs_x, n, b.hbuf, b.ff_stride, nullptr, 0, 1, b.limbs_ff, L.down->kpad, st,
+                               b.om_x, b.om_ff);
+    det::launch_gemv_dec_batch(*L.down, b.limbs_ff, n, nullptr, 0, b.ff_acc, H, 0, nullptr, 0, st, b.om_ff);
     const int32_t* w_next = l + 1 < m->layers.size() ? m->layers[l + 1].in_ln : m->final_norm;
     if (m->has_ple && L.has_ple) {
       // x += norm(down) (with x's limb planes); then the per-layer input block
       // (det_kernels.rs:1108-1128): x += norm(proj(gelu(gate(x)) * ple_in)),
       // the layer scalar and the next norm
       det::launch_dec_residual_norm(b.ff_acc, b.x, b.normed, L.post_ff_ln, false, 0, nullptr, H, L.eps, b.limbs_x,
-                                    kpad_x, st, n, nullptr, nullptr, true);
-      det::launch_gemv_dec_batch(*L.ple_gate, b.limbs_x, n, b.ple_g, P, nullptr, 0, 0, nullptr, 0, st);
-      det::launch_dec_row_limbs(b.ple_g, P, P, n, b.limbs_p, L.ple_proj->kpad, st, b.ple_in + l * P, LP);
-      det::launch_gemv_dec_batch(*L.ple_proj, b.limbs_p, n, nullptr, 0, b.ple_acc, H, 0, nullptr, 0, st);
+                                    kpad_x, st, n, nullptr, nullptr, true, b.om_x);
+      det::launch_gemv_dec_batch(*L.ple_gate, b.limbs_x, n, b.ple_g, P, nullptr, 0, 0, nullptr, 0, st, b.om_x);
+      det::launch_dec_row_limbs(b.ple_g, P, P, n, b.limbs_p, L.ple_proj->kpad, st, b.ple_in + l * P, LP, b.om_p);
+      det::launch_gemv_dec_batch(*L.ple_proj, b.limbs_p, n, nullptr, 0, b.ple_acc, H, 0, nullptr, 0, st, b.om_p);
       det::launch_dec_residual_norm(b.ple_acc, b.x, b.normed, L.ple_post_norm, L.layer_scalar.has_value(),
-                                    L.layer_scalar.value_or(0), w_next, H, L.eps, b.limbs_x, kpad_x, st, n);
+                                    L.layer_scalar.value_or(0), w_next, H, L.eps, b.limbs_x, kpad_x, st, n, nullptr,
+                                    nullptr, false, b.om_x);
     } else {
       det::launch_dec_residual_norm(b.ff_acc, b.x, b.normed, L.post_ff_ln, L.layer_scalar.has_value(),
-                                    L.layer_scalar.value_or(0), w_next, H, L.eps, b.limbs_x, kpad_x, st, n);
+                                    L.layer_scalar.value_or(0), w_next, H, L.eps, b.limbs_x, kpad_x, st, n, nullptr,
+                                    nullptr, false, b.om_x);
     }
   }
-  det::launch_gemv_dec_batch(*m->lm_head, b.limbs_x, n, b.logits, V, nullptr, 0, 0, nullptr, 0, st);
+  det::launch_gemv_dec_batch(*m->lm_head, b.limbs_x, n, b.logits, V, nullptr, 0, 0, nullptr, 0, st, b.om_x);
   if (m->softcap) det::launch_dec_softcap(b.logits, n * V, *m->softcap, st);
   det::launch_copy_rows(b.logits, V, n, reinterpret_cast<int32_t* const*>(b.desc + D.logit_dst), st);
   det::launch_argmax_rows(b.logits, n, V, b.am_keys, b.next, st);

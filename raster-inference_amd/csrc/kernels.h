@@ -137,12 +137,30 @@ bool gemv_decode_acc_plain(const DevMatrix& W);
 // (stride out_kpad) to out_limbs.
 void launch_gemv_dec(const DevMatrix& W, const int8_t* limbs, int32_t* out, int64_t* acc, int epilogue,
                      int8_t* out_limbs, uint64_t out_kpad, hipStream_t s);
+// Operand-major limb layout of the batched decode GEMV (k_gemv_rega): the
+// limbs of token t's row of kpad columns sit in the MFMA A operands that read
+// them. Tokens go in passes of 16 (pass p = t / 16, slot s = t % 16); column
+// c belongs to half-step hs = 2 (c / 128) + (c / 16) % 2, and limb j of it
+// is byte c % 16 of lane 16 ((c / 32) % 4) + 4 (s % 4) + j's 16-byte operand
+// of token group s / 4. A pass takes 64 kpad bytes (as many as 16 tokens'
+// limb planes), every half-step 4 KB: 1 KB per token group, one contiguous
+// wave load per operand.
+__host__ __device__ inline uint64_t om_offset(uint64_t kpad, uint64_t t, uint64_t c, int j) {
+  const uint64_t s = t & 15;
+  const uint64_t hs = 2 * (c >> 7) + ((c >> 4) & 1);
+  const uint64_t lane = 16 * ((c >> 5) & 3) + 4 * (s & 3) + uint64_t(j);
+  return (((t >> 4) * (kpad >> 6) + hs) * 4 + (s >> 2)) * 1024 + lane * 16 + (c & 15);
+}
 // The same for ntok activation rows (token t: limb planes 4t..4t+3), every
 // weight tile serving up to 16 tokens; token t's outputs go to
 // out + t * out_ld, acc + t * acc_ld and planes 4t..4t+3 of out_limbs.
+// limbs_om (optional): the same activations also in the operand-major layout,
+// which passes of 5-16 tokens then read instead of the planes. out_om
+// (epilogue 1, with out_limbs): the outputs' limbs are also written in that
+// layout (stride out_kpad) by every pass of 5 or more tokens.
 void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                            int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
-                           hipStream_t s);
+                           hipStream_t s, const int8_t* limbs_om = nullptr, int8_t* out_om = nullptr);
 // The same into Q32.32 accumulators (acc + t * acc_ld, added atomically)
 // from activation rows given as wrapped Q32.32 accumulators (acc_in + t *
 // in_ld, requantized on load): no limb planes in between. Applies when

@@ -965,7 +965,7 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
     int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
     int8_t* __restrict__ out_limbs, uint64_t out_kpad, int lp_arg, const int64_t* __restrict__ acc_in = nullptr,
-    uint64_t in_ld = 0) {
+    uint64_t in_ld = 0, int8_t* __restrict__ out_om = nullptr) {
   const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   __shared__ v4i al[2][NG][2][64];  // [buffer][token group][half][lane]
   const int planes = 1 << lp;  // digit planes
@@ -1128,6 +1128,9 @@ __global__ __launch_bounds__(256, 4) void k_gemv_dec_wg(
           int8_t* ol = out_limbs + uint64_t(tok) * 4 * out_kpad + f;
 #pragma unroll
           for (int j = 0; j < 4; ++j) ol[j * out_kpad] = int8_t(uint8_t(u >> (8 * j)));
+          if (out_om)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) out_om[om_offset(out_kpad, tok, f, j)] = int8_t(uint8_t(u >> (8 * j)));
         }
       } else if (ok) {
         out[tok * out_ld + row] = requant(limb_combine(p, rs, sc));
@@ -1160,7 +1163,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
     const int8_t* __restrict__ q, const int32_t* __restrict__ scale, const int32_t* __restrict__ rowsum,
     const int8_t* __restrict__ limbs, uint64_t n_rows, uint64_t kpad, uint32_t kchunks, uint32_t ntok,
     int32_t* __restrict__ out, uint64_t out_ld, int64_t* __restrict__ acc_out, uint64_t acc_ld,
-    int8_t* __restrict__ out_limbs, uint64_t out_kpad) {
+    int8_t* __restrict__ out_limbs, uint64_t out_kpad, const int8_t* __restrict__ a_om = nullptr,
+    int8_t* __restrict__ out_om = nullptr) {
   constexpr int kStage = 8;
   __shared__ v4i red[2][NW][NG][64];  // [tile parity][wave][token group][lane]
   __shared__ int32_t stage[EPI == 1 ? kStage : 1][NG][64];
@@ -1196,6 +1200,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
   // A operand of (half-step hs, token group tg) in lane 16 g + i: limb row
   // 16 tg + i (token 4 tg + i / 4, limb i % 4), columns 128 s + 32 g + 16 h
   // (clamped addresses, masked values: no predicated loads)
+  // (from the operand-major copy when given: one contiguous 1 KB per load)
   v4i ar[HPW][NG];
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
@@ -1205,7 +1210,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
 #pragma unroll
     for (int tg = 0; tg < NG; ++tg) {
       const bool on = k_on && uint32_t(4 * tg + (i >> 2)) < ntok;
-      const v4i v = *reinterpret_cast<const v4i*>(limbs + uint64_t(on ? 16 * tg + i : 0) * kpad + col);
+      const v4i v = a_om ? reinterpret_cast<const v4i*>(a_om)[((k_on ? hs : 0) * 4 + tg) * 64 + lane]
+                         : *reinterpret_cast<const v4i*>(limbs + uint64_t(on ? 16 * tg + i : 0) * kpad + col);
       ar[h][tg] = on ? v : zero;
     }
   }
@@ -1229,6 +1235,9 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
         int8_t* ol = out_limbs + uint64_t(tok) * 4 * out_kpad + f;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) ol[jj * out_kpad] = int8_t(uint8_t(u >> (8 * jj)));
+        if (out_om)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) out_om[om_offset(out_kpad, tok, f, jj)] = int8_t(uint8_t(u >> (8 * jj)));
       }
     }
     lds_barrier();
@@ -2600,7 +2609,8 @@ static uint64_t device_cus() {
 template <int NG>
 static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                                int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
-                               hipStream_t s, const int64_t* acc_in = nullptr, uint64_t in_ld = 0) {
+                               hipStream_t s, const int64_t* acc_in = nullptr, uint64_t in_ld = 0,
+                               int8_t* out_om = nullptr) {
   const uint64_t ntiles = (W.rows + 15) / 16, nsteps = W.kpad / 128;
   const void* fn = epilogue == 1 ? reinterpret_cast<const void*>(&k_gemv_dec_wg<1, NG, false>)
                                  : reinterpret_cast<const void*>(&k_gemv_dec_wg<0, NG, false>);
@@ -2617,7 +2627,7 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
 #define DET_DEC_WG(E, DG, IN)                                                                                    \
   hipLaunchKernelGGL((k_gemv_dec_wg<E, NG, DG, IN>), dim3(unsigned(g * kc)), dim3(256), 0, s, W.q, W.scale,        \
                      W.rowsum, limbs, W.rows, W.kpad, kc, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad,      \
-                     plane_log2(W), acc_in, in_ld)
+                     plane_log2(W), acc_in, in_ld, out_om)
   if (acc_in) {
     if (W.planes == 1) DET_DEC_WG(0, false, true);
     else DET_DEC_WG(0, true, true);
@@ -2650,7 +2660,7 @@ static void launch_gemv_dec_wg(const DevMatrix& W, const int8_t* limbs, uint32_t
 template <int NG>
 static bool launch_gemv_rega(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                              int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
-                             hipStream_t s) {
+                             hipStream_t s, const int8_t* a_om, int8_t* out_om) {
   const uint64_t nhs = W.kpad / 64;
   if (W.planes != 1 || nhs < 24) return false;
   const uint64_t ntiles = (W.rows + 15) / 16;
@@ -2668,7 +2678,7 @@ static bool launch_gemv_rega(const DevMatrix& W, const int8_t* limbs, uint32_t n
     const dim3 grid(unsigned(groups * kc)), block(128);
 #define DET_REGA2(H)                                                                                              \
     hipLaunchKernelGGL((k_gemv_rega<0, NG, 2, H>), grid, block, 0, s, W.q, W.scale, W.rowsum, limbs, W.rows, W.kpad, \
-                       uint32_t(kc), ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad)
+                       uint32_t(kc), ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, a_om, out_om)
     if (hpw == 5) DET_REGA2(5); else if (hpw == 4) DET_REGA2(4); else DET_REGA2(3);
 #undef DET_REGA2
     return true;
@@ -2679,7 +2689,7 @@ static bool launch_gemv_rega(const DevMatrix& W, const int8_t* limbs, uint32_t n
   const dim3 grid{unsigned(groups)}, block{512};
 #define DET_REGA(E, H)                                                                                          \
   hipLaunchKernelGGL((k_gemv_rega<E, NG, 8, H>), grid, block, 0, s, W.q, W.scale, W.rowsum, limbs, W.rows, W.kpad, \
-                     1u, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad)
+                     1u, ntok, out, out_ld, acc, acc_ld, out_limbs, out_kpad, a_om, out_om)
   if (epilogue == 1) {
     if (hpw == 5) DET_REGA(1, 5); else if (hpw == 4) DET_REGA(1, 4); else DET_REGA(1, 3);
   } else {
@@ -2710,21 +2720,24 @@ void launch_gemv_dec_batch_in64(const DevMatrix& W, const int64_t* acc_in, uint6
 
 void launch_gemv_dec_batch(const DevMatrix& W, const int8_t* limbs, uint32_t ntok, int32_t* out, uint64_t out_ld,
                            int64_t* acc, uint64_t acc_ld, int epilogue, int8_t* out_limbs, uint64_t out_kpad,
-                           hipStream_t s) {
+                           hipStream_t s, const int8_t* limbs_om, int8_t* out_om) {
   if (W.rows == 0 || ntok == 0) return;
-  // up to 16 tokens per pass over the weights
+  // up to 16 tokens per pass over the weights (pass p of the operand-major
+  // copies at p * 64 * kpad bytes)
   for (uint32_t t0 = 0; t0 < ntok; t0 += 16) {
     const uint32_t nt = ntok - t0 < 16 ? ntok - t0 : 16;
     const int8_t* l = limbs + uint64_t(t0) * 4 * W.kpad;
     int32_t* o = out ? out + uint64_t(t0) * out_ld : nullptr;
     int64_t* a = acc ? acc + uint64_t(t0) * acc_ld : nullptr;
     int8_t* ol = out_limbs ? out_limbs + uint64_t(t0) * 4 * out_kpad : nullptr;
+    const int8_t* lo = limbs_om ? limbs_om + uint64_t(t0) * 4 * W.kpad : nullptr;
+    int8_t* oo = (out_om && out_limbs) ? out_om + uint64_t(t0) * 4 * out_kpad : nullptr;
     if (nt <= 4) launch_gemv_dec_ng<1>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
     else if (nt <= 8) {
-      if (!launch_gemv_rega<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s))
-        launch_gemv_dec_wg<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
-    } else if (!launch_gemv_rega<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s)) {
-      launch_gemv_dec_wg<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s);
+      if (!launch_gemv_rega<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s, lo, oo))
+        launch_gemv_dec_wg<2>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s, nullptr, 0, oo);
+    } else if (!launch_gemv_rega<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s, lo, oo)) {
+      launch_gemv_dec_wg<4>(W, l, nt, o, out_ld, a, acc_ld, epilogue, ol, out_kpad, s, nullptr, 0, oo);
     }
   }
 }
