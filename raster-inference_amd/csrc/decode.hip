@@ -60,19 +60,37 @@ __device__ __forceinline__ int32_t wgt_bits(const DevMatrix& M, uint64_t r, uint
 // The normalised row is written as int32 and as the four limb planes (plane
 // stride kpad) that the next decode GEMV reads; with om also in the batched
 // GEMV's operand-major layout (om_offset, token t of the batch).
-__device__ __forceinline__ void put_limbs(int8_t* limbs, uint64_t kpad, uint64_t c, int32_t v, int8_t* om,
-                                          uint64_t t) {
+// The operand-major bytes of the workgroup's one token are staged in LDS
+// (oms) in their global order: 64-byte chunk (hs, g) holds limbs 0-3 of
+// columns 128 (hs / 2) + 32 g + 16 (hs % 2) + [0, 16), which om_offset puts
+// in four consecutive 16-byte lane operands; om_flush then copies whole
+// 16-byte pieces (scattered global byte stores were slower).
+__device__ __forceinline__ void put_limbs(int8_t* limbs, uint64_t kpad, uint64_t c, int32_t v, uint8_t* oms) {
   const uint32_t u = uint32_t(v) ^ 0x00808080u;
 #pragma unroll
   for (int j = 0; j < 4; ++j) limbs[j * kpad + c] = int8_t(uint8_t(u >> (8 * j)));
-  if (om)
+  if (oms) {
+    const uint64_t q = ((2 * (c >> 7) + ((c >> 4) & 1)) * 4 + ((c >> 5) & 3)) * 64 + (c & 15);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) om[om_offset(kpad, t, c, j)] = int8_t(uint8_t(u >> (8 * j)));
+    for (int j = 0; j < 4; ++j) oms[q + 16 * j] = uint8_t(u >> (8 * j));
+  }
 }
-__device__ __forceinline__ void put_row(int32_t* row, int8_t* limbs, uint64_t kpad, uint64_t c, int32_t v, int8_t* om,
-                                        uint64_t t) {
+__device__ __forceinline__ void put_row(int32_t* row, int8_t* limbs, uint64_t kpad, uint64_t c, int32_t v,
+                                        uint8_t* oms) {
   row[c] = v;
-  put_limbs(limbs, kpad, c, v, om, t);
+  put_limbs(limbs, kpad, c, v, oms);
+}
+// After the staging writes (every thread calls it): token t's operand-major
+// bytes from oms to om.
+template <int NT>
+__device__ __forceinline__ void om_flush(const uint8_t* oms, int8_t* om, uint64_t kpad, uint64_t t) {
+  __syncthreads();
+  const uint64_t pieces = kpad / 4;  // 16-byte pieces: 4 limbs x kpad bytes
+  for (uint64_t q = threadIdx.x; q < pieces; q += NT) {
+    const uint64_t chunk = q >> 2, j = q & 3, hs = chunk >> 2, g = chunk & 3;
+    const uint64_t c0 = 128 * (hs >> 1) + 32 * g + 16 * (hs & 1);
+    *reinterpret_cast<int4*>(om + om_offset(kpad, t, c0, int(j))) = *reinterpret_cast<const int4*>(oms + q * 16);
+  }
 }
 
 // Embed the step token (gemma/io.rs:2446-2518) and normalise it for layer 0.
@@ -84,6 +102,8 @@ __global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* 
                                                    uint64_t kpad, int8_t* __restrict__ om) {
   __shared__ int64_t red[NT / 64];
   __shared__ int32_t bc;
+  __shared__ __attribute__((aligned(16))) uint8_t oms_buf[4 * NT * EPT];
+  uint8_t* oms = om ? oms_buf : nullptr;
   const uint32_t seq = blockIdx.y;
   x += uint64_t(seq) * H;
   dec_in += uint64_t(seq) * H;
@@ -108,8 +128,9 @@ __global__ __launch_bounds__(NT) void k_dec_embed(DevMatrix E, const StepState* 
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const uint64_t c = threadIdx.x + uint64_t(NT) * e;
-    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(v[e], sc), w[e]), om, seq);
+    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(v[e], sc), w[e]), oms);
   }
+  if (om) om_flush<NT>(oms, om, kpad, seq);
 }
 
 // Residual add of a normalised sub-block output, then the next input norm:
@@ -129,6 +150,8 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
                                                            int8_t* __restrict__ om) {
   __shared__ int64_t red[NT / 64];
   __shared__ int32_t bc;
+  __shared__ __attribute__((aligned(16))) uint8_t oms_buf[4 * NT * EPT];
+  uint8_t* oms = om ? oms_buf : nullptr;
   const uint32_t seq = blockIdx.y;
   src += uint64_t(seq) * H;
   x_src += uint64_t(seq) * H;
@@ -167,16 +190,18 @@ __global__ __launch_bounds__(NT) void k_dec_residual_norm(int64_t* __restrict__ 
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         const uint64_t c = threadIdx.x + uint64_t(NT) * e;
-        if (c < H) put_limbs(limbs, kpad, c, xv[e], om, seq);
+        if (c < H) put_limbs(limbs, kpad, c, xv[e], oms);
       }
+    if (x_limbs && om) om_flush<NT>(oms, om, kpad, seq);
     return;
   }
   const int32_t s2 = blk_rms_scale<NT>(ss, H, eps, red, &bc);
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const uint64_t c = threadIdx.x + uint64_t(NT) * e;
-    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(xv[e], s2), wn[e]), om, seq);
+    if (c < H) put_row(normed, limbs, kpad, c, mul_sat(mul_sat(xv[e], s2), wn[e]), oms);
   }
+  if (om) om_flush<NT>(oms, om, kpad, seq);
 }
 
 // Window of the attention cache at this step (cache_windows + key_start,
