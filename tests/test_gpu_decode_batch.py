@@ -154,10 +154,12 @@ def test_other_widths_batch_matches_solo(ctx, hidden, ff, n):
     run_batch_vs_solo(gm, 8192, prompts, steps=3, max_tokens=48, flags=rd.DET_COMMIT_ALL)
 
 
-@pytest.mark.parametrize("n", [5, 7, 13])
+@pytest.mark.parametrize("n", [5, 7, 13, 19, 21])
 def test_e4b_shaped_layers_partial_batches_match_solo(ctx, n):
     """Batches of 5-8 tokens take the two-token-group GEMV instances and
-    13 tokens a partly filled last group (E4B widths: K of 2048-10240)."""
+    13 tokens a partly filled last group (E4B widths: K of 2048-10240); 19
+    and 21 tokens run a second pass of 3 (single-group kernels on the limb
+    planes) or 5 tokens (the operand-major copy at its second-pass offset)."""
     cfg = synthetic.e4b_config(layers=2, vocab=4096, sliding_window=8)
     gm = build(ctx, cfg, synthetic.synthetic_model_fast(cfg, seed=11))
     prompts = ragged_prompts(n, 1, 40, 4096, seed=n)
