@@ -174,6 +174,39 @@ def test_i16_e4b_shaped_batch_matches_solo(i16_two_layers, n):
             toks[i], tok_s[i] = r.next_token, e.next_token
 
 
+@pytest.mark.parametrize("n", [6, 16])
+def test_mixed_i16_int8_batch_matches_solo(ctx, n):
+    # gate/up and the q/k/v projections in i16 digit planes (the four-token-group
+    # batched GEMV and its GELU epilogue), down, O and the vocabulary projection
+    # int8 (the register-activation GEMV on the activations the digit-plane
+    # epilogue and the row kernels write)
+    cfg = synthetic.e4b_config(layers=2, vocab=8192, sliding_window=64)
+    wide = list(synthetic.synthetic_model_i16(cfg, seed=5))
+    narrow = {name: (v, s) for name, v, s in synthetic.synthetic_model_fast(cfg, seed=5)}
+    gm = rd.Model(ctx, cfg)
+    for name, v, s in wide:
+        if any(k in name for k in ("mlp.down_proj", "o_proj", "lm_head", "embed_tokens")):
+            v, s = narrow[name]
+        gm.set_tensor(name, v, s)
+    gm = gm.finalize()
+    assert gm.fused_decode
+    rng = np.random.default_rng(n + 40)
+    lens = rng.integers(10, 60, size=n)
+    prompts = [rng.integers(0, 8192, size=int(k)).tolist() for k in lens]
+    steps = 4
+    batch = [gm.session(int(k) + steps + 1) for k in lens]
+    toks = [s.prefill(p, rd.DET_COMMIT_NONE).next_token for s, p in zip(batch, prompts)]
+    solo = [s.clone() for s in batch]
+    tok_s = list(toks)
+    for step in range(steps):
+        res = rd.decode_batch(batch, toks, rd.DET_COMMIT_ALL)
+        for i, r in enumerate(res):
+            e = solo[i].decode(tok_s[i], rd.DET_COMMIT_ALL)
+            assert (r.activation, r.logits, r.kv, r.next_token) == (e.activation, e.logits, e.kv, e.next_token), \
+                (step, i)
+            toks[i], tok_s[i] = r.next_token, e.next_token
+
+
 def test_i32_model_matches_oracle(ctx):
     # every matrix in four digit planes (one wide value per matrix): the
     # GEMMs take the 256-row blocks, the decode step its per-op form where
