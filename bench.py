@@ -510,6 +510,9 @@ def ragged_batch(ctx, rd, args, model) -> dict:
 
 
 PREFILL_SHAPES = [(2048, 2560), (512, 2560), (512, 2560), (2560, 2048), (10240, 2560), (10240, 2560), (2560, 10240)]
+# the same projections grouped as the layer prefill runs them: q/k/v and
+# gate/up each one GEMM over their shared input (indices into PREFILL_SHAPES)
+PREFILL_GROUPS = [("qkv", (0, 1, 2)), ("o", (3,)), ("gate_up", (4, 5)), ("down", (6,))]
 MFMA_INT8_PEAK_TOPS = 5000.0
 
 
@@ -519,28 +522,49 @@ def prefill_gemm(ctx, rd, args) -> dict:
     layer-set = 2 M 91 750 400, timed with HIP events over the seven GEMMs
     (including each activation limb expansion, and the partial-plane sum of
     the K-split ones) replayed as one graph; the time through per-call
-    launches is reported beside it."""
+    launches is reported beside it. The grouped figure times the same
+    projections as the layer prefill runs them: q/k/v and gate/up each one
+    GEMM over their shared input (one limb expansion each), then o and down,
+    and checks that their outputs are the separate projections' outputs."""
     from rasterdet import synthetic
 
-    mats = []
+    mats, host = [], []
     for i, (n, k) in enumerate(PREFILL_SHAPES):
         q, s = synthetic.fast_int8_matrix(args.seed * 7 + i, n, k, 256)
+        host.append((q, s))
         mats.append(ctx.upload_matrix(q, s))
+    # the grouped matrices: the member projections' rows stacked (same weights)
+    gmats = [ctx.upload_matrix(np.concatenate([host[i][0] for i in idx]), np.concatenate([host[i][1] for i in idx]))
+             for _, idx in PREFILL_GROUPS]
+    del host
     weights = sum(n * k for n, k in PREFILL_SHAPES)
     out = {"shapes": "q 2048x2560, k/v 512x2560, o 2560x2048, gate/up 10240x2560, down 2560x10240",
+           "grouped": "qkv 3072x2560, o 2560x2048, gate_up 20480x2560, down 2560x10240 (one det_linear_slab each)",
            "peak_tops": MFMA_INT8_PEAK_TOPS}
     rng = np.random.default_rng(args.seed)
     for m in (128, 512, 2048):
         acts = {k: ctx.to_device(synthetic.f32_to_act(rng.standard_normal((m, k)).astype(np.float32)))
                 for k in {k for _, k in PREFILL_SHAPES}}
         outs = [ctx.empty((m, n)) for n, _ in PREFILL_SHAPES]
+        gouts = [ctx.empty((m, sum(PREFILL_SHAPES[i][0] for i in idx))) for _, idx in PREFILL_GROUPS]
 
         def layer_set():
             for mat, (n, k), o in zip(mats, PREFILL_SHAPES, outs):
                 ctx.det_linear_slab(mat, m, acts[k], o)
 
+        def layer_set_grouped():
+            for mat, (_, idx), o in zip(gmats, PREFILL_GROUPS, gouts):
+                ctx.det_linear_slab(mat, m, acts[PREFILL_SHAPES[idx[0]][1]], o)
+
         layer_set()
+        layer_set_grouped()
         ctx.synchronize()
+        # the grouped GEMMs' outputs are the member projections' outputs side by side
+        sep = [o.numpy().reshape(m, n) for o, (n, _) in zip(outs, PREFILL_SHAPES)]
+        grouped_equal = all(
+            np.array_equal(g.numpy().reshape(m, -1), np.concatenate([sep[i] for i in idx], axis=1))
+            for g, (_, idx) in zip(gouts, PREFILL_GROUPS))
+        del sep
         reps = 5
         # the GPU's time: the layer-set's launches recorded once and replayed
         # as a graph (per call from Python, the host's launch cost exceeds the
@@ -553,6 +577,15 @@ def prefill_gemm(ctx, rd, args) -> dict:
             graph.launch()
         e1.record()
         ms = e0.elapsed_ms(e1) / reps
+        ggraph = ctx.capture(layer_set_grouped)
+        ggraph.launch()
+        g0, g1 = ctx.event(), ctx.event()
+        g0.record()
+        for _ in range(reps):
+            ggraph.launch()
+        g1.record()
+        ms_grouped = g0.elapsed_ms(g1) / reps
+        del ggraph
         # the same through one C-ABI call per GEMM, queued behind untimed work
         layer_set()
         c0, c1 = ctx.event(), ctx.event()
@@ -578,9 +611,13 @@ def prefill_gemm(ctx, rd, args) -> dict:
                         "limbs_per_projection": limbs,
                         "hw_tops": round(hw_tops, 1),
                         "hw_frac_of_int8_peak": round(hw_tops / MFMA_INT8_PEAK_TOPS, 4),
-                        "ms_per_layer_set_calls": round(ms_calls, 4)}
+                        "ms_per_layer_set_calls": round(ms_calls, 4),
+                        "ms_per_layer_set_grouped": round(ms_grouped, 4),
+                        "grouped_alg_tops": round(2 * m * weights / (ms_grouped / 1e3) / 1e12, 1),
+                        "grouped_outputs_equal_separate": grouped_equal}
         log(f"[bench] prefill GEMM M={m}: {ms:.3f} ms per layer-set (graph replay), {ms_calls:.3f} ms through "
-            f"per-call launches, {tops:.1f} algorithmic TOPS")
+            f"per-call launches, {tops:.1f} algorithmic TOPS; grouped as the layer runs them (qkv, o, gate_up, "
+            f"down): {ms_grouped:.3f} ms, outputs equal: {grouped_equal}")
         del graph
     return out
 
@@ -620,11 +657,15 @@ def gemm_profile(ctx, rd, seed: int) -> int:
 def gemm_sets_profile(ctx, rd, seed: int) -> int:
     """Kernel-trace workload for the prefill GEMM: the seven E4B projections
     through det_linear_slab at M = 128, 512 and 2048 rows, 3 layer-sets each
-    (the per-projection limb expansions, GEMMs and partial-plane sums)."""
+    (the per-projection limb expansions, GEMMs and partial-plane sums), then
+    3 grouped layer-sets (qkv, o, gate_up, down) at the same row count."""
     from rasterdet import synthetic
 
-    mats = [ctx.upload_matrix(*synthetic.fast_int8_matrix(seed * 7 + i, n, k, 256))
-            for i, (n, k) in enumerate(PREFILL_SHAPES)]
+    host = [synthetic.fast_int8_matrix(seed * 7 + i, n, k, 256) for i, (n, k) in enumerate(PREFILL_SHAPES)]
+    mats = [ctx.upload_matrix(q, s) for q, s in host]
+    gmats = [ctx.upload_matrix(np.concatenate([host[i][0] for i in idx]), np.concatenate([host[i][1] for i in idx]))
+             for _, idx in PREFILL_GROUPS]
+    del host
     rng = np.random.default_rng(seed)
     for m in (128, 512, 2048):
         acts = {k: ctx.to_device(synthetic.f32_to_act(rng.standard_normal((m, k)).astype(np.float32)))
@@ -633,8 +674,13 @@ def gemm_sets_profile(ctx, rd, seed: int) -> int:
         for _ in range(3):
             for mat, (n, k), o in zip(mats, PREFILL_SHAPES, outs):
                 ctx.det_linear_slab(mat, m, acts[k], o)
+        gouts = [ctx.empty((m, sum(PREFILL_SHAPES[i][0] for i in idx))) for _, idx in PREFILL_GROUPS]
+        for _ in range(3):
+            for mat, (_, idx), o in zip(gmats, PREFILL_GROUPS, gouts):
+                ctx.det_linear_slab(mat, m, acts[PREFILL_SHAPES[idx[0]][1]], o)
         ctx.synchronize()
-    print(json.dumps({"gemm_sets_profile": True, "m": [128, 512, 2048], "layer_sets": 3}), flush=True)
+    print(json.dumps({"gemm_sets_profile": True, "m": [128, 512, 2048], "layer_sets": 3, "grouped_sets": 3}),
+          flush=True)
     return 0
 
 
