@@ -1389,7 +1389,10 @@ __global__ __launch_bounds__(256) void k_act_limbs_rows(const int32_t* __restric
 // Block: TA A tiles (TA / 4 token groups of 16 tokens, four limb tiles each)
 // x TB weight tiles on WM x WN waves, each wave (TA / WM) x (TB / WN) MFMA
 // tiles (whole token groups). A block whose token groups all take three limbs
-// copies and multiplies no fourth-limb tile. Every 128-column K step, the block's
+// multiplies no fourth-limb tile, and with two buffers does not copy them
+// either (with more, every wave copies a fixed number of tile-step halves per
+// step, so that one vmcnt immediate covers the steps in flight). Every
+// 128-column K step, the block's
 // TA + TB tile-steps (2 KB each) are copied straight from global memory into
 // one of NBUF LDS buffers with global_load_lds_dwordx4 (no register staging):
 // the copies of the next NBUF - 1 steps are in flight while step s's MFMAs
@@ -1421,7 +1424,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   constexpr int LPW = 2 * TS / NW;             // 1 KB wave copies per wave per K step
   constexpr int FA = TA / WM, FB = TB / WN;    // MFMA tiles per wave
   static_assert(2 * TS % NW == 0, "copies must divide evenly");
-  static_assert(FA % 4 == 0 && NBUF == 2, "whole token groups per wave; every step waits for all its copies");
+  static_assert(FA % 4 == 0 && NBUF >= 2, "whole token groups per wave");
   extern __shared__ __attribute__((aligned(16))) int8_t lds_gemm[];
   // the wave index as a scalar, so that copy addresses and LDS targets stay in SGPRs
   const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1485,7 +1488,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
 #pragma unroll
     for (int u = 0; u < LPW; ++u) {
       const uint32_t c = wave * LPW + u;
-      if (four || !limb3[u])
+      if (NBUF > 2 || four || !limb3[u])
         __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[u] + s * 2048),
                                          (void __attribute__((address_space(3)))*)(lds_gemm + (buf * TS * 2 + c) * 1024),
                                          16, 0, 0);
@@ -2908,11 +2911,22 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
   const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
   const uint32_t kc = planes ? gemm_kchunks(W, m) : 1;
   const bool small = gemm_small(W, m);
+  // Grids that fit one round at the deeper pipeline's residency (64 KB of LDS
+  // per small block, two per CU; 128 KB per 128 x 128 block, one per CU) keep
+  // three K steps of copies in flight instead of one: at 128 rows the K loop
+  // of a lone block waits on its copies' latency (q/k/v 3072 x 2560 18.4 ->
+  // 14.2 us, o 11.8 -> 9.5, down's three K chunks 27.2 -> 20.1 us); larger
+  // grids keep two buffers and two blocks per CU.
+  const uint64_t cus = device_cus();
+  const uint64_t vt = (W.rows + 15) / 16 * uint64_t(W.planes);
+  const bool deep = small ? ((m + 15) / 16) * ((vt + 3) / 4) * kc <= 2 * cus : ((m + 31) / 32) * ((vt + 7) / 8) * kc <= cus;
   if (kc > 1) {
     KSplit ks;
     ks.chunks = kc;
     ks.planes = planes;
-    if (small) launch_gemm_lds_shape<4, 4, 1, 4, 8, 2>(W, m, nullptr, 0, nullptr, a_tiled, a_tiles, s, {}, ks);
+    if (small && deep) launch_gemm_lds_shape<4, 4, 1, 4, 8, 4>(W, m, nullptr, 0, nullptr, a_tiled, a_tiles, s, {}, ks);
+    else if (small) launch_gemm_lds_shape<4, 4, 1, 4, 8, 2>(W, m, nullptr, 0, nullptr, a_tiled, a_tiles, s, {}, ks);
+    else if (deep) launch_gemm_lds_shape<8, 8, 2, 4, 8, 4>(W, m, nullptr, 0, nullptr, a_tiled, a_tiles, s, {}, ks);
     else launch_gemm_lds_shape<8, 8, 2, 4, 8, 2>(W, m, nullptr, 0, nullptr, a_tiled, a_tiles, s, {}, ks);
     const uint64_t total = m * W.rows;
     hipLaunchKernelGGL(k_gemm_reduce, dim3(unsigned((total + 511) / 512)), dim3(256), 0, s, planes, kc, m, W.rows,
@@ -2923,20 +2937,25 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
   // out of the 256 x 256 block's registers)
   if (split) {
     if (W.planes > 2) throw std::invalid_argument("row-split GEMM: at most two digit planes");
+    if (small && deep)
+      return launch_gemm_lds_shape<4, 4, 1, 4, 8, 4, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
     if (small) return launch_gemm_lds_shape<4, 4, 1, 4, 8, 2, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
+    if (deep) return launch_gemm_lds_shape<8, 8, 2, 4, 8, 4, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
     return launch_gemm_lds_shape<8, 8, 2, 4, 8, 2, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
   }
+  if (small && deep) return launch_gemm_lds_shape<4, 4, 1, 4, 8, 4>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   if (small) return launch_gemm_lds_shape<4, 4, 1, 4, 8, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   // 64 tokens x 256 rows on 8 waves (one block per CU) when its blocks fill
   // whole rounds of the device; otherwise 32 tokens x 128 rows on 8 waves
   // (two blocks per CU, so two waves per SIMD hide each other's LDS and
   // MFMA latency), whose finer grid leaves a smaller last round. Four digit
   // planes take the larger block (four weight tiles per wave).
-  const uint64_t cus = device_cus();
-  const uint64_t big = ((m + 63) / 64) * (((W.rows + 15) / 16 * uint64_t(W.planes) + 15) / 16);
+  const uint64_t big = ((m + 63) / 64) * ((vt + 15) / 16);
   const uint64_t rounds = (big + cus - 1) / cus;
   if (W.planes > 2 || (big >= cus && big * 10 >= rounds * cus * 9))
     launch_gemm_lds_shape<16, 16, 2, 4, 4, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
+  else if (deep)
+    launch_gemm_lds_shape<8, 8, 2, 4, 8, 4>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   else
     launch_gemm_lds_shape<8, 8, 2, 4, 8, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
 }
