@@ -597,6 +597,13 @@ def prefill_gemm(ctx, rd, args) -> dict:
             layer_set()
         c1.record()
         ms_calls = c0.elapsed_ms(c1) / reps
+        layer_set_grouped()
+        d0, d1 = ctx.event(), ctx.event()
+        d0.record()
+        for _ in range(reps):
+            layer_set_grouped()
+        d1.record()
+        ms_grouped_calls = d0.elapsed_ms(d1) / reps
         tops = 2 * m * weights / (ms / 1e3) / 1e12
         # int8 MFMA ops the GEMMs issue: 3 activation limbs per (16-token
         # group, 512-column part) whose values lie in [-2^23, 2^23), else 4
@@ -616,11 +623,13 @@ def prefill_gemm(ctx, rd, args) -> dict:
                         "hw_frac_of_int8_peak": round(hw_tops / MFMA_INT8_PEAK_TOPS, 4),
                         "ms_per_layer_set_calls": round(ms_calls, 4),
                         "ms_per_layer_set_grouped": round(ms_grouped, 4),
+                        "ms_per_layer_set_grouped_calls": round(ms_grouped_calls, 4),
                         "grouped_alg_tops": round(2 * m * weights / (ms_grouped / 1e3) / 1e12, 1),
                         "grouped_outputs_equal_separate": grouped_equal}
         log(f"[bench] prefill GEMM M={m}: {ms:.3f} ms per layer-set (graph replay), {ms_calls:.3f} ms through "
             f"per-call launches, {tops:.1f} algorithmic TOPS; grouped as the layer runs them (qkv, o, gate_up, "
-            f"down): {ms_grouped:.3f} ms, outputs equal: {grouped_equal}")
+            f"down): {ms_grouped:.3f} ms ({ms_grouped_calls:.3f} ms through per-call launches), outputs equal: "
+            f"{grouped_equal}")
         del graph
     return out
 
