@@ -2950,9 +2950,15 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
   // (two blocks per CU, so two waves per SIMD hide each other's LDS and
   // MFMA latency), whose finer grid leaves a smaller last round. Four digit
   // planes take the larger block (four weight tiles per wave).
+  // A single round of 256 x 256 blocks that fills at least five eighths of
+  // the CUs also beats 128 x 128 blocks that need more than one round at two
+  // per CU (the 20480-row gate/up slab at 128 rows: 160 blocks, 41 us against
+  // 49 us for 640 128 x 128 blocks, cold weights).
   const uint64_t big = ((m + 63) / 64) * ((vt + 15) / 16);
   const uint64_t rounds = (big + cus - 1) / cus;
-  if (W.planes > 2 || (big >= cus && big * 10 >= rounds * cus * 9))
+  const uint64_t blocks128 = ((m + 31) / 32) * ((vt + 7) / 8);
+  const bool one_round = big < cus && big * 8 >= cus * 5 && blocks128 > 2 * cus;
+  if (W.planes > 2 || (big >= cus && big * 10 >= rounds * cus * 9) || one_round)
     launch_gemm_lds_shape<16, 16, 2, 4, 4, 2>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
   else if (deep)
     launch_gemm_lds_shape<8, 8, 2, 4, 8, 4>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s);
