@@ -1394,7 +1394,11 @@ __global__ __launch_bounds__(256) void k_act_limbs_rows(const int32_t* __restric
 // step, so that one vmcnt immediate covers the steps in flight). Every
 // 128-column K step, the block's
 // TA + TB tile-steps (2 KB each) are copied straight from global memory into
-// one of NBUF LDS buffers with global_load_lds_dwordx4 (no register staging):
+// one of NBUF LDS buffers with global_load_lds_dwordx4 (no register staging).
+// The 2 (TA + TB) copy halves are dealt out LPW per wave; where they do not
+// divide evenly, the slots past them re-copy the block's first weight
+// tile-step half into the buffer's spare kilobytes, so that every wave issues
+// the same copies per step:
 // the copies of the next NBUF - 1 steps are in flight while step s's MFMAs
 // run, and one barrier per step hands a buffer over. Copy h of a tile-step
 // takes the 16-byte half h of every lane's 32 columns (a weight tile-step's
@@ -1421,9 +1425,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   const int lp = DG ? lp_arg : 0;  // (single-plane instances fold it to 0)
   constexpr int NW = WM * WN;                  // waves
   constexpr int TS = TA + TB;                  // tile-steps per K step
-  constexpr int LPW = 2 * TS / NW;             // 1 KB wave copies per wave per K step
+  constexpr int LPW = (2 * TS + NW - 1) / NW;  // 1 KB wave copies per wave per K step
+  constexpr int SLOTS = LPW * NW;               // 1 KB copy slots per LDS buffer (>= 2 TS)
   constexpr int FA = TA / WM, FB = TB / WN;    // MFMA tiles per wave
-  static_assert(2 * TS % NW == 0, "copies must divide evenly");
   static_assert(FA % 4 == 0 && NBUF >= 2, "whole token groups per wave");
   extern __shared__ __attribute__((aligned(16))) int8_t lds_gemm[];
   // the wave index as a scalar, so that copy addresses and LDS targets stay in SGPRs
@@ -1476,7 +1480,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
   for (int u = 0; u < LPW; ++u) {
     const uint32_t c = wave * LPW + u, ts = c >> 1, h = c & 1;
     const bool is_a = ts < uint32_t(TA);
-    uint64_t tile = is_a ? at0 + ts : bt0 + (ts - TA);
+    uint64_t tile = is_a ? at0 + ts : (ts < uint32_t(TS) ? bt0 + (ts - TA) : bt0);  // (spare slots: bt0)
     if (is_a ? tile >= a_tiles : tile >= ntiles) tile = (is_a ? a_tiles : ntiles) - 1;
     // (weight tile-steps hold each half of the lanes' operands contiguously;
     // the activation limb tiles keep the 32-byte lane slots)
@@ -1490,7 +1494,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
       const uint32_t c = wave * LPW + u;
       if (NBUF > 2 || four || !limb3[u])
         __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[u] + s * 2048),
-                                         (void __attribute__((address_space(3)))*)(lds_gemm + (buf * TS * 2 + c) * 1024),
+                                         (void __attribute__((address_space(3)))*)(lds_gemm + (buf * SLOTS + c) * 1024),
                                          16, 0, 0);
     }
   };
@@ -1549,7 +1553,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_lds(const int8_t* __restr
     constexpr int L = decltype(Lc)::value;
     for (uint64_t s = 0; s < nsteps; ++s) {
       const int buf = int(s % NBUF);
-      const int8_t* base = lds_gemm + buf * TS * 2048 + lane * 16;
+      const int8_t* base = lds_gemm + buf * SLOTS * 1024 + lane * 16;
       // the first half's operands, the copies, the second half's operands
       // (read while the first half's MFMAs run), then the MFMAs
       v4i ao[2][FA], bo[2][FB];
@@ -2832,7 +2836,9 @@ uint64_t gemm_act_bytes(uint64_t m, uint64_t kpad) {
 template <int TA, int TB, int WM, int WN, uint32_t GM, int NBUF, bool SPLIT, bool GELU, bool DG>
 static void launch_gemm_lds_dg(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,
                                const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s, RowSplit split, KSplit ks) {
-  constexpr uint32_t lds = uint32_t(NBUF) * (TA + TB) * 2048u;
+  constexpr int NW = WM * WN;
+  constexpr uint32_t lds = uint32_t(NBUF) * uint32_t((2 * (TA + TB) + NW - 1) / NW * NW) * 1024u;
+  static_assert(lds <= 160u * 1024u, "LDS of one workgroup");
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&k_gemm_lds<TA, TB, WM, WN, GM, NBUF, SPLIT, GELU, DG>),
       hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
@@ -2878,6 +2884,42 @@ static bool gemm_small(const DevMatrix& W, uint64_t m) {
   const uint64_t blocks128 = ((m + 31) / 32) * (((W.rows + 15) / 16 + 7) / 8);
   return blocks128 < device_cus();
 }
+// One-round block shapes: a grid of one block per CU that fills at least
+// nine tenths of the CUs, for single-plane matrices of at most 32 K steps,
+// each wave one token group x one or five weight tiles, four LDS buffers
+// where they fit (their copy halves per K step need not divide over the
+// waves). Tried in this order (cold weights, 128 rows):
+//   64 tokens x 160 rows, 8 waves, 2 buffers (112 KB): the 20480-row gate/up
+//     37.1 us against 39.7 us in 256 x 256 blocks, with the GELU epilogue
+//     41.1 against 51.2 us in 128 x 128 blocks;
+//   32 tokens x 48 rows, 6 waves (96 KB): q/k/v 3072 x 2560 11.7 against
+//     14.4 us in 384 16 x 64 blocks;
+//   16 tokens x 80 rows, 5 waves (80 KB): o 2560 x 2048 8.5 against 9.3 us.
+// At 512 and 2048 rows the grids take several rounds and none applies.
+enum class PadShape { kNone, k64x160, k32x48, k16x80 };
+static PadShape gemm_pad_shape(const DevMatrix& W, uint64_t m) {
+  if (W.storage != kInt8 || W.planes != 1 || W.kpad > 32 * 128) return PadShape::kNone;
+  const uint64_t tiles = (W.rows + 15) / 16, cus = device_cus();
+  auto fills = [&](uint64_t tokens, uint64_t tb) {
+    const uint64_t blocks = ((m + tokens - 1) / tokens) * ((tiles + tb - 1) / tb);
+    return blocks <= cus && blocks * 10 >= cus * 9;
+  };
+  if (fills(64, 10)) return PadShape::k64x160;
+  if (fills(32, 3)) return PadShape::k32x48;
+  if (fills(16, 5)) return PadShape::k16x80;
+  return PadShape::kNone;
+}
+template <bool SPLIT, bool GELU>
+static void launch_gemm_pad(PadShape p, const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out,
+                            int64_t* acc_out, const int8_t* a_tiled, uint64_t a_tiles, hipStream_t s,
+                            RowSplit split) {
+  if (p == PadShape::k64x160)
+    launch_gemm_lds_dg<16, 10, 4, 2, 8, 2, SPLIT, GELU, false>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s, split, {});
+  else if (p == PadShape::k32x48)
+    launch_gemm_lds_dg<8, 3, 2, 3, 8, 4, SPLIT, GELU, false>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s, split, {});
+  else
+    launch_gemm_lds_dg<4, 5, 1, 5, 8, 4, SPLIT, GELU, false>(W, m, out, ld_out, acc_out, a_tiled, a_tiles, s, split, {});
+}
 uint32_t gemm_kchunks(const DevMatrix& W, uint64_t m) {
   if (W.storage != kInt8 || m == 0 || W.rows == 0 || W.planes > 2) return 1;
   const bool small = gemm_small(W, m);
@@ -2909,6 +2951,11 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
                        const int8_t* a_tiled, hipStream_t s, const RowSplit* split, int64_t* planes) {
   if (W.rows == 0 || m == 0) return;
   const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
+  const PadShape pad = gemm_pad_shape(W, m);
+  if (pad != PadShape::kNone) {
+    if (split) return launch_gemm_pad<true, false>(pad, W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, *split);
+    return launch_gemm_pad<false, false>(pad, W, m, out, ld_out, acc_out, a_tiled, a_tiles, s, {});
+  }
   const uint32_t kc = planes ? gemm_kchunks(W, m) : 1;
   const bool small = gemm_small(W, m);
   // Grids that fit one round at the deeper pipeline's residency (64 KB of LDS
@@ -2972,8 +3019,12 @@ void launch_gemm_tiled_gelu(const DevMatrix& W, uint64_t m, int32_t* out, uint64
   if (W.rows % 16) throw std::invalid_argument("gate/up GEMM: rows must be whole tiles of 8 gate + 8 up rows");
   if (W.planes > 2) throw std::invalid_argument("gate/up GEMM: at most two digit planes");
   const uint64_t a_tiles = (m + 63) / 64 * 64 / 4;
-  // 128 x 128 blocks at every m (no K split): with the GELU arithmetic in its
-  // epilogue the 256 x 256 block does not fit its registers
+  // a one-round block shape where one fills the device, else 128 x 128
+  // blocks (no K split): with the GELU arithmetic in its epilogue the
+  // 256 x 256 block does not fit its registers
+  const PadShape pad = gemm_pad_shape(W, m);
+  if (pad != PadShape::kNone)
+    return launch_gemm_pad<false, true>(pad, W, m, out, ld_out, nullptr, a_tiled, a_tiles, s, {});
   launch_gemm_lds_shape<8, 8, 2, 4, 8, 2, false, true>(W, m, out, ld_out, nullptr, a_tiled, a_tiles, s);
 }
 

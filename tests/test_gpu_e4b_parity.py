@@ -108,7 +108,9 @@ def two_layer_models(ctx):
     return e4b_two_layers(ctx)
 
 
-@pytest.mark.parametrize("prompt_len", [600, 777])
+# 100 and 128 tokens: the layer prefill's gate/up GEMM with the GELU epilogue
+# in one round of 64 x 160 blocks
+@pytest.mark.parametrize("prompt_len", [100, 128, 600, 777])
 def test_two_layer_e4b_long_prompt_capture(two_layer_models, prompt_len):
     om, gm = two_layer_models
     rng = np.random.default_rng(prompt_len)
