@@ -42,8 +42,8 @@ struct DevMatrix {
 };
 
 // Columns per part of the prefill GEMM's per-part limb decomposition.
-constexpr uint64_t kLimbPartCols = 512;
-// More parts than this (K above 32768) take four limbs throughout.
+constexpr uint64_t kLimbPartCols = 256;
+// More parts than this (K above 16384) take four limbs throughout.
 constexpr uint64_t kLimbMaxParts = 64;
 __host__ __device__ inline uint64_t limb_parts(uint64_t kpad) { return (kpad + kLimbPartCols - 1) / kLimbPartCols; }
 

@@ -1321,32 +1321,37 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
 // the signed bytes of u; its top byte is 0, so the fourth limb tile is zero
 // and the GEMM skips it); otherwise u = a ^ 0x808080, a = sum_{j<4} c_j 256^j
 // + 8421504. flags[T * parts + p] = 1 marks the four-limb parts.
-// One workgroup per (16-token group T, part), 256 threads: thread (r, l)
-// reads token 16 T + r's columns 64 q + 4 l + [0, 4) of the part (q < 8), so
-// each load instruction covers four rows x 256 contiguous bytes (vec: act rows
-// are 16-byte aligned, base and ld, and load as 128-bit reads); the
-// workgroup decides the part's decomposition (__syncthreads_or); the limb
-// bytes are regrouped in LDS into the tile-step layout (limb j, step, lane
-// slot 16 g + i of 32 bytes: token i's columns 32 g + [0, 32) of the step)
-// and copied out in whole 16-byte pieces, each tile-step a contiguous 2 KB.
-// Tokens past m and columns past k are zero.
-__global__ __launch_bounds__(256) void k_act_limbs_rows(const int32_t* __restrict__ act, uint64_t m, uint64_t k,
-                                                       uint64_t ld, uint64_t kpad, int vec,
-                                                       uint32_t* __restrict__ flags, int8_t* __restrict__ out) {
-  constexpr uint32_t PS = uint32_t(kLimbPartCols / 128);  // K steps per part
-  static_assert(PS == 4, "four 128-column steps per part");
+// One workgroup per (16-token group T, part), NT threads (LPT = NT / 16 per
+// token): thread (r, l) reads token 16 T + r's columns 4 l + 4 LPT q + [0, 4)
+// of the part, so each load instruction covers 64 / LPT rows x 16 LPT
+// contiguous bytes (vec: act rows are 16-byte aligned, base and ld, and load
+// as 128-bit reads); the workgroup decides the part's decomposition
+// (__syncthreads_or); the limb bytes are regrouped in LDS into the tile-step
+// layout (limb j, step, lane slot 16 g + i of 32 bytes: token i's columns
+// 32 g + [0, 32) of the step) and copied out in whole 16-byte pieces, each
+// tile-step a contiguous 2 KB. Tokens past m and columns past k are zero.
+// 512 threads for grids of up to 512 workgroups (shorter chains per thread),
+// else 256: at 128 rows 3.1 us against 4.3 us for 256 threads and 512-column
+// parts (K = 2560), at 2048 rows x 10240 columns 24.6 against 26.1 us.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_act_limbs_rows(const int32_t* __restrict__ act, uint64_t m, uint64_t k,
+                                                      uint64_t ld, uint64_t kpad, int vec,
+                                                      uint32_t* __restrict__ flags, int8_t* __restrict__ out) {
+  constexpr int PC = int(kLimbPartCols), PS = PC / 128;  // columns and K steps per part
+  constexpr int LPT = NT / 16, Q = PC / (4 * LPT);       // threads per token, loads per thread
+  static_assert(Q >= 1 && PC % (4 * LPT) == 0, "whole 16-byte loads per thread");
   __shared__ __attribute__((aligned(16))) uint32_t st[4][PS][64][8];
   const uint64_t nsteps = kpad / 128, parts = limb_parts(kpad);
   const uint64_t T = blockIdx.x, part = blockIdx.y;
-  const uint32_t r = threadIdx.x >> 4, l = threadIdx.x & 15;
+  const uint32_t r = threadIdx.x / LPT, l = threadIdx.x % LPT;
   const uint64_t t = 16 * T + r;
   const bool row_on = t < m;
   const int32_t* src = act + (row_on ? t : 0) * ld;
-  const uint64_t c0 = part * kLimbPartCols + 4 * l;
-  uint32_t a[32];
+  const uint64_t c0 = part * PC + 4 * l;
+  uint32_t a[4 * Q];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const uint64_t c = c0 + 64 * q;
+  for (int q = 0; q < Q; ++q) {
+    const uint64_t c = c0 + 4 * LPT * q;
     if (vec && row_on && c + 4 <= k) {
       const int4 v = *reinterpret_cast<const int4*>(src + c);
       a[4 * q] = uint32_t(v.x), a[4 * q + 1] = uint32_t(v.y), a[4 * q + 2] = uint32_t(v.z), a[4 * q + 3] = uint32_t(v.w);
@@ -1357,28 +1362,31 @@ __global__ __launch_bounds__(256) void k_act_limbs_rows(const int32_t* __restric
   }
   uint32_t wide = 0;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) wide |= a[e] + 0x800000u >= 0x1000000u;
+  for (int e = 0; e < 4 * Q; ++e) wide |= a[e] + 0x800000u >= 0x1000000u;
   const bool four = __syncthreads_or(int(wide)) != 0 || parts > kLimbMaxParts;
   if (threadIdx.x == 0) flags[T * parts + part] = four ? 1u : 0u;
   const uint32_t off = four ? 0u : 0x800000u;
-  // column 64 q + 4 l + e of the part: step q / 2, lane group g = 2 (q % 2) +
-  // l / 8, byte 4 (l % 8) + e of the lane slot
+  // column cp = 4 l + 4 LPT q + e of the part: step cp / 128, lane group
+  // g = (cp % 128) / 32, byte cp % 32 of the lane slot (word (cp % 32) / 4)
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
+  for (int q = 0; q < Q; ++q) {
+    const uint32_t cp = 4 * l + 4 * LPT * q;
     uint32_t u[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) u[e] = (row_on && c0 + 64 * q + e < k) ? (a[4 * q + e] + off) ^ 0x00808080u : 0u;
-    const uint32_t g = 2 * (q & 1) + (l >> 3);
+    for (int e = 0; e < 4; ++e) u[e] = (row_on && c0 + 4 * LPT * q + e < k) ? (a[4 * q + e] + off) ^ 0x00808080u : 0u;
+    const uint32_t sl = cp / 128, g = (cp % 128) / 32, w = (cp % 32) / 4;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      st[j][q >> 1][16 * g + r][l & 7] = ((u[0] >> (8 * j)) & 0xffu) | ((u[1] >> (8 * j)) & 0xffu) << 8 |
-                                         ((u[2] >> (8 * j)) & 0xffu) << 16 | ((u[3] >> (8 * j)) & 0xffu) << 24;
+      st[j][sl][16 * g + r][w] = ((u[0] >> (8 * j)) & 0xffu) | ((u[1] >> (8 * j)) & 0xffu) << 8 |
+                                 ((u[2] >> (8 * j)) & 0xffu) << 16 | ((u[3] >> (8 * j)) & 0xffu) << 24;
   }
   __syncthreads();
-  // 16 tile-steps of 2 KB (limb j, step sl of the part), 128 pieces each
+  // 4 PS tile-steps of 2 KB (limb j, step sl of the part), 128 pieces each
+  constexpr int PIECES = 4 * PS * 128;
+  static_assert(PIECES % NT == 0, "whole pieces per thread");
 #pragma unroll
-  for (int kq = 0; kq < 8; ++kq) {
-    const uint32_t p = threadIdx.x + 256 * kq, chunk = p >> 7, j = chunk >> 2, sl = chunk & 3;
+  for (int kq = 0; kq < PIECES / NT; ++kq) {
+    const uint32_t p = threadIdx.x + NT * kq, chunk = p >> 7, j = chunk / PS, sl = chunk % PS;
     const uint64_t step = part * PS + sl;
     if (step < nsteps)
       *reinterpret_cast<int4*>(out + ((4 * T + j) * nsteps + step) * 2048 + (p & 127) * 16) =
@@ -2943,8 +2951,13 @@ void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_a
   if (m == 0) return;
   const uint64_t groups = (m + 63) / 64 * 4;  // the larger block's 4 token groups
   const int vec = (reinterpret_cast<uintptr_t>(act) % 16 == 0 && ld_act % 4 == 0) ? 1 : 0;
-  hipLaunchKernelGGL(k_act_limbs_rows, dim3(unsigned(groups), unsigned(limb_parts(kpad))), dim3(256), 0, s, act, m,
-                     k, ld_act, kpad, vec, gemm_flags(a_tiled, m, kpad), a_tiled);
+  const dim3 grid(unsigned(groups), unsigned(limb_parts(kpad)));
+  if (uint64_t(grid.x) * grid.y <= 512)
+    hipLaunchKernelGGL(k_act_limbs_rows<512>, grid, dim3(512), 0, s, act, m, k, ld_act, kpad, vec,
+                       gemm_flags(a_tiled, m, kpad), a_tiled);
+  else
+    hipLaunchKernelGGL(k_act_limbs_rows<256>, grid, dim3(256), 0, s, act, m, k, ld_act, kpad, vec,
+                       gemm_flags(a_tiled, m, kpad), a_tiled);
 }
 
 void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld_out, int64_t* acc_out,

@@ -90,7 +90,7 @@ def test_gemm_adversarial_values(ctx):
 @pytest.mark.parametrize("m,n,k", [(100, 300, 2600), (200, 1000, 777), (64, 128, 4096)])
 def test_gemm_limb_decompositions(ctx, m, n, k):
     # token groups of 16 whose activations lie in [-2^23, 2^23) over a
-    # 512-column part take three limbs there, the others four: values at both
+    # 256-column part take three limbs there, the others four: values at both
     # edges of the range, groups with a single value outside it, values at the
     # top of the int32 range, blocks mixing both kinds
     rng = np.random.default_rng(m + n + k)
