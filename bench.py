@@ -608,14 +608,14 @@ def prefill_gemm(ctx, rd, args) -> dict:
         ms_grouped_calls = d0.elapsed_ms(d1) / reps
         tops = 2 * m * weights / (ms / 1e3) / 1e12
         # int8 MFMA ops the GEMMs issue: 3 activation limbs per (16-token
-        # group, 512-column part) whose values lie in [-2^23, 2^23), else 4
+        # group, 256-column part) whose values lie in [-2^23, 2^23), else 4
         # (a block with any four-limb part runs four throughout: counted as
-        # four for the whole projection); rows past 32768 columns take four
+        # four for the whole projection); rows past 16384 columns take four
         host_acts = {k: v.numpy().reshape(m, k) for k, v in acts.items()}
         limbs = []
         for n, k in PREFILL_SHAPES:
             a = host_acts[k]
-            wide = k > 32768 or bool(((a < -(1 << 23)) | (a >= (1 << 23))).any())
+            wide = k > 16384 or bool(((a < -(1 << 23)) | (a >= (1 << 23))).any())
             limbs.append(4 if wide else 3)
         hw_tops = sum(2 * m * n * k * l for (n, k), l in zip(PREFILL_SHAPES, limbs)) / (ms / 1e3) / 1e12
         out[f"M{m}"] = {"ms_per_layer_set": round(ms, 4), "alg_tops": round(tops, 1),
