@@ -3012,8 +3012,10 @@ void launch_gemm_tiled(const DevMatrix& W, uint64_t m, int32_t* out, uint64_t ld
   // planes take the larger block (four weight tiles per wave).
   // A single round of 256 x 256 blocks that fills at least five eighths of
   // the CUs also beats 128 x 128 blocks that need more than one round at two
-  // per CU (the 20480-row gate/up slab at 128 rows: 160 blocks, 41 us against
-  // 49 us for 640 128 x 128 blocks, cold weights).
+  // per CU (measured on the 20480-row gate/up slab at 128 rows: 160 blocks,
+  // 41 us against 49 us for 640 128 x 128 blocks, cold weights; single-plane
+  // matrices of that shape now take the one-round 64 x 160 block above, and
+  // this rule serves digit-plane matrices and rows past 4096 columns).
   const uint64_t big = ((m + 63) / 64) * ((vt + 15) / 16);
   const uint64_t rounds = (big + cus - 1) / cus;
   const uint64_t blocks128 = ((m + 31) / 32) * ((vt + 7) / 8);
