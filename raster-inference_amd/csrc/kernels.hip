@@ -2930,6 +2930,7 @@ static void launch_gemm_pad(PadShape p, const DevMatrix& W, uint64_t m, int32_t*
 }
 uint32_t gemm_kchunks(const DevMatrix& W, uint64_t m) {
   if (W.storage != kInt8 || m == 0 || W.rows == 0 || W.planes > 2) return 1;
+  if (gemm_pad_shape(W, m) != PadShape::kNone) return 1;  // one-round blocks, no K split
   const bool small = gemm_small(W, m);
   const uint64_t blocks = small ? ((m + 15) / 16) * (((W.rows + 15) / 16 + 3) / 4)
                                 : ((m + 31) / 32) * (((W.rows + 15) / 16 * uint64_t(W.planes) + 7) / 8);
