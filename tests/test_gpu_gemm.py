@@ -127,12 +127,14 @@ def test_gemm_unaligned_activation_rows(ctx):
 # (160, 16384, 2560): one round of 256 x 256 blocks filling at least five
 # eighths of the CUs instead of more than one round of 128 x 128 blocks (a
 # ragged last token block). One-round blocks whose copy halves per K step do
-# not divide over the waves: (128 | 100, 20480, 2560) 64 x 160 blocks (the
-# stacked gate/up slab), (128 | 100, 3072, 2560) 32 x 48 blocks (q/k/v),
-# (128, 2560, 2048) 16 x 80 blocks (o).
-@pytest.mark.parametrize("m,n,k", [(128, 3072, 2560), (100, 3072, 2560), (64, 2560, 10240), (48, 2560, 2048),
-                                   (128, 2560, 2048), (256, 16384, 512), (300, 13100, 2600), (128, 20480, 2560),
-                                   (100, 20480, 2560), (160, 16384, 2560)])
+# not divide over the waves: (128 | 100 | 65, 20480, 2560) 64 x 160 blocks
+# (the stacked gate/up slab; 65 rows: one token in the last block),
+# (128 | 100 | 97, 3072, 2560) 32 x 48 blocks (q/k/v), (128 | 113, 2560, 2048)
+# 16 x 80 blocks (o; 113 rows: one token in the last group).
+@pytest.mark.parametrize("m,n,k", [(128, 3072, 2560), (100, 3072, 2560), (97, 3072, 2560), (64, 2560, 10240),
+                                   (48, 2560, 2048), (128, 2560, 2048), (113, 2560, 2048), (256, 16384, 512),
+                                   (300, 13100, 2600), (128, 20480, 2560), (100, 20480, 2560), (65, 20480, 2560),
+                                   (160, 16384, 2560)])
 def test_gemm_e4b_shapes_match_gemv_rows(ctx, m, n, k):
     q, s = synthetic.fast_int8_matrix(n * 31 + k, n, k, 256)
     acts = act_slab(m, k, seed=n + k)
