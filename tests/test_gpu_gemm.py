@@ -66,6 +66,21 @@ def test_gemm_matches_oracle(ctx, m, n, k):
     assert np.array_equal(got, exp)
 
 
+@pytest.mark.parametrize("m,n,k", [(40, 96, 16384), (40, 96, 17000)])
+def test_gemm_longest_rows(ctx, m, n, k):
+    # 16384 columns: 64 column parts, each with its own limb count (one value
+    # past 2^23 in the last part of one token group); 17000 columns: more parts
+    # than the per-group flag mask holds, so every part takes four limbs
+    rng = np.random.default_rng(k)
+    q, s = synthetic.random_int8_matrix(rng, n, k, scale_max=256)
+    acts = act_slab(m, k, seed=k)
+    acts[5, k - 3] = 2**23 + 5
+    mat = ctx.upload_matrix(q, s)
+    got = gpu_slab(ctx, mat, acts)
+    exp = oracle_lib.det_linear_slab(expand(q, s), acts, threads=oracle_lib.cpu_count())
+    assert np.array_equal(got, exp)
+
+
 def test_gemm_adversarial_values(ctx):
     # activations at the i32 edges, weights at +-127, scales at the largest
     # value that keeps every row mass below 2^31 (wrapping accumulators)
