@@ -66,11 +66,12 @@ def test_gemm_matches_oracle(ctx, m, n, k):
     assert np.array_equal(got, exp)
 
 
-@pytest.mark.parametrize("m,n,k", [(40, 96, 16384), (40, 96, 17000)])
+@pytest.mark.parametrize("m,n,k", [(40, 96, 16384), (40, 96, 17000), (24, 64, 33000)])
 def test_gemm_longest_rows(ctx, m, n, k):
-    # 16384 columns: 64 column parts, each with its own limb count (one value
-    # past 2^23 in the last part of one token group); 17000 columns: more parts
-    # than the per-group flag mask holds, so every part takes four limbs
+    # one value past 2^23 in the last column part of one token group: 16384
+    # columns (64 parts), each part with its own limb count; 17000 and 33000
+    # columns: more parts than the per-group flag mask holds, so every part
+    # takes four limbs
     rng = np.random.default_rng(k)
     q, s = synthetic.random_int8_matrix(rng, n, k, scale_max=256)
     acts = act_slab(m, k, seed=k)
