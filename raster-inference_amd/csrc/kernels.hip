@@ -1689,12 +1689,30 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const int64_t* __restrict__
   const uint64_t e0 = (uint64_t(blockIdx.x) * 256 + threadIdx.x) * 2;
   if (e0 >= total) return;
   const uint64_t plane = total;
+  // every plane's two values are requested before the first is added (up to
+  // kUnroll planes at clamped addresses, masked; more in a second loop)
+  constexpr uint32_t kUnroll = 8;
+  const uint64_t e1 = e0 + 1 < total ? e0 + 1 : e0;
+  int64_t p0[kUnroll], p1[kUnroll];
+#pragma unroll
+  for (uint32_t c = 0; c < kUnroll; ++c) {
+    const uint64_t cc = c < chunks ? c : 0;
+    p0[c] = planes[cc * plane + e0];
+    p1[c] = planes[cc * plane + e1];
+  }
+  uint64_t sum[2] = {0, 0};
+#pragma unroll
+  for (uint32_t c = 0; c < kUnroll; ++c)
+    if (c < chunks) sum[0] += uint64_t(p0[c]), sum[1] += uint64_t(p1[c]);
+  for (uint32_t c = kUnroll; c < chunks; ++c) {
+    sum[0] += uint64_t(planes[c * plane + e0]);
+    sum[1] += uint64_t(planes[c * plane + e1]);
+  }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const uint64_t e = e0 + h;
     if (e >= total) break;
-    uint64_t v = 0;
-    for (uint32_t c = 0; c < chunks; ++c) v += uint64_t(planes[c * plane + e]);
+    const uint64_t v = sum[h];
     const uint64_t token = e / n_rows, row = e % n_rows;
     if (acc_out) {
       acc_out[token * ld_out + row] = int64_t(v);
@@ -2953,7 +2971,11 @@ void launch_gemm_limbs(const int32_t* act, uint64_t m, uint64_t k, uint64_t ld_a
   const uint64_t groups = (m + 63) / 64 * 4;  // the larger block's 4 token groups
   const int vec = (reinterpret_cast<uintptr_t>(act) % 16 == 0 && ld_act % 4 == 0) ? 1 : 0;
   const dim3 grid(unsigned(groups), unsigned(limb_parts(kpad)));
-  if (uint64_t(grid.x) * grid.y <= 512)
+  const uint64_t wgs = uint64_t(grid.x) * grid.y;
+  if (wgs <= 256)
+    hipLaunchKernelGGL(k_act_limbs_rows<1024>, grid, dim3(1024), 0, s, act, m, k, ld_act, kpad, vec,
+                       gemm_flags(a_tiled, m, kpad), a_tiled);
+  else if (wgs <= 512)
     hipLaunchKernelGGL(k_act_limbs_rows<512>, grid, dim3(512), 0, s, act, m, k, ld_act, kpad, vec,
                        gemm_flags(a_tiled, m, kpad), a_tiled);
   else
