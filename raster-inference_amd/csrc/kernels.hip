@@ -1330,9 +1330,10 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemv_rega(
 // layout (limb j, step, lane slot 16 g + i of 32 bytes: token i's columns
 // 32 g + [0, 32) of the step) and copied out in whole 16-byte pieces, each
 // tile-step a contiguous 2 KB. Tokens past m and columns past k are zero.
-// 512 threads for grids of up to 512 workgroups (shorter chains per thread),
-// else 256: at 128 rows 3.1 us against 4.3 us for 256 threads and 512-column
-// parts (K = 2560), at 2048 rows x 10240 columns 24.6 against 26.1 us.
+// 1024 threads for grids of up to 256 workgroups and 512 for up to 512
+// (shorter chains per thread), else 256: at 128 rows 3.1 us on 512 threads
+// against 4.3 us for 256 threads and 512-column parts (K = 2560), at 2048 rows
+// x 10240 columns 24.6 against 26.1 us.
 template <int NT>
 __global__ __launch_bounds__(NT) void k_act_limbs_rows(const int32_t* __restrict__ act, uint64_t m, uint64_t k,
                                                       uint64_t ld, uint64_t kpad, int vec,
