@@ -108,9 +108,10 @@ def two_layer_models(ctx):
     return e4b_two_layers(ctx)
 
 
-# 100 and 128 tokens: the layer prefill's gate/up GEMM with the GELU epilogue
-# in one round of 64 x 160 blocks
-@pytest.mark.parametrize("prompt_len", [100, 128, 600, 777])
+# 65, 100 and 128 tokens: the layer prefill's gate/up GEMM with the GELU
+# epilogue in one round of 64 x 160 blocks (65: one token in the last block),
+# q/k/v in 32 x 48 blocks (100, 128), o in 16 x 80 blocks (128)
+@pytest.mark.parametrize("prompt_len", [65, 100, 128, 600, 777])
 def test_two_layer_e4b_long_prompt_capture(two_layer_models, prompt_len):
     om, gm = two_layer_models
     rng = np.random.default_rng(prompt_len)
